@@ -1,0 +1,419 @@
+/*
+ * gefen_oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's CPU-resident (fused=False) Gefen
+ * optimizer step, used exclusively as the checker for the HIP product path.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * this library; the product (gefen-x_amd/) never links, imports or calls it.
+ *
+ * Every function cites the reference file:line it follows (paths relative to
+ * the reference repo root, src/gefen/ omitted).  Numerics follow the torch CPU
+ * kernels the reference calls:
+ *   - Tensor.lerp with a scalar weight w < 0.5 is fma(w, end - self, self)
+ *     (ATen vectorised lerp), else fma(w - 1, end - self, end);
+ *   - searchsorted(side='left') is a lower_bound on `!(c[mid] >= x)`;
+ *   - `scalar / tensor` and `reciprocal` are correctly rounded fp32 divides;
+ *   - `a.add_(b, alpha=s)` is fma(b, s, a);
+ *   - dequantised coefficients are rounded through the grad dtype
+ *     (gefen.py:337-373 returns like_tensor.dtype).
+ * Summation order: torch's CPU cascade sums depend on the host's vector width,
+ * so the oracle accumulates in double and rounds once; comparisons against the
+ * oracle for sums (v_row, v_col, vmean, mean(v_row)) carry a tolerance.
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_BF16 = 2 };
+
+/* ---------------------------------------------------------------- rounding */
+
+static uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+/* fp32 -> bf16 -> fp32, round-to-nearest-even (c10::BFloat16 semantics). */
+float orc_bf16_round(float x) {
+    uint32_t u = f2u(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return u2f(u | 0x00400000u); /* NaN */
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    return u2f(u & 0xffff0000u);
+}
+
+/* fp32 -> binary16 -> fp32, round-to-nearest-even (IEEE semantics). */
+float orc_f16_round(float x) {
+    if (isnan(x)) return x;
+    float a = fabsf(x);
+    if (a >= 65520.0f) return copysignf(INFINITY, x); /* rounds to inf */
+    if (a < 5.9604644775390625e-08f * 0.5f) return copysignf(0.0f, x);
+    int e;
+    frexpf(a, &e); /* a = m * 2^e, m in [0.5,1) */
+    int exp_unbiased = e - 1;
+    if (exp_unbiased < -14) exp_unbiased = -14; /* subnormal spacing */
+    float ulp = ldexpf(1.0f, exp_unbiased - 10);
+    /* a / ulp is exact (power-of-two scale); rint is round-half-even */
+    float r = rintf(a / ulp) * ulp;
+    return copysignf(r, x);
+}
+
+float orc_round(float x, int dtype) {
+    if (dtype == ORC_BF16) return orc_bf16_round(x);
+    if (dtype == ORC_F16) return orc_f16_round(x);
+    return x;
+}
+
+void orc_round_array(float* x, int64_t n, int dtype) {
+    for (int64_t i = 0; i < n; ++i) x[i] = orc_round(x[i], dtype);
+}
+
+/* ----------------------------------------------------------- codebook search */
+
+/* torch.searchsorted(codebook, x) (side='left'): gefen.py:318 */
+int orc_lower_bound(const float* cb, int k, float x) {
+    int lo = 0, hi = k;
+    while (lo < hi) {
+        int mid = lo + ((hi - lo) >> 1);
+        if (!(cb[mid] >= x)) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+/* gefen_nearest_codebook_indices, one element: gefen.py:288-334 */
+uint8_t orc_nearest(const float* cb, int k, float x) {
+    if (k <= 1) return 0;
+    int idx = orc_lower_bound(cb, k, x);
+    int left = idx - 1;
+    if (left < 0) left = 0;
+    if (left > k - 1) left = k - 1;
+    int right = idx;
+    if (right > k - 1) right = k - 1;
+    float dl = fabsf(x - cb[left]);
+    float dr = fabsf(x - cb[right]);
+    return (uint8_t)((dl <= dr) ? left : right);
+}
+
+void orc_nearest_array(const float* cb, int k, const float* x, int64_t n, uint8_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_nearest(cb, k, x[i]);
+}
+
+/* _codebook_search_lut: kernels/automatic_gefen_fused.py:81-121.
+ * lut[b] = #{entries whose bucket < b}, bucket(c) = clamp(floor((c+1)*B/2)). */
+void orc_search_lut(const float* cb, int k, int buckets, int16_t* lut) {
+    for (int b = 0; b <= buckets; ++b) {
+        int cnt = 0;
+        for (int i = 0; i < k; ++i) {
+            float eb = floorf((cb[i] + 1.0f) * (float)(buckets / 2));
+            if (eb < 0.0f) eb = 0.0f;
+            if (eb > (float)(buckets - 1)) eb = (float)(buckets - 1);
+            if (eb < (float)b) ++cnt;
+        }
+        lut[b] = (int16_t)cnt;
+    }
+}
+
+/* ------------------------------------------------------- momentum recurrence */
+
+/* Tensor.lerp(end, w) with a scalar weight (ATen LerpKernel, vectorised form). */
+static float lerp_f(float self, float end, float w) {
+    if (fabsf(w) < 0.5f) return fmaf(w, end - self, self);
+    return fmaf(w - 1.0f, end - self, end);
+}
+
+/*
+ * _automatic_momentum_update_merged / _automatic_momentum_update:
+ * gefen.py:3438-3486 and 3329-3436 (identical arithmetic).
+ *   cm  = dtype_round(c[idx]) * mag                 (3394-3400, 3465-3469)
+ *   u   = cm.lerp(g, 1 - beta1)                     (3403-3405, 3470)
+ *   mag'= amax |u| over the block (NaN propagates)  (3409-3414, 3472-3476)
+ *   x   = mag' > 0 ? u / mag' : 0                   (3416-3418, 3478-3480)
+ *   idx'= nearest(x)                                (3421-3422, 3482-3483)
+ *   q   = dtype_round(c[idx']) * mag'               (3428-3429, 3485-3486)
+ * g holds the grad values already widened to fp32; dtype is the grad dtype.
+ * idx and mag are updated in place; q (may be NULL) receives the reconstructed
+ * momentum.  u_out (may be NULL) receives the pre-quantisation momentum.
+ */
+void orc_momentum_update(const float* g, uint8_t* idx, float* mag, int64_t nb,
+                         int64_t period, const float* cb, int k, int dtype,
+                         float w, float* q, float* u_out) {
+    float* u = (float*)malloc(sizeof(float) * (size_t)(period > 0 ? period : 1));
+    for (int64_t b = 0; b < nb; ++b) {
+        const int64_t base = b * period;
+        const float m_old = mag[b];
+        float amax = 0.0f;
+        int saw_nan = 0;
+        for (int64_t j = 0; j < period; ++j) {
+            float c = orc_round(cb[idx[base + j]], dtype);
+            float cm = c * m_old;
+            float uu = lerp_f(cm, g[base + j], w);
+            u[j] = uu;
+            if (u_out) u_out[base + j] = uu;
+            float a = fabsf(uu);
+            if (isnan(a)) saw_nan = 1;
+            else if (j == 0 || a > amax) amax = a;
+        }
+        float m_new = saw_nan ? NAN : amax;
+        mag[b] = m_new;
+        const int nonzero = (m_new > 0.0f);
+        for (int64_t j = 0; j < period; ++j) {
+            float x = nonzero ? u[j] / m_new : 0.0f;
+            uint8_t ni = orc_nearest(cb, k, x);
+            idx[base + j] = ni;
+            if (q) q[base + j] = orc_round(cb[ni], dtype) * m_new;
+        }
+    }
+    free(u);
+}
+
+/* ------------------------------------------------------- factored step (2D) */
+
+/*
+ * Decomposed factored update: gefen.py:2959-3018.
+ *   row_ms = sum_j g^2 / cols, col_ms = sum_i g^2 / rows  (2973-2994)
+ *   v <- fma(ms, 1-beta2, v*beta2)                          (2995-2996)
+ *   v_hat = (v_row ⊗ v_col) / max(mean(v_row), FLT_MIN)     (2998-3000)
+ *   step  = (1/bc1) * 1/(sqrt(v_hat/bc2) + eps)             (3001-3002)
+ *   p     = dtype(p * (1 - lr*wd)) if wd > 0                (3015-3016)
+ *   p     = dtype(p - (q*step)*lr)                          (3017-3018)
+ * Host scalars arrive exactly as the reference computes them in Python
+ * doubles: beta1, beta2, lr, eps, bc1 = 1-beta1^step, bc2 = 1-beta2^fstep, wd.
+ * p and g are fp32 arrays holding the dtype's values; p is re-rounded to dtype.
+ */
+void orc_factored_step(float* p, const float* g, uint8_t* idx, float* mag,
+                       float* v_row, float* v_col, int64_t rows, int64_t cols,
+                       int64_t period, const float* cb, int k, int dtype,
+                       double beta1, double beta2, double lr, double eps,
+                       double bc1, double bc2, double wd) {
+    const int64_t n = rows * cols;
+    const int64_t nb = n / period;
+    double* col_acc = (double*)calloc((size_t)cols, sizeof(double));
+    const float beta2_f = (float)beta2;
+    const float alpha_f = (float)(1.0 - beta2);
+    for (int64_t i = 0; i < rows; ++i) {
+        double racc = 0.0;
+        for (int64_t j = 0; j < cols; ++j) {
+            float gv = g[i * cols + j];
+            float sq = gv * gv;
+            racc += (double)sq;
+            col_acc[j] += (double)sq;
+        }
+        float row_ms = (float)racc / (float)cols;
+        v_row[i] = fmaf(row_ms, alpha_f, v_row[i] * beta2_f);
+    }
+    for (int64_t j = 0; j < cols; ++j) {
+        float col_ms = (float)col_acc[j] / (float)rows;
+        v_col[j] = fmaf(col_ms, alpha_f, v_col[j] * beta2_f);
+    }
+    free(col_acc);
+    double vsum = 0.0;
+    for (int64_t i = 0; i < rows; ++i) vsum += (double)v_row[i];
+    float mean_r = (float)vsum / (float)rows;
+    if (!(mean_r >= 1.17549435e-38f)) mean_r = (mean_r != mean_r) ? mean_r : 1.17549435e-38f;
+
+    float* q = (float*)malloc(sizeof(float) * (size_t)n);
+    orc_momentum_update(g, idx, mag, nb, period, cb, k, dtype, (float)(1.0 - beta1), q, NULL);
+
+    const float bc2_f = (float)bc2;
+    const float eps_f = (float)eps;
+    const float inv_bc1_f = (float)(1.0 / bc1);
+    const float lr_f = (float)lr;
+    const float wdf_f = (float)(1.0 - lr * wd);
+    for (int64_t i = 0; i < rows; ++i) {
+        for (int64_t j = 0; j < cols; ++j) {
+            const int64_t e = i * cols + j;
+            float vh = (v_row[i] * v_col[j]) / mean_r;
+            float h = sqrtf(vh / bc2_f) + eps_f;
+            float step = (1.0f / h) * inv_bc1_f;
+            float pv = p[e];
+            if (wd > 0.0) pv = orc_round(pv * wdf_f, dtype);
+            float upd = (q[e] * step) * lr_f;
+            p[e] = orc_round(pv - upd, dtype);
+        }
+    }
+    free(q);
+}
+
+/* ---------------------------------------------------- block-vmean step (1D) */
+
+/*
+ * automatic_vmean_update(use_fused=False): gefen.py:129-191.
+ * bf16 grads square in bf16 and take a bf16 mean (fp32 sum, /P, cast back);
+ * fp16 grads are promoted to fp32 first; fp32 squares in fp32.
+ */
+void orc_vmean_update(float* vmean, const float* g, int64_t nb, int64_t period,
+                      int dtype, double beta2) {
+    const float beta2_f = (float)beta2;
+    const float alpha_f = (float)(1.0 - beta2);
+    for (int64_t b = 0; b < nb; ++b) {
+        double acc = 0.0;
+        for (int64_t j = 0; j < period; ++j) {
+            float gv = g[b * period + j];
+            float sq = gv * gv;
+            if (dtype == ORC_BF16) sq = orc_bf16_round(sq);
+            acc += (double)sq;
+        }
+        float mean = (float)acc / (float)period;
+        if (dtype == ORC_BF16) mean = orc_bf16_round(mean);
+        vmean[b] = fmaf(mean, alpha_f, vmean[b] * beta2_f);
+    }
+}
+
+/*
+ * Non-fused block step: gefen.py:3776-3818 (+ vmean update 3626-3628 and the
+ * streamed momentum/apply 3329-3436).
+ *   p = dtype(p*(1-lr*wd)) if wd > 0
+ *   h = sqrt(vmean)/sqrt(bc2) + eps ; step = (1/h) * (1/bc1)
+ *   p = dtype(p - (q*step_b)*lr)
+ */
+void orc_block_step(float* p, const float* g, uint8_t* idx, float* mag,
+                    float* vmean, int64_t n, int64_t period, const float* cb,
+                    int k, int dtype, double beta1, double beta2, double lr,
+                    double eps, double bc1, double bc2, double wd) {
+    const int64_t nb = n / period;
+    orc_vmean_update(vmean, g, nb, period, dtype, beta2);
+    const float wdf_f = (float)(1.0 - lr * wd);
+    if (wd > 0.0) {
+        for (int64_t e = 0; e < n; ++e) p[e] = orc_round(p[e] * wdf_f, dtype);
+    }
+    const float sbc2_f = (float)sqrt(bc2);
+    const float eps_f = (float)eps;
+    const float inv_bc1_f = (float)(1.0 / bc1);
+    const float lr_f = (float)lr;
+    float* q = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    orc_momentum_update(g, idx, mag, nb, period, cb, k, dtype, (float)(1.0 - beta1), q, NULL);
+    for (int64_t b = 0; b < nb; ++b) {
+        float h = sqrtf(vmean[b]) / sbc2_f + eps_f;
+        float step = (1.0f / h) * inv_bc1_f;
+        for (int64_t j = 0; j < period; ++j) {
+            const int64_t e = b * period + j;
+            float upd = (q[e] * step) * lr_f;
+            p[e] = orc_round(p[e] - upd, dtype);
+        }
+    }
+    free(q);
+}
+
+/* ----------------------------------------------- step-1 codebook histogram */
+
+/*
+ * learn_gefen_exact_codebook_from_grad_periods, torch histogram branch:
+ * gefen.py:455-469.  counts has `bins` int64 entries and is accumulated.
+ */
+void orc_exact_histogram(const float* g, int64_t n, int64_t period, int bins,
+                         int64_t* counts) {
+    const float bin_width = (float)(2.0 / (double)bins);
+    const int64_t nb = n / period;
+    for (int64_t b = 0; b < nb; ++b) {
+        const float* blk = g + b * period;
+        float amax = 0.0f;
+        int saw_nan = 0;
+        for (int64_t j = 0; j < period; ++j) {
+            float a = fabsf(blk[j]);
+            if (isnan(a)) saw_nan = 1;
+            else if (a > amax) amax = a;
+        }
+        const int nonzero = !saw_nan && amax > 0.0f;
+        for (int64_t j = 0; j < period; ++j) {
+            float x = nonzero ? blk[j] / amax : 0.0f;
+            float t = floorf((x + 1.0f) / bin_width);
+            int64_t bi;
+            if (isnan(t)) bi = 0; /* long() of NaN then clamp(0, bins-1) */
+            else if (t < 0.0f) bi = 0;
+            else if (t > (float)(bins - 1)) bi = bins - 1;
+            else bi = (int64_t)t;
+            counts[bi] += 1;
+        }
+    }
+}
+
+/* ------------------------------------------------------------ exact DP */
+
+/*
+ * quantization.exact_dp numba/python kernel: quantization.py:75-139, 142-194.
+ * Optimal 1-D weighted k-means by DP in float64 with forced +-1 endpoints,
+ * strict `<` keeps the first minimum.  prefix arrays have n_points+1 entries.
+ * Writes the unsorted codebook (the caller sorts, quantization.py:252).
+ */
+int orc_exact_dp_kernel(const double* pw, const double* pwx, const double* pwx2,
+                        int n_points, int k, int force_endpoints, float* codebook) {
+    const int64_t W = (int64_t)k + 1;
+    double* dp = (double*)malloc(sizeof(double) * (size_t)(n_points + 1) * (size_t)W);
+    int64_t* bt = (int64_t*)malloc(sizeof(int64_t) * (size_t)(n_points + 1) * (size_t)W);
+    if (!dp || !bt) { free(dp); free(bt); return -1; }
+    for (int64_t i = 0; i < (int64_t)(n_points + 1) * W; ++i) { dp[i] = INFINITY; bt[i] = -1; }
+    dp[0] = 0.0;
+    for (int c = 1; c <= k; ++c) {
+        for (int end = c; end <= n_points; ++end) {
+            double best = INFINITY;
+            int64_t best_start = -1;
+            for (int s = c; s <= end; ++s) {
+                double sw = pw[end] - pw[s - 1];
+                double swx = pwx[end] - pwx[s - 1];
+                double swx2 = pwx2[end] - pwx2[s - 1];
+                double cost;
+                if (force_endpoints && c == 1) {
+                    double fc = -1.0;
+                    cost = swx2 - 2.0 * fc * swx + fc * fc * sw;
+                } else if (force_endpoints && c == k) {
+                    double fc = 1.0;
+                    cost = swx2 - 2.0 * fc * swx + fc * fc * sw;
+                } else {
+                    cost = swx2 - (swx * swx) / sw;
+                }
+                double cand = dp[(int64_t)(s - 1) * W + (c - 1)] + cost;
+                if (cand < best) { best = cand; best_start = s; }
+            }
+            dp[(int64_t)end * W + c] = best;
+            bt[(int64_t)end * W + c] = best_start;
+        }
+    }
+    int64_t end = n_points;
+    for (int c = k; c >= 1; --c) {
+        int64_t s = bt[end * W + c];
+        if (force_endpoints && c == 1) codebook[c - 1] = -1.0f;
+        else if (force_endpoints && c == k) codebook[c - 1] = 1.0f;
+        else {
+            double sw = pw[end] - pw[s - 1];
+            double swx = pwx[end] - pwx[s - 1];
+            codebook[c - 1] = (float)(swx / sw);
+        }
+        end = s - 1;
+    }
+    free(dp); free(bt);
+    return 0;
+}
+
+/* ------------------------------------------------------ stochastic rounding */
+
+/* gefen_sr_uniform: kernels/automatic_gefen_fused_kernel.cu:141-151
+ * (SplitMix64 finalizer over seed + golden_gamma * (idx + 1)). */
+float orc_sr_uniform(uint64_t seed, int64_t element_idx) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ULL * ((uint64_t)element_idx + 1ULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    z = z ^ (z >> 31);
+    return (float)(z >> 40) * (1.0f / 16777216.0f);
+}
+
+/* quantize_codebook_index, stochastic branch:
+ * kernels/automatic_gefen_fused_kernel.cu:160-211. */
+uint8_t orc_sr_quantize(const float* cb, int k, float x, uint64_t seed, int64_t element_idx) {
+    /* the kernel's own lower_bound moves right on `c[mid] < x` (:173-181) */
+    int r = 0, hi_ = k;
+    while (r < hi_) {
+        int mid = r + ((hi_ - r) >> 1);
+        if (cb[mid] < x) r = mid + 1; else hi_ = mid;
+    }
+    if (r > k - 1) r = k - 1;
+    int l = r - 1;
+    if (l < 0) l = 0;
+    if (l == r) return (uint8_t)r;
+    float lo = cb[l], hi = cb[r];
+    float span = hi - lo;
+    float v = x;
+    if (v < lo) v = lo; else if (v > hi) v = hi;
+    float p_up = (span > 0.0f) ? (v - lo) / span : 0.0f;
+    float u = orc_sr_uniform(seed, element_idx);
+    return (uint8_t)((u < p_up) ? r : l);
+}

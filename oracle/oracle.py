@@ -1,0 +1,350 @@
+"""CPU oracle for the Gefen optimizer step -- TEST INFRASTRUCTURE ONLY.
+
+Thin numpy/ctypes front end over ``oracle/gefen_oracle.c`` plus the pieces of
+the reference that are plain numpy/float64 host math (period search, exact-DP
+driver).  Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module; the product path never does.
+
+Every function cites the reference file:line it restates (paths relative to the
+reference repo root, ``src/gefen/`` omitted).
+
+Parity status of each function (how it is pinned):
+  nearest_indices      closed form + reference golden vectors (tests/golden)
+  search_lut           closed form + "LUT search == full search" invariant
+  momentum_update      reference golden vectors of the CPU step
+  factored_step        reference golden vectors (config-1 shaped trajectory)
+  block_step           reference golden vectors (bf16/fp16/fp32, several P)
+  exact_histogram      reference golden vectors + integer order-freedom
+  exact_dp             reference golden vectors (pure-Python DP) + brute force
+  find_period          reference golden vectors + closed-form rule tests
+  sr_quantize          SplitMix64 known answer + unbiasedness invariant
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+from typing import Iterable, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+F32, F16, BF16 = 0, 1, 2
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libgefen_oracle.so")
+_LIB = None
+
+
+def build() -> str:
+    """Compile the C oracle (``oracle/Makefile``); returns the .so path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def _lib():
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(_LIB_PATH):
+        build()
+    lib = ctypes.CDLL(_LIB_PATH)
+    P = ctypes.c_void_p
+    i64 = ctypes.c_int64
+    d = ctypes.c_double
+    i = ctypes.c_int
+    f = ctypes.c_float
+    lib.orc_round.restype = f
+    lib.orc_round.argtypes = [f, i]
+    lib.orc_round_array.argtypes = [P, i64, i]
+    lib.orc_nearest_array.argtypes = [P, i, P, i64, P]
+    lib.orc_search_lut.argtypes = [P, i, i, P]
+    lib.orc_momentum_update.argtypes = [P, P, P, i64, i64, P, i, i, f, P, P]
+    lib.orc_factored_step.argtypes = [P, P, P, P, P, P, i64, i64, i64, P, i, i,
+                                      d, d, d, d, d, d, d]
+    lib.orc_vmean_update.argtypes = [P, P, i64, i64, i, d]
+    lib.orc_block_step.argtypes = [P, P, P, P, P, i64, i64, P, i, i,
+                                   d, d, d, d, d, d, d]
+    lib.orc_exact_histogram.argtypes = [P, i64, i64, i, P]
+    lib.orc_exact_dp_kernel.restype = i
+    lib.orc_exact_dp_kernel.argtypes = [P, P, P, i, i, i, P]
+    lib.orc_sr_uniform.restype = f
+    lib.orc_sr_uniform.argtypes = [ctypes.c_uint64, i64]
+    lib.orc_sr_quantize.restype = ctypes.c_uint8
+    lib.orc_sr_quantize.argtypes = [P, i, f, ctypes.c_uint64, i64]
+    _LIB = lib
+    return lib
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def round_dtype(x: np.ndarray, dtype: int) -> np.ndarray:
+    """Round fp32 values through bf16/fp16 (RNE) and back to fp32."""
+    out = _f32(x).copy()
+    _lib().orc_round_array(_ptr(out), out.size, dtype)
+    return out
+
+
+# ------------------------------------------------------------------ search
+
+
+def nearest_indices(codebook, values) -> np.ndarray:
+    """gefen_nearest_codebook_indices: gefen.py:288-334."""
+    cb = _f32(codebook)
+    x = _f32(values).reshape(-1)
+    out = np.empty(x.size, dtype=np.uint8)
+    _lib().orc_nearest_array(_ptr(cb), cb.size, _ptr(x), x.size, _ptr(out))
+    return out.reshape(np.shape(values))
+
+
+def search_lut(codebook, buckets: int = 4096) -> np.ndarray:
+    """_codebook_search_lut: kernels/automatic_gefen_fused.py:81-121."""
+    cb = _f32(codebook)
+    lut = np.empty(buckets + 1, dtype=np.int16)
+    _lib().orc_search_lut(_ptr(cb), cb.size, buckets, _ptr(lut))
+    return lut
+
+
+def sr_uniform(seed: int, idx: int) -> float:
+    """gefen_sr_uniform: kernels/automatic_gefen_fused_kernel.cu:141-151."""
+    return float(_lib().orc_sr_uniform(ctypes.c_uint64(seed & (2**64 - 1)), idx))
+
+
+def sr_quantize(codebook, x: float, seed: int, idx: int) -> int:
+    """quantize_codebook_index (stochastic): automatic_gefen_fused_kernel.cu:160-211."""
+    cb = _f32(codebook)
+    return int(_lib().orc_sr_quantize(_ptr(cb), cb.size, float(x),
+                                      ctypes.c_uint64(seed & (2**64 - 1)), idx))
+
+
+# ---------------------------------------------------------------- momentum
+
+
+def momentum_update(g, idx, mag, period, codebook, dtype, beta1):
+    """Quantized-momentum recurrence: gefen.py:3438-3486.
+
+    Returns (new_idx, new_mag, q, u) without mutating the inputs.
+    """
+    g = _f32(g).reshape(-1)
+    idx = np.ascontiguousarray(np.asarray(idx, dtype=np.uint8).reshape(-1)).copy()
+    mag = _f32(mag).reshape(-1).copy()
+    nb = g.size // period
+    cb = _f32(codebook)
+    q = np.empty_like(g)
+    u = np.empty_like(g)
+    _lib().orc_momentum_update(_ptr(g), _ptr(idx), _ptr(mag), nb, period, _ptr(cb),
+                               cb.size, dtype, np.float32(1.0 - beta1), _ptr(q), _ptr(u))
+    return idx, mag, q, u
+
+
+# -------------------------------------------------------------- step paths
+
+
+def factored_step(p, g, idx, mag, v_row, v_col, period, codebook, dtype, *,
+                  beta1, beta2, lr, eps, bc1, bc2, wd):
+    """Decomposed factored step: gefen.py:2959-3018.  Returns new arrays."""
+    p = _f32(p).copy()
+    rows, cols = p.shape
+    g = _f32(g).reshape(rows, cols)
+    idx = np.ascontiguousarray(np.asarray(idx, dtype=np.uint8).reshape(-1)).copy()
+    mag = _f32(mag).reshape(-1).copy()
+    v_row = _f32(v_row).reshape(-1).copy()
+    v_col = _f32(v_col).reshape(-1).copy()
+    cb = _f32(codebook)
+    _lib().orc_factored_step(_ptr(p), _ptr(g), _ptr(idx), _ptr(mag), _ptr(v_row),
+                             _ptr(v_col), rows, cols, period, _ptr(cb), cb.size, dtype,
+                             beta1, beta2, lr, eps, bc1, bc2, wd)
+    return p, idx, mag, v_row, v_col
+
+
+def block_step(p, g, idx, mag, vmean, period, codebook, dtype, *,
+               beta1, beta2, lr, eps, bc1, bc2, wd):
+    """Non-fused block-vmean step: gefen.py:3776-3818 + 129-191 + 3329-3436."""
+    shape = np.shape(p)
+    p = _f32(p).reshape(-1).copy()
+    g = _f32(g).reshape(-1)
+    idx = np.ascontiguousarray(np.asarray(idx, dtype=np.uint8).reshape(-1)).copy()
+    mag = _f32(mag).reshape(-1).copy()
+    vmean = _f32(vmean).reshape(-1).copy()
+    cb = _f32(codebook)
+    _lib().orc_block_step(_ptr(p), _ptr(g), _ptr(idx), _ptr(mag), _ptr(vmean), p.size,
+                          period, _ptr(cb), cb.size, dtype, beta1, beta2, lr, eps,
+                          bc1, bc2, wd)
+    return p.reshape(shape), idx, mag, vmean
+
+
+# ------------------------------------------------------------ step-1 math
+
+
+def exact_histogram(g, period: int, bins: int = 4096, counts=None) -> np.ndarray:
+    """Block-absmax-normalised histogram: gefen.py:455-469."""
+    g = _f32(g).reshape(-1)
+    if counts is None:
+        counts = np.zeros(bins, dtype=np.int64)
+    _lib().orc_exact_histogram(_ptr(g), g.size, period, bins, _ptr(counts))
+    return counts
+
+
+def histogram_stats(bin_counts: np.ndarray):
+    """Bin centres and active set: gefen.py:474-493 (fp32 linspace is exact)."""
+    bins = bin_counts.size
+    edges = np.array([-1.0 + 2.0 * k / bins for k in range(bins + 1)], dtype=np.float32)
+    centers = (np.float32(0.5) * (edges[:-1] + edges[1:])).astype(np.float32)
+    counts = bin_counts.astype(np.float32)
+    active = counts > 0
+    return centers[active], counts[active]
+
+
+def exact_dp(active_centers, active_counts, num_codebooks: int = 256,
+             force_endpoints: bool = True) -> np.ndarray:
+    """quantization.exact_dp: quantization.py:197-253 (+ padding 59-72)."""
+    centers = _f32(active_centers)
+    counts = _f32(active_counts)
+    if centers.size == 0:
+        raise ValueError("Cannot run exact DP on an empty histogram.")
+    if num_codebooks > centers.size:
+        cb = np.empty(num_codebooks, dtype=np.float32)
+        cb[: centers.size] = centers
+        cb[centers.size:] = centers[-1]
+        if force_endpoints:
+            cb[0] = -1.0
+            cb[-1] = 1.0
+        return np.sort(cb)
+    w = counts.astype(np.float64)
+    c = centers.astype(np.float64)
+    n = centers.size
+    pw = np.zeros(n + 1)
+    pwx = np.zeros(n + 1)
+    pwx2 = np.zeros(n + 1)
+    # torch.cumsum on CPU is a sequential inclusive scan in the input dtype
+    acc_w = acc_wx = acc_wx2 = 0.0
+    wx = w * c
+    wx2 = w * (c * c)
+    for i in range(n):
+        acc_w += w[i]
+        acc_wx += wx[i]
+        acc_wx2 += wx2[i]
+        pw[i + 1] = acc_w
+        pwx[i + 1] = acc_wx
+        pwx2[i + 1] = acc_wx2
+    cb = np.empty(num_codebooks, dtype=np.float32)
+    rc = _lib().orc_exact_dp_kernel(_ptr(pw), _ptr(pwx), _ptr(pwx2), n, num_codebooks,
+                                    1 if force_endpoints else 0, _ptr(cb))
+    if rc != 0:
+        raise MemoryError("oracle exact DP allocation failed")
+    return np.sort(cb)
+
+
+def learn_codebook(grad_periods: Iterable[Tuple[np.ndarray, int]],
+                   num_codebooks: int = 256) -> Optional[np.ndarray]:
+    """learn_gefen_exact_codebook_from_grad_periods: gefen.py:417-517."""
+    bins = num_codebooks * 16
+    counts = np.zeros(bins, dtype=np.int64)
+    total = 0
+    for g, period in grad_periods:
+        g = _f32(g).reshape(-1)
+        if g.size == 0:
+            continue
+        exact_histogram(g, period, bins, counts)
+        total += g.size
+    if total == 0:
+        return None
+    centers, cnts = histogram_stats(counts)
+    return exact_dp(centers, cnts, num_codebooks, True)
+
+
+# ---------------------------------------------------------- period search
+
+
+def divisors(n: int) -> List[int]:
+    """partitioning.divisors: partitioning.py:50-59."""
+    small, large = [], []
+    for i in range(1, int(n ** 0.5) + 1):
+        if n % i == 0:
+            if i != n:
+                small.append(i)
+            if i != n // i and n // i != n:
+                large.append(n // i)
+    return small + large[::-1]
+
+
+def _largest_divisor_at_most(n: int, cap: int) -> int:
+    """partitioning.py:18-28."""
+    best = 1
+    for i in range(1, int(n ** 0.5) + 1):
+        if n % i == 0:
+            if cap >= i > best:
+                best = i
+            j = n // i
+            if cap >= j > best:
+                best = j
+    return best
+
+
+def memory_safe_fallback_period(n: int, shape, cap: int = 2048) -> int:
+    """partitioning.memory_safe_fallback_period: partitioning.py:31-47."""
+    if n < 8:
+        return 1
+    cands = []
+    if shape is not None and len(shape) >= 2:
+        inf = int(shape[-1])
+        if inf >= 8 and n % inf == 0:
+            cands.append(inf)
+    capped = _largest_divisor_at_most(n, cap)
+    if capped >= 8:
+        cands.append(capped)
+    if not cands:
+        return 1
+    return max(cands)
+
+
+def block_variance_error(values64: np.ndarray, period: int) -> float:
+    """average_within_block_variance_cpu: partitioning.py:62-84 (float64 numpy)."""
+    blocks = values64.reshape(-1, period)
+    return float(np.sqrt(blocks.var(axis=1).mean()))
+
+
+def finalize_period(results: Sequence[Tuple[int, float]]) -> int:
+    """_finalize_period_results: partitioning.py:237-271."""
+    if not results:
+        raise ValueError("Expected at least one valid period candidate.")
+    scored = []
+    prev = None
+    for p, err in results:
+        we = 1e-12 if prev is None else err - prev
+        prev = err
+        scored.append((p, err, we))
+    _, best = min((we, p) for p, _, we in scored)
+    return 1 if best < 8 else best
+
+
+def find_period(grad, shape=None, *, memory_safe_fallback: bool = True,
+                return_errors: bool = False):
+    """find_period_by_block_variance, backend 'cpu': partitioning.py:274-313,
+    fed as gefen.py:2639-2655 does (fp32 square, then float64)."""
+    g = _f32(grad).reshape(-1)
+    vals = (g * g).astype(np.float32).astype(np.float64)
+    n = vals.size
+    divs = divisors(n)
+    results = [(p, block_variance_error(vals, p)) for p in divs]
+    period = finalize_period(results)
+    if memory_safe_fallback and period == 1:
+        period = memory_safe_fallback_period(n, shape)
+    if return_errors:
+        return period, results
+    return period
+
+
+def resolve_period(grad, shape) -> int:
+    """_iter_gefen_grad_periods / _resolve_automatic_period for default flags:
+    gefen.py:2563-2577, 2712-2717 (numel 1 -> period 1)."""
+    g = np.asarray(grad).reshape(-1)
+    if g.size == 1:
+        return 1
+    return find_period(g, shape)
