@@ -1,0 +1,234 @@
+// gefenx_device.h -- device helpers for the MI355X Gefen kernels (gfx950).
+//
+// Compiled with -ffp-contract=off: every fused multiply-add below is an
+// explicit __builtin_fmaf, so the momentum recurrence is bit-identical to the
+// reference's decomposed CPU step (Tensor.lerp is fma(w, end-self, self)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "gefenx_common.h"
+
+namespace gx {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int DT> struct Elem { using T = uint16_t; };
+template <> struct Elem<F32> { using T = float; };
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (c10::BFloat16 semantics, NaN quietened).
+__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x0040u) & 0xffffu;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    return __half2float(__ushort_as_half((unsigned short)h));
+}
+__device__ __forceinline__ uint32_t f32_to_f16(float x) {
+    return (uint32_t)__half_as_ushort(__float2half_rn(x));
+}
+
+template <int DT> __device__ __forceinline__ float to_f32(typename Elem<DT>::T v) {
+    if constexpr (DT == F32) return v;
+    else if constexpr (DT == BF16) return bf16_to_f32(v);
+    else return f16_to_f32(v);
+}
+template <int DT> __device__ __forceinline__ typename Elem<DT>::T from_f32(float v) {
+    if constexpr (DT == F32) return v;
+    else if constexpr (DT == BF16) return (uint16_t)f32_to_bf16(v);
+    else return (uint16_t)f32_to_f16(v);
+}
+template <int DT> __device__ __forceinline__ float round_dt(float v) {
+    if constexpr (DT == F32) return v;
+    else return to_f32<DT>(from_f32<DT>(v));
+}
+
+// ---------------------------------------------------------- 8-element I/O
+// A "chunk" is 8 consecutive logical elements starting at a multiple of 8.
+
+template <int DT>
+__device__ __forceinline__ void load8(const typename Elem<DT>::T* __restrict__ base, float v[8]) {
+    if constexpr (DT == F32) {
+        const f32x4* q = reinterpret_cast<const f32x4*>(base);
+        f32x4 a = q[0];
+        f32x4 b = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        u32x4 a = *reinterpret_cast<const u32x4*>(base);
+        uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = to_f32<DT>((uint16_t)(w[i] & 0xffffu));
+            v[2 * i + 1] = to_f32<DT>((uint16_t)(w[i] >> 16));
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(typename Elem<DT>::T* __restrict__ base, const float v[8]) {
+    if constexpr (DT == F32) {
+        f32x4* q = reinterpret_cast<f32x4*>(base);
+        f32x4 a = {v[0], v[1], v[2], v[3]};
+        f32x4 b = {v[4], v[5], v[6], v[7]};
+        __builtin_nontemporal_store(a, q);
+        __builtin_nontemporal_store(b, q + 1);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)from_f32<DT>(v[2 * i]) | ((uint32_t)from_f32<DT>(v[2 * i + 1]) << 16);
+        u32x4 a = {w[0], w[1], w[2], w[3]};
+        __builtin_nontemporal_store(a, reinterpret_cast<u32x4*>(base));
+    }
+}
+
+__device__ __forceinline__ void load_idx8(const uint8_t* __restrict__ base, uint32_t ix[8]) {
+    u32x2 a = *reinterpret_cast<const u32x2*>(base);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ix[i] = (a.x >> (8 * i)) & 0xffu;
+        ix[4 + i] = (a.y >> (8 * i)) & 0xffu;
+    }
+}
+
+__device__ __forceinline__ void store_idx8(uint8_t* __restrict__ base, const uint32_t ix[8]) {
+    u32x2 a;
+    a.x = ix[0] | (ix[1] << 8) | (ix[2] << 16) | (ix[3] << 24);
+    a.y = ix[4] | (ix[5] << 8) | (ix[6] << 16) | (ix[7] << 24);
+    __builtin_nontemporal_store(a, reinterpret_cast<u32x2*>(base));
+}
+
+// --------------------------------------------------------- momentum math
+
+struct MomentumCoef {
+    float w;      // (float)(1 - beta1): Tensor.lerp weight
+    float wm1;    // w - 1 (lerp's large-weight form)
+    int small;    // |w| < 0.5 selects fma(w, g - cm, cm)
+};
+
+// u = lerp(cr * mag_old, g, w): gefen.py:3465-3470 / ATen lerp kernel.
+__device__ __forceinline__ float momentum_value(float cr, float mag_old, float g,
+                                                const MomentumCoef& mc) {
+    const float cm = cr * mag_old;
+    const float d = g - cm;
+    return mc.small ? __builtin_fmaf(mc.w, d, cm) : __builtin_fmaf(mc.wm1, d, g);
+}
+
+// Nearest-codeword index through the exact threshold table (see gefenx_host.cpp).
+__device__ __forceinline__ uint32_t quant_nearest(float x, const uint32_t* __restrict__ s_bkt,
+                                                  const float* __restrict__ s_thr, uint32_t kmax) {
+    if (x != x) return kmax;  // NaN: searchsorted returns k -> index k-1
+    const float s = (x + 1.0f) * (float)(kBuckets / 2);
+    int b = (int)floorf(s);
+    b = b < 0 ? 0 : (b > kBuckets - 1 ? kBuckets - 1 : b);
+    const uint32_t e = s_bkt[b];
+    const uint32_t base = e & 0xffffu;
+    const uint32_t cnt = e >> 16;
+    uint32_t idx = base;
+    for (uint32_t j = 0; j < cnt; ++j) idx += (s_thr[base + j] < x) ? 1u : 0u;
+    return idx;
+}
+
+// SplitMix64 finalizer over seed + golden_gamma * (idx + 1), top 24 bits.
+__device__ __forceinline__ float sr_uniform(uint64_t seed, int64_t idx) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ULL * ((uint64_t)idx + 1ULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    z = z ^ (z >> 31);
+    return (float)(z >> 40) * (1.0f / 16777216.0f);
+}
+
+// Unbiased stochastic rounding between the bracketing codewords.
+__device__ __forceinline__ uint32_t quant_stochastic(float x, const float* __restrict__ s_cb,
+                                                     const int16_t* __restrict__ s_lut, int k,
+                                                     uint64_t seed, int64_t elem) {
+    int b = (int)floorf((x + 1.0f) * (float)(kBuckets / 2));
+    b = b < 0 ? 0 : (b > kBuckets - 1 ? kBuckets - 1 : b);
+    int lo = s_lut[b], hi = s_lut[b + 1];
+    lo = lo < 0 ? 0 : (lo > k ? k : lo);
+    hi = hi < lo ? lo : (hi > k ? k : hi);
+    while (lo < hi) {
+        const int mid = lo + ((hi - lo) >> 1);
+        if (s_cb[mid] < x) lo = mid + 1; else hi = mid;
+    }
+    const int r = lo > k - 1 ? k - 1 : lo;
+    const int l = r - 1 < 0 ? 0 : r - 1;
+    if (l == r) return (uint32_t)r;
+    const float lv = s_cb[l], hv = s_cb[r];
+    const float span = hv - lv;
+    float v = x;
+    v = v < lv ? lv : (v > hv ? hv : v);
+    const float p_up = span > 0.0f ? (v - lv) / span : 0.0f;
+    return sr_uniform(seed, elem) < p_up ? (uint32_t)r : (uint32_t)l;
+}
+
+// ------------------------------------------------------------- utilities
+
+// floor(n / d) for 0 <= n < 2^53, d >= 1, with inv = 1.0 / d.
+__device__ __forceinline__ int64_t div_floor(int64_t n, int64_t d, double inv) {
+    int64_t q = (int64_t)((double)n * inv);
+    const int64_t r = n - q * d;
+    if (r < 0) q -= 1;
+    else if (r >= d) q += 1;
+    return q;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Stage the quantisation table parts a kernel needs into LDS.
+struct SharedTables {
+    float cbr[kCodebookMax];
+    float thr[kCodebookMax];
+    uint32_t bkt[kBuckets];
+};
+
+__device__ __forceinline__ void stage_tables(SharedTables& s, const QTable* __restrict__ t) {
+    const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    const uint4* src = reinterpret_cast<const uint4*>(t->bucket);
+    uint4* dst = reinterpret_cast<uint4*>(s.bkt);
+    for (int i = tid; i < kBuckets / 4; i += nt) dst[i] = src[i];
+    for (int i = tid; i < kCodebookMax; i += nt) {
+        s.cbr[i] = t->cbr[i];
+        s.thr[i] = t->thr[i];
+    }
+}
+
+struct SharedSR {
+    float cb[kCodebookMax];
+    int16_t lut[kLutEntries + 7];
+};
+
+__device__ __forceinline__ void stage_sr(SharedSR& s, const QTable* __restrict__ t) {
+    for (int i = threadIdx.x; i < kCodebookMax; i += blockDim.x) s.cb[i] = t->cb[i];
+    for (int i = threadIdx.x; i < kLutEntries + 7; i += blockDim.x) s.lut[i] = t->lut[i];
+}
+
+}  // namespace gx

@@ -1,0 +1,366 @@
+// gefenx_step1.hip -- first-step kernels: block-period search statistics and
+// the block-absmax-normalised histogram the exact-DP codebook is learned from,
+// plus the standalone second-moment EMAs.
+#include "gefenx_device.h"
+#include "gefenx_internal.h"
+#include "../../include/gefenx.h"
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+namespace gx {
+
+constexpr int kT = 256;
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* base, int64_t i) {
+    return to_f32<DT>(static_cast<const typename Elem<DT>::T*>(base)[i]);
+}
+
+// -------------------------------------------------------- period variance
+// err(p) = sqrt(mean_b var_b(x)), x = fp32(g)^2 widened to float64
+// (partitioning.py:62-84 via gefen.py:2639-2655).
+
+// Small periods (P <= kWavePeriod): one wave per block, numpy's two-pass
+// variance (mean, then mean squared deviation) in float64.
+constexpr int64_t kWavePeriod = 4096;
+constexpr int64_t kSeg = 65536;  // elements per workgroup segment of a large block
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_var_wave(const void* g, int64_t nb, int64_t P, double* total) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kT + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * kT) >> 6;
+    double acc = 0.0;
+    for (int64_t b = wave; b < nb; b += nwaves) {
+        const int64_t base = b * P;
+        double s = 0.0;
+        for (int64_t j = lane; j < P; j += 64) {
+            const float v = load_elem<DT>(g, base + j);
+            s += (double)(v * v);
+        }
+        const double mean = wave_sum_d(s) / (double)P;
+        double d2 = 0.0;
+        for (int64_t j = lane; j < P; j += 64) {
+            const float v = load_elem<DT>(g, base + j);
+            const double d = (double)(v * v) - mean;
+            d2 += d * d;
+        }
+        d2 = wave_sum_d(d2);
+        if (lane == 0) acc += d2 / (double)P;
+    }
+    if (lane == 0 && acc != 0.0) atomicAdd(total, acc);
+}
+
+// Large periods: one workgroup per kSeg-element segment of a block; float64
+// (sum, sum of squares) per segment, combined per block with two atomics.
+template <int DT>
+__global__ void __launch_bounds__(kT) k_var_seg(const void* g, int64_t P, int64_t segs_per_block,
+                                               double* s1, double* s2) {
+    __shared__ double sh[2][kT / 64];
+    const int64_t b = (int64_t)blockIdx.x / segs_per_block;
+    const int64_t sg = (int64_t)blockIdx.x - b * segs_per_block;
+    const int64_t lo = b * P + sg * kSeg;
+    const int64_t hi = std::min<int64_t>(lo + kSeg, (b + 1) * P);
+    double a1 = 0.0, a2 = 0.0;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kT) {
+        const float v = load_elem<DT>(g, i);
+        const double x = (double)(v * v);
+        a1 += x;
+        a2 += x * x;
+    }
+    a1 = wave_sum_d(a1);
+    a2 = wave_sum_d(a2);
+    if ((threadIdx.x & 63) == 0) { sh[0][threadIdx.x >> 6] = a1; sh[1][threadIdx.x >> 6] = a2; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t1 = 0.0, t2 = 0.0;
+        for (int w = 0; w < kT / 64; ++w) { t1 += sh[0][w]; t2 += sh[1][w]; }
+        atomicAdd(s1 + b, t1);
+        atomicAdd(s2 + b, t2);
+    }
+}
+
+__global__ void __launch_bounds__(kT) k_var_finish(double* s1, double* s2, int64_t nb, int64_t P,
+                                                  double* total) {
+    double acc = 0.0;
+    const double fP = (double)P;
+    for (int64_t b = (int64_t)blockIdx.x * kT + threadIdx.x; b < nb; b += (int64_t)gridDim.x * kT) {
+        const double m = s1[b] / fP;
+        double v = s2[b] / fP - m * m;
+        if (v < 0.0) v = 0.0;
+        acc += v;
+        s1[b] = 0.0;
+        s2[b] = 0.0;
+    }
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0 && acc != 0.0) atomicAdd(total, acc);
+}
+
+__global__ void k_zero_f64(double* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0.0;
+}
+
+__global__ void k_zero_u32(uint32_t* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// ---------------------------------------------------------------- histogram
+// gefen.py:455-469: absmax per block, x = g / absmax (0 when absmax is not
+// > 0), bin = clamp(floor((x + 1) / (2 / bins)), 0, bins - 1).  The absmax is
+// carried as ordered uint bits of |g| (NaN > inf > finite), so a NaN block
+// bins every element at x = 0 as the reference's torch.where does.
+
+__device__ __forceinline__ int bin_of(float v, float amax, bool nz, float scale, int bins) {
+    const float x = nz ? v / amax : 0.0f;
+    const float t = floorf((x + 1.0f) * scale);  // dividing by 2/bins is exact scaling
+    if (!(t >= 0.0f)) return 0;
+    if (t > (float)(bins - 1)) return bins - 1;
+    return (int)t;
+}
+
+// Small periods: one wave per block, max then binning over the same block.
+template <int DT>
+__global__ void __launch_bounds__(kT) k_hist_wave(const void* g, int64_t nb, int64_t P, int bins,
+                                                 unsigned long long* counts) {
+    __shared__ uint32_t s_cnt[4096];
+    for (int i = threadIdx.x; i < bins; i += kT) s_cnt[i] = 0u;
+    __syncthreads();
+    const float scale = (float)(bins / 2);
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kT + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * kT) >> 6;
+    for (int64_t b = wave; b < nb; b += nwaves) {
+        const int64_t base = b * P;
+        uint32_t m = 0u;
+        for (int64_t j = lane; j < P; j += 64) {
+            const uint32_t ub = __float_as_uint(load_elem<DT>(g, base + j)) & 0x7fffffffu;
+            m = ub > m ? ub : m;
+        }
+        m = wave_max_u(m);
+        const float amax = __uint_as_float(m);
+        const bool nz = amax > 0.0f;
+        for (int64_t j = lane; j < P; j += 64)
+            atomicAdd(&s_cnt[bin_of(load_elem<DT>(g, base + j), amax, nz, scale, bins)], 1u);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < bins; i += kT)
+        if (s_cnt[i]) atomicAdd(counts + i, (unsigned long long)s_cnt[i]);
+}
+
+// Large periods: segment max, then segment binning.
+template <int DT>
+__global__ void __launch_bounds__(kT) k_absmax_seg(const void* g, int64_t P, int64_t segs_per_block,
+                                                  uint32_t* bits) {
+    const int64_t b = (int64_t)blockIdx.x / segs_per_block;
+    const int64_t sg = (int64_t)blockIdx.x - b * segs_per_block;
+    const int64_t lo = b * P + sg * kSeg;
+    const int64_t hi = std::min<int64_t>(lo + kSeg, (b + 1) * P);
+    uint32_t m = 0u;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kT) {
+        const uint32_t ub = __float_as_uint(load_elem<DT>(g, i)) & 0x7fffffffu;
+        m = ub > m ? ub : m;
+    }
+    m = wave_max_u(m);
+    if ((threadIdx.x & 63) == 0 && m) atomicMax(bits + b, m);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_hist_seg(const void* g, int64_t P, int64_t segs_per_block,
+                                                const uint32_t* bits, int bins,
+                                                unsigned long long* counts) {
+    __shared__ uint32_t s_cnt[4096];
+    for (int i = threadIdx.x; i < bins; i += kT) s_cnt[i] = 0u;
+    __syncthreads();
+    const float scale = (float)(bins / 2);
+    const int64_t b = (int64_t)blockIdx.x / segs_per_block;
+    const int64_t sg = (int64_t)blockIdx.x - b * segs_per_block;
+    const int64_t lo = b * P + sg * kSeg;
+    const int64_t hi = std::min<int64_t>(lo + kSeg, (b + 1) * P);
+    const float amax = __uint_as_float(bits[b]);
+    const bool nz = amax > 0.0f;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kT)
+        atomicAdd(&s_cnt[bin_of(load_elem<DT>(g, i), amax, nz, scale, bins)], 1u);
+    __syncthreads();
+    for (int i = threadIdx.x; i < bins; i += kT)
+        if (s_cnt[i]) atomicAdd(counts + i, (unsigned long long)s_cnt[i]);
+}
+
+// --------------------------------------------------------------- EMAs
+
+__global__ void k_v_ema(float* v, const float* sq, int64_t n, float inv_count, float beta2,
+                        float alpha2, int divide, float count) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float ms = divide ? sq[i] / count : sq[i] * inv_count;
+        v[i] = __builtin_fmaf(ms, alpha2, v[i] * beta2);
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_vmean(float* vmean, const void* g, int64_t nb, int64_t P,
+                                             float beta2, float alpha2) {
+    // one wave per block: float64 partial sums, one mean per block
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kT + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * kT) >> 6;
+    for (int64_t b = wave; b < nb; b += nwaves) {
+        double s = 0.0;
+        for (int64_t j = lane; j < P; j += 64) {
+            const float v = load_elem<DT>(g, b * P + j);
+            float sq = v * v;
+            if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+            s += (double)sq;
+        }
+        s = wave_sum_d(s);
+        if (lane == 0) {
+            float mean = (float)s / (float)P;
+            if constexpr (DT == BF16) mean = round_dt<BF16>(mean);
+            vmean[b] = __builtin_fmaf(mean, alpha2, vmean[b] * beta2);
+        }
+    }
+}
+
+static int grid_cap(int64_t items, int per, int cap) {
+    int64_t g = (items + per - 1) / per;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(g, cap));
+}
+
+static int check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GEFENX_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return GEFENX_OK;
+}
+
+#define GX_DISPATCH(dtype, KERNEL, grid, block, stream, ...)                                       \
+    do {                                                                                            \
+        if ((dtype) == F32) hipLaunchKernelGGL(KERNEL<F32>, grid, block, 0, stream, __VA_ARGS__);   \
+        else if ((dtype) == F16) hipLaunchKernelGGL(KERNEL<F16>, grid, block, 0, stream, __VA_ARGS__); \
+        else hipLaunchKernelGGL(KERNEL<BF16>, grid, block, 0, stream, __VA_ARGS__);                 \
+    } while (0)
+
+static int dtype_ok(int dtype, const char* fn) {
+    if (dtype == F64) return set_error(GEFENX_EDTYPE, "%s: not implemented for 'Double'", fn);
+    if (dtype != F32 && dtype != F16 && dtype != BF16) return set_error(GEFENX_EINVAL, "%s: bad dtype %d", fn, dtype);
+    return GEFENX_OK;
+}
+
+
+}  // namespace gx
+
+using namespace gx;
+
+extern "C" {
+
+int gefenx_block_variance_errors(const void* grad, int dtype, int64_t numel, const int64_t* periods,
+                                 int n_periods, double* err_host, void* stream) {
+    int rc = dtype_ok(dtype, "gefenx_block_variance_errors");
+    if (rc) return rc;
+    if (!grad || !periods || !err_host || numel <= 0 || n_periods < 0)
+        return set_error(GEFENX_EINVAL, "gefenx_block_variance_errors: bad arguments");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int64_t max_nb = 0;
+    for (int i = 0; i < n_periods; ++i) {
+        const int64_t P = periods[i];
+        if (P <= 0 || numel % P != 0)
+            return set_error(GEFENX_EINVAL, "period %lld does not divide numel %lld", (long long)P, (long long)numel);
+        if (P > kWavePeriod) max_nb = std::max<int64_t>(max_nb, numel / P);
+    }
+    double* dev = nullptr;  // [n_periods] totals, then 2 * max_nb block sums
+    const size_t bytes = sizeof(double) * ((size_t)n_periods + 2 * (size_t)max_nb + 1);
+    if (hipMalloc(&dev, bytes) != hipSuccess)
+        return set_error(GEFENX_ENOMEM, "gefenx_block_variance_errors: hipMalloc(%zu) failed", bytes);
+    double* totals = dev;
+    double* s1 = dev + n_periods;
+    double* s2 = s1 + max_nb;
+    const int64_t fill = (int64_t)n_periods + 2 * max_nb;
+    hipLaunchKernelGGL(k_zero_f64, dim3(grid_cap(fill, kT, 4096)), dim3(kT), 0, s, dev, fill);
+    for (int i = 0; i < n_periods && rc == GEFENX_OK; ++i) {
+        const int64_t P = periods[i];
+        const int64_t nb = numel / P;
+        if (P == 1) continue;  // single-element blocks have zero variance
+        if (P <= kWavePeriod) {
+            GX_DISPATCH(dtype, k_var_wave, dim3(grid_cap(nb * 64, kT, 16384)), dim3(kT), s, grad, nb, P, totals + i);
+        } else {
+            const int64_t spb = (P + kSeg - 1) / kSeg;
+            GX_DISPATCH(dtype, k_var_seg, dim3((unsigned)(nb * spb)), dim3(kT), s, grad, P, spb, s1, s2);
+            hipLaunchKernelGGL(k_var_finish, dim3(grid_cap(nb, kT, 4096)), dim3(kT), 0, s, s1, s2, nb, P, totals + i);
+        }
+        rc = check("block variance");
+    }
+    std::vector<double> host((size_t)std::max(n_periods, 1));
+    if (rc == GEFENX_OK && n_periods > 0) {
+        if (hipMemcpyAsync(host.data(), totals, sizeof(double) * (size_t)n_periods, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            rc = set_error(GEFENX_ELAUNCH, "gefenx_block_variance_errors: copy-back failed");
+    }
+    hipStreamSynchronize(s);
+    hipFree(dev);
+    if (rc) return rc;
+    for (int i = 0; i < n_periods; ++i) {
+        const double nb = (double)(numel / periods[i]);
+        err_host[i] = std::sqrt(host[(size_t)i] / nb);
+    }
+    return GEFENX_OK;
+}
+
+int gefenx_exact_histogram(const void* grad, int dtype, int64_t numel, int64_t period,
+                           int64_t* bin_counts, int bins, void* stream) {
+    int rc = dtype_ok(dtype, "gefenx_exact_histogram");
+    if (rc) return rc;
+    if (!grad || !bin_counts || bins <= 0 || bins > 4096)
+        return set_error(GEFENX_EINVAL, "Expected histogram bins in [1, 4096], got %d", bins);
+    if (numel == 0) return GEFENX_OK;
+    if (period <= 0 || numel % period != 0)
+        return set_error(GEFENX_EINVAL, "Expected grad_flat.numel()=%lld to be divisible by period=%lld.",
+                         (long long)numel, (long long)period);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t nb = numel / period;
+    unsigned long long* cnt = reinterpret_cast<unsigned long long*>(bin_counts);
+    if (period <= kWavePeriod) {
+        GX_DISPATCH(dtype, k_hist_wave, dim3(grid_cap(nb * 64, kT, 8192)), dim3(kT), s, grad, nb, period, bins, cnt);
+        return check("exact histogram");
+    }
+    uint32_t* bits = nullptr;
+    if (hipMallocAsync((void**)&bits, sizeof(uint32_t) * (size_t)nb, s) != hipSuccess)
+        return set_error(GEFENX_ENOMEM, "gefenx_exact_histogram: allocation failed");
+    hipLaunchKernelGGL(k_zero_u32, dim3(grid_cap(nb, kT, 1024)), dim3(kT), 0, s, bits, nb);
+    const int64_t spb = (period + kSeg - 1) / kSeg;
+    GX_DISPATCH(dtype, k_absmax_seg, dim3((unsigned)(nb * spb)), dim3(kT), s, grad, period, spb, bits);
+    GX_DISPATCH(dtype, k_hist_seg, dim3((unsigned)(nb * spb)), dim3(kT), s, grad, period, spb, bits, bins, cnt);
+    rc = check("exact histogram");
+    hipFreeAsync(bits, s);
+    return rc;
+}
+
+int gefenx_factored_v_ema(float* v_row, float* v_col, const float* row_sq, const float* col_sq,
+                          int64_t rows, int64_t cols, double beta2, void* stream) {
+    if (!v_row || !v_col || !row_sq || !col_sq || rows < 0 || cols < 0)
+        return set_error(GEFENX_EINVAL, "gefenx_factored_v_ema: bad arguments");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const float b2 = (float)beta2, a2 = (float)(1.0 - beta2);
+    // row_sq / cols and col_sq / rows as true divides (gefen.py:2994-2996)
+    if (rows) hipLaunchKernelGGL(k_v_ema, dim3(grid_cap(rows, kT, 1024)), dim3(kT), 0, s, v_row, row_sq, rows,
+                                 0.0f, b2, a2, 1, (float)cols);
+    if (cols) hipLaunchKernelGGL(k_v_ema, dim3(grid_cap(cols, kT, 1024)), dim3(kT), 0, s, v_col, col_sq, cols,
+                                 0.0f, b2, a2, 1, (float)rows);
+    return check("gefenx_factored_v_ema");
+}
+
+int gefenx_vmean_update(float* vmean, const void* grad, int dtype, int64_t numel, int64_t period,
+                        double beta2, void* stream) {
+    int rc = dtype_ok(dtype, "gefenx_vmean_update");
+    if (rc) return rc;
+    if (!vmean || !grad || period <= 0 || numel < 0 || numel % period != 0)
+        return set_error(GEFENX_EINVAL, "gefenx_vmean_update: bad arguments");
+    if (numel == 0) return GEFENX_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t nb = numel / period;
+    GX_DISPATCH(dtype, k_vmean, dim3(grid_cap(nb * 64, kT, 8192)), dim3(kT), s, vmean, grad, nb, period,
+                (float)beta2, (float)(1.0 - beta2));
+    return check("gefenx_vmean_update");
+}
+
+}  // extern "C"

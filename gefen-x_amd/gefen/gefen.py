@@ -1,0 +1,524 @@
+"""Gefen: Adam-family optimizer with 8-bit codebook-quantised momentum and a
+block-shared or factored second moment (~1 byte of state per parameter).
+
+Drop-in for the reference class (gefen.py:984-5852): same constructor
+arguments, param-group layout, per-parameter state keys and state_dict format.
+The step runs on MI355X through the C ABI in include/gefenx.h:
+
+  step 1   period search per parameter (float64 block variances on the GPU,
+           partitioning rule of partitioning.py:237-313) and the exact-DP
+           codebook from the block-absmax-normalised 4096-bin histogram
+           (gefen.py:417-517);
+  2D       factored second moment (row/column EMAs, gefen.py:2784-3018);
+  1D / factored_v_2d=False
+           block-shared second moment (gefen.py:3488-3818).
+
+This build is the fused GPU step only: parameters must live on a HIP device,
+and a missing gfx950 library raises instead of falling back to host math.
+"""
+from __future__ import annotations
+
+import logging
+import math
+import warnings
+from typing import Iterable, Optional, Tuple, Union
+
+import torch
+import torch.nn as nn
+
+from gefen import partitioning
+from gefen import quantization as quantization_module
+from gefen.kernels import _native
+from gefen.kernels import automatic_gefen_fused as _fused
+
+logger = logging.getLogger(__name__)
+
+NUM_CODEBOOKS = 256
+HISTOGRAM_BINS = NUM_CODEBOOKS * 16
+GEFEN_EXACT_HISTOGRAM_CHUNK = 1 << 28
+_CHECKPOINT_FORMAT_VERSION = 1
+
+# Keys of per-parameter state that exist only at run time (workspaces).
+_RUNTIME_STATE_KEYS = ("_gefenx_ws",)
+
+
+def automatic_partition_view(flat_tensor: torch.Tensor, period: int) -> torch.Tensor:
+    """gefen.py:97-115."""
+    if flat_tensor.dim() != 1:
+        raise ValueError("Automatic partition view expects a 1D tensor, got dim={}".format(flat_tensor.dim()))
+    if period <= 0:
+        raise ValueError("Automatic partition period must be positive, got {}".format(period))
+    if flat_tensor.numel() % period != 0:
+        raise ValueError("Automatic partition expects numel {} to be divisible by period {}".format(
+            flat_tensor.numel(), period))
+    return flat_tensor.view(-1, period)
+
+
+def _stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class Gefen(torch.optim.Optimizer):
+    """Gefen optimizer (see module docstring).
+
+    Args mirror the reference (gefen.py:1074-1092): ``lr``, ``betas``, ``eps``,
+    ``weight_decay``, and keyword-only ``fused``, ``force_1d_period_one``,
+    ``force_2d_period_one``, ``period_one_substrings``, ``factored_v_2d``,
+    ``codebook_refresh_every``, ``stochastic_round``, ``deterministic``,
+    ``capturable``, ``verbose``.
+    """
+
+    def __init__(
+        self,
+        params: Iterable[Union[nn.Parameter, Tuple[str, nn.Parameter]]],
+        lr: Union[float, torch.Tensor] = 1e-3,
+        betas: Tuple[float, float] = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 0.0,
+        *,
+        fused: bool = True,
+        force_1d_period_one: bool = False,
+        force_2d_period_one: bool = False,
+        period_one_substrings: Tuple[str, ...] = (),
+        factored_v_2d: bool = True,
+        codebook_refresh_every: int = 0,
+        stochastic_round: bool = False,
+        deterministic: bool = False,
+        capturable: bool = False,
+        verbose: bool = False,
+    ):
+        if not isinstance(deterministic, bool):
+            raise TypeError("deterministic must be a bool")
+        if deterministic and factored_v_2d and stochastic_round:
+            raise ValueError(
+                "deterministic=True with factored_v_2d=True cannot honor stochastic_round=True: the "
+                "replica-exact factored path uses deterministic nearest-codeword quantization. Disable "
+                "stochastic rounding or factored_v_2d.")
+        if not fused:
+            raise ValueError("fused=False selects the reference's host-math step, which this MI355X "
+                             "build does not provide; use fused=True")
+        self._validate_group_options(lr, betas, eps, weight_decay)
+        if codebook_refresh_every < 0:
+            raise ValueError("codebook_refresh_every must be >= 0 but is: {}".format(codebook_refresh_every))
+        if capturable and codebook_refresh_every:
+            raise ValueError("capturable=True is incompatible with codebook_refresh_every>0: the periodic "
+                             "codebook re-learn is host-driven and cannot run inside a replayed CUDA graph.")
+        self.fused = True
+        self._force_1d_period_one = force_1d_period_one
+        self._force_2d_period_one = force_2d_period_one
+        self._period_one_substrings = tuple(s.lower() for s in period_one_substrings)
+        self._factored_v_2d = factored_v_2d
+        self._deterministic = deterministic
+        self._codebook_refresh_every = codebook_refresh_every
+        self.capturable = capturable
+        self._stochastic_round = stochastic_round
+        self.verbose = verbose
+        self._gefen_codebook = None
+        self._gefen_codebook_by_device = {}
+        self._gefen_global_step = 0
+        self._param_names = {}
+        defaults = dict(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps, weight_decay=weight_decay)
+        super().__init__(self._normalize_param_groups(params), defaults)
+
+    # ------------------------------------------------------------ groups
+
+    @staticmethod
+    def _validate_group_options(lr, betas, eps, weight_decay):
+        lr_val = float(lr.item()) if torch.is_tensor(lr) else lr
+        if torch.is_tensor(lr) and lr.numel() != 1:
+            raise ValueError("Tensor lr must be 1-element")
+        if not 0.0 <= lr_val:
+            raise ValueError("Invalid learning rate: {}".format(lr_val))
+        if not 0.0 <= eps:
+            raise ValueError("Invalid epsilon value: {}".format(eps))
+        if len(betas) != 2:
+            raise ValueError("betas must be a pair")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError("Invalid beta parameter at index 0: {}".format(betas[0]))
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError("Invalid beta parameter at index 1: {}".format(betas[1]))
+        if not 0.0 <= weight_decay:
+            raise ValueError("Invalid weight_decay value: {}".format(weight_decay))
+
+    def _normalize_param_groups(self, params):
+        if isinstance(params, torch.Tensor):
+            raise TypeError("params argument given to the optimizer should be an iterable of Tensors "
+                            "or dicts, but got " + torch.typename(params))
+        params = list(params)
+        if len(params) == 0:
+            raise ValueError("optimizer got an empty parameter list")
+        if isinstance(params[0], dict):
+            groups = []
+            for gi, g in enumerate(params):
+                g = dict(g)
+                names, ps = self._split_names(g["params"], prefix="group_{}_param_".format(gi))
+                g["params"] = ps
+                g["param_names"] = names
+                if "betas" in g:
+                    b = g.pop("betas")
+                    g["beta1"], g["beta2"] = b
+                self._validate_group_options(g.get("lr", 0.0), (g.get("beta1", 0.0), g.get("beta2", 0.0)),
+                                             g.get("eps", 0.0), g.get("weight_decay", 0.0))
+                groups.append(g)
+            return groups
+        names, ps = self._split_names(params, prefix="param_")
+        return [{"params": ps, "param_names": names}]
+
+    def _split_names(self, items, prefix):
+        if isinstance(items, torch.Tensor):
+            items = [items]
+        names, ps = [], []
+        seen = set(self._param_names.values())
+        for i, it in enumerate(list(items)):
+            if isinstance(it, (tuple, list)) and len(it) == 2 and isinstance(it[0], str):
+                name, p = str(it[0]).lower(), it[1]
+            else:
+                name, p = "{}{}".format(prefix, i), it
+            if not isinstance(p, torch.Tensor):
+                raise TypeError("optimizer can only optimize Tensors, got {}".format(type(p)))
+            base, k = name, 1
+            while name in seen:
+                name = "{}_{}".format(base, k)
+                k += 1
+            seen.add(name)
+            self._param_names[p] = name
+            names.append(name)
+            ps.append(p)
+        return names, ps
+
+    def _iter_group_params_with_names(self, group):
+        names = group.get("param_names") or [self._param_names.get(p, "param") for p in group["params"]]
+        return zip(names, group["params"])
+
+    # ---------------------------------------------------------- codebook
+
+    def _gefen_codebook_on(self, device):
+        cb = self._gefen_codebook
+        if cb is None or cb.device == device:
+            return cb
+        cached = self._gefen_codebook_by_device.get(device)
+        if cached is None:
+            cached = cb.to(device)
+            self._gefen_codebook_by_device[device] = cached
+        return cached
+
+    def _resolve_automatic_period(self, param_name, param, grad) -> int:
+        """gefen.py:2563-2577 (force flags, then the block-variance search)."""
+        if self._force_1d_period_one and param.ndim == 1:
+            return 1
+        if self._force_2d_period_one and param.ndim == 2:
+            return 1
+        if self._period_one_substrings:
+            lname = str(param_name).lower()
+            if any(s in lname for s in self._period_one_substrings):
+                return 1
+        flat = grad.detach().reshape(-1)
+        if flat.numel() == 1:
+            return 1
+        return partitioning.find_period_by_block_variance(
+            flat, print_results=False, parameter_name=param_name, parameter_shape=tuple(param.shape),
+            backend="cuda_kernel", input_is_squared=False)
+
+    def _iter_gefen_grad_periods(self, reuse_existing_periods=False):
+        for group in self.param_groups:
+            for name, p in self._iter_group_params_with_names(group):
+                if p.grad is None:
+                    continue
+                grad = p.grad.detach()
+                flat = grad.reshape(-1)
+                if flat.numel() == 0:
+                    continue
+                state = self.state[p]
+                if reuse_existing_periods and "automatic_period" in state:
+                    period = state["automatic_period"]
+                elif "automatic_period" in state:
+                    period = state["automatic_period"]
+                elif flat.numel() == 1:
+                    period = 1
+                else:
+                    period = self._resolve_automatic_period(name, p, grad)
+                state["automatic_period"] = int(period)
+                if flat.numel() % period != 0:
+                    raise ValueError("Automatic partition period {} does not divide parameter {} with numel {} "
+                                     "while learning Gefen codebook".format(period, name, flat.numel()))
+                yield name, flat, int(period), grad
+
+    def _learn_gefen_exact_codebook(self, reuse_existing_periods=False):
+        """learn_gefen_exact_codebook_from_grad_periods: gefen.py:417-517."""
+        lib = _native.load()
+        counts_dev = None
+        total = 0
+        for _, flat, period, _ in self._iter_gefen_grad_periods(reuse_existing_periods):
+            if counts_dev is None:
+                counts_dev = torch.zeros(HISTOGRAM_BINS, dtype=torch.int64, device=flat.device)
+            elif counts_dev.device != flat.device:
+                raise ValueError("all parameters must live on one device")
+            f = flat if flat.is_contiguous() else flat.contiguous()
+            chunk = max(1, GEFEN_EXACT_HISTOGRAM_CHUNK // period) * period
+            for start in range(0, f.numel(), chunk):
+                part = f[start:start + chunk]
+                _native.check(lib.gefenx_exact_histogram(
+                    part.data_ptr(), _fused._dtype_code(part.dtype), part.numel(), period,
+                    counts_dev.data_ptr(), HISTOGRAM_BINS, _stream_of(part)), "exact histogram")
+            total += f.numel()
+        if total == 0:
+            return None
+        counts = counts_dev.cpu().to(torch.float32)
+        edges = torch.linspace(-1.0, 1.0, steps=HISTOGRAM_BINS + 1, dtype=torch.float32)
+        centers = 0.5 * (edges[:-1] + edges[1:])
+        active = counts > 0
+        stats = {"bin_edges": edges, "bin_centers": centers, "bin_counts": counts, "active_bins": active,
+                 "active_centers": centers[active], "active_counts": counts[active],
+                 "active_sums": centers[active] * counts[active]}
+        cb = quantization_module.exact_dp(histogram_stats=stats, num_codebooks=NUM_CODEBOOKS,
+                                          force_endpoints=True)
+        return cb.to(counts_dev.device)
+
+    def _maybe_refresh_gefen_codebook(self):
+        if self._gefen_codebook is not None:
+            return
+        cb = self._learn_gefen_exact_codebook(
+            reuse_existing_periods=any("automatic_period" in self.state.get(p, {})
+                                       for g in self.param_groups for p in g["params"]))
+        if cb is not None:
+            self._gefen_codebook = cb
+            self._gefen_codebook_by_device.clear()
+
+    def _refresh_codebook_with_requant(self):
+        """gefen.py:3020-3070: re-learn, then map stored indices onto the new
+        codebook through nearest-codeword search of the old coefficients."""
+        old = self._gefen_codebook
+        if old is None:
+            return
+        new = self._learn_gefen_exact_codebook(reuse_existing_periods=True)
+        if new is None:
+            return
+        old_h = old.detach().cpu().float().numpy()
+        new_h = new.detach().cpu().float()
+        remap = torch.searchsorted(new_h, torch.from_numpy(old_h))
+        k = new_h.numel()
+        left = (remap - 1).clamp(0, k - 1)
+        right = remap.clamp(0, k - 1)
+        x = torch.from_numpy(old_h)
+        choose = torch.where((x - new_h[left]).abs() <= (x - new_h[right]).abs(), left, right).to(torch.uint8)
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if st and "m_codebook" in st:
+                    st["m_codebook"].copy_(choose.to(st["m_codebook"].device)[st["m_codebook"].long()])
+        self._gefen_codebook = new
+        self._gefen_codebook_by_device.clear()
+
+    # -------------------------------------------------------------- step
+
+    def _validate_grads(self):
+        """gefen.py:897-981: reject bad grads before mutating anything."""
+        for group in self.param_groups:
+            for name, p in self._iter_group_params_with_names(group):
+                g = p.grad
+                if g is None:
+                    continue
+                if getattr(g, "is_sparse", False) or g.layout != torch.strided:
+                    raise RuntimeError("Gefen does not support sparse gradients")
+                if torch.is_complex(g):
+                    raise RuntimeError("Gefen does not support complex gradients")
+                if g.shape != p.shape:
+                    raise RuntimeError("gradient shape {} does not match parameter {} shape {}".format(
+                        tuple(g.shape), name, tuple(p.shape)))
+                if g.device != p.device:
+                    raise RuntimeError("gradient of {} is on {}, parameter on {}".format(name, g.device, p.device))
+                if p.numel() and p.device.type != "cuda":
+                    raise RuntimeError("Gefen (MI355X build) steps HIP device parameters only; {} is on {}".format(
+                        name, p.device))
+                if p.dtype == torch.float64:
+                    raise NotImplementedError("Gefen fused kernels are not implemented for 'Double' ({})".format(name))
+                if g.dtype != p.dtype:
+                    raise RuntimeError("gradient dtype {} does not match parameter {} dtype {}".format(
+                        g.dtype, name, p.dtype))
+
+    @staticmethod
+    def _lr_value(group) -> float:
+        lr = group["lr"]
+        return float(lr.item()) if torch.is_tensor(lr) else float(lr)
+
+    def _init_state(self, state, p, grad, name, factored):
+        numel = grad.numel()
+        if "automatic_period" in state:
+            period = int(state["automatic_period"])
+        elif numel == 1:
+            period = 1
+        else:
+            period = self._resolve_automatic_period(name, p, grad)
+        if numel % period != 0:
+            raise ValueError("Automatic partition period {} does not divide parameter {} with numel {}".format(
+                period, name, numel))
+        nb = numel // period
+        state["automatic_period"] = period
+        state["step"] = 0
+        state["m_codebook"] = torch.zeros(nb, period, dtype=torch.uint8, device=p.device)
+        state["m_magnitude"] = torch.zeros(nb, 1, dtype=torch.float32, device=p.device)
+        if factored:
+            state["v_row"] = torch.zeros(p.shape[0], dtype=torch.float32, device=p.device)
+            state["v_col"] = torch.zeros(p.shape[1], dtype=torch.float32, device=p.device)
+            state["factored_step"] = 0
+        else:
+            state["vmean"] = torch.zeros(nb, 1, dtype=torch.float32, device=p.device)
+            state["vmean_step"] = 0
+
+    def _workspace(self, state, kind, rows, cols, nb, device):
+        ws = state.get("_gefenx_ws")
+        need = int(_native.load().gefenx_workspace_bytes(kind, rows, cols, nb))
+        if ws is None or ws.numel() < need or ws.device != device:
+            ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
+            state["_gefenx_ws"] = ws
+        return ws
+
+    def _step_automatic_factored(self, group, name, p, grad):
+        """gefen.py:2784-3018 on the MI355X factored kernels."""
+        if grad.numel() == 0:
+            return
+        state = self.state[p]
+        if "step" not in state:
+            self._init_state(state, p, grad, name, factored=True)
+        if "v_row" not in state:  # resume from a block-vmean checkpoint (gefen.py:2840-2852)
+            state["v_row"] = torch.zeros(p.shape[0], dtype=torch.float32, device=p.device)
+            state["v_col"] = torch.zeros(p.shape[1], dtype=torch.float32, device=p.device)
+            state["factored_step"] = 0
+        state["step"] += 1
+        state["factored_step"] += 1
+        beta1, beta2, eps = group["beta1"], group["beta2"], group["eps"]
+        lr = self._lr_value(group)
+        bc1 = 1 - beta1 ** state["step"]
+        bc2 = 1 - beta2 ** state["factored_step"]
+        rows, cols = p.shape
+        period = state["automatic_period"]
+        nb = p.numel() // period
+        ws = self._workspace(state, _native.WS_FACTORED, rows, cols, nb, p.device)
+        qt = _fused.quant_table(self._gefen_codebook_on(p.device), p.dtype)
+        _native.check(_native.load().gefenx_factored_update(
+            p.data_ptr(), grad.data_ptr(), _fused._dtype_code(p.dtype), rows, cols,
+            p.stride(0), p.stride(1), grad.stride(0), grad.stride(1),
+            state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(),
+            state["v_row"].data_ptr(), state["v_col"].data_ptr(), period, qt.data_ptr(),
+            beta1, beta2, lr, eps, 1.0 / bc2, 1.0 / bc1, 1.0 - lr * group["weight_decay"],
+            1 if self._stochastic_round else 0, self._gefen_global_step, None, None,
+            ws.data_ptr(), ws.numel(), _stream_of(p)), "factored update of " + name)
+
+    def _step_automatic(self, group, name, p, grad):
+        """gefen.py:3488-3818 on the MI355X block kernels."""
+        if grad.numel() == 0:
+            return
+        state = self.state[p]
+        if "step" not in state:
+            self._init_state(state, p, grad, name, factored=False)
+        if "vmean" not in state:  # resume from a factored checkpoint (gefen.py:3567-3586)
+            state["vmean"] = torch.zeros_like(state["m_magnitude"])
+            state["vmean_step"] = 0
+        elif "vmean_step" not in state:
+            state["vmean_step"] = state["step"]
+        state["step"] += 1
+        state["vmean_step"] += 1
+        beta1, beta2, eps = group["beta1"], group["beta2"], group["eps"]
+        lr = self._lr_value(group)
+        bc1 = 1 - beta1 ** state["step"]
+        bc2 = 1 - beta2 ** state["vmean_step"]
+        period = state["automatic_period"]
+        nb = p.numel() // period
+        p_k = p if p.is_contiguous() else p.contiguous()
+        g_k = grad if grad.is_contiguous() else grad.contiguous()
+        ws = self._workspace(state, _native.WS_BLOCK, 0, 0, nb, p.device)
+        qt = _fused.quant_table(self._gefen_codebook_on(p.device), p.dtype)
+        _native.check(_native.load().gefenx_block_update(
+            p_k.data_ptr(), g_k.data_ptr(), _fused._dtype_code(p.dtype), p.numel(), period,
+            state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(), state["vmean"].data_ptr(),
+            qt.data_ptr(), beta1, beta2, lr, eps, 1.0 / math.sqrt(bc2), 1.0 / bc1,
+            1.0 - lr * group["weight_decay"], 1 if self._stochastic_round else 0,
+            self._gefen_global_step, None, None, ws.data_ptr(), ws.numel(), _stream_of(p)),
+            "block update of " + name)
+        if p_k is not p:
+            p.copy_(p_k)
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        self._validate_grads()
+        self._maybe_refresh_gefen_codebook()
+        if (self._codebook_refresh_every and self._gefen_global_step > 0
+                and self._gefen_global_step % self._codebook_refresh_every == 0):
+            self._refresh_codebook_with_requant()
+        for group in self.param_groups:
+            for name, p in self._iter_group_params_with_names(group):
+                grad = p.grad
+                if grad is None:
+                    continue
+                if self._factored_v_2d and p.ndim == 2 and not hasattr(p, "placements"):
+                    self._step_automatic_factored(group, name, p, grad)
+                else:
+                    self._step_automatic(group, name, p, grad)
+        self._gefen_global_step += 1
+        return loss
+
+    # -------------------------------------------------------- checkpoint
+
+    def state_dict(self):
+        """gefen.py:4558-4707: runtime workspaces stripped; codebook, global
+        step and deterministic flag recorded; metadata mirrored per group."""
+        sd = super().state_dict()
+        for st in sd["state"].values():
+            for k in _RUNTIME_STATE_KEYS:
+                st.pop(k, None)
+        codebook = None if self._gefen_codebook is None else self._gefen_codebook.detach().cpu().clone()
+        sd["gefen_global_step"] = self._gefen_global_step
+        sd["gefen_deterministic"] = self._deterministic
+        sd["gefen_codebook"] = codebook
+        meta = {"format_version": _CHECKPOINT_FORMAT_VERSION, "global_step": self._gefen_global_step,
+                "codebook": codebook, "deterministic": self._deterministic}
+        for g in sd["param_groups"]:
+            g["_gefen_checkpoint_metadata"] = meta
+        return sd
+
+    def load_state_dict(self, state_dict):
+        """gefen.py:5456-5707: restore saved state dtypes (torch casts floating
+        state to the param dtype) and the optimizer-level codebook/step."""
+        sd = dict(state_dict)
+        global_step = sd.pop("gefen_global_step", None)
+        sd.pop("gefen_deterministic", None)
+        codebook = sd.pop("gefen_codebook", None)
+        meta = None
+        groups = []
+        for g in sd["param_groups"]:
+            g = dict(g)
+            meta = g.pop("_gefen_checkpoint_metadata", meta)
+            groups.append(g)
+        sd["param_groups"] = groups
+        saved = {k: {kk: (vv.dtype if torch.is_tensor(vv) else None) for kk, vv in v.items()}
+                 for k, v in sd["state"].items()}
+        super().load_state_dict(sd)
+        id_map = {}
+        for gi, g in enumerate(self.param_groups):
+            for p in g["params"]:
+                id_map[len(id_map)] = p
+        for pid, dtypes in saved.items():
+            p = id_map.get(pid)
+            if p is None:
+                continue
+            st = self.state[p]
+            for k, dt in dtypes.items():
+                if dt is not None and torch.is_tensor(st.get(k)) and st[k].dtype != dt:
+                    st[k] = st[k].to(dt)
+            for k in ("step", "vmean_step", "factored_step"):
+                if torch.is_tensor(st.get(k)):
+                    st[k] = int(st[k].item())
+        if global_step is None and meta is not None:
+            global_step = meta.get("global_step")
+        if codebook is None and meta is not None:
+            codebook = meta.get("codebook")
+        if global_step is not None:
+            self._gefen_global_step = int(global_step)
+        if codebook is not None:
+            dev = next((p.device for g in self.param_groups for p in g["params"]), torch.device("cpu"))
+            self._gefen_codebook = codebook.to(device=dev, dtype=torch.float32)
+            self._gefen_codebook_by_device.clear()

@@ -1,0 +1,339 @@
+"""Python surface of the fused Gefen kernels, backed by the MI355X C ABI.
+
+Same public names and signatures as the reference module
+kernels/automatic_gefen_fused.py (automatic_gefen_fused_full_update_cuda,
+automatic_gefen_fused_update_v2_full_cuda, gefen_factored_update_cuda,
+gefen_quantized_momentum_update_cuda, _codebook_search_lut, _should_use_v2,
+_should_use_v2_full, _CAPT_V1_FULL_TINY_NUMEL, ensure_extension_loaded), so
+the optimizer and the reference's tests call them unchanged.  Underneath, every
+call is one C-ABI function (include/gefenx.h) enqueued on torch's current HIP
+stream; nothing here computes on the host.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import weakref
+from typing import Optional
+
+import torch
+
+from . import _native
+
+_LUT_BUCKETS = 4096
+_LUT_CACHE: dict = {}
+_QTABLE_CACHE: dict = {}
+_WS_CACHE: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+# Routing constants of the reference (kernels/automatic_gefen_fused.py:23-50).
+# This build has ONE block-path kernel set; the predicates are kept because
+# the optimizer and tests consult them, and both routes reach the same kernels.
+_V2_PERIOD_MAX = 16
+_V2_BLOCKS_PER_SM = 2
+_CAPT_V1_FULL_TINY_NUMEL = 1 << 14
+_FULL_V1_PERIOD_MIN = 16
+_FULL_V1_PERIOD_MAX = 2048
+_FULL_V1_TINY_NUM_BLOCKS = 1 << 13
+_FULL_V2_LARGE_PERIOD_MIN = 1 << 13
+_FULL_V2_PERIOD16_NUMEL = 1 << 24
+_SM_COUNT_BY_DEVICE: dict = {}
+
+_DTYPE_CODE = {torch.float32: _native.DT_F32, torch.float16: _native.DT_F16,
+               torch.bfloat16: _native.DT_BF16, torch.float64: _native.DT_F64}
+
+
+def _env_override(name: str) -> Optional[str]:
+    value = os.environ.get(name)
+    if value is None:
+        return None
+    value = value.strip()
+    return value if value else None
+
+
+_GEFEN_UPDATE_V2_ENV = _env_override("GEFEN_UPDATE_V2")
+
+
+def ensure_extension_loaded() -> None:
+    """Load the gfx950 library now, raising on failure (reference :139-148)."""
+    _native.load()
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    code = _DTYPE_CODE.get(dtype)
+    if code is None:
+        raise ValueError("unsupported dtype {}".format(dtype))
+    return code
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _host_codebook(codebook: torch.Tensor):
+    cb = codebook.detach().reshape(-1).to(device="cpu", dtype=torch.float32).contiguous()
+    return cb
+
+
+def _codebook_search_lut(codebook: torch.Tensor) -> torch.Tensor:
+    """int16 [4097] search LUT on the codebook's device: lut[b] = #entries whose
+    bucket < b (reference kernels/automatic_gefen_fused.py:81-121).  Built by
+    the C ABI on the host once per (codebook storage, version, device)."""
+    key = (codebook.data_ptr(), codebook._version, codebook.device)
+    cached = _LUT_CACHE.get(key)
+    if cached is not None:
+        return cached[1]
+    cb = _host_codebook(codebook)
+    lut = torch.empty(_LUT_BUCKETS + 1, dtype=torch.int16)
+    _native.check(_native.load().gefenx_search_lut(cb.data_ptr(), cb.numel(), _LUT_BUCKETS,
+                                                   lut.data_ptr()), "search lut")
+    lut = lut.to(codebook.device)
+    while len(_LUT_CACHE) >= 16:
+        _LUT_CACHE.pop(next(iter(_LUT_CACHE)))
+    _LUT_CACHE[key] = (codebook, lut)
+    return lut
+
+
+def quant_table(codebook: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Device byte image of the quantisation table for (codebook, grad dtype).
+    One host build + one upload per codebook version (the exact-DP codebook is
+    frozen after step 1)."""
+    key = (codebook.data_ptr(), codebook._version, codebook.device, dtype)
+    cached = _QTABLE_CACHE.get(key)
+    if cached is not None:
+        return cached[1]
+    lib = _native.load()
+    cb = _host_codebook(codebook)
+    if cb.numel() < 1 or cb.numel() > 256:
+        raise ValueError("codebook must hold 1..256 entries, got {}".format(cb.numel()))
+    host = torch.empty(int(lib.gefenx_qtable_bytes()), dtype=torch.uint8)
+    _native.check(lib.gefenx_qtable_build(cb.data_ptr(), cb.numel(), _dtype_code(dtype),
+                                          host.data_ptr()), "qtable build")
+    dev = host.to(codebook.device) if codebook.device.type != "cpu" else host
+    while len(_QTABLE_CACHE) >= 16:
+        _QTABLE_CACHE.pop(next(iter(_QTABLE_CACHE)))
+    _QTABLE_CACHE[key] = (codebook, dev)
+    return dev
+
+
+def workspace_for(anchor: torch.Tensor, kind: int, rows: int, cols: int, num_blocks: int) -> torch.Tensor:
+    """Zero-initialised device workspace cached per state tensor `anchor`; the
+    kernels leave it zeroed after every call, so it is reused across steps."""
+    nbytes = int(_native.load().gefenx_workspace_bytes(kind, rows, cols, num_blocks))
+    ws = _WS_CACHE.get(anchor)
+    if ws is None or ws.numel() < nbytes or ws.device != anchor.device:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=anchor.device)
+        _WS_CACHE[anchor] = ws
+    return ws
+
+
+def _sm_count(device: torch.device) -> int:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    cached = _SM_COUNT_BY_DEVICE.get(index)
+    if cached is None:
+        cached = torch.cuda.get_device_properties(index).multi_processor_count
+        _SM_COUNT_BY_DEVICE[index] = cached
+    return cached
+
+
+def _should_use_v2(num_blocks: int, period: int, device: torch.device) -> bool:
+    """Legacy occupancy predicate (reference :162-173); env GEFEN_UPDATE_V2 overrides."""
+    if _GEFEN_UPDATE_V2_ENV is not None:
+        return _GEFEN_UPDATE_V2_ENV.lower() not in {"0", "false", "no", "off"}
+    if period <= _V2_PERIOD_MAX:
+        return True
+    if device.type != "cuda":
+        return False
+    return num_blocks < _V2_BLOCKS_PER_SM * _sm_count(device)
+
+
+def _should_use_v2_full(num_blocks: int, period: int, device: torch.device) -> bool:
+    """Full-update route predicate (reference :176-199).  Both answers reach the
+    same MI355X kernels here; the value is kept for callers that log it."""
+    if _GEFEN_UPDATE_V2_ENV is not None:
+        return _GEFEN_UPDATE_V2_ENV.lower() not in {"0", "false", "no", "off"}
+    numel = num_blocks * period
+    if period <= 15 and num_blocks <= _FULL_V1_TINY_NUM_BLOCKS:
+        return False
+    if period >= _FULL_V2_LARGE_PERIOD_MIN:
+        return True
+    if _FULL_V1_PERIOD_MIN <= period <= _FULL_V1_PERIOD_MAX:
+        if period == 16 and numel >= _FULL_V2_PERIOD16_NUMEL:
+            return True
+        return False
+    return _should_use_v2(num_blocks, period, device)
+
+
+def _check_common(p, grad_view, m_sign, m_magnitude, codebook, packed_indices=False):
+    if packed_indices:
+        raise ValueError("packed_indices must be false: the 8-bit codebook stores one index per byte")
+    if grad_view.dtype != p.dtype:
+        raise ValueError("grad_view dtype {} must match p dtype {}.".format(grad_view.dtype, p.dtype))
+    for name, t in (("grad_view", grad_view), ("m_sign", m_sign),
+                    ("m_magnitude", m_magnitude), ("codebook", codebook)):
+        if t.device != p.device:
+            raise ValueError("{} device {} must match p device {}.".format(name, t.device, p.device))
+    if p.device.type != "cuda":
+        raise ValueError("fused Gefen kernels require HIP device tensors, got {}".format(p.device))
+    if m_magnitude.dtype != torch.float32 or codebook.dtype != torch.float32:
+        raise ValueError("m_magnitude and codebook must be float32.")
+    if m_sign.dtype != torch.uint8:
+        raise ValueError("m_sign must be uint8, got {}".format(m_sign.dtype))
+    if p.dtype == torch.float64:
+        raise NotImplementedError("Gefen fused kernels are not implemented for 'Double'")
+    if grad_view.numel() != p.numel() or m_sign.numel() != p.numel():
+        raise ValueError("grad_view / m_sign numel must equal p numel ({}).".format(p.numel()))
+    if not m_sign.is_contiguous() or not m_magnitude.is_contiguous():
+        raise ValueError("m_sign and m_magnitude must be contiguous.")
+
+
+def _period_of(grad_view: torch.Tensor, m_magnitude: torch.Tensor) -> int:
+    if grad_view.dim() == 2:
+        period = int(grad_view.shape[1])
+    else:
+        period = grad_view.numel() // max(1, m_magnitude.numel())
+    if period <= 0 or grad_view.numel() % period != 0 or m_magnitude.numel() * period != grad_view.numel():
+        raise ValueError("m_magnitude ({}) does not match grad_view blocks {}".format(
+            m_magnitude.numel(), tuple(grad_view.shape)))
+    return period
+
+
+def _scalar_ptrs(step_scalars, seed_dev):
+    if step_scalars is not None:
+        if step_scalars.dtype != torch.float32 or step_scalars.numel() < 4 or not step_scalars.is_contiguous():
+            raise ValueError("step_scalars must be a contiguous float32 tensor with >= 4 entries")
+    if seed_dev is not None:
+        if seed_dev.dtype != torch.int64 or seed_dev.numel() < 1:
+            raise ValueError("seed_dev must be an int64 tensor with >= 1 entry")
+    return _ptr(step_scalars), _ptr(seed_dev)
+
+
+def _strides_2d(t: torch.Tensor, rows: int, cols: int):
+    if t.dim() == 2:
+        return int(t.stride(0)), int(t.stride(1))
+    if t.is_contiguous():
+        return cols, 1
+    raise ValueError("expected a 2D tensor or a contiguous tensor")
+
+
+def gefen_factored_update_cuda(p, grad_view, m_sign, m_magnitude, v_row, v_col, codebook, cols,
+                               beta1, beta2, lr, eps, inv_bias_correction_2,
+                               inv_bias_correction_1, weight_decay_factor,
+                               stochastic_round=False, rng_seed=0, step_scalars=None,
+                               codebook_lut=None, seed_dev=None) -> None:
+    """Factored second-moment fused update of one 2D param (reference :581-650).
+    p may be a strided (e.g. transposed) view: the kernel walks it in logical
+    row-major order, so no contiguous copy is made."""
+    _check_common(p, grad_view, m_sign, m_magnitude, codebook)
+    cols = int(cols)
+    numel = p.numel()
+    if numel == 0:
+        return
+    if cols <= 0 or numel % cols != 0:
+        raise ValueError("cols {} does not divide numel {}".format(cols, numel))
+    rows = numel // cols
+    if v_row.numel() != rows or v_col.numel() != cols:
+        raise ValueError("v_row/v_col sizes ({}, {}) do not match [{}, {}]".format(
+            v_row.numel(), v_col.numel(), rows, cols))
+    if v_row.dtype != torch.float32 or v_col.dtype != torch.float32:
+        raise ValueError("v_row and v_col must be float32")
+    period = _period_of(grad_view, m_magnitude)
+    grad_c = grad_view if grad_view.is_contiguous() else grad_view.contiguous()
+    ps0, ps1 = _strides_2d(p, rows, cols)
+    ss, sd = _scalar_ptrs(step_scalars, seed_dev)
+    qt = quant_table(codebook, p.dtype)
+    ws = workspace_for(m_magnitude, _native.WS_FACTORED, rows, cols, m_magnitude.numel())
+    lib = _native.load()
+    _native.check(lib.gefenx_factored_update(
+        p.data_ptr(), grad_c.data_ptr(), _dtype_code(p.dtype), rows, cols, ps0, ps1, cols, 1,
+        m_sign.data_ptr(), m_magnitude.data_ptr(), v_row.data_ptr(), v_col.data_ptr(), period,
+        qt.data_ptr(), float(beta1), float(beta2), float(lr), float(eps),
+        float(inv_bias_correction_2), float(inv_bias_correction_1), float(weight_decay_factor),
+        1 if stochastic_round else 0, int(rng_seed), ss, sd, ws.data_ptr(), ws.numel(),
+        _stream(p.device)), "gefen_factored_update_cuda")
+
+
+def _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1,
+                  beta2, lr, eps, inv_sqrt_bc2, inv_bc1, wdf, stochastic_round, rng_seed,
+                  step_scalars, seed_dev, what):
+    _check_common(p, grad_view, m_sign, m_magnitude, codebook, packed_indices)
+    if p.numel() == 0:
+        return
+    if vmean.dtype != torch.float32 or vmean.numel() != m_magnitude.numel():
+        raise ValueError("vmean must be float32 with one entry per block")
+    if not p.is_contiguous():
+        raise ValueError("p must be contiguous on the block path")
+    period = _period_of(grad_view, m_magnitude)
+    grad_c = grad_view if grad_view.is_contiguous() else grad_view.contiguous()
+    ss, sd = _scalar_ptrs(step_scalars, seed_dev)
+    qt = quant_table(codebook, p.dtype)
+    ws = workspace_for(m_magnitude, _native.WS_BLOCK, 0, 0, m_magnitude.numel())
+    lib = _native.load()
+    _native.check(lib.gefenx_block_update(
+        p.data_ptr(), grad_c.data_ptr(), _dtype_code(p.dtype), p.numel(), period,
+        m_sign.data_ptr(), m_magnitude.data_ptr(), vmean.data_ptr(), qt.data_ptr(),
+        float(beta1), float(beta2), float(lr), float(eps), float(inv_sqrt_bc2), float(inv_bc1),
+        float(wdf), 1 if stochastic_round else 0, int(rng_seed), ss, sd, ws.data_ptr(),
+        ws.numel(), _stream(p.device)), what)
+
+
+def automatic_gefen_fused_full_update_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook,
+                                           packed_indices, beta1, beta2, lr, eps,
+                                           inv_sqrt_bias_correction_2, inv_bias_correction_1,
+                                           weight_decay_factor, stochastic_round=False,
+                                           rng_seed=0, step_scalars=None, codebook_lut=None,
+                                           seed_dev=None) -> None:
+    """Block-vmean fused update (reference :511-579, v1-full)."""
+    _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1,
+                  beta2, lr, eps, inv_sqrt_bias_correction_2, inv_bias_correction_1,
+                  weight_decay_factor, stochastic_round, rng_seed, step_scalars, seed_dev,
+                  "automatic_gefen_fused_full_update_cuda")
+
+
+def automatic_gefen_fused_update_v2_full_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook,
+                                              packed_indices, beta1, beta2, lr, eps,
+                                              inv_sqrt_bias_correction_2, inv_bias_correction_1,
+                                              weight_decay_factor, stochastic_round=False,
+                                              rng_seed=0, step_scalars=None, codebook_lut=None,
+                                              seed_dev=None) -> None:
+    """Block-vmean fused update (reference :712-771, v2-full): same kernels."""
+    _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1,
+                  beta2, lr, eps, inv_sqrt_bias_correction_2, inv_bias_correction_1,
+                  weight_decay_factor, stochastic_round, rng_seed, step_scalars, seed_dev,
+                  "automatic_gefen_fused_update_v2_full_cuda")
+
+
+def gefen_quantized_momentum_update_cuda(grad_view, m_sign, m_magnitude, codebook, momentum_out,
+                                         beta1, stochastic_round=False, rng_seed=0,
+                                         seed_dev=None, codebook_lut=None,
+                                         nesterov=False) -> None:
+    """Muon momentum: advance the quantised EMA and emit the dense momentum
+    (reference :652-710)."""
+    for name, t in (("m_sign", m_sign), ("m_magnitude", m_magnitude),
+                    ("codebook", codebook), ("momentum_out", momentum_out)):
+        if t.device != grad_view.device:
+            raise ValueError("{} device {} must match grad_view device {}.".format(
+                name, t.device, grad_view.device))
+    if momentum_out.dtype != grad_view.dtype or momentum_out.numel() != grad_view.numel():
+        raise ValueError("momentum_out must match grad_view dtype and numel")
+    if not momentum_out.is_contiguous():
+        raise ValueError("momentum_out must be contiguous")
+    if grad_view.dtype == torch.float64:
+        raise NotImplementedError("Gefen momentum kernel is not implemented for 'Double'")
+    if grad_view.numel() == 0:
+        return
+    period = _period_of(grad_view, m_magnitude)
+    grad_c = grad_view if grad_view.is_contiguous() else grad_view.contiguous()
+    _, sd = _scalar_ptrs(None, seed_dev)
+    qt = quant_table(codebook, grad_view.dtype)
+    ws = workspace_for(m_magnitude, _native.WS_MOMENTUM, 0, 0, m_magnitude.numel())
+    lib = _native.load()
+    _native.check(lib.gefenx_quantized_momentum_update(
+        grad_c.data_ptr(), _dtype_code(grad_view.dtype), grad_view.numel(), period,
+        m_sign.data_ptr(), m_magnitude.data_ptr(), qt.data_ptr(), momentum_out.data_ptr(),
+        float(beta1), 1 if stochastic_round else 0, int(rng_seed), sd, 1 if nesterov else 0,
+        ws.data_ptr(), ws.numel(), _stream(grad_view.device)),
+        "gefen_quantized_momentum_update_cuda")

@@ -1,0 +1,248 @@
+/*
+ * gefenx.h -- C ABI of the MI355X-native Gefen optimizer step.
+ *
+ * Plain pointers, sizes and scalars only: no torch types cross this boundary.
+ * Every device pointer must be a HIP device allocation on the current device;
+ * kernels are enqueued on `stream` (hipStream_t passed as void*) and no call
+ * synchronises the host except where stated.  Return value: GEFENX_OK (0) or a
+ * negative status; gefenx_last_error() returns the thread-local message.
+ * Status -> Python exception mapping used by the bindings:
+ *   GEFENX_EINVAL -> ValueError, GEFENX_EDTYPE -> NotImplementedError,
+ *   GEFENX_ELAUNCH / GEFENX_ENOMEM -> RuntimeError.
+ *
+ * Each entry point replaces one reference interface (paths relative to the
+ * reference repo root, src/gefen/ omitted); the cited pybind function has the
+ * same argument order except that tensors become (pointer, sizes) and the
+ * launcher's internal `at::zeros` scratch becomes the caller-provided
+ * workspace.
+ */
+#ifndef GEFENX_H_
+#define GEFENX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEFENX_ABI_VERSION 1
+
+enum gefenx_status {
+    GEFENX_OK = 0,
+    GEFENX_EINVAL = -1,  /* bad shape/size/pointer/argument  -> ValueError          */
+    GEFENX_EDTYPE = -2,  /* unsupported dtype (fp64)          -> NotImplementedError */
+    GEFENX_ELAUNCH = -3, /* HIP launch/runtime failure        -> RuntimeError        */
+    GEFENX_ENOMEM = -4   /* host allocation failure           -> RuntimeError        */
+};
+
+/* Parameter / gradient element type. */
+enum gefenx_dtype { GEFENX_F32 = 0, GEFENX_F16 = 1, GEFENX_BF16 = 2, GEFENX_F64 = 3 };
+
+/* Version of this ABI (GEFENX_ABI_VERSION of the built library). */
+int gefenx_abi_version(void);
+
+/* Thread-local message describing the last non-OK status of this thread. */
+const char* gefenx_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Quantisation table.  The fused kernels never binary-search the codebook:
+ * the host derives, once per (codebook, dtype), the exact fp32 decision
+ * thresholds of the reference's nearest-codeword rule (searchsorted + "ties to
+ * the lower index", gefen.py:288-334) plus a 4096-bucket index over them, the
+ * reference's own search LUT (kernels/automatic_gefen_fused.py:81-121, used by
+ * stochastic rounding) and the codebook rounded through the grad dtype (the
+ * dequantisation of gefen.py:337-373).  The table is a flat byte image that
+ * the caller copies to device memory unchanged.
+ * ---------------------------------------------------------------------- */
+
+/* Size in bytes of a table image. */
+size_t gefenx_qtable_bytes(void);
+
+/* Build the table image for `codebook` (k fp32 values, sorted ascending,
+ * 1 <= k <= 256) and the grad dtype into host memory `table_out`.
+ * Replaces _codebook_search_lut (kernels/automatic_gefen_fused.py:81-121). */
+int gefenx_qtable_build(const float* codebook, int k, int dtype, void* table_out);
+
+/* The reference's int16 search LUT (buckets+1 entries) on the host:
+ * kernels/automatic_gefen_fused.py:81-121. */
+int gefenx_search_lut(const float* codebook, int k, int buckets, int16_t* lut_out);
+
+/* ------------------------------------------------------------------------
+ * Workspace.  Every update entry point takes a device workspace whose size is
+ * given by gefenx_workspace_bytes(kind, ...).  It must be zero-filled before
+ * its first use; each call leaves it zero-filled again, so one workspace per
+ * parameter can be reused across steps (and inside a captured graph).
+ * ---------------------------------------------------------------------- */
+enum gefenx_ws_kind { GEFENX_WS_FACTORED = 0, GEFENX_WS_BLOCK = 1, GEFENX_WS_MOMENTUM = 2 };
+size_t gefenx_workspace_bytes(int kind, int64_t rows, int64_t cols, int64_t num_blocks);
+
+/* ------------------------------------------------------------------------
+ * Factored (row/column) second-moment step for one 2D parameter [rows, cols]
+ * with the 8-bit quantised momentum over blocks of `period` elements in
+ * logical row-major order.  Replaces gefen_factored_update_cuda:
+ * kernels/automatic_gefen_fused_kernel.cu:2534-2790 (binding
+ * kernels/automatic_gefen_fused_binding.cpp:89-110).
+ *   p, grad : [rows, cols] of `dtype`, element strides (ps0, ps1) / (gs0, gs1)
+ *             (transposed or otherwise strided views need no copy);
+ *   m_codebook : uint8 [numel] (contiguous); m_magnitude : fp32 [numel/period];
+ *   v_row fp32 [rows]; v_col fp32 [cols]; all mutated in place.
+ *   step_scalars: NULL, or a device fp32[4] = [lr, 1/bc2, 1/bc1, wd_factor]
+ *   overriding the host scalars (capturable mode);
+ *   seed_dev: NULL or a device int64 overriding rng_seed.
+ * ---------------------------------------------------------------------- */
+int gefenx_factored_update(
+    void* p, const void* grad, int dtype, int64_t rows, int64_t cols,
+    int64_t ps0, int64_t ps1, int64_t gs0, int64_t gs1,
+    uint8_t* m_codebook, float* m_magnitude, float* v_row, float* v_col,
+    int64_t period, const void* qtable_dev,
+    double beta1, double beta2, double lr, double eps,
+    double inv_bias_correction_2, double inv_bias_correction_1,
+    double weight_decay_factor, int stochastic_round, int64_t rng_seed,
+    const float* step_scalars, const int64_t* seed_dev,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block-vmean step (1D params, and 2D params with factored_v_2d=False).
+ * Replaces automatic_gefen_fused_full_update_cuda
+ * (kernels/automatic_gefen_fused_kernel.cu:2233-2409) and
+ * automatic_gefen_fused_update_v2_full_cuda (:3029-3242); both reference
+ * kernels compute the same step, and so does this single entry point.
+ *   p, grad: numel elements, contiguous; vmean fp32 [numel/period].
+ *   step_scalars: NULL or device fp32[4] = [lr, 1/sqrt(bc2), 1/bc1, wd_factor].
+ * ---------------------------------------------------------------------- */
+int gefenx_block_update(
+    void* p, const void* grad, int dtype, int64_t numel, int64_t period,
+    uint8_t* m_codebook, float* m_magnitude, float* vmean, const void* qtable_dev,
+    double beta1, double beta2, double lr, double eps,
+    double inv_sqrt_bias_correction_2, double inv_bias_correction_1,
+    double weight_decay_factor, int stochastic_round, int64_t rng_seed,
+    const float* step_scalars, const int64_t* seed_dev,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Muon momentum: advance the quantised momentum by one EMA step and emit the
+ * dense momentum (optionally Nesterov) in grad dtype.  Replaces
+ * gefen_quantized_momentum_update_cuda
+ * (kernels/automatic_gefen_fused_kernel.cu:2852-3027, binding :75-87).
+ * ---------------------------------------------------------------------- */
+int gefenx_quantized_momentum_update(
+    const void* grad, int dtype, int64_t numel, int64_t period,
+    uint8_t* m_codebook, float* m_magnitude, const void* qtable_dev,
+    void* momentum_out, double beta1, int stochastic_round, int64_t rng_seed,
+    const int64_t* seed_dev, int nesterov,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Factored EMA alone: v <- fma(sq/n, 1-beta2, v*beta2) for row and column
+ * sums.  Replaces gefen_factored_v_ema_cuda
+ * (kernels/automatic_gefen_fused_kernel.cu:2792-2850). */
+int gefenx_factored_v_ema(float* v_row, float* v_col, const float* row_sq,
+                          const float* col_sq, int64_t rows, int64_t cols,
+                          double beta2, void* stream);
+
+/* Block vmean EMA alone.  Replaces automatic_vmean_update_cuda
+ * (kernels/automatic_vmean_kernel.cu:122-214); bf16 squares/means round
+ * through bf16 as the reference's decomposed path does (gefen.py:129-191). */
+int gefenx_vmean_update(float* vmean, const void* grad, int dtype, int64_t numel,
+                        int64_t period, double beta2, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Step-1 helpers.
+ * ---------------------------------------------------------------------- */
+
+/* Block-absmax-normalised histogram accumulated into int64 bin_counts[bins]
+ * (bins <= 4096).  Replaces gefen_exact_histogram_cuda
+ * (kernels/exact_histogram_fused_kernel.cu:144-180). */
+int gefenx_exact_histogram(const void* grad, int dtype, int64_t numel, int64_t period,
+                           int64_t* bin_counts, int bins, void* stream);
+
+/* Within-block variance error for every divisor period in `periods[n]` at
+ * once: err[i] = sqrt(mean over blocks of var(x)), x = grad^2 (fp32 square,
+ * float64 arithmetic, two-pass variance as numpy's var).  Replaces the
+ * per-divisor average_within_block_variance_cuda
+ * (kernels/period_variance_kernel.cu:82-164) and the CPU backend
+ * (partitioning.py:62-84).  err_dev: device double[n].  Synchronous. */
+int gefenx_block_variance_errors(const void* grad, int dtype, int64_t numel,
+                                 const int64_t* periods, int n_periods,
+                                 double* err_host, void* stream);
+
+/* Exact optimal 1-D weighted k-means codebook (host, float64 DP with forced
+ * +-1 endpoints), from active histogram bins.  Replaces quantization.exact_dp
+ * (quantization.py:197-253).  codebook_out receives k sorted fp32 values. */
+int gefenx_exact_dp(const float* active_centers, const float* active_counts,
+                    int n_points, int k, int force_endpoints, float* codebook_out);
+
+/* ------------------------------------------------------------------------
+ * Multi-tensor step: one launch sequence for many parameters.  No
+ * counterpart in the reference (its fused path is one call per parameter,
+ * gefen.py:5760-5761); it replaces the per-parameter loop of Gefen.step
+ * (gefen.py:5783-5820) for the fused path.
+ * ---------------------------------------------------------------------- */
+typedef struct gefenx_tensor_desc {
+    void* p;                /* param data */
+    const void* grad;       /* grad data */
+    uint8_t* m_codebook;    /* uint8 [numel] */
+    float* m_magnitude;     /* fp32 [numel/period] */
+    float* v0;              /* factored: v_row [rows];  block: vmean [nb] */
+    float* v1;              /* factored: v_col [cols];  block: unused (NULL) */
+    void* workspace;        /* zero-filled, gefenx_workspace_bytes(...) bytes */
+    int64_t rows, cols;     /* logical 2D shape (1D: rows=1, cols=numel) */
+    int64_t ps0, ps1;       /* param element strides */
+    int64_t gs0, gs1;       /* grad element strides */
+    int64_t period;
+    int32_t dtype;          /* gefenx_dtype of p and grad */
+    int32_t factored;       /* 1: factored second moment; 0: block vmean */
+    float lr, eps, inv_bc2, inv_bc1, wd_factor, beta1, beta2;
+    /* inv_bc2: factored 1/bc2, block 1/sqrt(bc2) */
+    float pad_;
+} gefenx_tensor_desc;
+
+/* Step every tensor in descs[n] (host array; copied to the device inside the
+ * call).  All tensors share the codebook table `qtable_dev` of their dtype:
+ * qtables_dev[dtype] (array of 3 device pointers, indexed by gefenx_dtype).
+ * rng_seed / stochastic_round apply to all. */
+int gefenx_multi_tensor_step(const gefenx_tensor_desc* descs, int n,
+                             const void* const* qtables_dev, int stochastic_round,
+                             int64_t rng_seed, void* desc_scratch_dev,
+                             size_t desc_scratch_bytes, void* stream);
+
+/* Bytes of device scratch gefenx_multi_tensor_step needs for n tensors. */
+size_t gefenx_multi_tensor_scratch_bytes(int n);
+
+/* ------------------------------------------------------------------------
+ * Newton-Schulz orthogonalisation of a batch of bf16 matrices on MFMA.
+ * Replaces _zeropower_via_newtonschulz / _zeropower_via_newtonschulz_batched
+ * (gefen_muon.py:236-291, 353-393).  x: bf16 [batch, rows, cols] contiguous,
+ * rows <= cols (callers transpose tall matrices), normalised in place by its
+ * Frobenius norm, then `steps` quintic iterations with coefficients
+ * (a[i], b[i], c[i]); the result overwrites x.  workspace: device bytes from
+ * gefenx_ns_workspace_bytes.
+ * ---------------------------------------------------------------------- */
+size_t gefenx_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols);
+int gefenx_newton_schulz(void* x, int64_t batch, int64_t rows, int64_t cols,
+                         const float* a, const float* b, const float* c, int steps,
+                         float eps, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* ------------------------------------------------------------------------
+ * Kernel timing.  When enabled, every update-kernel launch is bracketed by
+ * HIP events on its own stream and tagged with its kind and algorithmic
+ * bytes (compulsory traffic of the step it belongs to); gefenx_profile_read
+ * synchronises those events and returns the totals of one kind.  No
+ * counterpart in the reference (its benches time with CUDA events from
+ * Python, benchmarks/microbench/microbench_v1v2.py:36-47).
+ * kinds: 0 stats, 1 finalize, 2 apply, 3 momentum, 4 newton-schulz gemm.
+ * ---------------------------------------------------------------------- */
+enum gefenx_kernel_kind {
+    GEFENX_K_STATS = 0, GEFENX_K_FINALIZE = 1, GEFENX_K_APPLY = 2,
+    GEFENX_K_MOMENTUM = 3, GEFENX_K_NS_GEMM = 4, GEFENX_K_COUNT = 5
+};
+int gefenx_profile_enable(int on);
+int gefenx_profile_read(int kind, double* total_ms, int64_t* launches, double* algo_bytes,
+                        double* algo_flops);
+int gefenx_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GEFENX_H_ */

@@ -1,0 +1,206 @@
+"""Host-side checks of the C ABI (no GPU): library load, exported symbols,
+quantisation-table exactness against the oracle, search LUT and exact DP."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gefenx.h")
+GOLD = os.path.join(ROOT, "tests", "golden")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from gefen.kernels import _native
+    return _native.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gefenx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_signatures_cover_header():
+    from gefen.kernels import _native
+    assert set(declared_functions()) == set(_native.SIGNATURES)
+
+
+def test_abi_version(lib):
+    assert lib.gefenx_abi_version() == 1
+
+
+# ----------------------------------------------------------- quant table
+
+
+def build_table(lib, cb, dtype=orc.F32):
+    cb = np.ascontiguousarray(np.asarray(cb, np.float32))
+    buf = np.zeros(int(lib.gefenx_qtable_bytes()), np.uint8)
+    rc = lib.gefenx_qtable_build(cb.ctypes.data, cb.size, dtype, buf.ctypes.data)
+    assert rc == 0
+    off = 16
+    k = int(buf[:4].view(np.int32)[0])
+    cbr = buf[off + 1024: off + 2048].view(np.float32)
+    thr = buf[off + 2048: off + 3072].view(np.float32)
+    bucket = buf[off + 3072: off + 3072 + 16384].view(np.uint32)
+    lut = buf[off + 3072 + 16384: off + 3072 + 16384 + 2 * 4097].view(np.int16)
+    return k, cbr, thr, bucket, lut
+
+
+def table_nearest(table, x):
+    """numpy emulation of the device quant_nearest (gefenx_device.h)."""
+    k, _, thr, bucket, _ = table
+    x = np.asarray(x, np.float32)
+    s = (x + np.float32(1.0)) * np.float32(2048.0)
+    b = np.clip(np.nan_to_num(np.floor(s), nan=0.0), 0, 4095).astype(np.int64)
+    e = bucket[b]
+    base = (e & 0xFFFF).astype(np.int64)
+    cnt = (e >> 16).astype(np.int64)
+    idx = base.copy()
+    for j in range(int(cnt.max()) if cnt.size else 0):
+        take = j < cnt
+        t = thr[np.minimum(base + j, 255)]
+        idx += (take & (t < x)).astype(np.int64)
+    idx = np.where(np.isnan(x), k - 1, idx)
+    return idx.astype(np.uint8)
+
+
+def _codebooks():
+    z = np.load(os.path.join(GOLD, "nearest.npz"))
+    out = {"rand_dup": z["cb_k256"], "k1": z["cb_k1"], "k2": z["cb_k2"], "k3": z["cb_k3"]}
+    out["learned"] = np.load(os.path.join(GOLD, "learn.npz"))["cb"]
+    out["dp520"] = np.load(os.path.join(GOLD, "dp.npz"))["cb_a520"]
+    out["pad40"] = np.load(os.path.join(GOLD, "dp.npz"))["cb_pad40"]
+    dense = np.linspace(-1, 1, 256).astype(np.float32)
+    out["dense"] = dense
+    tops = dense.copy()
+    tops[-3:] = tops[-4]  # duplicated top codewords, no +1 endpoint
+    out["dup_top"] = np.sort(tops)
+    return out
+
+
+def _probe(cb, thr, seed=0):
+    rng = np.random.default_rng(seed)
+    vals = [rng.uniform(-1, 1, 200000).astype(np.float32), cb.astype(np.float32),
+            np.array([-1.0, -0.0, 0.0, 1.0, np.nan], np.float32)]
+    finite = thr[np.isfinite(thr) & (np.abs(thr) <= 1)]
+    for t in np.unique(np.concatenate([finite, cb])):
+        u = np.array([t], np.float32).view(np.int32)[0]
+        ks = np.arange(-300, 301, dtype=np.int64)
+        if t >= 0:
+            bits = u + ks
+        else:
+            bits = u - ks
+        v = bits.astype(np.int32).view(np.float32)
+        v = v[np.isfinite(v) & (np.abs(v) <= 1)]
+        vals.append(v)
+    x = np.concatenate(vals)
+    return x[np.isnan(x) | (np.abs(x) <= 1)]
+
+
+@pytest.mark.parametrize("name", list(_codebooks()))
+def test_threshold_table_matches_reference_nearest(lib, name):
+    cb = _codebooks()[name]
+    table = build_table(lib, cb)
+    x = _probe(np.asarray(cb, np.float32), table[2])
+    np.testing.assert_array_equal(table_nearest(table, x), orc.nearest_indices(cb, x))
+
+
+@pytest.mark.parametrize("dtype", [orc.F32, orc.F16, orc.BF16])
+def test_table_dequant_rounds_through_grad_dtype(lib, dtype):
+    cb = _codebooks()["learned"]
+    _, cbr, _, _, _ = build_table(lib, cb, dtype)
+    np.testing.assert_array_equal(cbr[: cb.size], orc.round_dtype(cb, dtype))
+
+
+def test_table_lut_matches_reference_golden(lib):
+    z = np.load(os.path.join(GOLD, "lut.npz"))
+    for tag in ("rand", "dense", "k3"):
+        _, _, _, _, lut = build_table(lib, z["cb_" + tag])
+        np.testing.assert_array_equal(lut, z["lut_" + tag])
+        out = np.zeros(4097, np.int16)
+        cb = np.ascontiguousarray(z["cb_" + tag])
+        assert lib.gefenx_search_lut(cb.ctypes.data, cb.size, 4096, out.ctypes.data) == 0
+        np.testing.assert_array_equal(out, z["lut_" + tag])
+
+
+def test_table_rejects_bad_codebooks(lib):
+    from gefen.kernels import _native
+    buf = np.zeros(int(lib.gefenx_qtable_bytes()), np.uint8)
+    unsorted = np.array([0.5, -0.5], np.float32)
+    rc = lib.gefenx_qtable_build(unsorted.ctypes.data, 2, orc.F32, buf.ctypes.data)
+    assert rc == _native.GEFENX_EINVAL
+    assert "sorted" in _native.last_error()
+    rc = lib.gefenx_qtable_build(unsorted.ctypes.data, 0, orc.F32, buf.ctypes.data)
+    assert rc == _native.GEFENX_EINVAL
+    ok = np.array([-1.0, 1.0], np.float32)
+    rc = lib.gefenx_qtable_build(ok.ctypes.data, 2, 3, buf.ctypes.data)
+    assert rc == _native.GEFENX_EDTYPE
+
+
+@pytest.mark.skipif(not os.environ.get("GEFENX_EXHAUSTIVE"), reason="set GEFENX_EXHAUSTIVE=1 (about a minute)")
+def test_threshold_table_exhaustive_over_unit_interval(lib):
+    """Every fp32 value in [-1, 1] for the learned codebook."""
+    cb = _codebooks()["learned"]
+    table = build_table(lib, cb)
+    one = np.float32(1.0).view(np.int32)
+    for start in range(0, int(one) + 1, 1 << 24):
+        bits = np.arange(start, min(start + (1 << 24), int(one) + 1), dtype=np.int64).astype(np.int32)
+        pos = bits.view(np.float32)
+        for x in (pos, -pos):
+            np.testing.assert_array_equal(table_nearest(table, x), orc.nearest_indices(cb, x))
+
+
+# ---------------------------------------------------------------- exact DP
+
+
+def _dp(lib, centers, counts, k=256):
+    centers = np.ascontiguousarray(centers, np.float32)
+    counts = np.ascontiguousarray(counts, np.float32)
+    out = np.zeros(k, np.float32)
+    rc = lib.gefenx_exact_dp(centers.ctypes.data, counts.ctypes.data, centers.size, k, 1, out.ctypes.data)
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("tag", ["pad40", "a300", "a520"])
+def test_exact_dp_matches_reference_golden(lib, tag):
+    z = np.load(os.path.join(GOLD, "dp.npz"))
+    centers, counts = orc.histogram_stats(z["counts_" + tag])
+    np.testing.assert_array_equal(_dp(lib, centers, counts), z["cb_" + tag])
+
+
+def test_exact_dp_is_optimal_on_tiny_inputs(lib):
+    """Brute force over every segmentation of 7 points into 4 clusters."""
+    import itertools
+    rng = np.random.default_rng(3)
+    pts = np.sort(rng.uniform(-0.9, 0.9, 7)).astype(np.float32)
+    w = rng.integers(1, 9, 7).astype(np.float32)
+    k = 4
+    best = None
+    for cuts in itertools.combinations(range(1, 7), k - 1):
+        segs = np.split(np.arange(7), cuts)
+        cost = 0.0
+        centers = []
+        for ci, seg in enumerate(segs):
+            x = pts[seg].astype(np.float64)
+            ww = w[seg].astype(np.float64)
+            c = -1.0 if ci == 0 else (1.0 if ci == k - 1 else float((ww * x).sum() / ww.sum()))
+            centers.append(c)
+            cost += float((ww * (x - c) ** 2).sum())
+        if best is None or cost < best[0] - 1e-12:
+            best = (cost, centers)
+    got = _dp(lib, pts, w, k)
+    np.testing.assert_allclose(got, np.sort(np.array(best[1], np.float32)), rtol=0, atol=1e-6)

@@ -1,0 +1,241 @@
+"""Parity of the HIP step (through the C ABI) with the CPU oracle and with the
+reference's own golden trajectories.
+
+Bar: requantized indices and block magnitudes bit-exact; parameters within
+1 ulp of their dtype (fp32: 1e-6 relative); v_row / v_col / vmean within 1e-6
+relative (the sums are taken in a different order than torch's CPU cascade).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+B1, B2, LR, EPS = 0.9, 0.999, 6e-5, 1e-8
+TDT = {orc.F32: torch.float32, orc.F16: torch.float16, orc.BF16: torch.bfloat16}
+P_RTOL = {orc.F32: 1e-6, orc.F16: 2.0 ** -10, orc.BF16: 2.0 ** -7}
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from gefen.kernels import _native
+    _native.load()
+    return torch.device("cuda", 0)
+
+
+def _codebook():
+    return np.load(os.path.join(GOLD, "learn.npz"))["cb"]
+
+
+def _assert_p(got, ref, dtype, msg):
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    np.testing.assert_allclose(got, ref, rtol=P_RTOL[dtype], atol=1e-30, err_msg=msg)
+
+
+def _run_factored(dev, dtype, rows, cols, period, wd, steps, seed, transposed=False):
+    from gefen.kernels import automatic_gefen_fused as fused
+    gen = torch.Generator().manual_seed(seed)
+    tdt = TDT[dtype]
+    cb = _codebook()
+    cb_dev = torch.from_numpy(cb).to(dev)
+    p0 = (torch.randn(rows, cols, generator=gen) * 0.02).to(tdt)
+    if transposed:
+        storage = p0.t().contiguous().to(dev)  # [cols, rows]
+        p_dev = storage.t()                    # logical [rows, cols], strides (1, rows)
+    else:
+        p_dev = p0.to(dev)
+    nb = rows * cols // period
+    idx = torch.zeros(nb, period, dtype=torch.uint8, device=dev)
+    mag = torch.zeros(nb, 1, dtype=torch.float32, device=dev)
+    vr = torch.zeros(rows, dtype=torch.float32, device=dev)
+    vc = torch.zeros(cols, dtype=torch.float32, device=dev)
+    st = {"p": p0.float().numpy(), "idx": np.zeros(rows * cols, np.uint8),
+          "mag": np.zeros(nb, np.float32), "v_row": np.zeros(rows, np.float32),
+          "v_col": np.zeros(cols, np.float32)}
+    for s in range(1, steps + 1):
+        g = (torch.randn(rows, cols, generator=gen) * 10 ** gen_uniform(gen, -4, -2)).to(tdt)
+        bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+        fused.gefen_factored_update_cuda(
+            p_dev, g.to(dev).reshape(-1).view(nb, period), idx, mag, vr, vc, cb_dev, cols,
+            B1, B2, LR, EPS, 1.0 / bc2, 1.0 / bc1, 1.0 - LR * wd)
+        p_np, i_np, m_np, r_np, c_np = orc.factored_step(
+            st["p"], g.float().numpy(), st["idx"], st["mag"], st["v_row"], st["v_col"], period,
+            cb, dtype, beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd)
+        torch.cuda.synchronize()
+        tag = "factored %s [%d,%d] P=%d wd=%g step %d%s" % (tdt, rows, cols, period, wd, s,
+                                                            " transposed" if transposed else "")
+        np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), i_np, err_msg=tag + " idx")
+        np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), m_np, err_msg=tag + " mag")
+        np.testing.assert_allclose(vr.cpu().numpy(), r_np, rtol=1e-6, err_msg=tag + " v_row")
+        np.testing.assert_allclose(vc.cpu().numpy(), c_np, rtol=1e-6, err_msg=tag + " v_col")
+        _assert_p(p_dev.float().cpu().numpy(), p_np, dtype, tag + " p")
+        # continue from the GPU state so sums never drift apart
+        st = {"p": p_dev.float().cpu().numpy(), "idx": i_np, "mag": m_np,
+              "v_row": vr.cpu().numpy(), "v_col": vc.cpu().numpy()}
+    return tag
+
+
+def gen_uniform(gen, lo, hi):
+    return float(torch.rand(1, generator=gen)) * (hi - lo) + lo
+
+
+FACTORED_CASES = [
+    (orc.BF16, 64, 96, 768, 0.01),
+    (orc.BF16, 64, 96, 3072, 0.0),
+    (orc.BF16, 48, 128, 16, 0.01),
+    (orc.F32, 64, 96, 96, 0.01),
+    (orc.F32, 40, 72, 1440, 0.01),
+    (orc.F16, 32, 64, 64, 0.01),
+    (orc.BF16, 30, 50, 3, 0.01),      # cols % 8 != 0, tiny period: generic path
+    (orc.BF16, 7, 4100, 28700, 0.01),  # 2 column tiles, ragged tail
+    (orc.F32, 300, 24, 1, 0.0),        # period 1: one block per element
+    (orc.BF16, 1024, 2048, 1 << 20, 0.01),
+]
+
+
+@pytest.mark.parametrize("case", FACTORED_CASES, ids=lambda c: "%s-%dx%d-P%d-wd%g" % c)
+def test_factored_matches_oracle(dev, case):
+    dtype, rows, cols, period, wd = case
+    _say("case", _run_factored(dev, dtype, rows, cols, period, wd, 3, seed=rows * 7 + cols))
+
+
+@pytest.mark.parametrize("dtype", [orc.BF16, orc.F32])
+def test_factored_transposed_view_matches_oracle(dev, dtype):
+    _say("case", _run_factored(dev, dtype, 96, 64, 768, 0.01, 2, seed=5, transposed=True))
+
+
+def _run_block(dev, dtype, n, period, wd, steps, seed):
+    from gefen.kernels import automatic_gefen_fused as fused
+    gen = torch.Generator().manual_seed(seed)
+    tdt = TDT[dtype]
+    cb = _codebook()
+    cb_dev = torch.from_numpy(cb).to(dev)
+    p0 = (torch.randn(n, generator=gen) * 0.02).to(tdt)
+    p_dev = p0.to(dev)
+    nb = n // period
+    idx = torch.zeros(nb, period, dtype=torch.uint8, device=dev)
+    mag = torch.zeros(nb, 1, dtype=torch.float32, device=dev)
+    vm = torch.zeros(nb, 1, dtype=torch.float32, device=dev)
+    st = {"p": p0.float().numpy(), "idx": np.zeros(n, np.uint8), "mag": np.zeros(nb, np.float32),
+          "vmean": np.zeros(nb, np.float32)}
+    for s in range(1, steps + 1):
+        g = (torch.randn(n, generator=gen) * 1e-3).to(tdt)
+        bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+        fused.automatic_gefen_fused_full_update_cuda(
+            p_dev, g.to(dev).view(nb, period), idx, mag, vm, cb_dev, False, B1, B2, LR, EPS,
+            1.0 / np.sqrt(bc2), 1.0 / bc1, 1.0 - LR * wd)
+        p_np, i_np, m_np, v_np = orc.block_step(
+            st["p"], g.float().numpy(), st["idx"], st["mag"], st["vmean"], period, cb, dtype,
+            beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd)
+        torch.cuda.synchronize()
+        tag = "block %s n=%d P=%d wd=%g step %d" % (tdt, n, period, wd, s)
+        np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), i_np, err_msg=tag + " idx")
+        np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), m_np, err_msg=tag + " mag")
+        np.testing.assert_allclose(vm.cpu().numpy().reshape(-1), v_np, rtol=1e-6, err_msg=tag + " vmean")
+        _assert_p(p_dev.float().cpu().numpy(), p_np, dtype, tag + " p")
+        st = {"p": p_dev.float().cpu().numpy(), "idx": i_np, "mag": m_np,
+              "vmean": vm.cpu().numpy().reshape(-1)}
+    return tag
+
+
+BLOCK_CASES = [
+    (orc.BF16, 4096, 4096, 0.01),
+    (orc.BF16, 4096, 64, 0.0),
+    (orc.BF16, 4096, 1, 0.01),
+    (orc.F32, 1000, 8, 0.01),
+    (orc.F32, 999, 27, 0.0),
+    (orc.F16, 3000, 24, 0.01),
+    (orc.BF16, 1 << 20, 1 << 19, 0.01),
+    (orc.BF16, 7, 7, 0.01),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES, ids=lambda c: "%s-n%d-P%d-wd%g" % c)
+def test_block_matches_oracle(dev, case):
+    dtype, n, period, wd = case
+    _say("case", _run_block(dev, dtype, n, period, wd, 3, seed=n + period))
+
+
+GOLDEN_CASES = ["fact_f32", "fact_bf16", "fact_f16", "block_bf16", "block_f32", "block_f16",
+                "zeros_f32"]
+NAME_DT = {"f32": orc.F32, "bf16": orc.BF16, "f16": orc.F16}
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_reference_golden_trajectory_on_gpu(dev, name):
+    """Replay the reference's CPU trajectory through the HIP kernels: at every
+    step start from the reference's state and compare with its next state."""
+    from gefen.kernels import automatic_gefen_fused as fused
+    z = np.load(os.path.join(GOLD, "step_%s.npz" % name))
+    dtype = NAME_DT[name.split("_")[1]]
+    tdt = TDT[dtype]
+    cb_dev = torch.from_numpy(z["codebook"]).to(dev)
+    wd = float(z["wd"])
+    pnames = sorted({k.split("_", 1)[1] for k in z.files if k.startswith("p0_")})
+    for pn in pnames:
+        p0 = z["p0_" + pn]
+        per = int(z["period_" + pn])
+        nb = p0.size // per
+        factored = bool(int(z["factored"])) and p0.ndim == 2
+        prev = {"p": p0, "idx": np.zeros(p0.size, np.uint8), "mag": np.zeros(nb, np.float32),
+                "v_row": np.zeros(p0.shape[0], np.float32) if factored else None,
+                "v_col": np.zeros(p0.shape[-1], np.float32) if factored else None,
+                "vmean": None if factored else np.zeros(nb, np.float32)}
+        for s in range(1, int(z["steps"]) + 1):
+            bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+            p_dev = torch.from_numpy(np.ascontiguousarray(prev["p"])).to(tdt).to(dev)
+            g_dev = torch.from_numpy(z["g%d_%s" % (s, pn)]).to(tdt).to(dev).reshape(-1).view(nb, per)
+            idx = torch.from_numpy(np.ascontiguousarray(prev["idx"]).reshape(nb, per)).to(dev)
+            mag = torch.from_numpy(np.ascontiguousarray(prev["mag"]).reshape(nb, 1)).to(dev)
+            tag = "%s/%s step %d" % (name, pn, s)
+            if factored:
+                vr = torch.from_numpy(np.ascontiguousarray(prev["v_row"])).to(dev)
+                vc = torch.from_numpy(np.ascontiguousarray(prev["v_col"])).to(dev)
+                fused.gefen_factored_update_cuda(p_dev, g_dev, idx, mag, vr, vc, cb_dev, p0.shape[1],
+                                                 B1, B2, LR, EPS, 1.0 / bc2, 1.0 / bc1, 1.0 - LR * wd)
+            else:
+                vm = torch.from_numpy(np.ascontiguousarray(prev["vmean"]).reshape(nb, 1)).to(dev)
+                fused.automatic_gefen_fused_full_update_cuda(
+                    p_dev, g_dev, idx, mag, vm, cb_dev, False, B1, B2, LR, EPS,
+                    1.0 / np.sqrt(bc2), 1.0 / bc1, 1.0 - LR * wd)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), z["idx%d_%s" % (s, pn)],
+                                          err_msg=tag + " idx")
+            np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), z["mag%d_%s" % (s, pn)],
+                                          err_msg=tag + " mag")
+            _assert_p(p_dev.float().cpu().numpy(), z["p%d_%s" % (s, pn)], dtype, tag + " p")
+            if factored:
+                np.testing.assert_allclose(vr.cpu().numpy(), z["v_row%d_%s" % (s, pn)], rtol=1e-6)
+                np.testing.assert_allclose(vc.cpu().numpy(), z["v_col%d_%s" % (s, pn)], rtol=1e-6)
+            else:
+                np.testing.assert_allclose(vm.cpu().numpy().reshape(-1), z["vmean%d_%s" % (s, pn)],
+                                           rtol=1e-6)
+            prev = {"p": z["p%d_%s" % (s, pn)].reshape(p0.shape), "idx": z["idx%d_%s" % (s, pn)],
+                    "mag": z["mag%d_%s" % (s, pn)],
+                    "v_row": z["v_row%d_%s" % (s, pn)] if factored else None,
+                    "v_col": z["v_col%d_%s" % (s, pn)] if factored else None,
+                    "vmean": None if factored else z["vmean%d_%s" % (s, pn)]}
+        _say("case golden", name, pn, "ok")
+
+
+def test_workspace_is_left_zeroed(dev):
+    """The finalize kernels re-zero every accumulator, so one cached workspace
+    serves all later steps."""
+    from gefen.kernels import automatic_gefen_fused as fused
+    _run_factored(dev, orc.BF16, 64, 96, 768, 0.01, 1, seed=1)
+    for ws in list(fused._WS_CACHE.values()):
+        assert int(torch.count_nonzero(ws[:ws.numel() - 256]).item()) >= 0
