@@ -32,45 +32,84 @@ static_assert(sizeof(QTable) % 16 == 0, "QTable must stay 16-byte aligned in siz
 // zero on entry and left zero on exit by the finalize kernels.
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Factored stats tiling: a workgroup covers kFactTileCols columns (one wave
+// row of 64 lanes x 8 columns) of `tile_rows` consecutive rows.
+constexpr int64_t kFactTileCols = 512;
+constexpr int64_t kFactTargetWgs = 1024;
+
+struct FactTiles {
+    int64_t ct, rt, tile_rows;
+    static FactTiles make(int64_t rows, int64_t cols) {
+        FactTiles t;
+        t.ct = (cols + kFactTileCols - 1) / kFactTileCols;
+        if (t.ct < 1) t.ct = 1;
+        int64_t rt = (kFactTargetWgs + t.ct - 1) / t.ct;
+        if (rt > rows) rt = rows;
+        if (rt < 1) rt = 1;
+        t.tile_rows = (rows + rt - 1) / rt;
+        t.rt = (rows + t.tile_rows - 1) / t.tile_rows;
+        if (t.rt < 1) t.rt = 1;
+        return t;
+    }
+};
+
+// Block-max accumulators are sharded when there are few blocks: workgroup w
+// folds into shard (w % shards), so one huge block is not a single atomic
+// hot spot; the finalize kernels take the max over the shards.
+constexpr int64_t kMagShardMaxBlocks = 4096;
+constexpr int64_t kMagShards = 32;
+inline int64_t mag_shards(int64_t nb) { return nb <= kMagShardMaxBlocks ? kMagShards : 1; }
+
+// Rows of v_row handled per finalize workgroup (one float64 partial of
+// sum(v_row) each; the apply kernel adds the partials in a fixed order).
+constexpr int64_t kFinRowsPerWg = 256;
+
 struct FactoredWs {
-    // double row_sq[rows], double col_sq[cols], uint32 magbits[nb],
-    // float mag_old[nb], float scalars[4] (mean_r, ...)
-    size_t off_row, off_col, off_magbits, off_magold, off_scal, total;
+    // double row_part[ct][rows], double col_part[rt][cols] (per-tile partial
+    // sums, fully rewritten every step), uint32 magbits[shards][nb] (zero
+    // between steps), float mag_old[nb], float minv[nb],
+    // double vrow_sum[ceil(rows/256)] (partials of sum(v_row))
+    size_t off_rowp, off_colp, off_magbits, off_magold, off_minv, off_vsum, total;
     static FactoredWs make(int64_t rows, int64_t cols, int64_t nb) {
         FactoredWs w;
+        const FactTiles t = FactTiles::make(rows, cols);
         size_t o = 0;
-        w.off_row = o;     o += align256(sizeof(double) * (size_t)rows);
-        w.off_col = o;     o += align256(sizeof(double) * (size_t)cols);
-        w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)nb);
+        w.off_rowp = o;    o += align256(sizeof(double) * (size_t)(t.ct * rows));
+        w.off_colp = o;    o += align256(sizeof(double) * (size_t)(t.rt * cols));
+        w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)(nb * mag_shards(nb)));
         w.off_magold = o;  o += align256(sizeof(float) * (size_t)nb);
-        w.off_scal = o;    o += 256;
+        w.off_minv = o;    o += align256(sizeof(float) * (size_t)nb);
+        w.off_vsum = o;    o += align256(sizeof(double) * (size_t)((rows + kFinRowsPerWg - 1) / kFinRowsPerWg));
         w.total = o;
         return w;
     }
 };
 
 struct BlockWs {
-    // double blk_sq[nb], uint32 magbits[nb], float mag_old[nb], float step[nb]
-    size_t off_sq, off_magbits, off_magold, off_step, total;
+    // double blk_sq[nb] (zero between steps), uint32 magbits[nb] (zero between
+    // steps), float mag_old[nb], float step[nb], float minv[nb]
+    size_t off_sq, off_magbits, off_magold, off_step, off_minv, total;
     static BlockWs make(int64_t nb) {
         BlockWs w;
         size_t o = 0;
         w.off_sq = o;      o += align256(sizeof(double) * (size_t)nb);
-        w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)nb);
+        w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)(nb * mag_shards(nb)));
         w.off_magold = o;  o += align256(sizeof(float) * (size_t)nb);
         w.off_step = o;    o += align256(sizeof(float) * (size_t)nb);
+        w.off_minv = o;    o += align256(sizeof(float) * (size_t)nb);
         w.total = o;
         return w;
     }
 };
 
 struct MomentumWs {
-    size_t off_magbits, off_magold, total;
+    size_t off_magbits, off_magold, off_minv, total;
     static MomentumWs make(int64_t nb) {
         MomentumWs w;
         size_t o = 0;
-        w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)nb);
+        w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)(nb * mag_shards(nb)));
         w.off_magold = o;  o += align256(sizeof(float) * (size_t)nb);
+        w.off_minv = o;    o += align256(sizeof(float) * (size_t)nb);
         w.total = o;
         return w;
     }

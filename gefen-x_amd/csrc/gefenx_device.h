@@ -22,12 +22,9 @@ template <> struct Elem<F32> { using T = float; };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// Round-to-nearest-even fp32 -> bf16 (c10::BFloat16 semantics, NaN quietened).
+// Round-to-nearest-even fp32 -> bf16 (gfx950 v_cvt_pk_bf16_f32; NaN stays NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x0040u) & 0xffffu;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)x);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
@@ -173,6 +170,27 @@ __device__ __forceinline__ uint32_t quant_stochastic(float x, const float* __res
 }
 
 // ------------------------------------------------------------- utilities
+
+// Correctly rounded u / b given y = RN(1 / b) (y == 0 marks blocks where the
+// reciprocal is not usable).  q0 = RN(u*y) is within 1 ulp of u/b, r = u - b*q0
+// is exact in one fma, and RN(q0 + r*y) is RN(u/b) (Markstein's theorem) when
+// nothing underflows; tiny |u| or an unusable y take the IEEE divide.
+__device__ __forceinline__ float div_by_block(float u, float b, float y) {
+    if (y != 0.0f && fabsf(u) >= 0x1p-100f) {
+        const float q0 = u * y;
+        if (fabsf(q0) >= 0x1p-100f) {
+            const float r = __builtin_fmaf(-q0, b, u);
+            return __builtin_fmaf(r, y, q0);
+        }
+    }
+    return u / b;
+}
+
+// Reciprocal for div_by_block: RN(1/b) when b and 1/b are normal and finite.
+__device__ __forceinline__ float block_recip(float b) {
+    if (!(b >= 0x1p-125f) || !(b <= 0x1p125f)) return 0.0f;
+    return 1.0f / b;
+}
 
 // floor(n / d) for 0 <= n < 2^53, d >= 1, with inv = 1.0 / d.
 __device__ __forceinline__ int64_t div_floor(int64_t n, int64_t d, double inv) {

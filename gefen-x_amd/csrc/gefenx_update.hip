@@ -2,16 +2,18 @@
 //
 // Per parameter the step is three launches on the caller's stream:
 //   stats    one pass over grad + stored indices: per-block max |u| (u = the
-//            updated momentum) and the second-moment sums (row/column sums of
-//            g^2 for the factored path, per-block sums for the block path);
-//   finalize tiny: EMA of the second moment, mean(v_row), new magnitudes,
-//            per-block stepsizes; re-zeroes the workspace accumulators;
+//            updated momentum) and the second-moment sums (per-tile row/column
+//            partial sums of g^2 for the factored path, per-block sums for the
+//            block path);
+//   finalize tiny: EMA of the second moment, mean(v_row), new magnitudes and
+//            their reciprocals, per-block stepsizes; re-zeroes the workspace
+//            accumulators;
 //   apply    one pass: recompute u, normalise by the new magnitude,
 //            requantise through the exact threshold table, write the indices
 //            and the parameter (decoupled weight decay folded in).
 // The math follows the reference's decomposed step (gefen.py:2959-3018,
-// 3329-3486, 3776-3818); see gefenx_device.h for the bit-exact momentum and
-// quantisation primitives.
+// 3329-3486, 3776-3818); gefenx_device.h holds the bit-exact momentum,
+// division and quantisation primitives.
 #include "gefenx_device.h"
 #include "gefenx_internal.h"
 #include "gefenx_profile.h"
@@ -24,8 +26,6 @@ namespace gx {
 
 constexpr int kThreads = 256;
 constexpr int kChunk = 8;
-constexpr int kTileCols = kThreads * kChunk;  // 2048 columns per stats tile
-constexpr int kMaxTileRows = 32;
 
 struct StepScalars {
     float lr, inv_bc2, inv_bc1, wdf;
@@ -41,34 +41,29 @@ __device__ __forceinline__ StepScalars read_scalars(StepScalars host, const floa
     return host;
 }
 
-// Per-thread running block max of |u| (as ordered uint bits: NaN > inf > finite,
-// so the integer max propagates NaN like torch's amax).
-struct BlockMax {
+// Wave-uniform running block max of |u| as ordered uint bits (NaN > inf >
+// finite, so the integer max propagates NaN like torch's amax).  `blk` is
+// identical in every lane; `bits` is each lane's partial.
+struct WaveMax {
     int64_t blk;
     uint32_t bits;
-    float mag_old;
 };
 
-__device__ __forceinline__ void blockmax_flush(uint32_t* __restrict__ magbits, const BlockMax& bm) {
-    if (bm.blk >= 0 && bm.bits != 0u) atomicMax(magbits + bm.blk, bm.bits);
-}
-
-// Wave-level final flush: one atomic per wave when every lane holds the same block.
-__device__ __forceinline__ void blockmax_final(uint32_t* __restrict__ magbits, const BlockMax& bm) {
-    const int lane = threadIdx.x & 63;
-    const int64_t blk0 = __shfl(bm.blk, 0, 64);
-    const bool same = __all(bm.blk == blk0);
-    if (same) {
-        const uint32_t m = wave_max_u(bm.bits);
-        if (lane == 0 && blk0 >= 0 && m != 0u) atomicMax(magbits + blk0, m);
-    } else {
-        blockmax_flush(magbits, bm);
+__device__ __forceinline__ void wavemax_flush(uint32_t* __restrict__ magbits, WaveMax& wm) {
+    if (wm.blk >= 0) {
+        const uint32_t m = wave_max_u(wm.bits);
+        if ((threadIdx.x & 63) == 0 && m != 0u) atomicMax(magbits + wm.blk, m);
     }
+    wm.bits = 0u;
 }
 
 // ====================================================================
-// Factored stats: grid (ceil(C / 2048), ceil(R / tile_rows)), 256 threads.
-// Thread t owns columns [c0, c0+8) of every row of its tile.
+// Factored stats.  Workgroup = 4 waves over a tile of `tile_rows` rows x 512
+// columns: lane l owns columns [c0 + 8l, c0 + 8l + 8), wave w takes rows
+// r0 + w, r0 + w + 4, ...  Row sums reduce per wave (one value per row per
+// column tile), column sums reduce across the 4 waves in LDS; both are
+// written as float64 partials (no atomics, deterministic), summed by the
+// finalize kernel.
 // ====================================================================
 struct FactStatsArgs {
     const void* grad;
@@ -77,147 +72,260 @@ struct FactStatsArgs {
     const QTable* qt;
     int64_t R, C, gs0, gs1, P;
     double invP;
-    int tile_rows;
-    int fast;  // contiguous, C % 8 == 0, 16-byte aligned grad
-    double* row_sq;
-    double* col_sq;
-    uint32_t* magbits;
+    int64_t tile_rows, ct;
+    int fast;  // contiguous grad, C % 8 == 0, P % 8 == 0, aligned
+    double* row_part;  // [ct][R]
+    double* col_part;  // [rt][C]
+    uint32_t* magbits; // [shards][nb]
+    int64_t nb, shards;
     MomentumCoef mc;
 };
 
-template <int DT>
+template <int DT, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_factored_stats(FactStatsArgs a) {
     using T = typename Elem<DT>::T;
     __shared__ float s_cbr[kCodebookMax];
-    __shared__ float s_row[kMaxTileRows][kThreads / 64];
+    __shared__ double s_col[kThreads / 64 - 1][kFactTileCols];
     for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = a.qt->cbr[i];
     __syncthreads();
 
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int64_t c0 = (int64_t)blockIdx.x * kTileCols + (int64_t)tid * kChunk;
-    const int64_t r_begin = (int64_t)blockIdx.y * a.tile_rows;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t ctile = (int64_t)blockIdx.x % a.ct;
+    const int64_t rtile = (int64_t)blockIdx.x / a.ct;
+    const int64_t c0 = ctile * kFactTileCols + (int64_t)lane * kChunk;
+    const int64_t r_begin = rtile * a.tile_rows;
     const int64_t r_end = std::min<int64_t>(r_begin + a.tile_rows, a.R);
-    const T* g = static_cast<const T*>(a.grad);
-
-    float colacc[kChunk];
-#pragma unroll
-    for (int k = 0; k < kChunk; ++k) colacc[k] = 0.0f;
-    BlockMax bm{-1, 0u, 0.0f};
     const int nvalid = (int)std::max<int64_t>(0, std::min<int64_t>(kChunk, a.C - c0));
+    const T* g = static_cast<const T*>(a.grad);
+    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
 
-    for (int64_t r = r_begin; r < r_end; ++r) {
-        float rowacc = 0.0f;
-        if (nvalid > 0) {
-            const int64_t e0 = r * a.C + c0;
-            float gv[kChunk];
-            uint32_t ix[kChunk];
-            if (a.fast && nvalid == kChunk) {
+    double colacc[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) colacc[k] = 0.0;
+    WaveMax wm{-1, 0u};
+    float mag_cur = 0.0f;
+
+    for (int64_t r = r_begin + wave; r < r_end; r += kThreads / 64) {
+        const int64_t e0 = r * a.C + c0;
+        float gv[kChunk];
+        uint32_t ix[kChunk];
+        if (FAST) {
+            if (nvalid == kChunk) {
                 load8<DT>(g + e0, gv);
                 load_idx8(a.idx + e0, ix);
             } else {
 #pragma unroll
-                for (int k = 0; k < kChunk; ++k) {
-                    if (k < nvalid) {
-                        gv[k] = to_f32<DT>(g[r * a.gs0 + (c0 + k) * a.gs1]);
-                        ix[k] = a.idx[e0 + k];
-                    } else {
-                        gv[k] = 0.0f;
-                        ix[k] = 0u;
-                    }
-                }
+                for (int k = 0; k < kChunk; ++k) { gv[k] = 0.0f; ix[k] = 0u; }
             }
-            int64_t blk = div_floor(e0, a.P, a.invP);
-            int64_t pin = e0 - blk * a.P;
+        } else {
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 if (k < nvalid) {
-                    if (blk != bm.blk) {
-                        blockmax_flush(a.magbits, bm);
-                        bm.blk = blk;
-                        bm.bits = 0u;
-                        bm.mag_old = a.mag_old[blk];
-                    }
-                    const float u = momentum_value(s_cbr[ix[k]], bm.mag_old, gv[k], a.mc);
-                    const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                    bm.bits = ub > bm.bits ? ub : bm.bits;
-                    const float sq = gv[k] * gv[k];
-                    rowacc += sq;
-                    colacc[k] += sq;
-                    if (++pin == a.P) { pin = 0; ++blk; }
+                    gv[k] = to_f32<DT>(g[r * a.gs0 + (c0 + k) * a.gs1]);
+                    ix[k] = a.idx[e0 + k];
+                } else {
+                    gv[k] = 0.0f;
+                    ix[k] = 0u;
                 }
             }
         }
-        const float rs = wave_sum(rowacc);
-        if (lane == 0) s_row[r - r_begin][wave] = rs;
-    }
-    blockmax_final(a.magbits, bm);
-    for (int k = 0; k < nvalid; ++k) atomicAdd(a.col_sq + c0 + k, (double)colacc[k]);
-    __syncthreads();
-    const int nrows = (int)(r_end - r_begin);
-    if (tid < nrows) {
-        double s = 0.0;
+        // block of this row strip: uniform across the wave when the wave's
+        // 512 columns never cross a block boundary
+        const int64_t e_first = r * a.C + ctile * kFactTileCols;
+        const int64_t blk0 = div_floor(e_first, a.P, a.invP);
+        const int64_t span = std::min<int64_t>(kFactTileCols, a.C - ctile * kFactTileCols);
+        const bool uniform = (e_first + span - 1) < (blk0 + 1) * a.P;
+        float rowacc = 0.0f;
+        if (uniform) {
+            if (blk0 != wm.blk) {
+                wavemax_flush(mb, wm);
+                wm.blk = blk0;
+                mag_cur = a.mag_old[blk0];
+            }
+            uint32_t m = wm.bits;
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) s += (double)s_row[tid][w];
-        atomicAdd(a.row_sq + r_begin + tid, s);
+            for (int k = 0; k < kChunk; ++k) {
+                if (k < nvalid) {
+                    const float u = momentum_value(s_cbr[ix[k]], mag_cur, gv[k], a.mc);
+                    const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                    m = ub > m ? ub : m;
+                    const float sq = gv[k] * gv[k];
+                    rowacc += sq;
+                    colacc[k] += (double)sq;
+                }
+            }
+            wm.bits = m;
+        } else {
+            // blocks smaller than the strip: per-lane runs, one atomic per run
+            wavemax_flush(mb, wm);
+            wm.blk = -1;
+            if (nvalid > 0) {
+                int64_t blk = div_floor(e0, a.P, a.invP);
+                int64_t pin = e0 - blk * a.P;
+                float mo = a.mag_old[blk];
+                uint32_t m = 0u;
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) {
+                    if (k < nvalid) {
+                        const float u = momentum_value(s_cbr[ix[k]], mo, gv[k], a.mc);
+                        const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                        m = ub > m ? ub : m;
+                        const float sq = gv[k] * gv[k];
+                        rowacc += sq;
+                        colacc[k] += (double)sq;
+                        if (++pin == a.P) {
+                            if (m) atomicMax(mb + blk, m);
+                            m = 0u;
+                            pin = 0;
+                            ++blk;
+                            if (k + 1 < nvalid) mo = a.mag_old[blk];
+                        }
+                    }
+                }
+                if (m) atomicMax(mb + blk, m);
+            }
+        }
+        const double rs = wave_sum_d((double)rowacc);
+        if (lane == 0) a.row_part[ctile * a.R + r] = rs;
+    }
+    // final block-max flush: one atomic per workgroup when the waves agree
+    __shared__ int64_t s_wblk[kThreads / 64];
+    __shared__ uint32_t s_wbits[kThreads / 64];
+    const uint32_t wbits = wave_max_u(wm.bits);
+    if (lane == 0) {
+        s_wblk[wave] = wm.blk;
+        s_wbits[wave] = wbits;
+    }
+    // column partials: waves 1..3 park theirs in LDS, wave 0 adds and stores
+    if (wave > 0) {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) s_col[wave - 1][lane * kChunk + k] = colacc[k];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        bool same = true;
+        uint32_t m = 0u;
+        for (int w = 0; w < kThreads / 64; ++w) {
+            same = same && (s_wblk[w] == s_wblk[0]);
+            m = s_wbits[w] > m ? s_wbits[w] : m;
+        }
+        if (same) {
+            if (s_wblk[0] >= 0 && m) atomicMax(mb + s_wblk[0], m);
+        } else {
+            for (int w = 0; w < kThreads / 64; ++w)
+                if (s_wblk[w] >= 0 && s_wbits[w]) atomicMax(mb + s_wblk[w], s_wbits[w]);
+        }
+    }
+    if (wave == 0) {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            double s = colacc[k];
+#pragma unroll
+            for (int w = 0; w < kThreads / 64 - 1; ++w) s += s_col[w][lane * kChunk + k];
+            if (k < nvalid) a.col_part[rtile * a.C + c0 + k] = s;
+        }
     }
 }
 
 // ====================================================================
-// Factored finalize: block 0 = rows/cols/mean, blocks 1.. = magnitudes.
+// Factored finalize.  Workgroups [0, nr): v_row EMA from the ct row partials,
+// one float64 partial of sum(v_row) per workgroup; [nr, nr+nc): v_col EMA
+// from the rt column partials; the rest: new magnitudes (max over shards),
+// their reciprocals, the old magnitudes.
 // v <- fma(sum/n, 1-beta2, v*beta2)  (gefen.py:2994-2996)
 // ====================================================================
 struct FactFinArgs {
-    double* row_sq;
-    double* col_sq;
+    const double* row_part;
+    const double* col_part;
     float* v_row;
     float* v_col;
-    int64_t R, C, nb;
+    int64_t R, C, nb, ct, rt, shards;
+    int64_t nr, nc;   // row / column workgroup counts
     float beta2, alpha2;
     uint32_t* magbits;
     float* mag;      // m_magnitude: receives the new magnitudes
     float* mag_old;  // workspace: receives the old magnitudes
-    float* scal;     // workspace scalars: [0] = max(mean(v_row), FLT_MIN)
+    float* minv;     // workspace: reciprocal of the new magnitudes
+    double* vsum;    // workspace: [nr] partials of sum(v_row)
 };
 
 __global__ void __launch_bounds__(kThreads) k_factored_finalize(FactFinArgs a) {
     const int tid = threadIdx.x;
-    if (blockIdx.x == 0) {
+    const int64_t wg = blockIdx.x;
+    if (wg < a.nr) {
         __shared__ double s_part[kThreads / 64];
-        double acc = 0.0;
-        const float fC = (float)a.C, fR = (float)a.R;
-        for (int64_t i = tid; i < a.R; i += kThreads) {
-            const float ms = (float)a.row_sq[i] / fC;
-            a.row_sq[i] = 0.0;
+        const int64_t i = wg * kFinRowsPerWg + tid;
+        double v64 = 0.0;
+        if (i < a.R) {
+            double s = 0.0;
+            for (int64_t t = 0; t < a.ct; ++t) s += a.row_part[t * a.R + i];
+            const float ms = (float)s / (float)a.C;
             const float v = __builtin_fmaf(ms, a.alpha2, a.v_row[i] * a.beta2);
             a.v_row[i] = v;
-            acc += (double)v;
+            v64 = (double)v;
         }
-        for (int64_t j = tid; j < a.C; j += kThreads) {
-            const float ms = (float)a.col_sq[j] / fR;
-            a.col_sq[j] = 0.0;
-            a.v_col[j] = __builtin_fmaf(ms, a.alpha2, a.v_col[j] * a.beta2);
-        }
-        acc = wave_sum_d(acc);
-        if ((tid & 63) == 0) s_part[tid >> 6] = acc;
+        v64 = wave_sum_d(v64);
+        if ((tid & 63) == 0) s_part[tid >> 6] = v64;
         __syncthreads();
         if (tid == 0) {
             double s = 0.0;
             for (int w = 0; w < kThreads / 64; ++w) s += s_part[w];
-            float mean = (float)s / fR;
-            if (!(mean >= 1.17549435e-38f) && mean == mean) mean = 1.17549435e-38f;
-            a.scal[0] = mean;
+            a.vsum[wg] = s;
         }
         return;
     }
-    for (int64_t b = (int64_t)(blockIdx.x - 1) * kThreads + tid; b < a.nb;
-         b += (int64_t)(gridDim.x - 1) * kThreads) {
+    if (wg < a.nr + a.nc) {
+        // 64 columns per workgroup; wave w adds row tiles t = w, w+4, ...
+        __shared__ double s_cp[kThreads / 64][64];
+        const int lane = tid & 63;
+        const int wave = tid >> 6;
+        const int64_t j = (wg - a.nr) * 64 + lane;
+        double s = 0.0;
+        if (j < a.C)
+            for (int64_t t = wave; t < a.rt; t += kThreads / 64) s += a.col_part[t * a.C + j];
+        s_cp[wave][lane] = s;
+        __syncthreads();
+        if (wave == 0 && j < a.C) {
+            double tot = 0.0;
+            for (int w = 0; w < kThreads / 64; ++w) tot += s_cp[w][lane];
+            const float ms = (float)tot / (float)a.R;
+            a.v_col[j] = __builtin_fmaf(ms, a.alpha2, a.v_col[j] * a.beta2);
+        }
+        return;
+    }
+    const int64_t gtid = (wg - a.nr - a.nc) * kThreads + tid;
+    const int64_t gstride = ((int64_t)gridDim.x - a.nr - a.nc) * kThreads;
+    for (int64_t b = gtid; b < a.nb; b += gstride) {
         const float old = a.mag[b];
         a.mag_old[b] = old;
-        a.mag[b] = __uint_as_float(a.magbits[b]);
-        a.magbits[b] = 0u;
+        uint32_t bits = 0u;
+        for (int64_t sh = 0; sh < a.shards; ++sh) {
+            const uint32_t v = a.magbits[sh * a.nb + b];
+            bits = v > bits ? v : bits;
+            a.magbits[sh * a.nb + b] = 0u;
+        }
+        const float m = __uint_as_float(bits);
+        a.mag[b] = m;
+        a.minv[b] = block_recip(m);
     }
+}
+
+// Deterministic mean(v_row) from the finalize partials, clamped at FLT_MIN
+// (gefen.py:2998-3000); every workgroup of the apply kernel recomputes it.
+__device__ __forceinline__ float mean_from_partials(const double* __restrict__ vsum, int64_t nr, int64_t R) {
+    __shared__ double s_red[kThreads];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < nr; i += kThreads) acc += vsum[i];
+    s_red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int off = kThreads / 2; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) s_red[threadIdx.x] += s_red[threadIdx.x + off];
+        __syncthreads();
+    }
+    float mean = (float)s_red[0] / (float)R;
+    if (!(mean >= 1.17549435e-38f) && mean == mean) mean = 1.17549435e-38f;
+    return mean;
 }
 
 // ====================================================================
@@ -233,7 +341,8 @@ struct BlockStatsArgs {
     double invP;
     int fast;
     double* blk_sq;
-    uint32_t* magbits;
+    uint32_t* magbits;  // [shards][nb]
+    int64_t nb, shards;
     MomentumCoef mc;
 };
 
@@ -244,10 +353,13 @@ __global__ void __launch_bounds__(kThreads) k_block_stats(BlockStatsArgs a) {
     for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = a.qt->cbr[i];
     __syncthreads();
     const T* g = static_cast<const T*>(a.grad);
+    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
     const int64_t nchunks = (a.N + kChunk - 1) / kChunk;
     const int64_t stride = (int64_t)gridDim.x * kThreads;
-    BlockMax bm{-1, 0u, 0.0f};
+    int64_t cur = -1;
+    uint32_t cbits = 0u;
     double bsum = 0.0;
+    float mo = 0.0f;
     for (int64_t ch = (int64_t)blockIdx.x * kThreads + threadIdx.x; ch < nchunks; ch += stride) {
         const int64_t e0 = ch * kChunk;
         const int nvalid = (int)std::min<int64_t>(kChunk, a.N - e0);
@@ -269,21 +381,21 @@ __global__ void __launch_bounds__(kThreads) k_block_stats(BlockStatsArgs a) {
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
             if (k < nvalid) {
-                if (blk != bm.blk) {
-                    if (bm.blk >= 0) {
+                if (blk != cur) {
+                    if (cur >= 0) {
                         bsum += (double)csum;
                         csum = 0.0f;
-                        if (bsum != 0.0) atomicAdd(a.blk_sq + bm.blk, bsum);
-                        bsum = 0.0;
+                        if (bsum != 0.0) atomicAdd(a.blk_sq + cur, bsum);
+                        if (cbits) atomicMax(mb + cur, cbits);
                     }
-                    blockmax_flush(a.magbits, bm);
-                    bm.blk = blk;
-                    bm.bits = 0u;
-                    bm.mag_old = a.mag_old[blk];
+                    bsum = 0.0;
+                    cbits = 0u;
+                    cur = blk;
+                    mo = a.mag_old[blk];
                 }
-                const float u = momentum_value(s_cbr[ix[k]], bm.mag_old, gv[k], a.mc);
+                const float u = momentum_value(s_cbr[ix[k]], mo, gv[k], a.mc);
                 const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                bm.bits = ub > bm.bits ? ub : bm.bits;
+                cbits = ub > cbits ? ub : cbits;
                 float sq = gv[k] * gv[k];
                 if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
                 csum += sq;
@@ -292,16 +404,19 @@ __global__ void __launch_bounds__(kThreads) k_block_stats(BlockStatsArgs a) {
         }
         bsum += (double)csum;
     }
-    // Final flush: combine the wave when all lanes hold the same block.
     const int lane = threadIdx.x & 63;
-    const int64_t blk0 = __shfl(bm.blk, 0, 64);
-    if (__all(bm.blk == blk0)) {
+    const int64_t c0 = __shfl(cur, 0, 64);
+    if (__all(cur == c0)) {
         const double s = wave_sum_d(bsum);
-        if (lane == 0 && blk0 >= 0 && s != 0.0) atomicAdd(a.blk_sq + blk0, s);
-    } else if (bm.blk >= 0 && bsum != 0.0) {
-        atomicAdd(a.blk_sq + bm.blk, bsum);
+        const uint32_t m = wave_max_u(cbits);
+        if (lane == 0 && c0 >= 0) {
+            if (s != 0.0) atomicAdd(a.blk_sq + c0, s);
+            if (m) atomicMax(mb + c0, m);
+        }
+    } else if (cur >= 0) {
+        if (bsum != 0.0) atomicAdd(a.blk_sq + cur, bsum);
+        if (cbits) atomicMax(mb + cur, cbits);
     }
-    blockmax_final(a.magbits, bm);
 }
 
 // vmean EMA + per-block stepsize (gefen.py:180-190, 3794-3805).
@@ -317,6 +432,8 @@ struct BlockFinArgs {
     float* mag;
     float* mag_old;
     float* step;
+    float* minv;
+    int64_t shards;
 };
 
 __global__ void __launch_bounds__(kThreads) k_block_finalize(BlockFinArgs a) {
@@ -333,13 +450,23 @@ __global__ void __launch_bounds__(kThreads) k_block_finalize(BlockFinArgs a) {
         a.step[b] = (1.0f / h) * sc.inv_bc1;
         const float old = a.mag[b];
         a.mag_old[b] = old;
-        a.mag[b] = __uint_as_float(a.magbits[b]);
-        a.magbits[b] = 0u;
+        uint32_t bits = 0u;
+        for (int64_t sh = 0; sh < a.shards; ++sh) {
+            const uint32_t v = a.magbits[sh * a.nb + b];
+            bits = v > bits ? v : bits;
+            a.magbits[sh * a.nb + b] = 0u;
+        }
+        const float m = __uint_as_float(bits);
+        a.mag[b] = m;
+        a.minv[b] = block_recip(m);
     }
 }
 
 // ====================================================================
-// Apply: flat over logical chunks of 8.  MODE 0 = factored, 1 = block.
+// Apply: grid-stride over logical chunks of 8 elements.  MODE 0 factored,
+// MODE 1 block.  FAST: contiguous p/grad, C % 8 == 0, P % 8 == 0, aligned --
+// a chunk then never crosses a row or a block, and (row, col, blk) advance
+// by constant strides between iterations (no per-chunk division).
 // ====================================================================
 struct ApplyArgs {
     void* p;
@@ -347,15 +474,18 @@ struct ApplyArgs {
     uint8_t* idx;
     const float* mag_old;
     const float* mag_new;
+    const float* minv;
     const float* v_row;   // factored
     const float* v_col;   // factored
-    const float* scal;    // factored: [0] = clamped mean(v_row)
+    const double* vsum;   // factored: [nr] partials of sum(v_row)
+    int64_t nr, R;
     const float* step;    // block: per-block stepsize
     const QTable* qt;
     int64_t N, C, P;
     double invC, invP;
     int64_t ps0, ps1, gs0, gs1;
-    int fast;        // contiguous p and grad, 16-byte aligned, C % 8 == 0 (or 1D)
+    // FAST iteration strides: S = gridDim.x * 256 * 8 elements = dR*C + dC = dB*P + dP
+    int64_t dR, dC, dB, dP;
     int write_p;     // 0 when lr == 0 and wd_factor == 1
     float eps;
     StepScalars sc;
@@ -365,7 +495,7 @@ struct ApplyArgs {
     const int64_t* seed_dev;
 };
 
-template <int DT, int MODE, bool SR>
+template <int DT, int MODE, bool SR, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
     using T = typename Elem<DT>::T;
     __shared__ SharedTables st;
@@ -380,99 +510,180 @@ __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
     if constexpr (SR) {
         if (a.seed_dev != nullptr) seed = (uint64_t)a.seed_dev[0];
     }
-    float inv_mean = 0.0f;
-    if constexpr (MODE == 0) inv_mean = 1.0f / a.scal[0];
+    float row_scale = 0.0f;  // mean(v_row)^-1 * (1/bc2)
+    if constexpr (MODE == 0) row_scale = (1.0f / mean_from_partials(a.vsum, a.nr, a.R)) * sc.inv_bc2;
+    const float c1 = sc.inv_bc1 * sc.lr;
+    const bool wd = sc.wdf != 1.0f;
 
     T* p = static_cast<T*>(a.p);
     const T* g = static_cast<const T*>(a.grad);
     const int64_t nchunks = (a.N + kChunk - 1) / kChunk;
+    int64_t ch = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t ch = (int64_t)blockIdx.x * kThreads + threadIdx.x; ch < nchunks; ch += stride) {
-        const int64_t e0 = ch * kChunk;
-        const int nvalid = (int)std::min<int64_t>(kChunk, a.N - e0);
+    if (ch >= nchunks) return;
+
+    if constexpr (FAST) {
+        int64_t e0 = ch * kChunk;
         int64_t row = 0, col = e0;
-        if (MODE == 0 || !a.fast) {
+        if constexpr (MODE == 0) {
             row = div_floor(e0, a.C, a.invC);
             col = e0 - row * a.C;
         }
         int64_t blk = div_floor(e0, a.P, a.invP);
         int64_t pin = e0 - blk * a.P;
-        float gv[kChunk], pv[kChunk];
-        uint32_t ix[kChunk];
-        const bool vec = a.fast && nvalid == kChunk;
-        if (vec) {
-            load8<DT>(g + e0, gv);
-            if (a.write_p) load8<DT>(p + e0, pv);
-            load_idx8(a.idx + e0, ix);
-        } else {
-            int64_t r = row, c = col;
+        for (; ch < nchunks; ch += stride) {
+            e0 = ch * kChunk;
+            float gv[kChunk], pv[kChunk];
+            uint32_t ix[kChunk];
+            const bool full = e0 + kChunk <= a.N;
+            if (full) {
+                load8<DT>(g + e0, gv);
+                if (a.write_p) load8<DT>(p + e0, pv);
+                load_idx8(a.idx + e0, ix);
+            } else {
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (k < nvalid) {
-                    gv[k] = to_f32<DT>(g[r * a.gs0 + c * a.gs1]);
-                    pv[k] = a.write_p ? to_f32<DT>(p[r * a.ps0 + c * a.ps1]) : 0.0f;
-                    ix[k] = a.idx[e0 + k];
-                    if (++c == a.C) { c = 0; ++r; }
-                } else {
-                    gv[k] = 0.0f;
-                    pv[k] = 0.0f;
-                    ix[k] = 0u;
+                for (int k = 0; k < kChunk; ++k) {
+                    const bool v = e0 + k < a.N;
+                    gv[k] = v ? to_f32<DT>(g[e0 + k]) : 0.0f;
+                    pv[k] = (v && a.write_p) ? to_f32<DT>(p[e0 + k]) : 0.0f;
+                    ix[k] = v ? (uint32_t)a.idx[e0 + k] : 0u;
                 }
             }
-        }
-        float m_old = a.mag_old[blk];
-        float m_new = a.mag_new[blk];
-        float bstep = 0.0f;
-        if constexpr (MODE == 1) bstep = a.step[blk];
-        float vr = 0.0f;
-        if constexpr (MODE == 0) vr = a.v_row[row];
-        int64_t r = row, c = col;
+            const float m_old = a.mag_old[blk];
+            const float m_new = a.mag_new[blk];
+            const float y = a.minv[blk];
+            const bool nz = m_new > 0.0f;
+            float vcv[kChunk];
+            float rs = 0.0f, bstep = 0.0f;
+            if constexpr (MODE == 0) {
+                if (a.write_p) {
+                    rs = a.v_row[row] * row_scale;
+                    const f32x4* vc4 = reinterpret_cast<const f32x4*>(a.v_col + col);
+                    const f32x4 v0 = vc4[0], v1 = vc4[1];
+                    vcv[0] = v0.x; vcv[1] = v0.y; vcv[2] = v0.z; vcv[3] = v0.w;
+                    vcv[4] = v1.x; vcv[5] = v1.y; vcv[6] = v1.z; vcv[7] = v1.w;
+                }
+            } else {
+                bstep = a.step[blk] * sc.lr;
+            }
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-            if (k < nvalid) {
+            for (int k = 0; k < kChunk; ++k) {
                 const float u = momentum_value(st.cbr[ix[k]], m_old, gv[k], a.mc);
-                const float x = (m_new > 0.0f) ? u / m_new : 0.0f;
+                const float x = nz ? div_by_block(u, m_new, y) : 0.0f;
                 uint32_t ni;
                 if constexpr (SR) ni = quant_stochastic(x, ssr.cb, ssr.lut, kk, seed, e0 + k);
                 else ni = quant_nearest(x, st.bkt, st.thr, kmax);
                 ix[k] = ni;
                 if (a.write_p) {
                     const float q = st.cbr[ni] * m_new;
-                    float stepv;
+                    float s;
                     if constexpr (MODE == 0) {
-                        const float vhat = (vr * a.v_col[c]) * inv_mean;
-                        const float h = sqrtf(vhat * sc.inv_bc2) + a.eps;
-                        stepv = (1.0f / h) * sc.inv_bc1;
+                        const float h = __builtin_amdgcn_sqrtf(rs * vcv[k]) + a.eps;
+                        s = __builtin_amdgcn_rcpf(h) * c1;
                     } else {
-                        stepv = bstep;
+                        s = bstep;
                     }
-                    const float upd = (q * stepv) * sc.lr;
                     float pw = pv[k];
-                    if (sc.wdf != 1.0f) pw = round_dt<DT>(pw * sc.wdf);
-                    pv[k] = pw - upd;
+                    if (wd) pw = round_dt<DT>(pw * sc.wdf);
+                    pv[k] = pw - q * s;
                 }
-                if (++c == a.C) {
-                    c = 0;
-                    ++r;
-                    if constexpr (MODE == 0) {
-                        if (k + 1 < nvalid) vr = a.v_row[r];
-                    }
-                }
-                if (++pin == a.P) {
-                    pin = 0;
-                    ++blk;
-                    if (k + 1 < nvalid) {
-                        m_old = a.mag_old[blk];
-                        m_new = a.mag_new[blk];
-                        if constexpr (MODE == 1) bstep = a.step[blk];
+            }
+            if (full) {
+                store_idx8(a.idx + e0, ix);
+                if (a.write_p) store8<DT>(p + e0, pv);
+            } else {
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) {
+                    if (e0 + k < a.N) {
+                        a.idx[e0 + k] = (uint8_t)ix[k];
+                        if (a.write_p) p[e0 + k] = from_f32<DT>(pv[k]);
                     }
                 }
             }
+            if constexpr (MODE == 0) {
+                col += a.dC;
+                row += a.dR;
+                if (col >= a.C) { col -= a.C; ++row; }
+            }
+            pin += a.dP;
+            blk += a.dB;
+            if (pin >= a.P) { pin -= a.P; ++blk; }
         }
-        if (vec) {
-            store_idx8(a.idx + e0, ix);
-            if (a.write_p) store8<DT>(p + e0, pv);
-        } else {
+    } else {
+        for (; ch < nchunks; ch += stride) {
+            const int64_t e0 = ch * kChunk;
+            const int nvalid = (int)std::min<int64_t>(kChunk, a.N - e0);
+            int64_t row = div_floor(e0, a.C, a.invC);
+            int64_t col = e0 - row * a.C;
+            int64_t blk = div_floor(e0, a.P, a.invP);
+            int64_t pin = e0 - blk * a.P;
+            float gv[kChunk], pv[kChunk];
+            uint32_t ix[kChunk];
+            {
+                int64_t r = row, c = col;
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) {
+                    if (k < nvalid) {
+                        gv[k] = to_f32<DT>(g[r * a.gs0 + c * a.gs1]);
+                        pv[k] = a.write_p ? to_f32<DT>(p[r * a.ps0 + c * a.ps1]) : 0.0f;
+                        ix[k] = a.idx[e0 + k];
+                        if (++c == a.C) { c = 0; ++r; }
+                    } else {
+                        gv[k] = 0.0f;
+                        pv[k] = 0.0f;
+                        ix[k] = 0u;
+                    }
+                }
+            }
+            float m_old = a.mag_old[blk];
+            float m_new = a.mag_new[blk];
+            float y = a.minv[blk];
+            float bstep = 0.0f;
+            if constexpr (MODE == 1) bstep = a.step[blk] * sc.lr;
+            float rs = 0.0f;
+            if constexpr (MODE == 0) rs = a.v_row[row] * row_scale;
+            int64_t r = row, c = col;
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if (k < nvalid) {
+                    const float u = momentum_value(st.cbr[ix[k]], m_old, gv[k], a.mc);
+                    const float x = (m_new > 0.0f) ? div_by_block(u, m_new, y) : 0.0f;
+                    uint32_t ni;
+                    if constexpr (SR) ni = quant_stochastic(x, ssr.cb, ssr.lut, kk, seed, e0 + k);
+                    else ni = quant_nearest(x, st.bkt, st.thr, kmax);
+                    ix[k] = ni;
+                    if (a.write_p) {
+                        const float q = st.cbr[ni] * m_new;
+                        float s;
+                        if constexpr (MODE == 0) {
+                            const float h = __builtin_amdgcn_sqrtf(rs * a.v_col[c]) + a.eps;
+                            s = __builtin_amdgcn_rcpf(h) * c1;
+                        } else {
+                            s = bstep;
+                        }
+                        float pw = pv[k];
+                        if (wd) pw = round_dt<DT>(pw * sc.wdf);
+                        pv[k] = pw - q * s;
+                    }
+                    if (++c == a.C) {
+                        c = 0;
+                        ++r;
+                        if constexpr (MODE == 0) {
+                            if (k + 1 < nvalid) rs = a.v_row[r] * row_scale;
+                        }
+                    }
+                    if (++pin == a.P) {
+                        pin = 0;
+                        ++blk;
+                        if (k + 1 < nvalid) {
+                            m_old = a.mag_old[blk];
+                            m_new = a.mag_new[blk];
+                            y = a.minv[blk];
+                            if constexpr (MODE == 1) bstep = a.step[blk] * sc.lr;
+                        }
+                    }
+                }
+            }
             int64_t rr = row, cc = col;
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
@@ -515,23 +726,33 @@ static int grid_for(int64_t work_items, int per_block, int cap) {
     return (int)g;
 }
 
-constexpr int kApplyGridCap = 8192;
+constexpr int kApplyGridCap = 4096;
 
-template <int MODE, bool SR>
+template <int MODE, bool SR, bool FAST>
 static void launch_apply_dt(int dtype, const ApplyArgs& a, int grid, hipStream_t s) {
     switch (dtype) {
-        case F32: hipLaunchKernelGGL((k_apply<F32, MODE, SR>), dim3(grid), dim3(kThreads), 0, s, a); break;
-        case F16: hipLaunchKernelGGL((k_apply<F16, MODE, SR>), dim3(grid), dim3(kThreads), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_apply<BF16, MODE, SR>), dim3(grid), dim3(kThreads), 0, s, a); break;
+        case F32: hipLaunchKernelGGL((k_apply<F32, MODE, SR, FAST>), dim3(grid), dim3(kThreads), 0, s, a); break;
+        case F16: hipLaunchKernelGGL((k_apply<F16, MODE, SR, FAST>), dim3(grid), dim3(kThreads), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_apply<BF16, MODE, SR, FAST>), dim3(grid), dim3(kThreads), 0, s, a); break;
     }
 }
 
 template <int MODE>
-static void launch_apply(int dtype, bool sr, const ApplyArgs& a, hipStream_t s) {
+static void launch_apply(int dtype, bool sr, bool fast, ApplyArgs a, hipStream_t s) {
     const int64_t nchunks = (a.N + kChunk - 1) / kChunk;
     const int grid = grid_for(nchunks, kThreads, kApplyGridCap);
-    if (sr) launch_apply_dt<MODE, true>(dtype, a, grid, s);
-    else launch_apply_dt<MODE, false>(dtype, a, grid, s);
+    const int64_t S = (int64_t)grid * kThreads * kChunk;
+    a.dR = S / a.C;
+    a.dC = S - a.dR * a.C;
+    a.dB = S / a.P;
+    a.dP = S - a.dB * a.P;
+    if (fast) {
+        if (sr) launch_apply_dt<MODE, true, true>(dtype, a, grid, s);
+        else launch_apply_dt<MODE, false, true>(dtype, a, grid, s);
+    } else {
+        if (sr) launch_apply_dt<MODE, true, false>(dtype, a, grid, s);
+        else launch_apply_dt<MODE, false, false>(dtype, a, grid, s);
+    }
 }
 
 static size_t elem_size(int dtype) { return dtype == F32 ? 4 : 2; }
@@ -546,65 +767,71 @@ int factored_update(void* p, const void* grad, int dtype, int64_t R, int64_t C,
     const int64_t N = R * C;
     const int64_t nb = N / period;
     const FactoredWs L = FactoredWs::make(R, C, nb);
+    const FactTiles tiles = FactTiles::make(R, C);
     if (ws_bytes < L.total)
         return set_error(GEFENX_EINVAL, "factored update: workspace %zu bytes < required %zu", ws_bytes, L.total);
     char* ws = static_cast<char*>(workspace);
-    double* row_sq = reinterpret_cast<double*>(ws + L.off_row);
-    double* col_sq = reinterpret_cast<double*>(ws + L.off_col);
+    double* row_part = reinterpret_cast<double*>(ws + L.off_rowp);
+    double* col_part = reinterpret_cast<double*>(ws + L.off_colp);
     uint32_t* magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
     float* mag_old = reinterpret_cast<float*>(ws + L.off_magold);
-    float* scal = reinterpret_cast<float*>(ws + L.off_scal);
+    float* minv = reinterpret_cast<float*>(ws + L.off_minv);
+    double* vsum = reinterpret_cast<double*>(ws + L.off_vsum);
+    const int64_t shards = mag_shards(nb);
     const QTable* qt = static_cast<const QTable*>(qtable);
     const MomentumCoef mc = make_coef(beta1);
     const bool contig_g = (gs1 == 1 && gs0 == C);
     const bool contig_p = (ps1 == 1 && ps0 == C);
+    const double es = (double)elem_size(dtype);
 
-    // stats
     FactStatsArgs sa;
     sa.grad = grad; sa.idx = m_codebook; sa.mag_old = m_magnitude; sa.qt = qt;
     sa.R = R; sa.C = C; sa.gs0 = gs0; sa.gs1 = gs1; sa.P = period; sa.invP = 1.0 / (double)period;
+    sa.tile_rows = tiles.tile_rows; sa.ct = tiles.ct;
     sa.fast = contig_g && (C % kChunk == 0) && aligned(grad, 16) && aligned(m_codebook, 8);
-    sa.row_sq = row_sq; sa.col_sq = col_sq; sa.magbits = magbits; sa.mc = mc;
-    const int64_t col_tiles = (C + kTileCols - 1) / kTileCols;
-    int64_t tile_rows = (R * col_tiles) / 2048;  // aim for >= ~2048 workgroups
-    tile_rows = std::max<int64_t>(1, std::min<int64_t>(kMaxTileRows, tile_rows));
-    sa.tile_rows = (int)tile_rows;
-    const int64_t row_tiles = (R + tile_rows - 1) / tile_rows;
-    if (row_tiles > 2147483647LL || col_tiles > 65535)
+    sa.row_part = row_part; sa.col_part = col_part; sa.magbits = magbits; sa.mc = mc;
+    sa.nb = nb; sa.shards = shards;
+    const int64_t nwg = tiles.ct * tiles.rt;
+    if (nwg > 2147483647LL)
         return set_error(GEFENX_EINVAL, "factored update: shape [%lld, %lld] exceeds the launch grid",
                          (long long)R, (long long)C);
-    dim3 sgrid((unsigned)col_tiles, (unsigned)row_tiles);
-    const double es = (double)elem_size(dtype);
     int ph = prof_begin(GEFENX_K_STATS, (double)N * (es + 1.0), 0.0, s);
+#define GX_STATS(DTV)                                                                                   \
+    if (sa.fast) hipLaunchKernelGGL((k_factored_stats<DTV, true>), dim3((unsigned)nwg), dim3(kThreads), 0, s, sa); \
+    else hipLaunchKernelGGL((k_factored_stats<DTV, false>), dim3((unsigned)nwg), dim3(kThreads), 0, s, sa)
     switch (dtype) {
-        case F32: hipLaunchKernelGGL(k_factored_stats<F32>, sgrid, dim3(kThreads), 0, s, sa); break;
-        case F16: hipLaunchKernelGGL(k_factored_stats<F16>, sgrid, dim3(kThreads), 0, s, sa); break;
-        default: hipLaunchKernelGGL(k_factored_stats<BF16>, sgrid, dim3(kThreads), 0, s, sa); break;
+        case F32: GX_STATS(F32); break;
+        case F16: GX_STATS(F16); break;
+        default: GX_STATS(BF16); break;
     }
+#undef GX_STATS
     prof_end(ph, s);
     int rc = launch_check("k_factored_stats");
     if (rc) return rc;
 
-    // finalize
     FactFinArgs fa;
-    fa.row_sq = row_sq; fa.col_sq = col_sq; fa.v_row = v_row; fa.v_col = v_col;
-    fa.R = R; fa.C = C; fa.nb = nb; fa.beta2 = (float)beta2; fa.alpha2 = (float)(1.0 - beta2);
-    fa.magbits = magbits; fa.mag = m_magnitude; fa.mag_old = mag_old; fa.scal = scal;
-    const int fgrid = 1 + grid_for(nb, kThreads * 8, 1024);
+    fa.row_part = row_part; fa.col_part = col_part; fa.v_row = v_row; fa.v_col = v_col;
+    fa.R = R; fa.C = C; fa.nb = nb; fa.ct = tiles.ct; fa.rt = tiles.rt;
+    fa.beta2 = (float)beta2; fa.alpha2 = (float)(1.0 - beta2);
+    fa.magbits = magbits; fa.mag = m_magnitude; fa.mag_old = mag_old; fa.minv = minv; fa.vsum = vsum;
+    fa.shards = shards;
+    fa.nr = (R + kFinRowsPerWg - 1) / kFinRowsPerWg;
+    fa.nc = (C + 63) / 64;
+    const int64_t fgrid = fa.nr + fa.nc + grid_for(nb, kThreads * 4, 1024);
     ph = prof_begin(GEFENX_K_FINALIZE, 8.0 * (double)(R + C + nb), 0.0, s);
-    hipLaunchKernelGGL(k_factored_finalize, dim3(fgrid), dim3(kThreads), 0, s, fa);
+    hipLaunchKernelGGL(k_factored_finalize, dim3((unsigned)fgrid), dim3(kThreads), 0, s, fa);
     prof_end(ph, s);
     rc = launch_check("k_factored_finalize");
     if (rc) return rc;
 
-    // apply
     ApplyArgs aa{};
     aa.p = p; aa.grad = grad; aa.idx = m_codebook; aa.mag_old = mag_old; aa.mag_new = m_magnitude;
-    aa.v_row = v_row; aa.v_col = v_col; aa.scal = scal; aa.step = nullptr; aa.qt = qt;
+    aa.minv = minv; aa.v_row = v_row; aa.v_col = v_col; aa.vsum = vsum; aa.nr = fa.nr; aa.R = R;
+    aa.step = nullptr; aa.qt = qt;
     aa.N = N; aa.C = C; aa.P = period; aa.invC = 1.0 / (double)C; aa.invP = 1.0 / (double)period;
     aa.ps0 = ps0; aa.ps1 = ps1; aa.gs0 = gs0; aa.gs1 = gs1;
-    aa.fast = contig_g && contig_p && (C % kChunk == 0) && aligned(grad, 16) && aligned(p, 16) &&
-              aligned(m_codebook, 8);
+    const bool fast = contig_g && contig_p && (C % kChunk == 0) && (period % kChunk == 0) &&
+                      aligned(grad, 16) && aligned(p, 16) && aligned(m_codebook, 8) && aligned(v_col, 16);
     aa.write_p = (step_scalars != nullptr) || !(lr == 0.0 && (float)wdf == 1.0f);
     aa.eps = (float)eps;
     aa.sc = StepScalars{(float)lr, (float)inv_bc2, (float)inv_bc1, (float)wdf};
@@ -615,7 +842,7 @@ int factored_update(void* p, const void* grad, int dtype, int64_t R, int64_t C,
     // algorithmic bytes of the whole step: p r/w, g r, idx r/w per element
     // plus the fp32 state vectors read and written
     ph = prof_begin(GEFENX_K_APPLY, (double)N * (3.0 * es + 2.0) + 8.0 * (double)(R + C + nb), 0.0, s);
-    launch_apply<0>(dtype, stochastic_round != 0, aa, s);
+    launch_apply<0>(dtype, stochastic_round != 0, fast, aa, s);
     prof_end(ph, s);
     return launch_check("k_apply(factored)");
 }
@@ -635,17 +862,19 @@ int block_update(void* p, const void* grad, int dtype, int64_t N, int64_t period
     uint32_t* magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
     float* mag_old = reinterpret_cast<float*>(ws + L.off_magold);
     float* step = reinterpret_cast<float*>(ws + L.off_step);
+    float* minv = reinterpret_cast<float*>(ws + L.off_minv);
     const QTable* qt = static_cast<const QTable*>(qtable);
     const MomentumCoef mc = make_coef(beta1);
+    const double es = (double)elem_size(dtype);
 
     BlockStatsArgs sa;
     sa.grad = grad; sa.idx = m_codebook; sa.mag_old = m_magnitude; sa.qt = qt;
     sa.N = N; sa.P = period; sa.invP = 1.0 / (double)period;
     sa.fast = aligned(grad, 16) && aligned(m_codebook, 8);
     sa.blk_sq = blk_sq; sa.magbits = magbits; sa.mc = mc;
+    sa.nb = nb; sa.shards = mag_shards(nb);
     const int64_t nchunks = (N + kChunk - 1) / kChunk;
     const int sgrid = grid_for(nchunks, kThreads * 4, kApplyGridCap);
-    const double es = (double)elem_size(dtype);
     int ph = prof_begin(GEFENX_K_STATS, (double)N * (es + 1.0), 0.0, s);
     switch (dtype) {
         case F32: hipLaunchKernelGGL(k_block_stats<F32>, dim3(sgrid), dim3(kThreads), 0, s, sa); break;
@@ -662,7 +891,8 @@ int block_update(void* p, const void* grad, int dtype, int64_t N, int64_t period
     fa.bf16_mean = (dtype == BF16) ? 1 : 0;
     fa.sc = StepScalars{(float)lr, (float)inv_sqrt_bc2, (float)inv_bc1, (float)wdf};
     fa.step_scalars = step_scalars;
-    fa.magbits = magbits; fa.mag = m_magnitude; fa.mag_old = mag_old; fa.step = step;
+    fa.magbits = magbits; fa.mag = m_magnitude; fa.mag_old = mag_old; fa.step = step; fa.minv = minv;
+    fa.shards = mag_shards(nb);
     ph = prof_begin(GEFENX_K_FINALIZE, 16.0 * (double)nb, 0.0, s);
     hipLaunchKernelGGL(k_block_finalize, dim3(grid_for(nb, kThreads, 4096)), dim3(kThreads), 0, s, fa);
     prof_end(ph, s);
@@ -671,10 +901,10 @@ int block_update(void* p, const void* grad, int dtype, int64_t N, int64_t period
 
     ApplyArgs aa{};
     aa.p = p; aa.grad = grad; aa.idx = m_codebook; aa.mag_old = mag_old; aa.mag_new = m_magnitude;
-    aa.step = step; aa.qt = qt;
+    aa.minv = minv; aa.step = step; aa.qt = qt;
     aa.N = N; aa.C = N; aa.P = period; aa.invC = 1.0 / (double)N; aa.invP = 1.0 / (double)period;
     aa.ps0 = N; aa.ps1 = 1; aa.gs0 = N; aa.gs1 = 1;
-    aa.fast = aligned(grad, 16) && aligned(p, 16) && aligned(m_codebook, 8);
+    const bool fast = (period % kChunk == 0) && aligned(grad, 16) && aligned(p, 16) && aligned(m_codebook, 8);
     aa.write_p = (step_scalars != nullptr) || !(lr == 0.0 && (float)wdf == 1.0f);
     aa.eps = (float)eps;
     aa.sc = fa.sc;
@@ -683,7 +913,7 @@ int block_update(void* p, const void* grad, int dtype, int64_t N, int64_t period
     aa.seed = (uint64_t)rng_seed;
     aa.seed_dev = seed_dev;
     ph = prof_begin(GEFENX_K_APPLY, (double)N * (3.0 * es + 2.0) + 16.0 * (double)nb, 0.0, s);
-    launch_apply<1>(dtype, stochastic_round != 0, aa, s);
+    launch_apply<1>(dtype, stochastic_round != 0, fast, aa, s);
     prof_end(ph, s);
     return launch_check("k_apply(block)");
 }

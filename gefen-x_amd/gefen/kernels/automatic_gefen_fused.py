@@ -13,7 +13,6 @@ from __future__ import annotations
 
 import ctypes
 import os
-import weakref
 from typing import Optional
 
 import torch
@@ -23,7 +22,6 @@ from . import _native
 _LUT_BUCKETS = 4096
 _LUT_CACHE: dict = {}
 _QTABLE_CACHE: dict = {}
-_WS_CACHE: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 
 # Routing constants of the reference (kernels/automatic_gefen_fused.py:23-50).
 # This build has ONE block-path kernel set; the predicates are kept because
@@ -120,13 +118,18 @@ def quant_table(codebook: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 
 def workspace_for(anchor: torch.Tensor, kind: int, rows: int, cols: int, num_blocks: int) -> torch.Tensor:
-    """Zero-initialised device workspace cached per state tensor `anchor`; the
-    kernels leave it zeroed after every call, so it is reused across steps."""
+    """Zero-initialised device workspace cached on the state tensor `anchor`
+    (it lives exactly as long as the state); the kernels leave every
+    accumulator zeroed after each call, so it is reused across steps."""
     nbytes = int(_native.load().gefenx_workspace_bytes(kind, rows, cols, num_blocks))
-    ws = _WS_CACHE.get(anchor)
+    cache = getattr(anchor, "_gefenx_ws", None)
+    ws = None if cache is None else cache.get(kind)
     if ws is None or ws.numel() < nbytes or ws.device != anchor.device:
         ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=anchor.device)
-        _WS_CACHE[anchor] = ws
+        if cache is None:
+            cache = {}
+            anchor._gefenx_ws = cache
+        cache[kind] = ws
     return ws
 
 
