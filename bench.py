@@ -117,7 +117,20 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy 4 times (scale for rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args(argv)
+    if args.calibrate_copy:
+        import torch
+        src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
+                          "launches": 4}))
+        return 0
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs the optimizer step on a single GPU "
               "(multi-GPU sharding is a design note, not part of this build); got --gpus %d" % args.gpus,

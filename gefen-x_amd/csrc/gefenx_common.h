@@ -18,7 +18,7 @@ struct QTable {
     int32_t k;                       // codebook size (1..256)
     int32_t dtype;                   // grad dtype the dequant table rounds through
     int32_t n_thr;                   // k - 1 decision thresholds
-    int32_t pad0;
+    int32_t max_cnt;                 // most thresholds falling in one bucket
     float cb[kCodebookMax];          // raw fp32 codebook (padded with its last entry)
     float cbr[kCodebookMax];         // codebook rounded through the grad dtype
     float thr[kCodebookMax];         // thr[i] = largest x in [-1,1] with nearest(x) <= i

@@ -105,6 +105,38 @@ __device__ __forceinline__ void store_idx8(uint8_t* __restrict__ base, const uin
     __builtin_nontemporal_store(a, reinterpret_cast<u32x2*>(base));
 }
 
+// Packed (as-loaded) 8-element chunks: loads stay packed while in flight and
+// are unpacked element by element at use (k is a compile-time index).
+template <int DT> struct Raw8 { uint32_t w[4]; };
+template <> struct Raw8<F32> { float f[8]; };
+
+template <int DT>
+__device__ __forceinline__ void load_raw8(const typename Elem<DT>::T* __restrict__ base, Raw8<DT>& r) {
+    if constexpr (DT == F32) {
+        load8<F32>(base, r.f);
+    } else {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(base);
+        r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float raw_elem(const Raw8<DT>& r, int k) {
+    if constexpr (DT == F32) return r.f[k];
+    else return to_f32<DT>((uint16_t)((k & 1) ? (r.w[k >> 1] >> 16) : (r.w[k >> 1] & 0xffffu)));
+}
+
+struct RawIdx8 { uint32_t lo, hi; };
+
+__device__ __forceinline__ RawIdx8 load_raw_idx8(const uint8_t* __restrict__ base) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(base);
+    return RawIdx8{v.x, v.y};
+}
+
+__device__ __forceinline__ uint32_t raw_idx(const RawIdx8& r, int k) {
+    return ((k < 4 ? r.lo : r.hi) >> (8 * (k & 3))) & 0xffu;
+}
+
 // --------------------------------------------------------- momentum math
 
 struct MomentumCoef {
@@ -220,11 +252,13 @@ __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
     return v;
 }
 
-// Stage the quantisation table parts a kernel needs into LDS.
+// Stage the quantisation table parts a kernel needs into LDS.  thr is padded
+// with +inf and bkt with a copy of its last bucket so the fast quantiser needs
+// no bounds checks (x = 1 lands in bucket 4096).
 struct SharedTables {
     float cbr[kCodebookMax];
-    float thr[kCodebookMax];
-    uint32_t bkt[kBuckets];
+    float thr[kCodebookMax + 4];
+    uint32_t bkt[kBuckets + 4];
 };
 
 __device__ __forceinline__ void stage_tables(SharedTables& s, const QTable* __restrict__ t) {
@@ -237,6 +271,26 @@ __device__ __forceinline__ void stage_tables(SharedTables& s, const QTable* __re
         s.cbr[i] = t->cbr[i];
         s.thr[i] = t->thr[i];
     }
+    if (tid < 4) {
+        s.thr[kCodebookMax + tid] = __builtin_inff();
+        s.bkt[kBuckets + tid] = t->bucket[kBuckets - 1];
+    }
+}
+
+// Nearest index for x in [-1, 1] (never NaN).  Thresholds in later buckets
+// are > x, so the first two slots from the bucket's base can be compared
+// unconditionally; buckets holding more than two thresholds (`dense` tables
+// only) continue with the remaining ones.
+__device__ __forceinline__ uint32_t quant_fast(float x, const SharedTables& s, bool dense) {
+    const int b = (int)__builtin_fmaf(x, (float)(kBuckets / 2), (float)(kBuckets / 2));
+    const uint32_t e = s.bkt[b];
+    const uint32_t base = e & 0xffffu;
+    uint32_t idx = base + (s.thr[base] < x ? 1u : 0u) + (s.thr[base + 1] < x ? 1u : 0u);
+    if (dense) {
+        const uint32_t cnt = e >> 16;
+        for (uint32_t j = 2; j < cnt; ++j) idx += (s.thr[base + j] < x) ? 1u : 0u;
+    }
+    return idx;
 }
 
 struct SharedSR {

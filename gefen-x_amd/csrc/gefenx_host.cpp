@@ -167,11 +167,13 @@ int gefenx_qtable_build(const float* codebook, int k, int dtype, void* table_out
     std::vector<int> bt((size_t)std::max(k - 1, 1));
     for (int i = 0; i < k - 1; ++i) bt[(size_t)i] = bucket_of(t->thr[i]);
     int j = 0;
+    t->max_cnt = 0;
     for (int b = 0; b < kBuckets; ++b) {
         while (j < k - 1 && bt[(size_t)j] < b) ++j;
         int base = j, cnt = 0;
         while (j + cnt < k - 1 && bt[(size_t)(j + cnt)] == b) ++cnt;
         t->bucket[b] = (uint32_t)base | ((uint32_t)cnt << 16);
+        t->max_cnt = std::max(t->max_cnt, cnt);
     }
     int rc = gefenx_search_lut(codebook, k, kBuckets, t->lut);
     if (rc != GEFENX_OK) return rc;

@@ -106,28 +106,55 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(FactStatsArgs a) {
     WaveMax wm{-1, 0u};
     float mag_cur = 0.0f;
 
-    for (int64_t r = r_begin + wave; r < r_end; r += kThreads / 64) {
-        const int64_t e0 = r * a.C + c0;
-        float gv[kChunk];
-        uint32_t ix[kChunk];
-        if (FAST) {
-            if (nvalid == kChunk) {
-                load8<DT>(g + e0, gv);
-                load_idx8(a.idx + e0, ix);
-            } else {
+    // kU rows of a wave are loaded before any is reduced, so each lane keeps
+    // kU grad + index loads in flight.
+    constexpr int kU = 4;
+    constexpr int64_t kWaves = kThreads / 64;
+    for (int64_t rg = r_begin + wave; rg < r_end; rg += kU * kWaves) {
+    Raw8<DT> graw[kU];
+    RawIdx8 iraw[kU];
+    float gvu[kU][kChunk];
+    uint32_t ixu[kU][kChunk];
 #pragma unroll
-                for (int k = 0; k < kChunk; ++k) { gv[k] = 0.0f; ix[k] = 0u; }
+    for (int u = 0; u < kU; ++u) {
+        const int64_t r = rg + (int64_t)u * kWaves;
+        const int64_t e0 = r * a.C + c0;
+        if constexpr (FAST) {
+            if (r < r_end && nvalid == kChunk) {
+                load_raw8<DT>(g + e0, graw[u]);
+                iraw[u] = load_raw_idx8(a.idx + e0);
+            } else {
+                graw[u] = Raw8<DT>{};
+                iraw[u] = RawIdx8{0u, 0u};
             }
         } else {
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                if (k < nvalid) {
-                    gv[k] = to_f32<DT>(g[r * a.gs0 + (c0 + k) * a.gs1]);
-                    ix[k] = a.idx[e0 + k];
+                if (r < r_end && k < nvalid) {
+                    gvu[u][k] = to_f32<DT>(g[r * a.gs0 + (c0 + k) * a.gs1]);
+                    ixu[u][k] = a.idx[e0 + k];
                 } else {
-                    gv[k] = 0.0f;
-                    ix[k] = 0u;
+                    gvu[u][k] = 0.0f;
+                    ixu[u][k] = 0u;
                 }
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        const int64_t r = rg + (int64_t)u * kWaves;
+        if (r >= r_end) break;
+        const int64_t e0 = r * a.C + c0;
+        float gv[kChunk];
+        uint32_t ix[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if constexpr (FAST) {
+                gv[k] = raw_elem<DT>(graw[u], k);
+                ix[k] = raw_idx(iraw[u], k);
+            } else {
+                gv[k] = gvu[u][k];
+                ix[k] = ixu[u][k];
             }
         }
         // block of this row strip: uniform across the wave when the wave's
@@ -188,6 +215,7 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(FactStatsArgs a) {
         }
         const double rs = wave_sum_d((double)rowacc);
         if (lane == 0) a.row_part[ctile * a.R + r] = rs;
+    }
     }
     // final block-max flush: one atomic per workgroup when the waves agree
     __shared__ int64_t s_wblk[kThreads / 64];
@@ -495,6 +523,96 @@ struct ApplyArgs {
     const int64_t* seed_dev;
 };
 
+// Logical position of a chunk: row/column (factored) and block/offset.
+struct Pos {
+    int64_t row, col, blk, pin;
+};
+
+template <int MODE>
+__device__ __forceinline__ Pos advance(const ApplyArgs& a, Pos q) {
+    if constexpr (MODE == 0) {
+        q.col += a.dC;
+        q.row += a.dR;
+        if (q.col >= a.C) { q.col -= a.C; ++q.row; }
+    }
+    q.pin += a.dP;
+    q.blk += a.dB;
+    if (q.pin >= a.P) { q.pin -= a.P; ++q.blk; }
+    return q;
+}
+
+__device__ __forceinline__ void load_vcol(const float* __restrict__ vc, float v[8]) {
+    const f32x4* q = reinterpret_cast<const f32x4*>(vc);
+    const f32x4 v0 = q[0], v1 = q[1];
+    v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+    v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+}
+
+// One chunk of 8 elements that shares a row and a block (fast path).  The
+// division u / m_new goes through the block reciprocal (div_by_block's
+// Markstein step) for every lane; a wave where any lane is outside that
+// step's safe range (tiny |u|, unusable reciprocal: zero, subnormal, huge,
+// inf or NaN magnitude) redoes the chunk with the fully guarded helpers.
+template <int DT, int MODE, bool SR>
+__device__ __forceinline__ void apply_chunk(const ApplyArgs& a, const SharedTables& st,
+                                            const SharedSR& ssr, int64_t e0, const Pos& ps,
+                                            const Raw8<DT>& gr, const Raw8<DT>& pr,
+                                            const RawIdx8& ir, const float vcv[kChunk],
+                                            uint32_t ix[kChunk], float pv[kChunk],
+                                            float row_scale, float c1, bool wd,
+                                            const StepScalars& sc, bool dense, uint32_t kmax,
+                                            int kk, uint64_t seed) {
+    const float m_old = a.mag_old[ps.blk];
+    const float m_new = a.mag_new[ps.blk];
+    const float y = a.minv[ps.blk];
+    const float tb = 0x1.00001p-100f * fmaxf(m_new, 1.0f);
+    float xs[kChunk];
+    bool bad = (y == 0.0f);
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        const float u = momentum_value(st.cbr[raw_idx(ir, k)], m_old, raw_elem<DT>(gr, k), a.mc);
+        const float q0 = u * y;
+        const float r = __builtin_fmaf(-q0, m_new, u);
+        xs[k] = __builtin_fmaf(r, y, q0);
+        bad = bad || !(fabsf(u) >= tb);
+    }
+    if (__any(bad)) {
+        const bool nz = m_new > 0.0f;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            const float u = momentum_value(st.cbr[raw_idx(ir, k)], m_old, raw_elem<DT>(gr, k), a.mc);
+            const float x = nz ? div_by_block(u, m_new, y) : 0.0f;
+            if constexpr (SR) ix[k] = quant_stochastic(x, ssr.cb, ssr.lut, kk, seed, e0 + k);
+            else ix[k] = quant_nearest(x, st.bkt, st.thr, kmax);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if constexpr (SR) ix[k] = quant_stochastic(xs[k], ssr.cb, ssr.lut, kk, seed, e0 + k);
+            else ix[k] = quant_fast(xs[k], st, dense);
+        }
+    }
+    if (a.write_p) {
+        float rs = 0.0f, bstep = 0.0f;
+        if constexpr (MODE == 0) rs = a.v_row[ps.row] * row_scale;
+        else bstep = a.step[ps.blk] * sc.lr;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            const float q = st.cbr[ix[k]] * m_new;
+            float s;
+            if constexpr (MODE == 0) {
+                const float h = __builtin_amdgcn_sqrtf(rs * vcv[k]) + a.eps;
+                s = __builtin_amdgcn_rcpf(h) * c1;
+            } else {
+                s = bstep;
+            }
+            float pw = raw_elem<DT>(pr, k);
+            if (wd) pw = round_dt<DT>(pw * sc.wdf);
+            pv[k] = pw - q * s;
+        }
+    }
+}
+
 template <int DT, int MODE, bool SR, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
     using T = typename Elem<DT>::T;
@@ -523,91 +641,57 @@ __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
     if (ch >= nchunks) return;
 
     if constexpr (FAST) {
-        int64_t e0 = ch * kChunk;
-        int64_t row = 0, col = e0;
-        if constexpr (MODE == 0) {
-            row = div_floor(e0, a.C, a.invC);
-            col = e0 - row * a.C;
+        // Two chunks per iteration (ch and ch + stride): both chunks' loads are
+        // issued before either is computed, so every lane keeps ~80 bytes of
+        // HBM reads in flight.  (row, col, blk, pin) of a chunk advance to the
+        // chunk one stride later by constant increments (no division).
+        Pos pa;
+        {
+            const int64_t e0 = ch * kChunk;
+            pa.row = 0;
+            pa.col = e0;
+            if constexpr (MODE == 0) {
+                pa.row = div_floor(e0, a.C, a.invC);
+                pa.col = e0 - pa.row * a.C;
+            }
+            pa.blk = div_floor(e0, a.P, a.invP);
+            pa.pin = e0 - pa.blk * a.P;
         }
-        int64_t blk = div_floor(e0, a.P, a.invP);
-        int64_t pin = e0 - blk * a.P;
-        for (; ch < nchunks; ch += stride) {
-            e0 = ch * kChunk;
-            float gv[kChunk], pv[kChunk];
+        const bool dense = a.qt->max_cnt > 2;
+        for (; ch < nchunks; ch += 2 * stride) {
+            const bool has_b = ch + stride < nchunks;
+            const Pos pb = advance<MODE>(a, pa);
+            const int64_t ea = ch * kChunk, eb = (ch + stride) * kChunk;
+            Raw8<DT> rga, rpa, rgb, rpb;
+            RawIdx8 ria, rib;
+            float va[kChunk], vb[kChunk];
+            load_raw8<DT>(g + ea, rga);
+            ria = load_raw_idx8(a.idx + ea);
+            if (a.write_p) {
+                load_raw8<DT>(p + ea, rpa);
+                if constexpr (MODE == 0) load_vcol(a.v_col + pa.col, va);
+            }
+            if (has_b) {
+                load_raw8<DT>(g + eb, rgb);
+                rib = load_raw_idx8(a.idx + eb);
+                if (a.write_p) {
+                    load_raw8<DT>(p + eb, rpb);
+                    if constexpr (MODE == 0) load_vcol(a.v_col + pb.col, vb);
+                }
+            }
             uint32_t ix[kChunk];
-            const bool full = e0 + kChunk <= a.N;
-            if (full) {
-                load8<DT>(g + e0, gv);
-                if (a.write_p) load8<DT>(p + e0, pv);
-                load_idx8(a.idx + e0, ix);
-            } else {
-#pragma unroll
-                for (int k = 0; k < kChunk; ++k) {
-                    const bool v = e0 + k < a.N;
-                    gv[k] = v ? to_f32<DT>(g[e0 + k]) : 0.0f;
-                    pv[k] = (v && a.write_p) ? to_f32<DT>(p[e0 + k]) : 0.0f;
-                    ix[k] = v ? (uint32_t)a.idx[e0 + k] : 0u;
-                }
+            float pv[kChunk];
+            apply_chunk<DT, MODE, SR>(a, st, ssr, ea, pa, rga, rpa, ria, va, ix, pv, row_scale, c1, wd, sc,
+                                      dense, kmax, kk, seed);
+            store_idx8(a.idx + ea, ix);
+            if (a.write_p) store8<DT>(p + ea, pv);
+            if (has_b) {
+                apply_chunk<DT, MODE, SR>(a, st, ssr, eb, pb, rgb, rpb, rib, vb, ix, pv, row_scale, c1, wd,
+                                          sc, dense, kmax, kk, seed);
+                store_idx8(a.idx + eb, ix);
+                if (a.write_p) store8<DT>(p + eb, pv);
             }
-            const float m_old = a.mag_old[blk];
-            const float m_new = a.mag_new[blk];
-            const float y = a.minv[blk];
-            const bool nz = m_new > 0.0f;
-            float vcv[kChunk];
-            float rs = 0.0f, bstep = 0.0f;
-            if constexpr (MODE == 0) {
-                if (a.write_p) {
-                    rs = a.v_row[row] * row_scale;
-                    const f32x4* vc4 = reinterpret_cast<const f32x4*>(a.v_col + col);
-                    const f32x4 v0 = vc4[0], v1 = vc4[1];
-                    vcv[0] = v0.x; vcv[1] = v0.y; vcv[2] = v0.z; vcv[3] = v0.w;
-                    vcv[4] = v1.x; vcv[5] = v1.y; vcv[6] = v1.z; vcv[7] = v1.w;
-                }
-            } else {
-                bstep = a.step[blk] * sc.lr;
-            }
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                const float u = momentum_value(st.cbr[ix[k]], m_old, gv[k], a.mc);
-                const float x = nz ? div_by_block(u, m_new, y) : 0.0f;
-                uint32_t ni;
-                if constexpr (SR) ni = quant_stochastic(x, ssr.cb, ssr.lut, kk, seed, e0 + k);
-                else ni = quant_nearest(x, st.bkt, st.thr, kmax);
-                ix[k] = ni;
-                if (a.write_p) {
-                    const float q = st.cbr[ni] * m_new;
-                    float s;
-                    if constexpr (MODE == 0) {
-                        const float h = __builtin_amdgcn_sqrtf(rs * vcv[k]) + a.eps;
-                        s = __builtin_amdgcn_rcpf(h) * c1;
-                    } else {
-                        s = bstep;
-                    }
-                    float pw = pv[k];
-                    if (wd) pw = round_dt<DT>(pw * sc.wdf);
-                    pv[k] = pw - q * s;
-                }
-            }
-            if (full) {
-                store_idx8(a.idx + e0, ix);
-                if (a.write_p) store8<DT>(p + e0, pv);
-            } else {
-#pragma unroll
-                for (int k = 0; k < kChunk; ++k) {
-                    if (e0 + k < a.N) {
-                        a.idx[e0 + k] = (uint8_t)ix[k];
-                        if (a.write_p) p[e0 + k] = from_f32<DT>(pv[k]);
-                    }
-                }
-            }
-            if constexpr (MODE == 0) {
-                col += a.dC;
-                row += a.dR;
-                if (col >= a.C) { col -= a.C; ++row; }
-            }
-            pin += a.dP;
-            blk += a.dB;
-            if (pin >= a.P) { pin -= a.P; ++blk; }
+            pa = advance<MODE>(a, pb);
         }
     } else {
         for (; ch < nchunks; ch += stride) {
