@@ -14,13 +14,6 @@ int gefenx_quantized_momentum_update(const void*, int, int64_t, int64_t, uint8_t
     return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: not available in this build");
 }
 
-int gefenx_multi_tensor_step(const gefenx_tensor_desc*, int, const void* const*, int, int64_t,
-                             void*, size_t, void*) {
-    return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: not available in this build");
-}
-
-size_t gefenx_multi_tensor_scratch_bytes(int) { return 0; }
-
 size_t gefenx_ns_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
 
 int gefenx_newton_schulz(void*, int64_t, int64_t, int64_t, const float*, const float*,

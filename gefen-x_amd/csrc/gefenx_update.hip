@@ -1,16 +1,20 @@
 // gefenx_update.hip -- fused Gefen update kernels for MI355X (gfx950, wave64).
 //
-// Per parameter the step is three launches on the caller's stream:
+// Per parameter the step has three phases:
 //   stats    one pass over grad + stored indices: per-block max |u| (u = the
 //            updated momentum) and the second-moment sums (per-tile row/column
 //            partial sums of g^2 for the factored path, per-block sums for the
 //            block path);
-//   finalize tiny: EMA of the second moment, mean(v_row), new magnitudes and
-//            their reciprocals, per-block stepsizes; re-zeroes the workspace
-//            accumulators;
+//   finalize tiny: EMA of the second moment, new magnitudes and their
+//            reciprocals, per-block stepsizes (block path), partial sums of
+//            v_row; re-zeroes the workspace accumulators;
 //   apply    one pass: recompute u, normalise by the new magnitude,
 //            requantise through the exact threshold table, write the indices
 //            and the parameter (decoupled weight decay folded in).
+// Every phase is a device function of (TensorWork, workgroup index): the
+// single-parameter entry points launch it for one descriptor passed by value,
+// the multi-tensor launcher (gefenx_multi_tensor_step) launches it for a
+// cohort of parameters whose workgroups are laid end to end.
 // The math follows the reference's decomposed step (gefen.py:2959-3018,
 // 3329-3486, 3776-3818); gefenx_device.h holds the bit-exact momentum,
 // division and quantisation primitives.
@@ -21,84 +25,118 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
 
 namespace gx {
 
 constexpr int kThreads = 256;
 constexpr int kChunk = 8;
+constexpr int64_t kWaves = kThreads / 64;
+constexpr int64_t kApplyChunksPerThread = 4;   // apply: 2 iterations of 2 chunks
+constexpr int64_t kBlockStatsChunksPerThread = 4;
+constexpr int64_t kFinBlocksPerWg = 1024;
 
 struct StepScalars {
     float lr, inv_bc2, inv_bc1, wdf;
 };
 
-__device__ __forceinline__ StepScalars read_scalars(StepScalars host, const float* dev) {
-    if (dev != nullptr) {
-        host.lr = dev[0];
-        host.inv_bc2 = dev[1];
-        host.inv_bc1 = dev[2];
-        host.wdf = dev[3];
+// Everything one phase needs about one parameter.  Built on the host
+// (build_work) from the C-ABI arguments; lives in kernel arguments (single
+// parameter) or in device memory (multi-tensor).
+struct TensorWork {
+    void* p;
+    const void* grad;
+    uint8_t* idx;
+    float* mag;          // m_magnitude
+    float* v0;           // factored: v_row; block: vmean
+    float* v1;           // factored: v_col
+    double* row_part;    // factored workspace
+    double* col_part;
+    double* vsum;
+    double* blk_sq;      // block workspace
+    float* step;
+    uint32_t* magbits;
+    float* mag_old;
+    float* minv;
+    const QTable* qt;
+    const float* step_scalars;
+    const int64_t* seed_dev;
+    int64_t R, C, N, P, nb;
+    double invC, invP;
+    int64_t ps0, ps1, gs0, gs1;
+    int64_t ct, rt, tile_rows, shards;
+    int64_t stats_wgs, nr, nc, nbw, fin_wgs, apply_wgs;
+    int64_t dR, dC, dB, dP;  // apply: chunk advance for a stride of apply_wgs*256*8 elements
+    uint64_t seed;
+    int32_t dtype, mode, fast_stats, fast_apply, write_p, sr, bf16_mean, pad_;
+    float eps, beta2, alpha2, pad2_;
+    StepScalars sc;
+    MomentumCoef mc;
+};
+
+__device__ __forceinline__ StepScalars read_scalars(const TensorWork& w) {
+    StepScalars s = w.sc;
+    if (w.step_scalars != nullptr) {
+        s.lr = w.step_scalars[0];
+        s.inv_bc2 = w.step_scalars[1];
+        s.inv_bc1 = w.step_scalars[2];
+        s.wdf = w.step_scalars[3];
     }
-    return host;
+    return s;
 }
 
 // Wave-uniform running block max of |u| as ordered uint bits (NaN > inf >
-// finite, so the integer max propagates NaN like torch's amax).  `blk` is
-// identical in every lane; `bits` is each lane's partial.
+// finite, so the integer max propagates NaN like torch's amax).
 struct WaveMax {
     int64_t blk;
     uint32_t bits;
 };
 
-__device__ __forceinline__ void wavemax_flush(uint32_t* __restrict__ magbits, WaveMax& wm) {
+__device__ __forceinline__ void wavemax_flush(uint32_t* __restrict__ mb, WaveMax& wm) {
     if (wm.blk >= 0) {
         const uint32_t m = wave_max_u(wm.bits);
-        if ((threadIdx.x & 63) == 0 && m != 0u) atomicMax(magbits + wm.blk, m);
+        if ((threadIdx.x & 63) == 0 && m != 0u) atomicMax(mb + wm.blk, m);
     }
     wm.bits = 0u;
 }
 
 // ====================================================================
-// Factored stats.  Workgroup = 4 waves over a tile of `tile_rows` rows x 512
-// columns: lane l owns columns [c0 + 8l, c0 + 8l + 8), wave w takes rows
+// Factored stats: workgroup = 4 waves over a tile of tile_rows rows x 512
+// columns; lane l owns columns [c0 + 8l, c0 + 8l + 8), wave w takes rows
 // r0 + w, r0 + w + 4, ...  Row sums reduce per wave (one value per row per
-// column tile), column sums reduce across the 4 waves in LDS; both are
-// written as float64 partials (no atomics, deterministic), summed by the
-// finalize kernel.
+// column tile), column sums across the 4 waves in LDS; both go out as
+// float64 partials (no atomics, deterministic) for the finalize phase.
 // ====================================================================
-struct FactStatsArgs {
-    const void* grad;
-    const uint8_t* idx;
-    const float* mag_old;
-    const QTable* qt;
-    int64_t R, C, gs0, gs1, P;
-    double invP;
-    int64_t tile_rows, ct;
-    int fast;  // contiguous grad, C % 8 == 0, P % 8 == 0, aligned
-    double* row_part;  // [ct][R]
-    double* col_part;  // [rt][C]
-    uint32_t* magbits; // [shards][nb]
-    int64_t nb, shards;
-    MomentumCoef mc;
-};
-
 template <int DT, bool FAST>
-__global__ void __launch_bounds__(kThreads) k_factored_stats(FactStatsArgs a) {
+__device__ __forceinline__ void stats_factored(const TensorWork& w, int64_t wg) {
     using T = typename Elem<DT>::T;
     __shared__ float s_cbr[kCodebookMax];
-    __shared__ double s_col[kThreads / 64 - 1][kFactTileCols];
-    for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = a.qt->cbr[i];
+    __shared__ double s_col[kWaves - 1][kFactTileCols];
+    __shared__ int64_t s_wblk[kWaves];
+    __shared__ uint32_t s_wbits[kWaves];
+    for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = w.qt->cbr[i];
     __syncthreads();
 
+    const int64_t R = w.R, C = w.C, P = w.P;
+    const double invP = w.invP;
+    const MomentumCoef mc = w.mc;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t ctile = (int64_t)blockIdx.x % a.ct;
-    const int64_t rtile = (int64_t)blockIdx.x / a.ct;
+    const int64_t ctile = wg % w.ct;
+    const int64_t rtile = wg / w.ct;
     const int64_t c0 = ctile * kFactTileCols + (int64_t)lane * kChunk;
-    const int64_t r_begin = rtile * a.tile_rows;
-    const int64_t r_end = std::min<int64_t>(r_begin + a.tile_rows, a.R);
-    const int nvalid = (int)std::max<int64_t>(0, std::min<int64_t>(kChunk, a.C - c0));
-    const T* g = static_cast<const T*>(a.grad);
-    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
+    const int64_t r_begin = rtile * w.tile_rows;
+    const int64_t r_end = std::min<int64_t>(r_begin + w.tile_rows, R);
+    const int nvalid = (int)std::max<int64_t>(0, std::min<int64_t>(kChunk, C - c0));
+    const T* g = static_cast<const T*>(w.grad);
+    const uint8_t* idxp = w.idx;
+    const float* mag_old = w.mag;
+    uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
 
     double colacc[kChunk];
 #pragma unroll
@@ -106,120 +144,116 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(FactStatsArgs a) {
     WaveMax wm{-1, 0u};
     float mag_cur = 0.0f;
 
-    // kU rows of a wave are loaded before any is reduced, so each lane keeps
-    // kU grad + index loads in flight.
+    // kU rows of a wave are loaded before any is reduced (kU loads in flight)
     constexpr int kU = 4;
-    constexpr int64_t kWaves = kThreads / 64;
     for (int64_t rg = r_begin + wave; rg < r_end; rg += kU * kWaves) {
-    Raw8<DT> graw[kU];
-    RawIdx8 iraw[kU];
-    float gvu[kU][kChunk];
-    uint32_t ixu[kU][kChunk];
+        Raw8<DT> graw[kU];
+        RawIdx8 iraw[kU];
+        float gvu[kU][kChunk];
+        uint32_t ixu[kU][kChunk];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-        const int64_t r = rg + (int64_t)u * kWaves;
-        const int64_t e0 = r * a.C + c0;
-        if constexpr (FAST) {
-            if (r < r_end && nvalid == kChunk) {
-                load_raw8<DT>(g + e0, graw[u]);
-                iraw[u] = load_raw_idx8(a.idx + e0);
-            } else {
-                graw[u] = Raw8<DT>{};
-                iraw[u] = RawIdx8{0u, 0u};
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (r < r_end && k < nvalid) {
-                    gvu[u][k] = to_f32<DT>(g[r * a.gs0 + (c0 + k) * a.gs1]);
-                    ixu[u][k] = a.idx[e0 + k];
-                } else {
-                    gvu[u][k] = 0.0f;
-                    ixu[u][k] = 0u;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-        const int64_t r = rg + (int64_t)u * kWaves;
-        if (r >= r_end) break;
-        const int64_t e0 = r * a.C + c0;
-        float gv[kChunk];
-        uint32_t ix[kChunk];
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
+        for (int u = 0; u < kU; ++u) {
+            const int64_t r = rg + (int64_t)u * kWaves;
+            const int64_t e0 = r * C + c0;
             if constexpr (FAST) {
-                gv[k] = raw_elem<DT>(graw[u], k);
-                ix[k] = raw_idx(iraw[u], k);
+                if (r < r_end && nvalid == kChunk) {
+                    load_raw8<DT>(g + e0, graw[u]);
+                    iraw[u] = load_raw_idx8(idxp + e0);
+                } else {
+                    graw[u] = Raw8<DT>{};
+                    iraw[u] = RawIdx8{0u, 0u};
+                }
             } else {
-                gv[k] = gvu[u][k];
-                ix[k] = ixu[u][k];
-            }
-        }
-        // block of this row strip: uniform across the wave when the wave's
-        // 512 columns never cross a block boundary
-        const int64_t e_first = r * a.C + ctile * kFactTileCols;
-        const int64_t blk0 = div_floor(e_first, a.P, a.invP);
-        const int64_t span = std::min<int64_t>(kFactTileCols, a.C - ctile * kFactTileCols);
-        const bool uniform = (e_first + span - 1) < (blk0 + 1) * a.P;
-        float rowacc = 0.0f;
-        if (uniform) {
-            if (blk0 != wm.blk) {
-                wavemax_flush(mb, wm);
-                wm.blk = blk0;
-                mag_cur = a.mag_old[blk0];
-            }
-            uint32_t m = wm.bits;
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (k < nvalid) {
-                    const float u = momentum_value(s_cbr[ix[k]], mag_cur, gv[k], a.mc);
-                    const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                    m = ub > m ? ub : m;
-                    const float sq = gv[k] * gv[k];
-                    rowacc += sq;
-                    colacc[k] += (double)sq;
+                for (int k = 0; k < kChunk; ++k) {
+                    if (r < r_end && k < nvalid) {
+                        gvu[u][k] = to_f32<DT>(g[r * w.gs0 + (c0 + k) * w.gs1]);
+                        ixu[u][k] = idxp[e0 + k];
+                    } else {
+                        gvu[u][k] = 0.0f;
+                        ixu[u][k] = 0u;
+                    }
                 }
             }
-            wm.bits = m;
-        } else {
-            // blocks smaller than the strip: per-lane runs, one atomic per run
-            wavemax_flush(mb, wm);
-            wm.blk = -1;
-            if (nvalid > 0) {
-                int64_t blk = div_floor(e0, a.P, a.invP);
-                int64_t pin = e0 - blk * a.P;
-                float mo = a.mag_old[blk];
-                uint32_t m = 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t r = rg + (int64_t)u * kWaves;
+            if (r >= r_end) break;
+            const int64_t e0 = r * C + c0;
+            float gv[kChunk];
+            uint32_t ix[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if constexpr (FAST) {
+                    gv[k] = raw_elem<DT>(graw[u], k);
+                    ix[k] = raw_idx(iraw[u], k);
+                } else {
+                    gv[k] = gvu[u][k];
+                    ix[k] = ixu[u][k];
+                }
+            }
+            // block of this row strip: uniform across the wave when the wave's
+            // columns never cross a block boundary
+            const int64_t e_first = r * C + ctile * kFactTileCols;
+            const int64_t blk0 = div_floor(e_first, P, invP);
+            const int64_t span = std::min<int64_t>(kFactTileCols, C - ctile * kFactTileCols);
+            const bool uniform = (e_first + span - 1) < (blk0 + 1) * P;
+            float rowacc = 0.0f;
+            if (uniform) {
+                if (blk0 != wm.blk) {
+                    wavemax_flush(mb, wm);
+                    wm.blk = blk0;
+                    mag_cur = mag_old[blk0];
+                }
+                uint32_t m = wm.bits;
 #pragma unroll
                 for (int k = 0; k < kChunk; ++k) {
                     if (k < nvalid) {
-                        const float u = momentum_value(s_cbr[ix[k]], mo, gv[k], a.mc);
-                        const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                        const float uu = momentum_value(s_cbr[ix[k]], mag_cur, gv[k], mc);
+                        const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
                         m = ub > m ? ub : m;
                         const float sq = gv[k] * gv[k];
                         rowacc += sq;
                         colacc[k] += (double)sq;
-                        if (++pin == a.P) {
-                            if (m) atomicMax(mb + blk, m);
-                            m = 0u;
-                            pin = 0;
-                            ++blk;
-                            if (k + 1 < nvalid) mo = a.mag_old[blk];
-                        }
                     }
                 }
-                if (m) atomicMax(mb + blk, m);
+                wm.bits = m;
+            } else {
+                // blocks smaller than the strip: per-lane runs, one atomic per run
+                wavemax_flush(mb, wm);
+                wm.blk = -1;
+                if (nvalid > 0) {
+                    int64_t blk = div_floor(e0, P, invP);
+                    int64_t pin = e0 - blk * P;
+                    float mo = mag_old[blk];
+                    uint32_t m = 0u;
+#pragma unroll
+                    for (int k = 0; k < kChunk; ++k) {
+                        if (k < nvalid) {
+                            const float uu = momentum_value(s_cbr[ix[k]], mo, gv[k], mc);
+                            const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
+                            m = ub > m ? ub : m;
+                            const float sq = gv[k] * gv[k];
+                            rowacc += sq;
+                            colacc[k] += (double)sq;
+                            if (++pin == P) {
+                                if (m) atomicMax(mb + blk, m);
+                                m = 0u;
+                                pin = 0;
+                                ++blk;
+                                if (k + 1 < nvalid) mo = mag_old[blk];
+                            }
+                        }
+                    }
+                    if (m) atomicMax(mb + blk, m);
+                }
             }
+            const double rs = wave_sum_d((double)rowacc);
+            if (lane == 0) w.row_part[ctile * R + r] = rs;
         }
-        const double rs = wave_sum_d((double)rowacc);
-        if (lane == 0) a.row_part[ctile * a.R + r] = rs;
-    }
     }
     // final block-max flush: one atomic per workgroup when the waves agree
-    __shared__ int64_t s_wblk[kThreads / 64];
-    __shared__ uint32_t s_wbits[kThreads / 64];
     const uint32_t wbits = wave_max_u(wm.bits);
     if (lane == 0) {
         s_wblk[wave] = wm.blk;
@@ -234,15 +268,15 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(FactStatsArgs a) {
     if (threadIdx.x == 0) {
         bool same = true;
         uint32_t m = 0u;
-        for (int w = 0; w < kThreads / 64; ++w) {
-            same = same && (s_wblk[w] == s_wblk[0]);
-            m = s_wbits[w] > m ? s_wbits[w] : m;
+        for (int ww = 0; ww < kWaves; ++ww) {
+            same = same && (s_wblk[ww] == s_wblk[0]);
+            m = s_wbits[ww] > m ? s_wbits[ww] : m;
         }
         if (same) {
             if (s_wblk[0] >= 0 && m) atomicMax(mb + s_wblk[0], m);
         } else {
-            for (int w = 0; w < kThreads / 64; ++w)
-                if (s_wblk[w] >= 0 && s_wbits[w]) atomicMax(mb + s_wblk[w], s_wbits[w]);
+            for (int ww = 0; ww < kWaves; ++ww)
+                if (s_wblk[ww] >= 0 && s_wbits[ww]) atomicMax(mb + s_wblk[ww], s_wbits[ww]);
         }
     }
     if (wave == 0) {
@@ -250,47 +284,126 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(FactStatsArgs a) {
         for (int k = 0; k < kChunk; ++k) {
             double s = colacc[k];
 #pragma unroll
-            for (int w = 0; w < kThreads / 64 - 1; ++w) s += s_col[w][lane * kChunk + k];
-            if (k < nvalid) a.col_part[rtile * a.C + c0 + k] = s;
+            for (int ww = 0; ww < kWaves - 1; ++ww) s += s_col[ww][lane * kChunk + k];
+            if (k < nvalid) w.col_part[rtile * C + c0 + k] = s;
         }
     }
 }
 
 // ====================================================================
-// Factored finalize.  Workgroups [0, nr): v_row EMA from the ct row partials,
-// one float64 partial of sum(v_row) per workgroup; [nr, nr+nc): v_col EMA
-// from the rt column partials; the rest: new magnitudes (max over shards),
-// their reciprocals, the old magnitudes.
+// Block stats: grid-stride over logical chunks of the parameter with nwg
+// workgroups; per-block sum of squares (rounded through bf16 for bf16 grads,
+// gefen.py:180-190) and max |u|.
+// ====================================================================
+template <int DT>
+__device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int64_t nwg) {
+    using T = typename Elem<DT>::T;
+    __shared__ float s_cbr[kCodebookMax];
+    for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = w.qt->cbr[i];
+    __syncthreads();
+    const T* g = static_cast<const T*>(w.grad);
+    const int64_t N = w.N, P = w.P;
+    const double invP = w.invP;
+    const MomentumCoef mc = w.mc;
+    uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
+    const int64_t nchunks = (N + kChunk - 1) / kChunk;
+    const int64_t stride = nwg * kThreads;
+    int64_t cur = -1;
+    uint32_t cbits = 0u;
+    double bsum = 0.0;
+    float mo = 0.0f;
+    for (int64_t ch = wg * kThreads + threadIdx.x; ch < nchunks; ch += stride) {
+        const int64_t e0 = ch * kChunk;
+        const int nvalid = (int)std::min<int64_t>(kChunk, N - e0);
+        float gv[kChunk];
+        uint32_t ix[kChunk];
+        if (w.fast_stats && nvalid == kChunk) {
+            load8<DT>(g + e0, gv);
+            load_idx8(w.idx + e0, ix);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                gv[k] = k < nvalid ? to_f32<DT>(g[e0 + k]) : 0.0f;
+                ix[k] = k < nvalid ? (uint32_t)w.idx[e0 + k] : 0u;
+            }
+        }
+        int64_t blk = div_floor(e0, P, invP);
+        int64_t pin = e0 - blk * P;
+        float csum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if (k < nvalid) {
+                if (blk != cur) {
+                    if (cur >= 0) {
+                        bsum += (double)csum;
+                        csum = 0.0f;
+                        if (bsum != 0.0) atomicAdd(w.blk_sq + cur, bsum);
+                        if (cbits) atomicMax(mb + cur, cbits);
+                    }
+                    bsum = 0.0;
+                    cbits = 0u;
+                    cur = blk;
+                    mo = w.mag[blk];
+                }
+                const float u = momentum_value(s_cbr[ix[k]], mo, gv[k], mc);
+                const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                cbits = ub > cbits ? ub : cbits;
+                float sq = gv[k] * gv[k];
+                if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                csum += sq;
+                if (++pin == P) { pin = 0; ++blk; }
+            }
+        }
+        bsum += (double)csum;
+    }
+    const int lane = threadIdx.x & 63;
+    const int64_t c0 = __shfl(cur, 0, 64);
+    if (__all(cur == c0)) {
+        const double s = wave_sum_d(bsum);
+        const uint32_t m = wave_max_u(cbits);
+        if (lane == 0 && c0 >= 0) {
+            if (s != 0.0) atomicAdd(w.blk_sq + c0, s);
+            if (m) atomicMax(mb + c0, m);
+        }
+    } else if (cur >= 0) {
+        if (bsum != 0.0) atomicAdd(w.blk_sq + cur, bsum);
+        if (cbits) atomicMax(mb + cur, cbits);
+    }
+}
+
+// New magnitude (max over the shards), its reciprocal and the old magnitude.
+__device__ __forceinline__ void finalize_magnitude(const TensorWork& w, int64_t b) {
+    const float old = w.mag[b];
+    w.mag_old[b] = old;
+    uint32_t bits = 0u;
+    for (int64_t sh = 0; sh < w.shards; ++sh) {
+        const uint32_t v = w.magbits[sh * w.nb + b];
+        bits = v > bits ? v : bits;
+        w.magbits[sh * w.nb + b] = 0u;
+    }
+    const float m = __uint_as_float(bits);
+    w.mag[b] = m;
+    w.minv[b] = block_recip(m);
+}
+
+// ====================================================================
+// Factored finalize.  Workgroups [0, nr): v_row EMA from the ct row partials
+// plus one float64 partial of sum(v_row); [nr, nr+nc): v_col EMA from the rt
+// column partials (64 columns each); the rest: magnitudes.
 // v <- fma(sum/n, 1-beta2, v*beta2)  (gefen.py:2994-2996)
 // ====================================================================
-struct FactFinArgs {
-    const double* row_part;
-    const double* col_part;
-    float* v_row;
-    float* v_col;
-    int64_t R, C, nb, ct, rt, shards;
-    int64_t nr, nc;   // row / column workgroup counts
-    float beta2, alpha2;
-    uint32_t* magbits;
-    float* mag;      // m_magnitude: receives the new magnitudes
-    float* mag_old;  // workspace: receives the old magnitudes
-    float* minv;     // workspace: reciprocal of the new magnitudes
-    double* vsum;    // workspace: [nr] partials of sum(v_row)
-};
-
-__global__ void __launch_bounds__(kThreads) k_factored_finalize(FactFinArgs a) {
+__device__ __forceinline__ void finalize_factored(const TensorWork& w, int64_t wg) {
     const int tid = threadIdx.x;
-    const int64_t wg = blockIdx.x;
-    if (wg < a.nr) {
-        __shared__ double s_part[kThreads / 64];
+    if (wg < w.nr) {
+        __shared__ double s_part[kWaves];
         const int64_t i = wg * kFinRowsPerWg + tid;
         double v64 = 0.0;
-        if (i < a.R) {
+        if (i < w.R) {
             double s = 0.0;
-            for (int64_t t = 0; t < a.ct; ++t) s += a.row_part[t * a.R + i];
-            const float ms = (float)s / (float)a.C;
-            const float v = __builtin_fmaf(ms, a.alpha2, a.v_row[i] * a.beta2);
-            a.v_row[i] = v;
+            for (int64_t t = 0; t < w.ct; ++t) s += w.row_part[t * w.R + i];
+            const float ms = (float)s / (float)w.C;
+            const float v = __builtin_fmaf(ms, w.alpha2, w.v0[i] * w.beta2);
+            w.v0[i] = v;
             v64 = (double)v;
         }
         v64 = wave_sum_d(v64);
@@ -298,49 +411,53 @@ __global__ void __launch_bounds__(kThreads) k_factored_finalize(FactFinArgs a) {
         __syncthreads();
         if (tid == 0) {
             double s = 0.0;
-            for (int w = 0; w < kThreads / 64; ++w) s += s_part[w];
-            a.vsum[wg] = s;
+            for (int ww = 0; ww < kWaves; ++ww) s += s_part[ww];
+            w.vsum[wg] = s;
         }
         return;
     }
-    if (wg < a.nr + a.nc) {
-        // 64 columns per workgroup; wave w adds row tiles t = w, w+4, ...
-        __shared__ double s_cp[kThreads / 64][64];
+    if (wg < w.nr + w.nc) {
+        // wave k adds row tiles t = k, k+4, ...
+        __shared__ double s_cp[kWaves][64];
         const int lane = tid & 63;
         const int wave = tid >> 6;
-        const int64_t j = (wg - a.nr) * 64 + lane;
+        const int64_t j = (wg - w.nr) * 64 + lane;
         double s = 0.0;
-        if (j < a.C)
-            for (int64_t t = wave; t < a.rt; t += kThreads / 64) s += a.col_part[t * a.C + j];
+        if (j < w.C)
+            for (int64_t t = wave; t < w.rt; t += kWaves) s += w.col_part[t * w.C + j];
         s_cp[wave][lane] = s;
         __syncthreads();
-        if (wave == 0 && j < a.C) {
+        if (wave == 0 && j < w.C) {
             double tot = 0.0;
-            for (int w = 0; w < kThreads / 64; ++w) tot += s_cp[w][lane];
-            const float ms = (float)tot / (float)a.R;
-            a.v_col[j] = __builtin_fmaf(ms, a.alpha2, a.v_col[j] * a.beta2);
+            for (int ww = 0; ww < kWaves; ++ww) tot += s_cp[ww][lane];
+            const float ms = (float)tot / (float)w.R;
+            w.v1[j] = __builtin_fmaf(ms, w.alpha2, w.v1[j] * w.beta2);
         }
         return;
     }
-    const int64_t gtid = (wg - a.nr - a.nc) * kThreads + tid;
-    const int64_t gstride = ((int64_t)gridDim.x - a.nr - a.nc) * kThreads;
-    for (int64_t b = gtid; b < a.nb; b += gstride) {
-        const float old = a.mag[b];
-        a.mag_old[b] = old;
-        uint32_t bits = 0u;
-        for (int64_t sh = 0; sh < a.shards; ++sh) {
-            const uint32_t v = a.magbits[sh * a.nb + b];
-            bits = v > bits ? v : bits;
-            a.magbits[sh * a.nb + b] = 0u;
-        }
-        const float m = __uint_as_float(bits);
-        a.mag[b] = m;
-        a.minv[b] = block_recip(m);
+    const int64_t gtid = (wg - w.nr - w.nc) * kThreads + tid;
+    const int64_t gstride = w.nbw * kThreads;
+    for (int64_t b = gtid; b < w.nb; b += gstride) finalize_magnitude(w, b);
+}
+
+// vmean EMA + per-block stepsize (gefen.py:180-190, 3794-3805) + magnitudes.
+__device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) {
+    const StepScalars sc = read_scalars(w);
+    const float fP = (float)w.P;
+    for (int64_t b = wg * kThreads + threadIdx.x; b < w.nb; b += w.nbw * kThreads) {
+        float mean = (float)w.blk_sq[b] / fP;
+        w.blk_sq[b] = 0.0;
+        if (w.bf16_mean) mean = round_dt<BF16>(mean);
+        const float v = __builtin_fmaf(mean, w.alpha2, w.v0[b] * w.beta2);
+        w.v0[b] = v;
+        const float h = sqrtf(v) * sc.inv_bc2 + w.eps;
+        w.step[b] = (1.0f / h) * sc.inv_bc1;
+        finalize_magnitude(w, b);
     }
 }
 
 // Deterministic mean(v_row) from the finalize partials, clamped at FLT_MIN
-// (gefen.py:2998-3000); every workgroup of the apply kernel recomputes it.
+// (gefen.py:2998-3000); every workgroup of the apply phase recomputes it.
 __device__ __forceinline__ float mean_from_partials(const double* __restrict__ vsum, int64_t nr, int64_t R) {
     __shared__ double s_red[kThreads];
     double acc = 0.0;
@@ -357,187 +474,25 @@ __device__ __forceinline__ float mean_from_partials(const double* __restrict__ v
 }
 
 // ====================================================================
-// Block stats: flat over logical chunks; per-block sum of squares (squares
-// rounded through bf16 for bf16 grads, gefen.py:180-190) and max |u|.
+// Apply: grid-stride over logical chunks of 8 elements with nwg workgroups.
+// MODE 0 factored, MODE 1 block.  FAST: contiguous p/grad, C % 8 == 0,
+// P % 8 == 0, aligned -- a chunk then never crosses a row or a block, and
+// (row, col, blk, pin) advance by constant strides (no per-chunk division).
 // ====================================================================
-struct BlockStatsArgs {
-    const void* grad;
-    const uint8_t* idx;
-    const float* mag_old;
-    const QTable* qt;
-    int64_t N, P;
-    double invP;
-    int fast;
-    double* blk_sq;
-    uint32_t* magbits;  // [shards][nb]
-    int64_t nb, shards;
-    MomentumCoef mc;
-};
-
-template <int DT>
-__global__ void __launch_bounds__(kThreads) k_block_stats(BlockStatsArgs a) {
-    using T = typename Elem<DT>::T;
-    __shared__ float s_cbr[kCodebookMax];
-    for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = a.qt->cbr[i];
-    __syncthreads();
-    const T* g = static_cast<const T*>(a.grad);
-    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
-    const int64_t nchunks = (a.N + kChunk - 1) / kChunk;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    int64_t cur = -1;
-    uint32_t cbits = 0u;
-    double bsum = 0.0;
-    float mo = 0.0f;
-    for (int64_t ch = (int64_t)blockIdx.x * kThreads + threadIdx.x; ch < nchunks; ch += stride) {
-        const int64_t e0 = ch * kChunk;
-        const int nvalid = (int)std::min<int64_t>(kChunk, a.N - e0);
-        float gv[kChunk];
-        uint32_t ix[kChunk];
-        if (a.fast && nvalid == kChunk) {
-            load8<DT>(g + e0, gv);
-            load_idx8(a.idx + e0, ix);
-        } else {
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                gv[k] = k < nvalid ? to_f32<DT>(g[e0 + k]) : 0.0f;
-                ix[k] = k < nvalid ? (uint32_t)a.idx[e0 + k] : 0u;
-            }
-        }
-        int64_t blk = div_floor(e0, a.P, a.invP);
-        int64_t pin = e0 - blk * a.P;
-        float csum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-            if (k < nvalid) {
-                if (blk != cur) {
-                    if (cur >= 0) {
-                        bsum += (double)csum;
-                        csum = 0.0f;
-                        if (bsum != 0.0) atomicAdd(a.blk_sq + cur, bsum);
-                        if (cbits) atomicMax(mb + cur, cbits);
-                    }
-                    bsum = 0.0;
-                    cbits = 0u;
-                    cur = blk;
-                    mo = a.mag_old[blk];
-                }
-                const float u = momentum_value(s_cbr[ix[k]], mo, gv[k], a.mc);
-                const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                cbits = ub > cbits ? ub : cbits;
-                float sq = gv[k] * gv[k];
-                if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                csum += sq;
-                if (++pin == a.P) { pin = 0; ++blk; }
-            }
-        }
-        bsum += (double)csum;
-    }
-    const int lane = threadIdx.x & 63;
-    const int64_t c0 = __shfl(cur, 0, 64);
-    if (__all(cur == c0)) {
-        const double s = wave_sum_d(bsum);
-        const uint32_t m = wave_max_u(cbits);
-        if (lane == 0 && c0 >= 0) {
-            if (s != 0.0) atomicAdd(a.blk_sq + c0, s);
-            if (m) atomicMax(mb + c0, m);
-        }
-    } else if (cur >= 0) {
-        if (bsum != 0.0) atomicAdd(a.blk_sq + cur, bsum);
-        if (cbits) atomicMax(mb + cur, cbits);
-    }
-}
-
-// vmean EMA + per-block stepsize (gefen.py:180-190, 3794-3805).
-struct BlockFinArgs {
-    double* blk_sq;
-    float* vmean;
-    int64_t nb, P;
-    float beta2, alpha2, eps;
-    int bf16_mean;
-    StepScalars sc;
-    const float* step_scalars;
-    uint32_t* magbits;
-    float* mag;
-    float* mag_old;
-    float* step;
-    float* minv;
-    int64_t shards;
-};
-
-__global__ void __launch_bounds__(kThreads) k_block_finalize(BlockFinArgs a) {
-    const StepScalars sc = read_scalars(a.sc, a.step_scalars);
-    const float fP = (float)a.P;
-    for (int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x; b < a.nb;
-         b += (int64_t)gridDim.x * kThreads) {
-        float mean = (float)a.blk_sq[b] / fP;
-        a.blk_sq[b] = 0.0;
-        if (a.bf16_mean) mean = round_dt<BF16>(mean);
-        const float v = __builtin_fmaf(mean, a.alpha2, a.vmean[b] * a.beta2);
-        a.vmean[b] = v;
-        const float h = sqrtf(v) * sc.inv_bc2 + a.eps;
-        a.step[b] = (1.0f / h) * sc.inv_bc1;
-        const float old = a.mag[b];
-        a.mag_old[b] = old;
-        uint32_t bits = 0u;
-        for (int64_t sh = 0; sh < a.shards; ++sh) {
-            const uint32_t v = a.magbits[sh * a.nb + b];
-            bits = v > bits ? v : bits;
-            a.magbits[sh * a.nb + b] = 0u;
-        }
-        const float m = __uint_as_float(bits);
-        a.mag[b] = m;
-        a.minv[b] = block_recip(m);
-    }
-}
-
-// ====================================================================
-// Apply: grid-stride over logical chunks of 8 elements.  MODE 0 factored,
-// MODE 1 block.  FAST: contiguous p/grad, C % 8 == 0, P % 8 == 0, aligned --
-// a chunk then never crosses a row or a block, and (row, col, blk) advance
-// by constant strides between iterations (no per-chunk division).
-// ====================================================================
-struct ApplyArgs {
-    void* p;
-    const void* grad;
-    uint8_t* idx;
-    const float* mag_old;
-    const float* mag_new;
-    const float* minv;
-    const float* v_row;   // factored
-    const float* v_col;   // factored
-    const double* vsum;   // factored: [nr] partials of sum(v_row)
-    int64_t nr, R;
-    const float* step;    // block: per-block stepsize
-    const QTable* qt;
-    int64_t N, C, P;
-    double invC, invP;
-    int64_t ps0, ps1, gs0, gs1;
-    // FAST iteration strides: S = gridDim.x * 256 * 8 elements = dR*C + dC = dB*P + dP
-    int64_t dR, dC, dB, dP;
-    int write_p;     // 0 when lr == 0 and wd_factor == 1
-    float eps;
-    StepScalars sc;
-    const float* step_scalars;
-    MomentumCoef mc;
-    uint64_t seed;
-    const int64_t* seed_dev;
-};
-
-// Logical position of a chunk: row/column (factored) and block/offset.
 struct Pos {
     int64_t row, col, blk, pin;
 };
 
 template <int MODE>
-__device__ __forceinline__ Pos advance(const ApplyArgs& a, Pos q) {
+__device__ __forceinline__ Pos advance(const TensorWork& w, Pos q) {
     if constexpr (MODE == 0) {
-        q.col += a.dC;
-        q.row += a.dR;
-        if (q.col >= a.C) { q.col -= a.C; ++q.row; }
+        q.col += w.dC;
+        q.row += w.dR;
+        if (q.col >= w.C) { q.col -= w.C; ++q.row; }
     }
-    q.pin += a.dP;
-    q.blk += a.dB;
-    if (q.pin >= a.P) { q.pin -= a.P; ++q.blk; }
+    q.pin += w.dP;
+    q.blk += w.dB;
+    if (q.pin >= w.P) { q.pin -= w.P; ++q.blk; }
     return q;
 }
 
@@ -548,29 +503,37 @@ __device__ __forceinline__ void load_vcol(const float* __restrict__ vc, float v[
     v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
 }
 
-// One chunk of 8 elements that shares a row and a block (fast path).  The
-// division u / m_new goes through the block reciprocal (div_by_block's
-// Markstein step) for every lane; a wave where any lane is outside that
-// step's safe range (tiny |u|, unusable reciprocal: zero, subnormal, huge,
-// inf or NaN magnitude) redoes the chunk with the fully guarded helpers.
+struct ApplyCtx {
+    float row_scale;  // (1 / mean(v_row)) * (1/bc2)
+    float c1;         // (1/bc1) * lr
+    bool wd;
+    StepScalars sc;
+    bool dense;
+    uint32_t kmax;
+    int kk;
+    uint64_t seed;
+};
+
+// One chunk of 8 elements sharing a row and a block (fast path).  u / m_new
+// goes through the block reciprocal (div_by_block's Markstein step) in every
+// lane; a wave where any lane is outside that step's safe range (tiny |u|;
+// zero, subnormal, huge, inf or NaN magnitude) redoes the chunk with the
+// fully guarded helpers.
 template <int DT, int MODE, bool SR>
-__device__ __forceinline__ void apply_chunk(const ApplyArgs& a, const SharedTables& st,
-                                            const SharedSR& ssr, int64_t e0, const Pos& ps,
-                                            const Raw8<DT>& gr, const Raw8<DT>& pr,
+__device__ __forceinline__ void apply_chunk(const TensorWork& w, const SharedTables& st,
+                                            const SharedSR& ssr, const ApplyCtx& cx, int64_t e0,
+                                            const Pos& ps, const Raw8<DT>& gr, const Raw8<DT>& pr,
                                             const RawIdx8& ir, const float vcv[kChunk],
-                                            uint32_t ix[kChunk], float pv[kChunk],
-                                            float row_scale, float c1, bool wd,
-                                            const StepScalars& sc, bool dense, uint32_t kmax,
-                                            int kk, uint64_t seed) {
-    const float m_old = a.mag_old[ps.blk];
-    const float m_new = a.mag_new[ps.blk];
-    const float y = a.minv[ps.blk];
+                                            uint32_t ix[kChunk], float pv[kChunk]) {
+    const float m_old = w.mag_old[ps.blk];
+    const float m_new = w.mag[ps.blk];
+    const float y = w.minv[ps.blk];
     const float tb = 0x1.00001p-100f * fmaxf(m_new, 1.0f);
     float xs[kChunk];
     bool bad = (y == 0.0f);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        const float u = momentum_value(st.cbr[raw_idx(ir, k)], m_old, raw_elem<DT>(gr, k), a.mc);
+        const float u = momentum_value(st.cbr[raw_idx(ir, k)], m_old, raw_elem<DT>(gr, k), w.mc);
         const float q0 = u * y;
         const float r = __builtin_fmaf(-q0, m_new, u);
         xs[k] = __builtin_fmaf(r, y, q0);
@@ -580,127 +543,120 @@ __device__ __forceinline__ void apply_chunk(const ApplyArgs& a, const SharedTabl
         const bool nz = m_new > 0.0f;
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
-            const float u = momentum_value(st.cbr[raw_idx(ir, k)], m_old, raw_elem<DT>(gr, k), a.mc);
+            const float u = momentum_value(st.cbr[raw_idx(ir, k)], m_old, raw_elem<DT>(gr, k), w.mc);
             const float x = nz ? div_by_block(u, m_new, y) : 0.0f;
-            if constexpr (SR) ix[k] = quant_stochastic(x, ssr.cb, ssr.lut, kk, seed, e0 + k);
-            else ix[k] = quant_nearest(x, st.bkt, st.thr, kmax);
+            if constexpr (SR) ix[k] = quant_stochastic(x, ssr.cb, ssr.lut, cx.kk, cx.seed, e0 + k);
+            else ix[k] = quant_nearest(x, st.bkt, st.thr, cx.kmax);
         }
     } else {
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
-            if constexpr (SR) ix[k] = quant_stochastic(xs[k], ssr.cb, ssr.lut, kk, seed, e0 + k);
-            else ix[k] = quant_fast(xs[k], st, dense);
+            if constexpr (SR) ix[k] = quant_stochastic(xs[k], ssr.cb, ssr.lut, cx.kk, cx.seed, e0 + k);
+            else ix[k] = quant_fast(xs[k], st, cx.dense);
         }
     }
-    if (a.write_p) {
+    if (w.write_p) {
         float rs = 0.0f, bstep = 0.0f;
-        if constexpr (MODE == 0) rs = a.v_row[ps.row] * row_scale;
-        else bstep = a.step[ps.blk] * sc.lr;
+        if constexpr (MODE == 0) rs = w.v0[ps.row] * cx.row_scale;
+        else bstep = w.step[ps.blk] * cx.sc.lr;
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
             const float q = st.cbr[ix[k]] * m_new;
             float s;
             if constexpr (MODE == 0) {
-                const float h = __builtin_amdgcn_sqrtf(rs * vcv[k]) + a.eps;
-                s = __builtin_amdgcn_rcpf(h) * c1;
+                const float h = __builtin_amdgcn_sqrtf(rs * vcv[k]) + w.eps;
+                s = __builtin_amdgcn_rcpf(h) * cx.c1;
             } else {
                 s = bstep;
             }
             float pw = raw_elem<DT>(pr, k);
-            if (wd) pw = round_dt<DT>(pw * sc.wdf);
+            if (cx.wd) pw = round_dt<DT>(pw * cx.sc.wdf);
             pv[k] = pw - q * s;
         }
     }
 }
 
 template <int DT, int MODE, bool SR, bool FAST>
-__global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
+__device__ __forceinline__ void apply_phase(const TensorWork& w, int64_t wg, int64_t nwg,
+                                            const SharedTables& st, const SharedSR& ssr) {
     using T = typename Elem<DT>::T;
-    __shared__ SharedTables st;
-    __shared__ SharedSR ssr;
-    stage_tables(st, a.qt);
-    if constexpr (SR) stage_sr(ssr, a.qt);
-    __syncthreads();
-    const uint32_t kmax = (uint32_t)(a.qt->k - 1);
-    const int kk = a.qt->k;
-    const StepScalars sc = read_scalars(a.sc, a.step_scalars);
-    uint64_t seed = a.seed;
+    ApplyCtx cx;
+    cx.sc = read_scalars(w);
+    cx.kmax = (uint32_t)(w.qt->k - 1);
+    cx.kk = w.qt->k;
+    cx.dense = w.qt->max_cnt > 2;
+    cx.seed = w.seed;
     if constexpr (SR) {
-        if (a.seed_dev != nullptr) seed = (uint64_t)a.seed_dev[0];
+        if (w.seed_dev != nullptr) cx.seed = (uint64_t)w.seed_dev[0];
     }
-    float row_scale = 0.0f;  // mean(v_row)^-1 * (1/bc2)
-    if constexpr (MODE == 0) row_scale = (1.0f / mean_from_partials(a.vsum, a.nr, a.R)) * sc.inv_bc2;
-    const float c1 = sc.inv_bc1 * sc.lr;
-    const bool wd = sc.wdf != 1.0f;
+    cx.row_scale = 0.0f;
+    if constexpr (MODE == 0) cx.row_scale = (1.0f / mean_from_partials(w.vsum, w.nr, w.R)) * cx.sc.inv_bc2;
+    cx.c1 = cx.sc.inv_bc1 * cx.sc.lr;
+    cx.wd = cx.sc.wdf != 1.0f;
 
-    T* p = static_cast<T*>(a.p);
-    const T* g = static_cast<const T*>(a.grad);
-    const int64_t nchunks = (a.N + kChunk - 1) / kChunk;
-    int64_t ch = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    T* p = static_cast<T*>(w.p);
+    const T* g = static_cast<const T*>(w.grad);
+    const int64_t nchunks = (w.N + kChunk - 1) / kChunk;
+    int64_t ch = wg * kThreads + threadIdx.x;
+    const int64_t stride = nwg * kThreads;
     if (ch >= nchunks) return;
 
     if constexpr (FAST) {
         // Two chunks per iteration (ch and ch + stride): both chunks' loads are
-        // issued before either is computed, so every lane keeps ~80 bytes of
-        // HBM reads in flight.  (row, col, blk, pin) of a chunk advance to the
-        // chunk one stride later by constant increments (no division).
+        // issued before either is computed.
         Pos pa;
         {
             const int64_t e0 = ch * kChunk;
             pa.row = 0;
             pa.col = e0;
             if constexpr (MODE == 0) {
-                pa.row = div_floor(e0, a.C, a.invC);
-                pa.col = e0 - pa.row * a.C;
+                pa.row = div_floor(e0, w.C, w.invC);
+                pa.col = e0 - pa.row * w.C;
             }
-            pa.blk = div_floor(e0, a.P, a.invP);
-            pa.pin = e0 - pa.blk * a.P;
+            pa.blk = div_floor(e0, w.P, w.invP);
+            pa.pin = e0 - pa.blk * w.P;
         }
-        const bool dense = a.qt->max_cnt > 2;
         for (; ch < nchunks; ch += 2 * stride) {
             const bool has_b = ch + stride < nchunks;
-            const Pos pb = advance<MODE>(a, pa);
+            const Pos pb = advance<MODE>(w, pa);
             const int64_t ea = ch * kChunk, eb = (ch + stride) * kChunk;
             Raw8<DT> rga, rpa, rgb, rpb;
             RawIdx8 ria, rib;
             float va[kChunk], vb[kChunk];
             load_raw8<DT>(g + ea, rga);
-            ria = load_raw_idx8(a.idx + ea);
-            if (a.write_p) {
+            ria = load_raw_idx8(w.idx + ea);
+            if (w.write_p) {
                 load_raw8<DT>(p + ea, rpa);
-                if constexpr (MODE == 0) load_vcol(a.v_col + pa.col, va);
+                if constexpr (MODE == 0) load_vcol(w.v1 + pa.col, va);
             }
             if (has_b) {
                 load_raw8<DT>(g + eb, rgb);
-                rib = load_raw_idx8(a.idx + eb);
-                if (a.write_p) {
+                rib = load_raw_idx8(w.idx + eb);
+                if (w.write_p) {
                     load_raw8<DT>(p + eb, rpb);
-                    if constexpr (MODE == 0) load_vcol(a.v_col + pb.col, vb);
+                    if constexpr (MODE == 0) load_vcol(w.v1 + pb.col, vb);
                 }
             }
             uint32_t ix[kChunk];
             float pv[kChunk];
-            apply_chunk<DT, MODE, SR>(a, st, ssr, ea, pa, rga, rpa, ria, va, ix, pv, row_scale, c1, wd, sc,
-                                      dense, kmax, kk, seed);
-            store_idx8(a.idx + ea, ix);
-            if (a.write_p) store8<DT>(p + ea, pv);
+            apply_chunk<DT, MODE, SR>(w, st, ssr, cx, ea, pa, rga, rpa, ria, va, ix, pv);
+            store_idx8(w.idx + ea, ix);
+            if (w.write_p) store8<DT>(p + ea, pv);
             if (has_b) {
-                apply_chunk<DT, MODE, SR>(a, st, ssr, eb, pb, rgb, rpb, rib, vb, ix, pv, row_scale, c1, wd,
-                                          sc, dense, kmax, kk, seed);
-                store_idx8(a.idx + eb, ix);
-                if (a.write_p) store8<DT>(p + eb, pv);
+                apply_chunk<DT, MODE, SR>(w, st, ssr, cx, eb, pb, rgb, rpb, rib, vb, ix, pv);
+                store_idx8(w.idx + eb, ix);
+                if (w.write_p) store8<DT>(p + eb, pv);
             }
-            pa = advance<MODE>(a, pb);
+            pa = advance<MODE>(w, pb);
         }
     } else {
         for (; ch < nchunks; ch += stride) {
             const int64_t e0 = ch * kChunk;
-            const int nvalid = (int)std::min<int64_t>(kChunk, a.N - e0);
-            int64_t row = div_floor(e0, a.C, a.invC);
-            int64_t col = e0 - row * a.C;
-            int64_t blk = div_floor(e0, a.P, a.invP);
-            int64_t pin = e0 - blk * a.P;
+            const int nvalid = (int)std::min<int64_t>(kChunk, w.N - e0);
+            int64_t row = div_floor(e0, w.C, w.invC);
+            int64_t col = e0 - row * w.C;
+            int64_t blk = div_floor(e0, w.P, w.invP);
+            int64_t pin = e0 - blk * w.P;
             float gv[kChunk], pv[kChunk];
             uint32_t ix[kChunk];
             {
@@ -708,10 +664,10 @@ __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
 #pragma unroll
                 for (int k = 0; k < kChunk; ++k) {
                     if (k < nvalid) {
-                        gv[k] = to_f32<DT>(g[r * a.gs0 + c * a.gs1]);
-                        pv[k] = a.write_p ? to_f32<DT>(p[r * a.ps0 + c * a.ps1]) : 0.0f;
-                        ix[k] = a.idx[e0 + k];
-                        if (++c == a.C) { c = 0; ++r; }
+                        gv[k] = to_f32<DT>(g[r * w.gs0 + c * w.gs1]);
+                        pv[k] = w.write_p ? to_f32<DT>(p[r * w.ps0 + c * w.ps1]) : 0.0f;
+                        ix[k] = w.idx[e0 + k];
+                        if (++c == w.C) { c = 0; ++r; }
                     } else {
                         gv[k] = 0.0f;
                         pv[k] = 0.0f;
@@ -719,51 +675,51 @@ __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
                     }
                 }
             }
-            float m_old = a.mag_old[blk];
-            float m_new = a.mag_new[blk];
-            float y = a.minv[blk];
+            float m_old = w.mag_old[blk];
+            float m_new = w.mag[blk];
+            float y = w.minv[blk];
             float bstep = 0.0f;
-            if constexpr (MODE == 1) bstep = a.step[blk] * sc.lr;
+            if constexpr (MODE == 1) bstep = w.step[blk] * cx.sc.lr;
             float rs = 0.0f;
-            if constexpr (MODE == 0) rs = a.v_row[row] * row_scale;
+            if constexpr (MODE == 0) rs = w.v0[row] * cx.row_scale;
             int64_t r = row, c = col;
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 if (k < nvalid) {
-                    const float u = momentum_value(st.cbr[ix[k]], m_old, gv[k], a.mc);
+                    const float u = momentum_value(st.cbr[ix[k]], m_old, gv[k], w.mc);
                     const float x = (m_new > 0.0f) ? div_by_block(u, m_new, y) : 0.0f;
                     uint32_t ni;
-                    if constexpr (SR) ni = quant_stochastic(x, ssr.cb, ssr.lut, kk, seed, e0 + k);
-                    else ni = quant_nearest(x, st.bkt, st.thr, kmax);
+                    if constexpr (SR) ni = quant_stochastic(x, ssr.cb, ssr.lut, cx.kk, cx.seed, e0 + k);
+                    else ni = quant_nearest(x, st.bkt, st.thr, cx.kmax);
                     ix[k] = ni;
-                    if (a.write_p) {
+                    if (w.write_p) {
                         const float q = st.cbr[ni] * m_new;
                         float s;
                         if constexpr (MODE == 0) {
-                            const float h = __builtin_amdgcn_sqrtf(rs * a.v_col[c]) + a.eps;
-                            s = __builtin_amdgcn_rcpf(h) * c1;
+                            const float h = __builtin_amdgcn_sqrtf(rs * w.v1[c]) + w.eps;
+                            s = __builtin_amdgcn_rcpf(h) * cx.c1;
                         } else {
                             s = bstep;
                         }
                         float pw = pv[k];
-                        if (wd) pw = round_dt<DT>(pw * sc.wdf);
+                        if (cx.wd) pw = round_dt<DT>(pw * cx.sc.wdf);
                         pv[k] = pw - q * s;
                     }
-                    if (++c == a.C) {
+                    if (++c == w.C) {
                         c = 0;
                         ++r;
                         if constexpr (MODE == 0) {
-                            if (k + 1 < nvalid) rs = a.v_row[r] * row_scale;
+                            if (k + 1 < nvalid) rs = w.v0[r] * cx.row_scale;
                         }
                     }
-                    if (++pin == a.P) {
+                    if (++pin == w.P) {
                         pin = 0;
                         ++blk;
                         if (k + 1 < nvalid) {
-                            m_old = a.mag_old[blk];
-                            m_new = a.mag_new[blk];
-                            y = a.minv[blk];
-                            if constexpr (MODE == 1) bstep = a.step[blk] * sc.lr;
+                            m_old = w.mag_old[blk];
+                            m_new = w.mag[blk];
+                            y = w.minv[blk];
+                            if constexpr (MODE == 1) bstep = w.step[blk] * cx.sc.lr;
                         }
                     }
                 }
@@ -772,9 +728,9 @@ __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 if (k < nvalid) {
-                    a.idx[e0 + k] = (uint8_t)ix[k];
-                    if (a.write_p) p[rr * a.ps0 + cc * a.ps1] = from_f32<DT>(pv[k]);
-                    if (++cc == a.C) { cc = 0; ++rr; }
+                    w.idx[e0 + k] = (uint8_t)ix[k];
+                    if (w.write_p) p[rr * w.ps0 + cc * w.ps1] = from_f32<DT>(pv[k]);
+                    if (++cc == w.C) { cc = 0; ++rr; }
                 }
             }
         }
@@ -782,12 +738,93 @@ __global__ void __launch_bounds__(kThreads) k_apply(ApplyArgs a) {
 }
 
 // ====================================================================
-// Host launchers
+// Kernels.  Single parameter: descriptor by value.  Multi-tensor: a
+// segment table maps launch workgroups to (descriptor, local workgroup).
+// ====================================================================
+struct Seg {
+    int32_t t;         // descriptor index
+    int32_t pad_;
+    int64_t wg_begin;  // first launch workgroup of this descriptor
+};
+
+__device__ __forceinline__ int64_t find_seg(const Seg* __restrict__ segs, int nseg, int64_t wg) {
+    int lo = 0, hi = nseg;  // last seg with wg_begin <= wg
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (segs[mid].wg_begin <= wg) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+template <int DT, bool FAST>
+__global__ void __launch_bounds__(kThreads) k_factored_stats(TensorWork w) {
+    stats_factored<DT, FAST>(w, blockIdx.x);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_block_stats(TensorWork w) {
+    stats_block<DT>(w, blockIdx.x, gridDim.x);
+}
+
+__global__ void __launch_bounds__(kThreads) k_finalize(TensorWork w) {
+    if (w.mode == 0) finalize_factored(w, blockIdx.x);
+    else finalize_block(w, blockIdx.x);
+}
+
+template <int DT, int MODE, bool SR, bool FAST>
+__global__ void __launch_bounds__(kThreads) k_apply(TensorWork w) {
+    __shared__ SharedTables st;
+    __shared__ SharedSR ssr;
+    stage_tables(st, w.qt);
+    if constexpr (SR) stage_sr(ssr, w.qt);
+    __syncthreads();
+    apply_phase<DT, MODE, SR, FAST>(w, blockIdx.x, gridDim.x, st, ssr);
+}
+
+template <int DT, bool FAST>
+__global__ void __launch_bounds__(kThreads) k_mt_factored_stats(const TensorWork* __restrict__ ws,
+                                                                const Seg* __restrict__ segs, int nseg) {
+    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+    stats_factored<DT, FAST>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_mt_block_stats(const TensorWork* __restrict__ ws,
+                                                             const Seg* __restrict__ segs, int nseg) {
+    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+    const TensorWork& w = ws[sg.t];
+    stats_block<DT>(w, (int64_t)blockIdx.x - sg.wg_begin, w.stats_wgs);
+}
+
+__global__ void __launch_bounds__(kThreads) k_mt_finalize(const TensorWork* __restrict__ ws,
+                                                          const Seg* __restrict__ segs, int nseg) {
+    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+    const TensorWork& w = ws[sg.t];
+    const int64_t local = (int64_t)blockIdx.x - sg.wg_begin;
+    if (w.mode == 0) finalize_factored(w, local);
+    else finalize_block(w, local);
+}
+
+template <int DT, int MODE, bool SR, bool FAST>
+__global__ void __launch_bounds__(kThreads) k_mt_apply(const TensorWork* __restrict__ ws,
+                                                       const Seg* __restrict__ segs, int nseg) {
+    __shared__ SharedTables st;
+    __shared__ SharedSR ssr;
+    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+    const TensorWork& w = ws[sg.t];
+    stage_tables(st, w.qt);
+    if constexpr (SR) stage_sr(ssr, w.qt);
+    __syncthreads();
+    apply_phase<DT, MODE, SR, FAST>(w, (int64_t)blockIdx.x - sg.wg_begin, w.apply_wgs, st, ssr);
+}
+
+// ====================================================================
+// Host side
 // ====================================================================
 
-static MomentumCoef make_coef(double beta1) {
+static MomentumCoef make_coef_w(float w1) {
     MomentumCoef mc;
-    mc.w = (float)(1.0 - beta1);
+    mc.w = w1;
     mc.wm1 = mc.w - 1.0f;
     mc.small = std::fabs(mc.w) < 0.5f ? 1 : 0;
     return mc;
@@ -803,203 +840,354 @@ static int launch_check(const char* what) {
     return GEFENX_OK;
 }
 
-static int grid_for(int64_t work_items, int per_block, int cap) {
-    int64_t g = (work_items + per_block - 1) / per_block;
-    if (g < 1) g = 1;
-    if (g > cap) g = cap;
-    return (int)g;
+static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+static size_t elem_size(int dtype) { return dtype == F32 ? 4 : 2; }
+
+// Fill the derived fields of a descriptor.  Everything that depends only on
+// shapes, strides, pointers and the workspace layout is computed here.
+struct WorkInput {
+    void* p;
+    const void* grad;
+    int dtype;
+    int mode;  // 0 factored, 1 block
+    int64_t R, C, ps0, ps1, gs0, gs1, period;
+    uint8_t* idx;
+    float* mag;
+    float* v0;
+    float* v1;
+    const void* qt;
+    float lerp_w, beta2, alpha2, eps;
+    StepScalars sc;
+    int sr;
+    uint64_t seed;
+    const float* step_scalars;
+    const int64_t* seed_dev;
+    void* workspace;
+    size_t ws_bytes;
+};
+
+static int build_work(const WorkInput& in, TensorWork& w) {
+    std::memset(&w, 0, sizeof(w));
+    const int64_t N = in.R * in.C;
+    const int64_t nb = N / in.period;
+    w.p = in.p; w.grad = in.grad; w.idx = in.idx; w.mag = in.mag; w.v0 = in.v0; w.v1 = in.v1;
+    w.qt = static_cast<const QTable*>(in.qt);
+    w.step_scalars = in.step_scalars; w.seed_dev = in.seed_dev;
+    w.R = in.R; w.C = in.C; w.N = N; w.P = in.period; w.nb = nb;
+    w.invC = 1.0 / (double)in.C; w.invP = 1.0 / (double)in.period;
+    w.ps0 = in.ps0; w.ps1 = in.ps1; w.gs0 = in.gs0; w.gs1 = in.gs1;
+    w.shards = mag_shards(nb);
+    w.seed = in.seed;
+    w.dtype = in.dtype; w.mode = in.mode; w.sr = in.sr;
+    w.bf16_mean = in.dtype == BF16 ? 1 : 0;
+    w.eps = in.eps; w.beta2 = in.beta2; w.alpha2 = in.alpha2;
+    w.sc = in.sc;
+    w.mc = make_coef_w(in.lerp_w);
+    w.write_p = (in.step_scalars != nullptr) || !(in.sc.lr == 0.0f && in.sc.wdf == 1.0f);
+    char* ws = static_cast<char*>(in.workspace);
+    const int64_t nchunks = ceil_div(N, kChunk);
+    if (in.mode == 0) {
+        const FactoredWs L = FactoredWs::make(in.R, in.C, nb);
+        if (in.ws_bytes < L.total)
+            return set_error(GEFENX_EINVAL, "factored update: workspace %zu bytes < required %zu", in.ws_bytes, L.total);
+        const FactTiles t = FactTiles::make(in.R, in.C);
+        w.row_part = reinterpret_cast<double*>(ws + L.off_rowp);
+        w.col_part = reinterpret_cast<double*>(ws + L.off_colp);
+        w.magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
+        w.mag_old = reinterpret_cast<float*>(ws + L.off_magold);
+        w.minv = reinterpret_cast<float*>(ws + L.off_minv);
+        w.vsum = reinterpret_cast<double*>(ws + L.off_vsum);
+        w.ct = t.ct; w.rt = t.rt; w.tile_rows = t.tile_rows;
+        w.stats_wgs = t.ct * t.rt;
+        w.nr = ceil_div(in.R, kFinRowsPerWg);
+        w.nc = ceil_div(in.C, 64);
+        w.nbw = std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(nb, kFinBlocksPerWg)));
+        w.fin_wgs = w.nr + w.nc + w.nbw;
+        const bool contig_g = (in.gs1 == 1 && in.gs0 == in.C);
+        const bool contig_p = (in.ps1 == 1 && in.ps0 == in.C);
+        w.fast_stats = contig_g && (in.C % kChunk == 0) && aligned(in.grad, 16) && aligned(in.idx, 8);
+        w.fast_apply = contig_g && contig_p && (in.C % kChunk == 0) && (in.period % kChunk == 0) &&
+                       aligned(in.grad, 16) && aligned(in.p, 16) && aligned(in.idx, 8) && aligned(in.v1, 16);
+    } else {
+        const BlockWs L = BlockWs::make(nb);
+        if (in.ws_bytes < L.total)
+            return set_error(GEFENX_EINVAL, "block update: workspace %zu bytes < required %zu", in.ws_bytes, L.total);
+        w.blk_sq = reinterpret_cast<double*>(ws + L.off_sq);
+        w.magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
+        w.mag_old = reinterpret_cast<float*>(ws + L.off_magold);
+        w.step = reinterpret_cast<float*>(ws + L.off_step);
+        w.minv = reinterpret_cast<float*>(ws + L.off_minv);
+        w.stats_wgs = std::max<int64_t>(1, ceil_div(nchunks, kThreads * kBlockStatsChunksPerThread));
+        w.nbw = std::max<int64_t>(1, std::min<int64_t>(4096, ceil_div(nb, kThreads)));
+        w.fin_wgs = w.nbw;
+        w.fast_stats = aligned(in.grad, 16) && aligned(in.idx, 8);
+        w.fast_apply = (in.period % kChunk == 0) && aligned(in.grad, 16) && aligned(in.p, 16) &&
+                       aligned(in.idx, 8);
+    }
+    w.apply_wgs = std::max<int64_t>(1, ceil_div(nchunks, kThreads * kApplyChunksPerThread));
+    const int64_t S = w.apply_wgs * kThreads * kChunk;
+    w.dR = S / w.C;
+    w.dC = S - w.dR * w.C;
+    w.dB = S / w.P;
+    w.dP = S - w.dB * w.P;
+    return GEFENX_OK;
 }
 
-constexpr int kApplyGridCap = 4096;
+// Algorithmic bytes of one parameter's step: p r/w, g r, idx r/w per element
+// plus the fp32 state vectors read and written.
+static double algo_bytes(const TensorWork& w) {
+    const double es = (double)elem_size(w.dtype);
+    const double vec = w.mode == 0 ? 8.0 * (double)(w.R + w.C + w.nb) : 16.0 * (double)w.nb;
+    return (double)w.N * (3.0 * es + 2.0) + vec;
+}
 
 template <int MODE, bool SR, bool FAST>
-static void launch_apply_dt(int dtype, const ApplyArgs& a, int grid, hipStream_t s) {
+static void launch_apply_one(int dtype, const TensorWork& w, hipStream_t s) {
+    const dim3 grid((unsigned)w.apply_wgs), block(kThreads);
     switch (dtype) {
-        case F32: hipLaunchKernelGGL((k_apply<F32, MODE, SR, FAST>), dim3(grid), dim3(kThreads), 0, s, a); break;
-        case F16: hipLaunchKernelGGL((k_apply<F16, MODE, SR, FAST>), dim3(grid), dim3(kThreads), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_apply<BF16, MODE, SR, FAST>), dim3(grid), dim3(kThreads), 0, s, a); break;
+        case F32: hipLaunchKernelGGL((k_apply<F32, MODE, SR, FAST>), grid, block, 0, s, w); break;
+        case F16: hipLaunchKernelGGL((k_apply<F16, MODE, SR, FAST>), grid, block, 0, s, w); break;
+        default: hipLaunchKernelGGL((k_apply<BF16, MODE, SR, FAST>), grid, block, 0, s, w); break;
     }
 }
 
 template <int MODE>
-static void launch_apply(int dtype, bool sr, bool fast, ApplyArgs a, hipStream_t s) {
-    const int64_t nchunks = (a.N + kChunk - 1) / kChunk;
-    const int grid = grid_for(nchunks, kThreads, kApplyGridCap);
-    const int64_t S = (int64_t)grid * kThreads * kChunk;
-    a.dR = S / a.C;
-    a.dC = S - a.dR * a.C;
-    a.dB = S / a.P;
-    a.dP = S - a.dB * a.P;
-    if (fast) {
-        if (sr) launch_apply_dt<MODE, true, true>(dtype, a, grid, s);
-        else launch_apply_dt<MODE, false, true>(dtype, a, grid, s);
+static void launch_apply_single(const TensorWork& w, hipStream_t s) {
+    if (w.fast_apply) {
+        if (w.sr) launch_apply_one<MODE, true, true>(w.dtype, w, s);
+        else launch_apply_one<MODE, false, true>(w.dtype, w, s);
     } else {
-        if (sr) launch_apply_dt<MODE, true, false>(dtype, a, grid, s);
-        else launch_apply_dt<MODE, false, false>(dtype, a, grid, s);
+        if (w.sr) launch_apply_one<MODE, true, false>(w.dtype, w, s);
+        else launch_apply_one<MODE, false, false>(w.dtype, w, s);
     }
 }
 
-static size_t elem_size(int dtype) { return dtype == F32 ? 4 : 2; }
-
-int factored_update(void* p, const void* grad, int dtype, int64_t R, int64_t C,
-                    int64_t ps0, int64_t ps1, int64_t gs0, int64_t gs1,
-                    uint8_t* m_codebook, float* m_magnitude, float* v_row, float* v_col,
-                    int64_t period, const void* qtable, double beta1, double beta2,
-                    double lr, double eps, double inv_bc2, double inv_bc1, double wdf,
-                    int stochastic_round, int64_t rng_seed, const float* step_scalars,
-                    const int64_t* seed_dev, void* workspace, size_t ws_bytes, hipStream_t s) {
-    const int64_t N = R * C;
-    const int64_t nb = N / period;
-    const FactoredWs L = FactoredWs::make(R, C, nb);
-    const FactTiles tiles = FactTiles::make(R, C);
-    if (ws_bytes < L.total)
-        return set_error(GEFENX_EINVAL, "factored update: workspace %zu bytes < required %zu", ws_bytes, L.total);
-    char* ws = static_cast<char*>(workspace);
-    double* row_part = reinterpret_cast<double*>(ws + L.off_rowp);
-    double* col_part = reinterpret_cast<double*>(ws + L.off_colp);
-    uint32_t* magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
-    float* mag_old = reinterpret_cast<float*>(ws + L.off_magold);
-    float* minv = reinterpret_cast<float*>(ws + L.off_minv);
-    double* vsum = reinterpret_cast<double*>(ws + L.off_vsum);
-    const int64_t shards = mag_shards(nb);
-    const QTable* qt = static_cast<const QTable*>(qtable);
-    const MomentumCoef mc = make_coef(beta1);
-    const bool contig_g = (gs1 == 1 && gs0 == C);
-    const bool contig_p = (ps1 == 1 && ps0 == C);
-    const double es = (double)elem_size(dtype);
-
-    FactStatsArgs sa;
-    sa.grad = grad; sa.idx = m_codebook; sa.mag_old = m_magnitude; sa.qt = qt;
-    sa.R = R; sa.C = C; sa.gs0 = gs0; sa.gs1 = gs1; sa.P = period; sa.invP = 1.0 / (double)period;
-    sa.tile_rows = tiles.tile_rows; sa.ct = tiles.ct;
-    sa.fast = contig_g && (C % kChunk == 0) && aligned(grad, 16) && aligned(m_codebook, 8);
-    sa.row_part = row_part; sa.col_part = col_part; sa.magbits = magbits; sa.mc = mc;
-    sa.nb = nb; sa.shards = shards;
-    const int64_t nwg = tiles.ct * tiles.rt;
-    if (nwg > 2147483647LL)
-        return set_error(GEFENX_EINVAL, "factored update: shape [%lld, %lld] exceeds the launch grid",
-                         (long long)R, (long long)C);
-    int ph = prof_begin(GEFENX_K_STATS, (double)N * (es + 1.0), 0.0, s);
-#define GX_STATS(DTV)                                                                                   \
-    if (sa.fast) hipLaunchKernelGGL((k_factored_stats<DTV, true>), dim3((unsigned)nwg), dim3(kThreads), 0, s, sa); \
-    else hipLaunchKernelGGL((k_factored_stats<DTV, false>), dim3((unsigned)nwg), dim3(kThreads), 0, s, sa)
-    switch (dtype) {
-        case F32: GX_STATS(F32); break;
-        case F16: GX_STATS(F16); break;
-        default: GX_STATS(BF16); break;
+// Run the three phases of one parameter (single-parameter entry points).
+static int run_single(const TensorWork& w, hipStream_t s) {
+    const double es = (double)elem_size(w.dtype);
+    int ph = prof_begin(GEFENX_K_STATS, (double)w.N * (es + 1.0), 0.0, s);
+    const dim3 block(kThreads);
+    if (w.mode == 0) {
+        const dim3 grid((unsigned)w.stats_wgs);
+#define GX_FSTATS(DTV)                                                                          \
+    if (w.fast_stats) hipLaunchKernelGGL((k_factored_stats<DTV, true>), grid, block, 0, s, w);  \
+    else hipLaunchKernelGGL((k_factored_stats<DTV, false>), grid, block, 0, s, w)
+        switch (w.dtype) {
+            case F32: GX_FSTATS(F32); break;
+            case F16: GX_FSTATS(F16); break;
+            default: GX_FSTATS(BF16); break;
+        }
+#undef GX_FSTATS
+    } else {
+        const dim3 grid((unsigned)w.stats_wgs);
+        switch (w.dtype) {
+            case F32: hipLaunchKernelGGL(k_block_stats<F32>, grid, block, 0, s, w); break;
+            case F16: hipLaunchKernelGGL(k_block_stats<F16>, grid, block, 0, s, w); break;
+            default: hipLaunchKernelGGL(k_block_stats<BF16>, grid, block, 0, s, w); break;
+        }
     }
-#undef GX_STATS
     prof_end(ph, s);
-    int rc = launch_check("k_factored_stats");
+    int rc = launch_check("stats");
     if (rc) return rc;
-
-    FactFinArgs fa;
-    fa.row_part = row_part; fa.col_part = col_part; fa.v_row = v_row; fa.v_col = v_col;
-    fa.R = R; fa.C = C; fa.nb = nb; fa.ct = tiles.ct; fa.rt = tiles.rt;
-    fa.beta2 = (float)beta2; fa.alpha2 = (float)(1.0 - beta2);
-    fa.magbits = magbits; fa.mag = m_magnitude; fa.mag_old = mag_old; fa.minv = minv; fa.vsum = vsum;
-    fa.shards = shards;
-    fa.nr = (R + kFinRowsPerWg - 1) / kFinRowsPerWg;
-    fa.nc = (C + 63) / 64;
-    const int64_t fgrid = fa.nr + fa.nc + grid_for(nb, kThreads * 4, 1024);
-    ph = prof_begin(GEFENX_K_FINALIZE, 8.0 * (double)(R + C + nb), 0.0, s);
-    hipLaunchKernelGGL(k_factored_finalize, dim3((unsigned)fgrid), dim3(kThreads), 0, s, fa);
+    ph = prof_begin(GEFENX_K_FINALIZE, 16.0 * (double)(w.R + w.C + w.nb), 0.0, s);
+    hipLaunchKernelGGL(k_finalize, dim3((unsigned)w.fin_wgs), block, 0, s, w);
     prof_end(ph, s);
-    rc = launch_check("k_factored_finalize");
+    rc = launch_check("finalize");
     if (rc) return rc;
-
-    ApplyArgs aa{};
-    aa.p = p; aa.grad = grad; aa.idx = m_codebook; aa.mag_old = mag_old; aa.mag_new = m_magnitude;
-    aa.minv = minv; aa.v_row = v_row; aa.v_col = v_col; aa.vsum = vsum; aa.nr = fa.nr; aa.R = R;
-    aa.step = nullptr; aa.qt = qt;
-    aa.N = N; aa.C = C; aa.P = period; aa.invC = 1.0 / (double)C; aa.invP = 1.0 / (double)period;
-    aa.ps0 = ps0; aa.ps1 = ps1; aa.gs0 = gs0; aa.gs1 = gs1;
-    const bool fast = contig_g && contig_p && (C % kChunk == 0) && (period % kChunk == 0) &&
-                      aligned(grad, 16) && aligned(p, 16) && aligned(m_codebook, 8) && aligned(v_col, 16);
-    aa.write_p = (step_scalars != nullptr) || !(lr == 0.0 && (float)wdf == 1.0f);
-    aa.eps = (float)eps;
-    aa.sc = StepScalars{(float)lr, (float)inv_bc2, (float)inv_bc1, (float)wdf};
-    aa.step_scalars = step_scalars;
-    aa.mc = mc;
-    aa.seed = (uint64_t)rng_seed;
-    aa.seed_dev = seed_dev;
-    // algorithmic bytes of the whole step: p r/w, g r, idx r/w per element
-    // plus the fp32 state vectors read and written
-    ph = prof_begin(GEFENX_K_APPLY, (double)N * (3.0 * es + 2.0) + 8.0 * (double)(R + C + nb), 0.0, s);
-    launch_apply<0>(dtype, stochastic_round != 0, fast, aa, s);
+    ph = prof_begin(GEFENX_K_APPLY, algo_bytes(w), 0.0, s);
+    if (w.mode == 0) launch_apply_single<0>(w, s);
+    else launch_apply_single<1>(w, s);
     prof_end(ph, s);
-    return launch_check("k_apply(factored)");
+    return launch_check("apply");
 }
 
-int block_update(void* p, const void* grad, int dtype, int64_t N, int64_t period,
-                 uint8_t* m_codebook, float* m_magnitude, float* vmean, const void* qtable,
-                 double beta1, double beta2, double lr, double eps, double inv_sqrt_bc2,
-                 double inv_bc1, double wdf, int stochastic_round, int64_t rng_seed,
-                 const float* step_scalars, const int64_t* seed_dev, void* workspace,
-                 size_t ws_bytes, hipStream_t s) {
-    const int64_t nb = N / period;
-    const BlockWs L = BlockWs::make(nb);
-    if (ws_bytes < L.total)
-        return set_error(GEFENX_EINVAL, "block update: workspace %zu bytes < required %zu", ws_bytes, L.total);
-    char* ws = static_cast<char*>(workspace);
-    double* blk_sq = reinterpret_cast<double*>(ws + L.off_sq);
-    uint32_t* magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
-    float* mag_old = reinterpret_cast<float*>(ws + L.off_magold);
-    float* step = reinterpret_cast<float*>(ws + L.off_step);
-    float* minv = reinterpret_cast<float*>(ws + L.off_minv);
-    const QTable* qt = static_cast<const QTable*>(qtable);
-    const MomentumCoef mc = make_coef(beta1);
-    const double es = (double)elem_size(dtype);
+// ------------------------------------------------------------ multi-tensor
 
-    BlockStatsArgs sa;
-    sa.grad = grad; sa.idx = m_codebook; sa.mag_old = m_magnitude; sa.qt = qt;
-    sa.N = N; sa.P = period; sa.invP = 1.0 / (double)period;
-    sa.fast = aligned(grad, 16) && aligned(m_codebook, 8);
-    sa.blk_sq = blk_sq; sa.magbits = magbits; sa.mc = mc;
-    sa.nb = nb; sa.shards = mag_shards(nb);
-    const int64_t nchunks = (N + kChunk - 1) / kChunk;
-    const int sgrid = grid_for(nchunks, kThreads * 4, kApplyGridCap);
-    int ph = prof_begin(GEFENX_K_STATS, (double)N * (es + 1.0), 0.0, s);
-    switch (dtype) {
-        case F32: hipLaunchKernelGGL(k_block_stats<F32>, dim3(sgrid), dim3(kThreads), 0, s, sa); break;
-        case F16: hipLaunchKernelGGL(k_block_stats<F16>, dim3(sgrid), dim3(kThreads), 0, s, sa); break;
-        default: hipLaunchKernelGGL(k_block_stats<BF16>, dim3(sgrid), dim3(kThreads), 0, s, sa); break;
+// Launch-group key: tensors of one cohort that share a kernel variant.
+struct GroupKey {
+    int mode, dtype, fast, sr;
+    bool operator<(const GroupKey& o) const {
+        return std::tie(mode, dtype, fast, sr) < std::tie(o.mode, o.dtype, o.fast, o.sr);
     }
-    prof_end(ph, s);
-    int rc = launch_check("k_block_stats");
-    if (rc) return rc;
+};
 
-    BlockFinArgs fa;
-    fa.blk_sq = blk_sq; fa.vmean = vmean; fa.nb = nb; fa.P = period;
-    fa.beta2 = (float)beta2; fa.alpha2 = (float)(1.0 - beta2); fa.eps = (float)eps;
-    fa.bf16_mean = (dtype == BF16) ? 1 : 0;
-    fa.sc = StepScalars{(float)lr, (float)inv_sqrt_bc2, (float)inv_bc1, (float)wdf};
-    fa.step_scalars = step_scalars;
-    fa.magbits = magbits; fa.mag = m_magnitude; fa.mag_old = mag_old; fa.step = step; fa.minv = minv;
-    fa.shards = mag_shards(nb);
-    ph = prof_begin(GEFENX_K_FINALIZE, 16.0 * (double)nb, 0.0, s);
-    hipLaunchKernelGGL(k_block_finalize, dim3(grid_for(nb, kThreads, 4096)), dim3(kThreads), 0, s, fa);
-    prof_end(ph, s);
-    rc = launch_check("k_block_finalize");
-    if (rc) return rc;
+struct Launch {
+    int phase;       // 0 stats, 1 finalize, 2 apply
+    GroupKey key;
+    size_t seg_off;  // index of the first Seg in the segment array
+    int nseg;
+    int64_t wgs;
+    double bytes;
+};
 
-    ApplyArgs aa{};
-    aa.p = p; aa.grad = grad; aa.idx = m_codebook; aa.mag_old = mag_old; aa.mag_new = m_magnitude;
-    aa.minv = minv; aa.step = step; aa.qt = qt;
-    aa.N = N; aa.C = N; aa.P = period; aa.invC = 1.0 / (double)N; aa.invP = 1.0 / (double)period;
-    aa.ps0 = N; aa.ps1 = 1; aa.gs0 = N; aa.gs1 = 1;
-    const bool fast = (period % kChunk == 0) && aligned(grad, 16) && aligned(p, 16) && aligned(m_codebook, 8);
-    aa.write_p = (step_scalars != nullptr) || !(lr == 0.0 && (float)wdf == 1.0f);
-    aa.eps = (float)eps;
-    aa.sc = fa.sc;
-    aa.step_scalars = step_scalars;
-    aa.mc = mc;
-    aa.seed = (uint64_t)rng_seed;
-    aa.seed_dev = seed_dev;
-    ph = prof_begin(GEFENX_K_APPLY, (double)N * (3.0 * es + 2.0) + 16.0 * (double)nb, 0.0, s);
-    launch_apply<1>(dtype, stochastic_round != 0, fast, aa, s);
-    prof_end(ph, s);
-    return launch_check("k_apply(block)");
+// Pinned, double-buffered staging for the per-step descriptor upload.
+struct Staging {
+    void* host[2] = {nullptr, nullptr};
+    size_t cap[2] = {0, 0};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    int next = 0;
+};
+static std::mutex g_stage_mu;
+static std::map<int, Staging> g_stage;  // per device; never freed (process lifetime)
+
+static int64_t cohort_limit() {
+    static int64_t v = -1;
+    if (v < 0) {
+        const char* e = std::getenv("GEFENX_COHORT_ELEMS");
+        v = e ? std::atoll(e) : (int64_t)1 << 62;  // default: one cohort per step
+        if (v <= 0) v = (int64_t)1 << 62;
+    }
+    return v;
+}
+
+struct MtLayout {
+    std::vector<TensorWork> works;
+    std::vector<Seg> segs;
+    std::vector<Launch> launches;
+};
+
+static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
+    L.works = works;
+    L.segs.clear();
+    L.launches.clear();
+    const int n = (int)works.size();
+    const int64_t limit = cohort_limit();
+    int c0 = 0;
+    while (c0 < n) {
+        int c1 = c0;
+        int64_t acc = 0;
+        while (c1 < n && (c1 == c0 || acc + works[(size_t)c1].N <= limit)) acc += works[(size_t)c1++].N;
+        for (int phase = 0; phase < 3; ++phase) {
+            std::map<GroupKey, std::vector<int>> groups;
+            for (int t = c0; t < c1; ++t) {
+                const TensorWork& w = works[(size_t)t];
+                GroupKey k{w.mode, w.dtype, 0, 0};
+                if (phase == 0) k.fast = w.fast_stats;
+                if (phase == 2) { k.fast = w.fast_apply; k.sr = w.sr; }
+                if (phase == 1) k = GroupKey{0, 0, 0, 0};
+                groups[k].push_back(t);
+            }
+            for (auto& kv : groups) {
+                Launch l;
+                l.phase = phase;
+                l.key = kv.first;
+                l.seg_off = L.segs.size();
+                l.nseg = (int)kv.second.size();
+                l.wgs = 0;
+                l.bytes = 0.0;
+                for (int t : kv.second) {
+                    const TensorWork& w = works[(size_t)t];
+                    L.segs.push_back(Seg{t, 0, l.wgs});
+                    const int64_t wgs = phase == 0 ? w.stats_wgs : phase == 1 ? w.fin_wgs : w.apply_wgs;
+                    l.wgs += wgs;
+                    const double es = (double)elem_size(w.dtype);
+                    l.bytes += phase == 0 ? (double)w.N * (es + 1.0)
+                             : phase == 1 ? 16.0 * (double)(w.R + w.C + w.nb) : algo_bytes(w);
+                }
+                L.launches.push_back(l);
+            }
+        }
+        c0 = c1;
+    }
+}
+
+template <int MODE, bool SR, bool FAST>
+static void launch_mt_apply(int dtype, dim3 grid, hipStream_t s, const TensorWork* ws, const Seg* sg, int nseg) {
+    switch (dtype) {
+        case F32: hipLaunchKernelGGL((k_mt_apply<F32, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg, nseg); break;
+        case F16: hipLaunchKernelGGL((k_mt_apply<F16, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg, nseg); break;
+        default: hipLaunchKernelGGL((k_mt_apply<BF16, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg, nseg); break;
+    }
+}
+
+static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hipStream_t s) {
+    const size_t works_bytes = align256(sizeof(TensorWork) * L.works.size());
+    const size_t segs_bytes = sizeof(Seg) * L.segs.size();
+    const size_t need = works_bytes + align256(segs_bytes);
+    if (scratch_bytes < need)
+        return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: scratch %zu bytes < required %zu", scratch_bytes, need);
+    int dev = 0;
+    hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(g_stage_mu);
+    Staging& st = g_stage[dev];
+    const int b = st.next;
+    st.next ^= 1;
+    if (st.done[b] == nullptr && hipEventCreateWithFlags(&st.done[b], hipEventDisableTiming) != hipSuccess)
+        return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: event creation failed");
+    if (st.host[b] != nullptr) hipEventSynchronize(st.done[b]);  // previous upload from this buffer finished
+    if (st.cap[b] < need) {
+        if (st.host[b]) hipHostFree(st.host[b]);
+        st.host[b] = nullptr;
+        st.cap[b] = 0;
+        if (hipHostMalloc(&st.host[b], need, hipHostMallocDefault) != hipSuccess)
+            return set_error(GEFENX_ENOMEM, "gefenx_multi_tensor_step: pinned staging of %zu bytes failed", need);
+        st.cap[b] = need;
+    }
+    char* h = static_cast<char*>(st.host[b]);
+    std::memcpy(h, L.works.data(), sizeof(TensorWork) * L.works.size());
+    std::memcpy(h + works_bytes, L.segs.data(), segs_bytes);
+    if (hipMemcpyAsync(scratch, h, need, hipMemcpyHostToDevice, s) != hipSuccess)
+        return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: descriptor upload failed");
+    hipEventRecord(st.done[b], s);
+    const TensorWork* dws = reinterpret_cast<const TensorWork*>(scratch);
+    const Seg* dsegs = reinterpret_cast<const Seg*>(static_cast<char*>(scratch) + works_bytes);
+    for (const Launch& l : L.launches) {
+        if (l.wgs <= 0) continue;
+        if (l.wgs > 2147483647LL) return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: launch too large");
+        const dim3 grid((unsigned)l.wgs), block(kThreads);
+        const Seg* sg = dsegs + l.seg_off;
+        const int kinds[3] = {GEFENX_K_STATS, GEFENX_K_FINALIZE, GEFENX_K_APPLY};
+        int ph = prof_begin(kinds[l.phase], l.bytes, 0.0, s);
+        if (l.phase == 0) {
+            if (l.key.mode == 0) {
+#define GX_MTS(DTV)                                                                                          \
+    if (l.key.fast) hipLaunchKernelGGL((k_mt_factored_stats<DTV, true>), grid, block, 0, s, dws, sg, l.nseg); \
+    else hipLaunchKernelGGL((k_mt_factored_stats<DTV, false>), grid, block, 0, s, dws, sg, l.nseg)
+                switch (l.key.dtype) {
+                    case F32: GX_MTS(F32); break;
+                    case F16: GX_MTS(F16); break;
+                    default: GX_MTS(BF16); break;
+                }
+#undef GX_MTS
+            } else {
+                switch (l.key.dtype) {
+                    case F32: hipLaunchKernelGGL(k_mt_block_stats<F32>, grid, block, 0, s, dws, sg, l.nseg); break;
+                    case F16: hipLaunchKernelGGL(k_mt_block_stats<F16>, grid, block, 0, s, dws, sg, l.nseg); break;
+                    default: hipLaunchKernelGGL(k_mt_block_stats<BF16>, grid, block, 0, s, dws, sg, l.nseg); break;
+                }
+            }
+        } else if (l.phase == 1) {
+            hipLaunchKernelGGL(k_mt_finalize, grid, block, 0, s, dws, sg, l.nseg);
+        } else {
+            const int dt = l.key.dtype;
+            if (l.key.mode == 0) {
+                if (l.key.fast) {
+                    if (l.key.sr) launch_mt_apply<0, true, true>(dt, grid, s, dws, sg, l.nseg);
+                    else launch_mt_apply<0, false, true>(dt, grid, s, dws, sg, l.nseg);
+                } else {
+                    if (l.key.sr) launch_mt_apply<0, true, false>(dt, grid, s, dws, sg, l.nseg);
+                    else launch_mt_apply<0, false, false>(dt, grid, s, dws, sg, l.nseg);
+                }
+            } else {
+                if (l.key.fast) {
+                    if (l.key.sr) launch_mt_apply<1, true, true>(dt, grid, s, dws, sg, l.nseg);
+                    else launch_mt_apply<1, false, true>(dt, grid, s, dws, sg, l.nseg);
+                } else {
+                    if (l.key.sr) launch_mt_apply<1, true, false>(dt, grid, s, dws, sg, l.nseg);
+                    else launch_mt_apply<1, false, false>(dt, grid, s, dws, sg, l.nseg);
+                }
+            }
+        }
+        prof_end(ph, s);
+        int rc = launch_check("multi-tensor launch");
+        if (rc) return rc;
+    }
+    return GEFENX_OK;
+}
+
+static size_t multi_scratch_bytes(int n_works, size_t n_segs) {
+    return align256(sizeof(TensorWork) * (size_t)n_works) + align256(sizeof(Seg) * n_segs);
 }
 
 }  // namespace gx
@@ -1036,11 +1224,21 @@ int gefenx_factored_update(
                          (long long)period, (long long)N);
     if (!p || !grad || !m_codebook || !m_magnitude || !v_row || !v_col || !qtable_dev || !workspace)
         return set_error(GEFENX_EINVAL, "gefenx_factored_update: null pointer argument");
-    return factored_update(p, grad, dtype, rows, cols, ps0, ps1, gs0, gs1, m_codebook, m_magnitude,
-                           v_row, v_col, period, qtable_dev, beta1, beta2, lr, eps,
-                           inv_bias_correction_2, inv_bias_correction_1, weight_decay_factor,
-                           stochastic_round, rng_seed, step_scalars, seed_dev, workspace,
-                           workspace_bytes, static_cast<hipStream_t>(stream));
+    WorkInput in{};
+    in.p = p; in.grad = grad; in.dtype = dtype; in.mode = 0;
+    in.R = rows; in.C = cols; in.ps0 = ps0; in.ps1 = ps1; in.gs0 = gs0; in.gs1 = gs1; in.period = period;
+    in.idx = m_codebook; in.mag = m_magnitude; in.v0 = v_row; in.v1 = v_col; in.qt = qtable_dev;
+    in.lerp_w = (float)(1.0 - beta1); in.beta2 = (float)beta2; in.alpha2 = (float)(1.0 - beta2);
+    in.eps = (float)eps;
+    in.sc = StepScalars{(float)lr, (float)inv_bias_correction_2, (float)inv_bias_correction_1,
+                        (float)weight_decay_factor};
+    in.sr = stochastic_round ? 1 : 0; in.seed = (uint64_t)rng_seed;
+    in.step_scalars = step_scalars; in.seed_dev = seed_dev;
+    in.workspace = workspace; in.ws_bytes = workspace_bytes;
+    TensorWork w;
+    rc = build_work(in, w);
+    if (rc) return rc;
+    return run_single(w, static_cast<hipStream_t>(stream));
 }
 
 int gefenx_block_update(
@@ -1060,10 +1258,87 @@ int gefenx_block_update(
                          (long long)period, (long long)numel);
     if (!p || !grad || !m_codebook || !m_magnitude || !vmean || !qtable_dev || !workspace)
         return set_error(GEFENX_EINVAL, "gefenx_block_update: null pointer argument");
-    return block_update(p, grad, dtype, numel, period, m_codebook, m_magnitude, vmean, qtable_dev,
-                        beta1, beta2, lr, eps, inv_sqrt_bias_correction_2, inv_bias_correction_1,
-                        weight_decay_factor, stochastic_round, rng_seed, step_scalars, seed_dev,
-                        workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+    WorkInput in{};
+    in.p = p; in.grad = grad; in.dtype = dtype; in.mode = 1;
+    in.R = 1; in.C = numel; in.ps0 = numel; in.ps1 = 1; in.gs0 = numel; in.gs1 = 1; in.period = period;
+    in.idx = m_codebook; in.mag = m_magnitude; in.v0 = vmean; in.v1 = nullptr; in.qt = qtable_dev;
+    in.lerp_w = (float)(1.0 - beta1); in.beta2 = (float)beta2; in.alpha2 = (float)(1.0 - beta2);
+    in.eps = (float)eps;
+    in.sc = StepScalars{(float)lr, (float)inv_sqrt_bias_correction_2, (float)inv_bias_correction_1,
+                        (float)weight_decay_factor};
+    in.sr = stochastic_round ? 1 : 0; in.seed = (uint64_t)rng_seed;
+    in.step_scalars = step_scalars; in.seed_dev = seed_dev;
+    in.workspace = workspace; in.ws_bytes = workspace_bytes;
+    TensorWork w;
+    rc = build_work(in, w);
+    if (rc) return rc;
+    return run_single(w, static_cast<hipStream_t>(stream));
+}
+
+static int desc_to_work(const gefenx_tensor_desc& d, int i, const void* const* qtables, int sr,
+                        int64_t seed, TensorWork& w) {
+    int rc = check_dtype(d.dtype, "gefenx_multi_tensor_step");
+    if (rc) return rc;
+    const int64_t N = d.rows * d.cols;
+    if (d.rows < 0 || d.cols < 0 || d.period <= 0 || N % d.period != 0)
+        return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: descriptor %d has period %lld not dividing [%lld, %lld]",
+                         i, (long long)d.period, (long long)d.rows, (long long)d.cols);
+    if (!d.p || !d.grad || !d.m_codebook || !d.m_magnitude || !d.v0 || (d.factored && !d.v1) || !d.workspace)
+        return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: descriptor %d has a null pointer", i);
+    const void* qt = qtables[d.dtype];
+    if (!qt) return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: no quantisation table for dtype %d", d.dtype);
+    WorkInput in{};
+    in.p = d.p; in.grad = d.grad; in.dtype = d.dtype; in.mode = d.factored ? 0 : 1;
+    if (d.factored) {
+        in.R = d.rows; in.C = d.cols; in.ps0 = d.ps0; in.ps1 = d.ps1; in.gs0 = d.gs0; in.gs1 = d.gs1;
+    } else {
+        if (d.ps1 != 1 || d.gs1 != 1 || (d.rows > 1 && (d.ps0 != d.cols || d.gs0 != d.cols)))
+            return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: block-path descriptor %d must be contiguous", i);
+        in.R = 1; in.C = N; in.ps0 = N; in.ps1 = 1; in.gs0 = N; in.gs1 = 1;
+    }
+    in.period = d.period;
+    in.idx = d.m_codebook; in.mag = d.m_magnitude; in.v0 = d.v0; in.v1 = d.v1; in.qt = qt;
+    in.lerp_w = d.lerp_w; in.beta2 = d.beta2; in.alpha2 = d.alpha2; in.eps = d.eps;
+    in.sc = StepScalars{d.lr, d.inv_bc2, d.inv_bc1, d.wd_factor};
+    in.sr = sr ? 1 : 0; in.seed = (uint64_t)seed;
+    in.workspace = d.workspace;
+    in.ws_bytes = d.factored ? gefenx_workspace_bytes(GEFENX_WS_FACTORED, d.rows, d.cols, N / d.period)
+                             : gefenx_workspace_bytes(GEFENX_WS_BLOCK, 0, 0, N / d.period);
+    return build_work(in, w);
+}
+
+static int build_layout(const gefenx_tensor_desc* descs, int n, const void* const* qtables, int sr,
+                        int64_t seed, MtLayout& L) {
+    if (n < 0 || (n > 0 && (!descs || !qtables)))
+        return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: bad descriptor array");
+    std::vector<TensorWork> works;
+    works.reserve((size_t)n);
+    for (int i = 0; i < n; ++i) {
+        if (descs[i].rows * descs[i].cols == 0) continue;  // empty tensors are a no-op
+        TensorWork w;
+        int rc = desc_to_work(descs[i], i, qtables, sr, seed, w);
+        if (rc) return rc;
+        works.push_back(w);
+    }
+    plan_multi(works, L);
+    return GEFENX_OK;
+}
+
+size_t gefenx_multi_tensor_scratch_bytes(int n) {
+    if (n <= 0) return 256;
+    // each tensor is one segment of one launch per phase
+    return multi_scratch_bytes(n, (size_t)n * 3);
+}
+
+int gefenx_multi_tensor_step(const gefenx_tensor_desc* descs, int n, const void* const* qtables_dev,
+                             int stochastic_round, int64_t rng_seed, void* desc_scratch_dev,
+                             size_t desc_scratch_bytes, void* stream) {
+    MtLayout L;
+    int rc = build_layout(descs, n, qtables_dev, stochastic_round, rng_seed, L);
+    if (rc) return rc;
+    if (L.works.empty()) return GEFENX_OK;
+    if (!desc_scratch_dev) return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: null scratch");
+    return run_multi(L, desc_scratch_dev, desc_scratch_bytes, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -18,11 +18,14 @@ and a missing gfx950 library raises instead of falling back to host math.
 """
 from __future__ import annotations
 
+import ctypes
 import logging
 import math
+import os
 import warnings
 from typing import Iterable, Optional, Tuple, Union
 
+import numpy as np
 import torch
 import torch.nn as nn
 
@@ -40,6 +43,9 @@ _CHECKPOINT_FORMAT_VERSION = 1
 
 # Keys of per-parameter state that exist only at run time (workspaces).
 _RUNTIME_STATE_KEYS = ("_gefenx_ws",)
+
+# numpy image of gefenx_tensor_desc (field order and offsets of the C struct)
+_DESC_DTYPE = np.dtype(_native.TensorDesc)
 
 
 def automatic_partition_view(flat_tensor: torch.Tensor, period: int) -> torch.Tensor:
@@ -117,6 +123,10 @@ class Gefen(torch.optim.Optimizer):
         self._gefen_codebook_by_device = {}
         self._gefen_global_step = 0
         self._param_names = {}
+        # All parameters of a device go through one gefenx_multi_tensor_step
+        # call; GEFENX_MULTI_TENSOR=0 selects one call per parameter.
+        self._multi_tensor = os.environ.get("GEFENX_MULTI_TENSOR", "1") != "0"
+        self._mt_scratch = {}
         defaults = dict(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps, weight_decay=weight_decay)
         super().__init__(self._normalize_param_groups(params), defaults)
 
@@ -373,10 +383,9 @@ class Gefen(torch.optim.Optimizer):
             state["_gefenx_ws"] = ws
         return ws
 
-    def _step_automatic_factored(self, group, name, p, grad):
-        """gefen.py:2784-3018 on the MI355X factored kernels."""
-        if grad.numel() == 0:
-            return
+    def _prepare_factored(self, group, name, p, grad):
+        """State bookkeeping of gefen.py:2784-2852 (lazy init, resume from a
+        block-vmean checkpoint, step counters); returns the kernel scalars."""
         state = self.state[p]
         if "step" not in state:
             self._init_state(state, p, grad, name, factored=True)
@@ -386,28 +395,14 @@ class Gefen(torch.optim.Optimizer):
             state["factored_step"] = 0
         state["step"] += 1
         state["factored_step"] += 1
-        beta1, beta2, eps = group["beta1"], group["beta2"], group["eps"]
         lr = self._lr_value(group)
-        bc1 = 1 - beta1 ** state["step"]
-        bc2 = 1 - beta2 ** state["factored_step"]
-        rows, cols = p.shape
-        period = state["automatic_period"]
-        nb = p.numel() // period
-        ws = self._workspace(state, _native.WS_FACTORED, rows, cols, nb, p.device)
-        qt = _fused.quant_table(self._gefen_codebook_on(p.device), p.dtype)
-        _native.check(_native.load().gefenx_factored_update(
-            p.data_ptr(), grad.data_ptr(), _fused._dtype_code(p.dtype), rows, cols,
-            p.stride(0), p.stride(1), grad.stride(0), grad.stride(1),
-            state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(),
-            state["v_row"].data_ptr(), state["v_col"].data_ptr(), period, qt.data_ptr(),
-            beta1, beta2, lr, eps, 1.0 / bc2, 1.0 / bc1, 1.0 - lr * group["weight_decay"],
-            1 if self._stochastic_round else 0, self._gefen_global_step, None, None,
-            ws.data_ptr(), ws.numel(), _stream_of(p)), "factored update of " + name)
+        bc1 = 1 - group["beta1"] ** state["step"]
+        bc2 = 1 - group["beta2"] ** state["factored_step"]
+        return state, lr, 1.0 / bc2, 1.0 / bc1, 1.0 - lr * group["weight_decay"]
 
-    def _step_automatic(self, group, name, p, grad):
-        """gefen.py:3488-3818 on the MI355X block kernels."""
-        if grad.numel() == 0:
-            return
+    def _prepare_block(self, group, name, p, grad):
+        """State bookkeeping of gefen.py:3488-3586; returns the kernel scalars
+        (the second one is 1/sqrt(bc2), as the block stepsize uses it)."""
         state = self.state[p]
         if "step" not in state:
             self._init_state(state, p, grad, name, factored=False)
@@ -418,10 +413,35 @@ class Gefen(torch.optim.Optimizer):
             state["vmean_step"] = state["step"]
         state["step"] += 1
         state["vmean_step"] += 1
-        beta1, beta2, eps = group["beta1"], group["beta2"], group["eps"]
         lr = self._lr_value(group)
-        bc1 = 1 - beta1 ** state["step"]
-        bc2 = 1 - beta2 ** state["vmean_step"]
+        bc1 = 1 - group["beta1"] ** state["step"]
+        bc2 = 1 - group["beta2"] ** state["vmean_step"]
+        return state, lr, 1.0 / math.sqrt(bc2), 1.0 / bc1, 1.0 - lr * group["weight_decay"]
+
+    def _step_automatic_factored(self, group, name, p, grad, prepared=None):
+        """gefen.py:2784-3018 on the MI355X factored kernels (one parameter)."""
+        if grad.numel() == 0:
+            return
+        state, lr, inv_bc2, inv_bc1, wdf = prepared or self._prepare_factored(group, name, p, grad)
+        rows, cols = p.shape
+        period = state["automatic_period"]
+        nb = p.numel() // period
+        ws = self._workspace(state, _native.WS_FACTORED, rows, cols, nb, p.device)
+        qt = _fused.quant_table(self._gefen_codebook_on(p.device), p.dtype)
+        _native.check(_native.load().gefenx_factored_update(
+            p.data_ptr(), grad.data_ptr(), _fused._dtype_code(p.dtype), rows, cols,
+            p.stride(0), p.stride(1), grad.stride(0), grad.stride(1),
+            state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(),
+            state["v_row"].data_ptr(), state["v_col"].data_ptr(), period, qt.data_ptr(),
+            group["beta1"], group["beta2"], lr, group["eps"], inv_bc2, inv_bc1, wdf,
+            1 if self._stochastic_round else 0, self._gefen_global_step, None, None,
+            ws.data_ptr(), ws.numel(), _stream_of(p)), "factored update of " + name)
+
+    def _step_automatic(self, group, name, p, grad, prepared=None):
+        """gefen.py:3488-3818 on the MI355X block kernels (one parameter)."""
+        if grad.numel() == 0:
+            return
+        state, lr, inv_sqrt_bc2, inv_bc1, wdf = prepared or self._prepare_block(group, name, p, grad)
         period = state["automatic_period"]
         nb = p.numel() // period
         p_k = p if p.is_contiguous() else p.contiguous()
@@ -431,12 +451,54 @@ class Gefen(torch.optim.Optimizer):
         _native.check(_native.load().gefenx_block_update(
             p_k.data_ptr(), g_k.data_ptr(), _fused._dtype_code(p.dtype), p.numel(), period,
             state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(), state["vmean"].data_ptr(),
-            qt.data_ptr(), beta1, beta2, lr, eps, 1.0 / math.sqrt(bc2), 1.0 / bc1,
-            1.0 - lr * group["weight_decay"], 1 if self._stochastic_round else 0,
-            self._gefen_global_step, None, None, ws.data_ptr(), ws.numel(), _stream_of(p)),
-            "block update of " + name)
+            qt.data_ptr(), group["beta1"], group["beta2"], lr, group["eps"], inv_sqrt_bc2, inv_bc1, wdf,
+            1 if self._stochastic_round else 0, self._gefen_global_step, None, None,
+            ws.data_ptr(), ws.numel(), _stream_of(p)), "block update of " + name)
         if p_k is not p:
             p.copy_(p_k)
+
+    def _desc_row(self, group, p, grad, factored, prepared):
+        """One gefenx_tensor_desc (include/gefenx.h) as a tuple in field order."""
+        state, lr, inv_bc2, inv_bc1, wdf = prepared
+        period = state["automatic_period"]
+        nb = p.numel() // period
+        if factored:
+            rows, cols = p.shape
+            ws = self._workspace(state, _native.WS_FACTORED, rows, cols, nb, p.device)
+            v0, v1 = state["v_row"].data_ptr(), state["v_col"].data_ptr()
+            ps0, ps1, gs0, gs1 = p.stride(0), p.stride(1), grad.stride(0), grad.stride(1)
+        else:
+            rows, cols = 1, p.numel()
+            ws = self._workspace(state, _native.WS_BLOCK, 0, 0, nb, p.device)
+            v0, v1 = state["vmean"].data_ptr(), 0
+            ps0, ps1, gs0, gs1 = cols, 1, cols, 1
+        beta1, beta2 = group["beta1"], group["beta2"]
+        return (p.data_ptr(), grad.data_ptr(), state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(),
+                v0, v1, ws.data_ptr(), rows, cols, ps0, ps1, gs0, gs1, period,
+                _fused._dtype_code(p.dtype), 1 if factored else 0,
+                lr, group["eps"], inv_bc2, inv_bc1, wdf, 1.0 - beta1, beta2, 1.0 - beta2)
+
+    def _multi_tensor_step(self, device, rows, dtypes):
+        """All parameters of one device in one gefenx_multi_tensor_step call
+        (stats, finalize and apply phases each launched once per kernel
+        variant instead of once per parameter)."""
+        lib = _native.load()
+        descs = np.array(rows, dtype=_DESC_DTYPE)
+        cb = self._gefen_codebook_on(device)
+        qt = [0, 0, 0]
+        for dt in dtypes:
+            qt[_fused._dtype_code(dt)] = _fused.quant_table(cb, dt).data_ptr()
+        qt_arr = (ctypes.c_void_p * 3)(*qt)
+        need = int(lib.gefenx_multi_tensor_scratch_bytes(len(rows)))
+        scratch = self._mt_scratch.get(device)
+        if scratch is None or scratch.numel() < need:
+            scratch = torch.empty(need, dtype=torch.uint8, device=device)
+            self._mt_scratch[device] = scratch
+        with torch.cuda.device(device):
+            _native.check(lib.gefenx_multi_tensor_step(
+                descs.ctypes.data, len(rows), qt_arr, 1 if self._stochastic_round else 0,
+                self._gefen_global_step, scratch.data_ptr(), scratch.numel(),
+                torch.cuda.current_stream(device).cuda_stream), "multi-tensor step")
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -449,15 +511,28 @@ class Gefen(torch.optim.Optimizer):
         if (self._codebook_refresh_every and self._gefen_global_step > 0
                 and self._gefen_global_step % self._codebook_refresh_every == 0):
             self._refresh_codebook_with_requant()
+        batches = {}  # device -> (desc rows, dtypes)
         for group in self.param_groups:
             for name, p in self._iter_group_params_with_names(group):
                 grad = p.grad
-                if grad is None:
+                if grad is None or grad.numel() == 0:
                     continue
-                if self._factored_v_2d and p.ndim == 2 and not hasattr(p, "placements"):
-                    self._step_automatic_factored(group, name, p, grad)
+                factored = self._factored_v_2d and p.ndim == 2 and not hasattr(p, "placements")
+                if factored:
+                    prepared = self._prepare_factored(group, name, p, grad)
                 else:
-                    self._step_automatic(group, name, p, grad)
+                    prepared = self._prepare_block(group, name, p, grad)
+                batchable = self._multi_tensor and (factored or (p.is_contiguous() and grad.is_contiguous()))
+                if batchable:
+                    rows, dtypes = batches.setdefault(p.device, ([], set()))
+                    rows.append(self._desc_row(group, p, grad, factored, prepared))
+                    dtypes.add(p.dtype)
+                elif factored:
+                    self._step_automatic_factored(group, name, p, grad, prepared)
+                else:
+                    self._step_automatic(group, name, p, grad, prepared)
+        for device, (rows, dtypes) in batches.items():
+            self._multi_tensor_step(device, rows, dtypes)
         self._gefen_global_step += 1
         return loss
 

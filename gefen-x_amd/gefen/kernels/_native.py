@@ -49,7 +49,7 @@ class TensorDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("factored", ctypes.c_int32),
         ("lr", ctypes.c_float), ("eps", ctypes.c_float), ("inv_bc2", ctypes.c_float),
         ("inv_bc1", ctypes.c_float), ("wd_factor", ctypes.c_float),
-        ("beta1", ctypes.c_float), ("beta2", ctypes.c_float), ("pad_", ctypes.c_float),
+        ("lerp_w", ctypes.c_float), ("beta2", ctypes.c_float), ("alpha2", ctypes.c_float),
     ]
 
 

@@ -192,9 +192,11 @@ typedef struct gefenx_tensor_desc {
     int64_t period;
     int32_t dtype;          /* gefenx_dtype of p and grad */
     int32_t factored;       /* 1: factored second moment; 0: block vmean */
-    float lr, eps, inv_bc2, inv_bc1, wd_factor, beta1, beta2;
+    float lr, eps, inv_bc2, inv_bc1, wd_factor;
     /* inv_bc2: factored 1/bc2, block 1/sqrt(bc2) */
-    float pad_;
+    float lerp_w;           /* (float)(1 - beta1): momentum lerp weight */
+    float beta2;            /* (float)beta2 */
+    float alpha2;           /* (float)(1 - beta2), rounded from double */
 } gefenx_tensor_desc;
 
 /* Step every tensor in descs[n] (host array; copied to the device inside the
@@ -206,7 +208,8 @@ int gefenx_multi_tensor_step(const gefenx_tensor_desc* descs, int n,
                              int64_t rng_seed, void* desc_scratch_dev,
                              size_t desc_scratch_bytes, void* stream);
 
-/* Bytes of device scratch gefenx_multi_tensor_step needs for n tensors. */
+/* Bytes of device scratch gefenx_multi_tensor_step needs for n tensors
+ * (descriptors and the workgroup -> tensor segment tables). */
 size_t gefenx_multi_tensor_scratch_bytes(int n);
 
 /* ------------------------------------------------------------------------
