@@ -11,6 +11,7 @@ enum DType : int { F32 = 0, F16 = 1, BF16 = 2, F64 = 3 };
 constexpr int kCodebookMax = 256;
 constexpr int kBuckets = 4096;        // bucket index over [-1, 1] (2^12)
 constexpr int kLutEntries = kBuckets + 1;
+constexpr int kFqEntries = kBuckets + 8;  // fast-quantiser entries incl. padding (x = 1 lands in 4096)
 
 // Byte image of the quantisation table (gefenx_qtable_build).  Plain data,
 // copied verbatim to device memory; kernels stage the parts they need in LDS.
@@ -24,6 +25,10 @@ struct QTable {
     float thr[kCodebookMax];         // thr[i] = largest x in [-1,1] with nearest(x) <= i
     uint32_t bucket[kBuckets];       // base | (count << 16) of thresholds per bucket
     int16_t lut[kLutEntries + 7];    // reference search LUT (stochastic rounding)
+    // Fast quantiser, one 8-byte entry per bucket: {bits of thr[base], base}.
+    // When no bucket holds more than one threshold (max_cnt <= 1) the nearest
+    // index of x in bucket b is base + (thr[base] < x).
+    uint32_t fq[2 * kFqEntries];
 };
 
 static_assert(sizeof(QTable) % 16 == 0, "QTable must stay 16-byte aligned in size");
@@ -68,8 +73,9 @@ struct FactoredWs {
     // double row_part[ct][rows], double col_part[rt][cols] (per-tile partial
     // sums, fully rewritten every step), uint32 magbits[shards][nb] (zero
     // between steps), float mag_old[nb], float minv[nb],
-    // double vrow_sum[ceil(rows/256)] (partials of sum(v_row))
-    size_t off_rowp, off_colp, off_magbits, off_magold, off_minv, off_vsum, total;
+    // double vrow_sum[ceil(rows/256)] (partials of sum(v_row)), float vcs[cols] (sqrt(v_col)),
+    // {uint32 finalize counter (zero between steps), float mean(v_row)}
+    size_t off_rowp, off_colp, off_magbits, off_magold, off_minv, off_vsum, off_vcs, off_fin, total;
     static FactoredWs make(int64_t rows, int64_t cols, int64_t nb) {
         FactoredWs w;
         const FactTiles t = FactTiles::make(rows, cols);
@@ -80,6 +86,8 @@ struct FactoredWs {
         w.off_magold = o;  o += align256(sizeof(float) * (size_t)nb);
         w.off_minv = o;    o += align256(sizeof(float) * (size_t)nb);
         w.off_vsum = o;    o += align256(sizeof(double) * (size_t)((rows + kFinRowsPerWg - 1) / kFinRowsPerWg));
+        w.off_vcs = o;     o += align256(sizeof(float) * (size_t)cols);
+        w.off_fin = o;     o += 256;
         w.total = o;
         return w;
     }

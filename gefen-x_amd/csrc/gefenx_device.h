@@ -17,6 +17,16 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Global-address-space views of generic pointers.  Pointers read from a
+// descriptor in memory are generic; loads through them would be FLAT
+// instructions, which count against lgkmcnt together with LDS reads, so every
+// wait for an LDS gather would also wait for the HBM loads in flight.
+#define GX_GLOBAL __attribute__((address_space(1)))
+template <class T> __device__ __forceinline__ GX_GLOBAL T* gbl(T* p) { return (GX_GLOBAL T*)p; }
+template <class T> __device__ __forceinline__ const GX_GLOBAL T* gbl(const T* p) {
+    return (const GX_GLOBAL T*)p;
+}
+
 template <int DT> struct Elem { using T = uint16_t; };
 template <> struct Elem<F32> { using T = float; };
 
@@ -55,13 +65,13 @@ template <int DT> __device__ __forceinline__ float round_dt(float v) {
 template <int DT>
 __device__ __forceinline__ void load8(const typename Elem<DT>::T* __restrict__ base, float v[8]) {
     if constexpr (DT == F32) {
-        const f32x4* q = reinterpret_cast<const f32x4*>(base);
+        const GX_GLOBAL f32x4* q = gbl(reinterpret_cast<const f32x4*>(base));
         f32x4 a = q[0];
         f32x4 b = q[1];
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
-        u32x4 a = *reinterpret_cast<const u32x4*>(base);
+        u32x4 a = *gbl(reinterpret_cast<const u32x4*>(base));
         uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -74,7 +84,7 @@ __device__ __forceinline__ void load8(const typename Elem<DT>::T* __restrict__ b
 template <int DT>
 __device__ __forceinline__ void store8(typename Elem<DT>::T* __restrict__ base, const float v[8]) {
     if constexpr (DT == F32) {
-        f32x4* q = reinterpret_cast<f32x4*>(base);
+        GX_GLOBAL f32x4* q = gbl(reinterpret_cast<f32x4*>(base));
         f32x4 a = {v[0], v[1], v[2], v[3]};
         f32x4 b = {v[4], v[5], v[6], v[7]};
         __builtin_nontemporal_store(a, q);
@@ -85,12 +95,12 @@ __device__ __forceinline__ void store8(typename Elem<DT>::T* __restrict__ base, 
         for (int i = 0; i < 4; ++i)
             w[i] = (uint32_t)from_f32<DT>(v[2 * i]) | ((uint32_t)from_f32<DT>(v[2 * i + 1]) << 16);
         u32x4 a = {w[0], w[1], w[2], w[3]};
-        __builtin_nontemporal_store(a, reinterpret_cast<u32x4*>(base));
+        __builtin_nontemporal_store(a, gbl(reinterpret_cast<u32x4*>(base)));
     }
 }
 
 __device__ __forceinline__ void load_idx8(const uint8_t* __restrict__ base, uint32_t ix[8]) {
-    u32x2 a = *reinterpret_cast<const u32x2*>(base);
+    u32x2 a = *gbl(reinterpret_cast<const u32x2*>(base));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         ix[i] = (a.x >> (8 * i)) & 0xffu;
@@ -102,7 +112,7 @@ __device__ __forceinline__ void store_idx8(uint8_t* __restrict__ base, const uin
     u32x2 a;
     a.x = ix[0] | (ix[1] << 8) | (ix[2] << 16) | (ix[3] << 24);
     a.y = ix[4] | (ix[5] << 8) | (ix[6] << 16) | (ix[7] << 24);
-    __builtin_nontemporal_store(a, reinterpret_cast<u32x2*>(base));
+    __builtin_nontemporal_store(a, gbl(reinterpret_cast<u32x2*>(base)));
 }
 
 // Packed (as-loaded) 8-element chunks: loads stay packed while in flight and
@@ -115,7 +125,7 @@ __device__ __forceinline__ void load_raw8(const typename Elem<DT>::T* __restrict
     if constexpr (DT == F32) {
         load8<F32>(base, r.f);
     } else {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(base);
+        const u32x4 v = *gbl(reinterpret_cast<const u32x4*>(base));
         r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
     }
 }
@@ -129,7 +139,7 @@ __device__ __forceinline__ float raw_elem(const Raw8<DT>& r, int k) {
 struct RawIdx8 { uint32_t lo, hi; };
 
 __device__ __forceinline__ RawIdx8 load_raw_idx8(const uint8_t* __restrict__ base) {
-    const u32x2 v = *reinterpret_cast<const u32x2*>(base);
+    const u32x2 v = *gbl(reinterpret_cast<const u32x2*>(base));
     return RawIdx8{v.x, v.y};
 }
 

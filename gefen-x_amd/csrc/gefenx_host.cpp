@@ -175,6 +175,13 @@ int gefenx_qtable_build(const float* codebook, int k, int dtype, void* table_out
         t->bucket[b] = (uint32_t)base | ((uint32_t)cnt << 16);
         t->max_cnt = std::max(t->max_cnt, cnt);
     }
+    for (int b = 0; b < kFqEntries; ++b) {
+        const uint32_t e = t->bucket[std::min(b, kBuckets - 1)];
+        const uint32_t base = e & 0xffffu;
+        const float t0 = (int)base < k - 1 ? t->thr[base] : std::numeric_limits<float>::infinity();
+        t->fq[2 * b] = f2u(t0);
+        t->fq[2 * b + 1] = base;
+    }
     int rc = gefenx_search_lut(codebook, k, kBuckets, t->lut);
     if (rc != GEFENX_OK) return rc;
     for (int i = kLutEntries; i < kLutEntries + 7; ++i) t->lut[i] = (int16_t)k;

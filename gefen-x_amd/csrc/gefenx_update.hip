@@ -37,7 +37,7 @@ namespace gx {
 constexpr int kThreads = 256;
 constexpr int kChunk = 8;
 constexpr int64_t kWaves = kThreads / 64;
-constexpr int64_t kApplyChunksPerThread = 4;   // apply: 2 iterations of 2 chunks
+constexpr int64_t kApplyChunksPerThread = 8;   // apply: 4 iterations of 2 chunks
 constexpr int64_t kBlockStatsChunksPerThread = 4;
 constexpr int64_t kFinBlocksPerWg = 1024;
 
@@ -63,6 +63,8 @@ struct TensorWork {
     uint32_t* magbits;
     float* mag_old;
     float* minv;
+    float* vcs;          // factored: sqrt(v_col), written by finalize
+    uint32_t* fin;       // factored: {finalize counter, bits of mean(v_row)}
     const QTable* qt;
     const float* step_scalars;
     const int64_t* seed_dev;
@@ -72,6 +74,7 @@ struct TensorWork {
     int64_t ct, rt, tile_rows, shards;
     int64_t stats_wgs, nr, nc, nbw, fin_wgs, apply_wgs;
     int64_t dR, dC, dB, dP;  // apply: chunk advance for a stride of apply_wgs*256*8 elements
+    int64_t fR, fC, fB, fP;  // fast apply: advance for a stride of 256*8 elements
     uint64_t seed;
     int32_t dtype, mode, fast_stats, fast_apply, write_p, sr, bf16_mean, pad_;
     float eps, beta2, alpha2, pad2_;
@@ -431,7 +434,9 @@ __device__ __forceinline__ void finalize_factored(const TensorWork& w, int64_t w
             double tot = 0.0;
             for (int ww = 0; ww < kWaves; ++ww) tot += s_cp[ww][lane];
             const float ms = (float)tot / (float)w.R;
-            w.v1[j] = __builtin_fmaf(ms, w.alpha2, w.v1[j] * w.beta2);
+            const float v = __builtin_fmaf(ms, w.alpha2, w.v1[j] * w.beta2);
+            w.v1[j] = v;
+            w.vcs[j] = sqrtf(v);
         }
         return;
     }
@@ -456,21 +461,28 @@ __device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) 
     }
 }
 
-// Deterministic mean(v_row) from the finalize partials, clamped at FLT_MIN
-// (gefen.py:2998-3000); every workgroup of the apply phase recomputes it.
-__device__ __forceinline__ float mean_from_partials(const double* __restrict__ vsum, int64_t nr, int64_t R) {
-    __shared__ double s_red[kThreads];
+// mean(v_row) of one factored parameter from the finalize partials, in a
+// fixed order, clamped at FLT_MIN (gefen.py:2998-3000); one workgroup.
+__device__ __forceinline__ void mean_phase(const TensorWork& w) {
+    __shared__ double s_part[kWaves];
+    const int tid = threadIdx.x;
     double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < nr; i += kThreads) acc += vsum[i];
-    s_red[threadIdx.x] = acc;
+    for (int64_t k = tid; k < w.nr; k += kThreads) acc += *gbl(w.vsum + k);
+    acc = wave_sum_d(acc);
+    if ((tid & 63) == 0) s_part[tid >> 6] = acc;
     __syncthreads();
-    for (int off = kThreads / 2; off > 0; off >>= 1) {
-        if ((int)threadIdx.x < off) s_red[threadIdx.x] += s_red[threadIdx.x + off];
-        __syncthreads();
+    if (tid == 0) {
+        double t = 0.0;
+        for (int ww = 0; ww < kWaves; ++ww) t += s_part[ww];
+        float mean = (float)t / (float)w.R;
+        if (!(mean >= 1.17549435e-38f) && mean == mean) mean = 1.17549435e-38f;
+        w.fin[1] = __float_as_uint(mean);
     }
-    float mean = (float)s_red[0] / (float)R;
-    if (!(mean >= 1.17549435e-38f) && mean == mean) mean = 1.17549435e-38f;
-    return mean;
+}
+
+// mean(v_row) as finalize stored it (already clamped at FLT_MIN).
+__device__ __forceinline__ float stored_mean(const TensorWork& w) {
+    return __uint_as_float(*gbl(w.fin + 1));
 }
 
 // ====================================================================
@@ -497,7 +509,7 @@ __device__ __forceinline__ Pos advance(const TensorWork& w, Pos q) {
 }
 
 __device__ __forceinline__ void load_vcol(const float* __restrict__ vc, float v[8]) {
-    const f32x4* q = reinterpret_cast<const f32x4*>(vc);
+    const GX_GLOBAL f32x4* q = gbl(reinterpret_cast<const f32x4*>(vc));
     const f32x4 v0 = q[0], v1 = q[1];
     v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
     v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
@@ -590,7 +602,7 @@ __device__ __forceinline__ void apply_phase(const TensorWork& w, int64_t wg, int
         if (w.seed_dev != nullptr) cx.seed = (uint64_t)w.seed_dev[0];
     }
     cx.row_scale = 0.0f;
-    if constexpr (MODE == 0) cx.row_scale = (1.0f / mean_from_partials(w.vsum, w.nr, w.R)) * cx.sc.inv_bc2;
+    if constexpr (MODE == 0) cx.row_scale = (1.0f / stored_mean(w)) * cx.sc.inv_bc2;
     cx.c1 = cx.sc.inv_bc1 * cx.sc.lr;
     cx.wd = cx.sc.wdf != 1.0f;
 
@@ -738,6 +750,258 @@ __device__ __forceinline__ void apply_phase(const TensorWork& w, int64_t wg, int
 }
 
 // ====================================================================
+// Fast apply (the hot path): contiguous p/grad, C % 8 == 0, P % 8 == 0,
+// nearest rounding, a table with at most one threshold per bucket.
+// Workgroup `wg` owns chunks [wg*256*kApplyChunksPerThread, ...): thread t
+// takes chunks t, t+256, ... of that range, two at a time with all loads
+// issued before any math.  Per element the only LDS traffic is the old
+// codeword, one 8-byte quantiser entry {thr[base], base} and the new
+// codeword; the step uses sqrt(v_col) precomputed by finalize and one
+// sqrt(v_row * scale) per chunk.
+// ====================================================================
+struct FastTables {
+    uint2 fq[kFqEntries];
+    float cbr[kCodebookMax];
+};
+
+// All loads of a thread's share are issued before the first LDS write.
+__device__ __forceinline__ void stage_fast(FastTables& s, const QTable* __restrict__ t) {
+    constexpr int kVec = kFqEntries / 2;                   // uint4 per table
+    constexpr int kPer = (kVec + kThreads - 1) / kThreads;
+    const GX_GLOBAL u32x4* src = gbl(reinterpret_cast<const u32x4*>(t->fq));
+    u32x4* dst = reinterpret_cast<u32x4*>(s.fq);
+    u32x4 v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < kVec) v[j] = src[i];
+    }
+    const float c = threadIdx.x < kCodebookMax ? *gbl(t->cbr + threadIdx.x) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < kVec) dst[i] = v[j];
+    }
+    if (threadIdx.x < kCodebookMax) s.cbr[threadIdx.x] = c;
+}
+
+// Everything the fast loop touches, copied out of the descriptor once: the
+// stores to p / indices could alias the descriptor memory, so fields read
+// through it would be re-fetched after every store.
+template <int DT>
+struct FastArgs {
+    using T = typename Elem<DT>::T;
+    T* p;
+    const T* g;
+    uint8_t* idx;
+    const float* mag_old;
+    const float* mag;
+    const float* minv;
+    const float* vrow;   // factored: v_row
+    const float* vcs;    // factored: sqrt(v_col)
+    const float* bstep;  // block: per-block stepsize
+    const QTable* qt;
+    int64_t C, P, fR, fC, fB, fP;
+    float row_scale, c1, eps, wdf, lr;
+    bool wd;
+    MomentumCoef mc;
+};
+
+// Inputs of one chunk, loaded one pipeline stage ahead of its math.
+template <int DT>
+struct ChunkIn {
+    Raw8<DT> g, p;
+    RawIdx8 i;
+    float vc[kChunk];
+    float m_old, m_new, y, rv;  // rv: v_row (factored) or the block stepsize (block)
+};
+
+template <int DT, int MODE>
+__device__ __forceinline__ Pos advance_fast(const FastArgs<DT>& a, Pos q) {
+    if constexpr (MODE == 0) {
+        q.col += a.fC;
+        q.row += a.fR;
+        if (q.col >= a.C) { q.col -= a.C; ++q.row; }
+    }
+    q.pin += a.fP;
+    q.blk += a.fB;
+    if (q.pin >= a.P) { q.pin -= a.P; ++q.blk; }
+    return q;
+}
+
+// Nearest index through the global threshold table (rare fallback).
+__device__ __forceinline__ uint32_t quant_global(float x, const QTable* __restrict__ qt) {
+    return quant_nearest(x, qt->bucket, qt->thr, (uint32_t)(qt->k - 1));
+}
+
+// Issue the loads of one chunk: the small per-row/per-block values first, so
+// that waiting for them never waits for the streams issued after them.
+template <int DT, int MODE>
+__device__ __forceinline__ void fast_load(const FastArgs<DT>& a, const Pos& ps, int64_t e0, ChunkIn<DT>& in) {
+    in.m_old = *gbl(a.mag_old + ps.blk);
+    in.m_new = *gbl(a.mag + ps.blk);
+    in.y = *gbl(a.minv + ps.blk);
+    if constexpr (MODE == 0) {
+        in.rv = *gbl(a.vrow + ps.row);
+        load_vcol(a.vcs + ps.col, in.vc);
+    } else {
+        in.rv = *gbl(a.bstep + ps.blk);
+    }
+    load_raw8<DT>(a.g + e0, in.g);
+    in.i = load_raw_idx8(a.idx + e0);
+    load_raw8<DT>(a.p + e0, in.p);
+}
+
+// Requantise and apply one chunk, then store its indices and parameters.
+template <int DT, int MODE>
+__device__ __forceinline__ void fast_compute(const FastArgs<DT>& a, const FastTables& ft, int64_t e0,
+                                             const ChunkIn<DT>& in) {
+    const float m_old = in.m_old, m_new = in.m_new, y = in.y;
+    const float tb = 0x1.00001p-100f * fmaxf(m_new, 1.0f);
+    float xs[kChunk];
+    uint32_t ix[kChunk];
+    bool bad = (y == 0.0f);
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        const float u = momentum_value(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
+        const float q0 = u * y;
+        const float r = __builtin_fmaf(-q0, m_new, u);
+        xs[k] = __builtin_fmaf(r, y, q0);
+        bad = bad || !(fabsf(u) >= tb);
+    }
+    if (__builtin_expect(__any(bad), 0)) {
+        const bool nz = m_new > 0.0f;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            const float u = momentum_value(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
+            const float x = nz ? div_by_block(u, m_new, y) : 0.0f;
+            ix[k] = quant_global(x, a.qt);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            int b = (int)__builtin_fmaf(xs[k], (float)(kBuckets / 2), (float)(kBuckets / 2));
+            b = b < 0 ? 0 : (b > kFqEntries - 1 ? kFqEntries - 1 : b);  // |x| <= 1 already (v_med3)
+            const uint2 e = ft.fq[b];
+            ix[k] = e.y + (__uint_as_float(e.x) < xs[k] ? 1u : 0u);
+        }
+    }
+    float sr = 0.0f, bstep = 0.0f;
+    if constexpr (MODE == 0) sr = __builtin_amdgcn_sqrtf(in.rv * a.row_scale);
+    else bstep = in.rv * a.lr;
+    float pv[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        const float q = ft.cbr[ix[k]] * m_new;
+        float st;
+        if constexpr (MODE == 0) st = __builtin_amdgcn_rcpf(__builtin_fmaf(sr, in.vc[k], a.eps)) * a.c1;
+        else st = bstep;
+        float pw = raw_elem<DT>(in.p, k);
+        if (a.wd) pw = round_dt<DT>(pw * a.wdf);
+        pv[k] = pw - q * st;
+    }
+    store_idx8(a.idx + e0, ix);
+    store8<DT>(a.p + e0, pv);
+}
+
+// Workgroup `wg` of one parameter's fast apply.  Two chunks are computed per
+// iteration while the next two are already loading.
+template <int DT, int MODE>
+__device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, const FastTables& ft,
+                                           float row_scale) {
+    FastArgs<DT> a;
+    {
+        const StepScalars sc = read_scalars(w);
+        a.p = static_cast<typename Elem<DT>::T*>(w.p);
+        a.g = static_cast<const typename Elem<DT>::T*>(w.grad);
+        a.idx = w.idx;
+        a.mag_old = w.mag_old;
+        a.mag = w.mag;
+        a.minv = w.minv;
+        a.vrow = w.v0;
+        a.vcs = w.vcs;
+        a.bstep = w.step;
+        a.qt = w.qt;
+        a.C = w.C; a.P = w.P; a.fR = w.fR; a.fC = w.fC; a.fB = w.fB; a.fP = w.fP;
+        a.row_scale = row_scale;
+        a.c1 = sc.inv_bc1 * sc.lr;
+        a.eps = w.eps;
+        a.wdf = sc.wdf;
+        a.lr = sc.lr;
+        a.wd = sc.wdf != 1.0f;
+        a.mc = w.mc;
+    }
+    const int64_t nchunks = w.N / kChunk;
+    const int64_t first = wg * (kThreads * kApplyChunksPerThread) + threadIdx.x;
+    if (first >= nchunks) return;
+    // chunks of this thread: first + i*256 for i < n (n >= 1)
+    const int n = (int)std::min<int64_t>(kApplyChunksPerThread, (nchunks - first + kThreads - 1) / kThreads);
+    Pos p0;
+    {
+        const int64_t e0 = first * kChunk;
+        p0.row = 0;
+        p0.col = e0;
+        if constexpr (MODE == 0) {
+            p0.row = div_floor(e0, w.C, w.invC);
+            p0.col = e0 - p0.row * w.C;
+        }
+        p0.blk = div_floor(e0, w.P, w.invP);
+        p0.pin = e0 - p0.blk * w.P;
+    }
+    Pos p1 = advance_fast<DT, MODE>(a, p0);
+    ChunkIn<DT> A, B;
+    fast_load<DT, MODE>(a, p0, first * kChunk, A);
+    if (n > 1) fast_load<DT, MODE>(a, p1, (first + kThreads) * kChunk, B);
+#pragma unroll 1
+    for (int i = 0; i < n; i += 2) {
+        const int64_t ea = (first + (int64_t)i * kThreads) * kChunk;
+        const int64_t eb = ea + kThreads * kChunk;
+        const Pos p2 = advance_fast<DT, MODE>(a, p1);
+        const Pos p3 = advance_fast<DT, MODE>(a, p2);
+        fast_compute<DT, MODE>(a, ft, ea, A);
+        if (i + 2 < n) fast_load<DT, MODE>(a, p2, ea + 2 * kThreads * kChunk, A);
+        if (i + 1 < n) fast_compute<DT, MODE>(a, ft, eb, B);
+        if (i + 3 < n) fast_load<DT, MODE>(a, p3, eb + 2 * kThreads * kChunk, B);
+        p0 = p2;
+        p1 = p3;
+    }
+}
+
+// LDS of the apply kernels: the fast tables or the general ones, never both.
+union ApplyLds {
+    FastTables f;
+    struct {
+        SharedTables st;
+        SharedSR ssr;
+    } g;
+};
+
+// One apply workgroup: the fast path when the parameter and the table allow
+// it, the general path (grid-stride over all chunks, any strides, stochastic
+// rounding, dense tables) otherwise.
+template <int DT, int MODE, bool SR, bool FAST>
+__device__ __forceinline__ void apply_wg(const TensorWork& w, int64_t wg, int64_t nwg, ApplyLds& lds) {
+    const QTable* qt = w.qt;
+    if constexpr (FAST && !SR) {
+        if (w.write_p && qt->max_cnt <= 1) {
+            stage_fast(lds.f, qt);
+            float row_scale = 0.0f;
+            if constexpr (MODE == 0) {
+                const StepScalars sc = read_scalars(w);
+                row_scale = (1.0f / stored_mean(w)) * sc.inv_bc2;
+            }
+            __syncthreads();
+            apply_fast<DT, MODE>(w, wg, lds.f, row_scale);
+            return;
+        }
+    }
+    stage_tables(lds.g.st, qt);
+    if constexpr (SR) stage_sr(lds.g.ssr, qt);
+    __syncthreads();
+    apply_phase<DT, MODE, SR, FAST>(w, wg, nwg, lds.g.st, lds.g.ssr);
+}
+
+// ====================================================================
 // Kernels.  Single parameter: descriptor by value.  Multi-tensor: a
 // segment table maps launch workgroups to (descriptor, local workgroup).
 // ====================================================================
@@ -747,13 +1011,31 @@ struct Seg {
     int64_t wg_begin;  // first launch workgroup of this descriptor
 };
 
-__device__ __forceinline__ int64_t find_seg(const Seg* __restrict__ segs, int nseg, int64_t wg) {
-    int lo = 0, hi = nseg;  // last seg with wg_begin <= wg
+// Launch workgroup -> segment.  coarse[j] is the segment holding workgroup
+// j << gshift (the host picks gshift so the table stays small), so a lookup
+// is one load plus a binary search inside one granule (usually empty).
+struct SegTable {
+    const Seg* segs;
+    const int32_t* coarse;
+    int nseg;
+    int gshift;
+};
+
+__device__ __forceinline__ Seg find_seg(const SegTable& tb, int64_t wg) {
+    const int64_t j = wg >> tb.gshift;
+    int lo = gbl(tb.coarse)[j];
+    int hi = gbl(tb.coarse)[j + 1] + 1;  // last seg with wg_begin <= wg lies in [lo, hi)
+    hi = hi > tb.nseg ? tb.nseg : hi;
+    const Seg* sg = tb.segs;
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (segs[mid].wg_begin <= wg) lo = mid; else hi = mid;
+        if (*gbl(&sg[mid].wg_begin) <= wg) lo = mid; else hi = mid;
     }
-    return lo;
+    Seg r;
+    r.t = *gbl(&sg[lo].t);
+    r.pad_ = 0;
+    r.wg_begin = *gbl(&sg[lo].wg_begin);
+    return r;
 }
 
 template <int DT, bool FAST>
@@ -771,51 +1053,50 @@ __global__ void __launch_bounds__(kThreads) k_finalize(TensorWork w) {
     else finalize_block(w, blockIdx.x);
 }
 
+__global__ void __launch_bounds__(kThreads) k_mean(TensorWork w) { mean_phase(w); }
+
 template <int DT, int MODE, bool SR, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_apply(TensorWork w) {
-    __shared__ SharedTables st;
-    __shared__ SharedSR ssr;
-    stage_tables(st, w.qt);
-    if constexpr (SR) stage_sr(ssr, w.qt);
-    __syncthreads();
-    apply_phase<DT, MODE, SR, FAST>(w, blockIdx.x, gridDim.x, st, ssr);
+    __shared__ ApplyLds lds;
+    apply_wg<DT, MODE, SR, FAST>(w, blockIdx.x, gridDim.x, lds);
 }
 
 template <int DT, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_mt_factored_stats(const TensorWork* __restrict__ ws,
-                                                                const Seg* __restrict__ segs, int nseg) {
-    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+                                                                SegTable tb) {
+    const Seg sg = find_seg(tb, blockIdx.x);
     stats_factored<DT, FAST>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
 }
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) k_mt_block_stats(const TensorWork* __restrict__ ws,
-                                                             const Seg* __restrict__ segs, int nseg) {
-    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+                                                             SegTable tb) {
+    const Seg sg = find_seg(tb, blockIdx.x);
     const TensorWork& w = ws[sg.t];
     stats_block<DT>(w, (int64_t)blockIdx.x - sg.wg_begin, w.stats_wgs);
 }
 
 __global__ void __launch_bounds__(kThreads) k_mt_finalize(const TensorWork* __restrict__ ws,
-                                                          const Seg* __restrict__ segs, int nseg) {
-    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+                                                          SegTable tb) {
+    const Seg sg = find_seg(tb, blockIdx.x);
     const TensorWork& w = ws[sg.t];
     const int64_t local = (int64_t)blockIdx.x - sg.wg_begin;
     if (w.mode == 0) finalize_factored(w, local);
     else finalize_block(w, local);
 }
 
+__global__ void __launch_bounds__(kThreads) k_mt_mean(const TensorWork* __restrict__ ws, SegTable tb) {
+    const Seg sg = find_seg(tb, blockIdx.x);
+    mean_phase(ws[sg.t]);
+}
+
 template <int DT, int MODE, bool SR, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_mt_apply(const TensorWork* __restrict__ ws,
-                                                       const Seg* __restrict__ segs, int nseg) {
-    __shared__ SharedTables st;
-    __shared__ SharedSR ssr;
-    const Seg sg = segs[find_seg(segs, nseg, blockIdx.x)];
+                                                       SegTable tb) {
+    __shared__ ApplyLds lds;
+    const Seg sg = find_seg(tb, blockIdx.x);
     const TensorWork& w = ws[sg.t];
-    stage_tables(st, w.qt);
-    if constexpr (SR) stage_sr(ssr, w.qt);
-    __syncthreads();
-    apply_phase<DT, MODE, SR, FAST>(w, (int64_t)blockIdx.x - sg.wg_begin, w.apply_wgs, st, ssr);
+    apply_wg<DT, MODE, SR, FAST>(w, (int64_t)blockIdx.x - sg.wg_begin, w.apply_wgs, lds);
 }
 
 // ====================================================================
@@ -898,6 +1179,8 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         w.mag_old = reinterpret_cast<float*>(ws + L.off_magold);
         w.minv = reinterpret_cast<float*>(ws + L.off_minv);
         w.vsum = reinterpret_cast<double*>(ws + L.off_vsum);
+        w.vcs = reinterpret_cast<float*>(ws + L.off_vcs);
+        w.fin = reinterpret_cast<uint32_t*>(ws + L.off_fin);
         w.ct = t.ct; w.rt = t.rt; w.tile_rows = t.tile_rows;
         w.stats_wgs = t.ct * t.rt;
         w.nr = ceil_div(in.R, kFinRowsPerWg);
@@ -931,6 +1214,11 @@ static int build_work(const WorkInput& in, TensorWork& w) {
     w.dC = S - w.dR * w.C;
     w.dB = S / w.P;
     w.dP = S - w.dB * w.P;
+    const int64_t F = kThreads * kChunk;
+    w.fR = F / w.C;
+    w.fC = F - w.fR * w.C;
+    w.fB = F / w.P;
+    w.fP = F - w.fB * w.P;
     return GEFENX_OK;
 }
 
@@ -992,6 +1280,7 @@ static int run_single(const TensorWork& w, hipStream_t s) {
     if (rc) return rc;
     ph = prof_begin(GEFENX_K_FINALIZE, 16.0 * (double)(w.R + w.C + w.nb), 0.0, s);
     hipLaunchKernelGGL(k_finalize, dim3((unsigned)w.fin_wgs), block, 0, s, w);
+    if (w.mode == 0) hipLaunchKernelGGL(k_mean, dim3(1), block, 0, s, w);
     prof_end(ph, s);
     rc = launch_check("finalize");
     if (rc) return rc;
@@ -1017,6 +1306,8 @@ struct Launch {
     GroupKey key;
     size_t seg_off;  // index of the first Seg in the segment array
     int nseg;
+    size_t coarse_off;  // index of the first coarse entry
+    int gshift;
     int64_t wgs;
     double bytes;
 };
@@ -1044,12 +1335,14 @@ static int64_t cohort_limit() {
 struct MtLayout {
     std::vector<TensorWork> works;
     std::vector<Seg> segs;
+    std::vector<int32_t> coarse;
     std::vector<Launch> launches;
 };
 
 static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
     L.works = works;
     L.segs.clear();
+    L.coarse.clear();
     L.launches.clear();
     const int n = (int)works.size();
     const int64_t limit = cohort_limit();
@@ -1058,14 +1351,16 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
         int c1 = c0;
         int64_t acc = 0;
         while (c1 < n && (c1 == c0 || acc + works[(size_t)c1].N <= limit)) acc += works[(size_t)c1++].N;
-        for (int phase = 0; phase < 3; ++phase) {
+        // phases in launch order: 0 stats, 1 finalize, 3 mean(v_row), 2 apply
+        for (int phase : {0, 1, 3, 2}) {
             std::map<GroupKey, std::vector<int>> groups;
             for (int t = c0; t < c1; ++t) {
                 const TensorWork& w = works[(size_t)t];
                 GroupKey k{w.mode, w.dtype, 0, 0};
                 if (phase == 0) k.fast = w.fast_stats;
                 if (phase == 2) { k.fast = w.fast_apply; k.sr = w.sr; }
-                if (phase == 1) k = GroupKey{0, 0, 0, 0};
+                if (phase == 1 || phase == 3) k = GroupKey{0, 0, 0, 0};
+                if (phase == 3 && w.mode != 0) continue;
                 groups[k].push_back(t);
             }
             for (auto& kv : groups) {
@@ -1079,11 +1374,25 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
                 for (int t : kv.second) {
                     const TensorWork& w = works[(size_t)t];
                     L.segs.push_back(Seg{t, 0, l.wgs});
-                    const int64_t wgs = phase == 0 ? w.stats_wgs : phase == 1 ? w.fin_wgs : w.apply_wgs;
+                    const int64_t wgs = phase == 0 ? w.stats_wgs : phase == 1 ? w.fin_wgs
+                                      : phase == 3 ? 1 : w.apply_wgs;
                     l.wgs += wgs;
                     const double es = (double)elem_size(w.dtype);
                     l.bytes += phase == 0 ? (double)w.N * (es + 1.0)
-                             : phase == 1 ? 16.0 * (double)(w.R + w.C + w.nb) : algo_bytes(w);
+                             : phase == 1 ? 16.0 * (double)(w.R + w.C + w.nb)
+                             : phase == 3 ? 8.0 * (double)w.nr : algo_bytes(w);
+                }
+                // coarse table: at most 4 entries per segment (+2)
+                int gs = 0;
+                while ((l.wgs >> gs) > 4 * (int64_t)l.nseg) ++gs;
+                l.gshift = gs;
+                l.coarse_off = L.coarse.size();
+                const int64_t ncoarse = (l.wgs >> gs) + 2;
+                int cur = 0;
+                for (int64_t j = 0; j < ncoarse; ++j) {
+                    const int64_t wgj = j << gs;
+                    while (cur + 1 < l.nseg && L.segs[l.seg_off + (size_t)cur + 1].wg_begin <= wgj) ++cur;
+                    L.coarse.push_back(cur);
                 }
                 L.launches.push_back(l);
             }
@@ -1093,18 +1402,19 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
 }
 
 template <int MODE, bool SR, bool FAST>
-static void launch_mt_apply(int dtype, dim3 grid, hipStream_t s, const TensorWork* ws, const Seg* sg, int nseg) {
+static void launch_mt_apply(int dtype, dim3 grid, hipStream_t s, const TensorWork* ws, SegTable sg) {
     switch (dtype) {
-        case F32: hipLaunchKernelGGL((k_mt_apply<F32, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg, nseg); break;
-        case F16: hipLaunchKernelGGL((k_mt_apply<F16, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg, nseg); break;
-        default: hipLaunchKernelGGL((k_mt_apply<BF16, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg, nseg); break;
+        case F32: hipLaunchKernelGGL((k_mt_apply<F32, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg); break;
+        case F16: hipLaunchKernelGGL((k_mt_apply<F16, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg); break;
+        default: hipLaunchKernelGGL((k_mt_apply<BF16, MODE, SR, FAST>), grid, dim3(kThreads), 0, s, ws, sg); break;
     }
 }
 
 static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hipStream_t s) {
     const size_t works_bytes = align256(sizeof(TensorWork) * L.works.size());
     const size_t segs_bytes = sizeof(Seg) * L.segs.size();
-    const size_t need = works_bytes + align256(segs_bytes);
+    const size_t coarse_bytes = sizeof(int32_t) * L.coarse.size();
+    const size_t need = works_bytes + align256(segs_bytes) + align256(coarse_bytes);
     if (scratch_bytes < need)
         return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: scratch %zu bytes < required %zu", scratch_bytes, need);
     int dev = 0;
@@ -1127,23 +1437,26 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
     char* h = static_cast<char*>(st.host[b]);
     std::memcpy(h, L.works.data(), sizeof(TensorWork) * L.works.size());
     std::memcpy(h + works_bytes, L.segs.data(), segs_bytes);
+    std::memcpy(h + works_bytes + align256(segs_bytes), L.coarse.data(), coarse_bytes);
     if (hipMemcpyAsync(scratch, h, need, hipMemcpyHostToDevice, s) != hipSuccess)
         return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: descriptor upload failed");
     hipEventRecord(st.done[b], s);
     const TensorWork* dws = reinterpret_cast<const TensorWork*>(scratch);
     const Seg* dsegs = reinterpret_cast<const Seg*>(static_cast<char*>(scratch) + works_bytes);
+    const int32_t* dcoarse = reinterpret_cast<const int32_t*>(static_cast<char*>(scratch) + works_bytes +
+                                                             align256(segs_bytes));
     for (const Launch& l : L.launches) {
         if (l.wgs <= 0) continue;
         if (l.wgs > 2147483647LL) return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: launch too large");
         const dim3 grid((unsigned)l.wgs), block(kThreads);
-        const Seg* sg = dsegs + l.seg_off;
-        const int kinds[3] = {GEFENX_K_STATS, GEFENX_K_FINALIZE, GEFENX_K_APPLY};
+        const SegTable sg{dsegs + l.seg_off, dcoarse + l.coarse_off, l.nseg, l.gshift};
+        const int kinds[4] = {GEFENX_K_STATS, GEFENX_K_FINALIZE, GEFENX_K_APPLY, GEFENX_K_FINALIZE};
         int ph = prof_begin(kinds[l.phase], l.bytes, 0.0, s);
         if (l.phase == 0) {
             if (l.key.mode == 0) {
 #define GX_MTS(DTV)                                                                                          \
-    if (l.key.fast) hipLaunchKernelGGL((k_mt_factored_stats<DTV, true>), grid, block, 0, s, dws, sg, l.nseg); \
-    else hipLaunchKernelGGL((k_mt_factored_stats<DTV, false>), grid, block, 0, s, dws, sg, l.nseg)
+    if (l.key.fast) hipLaunchKernelGGL((k_mt_factored_stats<DTV, true>), grid, block, 0, s, dws, sg); \
+    else hipLaunchKernelGGL((k_mt_factored_stats<DTV, false>), grid, block, 0, s, dws, sg)
                 switch (l.key.dtype) {
                     case F32: GX_MTS(F32); break;
                     case F16: GX_MTS(F16); break;
@@ -1152,30 +1465,32 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
 #undef GX_MTS
             } else {
                 switch (l.key.dtype) {
-                    case F32: hipLaunchKernelGGL(k_mt_block_stats<F32>, grid, block, 0, s, dws, sg, l.nseg); break;
-                    case F16: hipLaunchKernelGGL(k_mt_block_stats<F16>, grid, block, 0, s, dws, sg, l.nseg); break;
-                    default: hipLaunchKernelGGL(k_mt_block_stats<BF16>, grid, block, 0, s, dws, sg, l.nseg); break;
+                    case F32: hipLaunchKernelGGL(k_mt_block_stats<F32>, grid, block, 0, s, dws, sg); break;
+                    case F16: hipLaunchKernelGGL(k_mt_block_stats<F16>, grid, block, 0, s, dws, sg); break;
+                    default: hipLaunchKernelGGL(k_mt_block_stats<BF16>, grid, block, 0, s, dws, sg); break;
                 }
             }
+        } else if (l.phase == 3) {
+            hipLaunchKernelGGL(k_mt_mean, grid, block, 0, s, dws, sg);
         } else if (l.phase == 1) {
-            hipLaunchKernelGGL(k_mt_finalize, grid, block, 0, s, dws, sg, l.nseg);
+            hipLaunchKernelGGL(k_mt_finalize, grid, block, 0, s, dws, sg);
         } else {
             const int dt = l.key.dtype;
             if (l.key.mode == 0) {
                 if (l.key.fast) {
-                    if (l.key.sr) launch_mt_apply<0, true, true>(dt, grid, s, dws, sg, l.nseg);
-                    else launch_mt_apply<0, false, true>(dt, grid, s, dws, sg, l.nseg);
+                    if (l.key.sr) launch_mt_apply<0, true, true>(dt, grid, s, dws, sg);
+                    else launch_mt_apply<0, false, true>(dt, grid, s, dws, sg);
                 } else {
-                    if (l.key.sr) launch_mt_apply<0, true, false>(dt, grid, s, dws, sg, l.nseg);
-                    else launch_mt_apply<0, false, false>(dt, grid, s, dws, sg, l.nseg);
+                    if (l.key.sr) launch_mt_apply<0, true, false>(dt, grid, s, dws, sg);
+                    else launch_mt_apply<0, false, false>(dt, grid, s, dws, sg);
                 }
             } else {
                 if (l.key.fast) {
-                    if (l.key.sr) launch_mt_apply<1, true, true>(dt, grid, s, dws, sg, l.nseg);
-                    else launch_mt_apply<1, false, true>(dt, grid, s, dws, sg, l.nseg);
+                    if (l.key.sr) launch_mt_apply<1, true, true>(dt, grid, s, dws, sg);
+                    else launch_mt_apply<1, false, true>(dt, grid, s, dws, sg);
                 } else {
-                    if (l.key.sr) launch_mt_apply<1, true, false>(dt, grid, s, dws, sg, l.nseg);
-                    else launch_mt_apply<1, false, false>(dt, grid, s, dws, sg, l.nseg);
+                    if (l.key.sr) launch_mt_apply<1, true, false>(dt, grid, s, dws, sg);
+                    else launch_mt_apply<1, false, false>(dt, grid, s, dws, sg);
                 }
             }
         }
@@ -1187,7 +1502,10 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
 }
 
 static size_t multi_scratch_bytes(int n_works, size_t n_segs) {
-    return align256(sizeof(TensorWork) * (size_t)n_works) + align256(sizeof(Seg) * n_segs);
+    // coarse tables: <= 4 entries per segment + 2 per launch, and every launch
+    // holds at least one segment
+    return align256(sizeof(TensorWork) * (size_t)n_works) + align256(sizeof(Seg) * n_segs) +
+           align256(sizeof(int32_t) * 6 * n_segs);
 }
 
 }  // namespace gx
@@ -1326,8 +1644,8 @@ static int build_layout(const gefenx_tensor_desc* descs, int n, const void* cons
 
 size_t gefenx_multi_tensor_scratch_bytes(int n) {
     if (n <= 0) return 256;
-    // each tensor is one segment of one launch per phase
-    return multi_scratch_bytes(n, (size_t)n * 3);
+    // each tensor is one segment of one launch per phase (4 phases)
+    return multi_scratch_bytes(n, (size_t)n * 4);
 }
 
 int gefenx_multi_tensor_step(const gefenx_tensor_desc* descs, int n, const void* const* qtables_dev,

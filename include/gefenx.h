@@ -71,8 +71,9 @@ int gefenx_search_lut(const float* codebook, int k, int buckets, int16_t* lut_ou
 /* ------------------------------------------------------------------------
  * Workspace.  Every update entry point takes a device workspace whose size is
  * given by gefenx_workspace_bytes(kind, ...).  It must be zero-filled before
- * its first use; each call leaves it zero-filled again, so one workspace per
- * parameter can be reused across steps (and inside a captured graph).
+ * its first use; each call returns its accumulators and counters to zero (the
+ * rest is scratch rewritten by every call), so one workspace per parameter can
+ * be reused across steps (and inside a captured graph) without clearing.
  * ---------------------------------------------------------------------- */
 enum gefenx_ws_kind { GEFENX_WS_FACTORED = 0, GEFENX_WS_BLOCK = 1, GEFENX_WS_MOMENTUM = 2 };
 size_t gefenx_workspace_bytes(int kind, int64_t rows, int64_t cols, int64_t num_blocks);
