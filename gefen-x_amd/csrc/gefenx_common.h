@@ -37,10 +37,13 @@ static_assert(sizeof(QTable) % 16 == 0, "QTable must stay 16-byte aligned in siz
 // zero on entry and left zero on exit by the finalize kernels.
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Factored stats tiling: a workgroup covers kFactTileCols columns (one wave
-// row of 64 lanes x 8 columns) of `tile_rows` consecutive rows.
-constexpr int64_t kFactTileCols = 512;
-constexpr int64_t kFactTargetWgs = 1024;
+// Factored stats tiling: a workgroup covers kFactTileCols columns (64 lanes x
+// two 8-column chunks) of `tile_rows` consecutive rows.  Tiles hold about
+// N/256 elements (so one parameter alone still fills the GPU), between 16K
+// and 256K (so a many-parameter launch writes few float64 partials).
+constexpr int64_t kFactTileCols = 1024;
+constexpr int64_t kFactTileMinElems = 1 << 14;
+constexpr int64_t kFactTileMaxElems = 1 << 18;
 
 struct FactTiles {
     int64_t ct, rt, tile_rows;
@@ -48,11 +51,15 @@ struct FactTiles {
         FactTiles t;
         t.ct = (cols + kFactTileCols - 1) / kFactTileCols;
         if (t.ct < 1) t.ct = 1;
-        int64_t rt = (kFactTargetWgs + t.ct - 1) / t.ct;
-        if (rt > rows) rt = rows;
-        if (rt < 1) rt = 1;
-        t.tile_rows = (rows + rt - 1) / rt;
-        t.rt = (rows + t.tile_rows - 1) / t.tile_rows;
+        const int64_t tc = cols < kFactTileCols ? (cols < 1 ? 1 : cols) : kFactTileCols;
+        int64_t elems = rows * cols / 256;
+        elems = elems < kFactTileMinElems ? kFactTileMinElems : (elems > kFactTileMaxElems ? kFactTileMaxElems : elems);
+        int64_t tr = (elems + tc - 1) / tc;
+        tr = (tr + 7) & ~int64_t(7);  // whole two-row steps for each of the 4 waves
+        if (tr > rows) tr = rows;
+        if (tr < 1) tr = 1;
+        t.tile_rows = tr;
+        t.rt = (rows + tr - 1) / tr;
         if (t.rt < 1) t.rt = 1;
         return t;
     }

@@ -108,164 +108,260 @@ __device__ __forceinline__ void wavemax_flush(uint32_t* __restrict__ mb, WaveMax
     wm.bits = 0u;
 }
 
+// ---------------------------------------------------- DPP wave reductions
+// GFX9 full-wave sequence (quad_perm 1032, quad_perm 2301, row_half_mirror,
+// row_mirror, row_bcast:15 into rows 1/3, row_bcast:31 into rows 2/3): the
+// total ends in lane 63.  No LDS traffic, unlike a shuffle.
+template <int CTRL, int RMASK>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RMASK, 0xf, false);
+}
+template <int CTRL, int RMASK>
+__device__ __forceinline__ double dpp64(double v) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = dpp32<CTRL, RMASK>((uint32_t)b);
+    const uint32_t hi = dpp32<CTRL, RMASK>((uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// sum over the wave, valid in lane 63
+__device__ __forceinline__ double wave_sum_d63(double v) {
+    v += dpp64<0xB1, 0xf>(v);
+    v += dpp64<0x4E, 0xf>(v);
+    v += dpp64<0x141, 0xf>(v);
+    v += dpp64<0x140, 0xf>(v);
+    v += dpp64<0x142, 0xa>(v);
+    v += dpp64<0x143, 0xc>(v);
+    return v;
+}
+// max over the wave, valid in lane 63
+__device__ __forceinline__ uint32_t wave_max_u63(uint32_t v) {
+    uint32_t o;
+    o = dpp32<0xB1, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x4E, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x141, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x140, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x142, 0xa>(v); v = o > v ? o : v;
+    o = dpp32<0x143, 0xc>(v); v = o > v ? o : v;
+    return v;
+}
+
+// Flush a wave-uniform running block max: one atomic per wave.
+__device__ __forceinline__ void wavemax_flush63(uint32_t* __restrict__ mb, WaveMax& wm) {
+    if (wm.blk >= 0) {
+        const uint32_t m = wave_max_u63(wm.bits);
+        if ((threadIdx.x & 63) == 63 && m != 0u) atomicMax(mb + wm.blk, m);
+    }
+    wm.bits = 0u;
+}
+
 // ====================================================================
-// Factored stats: workgroup = 4 waves over a tile of tile_rows rows x 512
-// columns; lane l owns columns [c0 + 8l, c0 + 8l + 8), wave w takes rows
-// r0 + w, r0 + w + 4, ...  Row sums reduce per wave (one value per row per
-// column tile), column sums across the 4 waves in LDS; both go out as
-// float64 partials (no atomics, deterministic) for the finalize phase.
+// Factored stats: workgroup = 4 waves over a tile of tile_rows rows x 1024
+// columns; lane l owns the chunks at columns c0 + 8l and c0 + 512 + 8l, wave
+// w takes rows r0 + w, r0 + w + 4, ... two at a time.  Per row: squares and
+// the momentum max over the lane's 16 elements, then a float64 DPP reduction
+// of the row sum (one value per row per column tile).  Column sums: fp32 in
+// registers over 8 rows, then float64; the 4 waves combine in LDS at the end.
+// Both go out as float64 partials (no float atomics, deterministic).
+// FAST: contiguous, 16-byte aligned grad, C % 8 == 0, P % 8 == 0.
 // ====================================================================
 template <int DT, bool FAST>
-__device__ __forceinline__ void stats_factored(const TensorWork& w, int64_t wg) {
+__device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg) {
     using T = typename Elem<DT>::T;
+    constexpr int H = 2;  // chunks per lane per row
     __shared__ float s_cbr[kCodebookMax];
     __shared__ double s_col[kWaves - 1][kFactTileCols];
     __shared__ int64_t s_wblk[kWaves];
     __shared__ uint32_t s_wbits[kWaves];
-    for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = w.qt->cbr[i];
+    const QTable* qt = wr.qt;
+    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
+
+    const T* g = static_cast<const T*>(wr.grad);
+    const uint8_t* idxp = wr.idx;
+    const float* mag_old = wr.mag;
+    double* row_part = wr.row_part;
+    double* col_part = wr.col_part;
+    const int64_t R = wr.R, C = wr.C, P = wr.P, gs0 = wr.gs0, gs1 = wr.gs1;
+    const int64_t ct = wr.ct, tile_rows = wr.tile_rows, nb = wr.nb;
+    const double invP = wr.invP;
+    const MomentumCoef mc = wr.mc;
+    uint32_t* mb = wr.magbits + (wg % wr.shards) * nb;
     __syncthreads();
 
-    const int64_t R = w.R, C = w.C, P = w.P;
-    const double invP = w.invP;
-    const MomentumCoef mc = w.mc;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t ctile = wg % w.ct;
-    const int64_t rtile = wg / w.ct;
-    const int64_t c0 = ctile * kFactTileCols + (int64_t)lane * kChunk;
-    const int64_t r_begin = rtile * w.tile_rows;
-    const int64_t r_end = std::min<int64_t>(r_begin + w.tile_rows, R);
-    const int nvalid = (int)std::max<int64_t>(0, std::min<int64_t>(kChunk, C - c0));
-    const T* g = static_cast<const T*>(w.grad);
-    const uint8_t* idxp = w.idx;
-    const float* mag_old = w.mag;
-    uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
-
-    double colacc[kChunk];
+    const int64_t ctile = wg % ct;
+    const int64_t rtile = wg / ct;
+    const int64_t tc0 = ctile * kFactTileCols;
+    const int64_t span = std::min<int64_t>(kFactTileCols, C - tc0);
+    int64_t cc[H];
+    int nv[H];
 #pragma unroll
-    for (int k = 0; k < kChunk; ++k) colacc[k] = 0.0;
+    for (int h = 0; h < H; ++h) {
+        cc[h] = tc0 + h * (kFactTileCols / 2) + (int64_t)lane * kChunk;
+        nv[h] = (int)std::max<int64_t>(0, std::min<int64_t>(kChunk, C - cc[h]));
+    }
+    const int64_t r_begin = rtile * tile_rows;
+    const int64_t r_end = std::min<int64_t>(r_begin + tile_rows, R);
+
+    // block position of the first element of the wave's row segment, and its
+    // advance for 4 rows: (blk, pin) += divmod(4C, P)
+    int64_t blk = 0, pin = 0;
+    {
+        const int64_t e = (r_begin + wave) * C + tc0;
+        blk = div_floor(e, P, invP);
+        pin = e - blk * P;
+    }
+    const int64_t d4 = 4 * C;
+    const int64_t dB4 = div_floor(d4, P, invP);
+    const int64_t dP4 = d4 - dB4 * P;
+
+    float colf[H][kChunk];
+    double cold[H][kChunk];
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) { colf[h][k] = 0.0f; cold[h][k] = 0.0; }
+    int nrows_f = 0;
     WaveMax wm{-1, 0u};
     float mag_cur = 0.0f;
 
-    // kU rows of a wave are loaded before any is reduced (kU loads in flight)
-    constexpr int kU = 4;
-    for (int64_t rg = r_begin + wave; rg < r_end; rg += kU * kWaves) {
-        Raw8<DT> graw[kU];
-        RawIdx8 iraw[kU];
-        float gvu[kU][kChunk];
-        uint32_t ixu[kU][kChunk];
+    for (int64_t r0 = r_begin + wave; r0 < r_end; r0 += 2 * kWaves) {
+        // loads of two rows (r0, r0 + 4) before any math
+        Raw8<DT> graw[2][H];
+        RawIdx8 iraw[2][H];
+        float gsc[2][H][kChunk];
+        uint32_t isc[2][H][kChunk];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t r = rg + (int64_t)u * kWaves;
-            const int64_t e0 = r * C + c0;
-            if constexpr (FAST) {
-                if (r < r_end && nvalid == kChunk) {
-                    load_raw8<DT>(g + e0, graw[u]);
-                    iraw[u] = load_raw_idx8(idxp + e0);
-                } else {
-                    graw[u] = Raw8<DT>{};
-                    iraw[u] = RawIdx8{0u, 0u};
-                }
-            } else {
+        for (int u = 0; u < 2; ++u) {
+            const int64_t r = r0 + (int64_t)u * kWaves;
 #pragma unroll
-                for (int k = 0; k < kChunk; ++k) {
-                    if (r < r_end && k < nvalid) {
-                        gvu[u][k] = to_f32<DT>(g[r * w.gs0 + (c0 + k) * w.gs1]);
-                        ixu[u][k] = idxp[e0 + k];
+            for (int h = 0; h < H; ++h) {
+                const int64_t e0 = r * C + cc[h];
+                if constexpr (FAST) {
+                    if (r < r_end && nv[h] == kChunk) {
+                        load_raw8<DT>(g + e0, graw[u][h]);
+                        iraw[u][h] = load_raw_idx8(idxp + e0);
                     } else {
-                        gvu[u][k] = 0.0f;
-                        ixu[u][k] = 0u;
+                        graw[u][h] = Raw8<DT>{};
+                        iraw[u][h] = RawIdx8{0u, 0u};
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < kChunk; ++k) {
+                        const bool ok = r < r_end && k < nv[h];
+                        gsc[u][h][k] = ok ? to_f32<DT>(*gbl(g + r * gs0 + (cc[h] + k) * gs1)) : 0.0f;
+                        isc[u][h][k] = ok ? (uint32_t)*gbl(idxp + e0 + k) : 0u;
                     }
                 }
             }
         }
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int64_t r = rg + (int64_t)u * kWaves;
+        for (int u = 0; u < 2; ++u) {
+            const int64_t r = r0 + (int64_t)u * kWaves;
             if (r >= r_end) break;
-            const int64_t e0 = r * C + c0;
-            float gv[kChunk];
-            uint32_t ix[kChunk];
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if constexpr (FAST) {
-                    gv[k] = raw_elem<DT>(graw[u], k);
-                    ix[k] = raw_idx(iraw[u], k);
-                } else {
-                    gv[k] = gvu[u][k];
-                    ix[k] = ixu[u][k];
-                }
-            }
-            // block of this row strip: uniform across the wave when the wave's
-            // columns never cross a block boundary
-            const int64_t e_first = r * C + ctile * kFactTileCols;
-            const int64_t blk0 = div_floor(e_first, P, invP);
-            const int64_t span = std::min<int64_t>(kFactTileCols, C - ctile * kFactTileCols);
-            const bool uniform = (e_first + span - 1) < (blk0 + 1) * P;
-            float rowacc = 0.0f;
+            float rs[H];
+            const bool uniform = (pin + span - 1) < P;
             if (uniform) {
-                if (blk0 != wm.blk) {
-                    wavemax_flush(mb, wm);
-                    wm.blk = blk0;
-                    mag_cur = mag_old[blk0];
+                if (blk != wm.blk) {
+                    wavemax_flush63(mb, wm);
+                    wm.blk = blk;
+                    mag_cur = *gbl(mag_old + blk);
                 }
                 uint32_t m = wm.bits;
 #pragma unroll
-                for (int k = 0; k < kChunk; ++k) {
-                    if (k < nvalid) {
-                        const float uu = momentum_value(s_cbr[ix[k]], mag_cur, gv[k], mc);
+                for (int h = 0; h < H; ++h) {
+                    rs[h] = 0.0f;
+                    if (nv[h] == 0) continue;  // columns past C (last tile)
+#pragma unroll
+                    for (int k = 0; k < kChunk; ++k) {
+                        if (!FAST && k >= nv[h]) continue;
+                        float gv;
+                        uint32_t ix;
+                        if constexpr (FAST) { gv = raw_elem<DT>(graw[u][h], k); ix = raw_idx(iraw[u][h], k); }
+                        else { gv = gsc[u][h][k]; ix = isc[u][h][k]; }
+                        const float uu = momentum_value(s_cbr[ix], mag_cur, gv, mc);
                         const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
                         m = ub > m ? ub : m;
-                        const float sq = gv[k] * gv[k];
-                        rowacc += sq;
-                        colacc[k] += (double)sq;
+                        const float sq = gv * gv;
+                        rs[h] += sq;
+                        colf[h][k] += sq;
                     }
                 }
                 wm.bits = m;
             } else {
-                // blocks smaller than the strip: per-lane runs, one atomic per run
-                wavemax_flush(mb, wm);
+                // blocks end inside this row segment: per-lane runs, one atomic per run
+                wavemax_flush63(mb, wm);
                 wm.blk = -1;
-                if (nvalid > 0) {
-                    int64_t blk = div_floor(e0, P, invP);
-                    int64_t pin = e0 - blk * P;
-                    float mo = mag_old[blk];
+#pragma unroll
+                for (int h = 0; h < H; ++h) {
+                    rs[h] = 0.0f;
+                    if (nv[h] == 0) continue;
+                    const int64_t off = pin + (cc[h] - tc0);
+                    const int64_t db = div_floor(off, P, invP);
+                    int64_t bb = blk + db;
+                    int64_t pp = off - db * P;
+                    float mo = *gbl(mag_old + bb);
                     uint32_t m = 0u;
 #pragma unroll
                     for (int k = 0; k < kChunk; ++k) {
-                        if (k < nvalid) {
-                            const float uu = momentum_value(s_cbr[ix[k]], mo, gv[k], mc);
+                        if (k < nv[h]) {
+                            float gv;
+                            uint32_t ix;
+                            if constexpr (FAST) { gv = raw_elem<DT>(graw[u][h], k); ix = raw_idx(iraw[u][h], k); }
+                            else { gv = gsc[u][h][k]; ix = isc[u][h][k]; }
+                            const float uu = momentum_value(s_cbr[ix], mo, gv, mc);
                             const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
                             m = ub > m ? ub : m;
-                            const float sq = gv[k] * gv[k];
-                            rowacc += sq;
-                            colacc[k] += (double)sq;
-                            if (++pin == P) {
-                                if (m) atomicMax(mb + blk, m);
+                            const float sq = gv * gv;
+                            rs[h] += sq;
+                            colf[h][k] += sq;
+                            if (++pp == P) {
+                                if (m) atomicMax(mb + bb, m);
                                 m = 0u;
-                                pin = 0;
-                                ++blk;
-                                if (k + 1 < nvalid) mo = mag_old[blk];
+                                pp = 0;
+                                ++bb;
+                                if (k + 1 < nv[h]) mo = *gbl(mag_old + bb);
                             }
                         }
                     }
-                    if (m) atomicMax(mb + blk, m);
+                    if (m) atomicMax(mb + bb, m);
                 }
             }
-            const double rs = wave_sum_d((double)rowacc);
-            if (lane == 0) w.row_part[ctile * R + r] = rs;
+            double rsum = 0.0;
+#pragma unroll
+            for (int h = 0; h < H; ++h) rsum += (double)rs[h];
+            rsum = wave_sum_d63(rsum);
+            if (lane == 63) *gbl(row_part + ctile * R + r) = rsum;
+            if (++nrows_f == 8) {
+#pragma unroll
+                for (int h = 0; h < H; ++h)
+#pragma unroll
+                    for (int k = 0; k < kChunk; ++k) { cold[h][k] += (double)colf[h][k]; colf[h][k] = 0.0f; }
+                nrows_f = 0;
+            }
+            pin += dP4;
+            blk += dB4;
+            if (pin >= P) { pin -= P; ++blk; }
         }
     }
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) cold[h][k] += (double)colf[h][k];
+
     // final block-max flush: one atomic per workgroup when the waves agree
-    const uint32_t wbits = wave_max_u(wm.bits);
-    if (lane == 0) {
+    const uint32_t wbits = wm.blk >= 0 ? wave_max_u63(wm.bits) : 0u;
+    if (lane == 63) {
         s_wblk[wave] = wm.blk;
         s_wbits[wave] = wbits;
     }
     // column partials: waves 1..3 park theirs in LDS, wave 0 adds and stores
     if (wave > 0) {
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) s_col[wave - 1][lane * kChunk + k] = colacc[k];
+        for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k)
+                s_col[wave - 1][h * (kFactTileCols / 2) + lane * kChunk + k] = cold[h][k];
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -284,11 +380,14 @@ __device__ __forceinline__ void stats_factored(const TensorWork& w, int64_t wg) 
     }
     if (wave == 0) {
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-            double s = colacc[k];
+        for (int h = 0; h < H; ++h) {
 #pragma unroll
-            for (int ww = 0; ww < kWaves - 1; ++ww) s += s_col[ww][lane * kChunk + k];
-            if (k < nvalid) w.col_part[rtile * C + c0 + k] = s;
+            for (int k = 0; k < kChunk; ++k) {
+                double sum = cold[h][k];
+#pragma unroll
+                for (int ww = 0; ww < kWaves - 1; ++ww) sum += s_col[ww][h * (kFactTileCols / 2) + lane * kChunk + k];
+                if (k < nv[h]) *gbl(col_part + rtile * C + cc[h] + k) = sum;
+            }
         }
     }
 }
