@@ -79,6 +79,20 @@ def fill_grads(torch, params, step_seed, device):
         p.grad.normal_(0.0, sigma, generator=gen)
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gefen_step_llama3_8b_traffic.json")
+
+
+def _measured_traffic():
+    """HBM bytes per launch of the factored apply from the committed rocprofv3
+    PMC passes (FETCH_SIZE x its copy-calibrated scale + WRITE_SIZE x its
+    scale), or None when no measurement is committed."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return float(json.load(f)["apply_traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(seconds: float = 12.0):
     """The C oracle (single-threaded restatement of the reference's decomposed
     CPU step) on a bounded sample: factored bf16 steps of a 2048x4096 weight."""
@@ -175,12 +189,14 @@ def main(argv=None):
     value = n_params / (elapsed / args.steps)
 
     kinds = {}
-    for name, kind in (("stats", _native.K_STATS), ("finalize", _native.K_FINALIZE), ("apply", _native.K_APPLY)):
+    for name, kind in (("stats", _native.K_STATS), ("finalize", _native.K_FINALIZE), ("apply", _native.K_APPLY),
+                       ("block_stats", _native.K_BLOCK_STATS), ("block_apply", _native.K_BLOCK_APPLY)):
         kinds[name] = _native.profile_read(kind)
     lib.gefenx_profile_reset()
+    # dominant kernel: the factored (2D) apply, one launch per step
     apply_ms, apply_n, apply_bytes, _ = kinds["apply"]
     achieved = apply_bytes / (apply_ms / 1e3) / 1e9 if apply_ms > 0 else 0.0
-    step_bytes = apply_bytes / args.steps  # compulsory bytes per step
+    step_bytes = (apply_bytes + kinds["block_apply"][2]) / args.steps  # compulsory bytes per step
     _log("bench: kernel ms per step: " + ", ".join(
         "%s %.3f (%d launches)" % (k, v[0] / args.steps, v[1] // args.steps) for k, v in kinds.items()))
     _log("bench: %.3f ms/step, %.1f GB/s compulsory over the whole step" % (
@@ -207,9 +223,9 @@ def main(argv=None):
         "kernel_ms_per_step": {k: v[0] / args.steps for k, v in kinds.items()},
         "first_step_s": t_first,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "k_apply (fused requantize + apply), all launches of the timed region",
-                     "algo_bytes_per_launch_avg": apply_bytes / max(1, apply_n),
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": _measured_traffic(),
+                     "kernel": "k_mt_apply<bf16, factored> (fused requantize + apply of the 226 2D tensors)",
+                     "algo_bytes_per_launch": apply_bytes / max(1, apply_n),
                      "avg_launch_ms": apply_ms / max(1, apply_n)},
     }
     if not args.no_cpu_baseline:

@@ -1353,7 +1353,7 @@ static void launch_apply_single(const TensorWork& w, hipStream_t s) {
 // Run the three phases of one parameter (single-parameter entry points).
 static int run_single(const TensorWork& w, hipStream_t s) {
     const double es = (double)elem_size(w.dtype);
-    int ph = prof_begin(GEFENX_K_STATS, (double)w.N * (es + 1.0), 0.0, s);
+    int ph = prof_begin(w.mode == 0 ? GEFENX_K_STATS : GEFENX_K_BLOCK_STATS, (double)w.N * (es + 1.0), 0.0, s);
     const dim3 block(kThreads);
     if (w.mode == 0) {
         const dim3 grid((unsigned)w.stats_wgs);
@@ -1383,7 +1383,7 @@ static int run_single(const TensorWork& w, hipStream_t s) {
     prof_end(ph, s);
     rc = launch_check("finalize");
     if (rc) return rc;
-    ph = prof_begin(GEFENX_K_APPLY, algo_bytes(w), 0.0, s);
+    ph = prof_begin(w.mode == 0 ? GEFENX_K_APPLY : GEFENX_K_BLOCK_APPLY, algo_bytes(w), 0.0, s);
     if (w.mode == 0) launch_apply_single<0>(w, s);
     else launch_apply_single<1>(w, s);
     prof_end(ph, s);
@@ -1550,7 +1550,10 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
         const dim3 grid((unsigned)l.wgs), block(kThreads);
         const SegTable sg{dsegs + l.seg_off, dcoarse + l.coarse_off, l.nseg, l.gshift};
         const int kinds[4] = {GEFENX_K_STATS, GEFENX_K_FINALIZE, GEFENX_K_APPLY, GEFENX_K_FINALIZE};
-        int ph = prof_begin(kinds[l.phase], l.bytes, 0.0, s);
+        int kind = kinds[l.phase];
+        if (l.key.mode == 1 && l.phase == 0) kind = GEFENX_K_BLOCK_STATS;
+        if (l.key.mode == 1 && l.phase == 2) kind = GEFENX_K_BLOCK_APPLY;
+        int ph = prof_begin(kind, l.bytes, 0.0, s);
         if (l.phase == 0) {
             if (l.key.mode == 0) {
 #define GX_MTS(DTV)                                                                                          \

@@ -94,7 +94,7 @@ SIGNATURES = {
     "gefenx_profile_reset": (_I, []),
 }
 
-K_STATS, K_FINALIZE, K_APPLY, K_MOMENTUM, K_NS_GEMM = 0, 1, 2, 3, 4
+K_STATS, K_FINALIZE, K_APPLY, K_MOMENTUM, K_NS_GEMM, K_BLOCK_STATS, K_BLOCK_APPLY = 0, 1, 2, 3, 4, 5, 6
 
 
 def profile_read(kind: int):

@@ -235,11 +235,14 @@ int gefenx_newton_schulz(void* x, int64_t batch, int64_t rows, int64_t cols,
  * synchronises those events and returns the totals of one kind.  No
  * counterpart in the reference (its benches time with CUDA events from
  * Python, benchmarks/microbench/microbench_v1v2.py:36-47).
- * kinds: 0 stats, 1 finalize, 2 apply, 3 momentum, 4 newton-schulz gemm.
+ * kinds: 0 stats and 2 apply of the factored (2D) path, 1 finalize (both
+ * paths, incl. the mean(v_row) launch), 5 stats and 6 apply of the block
+ * path, 3 momentum, 4 newton-schulz gemm.
  * ---------------------------------------------------------------------- */
 enum gefenx_kernel_kind {
     GEFENX_K_STATS = 0, GEFENX_K_FINALIZE = 1, GEFENX_K_APPLY = 2,
-    GEFENX_K_MOMENTUM = 3, GEFENX_K_NS_GEMM = 4, GEFENX_K_COUNT = 5
+    GEFENX_K_MOMENTUM = 3, GEFENX_K_NS_GEMM = 4, GEFENX_K_BLOCK_STATS = 5,
+    GEFENX_K_BLOCK_APPLY = 6, GEFENX_K_COUNT = 7
 };
 int gefenx_profile_enable(int on);
 int gefenx_profile_read(int kind, double* total_ms, int64_t* launches, double* algo_bytes,

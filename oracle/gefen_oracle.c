@@ -166,6 +166,61 @@ void orc_momentum_update(const float* g, uint8_t* idx, float* mag, int64_t nb,
     free(u);
 }
 
+/* ------------------------------------------------- Muon quantised momentum */
+
+/*
+ * GefenMuon._prepare_muon_momentum, decomposed path: gefen_muon.py:1136-1141
+ * with _quantize_momentum_ (gefen_muon.py:948-974).  Every intermediate is a
+ * tensor of the grad dtype D, so each op rounds to D:
+ *   cm  = D(D(c[idx]) * mag)                          (dequant, mul_)
+ *   u   = D(lerp(cm, g, 1 - beta))                    (lerp_)
+ *   mag'= amax |u| over the block (NaN propagates)    (copy_ into fp32 state)
+ *   x   = mag' > 0 ? D(u / max(mag', tiny)) : 0       (div_, masked_fill_)
+ *   idx'= nearest(x)
+ *   out = D(D(c[idx']) * mag')                        (copy_, mul_)
+ *   nesterov: out = D(fma(a, g, D(out * beta))), a = D((float)(1 - beta))
+ *             (gefen_muon.py:1143-1144: mul_(beta).add_(g, alpha=1-beta); torch
+ *             converts `alpha` to the tensor dtype, a `mul_` scalar stays fp32)
+ * g holds the grad values widened to fp32.  idx / mag are updated in place.
+ */
+void orc_muon_momentum(const float* g, uint8_t* idx, float* mag, int64_t nb,
+                       int64_t period, const float* cb, int k, int dtype,
+                       double beta, int nesterov, float* out) {
+    const float w = (float)(1.0 - beta);
+    const float beta_f = (float)beta;
+    const float alpha_d = orc_round(w, dtype);
+    const float tiny = 1.17549435e-38f;
+    float* u = (float*)malloc(sizeof(float) * (size_t)(period > 0 ? period : 1));
+    for (int64_t b = 0; b < nb; ++b) {
+        const int64_t base = b * period;
+        const float m_old = mag[b];
+        float amax = 0.0f;
+        int saw_nan = 0;
+        for (int64_t j = 0; j < period; ++j) {
+            const float c = orc_round(cb[idx[base + j]], dtype);
+            const float cm = orc_round(c * m_old, dtype);
+            const float uu = orc_round(lerp_f(cm, g[base + j], w), dtype);
+            u[j] = uu;
+            const float a = fabsf(uu);
+            if (isnan(a)) saw_nan = 1;
+            else if (j == 0 || a > amax) amax = a;
+        }
+        const float m_new = saw_nan ? NAN : amax;
+        mag[b] = m_new;
+        const float den = m_new < tiny ? tiny : m_new;  /* clamp(min=tiny); NaN stays NaN */
+        for (int64_t j = 0; j < period; ++j) {
+            float x = orc_round(u[j] / den, dtype);
+            if (m_new <= 0.0f) x = 0.0f;
+            const uint8_t ni = orc_nearest(cb, k, x);
+            idx[base + j] = ni;
+            float o = orc_round(orc_round(cb[ni], dtype) * m_new, dtype);
+            if (nesterov) o = orc_round(fmaf(alpha_d, g[base + j], orc_round(o * beta_f, dtype)), dtype);
+            out[base + j] = o;
+        }
+    }
+    free(u);
+}
+
 /* ------------------------------------------------------- factored step (2D) */
 
 /*

@@ -59,6 +59,7 @@ def _lib():
     lib.orc_nearest_array.argtypes = [P, i, P, i64, P]
     lib.orc_search_lut.argtypes = [P, i, i, P]
     lib.orc_momentum_update.argtypes = [P, P, P, i64, i64, P, i, i, f, P, P]
+    lib.orc_muon_momentum.argtypes = [P, P, P, i64, i64, P, i, i, d, i, P]
     lib.orc_factored_step.argtypes = [P, P, P, P, P, P, i64, i64, i64, P, i, i,
                                       d, d, d, d, d, d, d]
     lib.orc_vmean_update.argtypes = [P, P, i64, i64, i, d]
@@ -141,6 +142,101 @@ def momentum_update(g, idx, mag, period, codebook, dtype, beta1):
     _lib().orc_momentum_update(_ptr(g), _ptr(idx), _ptr(mag), nb, period, _ptr(cb),
                                cb.size, dtype, np.float32(1.0 - beta1), _ptr(q), _ptr(u))
     return idx, mag, q, u
+
+
+def muon_momentum(g, idx, mag, period, codebook, dtype, beta, nesterov=True):
+    """GefenMuon decomposed quantised momentum: gefen_muon.py:1136-1144, 948-974.
+
+    Returns (new_idx, new_mag, out) without mutating the inputs; out is the
+    dense momentum handed to Newton-Schulz (grad-dtype values as fp32).
+    """
+    g = _f32(g).reshape(-1)
+    idx = np.ascontiguousarray(np.asarray(idx, dtype=np.uint8).reshape(-1)).copy()
+    mag = _f32(mag).reshape(-1).copy()
+    nb = g.size // period
+    cb = _f32(codebook)
+    out = np.empty_like(g)
+    _lib().orc_muon_momentum(_ptr(g), _ptr(idx), _ptr(mag), nb, period, _ptr(cb), cb.size, dtype,
+                             float(beta), 1 if nesterov else 0, _ptr(out))
+    return idx, mag, out
+
+
+NS_STANDARD = [(3.4445, -4.7750, 2.0315)] * 5
+
+
+def bf16(x) -> np.ndarray:
+    """Round to bf16 (RNE) and widen back to fp32."""
+    return round_dtype(np.asarray(x, dtype=np.float32), BF16)
+
+
+def newton_schulz(m, schedule=None, eps: float = 1e-7) -> np.ndarray:
+    """_zeropower_via_newtonschulz: gefen_muon.py:236-291 (bf16 path).
+
+    Every torch op of the reference returns a bf16 tensor, so each GEMM output
+    and each elementwise result is rounded to bf16 once; products accumulate
+    in float64 here (the reference's bf16 GEMMs accumulate in fp32), so the
+    comparison carries a tolerance.
+    """
+    schedule = NS_STANDARD if schedule is None else [tuple(map(float, t)) for t in schedule]
+    x = bf16(m)
+    tall = x.shape[0] > x.shape[1]
+    if tall:
+        x = np.ascontiguousarray(x.T)
+    norm = bf16(np.float32(np.sqrt(np.sum(x.astype(np.float64) ** 2))))
+    norm = np.maximum(norm, np.float32(eps))
+    x = bf16(x / bf16(norm))
+    for a, b, c in schedule:
+        x64 = x.astype(np.float64)
+        gram = bf16((x64 @ x64.T).astype(np.float32))
+        g64 = gram.astype(np.float64)
+        upd = bf16((b * g64 + c * (g64 @ g64)).astype(np.float32))
+        x = bf16((a * x64 + upd.astype(np.float64) @ x64).astype(np.float32))
+    if tall:
+        x = np.ascontiguousarray(x.T)
+    return x
+
+
+def normuon(ortho, v, step: int, beta2: float = 0.95, eps: float = 1e-8):
+    """_normuon_normalize: gefen_muon.py:1192-1230.  Returns (new ortho (bf16
+    values), new v); `step` is the normuon step after this call's increment."""
+    o = bf16(ortho)
+    rows, cols = o.shape
+    row_norm = np.sqrt(np.sum(o.astype(np.float64) ** 2, axis=1)).astype(np.float32)
+    row_sq = (row_norm * row_norm).astype(np.float32)
+    v = np.asarray(v, np.float32).reshape(-1)
+    alpha = np.float32((1 - beta2) / cols)
+    v = (v * np.float32(beta2) + row_sq * alpha).astype(np.float32)
+    bc = np.float32(1 - beta2 ** step)
+    denom = (np.sqrt(v / bc) + np.float32(eps)).astype(np.float32)
+    frob = np.float32(np.sqrt(np.sum(row_sq.astype(np.float64))))
+    scaled = np.float32(np.sqrt(np.sum((row_norm / denom).astype(np.float64) ** 2)))
+    frob_scale = frob / max(scaled, np.float32(1.17549435e-38))
+    scale = bf16((frob_scale / denom).astype(np.float32))
+    return bf16(o * scale[:, None]), v
+
+
+def adjust_lr_ratio(fn, shape) -> float:
+    """_adjust_lr_ratio: gefen_muon.py:409-419."""
+    rows, cols = shape[:2]
+    if fn is None or fn == "original":
+        return math.sqrt(max(1, rows / cols))
+    if fn == "match_rms_adamw":
+        return 0.2 * math.sqrt(max(rows, cols))
+    return 1.0
+
+
+def muon_apply(p, update, dtype, lr: float, wd: float, adjusted_lr: float) -> np.ndarray:
+    """_apply_muon_update (non-capturable, unsharded): gefen_muon.py:1286-1300.
+    p <- D(p * (1 - lr*wd)) when wd > 0, then D(fma(update, alpha, p)) with
+    alpha = -adjusted_lr converted to p's dtype (torch's add_ converts `alpha`
+    to the tensor dtype; a `mul_` scalar stays fp32)."""
+    p = np.asarray(p, np.float32)
+    if wd > 0.0:
+        p = round_dtype((p * np.float32(1.0 - lr * wd)).astype(np.float32), dtype)
+    alpha = round_dtype(np.array([-adjusted_lr], np.float32), dtype)[0]
+    upd = np.asarray(update, np.float32).astype(np.float64)
+    res = (upd * np.float64(alpha) + p.astype(np.float64)).astype(np.float32)
+    return round_dtype(res, dtype)
 
 
 # -------------------------------------------------------------- step paths

@@ -15,6 +15,9 @@ Cases (each a separate file so they can be regenerated independently):
   step_<name>.npz  Gefen(fused=False).step trajectories  gefen.py:2784-3018, 3488-3818
   config1.npz      config-1 trajectory (4096x4096 fp32 + 4096 bias, 10 steps);
                    large arrays are stored as sha256 digests plus subsamples.
+  muon_ns.npz      _zeropower_via_newtonschulz on bf16 inputs gefen_muon.py:236-291
+  muon_<dt>.npz    GefenMuon(fused=False) trajectories         gefen_muon.py:2945-3030
+  hybrid_bf16.npz  GefenMuonHybrid(fused=False) trajectory      hybrid.py:693-776
 
 Usage:  python tests/golden/make_golden.py [case ...]   (default: all but config1)
 """
@@ -351,10 +354,144 @@ def case_config1():
     del ref
 
 
+# ------------------------------------------------------------------- Muon
+
+NS_CASES = {
+    # name: (shape, schedule)  schedule None = standard (a, b, c) x 5
+    "wide": ((48, 96), None),
+    "tall": ((96, 40), None),
+    "square": ((64, 64), "tuned3"),
+    "wide4": ((32, 80), "tuned4"),
+}
+
+
+def case_muon_ns():
+    """_zeropower_via_newtonschulz (gefen_muon.py:236-291) on bf16 inputs."""
+    _ref()
+    from gefen import gefen_muon as gm
+    out = {}
+    gen = torch.Generator().manual_seed(5)
+    for name, (shape, sched) in NS_CASES.items():
+        m = (torch.randn(*shape, generator=gen) * 1e-3).to(torch.bfloat16)
+        coeffs = (gm.DEFAULT_A, gm.DEFAULT_B, gm.DEFAULT_C) if sched is None else gm.NS_SCHEDULES[sched]
+        o = gm._zeropower_via_newtonschulz(m, coeffs, gm.DEFAULT_NS_STEPS, gm.EPS)
+        out["in_" + name] = _f32(m)
+        out["out_" + name] = _f32(o)
+        sch = gm._normalize_ns_schedule(coeffs, gm.DEFAULT_NS_STEPS)
+        out["abc_" + name] = np.array(sch, dtype=np.float64)
+    # zero input: the eps clamp keeps the output zero
+    z = torch.zeros(16, 24, dtype=torch.bfloat16)
+    out["in_zero"] = _f32(z)
+    out["out_zero"] = _f32(gm._zeropower_via_newtonschulz(
+        z, (gm.DEFAULT_A, gm.DEFAULT_B, gm.DEFAULT_C), gm.DEFAULT_NS_STEPS, gm.EPS))
+    _save("muon_ns.npz", **out)
+
+
+MUON_CASES = {
+    # name: (dtype, [(pname, shape, period)], kwargs, steps)
+    "muon_bf16": (torch.bfloat16, [("a", (48, 80), 80), ("b", (80, 48), 16)],
+                  dict(lr=0.02, weight_decay=0.1, momentum=0.95, nesterov=True), 4),
+    "muon_f32": (torch.float32, [("a", (40, 64), 64), ("b", (64, 40), 40)],
+                 dict(lr=0.02, weight_decay=0.1, momentum=0.9, nesterov=False,
+                      adjust_lr_fn="match_rms_adamw", normuon=True), 3),
+}
+
+
+def muon_case_inputs(name):
+    dtype, specs, kw, steps = MUON_CASES[name]
+    gen = torch.Generator().manual_seed(3)
+    params = [(pn, (torch.randn(*shape, generator=gen) * 0.02).to(dtype), per) for pn, shape, per in specs]
+    grads = []
+    for t in range(1, steps + 1):
+        gt = torch.Generator().manual_seed(2000 + t)
+        grads.append([(torch.randn(*shape, generator=gt) * 1e-3).to(dtype) for _, shape, _ in specs])
+    return dtype, params, grads, kw, steps
+
+
+def case_muon(name):
+    """GefenMuon(fused=False) trajectory on the CPU (gefen_muon.py:2945-3030)."""
+    _ref()
+    from gefen import GefenMuon
+    dtype, params, grads, kw, steps = muon_case_inputs(name)
+    cb = _golden_codebook()
+    ps = [(n, torch.nn.Parameter(t.clone())) for n, t, _ in params]
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        opt = GefenMuon(ps, fused=False, **kw)
+    opt._gefen_codebook = cb.clone()
+    for (n, t, per), (_, p) in zip(params, ps):
+        opt.state[p]["automatic_period"] = int(per)
+    out = {"codebook": _f32(cb)}
+    for n, t, per in params:
+        out["p0_" + n] = _f32(t)
+        out["period_" + n] = np.int64(per)
+    for s_, step_grads in enumerate(grads, start=1):
+        for (_, p), gv in zip(ps, step_grads):
+            p.grad = gv.clone()
+        opt.step()
+        for (n, p), gv in zip(ps, step_grads):
+            st = opt.state[p]
+            out["g%d_%s" % (s_, n)] = _f32(gv)
+            out["p%d_%s" % (s_, n)] = _f32(p.detach())
+            out["idx%d_%s" % (s_, n)] = st["m_codebook"].reshape(-1).numpy().copy()
+            out["mag%d_%s" % (s_, n)] = _f32(st["m_magnitude"]).reshape(-1)
+            if "normuon_v" in st:
+                out["nv%d_%s" % (s_, n)] = _f32(st["normuon_v"]).reshape(-1)
+    _save("%s.npz" % name, **out)
+
+
+def case_hybrid():
+    """GefenMuonHybrid(fused=False) with its defaults (hybrid.py:228-265):
+    two hidden matrices go to GefenMuon, an embedding and a norm vector to the
+    block-vmean Gefen backup."""
+    _ref()
+    from gefen import GefenMuonHybrid
+    gen = torch.Generator().manual_seed(4)
+    specs = [("layers.0.mlp.w", (40, 72), 72, True), ("layers.0.attn.o", (72, 40), 24, True),
+             ("embed_tokens.weight", (50, 16), 16, False), ("layers.0.norm.weight", (72,), 8, False)]
+    dtype = torch.bfloat16
+    tensors = {n: (torch.randn(*sh, generator=gen) * 0.02).to(dtype) for n, sh, _, _ in specs}
+    muon = [(n, torch.nn.Parameter(tensors[n].clone())) for n, _, _, m in specs if m]
+    backup = [(n, torch.nn.Parameter(tensors[n].clone())) for n, _, _, m in specs if not m]
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        opt = GefenMuonHybrid(muon, backup, lr=1e-3, weight_decay=0.01, fused=False)
+    cb = _golden_codebook()
+    opt.muon._gefen_codebook = cb.clone()
+    opt.backup._gefen_codebook = cb.clone()
+    named = dict(muon + backup)
+    for n, _, per, m in specs:
+        (opt.muon if m else opt.backup).state[named[n]]["automatic_period"] = int(per)
+    out = {"codebook": _f32(cb)}
+    for n, sh, per, m in specs:
+        out["p0_" + n] = _f32(tensors[n])
+        out["period_" + n] = np.int64(per)
+    for s_ in range(1, 4):
+        gt = torch.Generator().manual_seed(3000 + s_)
+        for n, sh, _, _ in specs:
+            gv = (torch.randn(*sh, generator=gt) * 1e-3).to(dtype)
+            named[n].grad = gv
+            out["g%d_%s" % (s_, n)] = _f32(gv)
+        opt.step()
+        for n, sh, per, m in specs:
+            st = (opt.muon if m else opt.backup).state[named[n]]
+            out["p%d_%s" % (s_, n)] = _f32(named[n].detach())
+            out["idx%d_%s" % (s_, n)] = st["m_codebook"].reshape(-1).numpy().copy()
+            out["mag%d_%s" % (s_, n)] = _f32(st["m_magnitude"]).reshape(-1)
+            for key in ("vmean", "normuon_v"):
+                if key in st:
+                    out["%s%d_%s" % (key, s_, n)] = _f32(st[key]).reshape(-1)
+    _save("hybrid_bf16.npz", **out)
+
+
 CASES = {"nearest": case_nearest, "lut": case_lut, "dp": case_dp,
          "learn": case_learn, "period": case_period, "config1": case_config1}
 for _n in STEP_CASES:
     CASES["step_" + _n] = (lambda n=_n: case_step(n))
+CASES["muon_ns"] = case_muon_ns
+for _n in MUON_CASES:
+    CASES[_n] = (lambda n=_n: case_muon(n))
+CASES["hybrid"] = case_hybrid
 
 
 def main(argv):
