@@ -40,7 +40,12 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float x) {
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short)h));
 }
+// The fp32 value reaches the conversion through an empty asm, so the compiler
+// cannot fold the fp32 op that produced it into a mixed-precision instruction
+// with a 16-bit result (v_fma_mixlo_f16 rounds once; the reference's torch ops
+// round to fp32, then to fp16, and the two differ on some inputs).
 __device__ __forceinline__ uint32_t f32_to_f16(float x) {
+    asm volatile("" : "+v"(x));
     return (uint32_t)__half_as_ushort(__float2half_rn(x));
 }
 

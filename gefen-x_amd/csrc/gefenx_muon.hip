@@ -1,0 +1,694 @@
+// gefenx_muon.hip -- the Muon half of the step on MI355X (gfx950):
+//
+//   momentum     advance the 8-bit quantised momentum of a 2D parameter by one
+//                EMA step and emit the dense momentum (optionally Nesterov)
+//                that Newton-Schulz orthogonalises.  Two passes: the block
+//                max of |u|, then requantise + emit (gefen_muon.py:1064-1146,
+//                948-974; every intermediate rounds to the grad dtype D, as
+//                the reference's tensors of dtype D do).
+//   newton-schulz  X = bf16(M) (transposed when tall), X /= max(||X||, eps),
+//                then per iteration G = XX^T, B = bG + cGG, X = aX + BX, each
+//                product rounded to bf16 (gefen_muon.py:236-291).  Every
+//                product is an "NT" GEMM C = A B^T with K contiguous in both
+//                operands: G = X X^T; GG = G G^T (G is symmetric); BX =
+//                B (X^T)^T -- so the kernel keeps X and X^T side by side and
+//                the X update writes both.  bf16 MFMA 32x32x16, fp32
+//                accumulation, LDS double buffering.
+//   normuon      per-row EMA of the mean square of the update, rescaled to
+//                keep the Frobenius norm (gefen_muon.py:1192-1230).
+//   apply        p = D(p * (1 - lr*wd)); p = D(fma(update, alpha, p)),
+//                alpha = D(-adjusted_lr) (gefen_muon.py:1286-1300).
+#include "gefenx_device.h"
+#include "gefenx_internal.h"
+#include "gefenx_profile.h"
+#include "../../include/gefenx.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace gx {
+namespace muon {
+
+constexpr int kT = 256;
+constexpr float kTiny = 1.17549435e-38f;
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+static int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GEFENX_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return GEFENX_OK;
+}
+
+// ==================================================================
+// Quantised momentum
+// ==================================================================
+struct MomArgs {
+    const void* g;
+    uint8_t* idx;
+    float* mag;       // m_magnitude (old on entry, new after finalize)
+    void* out;        // dense momentum, grad dtype
+    uint32_t* magbits;
+    float* mag_old;
+    float* minv;      // RN(1 / max(mag_new, tiny)) or 0 when unusable
+    const QTable* qt;
+    const int64_t* seed_dev;
+    int64_t N, P, nb, shards;
+    double invP;
+    uint64_t seed;
+    float w;          // (float)(1 - beta)
+    float beta;       // (float)beta
+    float alpha_d;    // D((float)(1 - beta)): torch's add_ alpha in the grad dtype
+    int nesterov, sr, dtype;
+};
+
+// u = D(lerp(D(D(c) * m_old), g, w)); cr already rounded through D.
+template <int DT>
+__device__ __forceinline__ float mom_u(float cr, float m_old, float g, float w) {
+    const float cm = round_dt<DT>(cr * m_old);
+    const float d = g - cm;
+    const float l = fabsf(w) < 0.5f ? __builtin_fmaf(w, d, cm) : __builtin_fmaf(w - 1.0f, d, g);
+    return round_dt<DT>(l);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_mom_max(MomArgs a) {
+    using T = typename Elem<DT>::T;
+    __shared__ float s_cbr[kCodebookMax];
+    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(a.qt->cbr + threadIdx.x);
+    __syncthreads();
+    const T* g = static_cast<const T*>(a.g);
+    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
+    const int64_t stride = (int64_t)gridDim.x * kT;
+    int64_t cur = -1;
+    uint32_t cbits = 0u;
+    float mo = 0.0f;
+    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < a.N; e += stride) {
+        const int64_t b = div_floor(e, a.P, a.invP);
+        if (b != cur) {
+            if (cur >= 0 && cbits) atomicMax(mb + cur, cbits);
+            cur = b;
+            cbits = 0u;
+            mo = *gbl(a.mag + b);
+        }
+        const float gv = to_f32<DT>(*gbl(g + e));
+        const float u = mom_u<DT>(s_cbr[*gbl(a.idx + e)], mo, gv, a.w);
+        const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;  // ordered: NaN > inf > finite
+        cbits = ub > cbits ? ub : cbits;
+    }
+    if (cur >= 0 && cbits) atomicMax(mb + cur, cbits);
+}
+
+__global__ void __launch_bounds__(kT) k_mom_finalize(MomArgs a) {
+    for (int64_t b = (int64_t)blockIdx.x * kT + threadIdx.x; b < a.nb; b += (int64_t)gridDim.x * kT) {
+        a.mag_old[b] = a.mag[b];
+        uint32_t bits = 0u;
+        for (int64_t sh = 0; sh < a.shards; ++sh) {
+            const uint32_t v = a.magbits[sh * a.nb + b];
+            bits = v > bits ? v : bits;
+            a.magbits[sh * a.nb + b] = 0u;
+        }
+        const float m = __uint_as_float(bits);
+        a.mag[b] = m;
+        a.minv[b] = block_recip(m < kTiny ? kTiny : m);
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_mom_emit(MomArgs a) {
+    using T = typename Elem<DT>::T;
+    __shared__ float s_cbr[kCodebookMax];
+    __shared__ float s_cb[kCodebookMax];
+    __shared__ int16_t s_lut[kLutEntries + 7];
+    const QTable* qt = a.qt;
+    for (int i = threadIdx.x; i < kCodebookMax; i += kT) {
+        s_cbr[i] = *gbl(qt->cbr + i);
+        s_cb[i] = *gbl(qt->cb + i);
+    }
+    if (a.sr)
+        for (int i = threadIdx.x; i < kLutEntries + 7; i += kT) s_lut[i] = *gbl(qt->lut + i);
+    __syncthreads();
+    uint64_t seed = a.seed;
+    if (a.sr && a.seed_dev != nullptr) seed = (uint64_t)*gbl(a.seed_dev);
+    const int k = qt->k;
+    const uint32_t kmax = (uint32_t)(k - 1);
+    const T* g = static_cast<const T*>(a.g);
+    T* out = static_cast<T*>(a.out);
+    const int64_t stride = (int64_t)gridDim.x * kT;
+    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < a.N; e += stride) {
+        const int64_t b = div_floor(e, a.P, a.invP);
+        const float m_old = *gbl(a.mag_old + b);
+        const float m_new = *gbl(a.mag + b);
+        const float y = *gbl(a.minv + b);
+        const float gv = to_f32<DT>(*gbl(g + e));
+        const float u = mom_u<DT>(s_cbr[*gbl(a.idx + e)], m_old, gv, a.w);
+        float x = 0.0f;
+        if (m_new > 0.0f) {
+            const float den = m_new < kTiny ? kTiny : m_new;
+            x = round_dt<DT>(div_by_block(u, den, y));
+        } else if (m_new != m_new) {
+            x = u / m_new;  // NaN magnitude: NaN (masked_fill only zeroes mag <= 0)
+        }
+        uint32_t ni;
+        if (a.sr) ni = quant_stochastic(x, s_cb, s_lut, k, seed, e);
+        else ni = quant_nearest(x, qt->bucket, qt->thr, kmax);
+        *gbl(a.idx + e) = (uint8_t)ni;
+        float o = round_dt<DT>(s_cbr[ni] * m_new);
+        if (a.nesterov) o = round_dt<DT>(__builtin_fmaf(a.alpha_d, gv, round_dt<DT>(o * a.beta)));
+        *gbl(out + e) = from_f32<DT>(o);
+    }
+}
+
+// ==================================================================
+// NT GEMM on bf16 MFMA: D = bf16(alpha * (A B^T) + beta * Cin), optionally
+// also Dt = D^T.  A: M x K, B: N x K, both row-major (K contiguous);
+// Cin, D: M x N; Dt: N x M.  grid (ceil(N/128), ceil(M/128), batch).
+// ==================================================================
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kLds = kBK + 8;  // bf16 per LDS row: 80 B, spreads the 16-B MFMA operand reads over banks
+
+struct GemmArgs {
+    const uint16_t* A; int64_t lda, sA;   // sA: elements between batch items
+    const uint16_t* B; int64_t ldb, sB;
+    const uint16_t* C; int64_t ldc, sC;   // epilogue input (nullptr: none)
+    uint16_t* D; int64_t ldd, sD;
+    uint16_t* Dt; int64_t lddt, sDt;      // transposed copy of D (nullptr: none)
+    int64_t M, N, K;
+    float alpha, beta;
+    int vec;                              // 16-byte loads allowed (K, lda, ldb % 8 == 0, aligned)
+};
+
+__device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ uint16_t f2bf(float x) { return (uint16_t)f32_to_bf16(x); }
+
+// Load a 128 x 32 tile (rows r0.., k k0..) of a row-major bf16 matrix into
+// two 16-byte registers per thread; rows >= R or k >= K read as zero.
+__device__ __forceinline__ void gemm_load_tile(const uint16_t* __restrict__ base, int64_t ld, int64_t R,
+                                               int64_t K, int64_t r0, int64_t k0, bool vec, u32x4 v[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + i * kT;  // 512 chunks of 8 bf16
+        const int row = c >> 2;
+        const int kc = (c & 3) * 8;
+        const int64_t gr = r0 + row;
+        const int64_t gk = k0 + kc;
+        if (vec) {
+            if (gr < R && gk < K) v[i] = *gbl(reinterpret_cast<const u32x4*>(base + gr * ld + gk));
+            else v[i] = u32x4{0u, 0u, 0u, 0u};
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t lo = (gr < R && gk + 2 * j < K) ? *gbl(base + gr * ld + gk + 2 * j) : 0u;
+                const uint32_t hi = (gr < R && gk + 2 * j + 1 < K) ? *gbl(base + gr * ld + gk + 2 * j + 1) : 0u;
+                w[j] = lo | (hi << 16);
+            }
+            v[i] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+__device__ __forceinline__ void gemm_store_tile(uint16_t* __restrict__ s, const u32x4 v[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + i * kT;
+        const int row = c >> 2;
+        const int kc = (c & 3) * 8;
+        *reinterpret_cast<u32x4*>(s + row * kLds + kc) = v[i];
+    }
+}
+
+__global__ void __launch_bounds__(kT) k_gemm_nt(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][kBM * kLds];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][kBN * kLds];
+    const int64_t bz = blockIdx.z;
+    const uint16_t* A = g.A + bz * g.sA;
+    const uint16_t* B = g.B + bz * g.sB;
+    const int64_t m0 = (int64_t)blockIdx.y * kBM;
+    const int64_t n0 = (int64_t)blockIdx.x * kBN;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;   // 2 x 2 waves, 64 x 64 each
+    const int l32 = lane & 31, lhi = lane >> 5;
+    const bool vec = g.vec != 0;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int64_t nk = cdiv(g.K, kBK);
+    u32x4 ra[2], rb[2];
+    gemm_load_tile(A, g.lda, g.M, g.K, m0, 0, vec, ra);
+    gemm_load_tile(B, g.ldb, g.N, g.K, n0, 0, vec, rb);
+    gemm_store_tile(sA[0], ra);
+    gemm_store_tile(sB[0], rb);
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int cur = (int)(kt & 1);
+        if (kt + 1 < nk) {
+            gemm_load_tile(A, g.lda, g.M, g.K, m0, (kt + 1) * kBK, vec, ra);
+            gemm_load_tile(B, g.ldb, g.N, g.K, n0, (kt + 1) * kBK, vec, rb);
+        }
+        const uint16_t* a_s = sA[cur];
+        const uint16_t* b_s = sB[cur];
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            bf16x8 av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = wm * 64 + i * 32 + l32;
+                av[i] = *reinterpret_cast<const bf16x8*>(a_s + row * kLds + ks * 16 + lhi * 8);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = wn * 64 + j * 32 + l32;
+                bv[j] = *reinterpret_cast<const bf16x8*>(b_s + col * kLds + ks * 16 + lhi * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) {
+            gemm_store_tile(sA[cur ^ 1], ra);
+            gemm_store_tile(sB[cur ^ 1], rb);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: lane holds D[row][col], col = l32, row = (r/4)*8 + lhi*4 + r%4
+    const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
+    uint16_t* D = g.D + bz * g.sD;
+    uint16_t* Dt = g.Dt ? g.Dt + bz * g.sDt : nullptr;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t col = n0 + wn * 64 + j * 32 + l32;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint16_t hv[4];
+                const int64_t rbase = m0 + wm * 64 + i * 32 + q * 8 + lhi * 4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t row = rbase + e;
+                    float v = g.alpha * acc[i][j][q * 4 + e];
+                    if (C != nullptr && row < g.M && col < g.N) v = __builtin_fmaf(g.beta, bf16f(*gbl(C + row * g.ldc + col)), v);
+                    hv[e] = f2bf(v);
+                    if (row < g.M && col < g.N) *gbl(D + row * g.ldd + col) = hv[e];
+                }
+                if (Dt != nullptr && col < g.N) {
+                    uint16_t* dst = Dt + col * g.lddt + rbase;
+                    if (rbase + 3 < g.M && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+                        const u32x2 pk = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
+                        *gbl(reinterpret_cast<u32x2*>(dst)) = pk;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (rbase + e < g.M) *gbl(Dt + col * g.lddt + rbase + e) = hv[e];
+                    }
+                }
+            }
+        }
+    }
+}
+
+static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
+    if (g.M <= 0 || g.N <= 0 || batch <= 0) return GEFENX_OK;
+    GemmArgs a = g;
+    const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    a.vec = (g.K % 8 == 0) && (g.lda % 8 == 0) && (g.ldb % 8 == 0) && (g.sA % 8 == 0) && (g.sB % 8 == 0) &&
+            al(g.A) && al(g.B);
+    const dim3 grid((unsigned)cdiv(g.N, kBN), (unsigned)cdiv(g.M, kBM), (unsigned)batch);
+    hipLaunchKernelGGL(k_gemm_nt, grid, dim3(kT), 0, s, a);
+    return launch_check("newton-schulz gemm");
+}
+
+// ==================================================================
+// Newton-Schulz driver kernels
+// ==================================================================
+// X (m x n) and Xt (n x m) from the input [R x C] of any grad dtype, values
+// rounded to bf16 (Tensor.bfloat16()); tall inputs (R > C) are transposed:
+// m = min(R, C), n = max(R, C).
+template <int DT>
+__global__ void __launch_bounds__(kT) k_ns_load(const void* in, int64_t R, int64_t Cc, int64_t s_in,
+                                                uint16_t* X, uint16_t* Xt, int64_t sX) {
+    using T = typename Elem<DT>::T;
+    const int64_t bz = blockIdx.y;
+    const T* src = static_cast<const T*>(in) + bz * s_in;
+    uint16_t* x = X + bz * sX;
+    uint16_t* xt = Xt + bz * sX;
+    const bool tall = R > Cc;
+    const int64_t m = tall ? Cc : R, n = tall ? R : Cc;
+    const int64_t N = R * Cc;
+    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
+        const int64_t r = e / Cc, c = e - (e / Cc) * Cc;
+        const uint16_t h = f2bf(to_f32<DT>(*gbl(src + e)));
+        // element (r, c) of the input is X[r][c] (wide) or X[c][r] (tall)
+        const int64_t i = tall ? c : r, j = tall ? r : c;
+        *gbl(x + i * n + j) = h;
+        *gbl(xt + j * m + i) = h;
+    }
+}
+
+// Partial sums of squares of X (float64), one per workgroup.
+__global__ void __launch_bounds__(kT) k_ns_sumsq(const uint16_t* X, int64_t N, int64_t sX, double* part) {
+    __shared__ double s_w[kT / 64];
+    const int64_t bz = blockIdx.y;
+    const uint16_t* x = X + bz * sX;
+    double acc = 0.0;
+    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
+        const float v = bf16f(*gbl(x + e));
+        acc += (double)(v * v);
+    }
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < kT / 64; ++w) t += s_w[w];
+        part[bz * gridDim.x + blockIdx.x] = t;
+    }
+}
+
+// den = max(bf16(||X||), eps) per matrix (Tensor.norm of bf16 returns bf16).
+__global__ void k_ns_norm(const double* part, int nparts, int64_t batch, float eps, float* den) {
+    const int64_t bz = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (bz >= batch) return;
+    double t = 0.0;
+    for (int i = 0; i < nparts; ++i) t += part[bz * nparts + i];
+    const float nb = bf16f(f2bf((float)sqrt(t)));
+    den[bz] = nb < eps ? bf16f(f2bf(eps)) : nb;
+}
+
+// X <- bf16(X / den) and Xt likewise.
+__global__ void __launch_bounds__(kT) k_ns_scale(uint16_t* X, uint16_t* Xt, int64_t N, int64_t sX, const float* den) {
+    const int64_t bz = blockIdx.y;
+    const float d = den[bz];
+    uint16_t* x = X + bz * sX;
+    uint16_t* xt = Xt + bz * sX;
+    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
+        *gbl(x + e) = f2bf(bf16f(*gbl(x + e)) / d);
+        *gbl(xt + e) = f2bf(bf16f(*gbl(xt + e)) / d);
+    }
+}
+
+// out [R x C] (bf16) from the final X / Xt.
+__global__ void __launch_bounds__(kT) k_ns_store(const uint16_t* src, int64_t N, int64_t sX, uint16_t* out, int64_t s_out) {
+    const int64_t bz = blockIdx.y;
+    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT)
+        *gbl(out + bz * s_out + e) = *gbl(src + bz * sX + e);
+}
+
+struct NsWs {
+    size_t off_x, off_xt0, off_xt1, off_g, off_b, off_part, off_den, total;
+    static constexpr int kParts = 256;
+    static NsWs make(int64_t batch, int64_t R, int64_t C) {
+        const int64_t m = std::min(R, C), n = std::max(R, C);
+        NsWs w;
+        size_t o = 0;
+        const size_t mn = align256(sizeof(uint16_t) * (size_t)(batch * m * n));
+        const size_t mm = align256(sizeof(uint16_t) * (size_t)(batch * m * m));
+        w.off_x = o; o += mn;
+        w.off_xt0 = o; o += mn;
+        w.off_xt1 = o; o += mn;
+        w.off_g = o; o += mm;
+        w.off_b = o; o += mm;
+        w.off_part = o; o += align256(sizeof(double) * (size_t)(batch * kParts));
+        w.off_den = o; o += align256(sizeof(float) * (size_t)batch);
+        w.total = o;
+        return w;
+    }
+};
+
+// ==================================================================
+// NorMuon and the Muon apply
+// ==================================================================
+// row_norm[r] = sqrt(sum_c u[r][c]^2) in fp32 from float64 partial sums
+// (torch.linalg.vector_norm(..., dtype=float32)); one wave per row.
+__global__ void __launch_bounds__(kT) k_row_norm(const uint16_t* U, int64_t R, int64_t C, float* row_norm) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * (kT / 64) + (threadIdx.x >> 6);
+    if (r >= R) return;
+    double acc = 0.0;
+    for (int64_t c = lane; c < C; c += 64) {
+        const float v = bf16f(*gbl(U + r * C + c));
+        acc += (double)(v * v);
+    }
+    acc = wave_sum_d(acc);
+    if (lane == 0) row_norm[r] = (float)sqrt(acc);
+}
+
+// v <- v*beta2 + row_sq * ((1-beta2)/C); denom = sqrt(v/bc) + eps;
+// frob_scale = sqrt(sum row_sq) / max(||row_norm / denom||, tiny);
+// scale[r] = bf16(frob_scale / denom[r]).  One workgroup.
+__global__ void __launch_bounds__(kT) k_normuon_scale(const float* row_norm, float* v, int64_t R, float beta2,
+                                                      float alpha, float bc, float eps, float* denom,
+                                                      uint16_t* scale) {
+    __shared__ double s_a[kT / 64], s_b[kT / 64];
+    double sa = 0.0, sb = 0.0;
+    for (int64_t r = threadIdx.x; r < R; r += kT) {
+        const float rn = row_norm[r];
+        const float rs = rn * rn;
+        const float nv = __builtin_fmaf(rs, alpha, v[r] * beta2);
+        v[r] = nv;
+        const float d = sqrtf(nv / bc) + eps;
+        denom[r] = d;
+        const float q = rn / d;
+        sa += (double)rs;
+        sb += (double)(q * q);
+    }
+    sa = wave_sum_d(sa);
+    sb = wave_sum_d(sb);
+    if ((threadIdx.x & 63) == 0) { s_a[threadIdx.x >> 6] = sa; s_b[threadIdx.x >> 6] = sb; }
+    __syncthreads();
+    double ta = 0.0, tb = 0.0;
+    for (int w = 0; w < kT / 64; ++w) { ta += s_a[w]; tb += s_b[w]; }
+    const float num = sqrtf((float)ta);
+    float den = sqrtf((float)tb);
+    den = den < kTiny ? kTiny : den;
+    const float fs = num / den;
+    for (int64_t r = threadIdx.x; r < R; r += kT) scale[r] = f2bf(fs / denom[r]);
+}
+
+// p = D(p * wdf) (when wd); p = D(fma(u', alpha, p)), u' = bf16(u * scale[row])
+// when a NorMuon scale is given, else u.
+template <int DT>
+__global__ void __launch_bounds__(kT) k_muon_apply(void* p, const uint16_t* U, const uint16_t* scale, int64_t R,
+                                                   int64_t C, float wdf, int wd, float alpha) {
+    using T = typename Elem<DT>::T;
+    T* pp = static_cast<T*>(p);
+    const int64_t N = R * C;
+    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
+        float u = bf16f(*gbl(U + e));
+        if (scale != nullptr) u = bf16f(f2bf(u * bf16f(*gbl(scale + e / C))));
+        float pv = to_f32<DT>(*gbl(pp + e));
+        if (wd) pv = round_dt<DT>(pv * wdf);
+        *gbl(pp + e) = from_f32<DT>(__builtin_fmaf(u, alpha, pv));
+    }
+}
+
+static unsigned grid_for(int64_t n, int64_t cap = 8192) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(cap, cdiv(n, kT)));
+}
+
+static int check_dt(int dtype, const char* fn) {
+    if (dtype == F64) return set_error(GEFENX_EDTYPE, "%s: not implemented for 'Double'", fn);
+    if (dtype != F32 && dtype != F16 && dtype != BF16) return set_error(GEFENX_EINVAL, "%s: unknown dtype %d", fn, dtype);
+    return GEFENX_OK;
+}
+
+}  // namespace muon
+}  // namespace gx
+
+using namespace gx;
+using namespace gx::muon;
+
+extern "C" {
+
+int gefenx_quantized_momentum_update(const void* grad, int dtype, int64_t numel, int64_t period,
+                                     uint8_t* m_codebook, float* m_magnitude, const void* qtable_dev,
+                                     void* momentum_out, double beta1, int stochastic_round, int64_t rng_seed,
+                                     const int64_t* seed_dev, int nesterov, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+    int rc = check_dt(dtype, "gefenx_quantized_momentum_update");
+    if (rc) return rc;
+    if (numel < 0) return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: negative numel");
+    if (numel == 0) return GEFENX_OK;
+    if (period <= 0 || numel % period != 0)
+        return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: period %lld does not divide numel %lld",
+                         (long long)period, (long long)numel);
+    if (!grad || !m_codebook || !m_magnitude || !qtable_dev || !momentum_out || !workspace)
+        return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: null pointer argument");
+    const int64_t nb = numel / period;
+    const MomentumWs L = MomentumWs::make(nb);
+    if (workspace_bytes < L.total)
+        return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: workspace %zu bytes < required %zu",
+                         workspace_bytes, L.total);
+    char* ws = static_cast<char*>(workspace);
+    MomArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.g = grad; a.idx = m_codebook; a.mag = m_magnitude; a.out = momentum_out;
+    a.magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
+    a.mag_old = reinterpret_cast<float*>(ws + L.off_magold);
+    a.minv = reinterpret_cast<float*>(ws + L.off_minv);
+    a.qt = static_cast<const QTable*>(qtable_dev);
+    a.seed_dev = seed_dev;
+    a.N = numel; a.P = period; a.nb = nb; a.shards = mag_shards(nb); a.invP = 1.0 / (double)period;
+    a.seed = (uint64_t)rng_seed;
+    a.w = (float)(1.0 - beta1);
+    a.beta = (float)beta1;
+    a.alpha_d = dtype == BF16 ? round_bf16(a.w) : dtype == F16 ? round_f16(a.w) : a.w;
+    a.nesterov = nesterov ? 1 : 0;
+    a.sr = stochastic_round ? 1 : 0;
+    a.dtype = dtype;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const unsigned grid = grid_for(numel, 16384);
+    int ph = prof_begin(GEFENX_K_MOMENTUM, (double)numel * (dtype == F32 ? 12.0 : 6.0), 0.0, s);
+    switch (dtype) {
+        case F32: hipLaunchKernelGGL(k_mom_max<F32>, dim3(grid), dim3(kT), 0, s, a); break;
+        case F16: hipLaunchKernelGGL(k_mom_max<F16>, dim3(grid), dim3(kT), 0, s, a); break;
+        default: hipLaunchKernelGGL(k_mom_max<BF16>, dim3(grid), dim3(kT), 0, s, a); break;
+    }
+    hipLaunchKernelGGL(k_mom_finalize, dim3(grid_for(nb, 4096)), dim3(kT), 0, s, a);
+    switch (dtype) {
+        case F32: hipLaunchKernelGGL(k_mom_emit<F32>, dim3(grid), dim3(kT), 0, s, a); break;
+        case F16: hipLaunchKernelGGL(k_mom_emit<F16>, dim3(grid), dim3(kT), 0, s, a); break;
+        default: hipLaunchKernelGGL(k_mom_emit<BF16>, dim3(grid), dim3(kT), 0, s, a); break;
+    }
+    prof_end(ph, s);
+    return launch_check("quantized momentum update");
+}
+
+size_t gefenx_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols) {
+    if (batch <= 0 || rows <= 0 || cols <= 0) return 256;
+    return NsWs::make(batch, rows, cols).total;
+}
+
+int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch, int64_t rows, int64_t cols,
+                         const double* abc, int steps, double eps, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+    int rc = check_dt(in_dtype, "gefenx_newton_schulz");
+    if (rc) return rc;
+    if (batch < 0 || rows < 0 || cols < 0 || steps < 0 || (steps > 0 && !abc))
+        return set_error(GEFENX_EINVAL, "gefenx_newton_schulz: bad shape or schedule");
+    if (batch == 0 || rows == 0 || cols == 0) return GEFENX_OK;
+    if (!in || !out || !workspace) return set_error(GEFENX_EINVAL, "gefenx_newton_schulz: null pointer argument");
+    const NsWs L = NsWs::make(batch, rows, cols);
+    if (workspace_bytes < L.total)
+        return set_error(GEFENX_EINVAL, "gefenx_newton_schulz: workspace %zu bytes < required %zu", workspace_bytes,
+                         L.total);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    uint16_t* X = reinterpret_cast<uint16_t*>(ws + L.off_x);
+    uint16_t* Xt[2] = {reinterpret_cast<uint16_t*>(ws + L.off_xt0), reinterpret_cast<uint16_t*>(ws + L.off_xt1)};
+    uint16_t* G = reinterpret_cast<uint16_t*>(ws + L.off_g);
+    uint16_t* Bm = reinterpret_cast<uint16_t*>(ws + L.off_b);
+    double* part = reinterpret_cast<double*>(ws + L.off_part);
+    float* den = reinterpret_cast<float*>(ws + L.off_den);
+    const int64_t m = std::min(rows, cols), n = std::max(rows, cols);
+    const int64_t N = m * n;
+    const bool tall = rows > cols;
+    const dim3 g2(grid_for(N, 4096), (unsigned)batch);
+    switch (in_dtype) {
+        case F32: hipLaunchKernelGGL(k_ns_load<F32>, g2, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
+        case F16: hipLaunchKernelGGL(k_ns_load<F16>, g2, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
+        default: hipLaunchKernelGGL(k_ns_load<BF16>, g2, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
+    }
+    hipLaunchKernelGGL(k_ns_sumsq, dim3(NsWs::kParts, (unsigned)batch), dim3(kT), 0, s, X, N, N, part);
+    hipLaunchKernelGGL(k_ns_norm, dim3((unsigned)cdiv(batch, 64)), dim3(64), 0, s, part, NsWs::kParts, batch,
+                       (float)eps, den);
+    hipLaunchKernelGGL(k_ns_scale, g2, dim3(kT), 0, s, X, Xt[0], N, N, den);
+    rc = launch_check("newton-schulz prologue");
+    if (rc) return rc;
+    int cur = 0;
+    const double flops_iter = 2.0 * (double)batch * ((double)m * m * n * 2.0 + (double)m * m * m);
+    for (int it = 0; it < steps; ++it) {
+        const float a = (float)abc[3 * it], b = (float)abc[3 * it + 1], c = (float)abc[3 * it + 2];
+        int ph = prof_begin(GEFENX_K_NS_GEMM, 0.0, flops_iter, s);
+        // G = X X^T
+        GemmArgs g1{X, n, N, X, n, N, nullptr, 0, 0, G, m, m * m, nullptr, 0, 0, m, m, n, 1.0f, 0.0f, 0};
+        rc = gemm_nt(g1, batch, s);
+        // B = b G + c G G^T
+        GemmArgs gg{G, m, m * m, G, m, m * m, G, m, m * m, Bm, m, m * m, nullptr, 0, 0, m, m, m, c, b, 0};
+        if (!rc) rc = gemm_nt(gg, batch, s);
+        // X = a X + B X  (B operand X^T), X^T of the result into the other buffer
+        GemmArgs gx{Bm, m, m * m, Xt[cur], m, N, X, n, N, X, n, N, Xt[cur ^ 1], m, N, m, n, m, 1.0f, a, 0};
+        if (!rc) rc = gemm_nt(gx, batch, s);
+        prof_end(ph, s);
+        if (rc) return rc;
+        cur ^= 1;
+    }
+    // result in the input's orientation: X (wide) or X^T (tall)
+    hipLaunchKernelGGL(k_ns_store, g2, dim3(kT), 0, s, tall ? Xt[cur] : X, N, N, static_cast<uint16_t*>(out), N);
+    return launch_check("newton-schulz epilogue");
+}
+
+int gefenx_normuon_scale(const void* update, int64_t rows, int64_t cols, float* normuon_v, double beta2,
+                         int64_t step, double eps, void* scale_out, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+    if (rows <= 0 || cols <= 0) return GEFENX_OK;
+    if (!update || !normuon_v || !scale_out || !workspace || step < 1)
+        return set_error(GEFENX_EINVAL, "gefenx_normuon_scale: bad argument");
+    const size_t need = 2 * align256(sizeof(float) * (size_t)rows);
+    if (workspace_bytes < need)
+        return set_error(GEFENX_EINVAL, "gefenx_normuon_scale: workspace %zu bytes < required %zu", workspace_bytes, need);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    float* row_norm = static_cast<float*>(workspace);
+    float* denom = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(sizeof(float) * (size_t)rows));
+    hipLaunchKernelGGL(k_row_norm, dim3((unsigned)cdiv(rows, kT / 64)), dim3(kT), 0, s,
+                       static_cast<const uint16_t*>(update), rows, cols, row_norm);
+    const float alpha = (float)((1.0 - beta2) / (double)cols);
+    const float bc = (float)(1.0 - std::pow(beta2, (double)step));
+    hipLaunchKernelGGL(k_normuon_scale, dim3(1), dim3(kT), 0, s, row_norm, normuon_v, rows, (float)beta2, alpha, bc,
+                       (float)eps, denom, static_cast<uint16_t*>(scale_out));
+    return launch_check("normuon scale");
+}
+
+size_t gefenx_normuon_workspace_bytes(int64_t rows) {
+    return 2 * align256(sizeof(float) * (size_t)(rows > 0 ? rows : 1));
+}
+
+int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_scale, int64_t rows, int64_t cols,
+                      double lr, double weight_decay, double adjusted_lr, void* stream) {
+    int rc = check_dt(dtype, "gefenx_muon_apply");
+    if (rc) return rc;
+    if (rows <= 0 || cols <= 0) return GEFENX_OK;
+    if (!p || !update) return set_error(GEFENX_EINVAL, "gefenx_muon_apply: null pointer argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const float wdf = (float)(1.0 - lr * weight_decay);
+    const int wd = weight_decay > 0.0 ? 1 : 0;
+    float alpha = (float)(-adjusted_lr);
+    alpha = dtype == BF16 ? round_bf16(alpha) : dtype == F16 ? round_f16(alpha) : alpha;
+    const unsigned grid = grid_for(rows * cols, 16384);
+    const uint16_t* u = static_cast<const uint16_t*>(update);
+    const uint16_t* sc = static_cast<const uint16_t*>(row_scale);
+    switch (dtype) {
+        case F32: hipLaunchKernelGGL(k_muon_apply<F32>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha); break;
+        case F16: hipLaunchKernelGGL(k_muon_apply<F16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha); break;
+        default: hipLaunchKernelGGL(k_muon_apply<BF16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha); break;
+    }
+    return launch_check("muon apply");
+}
+
+int gefenx_gemm_nt_bf16(const void* A, const void* B, const void* C, void* D, int64_t M, int64_t N, int64_t K,
+                        float alpha, float beta, void* stream) {
+    if (M < 0 || N < 0 || K < 0) return set_error(GEFENX_EINVAL, "gefenx_gemm_nt_bf16: negative shape");
+    if (M == 0 || N == 0) return GEFENX_OK;
+    if (!A || !B || !D) return set_error(GEFENX_EINVAL, "gefenx_gemm_nt_bf16: null pointer argument");
+    GemmArgs g{static_cast<const uint16_t*>(A), K, 0, static_cast<const uint16_t*>(B), K, 0,
+               static_cast<const uint16_t*>(C), N, 0, static_cast<uint16_t*>(D), N, 0, nullptr, 0, 0,
+               M, N, K, alpha, beta, 0};
+    return gemm_nt(g, 1, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

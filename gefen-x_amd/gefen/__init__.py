@@ -2,9 +2,13 @@
 
 Drop-in for the reference package's public surface (src/gefen/__init__.py):
 the optimizer classes keep their constructor arguments, param-group layout and
-state_dict format; the fused step runs hand-written gfx950 HIP kernels through
-the C ABI in include/gefenx.h.
+state_dict format; the step runs hand-written gfx950 HIP kernels through the C
+ABI in include/gefenx.h.
 """
 from gefen.gefen import Gefen
+from gefen.gefen_muon import GefenMuon
+from gefen.hybrid import GefenMuonHybrid
+from gefen.params import DEFAULT_BACKUP_SUBSTRINGS, is_muon_param, split_params_for_muon, validate_split
 
-__all__ = ["Gefen"]
+__all__ = ["Gefen", "GefenMuon", "GefenMuonHybrid", "split_params_for_muon", "validate_split", "is_muon_param",
+           "DEFAULT_BACKUP_SUBSTRINGS"]

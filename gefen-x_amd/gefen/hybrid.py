@@ -1,0 +1,292 @@
+"""GefenMuonHybrid: GefenMuon for the 2D hidden matrices, a plain Gefen
+(block-shared second moment) or torch AdamW backup for everything else.
+
+Drop-in for the reference class (hybrid.py:202-1053): same constructor forms
+(two named lists, a model, or one named-parameter iterable), the same
+defaults (tuned 3-step Newton-Schulz, match_rms_adamw, NorMuon), the same
+composite state_dict {"muon", "backup", "backup_optimizer"}.  The backup steps
+first, then Muon (hybrid.py:760-776).
+"""
+from __future__ import annotations
+
+import warnings
+from collections.abc import Mapping
+from typing import Iterable
+
+import torch
+import torch.nn as nn
+
+from gefen.gefen import Gefen
+from gefen.gefen_muon import GefenMuon
+from gefen.params import DEFAULT_BACKUP_SUBSTRINGS, split_params_for_muon, validate_split
+
+
+class _StateView(Mapping):
+    """Read view of the children's per-parameter state, keyed by parameter."""
+
+    def __init__(self, owner):
+        self._owner = owner
+
+    def _child(self, p):
+        entry = self._owner._state_param_owner.get(id(p))
+        if entry is None:
+            raise KeyError(p)
+        return entry[1]
+
+    def __getitem__(self, p):
+        return self._child(p).state[p]
+
+    def __iter__(self):
+        for o in self._owner._subopts:
+            yield from o.state
+
+    def __len__(self):
+        return sum(len(o.state) for o in self._owner._subopts)
+
+
+class GefenMuonHybrid(torch.optim.Optimizer):
+    """Hybrid Muon + Gefen optimizer (hybrid.py:228-265 arguments)."""
+
+    def __init__(
+        self,
+        muon_named_params,
+        backup_named_params=None,
+        *,
+        lr,
+        backup_substrings=None,
+        muon_lr=None,
+        backup_lr=None,
+        backup_optimizer="gefen",
+        weight_decay=0.0,
+        muon_weight_decay=None,
+        backup_weight_decay=None,
+        no_decay_substrings=(),
+        backup_1d_period_one=False,
+        backup_2d_period_one=False,
+        betas=(0.9, 0.999),
+        eps=1e-8,
+        fused=True,
+        momentum=0.95,
+        nesterov=True,
+        ns_steps=5,
+        ns_schedule="tuned3",
+        adjust_lr_fn="match_rms_adamw",
+        sharded_mode="exact",
+        fp8_ns=False,
+        fp8_ns_compile=True,
+        batched_ns=False,
+        batched_ns_workspace_bytes=256 << 20,
+        stochastic_round=False,
+        deterministic=False,
+        normuon=True,
+        normuon_beta2=0.95,
+        normuon_eps=1e-8,
+        cautious=False,
+        capturable=False,
+        verbose=False,
+    ):
+        if not isinstance(deterministic, bool):
+            raise TypeError("deterministic must be a bool")
+        self._deterministic = deterministic
+        self.capturable = capturable
+        if backup_named_params is None:
+            muon_named_params, backup_named_params = self._auto_split(muon_named_params, backup_substrings)
+        elif backup_substrings is not None:
+            raise TypeError("backup_substrings is only valid with the single-argument (model / named-params) "
+                            "form; you also passed backup_named_params.")
+        muon_named_params = list(muon_named_params)
+        backup_named_params = list(backup_named_params)
+        if not muon_named_params and not backup_named_params:
+            raise ValueError("GefenMuonHybrid received no parameters to optimize")
+        if backup_optimizer not in ("gefen", "adamw"):
+            raise ValueError("backup_optimizer must be 'gefen' or 'adamw' but is: {!r}".format(backup_optimizer))
+        self.backup_optimizer = backup_optimizer
+        validate_split(muon_named_params, backup_named_params)
+        if adjust_lr_fn in (None, "original"):
+            warnings.warn(
+                "GefenMuonHybrid: adjust_lr_fn={!r} uses Muon-native LR scaling, so an AdamW-scale lr will "
+                "mis-scale the 2D Muon matrices relative to the backup half. Use adjust_lr_fn='match_rms_adamw' "
+                "(the default) to share one AdamW-scale lr, or set muon_lr explicitly.".format(adjust_lr_fn),
+                stacklevel=2)
+        muon_lr = lr if muon_lr is None else muon_lr
+        backup_lr = lr if backup_lr is None else backup_lr
+        muon_weight_decay = weight_decay if muon_weight_decay is None else muon_weight_decay
+        backup_weight_decay = weight_decay if backup_weight_decay is None else backup_weight_decay
+        self.muon = GefenMuon(
+            muon_named_params, lr=muon_lr, weight_decay=muon_weight_decay, momentum=momentum, nesterov=nesterov,
+            ns_steps=ns_steps, ns_schedule=ns_schedule, adjust_lr_fn=adjust_lr_fn, fused=fused,
+            sharded_mode=sharded_mode, fp8_ns=fp8_ns, fp8_ns_compile=fp8_ns_compile, batched_ns=batched_ns,
+            batched_ns_workspace_bytes=batched_ns_workspace_bytes, stochastic_round=stochastic_round,
+            deterministic=deterministic, normuon=normuon, normuon_beta2=normuon_beta2, normuon_eps=normuon_eps,
+            cautious=cautious, capturable=capturable, verbose=verbose) if muon_named_params else None
+        no_decay_substrings = tuple(s.lower() for s in no_decay_substrings)
+
+        def _is_no_decay(name):
+            lname = name.lower()
+            return any(sub in lname for sub in no_decay_substrings)
+
+        if backup_named_params and no_decay_substrings:
+            decay = [(n, p) for n, p in backup_named_params if not _is_no_decay(n)]
+            no_decay = [(n, p) for n, p in backup_named_params if _is_no_decay(n)]
+            backup_groups = [g for g in (
+                {"params": decay, "lr": backup_lr, "betas": betas, "eps": eps, "weight_decay": backup_weight_decay}
+                if decay else None,
+                {"params": no_decay, "lr": backup_lr, "betas": betas, "eps": eps, "weight_decay": 0.0}
+                if no_decay else None) if g is not None]
+        else:
+            backup_groups = backup_named_params
+        if not backup_named_params:
+            self.backup = None
+        elif backup_optimizer == "gefen":
+            self.backup = Gefen(backup_groups, lr=backup_lr, betas=betas, eps=eps, weight_decay=backup_weight_decay,
+                                fused=fused, force_1d_period_one=backup_1d_period_one,
+                                force_2d_period_one=backup_2d_period_one, factored_v_2d=False,
+                                stochastic_round=stochastic_round, deterministic=deterministic,
+                                capturable=capturable, verbose=verbose)
+        else:
+            if no_decay_substrings:
+                adamw_groups = [{**{k: v for k, v in g.items() if k != "params"},
+                                 "params": [p for _, p in g["params"]], "param_names": [n for n, _ in g["params"]]}
+                                for g in backup_groups]
+            else:
+                adamw_groups = [{"params": [p for _, p in backup_groups], "param_names": [n for n, _ in backup_groups]}]
+            self.backup = torch.optim.AdamW(adamw_groups, lr=backup_lr, betas=betas, eps=eps,
+                                            weight_decay=backup_weight_decay, fused=fused, capturable=capturable)
+        self._subopts = [o for o in (self.muon, self.backup) if o is not None]
+        self._state_param_owner = {}
+        for o in self._subopts:
+            for group in o.param_groups:
+                for p in group["params"]:
+                    self._state_param_owner[id(p)] = (p, o)
+        # torch.optim.Optimizer.__init__ is not called: param_groups and state
+        # are the children's own (shared) objects, so an LR scheduler's in-place
+        # group["lr"] updates reach them.
+        self.defaults = self._subopts[0].defaults
+        from collections import OrderedDict
+        self._optimizer_step_pre_hooks = OrderedDict()
+        self._optimizer_step_post_hooks = OrderedDict()
+        self._optimizer_state_dict_pre_hooks = OrderedDict()
+        self._optimizer_state_dict_post_hooks = OrderedDict()
+        self._optimizer_load_state_dict_pre_hooks = OrderedDict()
+        self._optimizer_load_state_dict_post_hooks = OrderedDict()
+
+    # ------------------------------------------------------------ routing
+
+    @staticmethod
+    def _auto_split(params_or_model, backup_substrings):
+        """hybrid.py:968-1018."""
+        subs = DEFAULT_BACKUP_SUBSTRINGS if backup_substrings is None else tuple(backup_substrings)
+        if isinstance(params_or_model, nn.Module):
+            muon_named, backup_named = split_params_for_muon(params_or_model, backup_substrings=subs)
+            validate_split(muon_named, backup_named, model=params_or_model)
+            return muon_named, backup_named
+        items = list(params_or_model)
+        for item in items:
+            if not (isinstance(item, (tuple, list)) and len(item) == 2 and isinstance(item[0], str)):
+                raise TypeError("GefenMuonHybrid's single-argument form needs an nn.Module or (name, param) pairs "
+                                "(e.g. model.named_parameters()); bare tensors cannot be routed")
+        from gefen.params import is_muon_param
+        muon = [(n, p) for n, p in items if p.requires_grad and is_muon_param(n, p, subs)]
+        backup = [(n, p) for n, p in items if p.requires_grad and not is_muon_param(n, p, subs)]
+        return muon, backup
+
+    @classmethod
+    def from_model(cls, model, *, backup_substrings=None, **kwargs):
+        """hybrid.py:1021-1032."""
+        split_kwargs = {} if backup_substrings is None else {"backup_substrings": backup_substrings}
+        muon_named, backup_named = split_params_for_muon(model, **split_kwargs)
+        validate_split(muon_named, backup_named, model=model)
+        return cls(muon_named, backup_named, **kwargs)
+
+    def add_param_group(self, param_group):
+        raise NotImplementedError("GefenMuonHybrid splits params at construction; add_param_group is unsupported")
+
+    @property
+    def param_groups(self):
+        return [g for o in self._subopts for g in o.param_groups]
+
+    @param_groups.setter
+    def param_groups(self, value):
+        raise AttributeError("GefenMuonHybrid.param_groups is the children's groups and cannot be replaced")
+
+    @property
+    def state(self):
+        return _StateView(self)
+
+    @state.setter
+    def state(self, value):
+        raise AttributeError("GefenMuonHybrid.state is a view of the children's state")
+
+    def __repr__(self):
+        nm = sum(len(g["params"]) for g in self.muon.param_groups) if self.muon is not None else 0
+        nb = sum(len(g["params"]) for g in self.backup.param_groups) if self.backup is not None else 0
+        return "GefenMuonHybrid(muon={} params, backup={} params, backup_optimizer={!r})".format(
+            nm, nb, self.backup_optimizer)
+
+    # --------------------------------------------------------------- step
+
+    def zero_grad(self, set_to_none: bool = True):
+        for o in self._subopts:
+            o.zero_grad(set_to_none=set_to_none)
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        args = (self, closure) if closure is not None else (self,)
+        kwargs = {}
+        for pre_hook in self._optimizer_step_pre_hooks.values():
+            result = pre_hook(self, args, kwargs)
+            if result is not None:
+                args, kwargs = result
+        closure = args[1] if len(args) > 1 else kwargs.get("closure")
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        # validate every child before either mutates anything
+        for o in self._subopts:
+            if hasattr(o, "_validate_grads"):
+                o._validate_grads()
+        for o in self._subopts:
+            if o is not self.muon:
+                o.step()
+        if self.muon is not None:
+            self.muon.step()
+        for post_hook in self._optimizer_step_post_hooks.values():
+            post_hook(self, args, kwargs)
+        return loss
+
+    # --------------------------------------------------------- checkpoint
+
+    def state_dict(self):
+        """hybrid.py:778-793."""
+        for pre_hook in self._optimizer_state_dict_pre_hooks.values():
+            pre_hook(self)
+        sd = {"muon": self.muon.state_dict() if self.muon is not None else None,
+              "backup": self.backup.state_dict() if self.backup is not None else None,
+              "backup_optimizer": self.backup_optimizer}
+        for post_hook in self._optimizer_state_dict_post_hooks.values():
+            r = post_hook(self, sd)
+            if r is not None:
+                sd = r
+        return sd
+
+    def load_state_dict(self, state_dict):
+        """hybrid.py:795-920 (composite layout; each child loads its part)."""
+        state_dict = state_dict.copy()
+        for pre_hook in self._optimizer_load_state_dict_pre_hooks.values():
+            r = pre_hook(self, state_dict)
+            if r is not None:
+                state_dict = r
+        saved_backup = state_dict.get("backup_optimizer", self.backup_optimizer)
+        if saved_backup != self.backup_optimizer:
+            raise ValueError("checkpoint backup_optimizer {!r} does not match this hybrid's {!r}".format(
+                saved_backup, self.backup_optimizer))
+        for key, child in (("muon", self.muon), ("backup", self.backup)):
+            part = state_dict.get(key)
+            if (part is None) != (child is None):
+                raise ValueError("checkpoint {} half {} but this hybrid's is {}".format(
+                    key, "absent" if part is None else "present", "absent" if child is None else "present"))
+            if child is not None:
+                child.load_state_dict(part)
+        for post_hook in self._optimizer_load_state_dict_post_hooks.values():
+            post_hook(self)

@@ -126,6 +126,10 @@ int gefenx_block_update(
  * dense momentum (optionally Nesterov) in grad dtype.  Replaces
  * gefen_quantized_momentum_update_cuda
  * (kernels/automatic_gefen_fused_kernel.cu:2852-3027, binding :75-87).
+ * Arithmetic of the reference's decomposed Muon momentum
+ * (gefen_muon.py:1136-1144, 948-974): every intermediate rounds to the grad
+ * dtype D; Nesterov out = D(fma(D(1-beta), g, D(out*beta))).
+ * workspace: gefenx_workspace_bytes(GEFENX_WS_MOMENTUM, 0, 0, numel/period).
  * ---------------------------------------------------------------------- */
 int gefenx_quantized_momentum_update(
     const void* grad, int dtype, int64_t numel, int64_t period,
@@ -214,19 +218,44 @@ int gefenx_multi_tensor_step(const gefenx_tensor_desc* descs, int n,
 size_t gefenx_multi_tensor_scratch_bytes(int n);
 
 /* ------------------------------------------------------------------------
- * Newton-Schulz orthogonalisation of a batch of bf16 matrices on MFMA.
+ * Newton-Schulz orthogonalisation of a batch of matrices on bf16 MFMA.
  * Replaces _zeropower_via_newtonschulz / _zeropower_via_newtonschulz_batched
- * (gefen_muon.py:236-291, 353-393).  x: bf16 [batch, rows, cols] contiguous,
- * rows <= cols (callers transpose tall matrices), normalised in place by its
- * Frobenius norm, then `steps` quintic iterations with coefficients
- * (a[i], b[i], c[i]); the result overwrites x.  workspace: device bytes from
- * gefenx_ns_workspace_bytes.
+ * (gefen_muon.py:236-291, 353-393).  in: [batch, rows, cols] contiguous of
+ * in_dtype (the dense momentum); it is rounded to bf16, transposed when
+ * rows > cols, divided by max(bf16(||X||_F), eps), then for i < steps:
+ * G = XX^T, B = b_i G + c_i G G, X = a_i X + B X, each product rounded to
+ * bf16 (fp32 accumulation).  out: bf16 [batch, rows, cols] in the input's
+ * orientation.  abc: steps x (a, b, c) doubles.  workspace:
+ * gefenx_ns_workspace_bytes(batch, rows, cols) bytes (any contents).
  * ---------------------------------------------------------------------- */
 size_t gefenx_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols);
-int gefenx_newton_schulz(void* x, int64_t batch, int64_t rows, int64_t cols,
-                         const float* a, const float* b, const float* c, int steps,
-                         float eps, void* workspace, size_t workspace_bytes,
-                         void* stream);
+int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch, int64_t rows,
+                         int64_t cols, const double* abc, int steps, double eps, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* NorMuon row scale of a bf16 update [rows, cols] (gefen_muon.py:1192-1230):
+ * normuon_v (fp32 [rows], mutated) <- v*beta2 + row_sq*((1-beta2)/cols);
+ * scale_out (bf16 [rows]) = bf16(frob_scale / (sqrt(v/(1-beta2^step)) + eps)).
+ * workspace: gefenx_normuon_workspace_bytes(rows) bytes. */
+size_t gefenx_normuon_workspace_bytes(int64_t rows);
+int gefenx_normuon_scale(const void* update, int64_t rows, int64_t cols, float* normuon_v,
+                         double beta2, int64_t step, double eps, void* scale_out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Muon parameter update (gefen_muon.py:1286-1300): p = D(p*(1-lr*wd)) when
+ * weight_decay > 0, then p = D(fma(u, D(-adjusted_lr), p)) with u the bf16
+ * update [rows, cols], multiplied first by row_scale (bf16 [rows], NorMuon)
+ * and rounded to bf16 when row_scale is not NULL. */
+int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_scale,
+                      int64_t rows, int64_t cols, double lr, double weight_decay,
+                      double adjusted_lr, void* stream);
+
+/* The Newton-Schulz GEMM alone: D = bf16(alpha * A B^T + beta * C) for bf16
+ * row-major A [M, K], B [N, K], C / D [M, N] (C may be NULL).  No counterpart
+ * in the reference (its Newton-Schulz calls torch.matmul / addmm); exposed
+ * for testing and measuring the MFMA kernel. */
+int gefenx_gemm_nt_bf16(const void* A, const void* B, const void* C, void* D, int64_t M,
+                        int64_t N, int64_t K, float alpha, float beta, void* stream);
 
 /* ------------------------------------------------------------------------
  * Kernel timing.  When enabled, every update-kernel launch is bracketed by

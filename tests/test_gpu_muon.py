@@ -1,0 +1,299 @@
+"""GPU parity of the Muon kernels against the oracle (through the C ABI).
+
+- the bf16 MFMA GEMM behind Newton-Schulz against a float64 product rounded
+  to bf16 (odd shapes, K not a multiple of 8, alpha/beta epilogue);
+- the quantised Muon momentum: indices, magnitudes and the emitted momentum
+  bit-exact against oracle.muon_momentum (bf16 / fp16 / fp32, Nesterov on/off);
+- Newton-Schulz against oracle.newton_schulz and the reference's own outputs;
+- NorMuon scale and the Muon apply against the oracle.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TORCH_DT = {orc.F32: torch.float32, orc.F16: torch.float16, orc.BF16: torch.bfloat16}
+NS_REL = 2e-2  # the reference's own batched-vs-serial Newton-Schulz bound
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    return torch.device("cuda", 0)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from gefen.kernels import _native
+    return _native.load()
+
+
+def _check(rc, lib):
+    from gefen.kernels import _native
+    _native.check(rc, "call")
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _bf16_np(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("mnk", [(128, 128, 32), (256, 192, 160), (200, 136, 72), (100, 60, 30), (33, 257, 48)])
+def test_gemm_nt_matches_float64(dev, lib, mnk):
+    M, N, K = mnk
+    gen = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
+    A = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+    B = torch.randn(N, K, generator=gen).to(torch.bfloat16)
+    C = torch.randn(M, N, generator=gen).to(torch.bfloat16)
+    for alpha, beta, use_c in ((1.0, 0.0, False), (0.75, -1.5, True)):
+        Ad, Bd, Cd = A.to(dev), B.to(dev), C.to(dev)
+        D = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        _check(lib.gefenx_gemm_nt_bf16(Ad.data_ptr(), Bd.data_ptr(), Cd.data_ptr() if use_c else None, D.data_ptr(),
+                                       M, N, K, alpha, beta, _stream(dev)), lib)
+        torch.cuda.synchronize()
+        ref = alpha * (A.double() @ B.double().T)
+        if use_c:
+            ref = ref + beta * C.double()
+        ref_b = orc.bf16(ref.numpy().astype(np.float32))
+        got = _bf16_np(D)
+        # fp32 accumulation in another order than float64: an element may
+        # round to the neighbouring bf16 value
+        assert np.mean(got == ref_b) > 0.98, "gemm %s alpha %g: exact %.4f" % (mnk, alpha, np.mean(got == ref_b))
+        np.testing.assert_allclose(got, ref_b, rtol=2.0 ** -7, atol=2.0 ** -7 * np.abs(ref_b).max() * 2 ** -6)
+
+
+def _mom_state(numel, period, seed):
+    rng = np.random.default_rng(seed)
+    idx = rng.integers(0, 256, numel).astype(np.uint8)
+    mag = (rng.random(numel // period) * 1e-3).astype(np.float32)
+    return idx, mag
+
+
+MOM_CASES = [(orc.BF16, 96 * 40, 96, True), (orc.BF16, 4096, 512, False), (orc.F32, 3000, 24, True),
+             (orc.F16, 2048, 64, True), (orc.BF16, 1000, 1000, True), (orc.BF16, 999, 27, False)]
+
+
+@pytest.mark.parametrize("case", MOM_CASES, ids=lambda c: "dt%d-n%d-P%d-nest%d" % c)
+def test_muon_momentum_matches_oracle(dev, lib, case):
+    dtype, numel, period, nesterov = case
+    from gefen.kernels import _native
+    from gefen.kernels import automatic_gefen_fused as fused
+    td = TORCH_DT[dtype]
+    rng = np.random.default_rng(numel + period)
+    cb = np.load(os.path.join(GOLDEN, "learn.npz"))["cb"].astype(np.float32)
+    qt = fused.quant_table(torch.from_numpy(cb).to(dev), td)
+    idx_np, mag_np = _mom_state(numel, period, 1)
+    idx = torch.from_numpy(idx_np.copy()).to(dev)
+    mag = torch.from_numpy(mag_np.copy()).to(dev)
+    ws = torch.zeros(int(lib.gefenx_workspace_bytes(_native.WS_MOMENTUM, 0, 0, numel // period)) + 256,
+                     dtype=torch.uint8, device=dev)
+    for step in range(3):
+        g = torch.from_numpy((rng.standard_normal(numel) * 1e-3).astype(np.float32)).to(td)
+        if step == 1 and numel >= 2 * period:
+            g[:period] = 0  # a block whose magnitude decays towards zero
+        out = torch.empty(numel, dtype=td, device=dev)
+        gd = g.to(dev)
+        _check(lib.gefenx_quantized_momentum_update(gd.data_ptr(), fused._dtype_code(td), numel, period,
+                                                    idx.data_ptr(), mag.data_ptr(), qt.data_ptr(), out.data_ptr(),
+                                                    0.95, 0, 0, None, 1 if nesterov else 0, ws.data_ptr(),
+                                                    ws.numel(), _stream(dev)), lib)
+        torch.cuda.synchronize()
+        idx_np, mag_np, out_np = orc.muon_momentum(g.float().numpy(), idx_np, mag_np, period, cb, dtype, 0.95,
+                                                   nesterov)
+        tag = "step %d %s" % (step, case)
+        np.testing.assert_array_equal(idx.cpu().numpy(), idx_np, err_msg=tag + " indices")
+        np.testing.assert_array_equal(mag.cpu().numpy(), mag_np, err_msg=tag + " magnitudes")
+        np.testing.assert_array_equal(out.float().cpu().numpy(), out_np, err_msg=tag + " momentum")
+
+
+def _ns_gpu(dev, lib, m, sched, in_dtype=torch.bfloat16):
+    from gefen.kernels import automatic_gefen_fused as fused
+    x = torch.from_numpy(np.asarray(m, np.float32)).to(in_dtype).to(dev)
+    if x.dim() == 2:
+        x = x.unsqueeze(0)
+    b, r, c = x.shape
+    out = torch.empty(b, r, c, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(int(lib.gefenx_ns_workspace_bytes(b, r, c)), dtype=torch.uint8, device=dev)
+    abc = np.ascontiguousarray(np.asarray(sched, np.float64).reshape(-1))
+    _check(lib.gefenx_newton_schulz(x.data_ptr(), fused._dtype_code(in_dtype), out.data_ptr(), b, r, c,
+                                    abc.ctypes.data_as(ctypes.c_void_p), len(sched), 1e-7, ws.data_ptr(), ws.numel(),
+                                    _stream(dev)), lib)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["wide", "tall", "square", "zero"])
+def test_newton_schulz_matches_reference_golden(dev, lib, name):
+    z = np.load(os.path.join(GOLDEN, "muon_ns.npz"))
+    sched = z["abc_" + name] if "abc_" + name in z else np.array(orc.NS_STANDARD)
+    got = _ns_gpu(dev, lib, z["in_" + name], sched)[0]
+    ref = z["out_" + name]
+    assert np.linalg.norm(got - ref) <= NS_REL * max(np.linalg.norm(ref), 1e-30), name
+    o = orc.newton_schulz(z["in_" + name], sched)
+    assert np.linalg.norm(got - o) <= NS_REL * max(np.linalg.norm(o), 1e-30), name
+
+
+@pytest.mark.parametrize("shape", [(3, 256, 384), (2, 320, 136), (1, 130, 70)])
+def test_newton_schulz_batched_matches_oracle(dev, lib, shape):
+    rng = np.random.default_rng(sum(shape))
+    m = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
+    got = _ns_gpu(dev, lib, m, orc.NS_STANDARD)
+    for i in range(shape[0]):
+        o = orc.newton_schulz(m[i])
+        rel = np.linalg.norm(got[i] - o) / np.linalg.norm(o)
+        assert rel <= NS_REL, "batch item %d rel %.3e" % (i, rel)
+        s = np.linalg.svd(got[i].astype(np.float64), compute_uv=False)
+        assert s.max() < 1.3
+
+
+def test_newton_schulz_fp32_input(dev, lib):
+    rng = np.random.default_rng(3)
+    m = (rng.standard_normal((96, 160)) * 1e-2).astype(np.float32)
+    got = _ns_gpu(dev, lib, m, orc.NS_STANDARD, torch.float32)[0]
+    o = orc.newton_schulz(m)
+    assert np.linalg.norm(got - o) <= NS_REL * np.linalg.norm(o)
+
+
+@pytest.mark.parametrize("dtype", [orc.BF16, orc.F32])
+def test_normuon_and_apply_match_oracle(dev, lib, dtype):
+    from gefen.kernels import automatic_gefen_fused as fused
+    td = TORCH_DT[dtype]
+    rng = np.random.default_rng(9)
+    R, C = 72, 40
+    upd = orc.bf16((rng.standard_normal((R, C)) * 0.1).astype(np.float32))
+    p0 = orc.round_dtype((rng.standard_normal((R, C)) * 0.02).astype(np.float32), dtype)
+    v0 = (rng.random(R) * 1e-4).astype(np.float32)
+    ud = torch.from_numpy(upd).to(torch.bfloat16).to(dev)
+    vd = torch.from_numpy(v0.copy()).to(dev)
+    scale = torch.empty(R, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(int(lib.gefenx_normuon_workspace_bytes(R)), dtype=torch.uint8, device=dev)
+    _check(lib.gefenx_normuon_scale(ud.data_ptr(), R, C, vd.data_ptr(), 0.95, 3, 1e-8, scale.data_ptr(),
+                                    ws.data_ptr(), ws.numel(), _stream(dev)), lib)
+    pd = torch.from_numpy(p0.copy()).to(td).to(dev)
+    lr, wd = 1e-3, 0.01
+    adj = lr * orc.adjust_lr_ratio("match_rms_adamw", (R, C))
+    _check(lib.gefenx_muon_apply(pd.data_ptr(), fused._dtype_code(td), ud.data_ptr(), scale.data_ptr(), R, C, lr, wd,
+                                 adj, _stream(dev)), lib)
+    torch.cuda.synchronize()
+    o2, v = orc.normuon(upd, v0, 3)
+    np.testing.assert_allclose(vd.cpu().numpy(), v, rtol=1e-6)
+    p_ref = orc.muon_apply(p0, o2, dtype, lr, wd, adj)
+    got = pd.float().cpu().numpy()
+    # the float64-summed row norms may move one row's bf16 scale by an ulp
+    assert np.mean(got == p_ref) > 0.97
+    np.testing.assert_allclose(got, p_ref, rtol=0, atol=adj * 2.0 ** -7 + np.abs(p_ref).max() * 2.0 ** -7)
+
+
+def _ulp(x, dtype):
+    bits = 7 if dtype == orc.BF16 else 23
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - bits)
+
+
+def _assert_update_close(got, ref, adj, dtype, msg):
+    """Newton-Schulz on another GEMM order moves the update within the
+    reference's rel-L2 2e-2 (||ortho||_F <= 1.3 sqrt(min(R, C))); p rounds."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    lim = adj * NS_REL * 1.3 * np.sqrt(min(got.shape)) + np.linalg.norm(_ulp(np.maximum(np.abs(got), np.abs(ref)), dtype))
+    d = np.linalg.norm(got - ref)
+    assert d <= lim, "%s: ||dp|| %.3e > %.3e" % (msg, d, lim)
+
+
+MUON_KW = {
+    "muon_bf16": (orc.BF16, dict(lr=0.02, weight_decay=0.1, momentum=0.95, nesterov=True), 4),
+    "muon_f32": (orc.F32, dict(lr=0.02, weight_decay=0.1, momentum=0.9, nesterov=False,
+                               adjust_lr_fn="match_rms_adamw", normuon=True), 3),
+}
+
+
+@pytest.mark.parametrize("case", list(MUON_KW))
+def test_gefen_muon_class_matches_reference_golden(dev, case):
+    """GefenMuon.step against the reference's GefenMuon(fused=False) step:
+    indices and magnitudes bit-exact; parameters within the Newton-Schulz
+    bound (each step starts from the reference's parameters)."""
+    from gefen import GefenMuon
+    dtype, kw, steps = MUON_KW[case]
+    td = TORCH_DT[dtype]
+    z = np.load(os.path.join(GOLDEN, case + ".npz"))
+    names = ["a", "b"]
+    ps = [(n, torch.nn.Parameter(torch.from_numpy(z["p0_" + n]).to(td).to(dev))) for n in names]
+    opt = GefenMuon(ps, **kw)
+    opt._gefen_codebook = torch.from_numpy(z["codebook"]).to(dev)
+    for n, p in ps:
+        opt.state[p]["automatic_period"] = int(z["period_" + n])
+    for s in range(1, steps + 1):
+        for n, p in ps:
+            p.grad = torch.from_numpy(z["g%d_%s" % (s, n)]).to(td).to(dev)
+        opt.step()
+        torch.cuda.synchronize()
+        for n, p in ps:
+            st = opt.state[p]
+            tag = "%s step %d %s" % (case, s, n)
+            np.testing.assert_array_equal(st["m_codebook"].cpu().numpy().reshape(-1), z["idx%d_%s" % (s, n)],
+                                          err_msg=tag + " indices")
+            np.testing.assert_array_equal(st["m_magnitude"].cpu().numpy().reshape(-1), z["mag%d_%s" % (s, n)],
+                                          err_msg=tag + " magnitudes")
+            adj = kw["lr"] * orc.adjust_lr_ratio(kw.get("adjust_lr_fn"), p.shape)
+            ref = z["p%d_%s" % (s, n)]
+            _assert_update_close(p.detach().float().cpu().numpy(), ref, adj, dtype, tag + " params")
+            if "nv%d_%s" % (s, n) in z:
+                nv = st["normuon_v"].cpu().numpy().reshape(-1)
+                nv_ref = z["nv%d_%s" % (s, n)]
+                assert np.linalg.norm(nv - nv_ref) <= 2 * NS_REL * np.linalg.norm(nv_ref), tag + " normuon_v"
+                st["normuon_v"].copy_(torch.from_numpy(nv_ref).reshape(-1, 1).to(dev))
+            p.data.copy_(torch.from_numpy(ref).to(td).to(dev))
+
+
+def test_gefen_muon_hybrid_matches_reference_golden(dev):
+    """GefenMuonHybrid with its defaults against the reference's hybrid step."""
+    from gefen import GefenMuonHybrid
+    z = np.load(os.path.join(GOLDEN, "hybrid_bf16.npz"))
+    muon_names = ["layers.0.mlp.w", "layers.0.attn.o"]
+    backup_names = ["embed_tokens.weight", "layers.0.norm.weight"]
+    mk = lambda n: torch.nn.Parameter(torch.from_numpy(z["p0_" + n]).to(torch.bfloat16).to(dev))
+    muon = [(n, mk(n)) for n in muon_names]
+    backup = [(n, mk(n)) for n in backup_names]
+    opt = GefenMuonHybrid(muon, backup, lr=1e-3, weight_decay=0.01)
+    cb = torch.from_numpy(z["codebook"]).to(dev)
+    opt.muon._gefen_codebook = cb.clone()
+    opt.backup._gefen_codebook = cb.clone()
+    named = dict(muon + backup)
+    for n in muon_names + backup_names:
+        opt.state[named[n]]["automatic_period"] = int(z["period_" + n])
+    for s in range(1, 4):
+        for n, p in named.items():
+            p.grad = torch.from_numpy(z["g%d_%s" % (s, n)]).to(torch.bfloat16).to(dev)
+        opt.step()
+        torch.cuda.synchronize()
+        for n, p in named.items():
+            st = opt.state[p]
+            tag = "hybrid step %d %s" % (s, n)
+            np.testing.assert_array_equal(st["m_codebook"].cpu().numpy().reshape(-1), z["idx%d_%s" % (s, n)],
+                                          err_msg=tag + " indices")
+            np.testing.assert_array_equal(st["m_magnitude"].cpu().numpy().reshape(-1), z["mag%d_%s" % (s, n)],
+                                          err_msg=tag + " magnitudes")
+            ref = z["p%d_%s" % (s, n)]
+            got = p.detach().float().cpu().numpy()
+            if n in muon_names:
+                adj = 1e-3 * orc.adjust_lr_ratio("match_rms_adamw", p.shape)
+                _assert_update_close(got, ref, adj, orc.BF16, tag + " params")
+                st["normuon_v"].copy_(torch.from_numpy(z["normuon_v%d_%s" % (s, n)]).reshape(-1, 1).to(dev))
+            else:
+                np.testing.assert_allclose(st["vmean"].cpu().numpy().reshape(-1), z["vmean%d_%s" % (s, n)], rtol=1e-6)
+                lim = _ulp(np.maximum(np.abs(got), np.abs(ref)), orc.BF16)
+                assert (np.abs(got - ref) <= lim).all(), tag + " params"
+            p.data.copy_(torch.from_numpy(ref).to(torch.bfloat16).to(dev))
+    sd = opt.state_dict()
+    assert set(sd) == {"muon", "backup", "backup_optimizer"} and sd["backup_optimizer"] == "gefen"
