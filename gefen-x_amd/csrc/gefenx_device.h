@@ -267,6 +267,43 @@ __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
     return v;
 }
 
+// ---------------------------------------------------- DPP wave reductions
+// GFX9 full-wave sequence (quad_perm 1032, quad_perm 2301, row_half_mirror,
+// row_mirror, row_bcast:15 into rows 1/3, row_bcast:31 into rows 2/3): the
+// total ends in lane 63.  No LDS traffic, unlike a shuffle.
+template <int CTRL, int RMASK>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RMASK, 0xf, false);
+}
+template <int CTRL, int RMASK>
+__device__ __forceinline__ double dpp64(double v) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = dpp32<CTRL, RMASK>((uint32_t)b);
+    const uint32_t hi = dpp32<CTRL, RMASK>((uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// sum over the wave, valid in lane 63
+__device__ __forceinline__ double wave_sum_d63(double v) {
+    v += dpp64<0xB1, 0xf>(v);
+    v += dpp64<0x4E, 0xf>(v);
+    v += dpp64<0x141, 0xf>(v);
+    v += dpp64<0x140, 0xf>(v);
+    v += dpp64<0x142, 0xa>(v);
+    v += dpp64<0x143, 0xc>(v);
+    return v;
+}
+// max over the wave, valid in lane 63
+__device__ __forceinline__ uint32_t wave_max_u63(uint32_t v) {
+    uint32_t o;
+    o = dpp32<0xB1, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x4E, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x141, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x140, 0xf>(v); v = o > v ? o : v;
+    o = dpp32<0x142, 0xa>(v); v = o > v ? o : v;
+    o = dpp32<0x143, 0xc>(v); v = o > v ? o : v;
+    return v;
+}
+
 // Stage the quantisation table parts a kernel needs into LDS.  thr is padded
 // with +inf and bkt with a copy of its last bucket so the fast quantiser needs
 // no bounds checks (x = 1 lands in bucket 4096).

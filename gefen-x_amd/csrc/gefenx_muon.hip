@@ -160,6 +160,165 @@ __global__ void __launch_bounds__(kT) k_mom_emit(MomArgs a) {
     }
 }
 
+// ---------------------------------------------------- fast momentum path
+// P % 8 == 0, N % 8 == 0, 16-byte aligned grad / momentum, 8-byte aligned
+// indices: 8-element chunks never cross a block.  Workgroup w owns chunks
+// [w * 256 * kMomCpt, ...); thread t takes chunks t, t + 256, ... so a wave
+// covers 512 consecutive elements per iteration.
+constexpr int kChunk = 8;
+constexpr int kMomCpt = 8;
+
+struct BlkPos {
+    int64_t blk, pin;
+};
+
+__device__ __forceinline__ BlkPos blk_advance(BlkPos q, int64_t dB, int64_t dP, int64_t P) {
+    q.pin += dP;
+    q.blk += dB;
+    if (q.pin >= P) { q.pin -= P; ++q.blk; }
+    return q;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a) {
+    using T = typename Elem<DT>::T;
+    __shared__ float s_cbr[kCodebookMax];
+    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(a.qt->cbr + threadIdx.x);
+    __syncthreads();
+    const T* g = static_cast<const T*>(a.g);
+    const uint8_t* idxp = a.idx;
+    const float* mag = a.mag;
+    const float w = a.w;
+    const int64_t P = a.P;
+    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
+    const int64_t nch = a.N / kChunk;
+    const int64_t first = (int64_t)blockIdx.x * (kT * kMomCpt) + threadIdx.x;
+    const int64_t F = (int64_t)kT * kChunk;
+    const int64_t dB = F / P, dP = F - (F / P) * P;
+    BlkPos pos;
+    {
+        const int64_t e0 = first * kChunk;
+        pos.blk = div_floor(e0, P, a.invP);
+        pos.pin = e0 - pos.blk * P;
+    }
+    int64_t wblk = -1;   // wave-uniform running block
+    uint32_t wbits = 0u;
+#pragma unroll 1
+    for (int i = 0; i < kMomCpt; ++i) {
+        const int64_t ch = first + (int64_t)i * kT;
+        const bool valid = ch < nch;
+        uint32_t m = 0u;
+        if (valid) {
+            Raw8<DT> gr;
+            load_raw8<DT>(g + ch * kChunk, gr);
+            const RawIdx8 ir = load_raw_idx8(idxp + ch * kChunk);
+            const float mo = *gbl(mag + pos.blk);
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                const float u = mom_u<DT>(s_cbr[raw_idx(ir, k)], mo, raw_elem<DT>(gr, k), w);
+                const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                m = ub > m ? ub : m;
+            }
+        }
+        // lane 0 holds the wave's lowest chunk, valid whenever any lane is
+        const int64_t b0 = __shfl(pos.blk, 0, 64);
+        if (__all(!valid || pos.blk == b0)) {
+            if (b0 != wblk) {
+                if (wblk >= 0) {
+                    const uint32_t r = wave_max_u63(wbits);
+                    if ((threadIdx.x & 63) == 63 && r) atomicMax(mb + wblk, r);
+                }
+                wblk = b0;
+                wbits = 0u;
+            }
+            wbits = m > wbits ? m : wbits;
+        } else {
+            if (wblk >= 0) {
+                const uint32_t r = wave_max_u63(wbits);
+                if ((threadIdx.x & 63) == 63 && r) atomicMax(mb + wblk, r);
+            }
+            wblk = -1;
+            wbits = 0u;
+            if (valid && m) atomicMax(mb + pos.blk, m);
+        }
+        pos = blk_advance(pos, dB, dP, P);
+    }
+    if (wblk >= 0) {
+        const uint32_t r = wave_max_u63(wbits);
+        if ((threadIdx.x & 63) == 63 && r) atomicMax(mb + wblk, r);
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a) {
+    using T = typename Elem<DT>::T;
+    __shared__ uint2 s_fq[kFqEntries];
+    __shared__ float s_cbr[kCodebookMax];
+    const QTable* qt = a.qt;
+    for (int i = threadIdx.x; i < kFqEntries; i += kT)
+        s_fq[i] = uint2{*gbl(qt->fq + 2 * i), *gbl(qt->fq + 2 * i + 1)};
+    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
+    __syncthreads();
+    const bool fastq = qt->max_cnt <= 1;
+    const uint32_t kmax = (uint32_t)(qt->k - 1);
+    const T* g = static_cast<const T*>(a.g);
+    T* out = static_cast<T*>(a.out);
+    uint8_t* idxp = a.idx;
+    const float w = a.w, beta = a.beta, alpha_d = a.alpha_d;
+    const bool nest = a.nesterov != 0;
+    const int64_t P = a.P;
+    const int64_t nch = a.N / kChunk;
+    const int64_t first = (int64_t)blockIdx.x * (kT * kMomCpt) + threadIdx.x;
+    const int64_t F = (int64_t)kT * kChunk;
+    const int64_t dB = F / P, dP = F - (F / P) * P;
+    if (first >= nch) return;
+    BlkPos pos;
+    {
+        const int64_t e0 = first * kChunk;
+        pos.blk = div_floor(e0, P, a.invP);
+        pos.pin = e0 - pos.blk * P;
+    }
+#pragma unroll 1
+    for (int i = 0; i < kMomCpt; ++i) {
+        const int64_t ch = first + (int64_t)i * kT;
+        if (ch >= nch) break;
+        const int64_t e0 = ch * kChunk;
+        const float m_old = *gbl(a.mag_old + pos.blk);
+        const float m_new = *gbl(a.mag + pos.blk);
+        const float y = *gbl(a.minv + pos.blk);
+        Raw8<DT> gr;
+        load_raw8<DT>(g + e0, gr);
+        const RawIdx8 ir = load_raw_idx8(idxp + e0);
+        const float den = m_new < kTiny ? kTiny : m_new;
+        uint32_t ix[kChunk];
+        float o[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            const float gv = raw_elem<DT>(gr, k);
+            const float u = mom_u<DT>(s_cbr[raw_idx(ir, k)], m_old, gv, w);
+            float x = 0.0f;
+            if (m_new > 0.0f) x = round_dt<DT>(div_by_block(u, den, y));
+            else if (m_new != m_new) x = u / m_new;
+            uint32_t ni;
+            if (fastq && x >= -1.0f && x <= 1.0f) {
+                int b = (int)__builtin_fmaf(x, (float)(kBuckets / 2), (float)(kBuckets / 2));
+                b = b < 0 ? 0 : (b > kFqEntries - 1 ? kFqEntries - 1 : b);
+                const uint2 e = s_fq[b];
+                ni = e.y + (__uint_as_float(e.x) < x ? 1u : 0u);
+            } else {
+                ni = quant_nearest(x, qt->bucket, qt->thr, kmax);
+            }
+            ix[k] = ni;
+            float v = round_dt<DT>(s_cbr[ni] * m_new);
+            if (nest) v = round_dt<DT>(__builtin_fmaf(alpha_d, gv, round_dt<DT>(v * beta)));
+            o[k] = v;
+        }
+        store_idx8(idxp + e0, ix);
+        store8<DT>(out + e0, o);
+        pos = blk_advance(pos, dB, dP, P);
+    }
+}
+
 // ==================================================================
 // NT GEMM on bf16 MFMA: D = bf16(alpha * (A B^T) + beta * Cin), optionally
 // also Dt = D^T.  A: M x K, B: N x K, both row-major (K contiguous);
@@ -328,6 +487,9 @@ static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
     const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     a.vec = (g.K % 8 == 0) && (g.lda % 8 == 0) && (g.ldb % 8 == 0) && (g.sA % 8 == 0) && (g.sB % 8 == 0) &&
             al(g.A) && al(g.B);
+    if (cdiv(g.M, kBM) > 65535 || batch > 65535 || cdiv(g.N, kBN) > 2147483647LL)
+        return set_error(GEFENX_EINVAL, "newton-schulz gemm: %lld x %lld x batch %lld exceeds the launch grid",
+                         (long long)g.M, (long long)g.N, (long long)batch);
     const dim3 grid((unsigned)cdiv(g.N, kBN), (unsigned)cdiv(g.M, kBM), (unsigned)batch);
     hipLaunchKernelGGL(k_gemm_nt, grid, dim3(kT), 0, s, a);
     return launch_check("newton-schulz gemm");
@@ -338,25 +500,38 @@ static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
 // ==================================================================
 // X (m x n) and Xt (n x m) from the input [R x C] of any grad dtype, values
 // rounded to bf16 (Tensor.bfloat16()); tall inputs (R > C) are transposed:
-// m = min(R, C), n = max(R, C).
+// m = min(R, C), n = max(R, C).  The input's own layout goes to X (wide) or
+// Xt (tall) directly, the transposed layout through a 64 x 64 LDS tile, so
+// every global access is coalesced.  grid (ceil(C/64), ceil(R/64), batch).
 template <int DT>
 __global__ void __launch_bounds__(kT) k_ns_load(const void* in, int64_t R, int64_t Cc, int64_t s_in,
                                                 uint16_t* X, uint16_t* Xt, int64_t sX) {
     using T = typename Elem<DT>::T;
-    const int64_t bz = blockIdx.y;
+    __shared__ uint16_t tile[64][65];
+    const int64_t bz = blockIdx.z;
     const T* src = static_cast<const T*>(in) + bz * s_in;
-    uint16_t* x = X + bz * sX;
-    uint16_t* xt = Xt + bz * sX;
     const bool tall = R > Cc;
-    const int64_t m = tall ? Cc : R, n = tall ? R : Cc;
-    const int64_t N = R * Cc;
-    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
-        const int64_t r = e / Cc, c = e - (e / Cc) * Cc;
-        const uint16_t h = f2bf(to_f32<DT>(*gbl(src + e)));
-        // element (r, c) of the input is X[r][c] (wide) or X[c][r] (tall)
-        const int64_t i = tall ? c : r, j = tall ? r : c;
-        *gbl(x + i * n + j) = h;
-        *gbl(xt + j * m + i) = h;
+    uint16_t* same = (tall ? Xt : X) + bz * sX;   // [R x C]
+    uint16_t* trans = (tall ? X : Xt) + bz * sX;  // [C x R]
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int id = threadIdx.x + i * kT;
+        const int row = id >> 6, col = id & 63;
+        const int64_t r = r0 + row, c = c0 + col;
+        if (r < R && c < Cc) {
+            const uint16_t h = f2bf(to_f32<DT>(*gbl(src + r * Cc + c)));
+            *gbl(same + r * Cc + c) = h;
+            tile[row][col] = h;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int id = threadIdx.x + i * kT;
+        const int crow = id >> 6, rcol = id & 63;  // output row = input column
+        const int64_t c = c0 + crow, r = r0 + rcol;
+        if (r < R && c < Cc) *gbl(trans + c * R + r) = tile[rcol][crow];
     }
 }
 
@@ -553,18 +728,26 @@ int gefenx_quantized_momentum_update(const void* grad, int dtype, int64_t numel,
     a.dtype = dtype;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const unsigned grid = grid_for(numel, 16384);
-    int ph = prof_begin(GEFENX_K_MOMENTUM, (double)numel * (dtype == F32 ? 12.0 : 6.0), 0.0, s);
-    switch (dtype) {
-        case F32: hipLaunchKernelGGL(k_mom_max<F32>, dim3(grid), dim3(kT), 0, s, a); break;
-        case F16: hipLaunchKernelGGL(k_mom_max<F16>, dim3(grid), dim3(kT), 0, s, a); break;
-        default: hipLaunchKernelGGL(k_mom_max<BF16>, dim3(grid), dim3(kT), 0, s, a); break;
+    const auto al = [](const void* ptr, size_t n) { return (reinterpret_cast<uintptr_t>(ptr) % n) == 0; };
+    const bool fast = period % kChunk == 0 && al(grad, 16) && al(momentum_out, 16) && al(m_codebook, 8);
+    const int64_t fwgs = cdiv(numel / kChunk, (int64_t)kT * kMomCpt);
+    if (fast && fwgs > 2147483647LL) return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: too large");
+    // algorithmic bytes: grad read, indices read + write, momentum written
+    const double es = dtype == F32 ? 4.0 : 2.0;
+    int ph = prof_begin(GEFENX_K_MOMENTUM, (double)numel * (2.0 * es + 2.0), 0.0, s);
+#define GX_MOM(KFAST, KSLOW)                                                                             \
+    switch (dtype) {                                                                                     \
+        case F32: if (fast) hipLaunchKernelGGL(KFAST<F32>, dim3((unsigned)fwgs), dim3(kT), 0, s, a);     \
+                  else hipLaunchKernelGGL(KSLOW<F32>, dim3(grid), dim3(kT), 0, s, a); break;             \
+        case F16: if (fast) hipLaunchKernelGGL(KFAST<F16>, dim3((unsigned)fwgs), dim3(kT), 0, s, a);     \
+                  else hipLaunchKernelGGL(KSLOW<F16>, dim3(grid), dim3(kT), 0, s, a); break;             \
+        default: if (fast) hipLaunchKernelGGL(KFAST<BF16>, dim3((unsigned)fwgs), dim3(kT), 0, s, a);     \
+                 else hipLaunchKernelGGL(KSLOW<BF16>, dim3(grid), dim3(kT), 0, s, a); break;             \
     }
+    GX_MOM(k_mom_max_fast, k_mom_max)
     hipLaunchKernelGGL(k_mom_finalize, dim3(grid_for(nb, 4096)), dim3(kT), 0, s, a);
-    switch (dtype) {
-        case F32: hipLaunchKernelGGL(k_mom_emit<F32>, dim3(grid), dim3(kT), 0, s, a); break;
-        case F16: hipLaunchKernelGGL(k_mom_emit<F16>, dim3(grid), dim3(kT), 0, s, a); break;
-        default: hipLaunchKernelGGL(k_mom_emit<BF16>, dim3(grid), dim3(kT), 0, s, a); break;
-    }
+    GX_MOM(k_mom_emit_fast, k_mom_emit)
+#undef GX_MOM
     prof_end(ph, s);
     return launch_check("quantized momentum update");
 }
@@ -599,10 +782,14 @@ int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch,
     const int64_t N = m * n;
     const bool tall = rows > cols;
     const dim3 g2(grid_for(N, 4096), (unsigned)batch);
+    const dim3 gt((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64), (unsigned)batch);
+    if (cdiv(rows, 64) > 65535 || batch > 65535)
+        return set_error(GEFENX_EINVAL, "gefenx_newton_schulz: %lld rows x batch %lld exceed the launch grid",
+                         (long long)rows, (long long)batch);
     switch (in_dtype) {
-        case F32: hipLaunchKernelGGL(k_ns_load<F32>, g2, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
-        case F16: hipLaunchKernelGGL(k_ns_load<F16>, g2, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
-        default: hipLaunchKernelGGL(k_ns_load<BF16>, g2, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
+        case F32: hipLaunchKernelGGL(k_ns_load<F32>, gt, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
+        case F16: hipLaunchKernelGGL(k_ns_load<F16>, gt, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
+        default: hipLaunchKernelGGL(k_ns_load<BF16>, gt, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
     }
     hipLaunchKernelGGL(k_ns_sumsq, dim3(NsWs::kParts, (unsigned)batch), dim3(kT), 0, s, X, N, N, part);
     hipLaunchKernelGGL(k_ns_norm, dim3((unsigned)cdiv(batch, 64)), dim3(64), 0, s, part, NsWs::kParts, batch,

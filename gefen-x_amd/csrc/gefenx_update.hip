@@ -38,7 +38,7 @@ constexpr int kThreads = 256;
 constexpr int kChunk = 8;
 constexpr int64_t kWaves = kThreads / 64;
 constexpr int64_t kApplyChunksPerThread = 8;   // apply: 4 iterations of 2 chunks
-constexpr int64_t kBlockStatsChunksPerThread = 4;
+constexpr int64_t kBlockStatsChunksPerThread = 8;
 constexpr int64_t kFinBlocksPerWg = 1024;
 
 struct StepScalars {
@@ -106,43 +106,6 @@ __device__ __forceinline__ void wavemax_flush(uint32_t* __restrict__ mb, WaveMax
         if ((threadIdx.x & 63) == 0 && m != 0u) atomicMax(mb + wm.blk, m);
     }
     wm.bits = 0u;
-}
-
-// ---------------------------------------------------- DPP wave reductions
-// GFX9 full-wave sequence (quad_perm 1032, quad_perm 2301, row_half_mirror,
-// row_mirror, row_bcast:15 into rows 1/3, row_bcast:31 into rows 2/3): the
-// total ends in lane 63.  No LDS traffic, unlike a shuffle.
-template <int CTRL, int RMASK>
-__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RMASK, 0xf, false);
-}
-template <int CTRL, int RMASK>
-__device__ __forceinline__ double dpp64(double v) {
-    const uint64_t b = (uint64_t)__double_as_longlong(v);
-    const uint32_t lo = dpp32<CTRL, RMASK>((uint32_t)b);
-    const uint32_t hi = dpp32<CTRL, RMASK>((uint32_t)(b >> 32));
-    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
-// sum over the wave, valid in lane 63
-__device__ __forceinline__ double wave_sum_d63(double v) {
-    v += dpp64<0xB1, 0xf>(v);
-    v += dpp64<0x4E, 0xf>(v);
-    v += dpp64<0x141, 0xf>(v);
-    v += dpp64<0x140, 0xf>(v);
-    v += dpp64<0x142, 0xa>(v);
-    v += dpp64<0x143, 0xc>(v);
-    return v;
-}
-// max over the wave, valid in lane 63
-__device__ __forceinline__ uint32_t wave_max_u63(uint32_t v) {
-    uint32_t o;
-    o = dpp32<0xB1, 0xf>(v); v = o > v ? o : v;
-    o = dpp32<0x4E, 0xf>(v); v = o > v ? o : v;
-    o = dpp32<0x141, 0xf>(v); v = o > v ? o : v;
-    o = dpp32<0x140, 0xf>(v); v = o > v ? o : v;
-    o = dpp32<0x142, 0xa>(v); v = o > v ? o : v;
-    o = dpp32<0x143, 0xc>(v); v = o > v ? o : v;
-    return v;
 }
 
 // Flush a wave-uniform running block max: one atomic per wave.
@@ -471,6 +434,102 @@ __device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int
         if (bsum != 0.0) atomicAdd(w.blk_sq + cur, bsum);
         if (cbits) atomicMax(mb + cur, cbits);
     }
+}
+
+// Block stats, fast path (contiguous 16-byte aligned grad, 8-byte aligned
+// indices, P % 8 == 0 so a chunk never crosses a block): workgroup wg owns
+// chunks [wg * 256 * kBlockStatsChunksPerThread, ...), a wave covers 512
+// consecutive elements per iteration and keeps a running block max and sum
+// while the whole wave stays in one block, flushed with one atomic pair per
+// wave and block.
+__device__ __forceinline__ void bstats_flush(uint32_t* __restrict__ mb, double* __restrict__ bsq, int64_t blk,
+                                             uint32_t bits, double sum) {
+    if (blk < 0) return;
+    const uint32_t r = wave_max_u63(bits);
+    const double t = wave_sum_d63(sum);
+    if ((threadIdx.x & 63) == 63) {
+        if (r) atomicMax(mb + blk, r);
+        if (t != 0.0) atomicAdd(bsq + blk, t);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void stats_block_fast(const TensorWork& w, int64_t wg) {
+    using T = typename Elem<DT>::T;
+    __shared__ float s_cbr[kCodebookMax];
+    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(w.qt->cbr + threadIdx.x);
+    __syncthreads();
+    const T* g = static_cast<const T*>(w.grad);
+    const uint8_t* idxp = w.idx;
+    const float* mag = w.mag;
+    double* bsq = w.blk_sq;
+    const int64_t P = w.P;
+    const MomentumCoef mc = w.mc;
+    uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
+    const int64_t nch = w.N / kChunk;
+    const int64_t first = wg * (kThreads * kBlockStatsChunksPerThread) + threadIdx.x;
+    const int64_t F = kThreads * kChunk;
+    const int64_t dB = F / P, dP = F - (F / P) * P;
+    int64_t blk, pin;
+    {
+        const int64_t e0 = first * kChunk;
+        blk = div_floor(e0, P, w.invP);
+        pin = e0 - blk * P;
+    }
+    int64_t wblk = -1;
+    uint32_t wbits = 0u;
+    double wsum = 0.0;
+#pragma unroll 1
+    for (int i = 0; i < kBlockStatsChunksPerThread; ++i) {
+        const int64_t ch = first + (int64_t)i * kThreads;
+        const bool valid = ch < nch;
+        uint32_t m = 0u;
+        float cs = 0.0f;
+        if (valid) {
+            Raw8<DT> gr;
+            load_raw8<DT>(g + ch * kChunk, gr);
+            const RawIdx8 ir = load_raw_idx8(idxp + ch * kChunk);
+            const float mo = *gbl(mag + blk);
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                const float gv = raw_elem<DT>(gr, k);
+                const float u = momentum_value(s_cbr[raw_idx(ir, k)], mo, gv, mc);
+                const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                m = ub > m ? ub : m;
+                float sq = gv * gv;
+                if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                cs += sq;
+            }
+        }
+        const int64_t b0 = __shfl(blk, 0, 64);  // lane 0 holds the wave's lowest chunk
+        if (__all(!valid || blk == b0)) {
+            if (b0 != wblk) {
+                bstats_flush(mb, bsq, wblk, wbits, wsum);
+                wblk = b0;
+                wbits = 0u;
+                wsum = 0.0;
+            }
+            wbits = m > wbits ? m : wbits;
+            wsum += (double)cs;
+        } else {
+            bstats_flush(mb, bsq, wblk, wbits, wsum);
+            wblk = -1;
+            wbits = 0u;
+            wsum = 0.0;
+            if (valid) {
+                if (m) atomicMax(mb + blk, m);
+                if (cs != 0.0f) atomicAdd(bsq + blk, (double)cs);
+            }
+        }
+        pin += dP;
+        blk += dB;
+        if (pin >= P) { pin -= P; ++blk; }
+    }
+    bstats_flush(mb, bsq, wblk, wbits, wsum);
+}
+
+__device__ __forceinline__ bool block_stats_fast_ok(const TensorWork& w) {
+    return w.fast_stats && (w.P % kChunk) == 0 && (w.N % kChunk) == 0;
 }
 
 // New magnitude (max over the shards), its reciprocal and the old magnitude.
@@ -1144,7 +1203,8 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(TensorWork w) {
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) k_block_stats(TensorWork w) {
-    stats_block<DT>(w, blockIdx.x, gridDim.x);
+    if (block_stats_fast_ok(w)) stats_block_fast<DT>(w, blockIdx.x);
+    else stats_block<DT>(w, blockIdx.x, gridDim.x);
 }
 
 __global__ void __launch_bounds__(kThreads) k_finalize(TensorWork w) {
@@ -1172,7 +1232,8 @@ __global__ void __launch_bounds__(kThreads) k_mt_block_stats(const TensorWork* _
                                                              SegTable tb) {
     const Seg sg = find_seg(tb, blockIdx.x);
     const TensorWork& w = ws[sg.t];
-    stats_block<DT>(w, (int64_t)blockIdx.x - sg.wg_begin, w.stats_wgs);
+    if (block_stats_fast_ok(w)) stats_block_fast<DT>(w, (int64_t)blockIdx.x - sg.wg_begin);
+    else stats_block<DT>(w, (int64_t)blockIdx.x - sg.wg_begin, w.stats_wgs);
 }
 
 __global__ void __launch_bounds__(kThreads) k_mt_finalize(const TensorWork* __restrict__ ws,
