@@ -190,6 +190,95 @@ def bench_muon(args):
     return 0
 
 
+def qwen3_4b_shapes():
+    """Qwen3-4B (36 layers, hidden 2560, GQA q 4096x2560,
+    k/v 1024x2560, o 2560x4096, MLP 9728, q/k-norm 128, vocab 151936 tied)."""
+    shapes = [("model.embed_tokens.weight", (151936, 2560))]
+    for i in range(36):
+        pre = "model.layers.%d." % i
+        shapes += [(pre + "self_attn.q_proj.weight", (4096, 2560)), (pre + "self_attn.k_proj.weight", (1024, 2560)),
+                   (pre + "self_attn.v_proj.weight", (1024, 2560)), (pre + "self_attn.o_proj.weight", (2560, 4096)),
+                   (pre + "self_attn.q_norm.weight", (128,)), (pre + "self_attn.k_norm.weight", (128,)),
+                   (pre + "mlp.gate_proj.weight", (9728, 2560)), (pre + "mlp.up_proj.weight", (9728, 2560)),
+                   (pre + "mlp.down_proj.weight", (2560, 9728)), (pre + "input_layernorm.weight", (2560,)),
+                   (pre + "post_attention_layernorm.weight", (2560,))]
+    shapes.append(("model.norm.weight", (2560,)))
+    return shapes
+
+
+def bench_qwen(args):
+    """the many-tensor launcher on a Qwen3-4B-shaped
+    bf16 set (398 tensors, 4,022,468,096 params); 25 of the 253 2D tensors
+    (every 10th) are transposed views of [C, R] storage; grads 1e-3 *
+    StudentT(nu=3) from a seed; factored_v_2d on, then off.  Reports ms/step,
+    launches per step and the host time of opt.step() (launch overhead)."""
+    import torch
+    from gefen import Gefen
+    from gefen.kernels import _native
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    shapes = qwen3_4b_shapes()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    params, n2d = [], 0
+    for name, shape in shapes:
+        if len(shape) == 2:
+            n2d += 1
+            if n2d % 10 == 0:
+                st = torch.empty(shape[1], shape[0], dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gen)
+                params.append((name, torch.nn.Parameter(st.t())))
+                continue
+        params.append((name, torch.nn.Parameter(
+            torch.empty(shape, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gen))))
+    n_params = sum(p.numel() for _, p in params)
+    n_views = sum(1 for _, p in params if not p.is_contiguous())
+    t3 = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
+    for _, p in params:
+        p.grad = (t3.sample(p.shape) * 1e-3).to(torch.bfloat16)
+        if not p.is_contiguous():
+            p.grad = p.grad.t().contiguous().t()
+    lib = _native.load()
+    results = {}
+    for factored in (True, False):
+        opt = Gefen(params, lr=6e-5, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, factored_v_2d=factored)
+        for _ in range(max(1, args.warmup)):
+            opt.step()
+        torch.cuda.synchronize()
+        lib.gefenx_profile_reset()
+        lib.gefenx_profile_enable(1)
+        host = 0.0
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            h0 = time.perf_counter()
+            opt.step()
+            host += time.perf_counter() - h0
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        lib.gefenx_profile_enable(0)
+        launches = sum(_native.profile_read(k)[1] for k in (_native.K_STATS, _native.K_FINALIZE, _native.K_APPLY,
+                                                             _native.K_BLOCK_STATS, _native.K_BLOCK_APPLY))
+        apply_ms, apply_n, apply_b, _ = _native.profile_read(_native.K_APPLY)
+        bapply_ms, _, bapply_b, _ = _native.profile_read(_native.K_BLOCK_APPLY)
+        lib.gefenx_profile_reset()
+        ms = elapsed * 1e3 / args.steps
+        results["factored" if factored else "block"] = {
+            "ms_per_step": ms, "params_per_s": n_params / (elapsed / args.steps),
+            "compulsory_GB_per_s": (apply_b + bapply_b) / args.steps / (ms / 1e3) / 1e9,
+            "launches_per_step": launches / args.steps, "host_us_per_step": host * 1e6 / args.steps}
+        _log("bench qwen factored=%s: %s" % (factored, results["factored" if factored else "block"]))
+        del opt
+        torch.cuda.empty_cache()
+    r = results["factored"]
+    out = {"metric": METRIC + " (Qwen3-4B many-tensor workload)", "value": r["params_per_s"], "unit": "params/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (seeded N(0,0.02) params, 1e-3*StudentT(3) grads)",
+           "config": {"workload": "Qwen3-4B-shaped bf16 set, 398 tensors, %d transposed views" % n_views,
+                      "params": n_params, "parallelism": "single GPU"},
+           "factored_v_2d_on": results["factored"], "factored_v_2d_off": results["block"]}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,9 +289,10 @@ def main(argv=None):
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy 4 times (scale for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--workload", choices=["gefen", "muon"], default="gefen",
+    ap.add_argument("--workload", choices=["gefen", "muon", "qwen"], default="gefen",
                     help="gefen: configs[1], the headline Llama-3-8B Gefen step (default); "
-                         "muon: configs[3], GefenMuonHybrid with MFMA utilisation")
+                         "muon: configs[3], GefenMuonHybrid with MFMA utilisation; "
+                         "qwen: configs[2], the many-tensor Qwen3-4B set, factored on and off")
     args = ap.parse_args(argv)
     if args.calibrate_copy:
         import torch
@@ -221,6 +311,8 @@ def main(argv=None):
         return 2
     if args.workload == "muon":
         return bench_muon(args)
+    if args.workload == "qwen":
+        return bench_qwen(args)
     import torch
     from gefen import Gefen
     from gefen.kernels import _native
