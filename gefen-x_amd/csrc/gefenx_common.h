@@ -45,8 +45,13 @@ constexpr int64_t kFactTileCols = 1024;
 constexpr int64_t kFactTileMinElems = 1 << 14;
 constexpr int64_t kFactTileMaxElems = 1 << 18;
 
+// Transposed-view stats (strides (1, ld)) use the same column tiles but row
+// tiles of whole 64-row bands, at most kTvStatsMaxRows rows.
+constexpr int64_t kTvStatsMaxRows = 256;
+
 struct FactTiles {
     int64_t ct, rt, tile_rows;
+    int64_t rt_tv, tv_rows;  // row tiles of the transposed-view stats kernel
     static FactTiles make(int64_t rows, int64_t cols) {
         FactTiles t;
         t.ct = (cols + kFactTileCols - 1) / kFactTileCols;
@@ -61,6 +66,12 @@ struct FactTiles {
         t.tile_rows = tr;
         t.rt = (rows + tr - 1) / tr;
         if (t.rt < 1) t.rt = 1;
+        int64_t tv = (tr + 63) & ~int64_t(63);
+        if (tv > kTvStatsMaxRows) tv = kTvStatsMaxRows;
+        if (tv > rows) tv = rows < 1 ? 1 : rows;
+        t.tv_rows = tv;
+        t.rt_tv = (rows + tv - 1) / tv;
+        if (t.rt_tv < 1) t.rt_tv = 1;
         return t;
     }
 };
@@ -77,7 +88,7 @@ inline int64_t mag_shards(int64_t nb) { return nb <= kMagShardMaxBlocks ? kMagSh
 constexpr int64_t kFinRowsPerWg = 256;
 
 struct FactoredWs {
-    // double row_part[ct][rows], double col_part[rt][cols] (per-tile partial
+    // double row_part[ct][rows], double col_part[max(rt, rt_tv)][cols] (per-tile partial
     // sums, fully rewritten every step), uint32 magbits[shards][nb] (zero
     // between steps), float mag_old[nb], float minv[nb],
     // double vrow_sum[ceil(rows/256)] (partials of sum(v_row)), float vcs[cols] (sqrt(v_col)),
@@ -88,7 +99,8 @@ struct FactoredWs {
         const FactTiles t = FactTiles::make(rows, cols);
         size_t o = 0;
         w.off_rowp = o;    o += align256(sizeof(double) * (size_t)(t.ct * rows));
-        w.off_colp = o;    o += align256(sizeof(double) * (size_t)(t.rt * cols));
+        const int64_t rt = t.rt > t.rt_tv ? t.rt : t.rt_tv;  // either stats layout fits
+        w.off_colp = o;    o += align256(sizeof(double) * (size_t)(rt * cols));
         w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)(nb * mag_shards(nb)));
         w.off_magold = o;  o += align256(sizeof(float) * (size_t)nb);
         w.off_minv = o;    o += align256(sizeof(float) * (size_t)nb);

@@ -76,7 +76,9 @@ struct TensorWork {
     int64_t dR, dC, dB, dP;  // apply: chunk advance for a stride of apply_wgs*256*8 elements
     int64_t fR, fC, fB, fP;  // fast apply: advance for a stride of 256*8 elements
     uint64_t seed;
-    int32_t dtype, mode, fast_stats, fast_apply, write_p, sr, bf16_mean, pad_;
+    int32_t dtype, mode;
+    int32_t fast_stats, fast_apply;  // kernel variant: 0 general, 1 contiguous, 2 transposed view
+    int32_t write_p, sr, bf16_mean, pad_;
     float eps, beta2, alpha2, pad2_;
     StepScalars sc;
     MomentumCoef mc;
@@ -352,6 +354,252 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
                 if (k < nv[h]) *gbl(col_part + rtile * C + cc[h] + k) = sum;
             }
         }
+    }
+}
+
+// ====================================================================
+// Transposed views: g (and p) with strides (1, ld), ld >= R -- the layout of
+// x.t() for a contiguous [C, R] tensor x.  Logical row-major order still
+// fixes the blocks, the indices and v_row / v_col, but the data run along
+// logical columns.  Both view kernels move 64 x 64 logical tiles through
+// LDS: g and p travel between HBM and LDS along storage rows (16-byte
+// vectors, 128 B per storage row and tile for 16-bit types), while the math
+// and the index traffic run in logical 8-element chunks as in the contiguous
+// kernels.  Thread t owns the chunks at tile rows t/8 and t/8 + 32, tile
+// columns 8*(t%8) .. +7, so the 8 lanes of a tile row are adjacent.
+// Requires R, C, P multiples of 8 and 16-byte aligned storage rows.
+// ====================================================================
+constexpr int kTv = 64;
+constexpr int kTvTilesPerWg = 4;  // apply: consecutive tiles per workgroup
+
+template <int DT>
+struct TvTile {
+    static constexpr int kEs = (int)sizeof(typename Elem<DT>::T);
+    static constexpr int kRowVec = 16 / kEs;                      // tile rows per 16-byte vector
+    static constexpr int kVecPerCol = kTv / kRowVec;              // vectors per storage-row segment
+    static constexpr int kVecPerThread = kTv * kVecPerCol / kThreads;
+    static constexpr int kPitch = kTv * kEs / 4 + 1;              // dwords per storage row (+1 skews banks)
+    uint32_t d[kTv * kPitch];
+};
+
+// Storage-row vector V of a tile: tile column j = V / kVecPerCol, first tile
+// row (V % kVecPerCol) * kRowVec.
+template <int DT>
+__device__ __forceinline__ void tv_put_vec(TvTile<DT>& t, int V, const u32x4& v) {
+    using TT = TvTile<DT>;
+    uint32_t* d = t.d + (V / TT::kVecPerCol) * TT::kPitch + (V % TT::kVecPerCol) * 4;
+    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4 tv_get_vec(const TvTile<DT>& t, int V) {
+    using TT = TvTile<DT>;
+    const uint32_t* d = t.d + (V / TT::kVecPerCol) * TT::kPitch + (V % TT::kVecPerCol) * 4;
+    return u32x4{d[0], d[1], d[2], d[3]};
+}
+
+// Raw bits of tile element (row i, column j).
+template <int DT>
+__device__ __forceinline__ uint32_t tv_get(const TvTile<DT>& t, int i, int j) {
+    if constexpr (DT == F32) return t.d[j * TvTile<DT>::kPitch + i];
+    else return reinterpret_cast<const uint16_t*>(t.d)[j * 2 * TvTile<DT>::kPitch + i];
+}
+
+template <int DT>
+__device__ __forceinline__ void tv_put(TvTile<DT>& t, int i, int j, float v) {
+    if constexpr (DT == F32) t.d[j * TvTile<DT>::kPitch + i] = __float_as_uint(v);
+    else reinterpret_cast<uint16_t*>(t.d)[j * 2 * TvTile<DT>::kPitch + i] = (uint16_t)from_f32<DT>(v);
+}
+
+// The 8 elements of tile row i, columns j0 .. j0+7, packed as a chunk load.
+template <int DT>
+__device__ __forceinline__ void tv_raw8(const TvTile<DT>& t, int i, int j0, Raw8<DT>& r) {
+    if constexpr (DT == F32) {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) r.f[k] = __uint_as_float(tv_get<DT>(t, i, j0 + k));
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) r.w[m] = tv_get<DT>(t, i, j0 + 2 * m) | (tv_get<DT>(t, i, j0 + 2 * m + 1) << 16);
+    }
+}
+
+// Logical element (r, c) of a view with strides (1, ld) lives at base[c*ld + r].
+template <int DT>
+__device__ __forceinline__ u32x4 tv_load(const typename Elem<DT>::T* base, int64_t ld, int64_t r, int64_t c,
+                                         bool ok) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (ok) v = *gbl(reinterpret_cast<const u32x4*>(base + c * ld + r));
+    return v;
+}
+
+// Stats of a transposed view.  Workgroup (ctile, rtile) covers the same
+// kFactTileCols columns as the contiguous factored kernel (so row_part keeps
+// its layout) and tile_rows (<= 256) rows, as 64 x 64 sub-tiles with the row
+// bands innermost.  MODE 0 (factored): column sums stay in registers across
+// a column's bands (fp32 per sub-tile, then float64), row sums collect in
+// LDS (float64, one owner thread per row).  Block max |u| (and, MODE 1, the
+// block's sum of squares, each square rounded to bf16 for bf16 grads, fp32
+// per chunk, float64 across chunks): a segmented reduction over the 8 lanes
+// of a tile row (blocks are contiguous runs of chunks) and one atomic per
+// run.  Sub-tiles are double-buffered in LDS and the next one's loads are
+// issued before the current one's math.
+template <int DT, int MODE>
+__device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
+    using T = typename Elem<DT>::T;
+    using TT = TvTile<DT>;
+    __shared__ float s_cbr[kCodebookMax];
+    __shared__ TT s_t[2];
+    __shared__ double s_row[kTvStatsMaxRows];
+    __shared__ double s_col[kWaves][kTv];
+    const QTable* qt = wr.qt;
+    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
+    for (int k = threadIdx.x; k < kTvStatsMaxRows; k += kThreads) s_row[k] = 0.0;
+
+    const T* g = static_cast<const T*>(wr.grad);
+    const uint8_t* idxp = wr.idx;
+    const float* mag_old = wr.mag;
+    double* row_part = wr.row_part;
+    double* col_part = wr.col_part;
+    const int64_t R = wr.R, C = wr.C, P = wr.P, ld = wr.gs1;
+    const double invP = wr.invP;
+    const MomentumCoef mc = wr.mc;
+    uint32_t* mb = wr.magbits + (wg % wr.shards) * wr.nb;
+    const int64_t ctile = wg % wr.ct, rtile = wg / wr.ct;
+    const int64_t c_begin = ctile * kFactTileCols;
+    const int64_t c_end = std::min<int64_t>(c_begin + kFactTileCols, C);
+    const int64_t r_begin = rtile * wr.tile_rows;
+    const int64_t r_end = std::min<int64_t>(r_begin + wr.tile_rows, R);
+    const int n_rb = (int)((r_end - r_begin + kTv - 1) / kTv);
+    const int n_sub = (int)((c_end - c_begin + kTv - 1) / kTv) * n_rb;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int jc = tid & 7, ib = tid >> 3;
+
+    struct Pre {
+        u32x4 v[TT::kVecPerThread];
+        RawIdx8 ix[2];
+        float mo[2];
+        int64_t blk[2];  // -1: chunk outside the tensor
+    };
+    auto fetch = [&](int s, Pre& f) {
+        const int cs = s / n_rb, rb = s - cs * n_rb;
+        const int64_t r0 = r_begin + (int64_t)rb * kTv, c0 = c_begin + (int64_t)cs * kTv;
+#pragma unroll
+        for (int q = 0; q < TT::kVecPerThread; ++q) {
+            const int V = tid + q * kThreads;
+            const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
+            f.v[q] = tv_load<DT>(g, ld, r, c, r < r_end && c < c_end);
+        }
+        const int64_t c = c0 + kChunk * jc;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t r = r0 + ib + 32 * h;
+            f.blk[h] = -1;
+            f.mo[h] = 0.0f;
+            f.ix[h] = RawIdx8{0u, 0u};
+            if (r < r_end && c < c_end) {
+                const int64_t e = r * C + c;
+                const int64_t b = div_floor(e, P, invP);
+                f.blk[h] = b;
+                f.mo[h] = *gbl(mag_old + b);
+                f.ix[h] = load_raw_idx8(idxp + e);
+            }
+        }
+    };
+
+    Pre cur, nxt;
+    fetch(0, cur);
+    double colacc[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) colacc[k] = 0.0;
+    for (int s = 0; s < n_sub; ++s) {
+        TT& t = s_t[s & 1];
+#pragma unroll
+        for (int q = 0; q < TT::kVecPerThread; ++q) tv_put_vec<DT>(t, tid + q * kThreads, cur.v[q]);
+        __syncthreads();
+        if (s + 1 < n_sub) fetch(s + 1, nxt);
+        const int cs = s / n_rb, rb = s - cs * n_rb;
+        float colf[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) colf[k] = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = ib + 32 * h;
+            const int64_t b = cur.blk[h];
+            float rs = 0.0f;
+            uint32_t m = 0u;
+            if (b >= 0) {
+                Raw8<DT> gr;
+                tv_raw8<DT>(t, i, kChunk * jc, gr);
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) {
+                    const float gv = raw_elem<DT>(gr, k);
+                    const float uu = momentum_value(s_cbr[raw_idx(cur.ix[h], k)], cur.mo[h], gv, mc);
+                    const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
+                    m = ub > m ? ub : m;
+                    float sq = gv * gv;
+                    if constexpr (MODE == 1 && DT == BF16) sq = round_dt<BF16>(sq);
+                    rs += sq;
+                    if constexpr (MODE == 0) colf[k] += sq;
+                }
+            }
+            double rsd = (double)rs;
+            if constexpr (MODE == 0) {
+                // row sum over the 8 lanes of tile row i; its jc == 0 lane owns s_row
+                rsd += __shfl_xor(rsd, 1, 64);
+                rsd += __shfl_xor(rsd, 2, 64);
+                rsd += __shfl_xor(rsd, 4, 64);
+                if (jc == 0 && b >= 0) s_row[rb * kTv + i] += rsd;
+            }
+            // segmented suffix reduction: after the scan, the first lane of
+            // each block run holds the run's max (and sum)
+#pragma unroll
+            for (int d = 1; d < kChunk; d <<= 1) {
+                const int64_t ob = __shfl_down(b, d, kChunk);
+                const uint32_t om = __shfl_down(m, d, kChunk);
+                const bool same = jc + d < kChunk && ob == b;
+                if (same) m = om > m ? om : m;
+                if constexpr (MODE == 1) {
+                    const double os = __shfl_down(rsd, d, kChunk);
+                    if (same) rsd += os;
+                }
+            }
+            const int64_t pb = __shfl_up(b, 1, kChunk);
+            if (b >= 0 && (jc == 0 || pb != b)) {
+                if (m != 0u) atomicMax(mb + b, m);
+                if constexpr (MODE == 1) {
+                    if (rsd != 0.0) atomicAdd(wr.blk_sq + b, rsd);
+                }
+            }
+        }
+        if constexpr (MODE == 1) {
+            cur = nxt;
+            continue;
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) colacc[k] += (double)colf[k];
+        if (rb == n_rb - 1) {
+            // column sums of this 64-column band: lanes of equal jc, then the waves
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                double v = colacc[k];
+                v += __shfl_xor(v, 8, 64);
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                colacc[k] = 0.0;
+                if (lane < kChunk) s_col[wave][kChunk * lane + k] = v;
+            }
+            __syncthreads();
+            if (tid < kTv) {
+                const int64_t c = c_begin + (int64_t)cs * kTv + tid;
+                if (c < c_end)
+                    *gbl(col_part + rtile * C + c) = s_col[0][tid] + s_col[1][tid] + s_col[2][tid] + s_col[3][tid];
+            }
+        }
+        cur = nxt;
+    }
+    if constexpr (MODE == 0) {
+        __syncthreads();
+        for (int64_t r = r_begin + tid; r < r_end; r += kThreads) *gbl(row_part + ctile * R + r) = s_row[r - r_begin];
     }
 }
 
@@ -1010,15 +1258,16 @@ __device__ __forceinline__ void fast_load(const FastArgs<DT>& a, const Pos& ps, 
     load_raw8<DT>(a.p + e0, in.p);
 }
 
-// Requantise and apply one chunk, then store its indices and parameters.
+// Requantise and apply one chunk: new indices in ix, new parameter values
+// in pv.  GENERAL_Q: the table may hold several thresholds per bucket (the
+// fq entries do not describe it), so every element takes the exact search.
 template <int DT, int MODE>
-__device__ __forceinline__ void fast_compute(const FastArgs<DT>& a, const FastTables& ft, int64_t e0,
-                                             const ChunkIn<DT>& in) {
+__device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTables& ft, const ChunkIn<DT>& in,
+                                          bool general_q, uint32_t ix[kChunk], float pv[kChunk]) {
     const float m_old = in.m_old, m_new = in.m_new, y = in.y;
     const float tb = 0x1.00001p-100f * fmaxf(m_new, 1.0f);
     float xs[kChunk];
-    uint32_t ix[kChunk];
-    bool bad = (y == 0.0f);
+    bool bad = (y == 0.0f) || general_q;
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
         const float u = momentum_value(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
@@ -1047,7 +1296,6 @@ __device__ __forceinline__ void fast_compute(const FastArgs<DT>& a, const FastTa
     float sr = 0.0f, bstep = 0.0f;
     if constexpr (MODE == 0) sr = __builtin_amdgcn_sqrtf(in.rv * a.row_scale);
     else bstep = in.rv * a.lr;
-    float pv[kChunk];
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
         const float q = ft.cbr[ix[k]] * m_new;
@@ -1058,37 +1306,50 @@ __device__ __forceinline__ void fast_compute(const FastArgs<DT>& a, const FastTa
         if (a.wd) pw = round_dt<DT>(pw * a.wdf);
         pv[k] = pw - q * st;
     }
+}
+
+// Requantise and apply one chunk, then store its indices and parameters.
+template <int DT, int MODE>
+__device__ __forceinline__ void fast_compute(const FastArgs<DT>& a, const FastTables& ft, int64_t e0,
+                                             const ChunkIn<DT>& in) {
+    uint32_t ix[kChunk];
+    float pv[kChunk];
+    fast_math<DT, MODE>(a, ft, in, false, ix, pv);
     store_idx8(a.idx + e0, ix);
     store8<DT>(a.p + e0, pv);
 }
 
 // Workgroup `wg` of one parameter's fast apply.  Two chunks are computed per
 // iteration while the next two are already loading.
+template <int DT>
+__device__ __forceinline__ FastArgs<DT> make_fast_args(const TensorWork& w, float row_scale) {
+    FastArgs<DT> a;
+    const StepScalars sc = read_scalars(w);
+    a.p = static_cast<typename Elem<DT>::T*>(w.p);
+    a.g = static_cast<const typename Elem<DT>::T*>(w.grad);
+    a.idx = w.idx;
+    a.mag_old = w.mag_old;
+    a.mag = w.mag;
+    a.minv = w.minv;
+    a.vrow = w.v0;
+    a.vcs = w.vcs;
+    a.bstep = w.step;
+    a.qt = w.qt;
+    a.C = w.C; a.P = w.P; a.fR = w.fR; a.fC = w.fC; a.fB = w.fB; a.fP = w.fP;
+    a.row_scale = row_scale;
+    a.c1 = sc.inv_bc1 * sc.lr;
+    a.eps = w.eps;
+    a.wdf = sc.wdf;
+    a.lr = sc.lr;
+    a.wd = sc.wdf != 1.0f;
+    a.mc = w.mc;
+    return a;
+}
+
 template <int DT, int MODE>
 __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, const FastTables& ft,
                                            float row_scale) {
-    FastArgs<DT> a;
-    {
-        const StepScalars sc = read_scalars(w);
-        a.p = static_cast<typename Elem<DT>::T*>(w.p);
-        a.g = static_cast<const typename Elem<DT>::T*>(w.grad);
-        a.idx = w.idx;
-        a.mag_old = w.mag_old;
-        a.mag = w.mag;
-        a.minv = w.minv;
-        a.vrow = w.v0;
-        a.vcs = w.vcs;
-        a.bstep = w.step;
-        a.qt = w.qt;
-        a.C = w.C; a.P = w.P; a.fR = w.fR; a.fC = w.fC; a.fB = w.fB; a.fP = w.fP;
-        a.row_scale = row_scale;
-        a.c1 = sc.inv_bc1 * sc.lr;
-        a.eps = w.eps;
-        a.wdf = sc.wdf;
-        a.lr = sc.lr;
-        a.wd = sc.wdf != 1.0f;
-        a.mc = w.mc;
-    }
+    const FastArgs<DT> a = make_fast_args<DT>(w, row_scale);
     const int64_t nchunks = w.N / kChunk;
     const int64_t first = wg * (kThreads * kApplyChunksPerThread) + threadIdx.x;
     if (first >= nchunks) return;
@@ -1123,6 +1384,134 @@ __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, cons
         p0 = p2;
         p1 = p3;
     }
+}
+
+// Apply of a transposed view, MODE 0 factored / 1 block (nearest rounding; a
+// table with several thresholds per bucket takes the exact search for every
+// element).
+// Workgroup wg owns tiles [wg*4, wg*4 + 4) in tile-row-fastest order, so its
+// storage-row segments of one tile column are consecutive.  Per tile: g and
+// p go to LDS, the chunks requantise and apply (indices straight to HBM, new
+// p back into the LDS tile), then p leaves along storage rows.  The next
+// tile's loads are in flight during the current tile's math.
+template <int DT, int MODE>
+__device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const FastTables& ft,
+                                         TvTile<DT>& tg, TvTile<DT>& tp, float row_scale) {
+    using TT = TvTile<DT>;
+    const FastArgs<DT> a = make_fast_args<DT>(w, row_scale);
+    const int64_t R = w.R, C = w.C, P = w.P, ldg = w.gs1, ldp = w.ps1;
+    const double invP = w.invP;
+    const int64_t nrt = (R + kTv - 1) / kTv;
+    const int64_t ntiles = nrt * ((C + kTv - 1) / kTv);
+    const int64_t t0 = wg * kTvTilesPerWg;
+    if (t0 >= ntiles) return;
+    const int64_t t1 = std::min<int64_t>(t0 + kTvTilesPerWg, ntiles);
+    const bool general_q = w.qt->max_cnt > 1;
+    const int tid = threadIdx.x, jc = tid & 7, ib = tid >> 3;
+
+    struct Pre {
+        u32x4 g[TT::kVecPerThread], p[TT::kVecPerThread];
+        RawIdx8 ix[2];
+        float mo[2], mn[2], y[2], rv[2];
+        float vc[kChunk];
+        bool ok[2];
+    };
+    auto fetch = [&](int64_t T, Pre& f) {
+        const int64_t r0 = (T % nrt) * kTv, c0 = (T / nrt) * kTv;
+#pragma unroll
+        for (int q = 0; q < TT::kVecPerThread; ++q) {
+            const int V = tid + q * kThreads;
+            const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
+            const bool ok = r < R && c < C;
+            f.g[q] = tv_load<DT>(a.g, ldg, r, c, ok);
+            f.p[q] = tv_load<DT>(a.p, ldp, r, c, ok);
+        }
+        const int64_t c = c0 + kChunk * jc;
+        if (MODE == 0 && c < C) {
+            load_vcol(a.vcs + c, f.vc);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) f.vc[k] = 0.0f;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t r = r0 + ib + 32 * h;
+            f.ok[h] = r < R && c < C;
+            f.ix[h] = RawIdx8{0u, 0u};
+            f.mo[h] = f.mn[h] = f.y[h] = f.rv[h] = 0.0f;
+            if (f.ok[h]) {
+                const int64_t e = r * C + c;
+                const int64_t b = div_floor(e, P, invP);
+                f.mo[h] = *gbl(a.mag_old + b);
+                f.mn[h] = *gbl(a.mag + b);
+                f.y[h] = *gbl(a.minv + b);
+                f.rv[h] = MODE == 0 ? *gbl(a.vrow + r) : *gbl(a.bstep + b);
+                f.ix[h] = load_raw_idx8(a.idx + e);
+            }
+        }
+    };
+
+    Pre cur, nxt;
+    fetch(t0, cur);
+    for (int64_t T = t0; T < t1; ++T) {
+#pragma unroll
+        for (int q = 0; q < TT::kVecPerThread; ++q) {
+            tv_put_vec<DT>(tg, tid + q * kThreads, cur.g[q]);
+            tv_put_vec<DT>(tp, tid + q * kThreads, cur.p[q]);
+        }
+        __syncthreads();
+        if (T + 1 < t1) fetch(T + 1, nxt);
+        const int64_t r0 = (T % nrt) * kTv, c0 = (T / nrt) * kTv;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (!cur.ok[h]) continue;
+            const int i = ib + 32 * h;
+            ChunkIn<DT> in;
+            tv_raw8<DT>(tg, i, kChunk * jc, in.g);
+            tv_raw8<DT>(tp, i, kChunk * jc, in.p);
+            in.i = cur.ix[h];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) in.vc[k] = cur.vc[k];
+            in.m_old = cur.mo[h];
+            in.m_new = cur.mn[h];
+            in.y = cur.y[h];
+            in.rv = cur.rv[h];
+            uint32_t ix[kChunk];
+            float pv[kChunk];
+            fast_math<DT, MODE>(a, ft, in, general_q, ix, pv);
+            store_idx8(a.idx + (r0 + i) * C + c0 + kChunk * jc, ix);
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) tv_put<DT>(tp, i, kChunk * jc + k, pv[k]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < TT::kVecPerThread; ++q) {
+            const int V = tid + q * kThreads;
+            const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
+            if (r < R && c < C)
+                __builtin_nontemporal_store(tv_get_vec<DT>(tp, V), gbl(reinterpret_cast<u32x4*>(a.p + c * ldp + r)));
+        }
+        __syncthreads();
+        cur = nxt;
+    }
+}
+
+template <int DT>
+struct TvApplyLds {
+    FastTables f;
+    TvTile<DT> g, p;
+};
+
+template <int DT, int MODE>
+__device__ __forceinline__ void apply_tv_wg(const TensorWork& w, int64_t wg, TvApplyLds<DT>& lds) {
+    stage_fast(lds.f, w.qt);
+    float row_scale = 0.0f;
+    if constexpr (MODE == 0) {
+        const StepScalars sc = read_scalars(w);
+        row_scale = (1.0f / stored_mean(w)) * sc.inv_bc2;
+    }
+    __syncthreads();
+    apply_tv<DT, MODE>(w, wg, lds.f, lds.g, lds.p, row_scale);
 }
 
 // LDS of the apply kernels: the fast tables or the general ones, never both.
@@ -1202,6 +1591,17 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(TensorWork w) {
 }
 
 template <int DT>
+__global__ void __launch_bounds__(kThreads) k_factored_stats_tv(TensorWork w) {
+    stats_tv<DT, 0>(w, blockIdx.x);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_apply_tv(TensorWork w) {
+    __shared__ TvApplyLds<DT> lds;
+    apply_tv_wg<DT, 0>(w, blockIdx.x, lds);
+}
+
+template <int DT>
 __global__ void __launch_bounds__(kThreads) k_block_stats(TensorWork w) {
     if (block_stats_fast_ok(w)) stats_block_fast<DT>(w, blockIdx.x);
     else stats_block<DT>(w, blockIdx.x, gridDim.x);
@@ -1225,6 +1625,19 @@ __global__ void __launch_bounds__(kThreads) k_mt_factored_stats(const TensorWork
                                                                 SegTable tb) {
     const Seg sg = find_seg(tb, blockIdx.x);
     stats_factored<DT, FAST>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
+}
+
+template <int DT, int MODE>
+__global__ void __launch_bounds__(kThreads) k_mt_stats_tv(const TensorWork* __restrict__ ws, SegTable tb) {
+    const Seg sg = find_seg(tb, blockIdx.x);
+    stats_tv<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
+}
+
+template <int DT, int MODE>
+__global__ void __launch_bounds__(kThreads) k_mt_apply_tv(const TensorWork* __restrict__ ws, SegTable tb) {
+    __shared__ TvApplyLds<DT> lds;
+    const Seg sg = find_seg(tb, blockIdx.x);
+    apply_tv_wg<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin, lds);
 }
 
 template <int DT>
@@ -1328,6 +1741,12 @@ static int build_work(const WorkInput& in, TensorWork& w) {
     w.write_p = (in.step_scalars != nullptr) || !(in.sc.lr == 0.0f && in.sc.wdf == 1.0f);
     char* ws = static_cast<char*>(in.workspace);
     const int64_t nchunks = ceil_div(N, kChunk);
+    // transposed views: strides (1, ld), storage rows 16-byte aligned
+    const int64_t es = (int64_t)elem_size(in.dtype);
+    const bool tv_shape = in.R > 1 && in.R % kChunk == 0 && in.C % kChunk == 0 && in.period % kChunk == 0 &&
+                          aligned(in.idx, 8);
+    const bool tv_g = in.gs0 == 1 && in.gs1 >= in.R && (in.gs1 * es) % 16 == 0 && aligned(in.grad, 16);
+    const bool tv_p = in.ps0 == 1 && in.ps1 >= in.R && (in.ps1 * es) % 16 == 0 && aligned(in.p, 16);
     if (in.mode == 0) {
         const FactoredWs L = FactoredWs::make(in.R, in.C, nb);
         if (in.ws_bytes < L.total)
@@ -1352,6 +1771,13 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         w.fast_stats = contig_g && (in.C % kChunk == 0) && aligned(in.grad, 16) && aligned(in.idx, 8);
         w.fast_apply = contig_g && contig_p && (in.C % kChunk == 0) && (in.period % kChunk == 0) &&
                        aligned(in.grad, 16) && aligned(in.p, 16) && aligned(in.idx, 8) && aligned(in.v1, 16);
+        if (!w.fast_stats && tv_shape && tv_g) {
+            w.fast_stats = 2;
+            w.rt = t.rt_tv;
+            w.tile_rows = t.tv_rows;
+            w.stats_wgs = t.ct * t.rt_tv;
+        }
+        if (!w.fast_apply && tv_shape && tv_g && tv_p && !in.sr && w.write_p) w.fast_apply = 2;
     } else {
         const BlockWs L = BlockWs::make(nb);
         if (in.ws_bytes < L.total)
@@ -1367,8 +1793,30 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         w.fast_stats = aligned(in.grad, 16) && aligned(in.idx, 8);
         w.fast_apply = (in.period % kChunk == 0) && aligned(in.grad, 16) && aligned(in.p, 16) &&
                        aligned(in.idx, 8);
+        if (in.R > 1) {
+            // a 2D descriptor that is not contiguous (the callers flatten the
+            // contiguous ones): the grad must be contiguous (flat stats) or a
+            // transposed view; p any strides (general apply) or a view too
+            const bool g_contig = in.gs1 == 1 && in.gs0 == in.C;
+            const bool p_contig = in.ps1 == 1 && in.ps0 == in.C;
+            if (tv_shape && tv_g) {
+                const FactTiles t = FactTiles::make(in.R, in.C);
+                w.ct = t.ct; w.rt = t.rt_tv; w.tile_rows = t.tv_rows;
+                w.stats_wgs = t.ct * t.rt_tv;
+                w.fast_stats = 2;
+            } else if (!g_contig) {
+                return set_error(GEFENX_EINVAL,
+                                 "block update: grad strides (%lld, %lld) of [%lld, %lld] are neither contiguous nor "
+                                 "a transposed view with rows, cols and period multiples of 8",
+                                 (long long)in.gs0, (long long)in.gs1, (long long)in.R, (long long)in.C);
+            }
+            w.fast_apply = (tv_shape && tv_g && tv_p && !in.sr && w.write_p) ? 2
+                         : (g_contig && p_contig) ? w.fast_apply : 0;
+        }
     }
     w.apply_wgs = std::max<int64_t>(1, ceil_div(nchunks, kThreads * kApplyChunksPerThread));
+    if (w.fast_apply == 2)
+        w.apply_wgs = ceil_div(ceil_div(in.R, kTv) * ceil_div(in.C, kTv), kTvTilesPerWg);
     const int64_t S = w.apply_wgs * kThreads * kChunk;
     w.dR = S / w.C;
     w.dC = S - w.dR * w.C;
@@ -1402,6 +1850,15 @@ static void launch_apply_one(int dtype, const TensorWork& w, hipStream_t s) {
 
 template <int MODE>
 static void launch_apply_single(const TensorWork& w, hipStream_t s) {
+    if (MODE == 0 && w.fast_apply == 2) {
+        const dim3 grid((unsigned)w.apply_wgs), block(kThreads);
+        switch (w.dtype) {
+            case F32: hipLaunchKernelGGL(k_apply_tv<F32>, grid, block, 0, s, w); break;
+            case F16: hipLaunchKernelGGL(k_apply_tv<F16>, grid, block, 0, s, w); break;
+            default: hipLaunchKernelGGL(k_apply_tv<BF16>, grid, block, 0, s, w); break;
+        }
+        return;
+    }
     if (w.fast_apply) {
         if (w.sr) launch_apply_one<MODE, true, true>(w.dtype, w, s);
         else launch_apply_one<MODE, false, true>(w.dtype, w, s);
@@ -1419,7 +1876,8 @@ static int run_single(const TensorWork& w, hipStream_t s) {
     if (w.mode == 0) {
         const dim3 grid((unsigned)w.stats_wgs);
 #define GX_FSTATS(DTV)                                                                          \
-    if (w.fast_stats) hipLaunchKernelGGL((k_factored_stats<DTV, true>), grid, block, 0, s, w);  \
+    if (w.fast_stats == 2) hipLaunchKernelGGL(k_factored_stats_tv<DTV>, grid, block, 0, s, w);  \
+    else if (w.fast_stats) hipLaunchKernelGGL((k_factored_stats<DTV, true>), grid, block, 0, s, w);  \
     else hipLaunchKernelGGL((k_factored_stats<DTV, false>), grid, block, 0, s, w)
         switch (w.dtype) {
             case F32: GX_FSTATS(F32); break;
@@ -1618,7 +2076,8 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
         if (l.phase == 0) {
             if (l.key.mode == 0) {
 #define GX_MTS(DTV)                                                                                          \
-    if (l.key.fast) hipLaunchKernelGGL((k_mt_factored_stats<DTV, true>), grid, block, 0, s, dws, sg); \
+    if (l.key.fast == 2) hipLaunchKernelGGL((k_mt_stats_tv<DTV, 0>), grid, block, 0, s, dws, sg); \
+    else if (l.key.fast) hipLaunchKernelGGL((k_mt_factored_stats<DTV, true>), grid, block, 0, s, dws, sg); \
     else hipLaunchKernelGGL((k_mt_factored_stats<DTV, false>), grid, block, 0, s, dws, sg)
                 switch (l.key.dtype) {
                     case F32: GX_MTS(F32); break;
@@ -1626,6 +2085,12 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
                     default: GX_MTS(BF16); break;
                 }
 #undef GX_MTS
+            } else if (l.key.fast == 2) {
+                switch (l.key.dtype) {
+                    case F32: hipLaunchKernelGGL((k_mt_stats_tv<F32, 1>), grid, block, 0, s, dws, sg); break;
+                    case F16: hipLaunchKernelGGL((k_mt_stats_tv<F16, 1>), grid, block, 0, s, dws, sg); break;
+                    default: hipLaunchKernelGGL((k_mt_stats_tv<BF16, 1>), grid, block, 0, s, dws, sg); break;
+                }
             } else {
                 switch (l.key.dtype) {
                     case F32: hipLaunchKernelGGL(k_mt_block_stats<F32>, grid, block, 0, s, dws, sg); break;
@@ -1639,7 +2104,16 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
             hipLaunchKernelGGL(k_mt_finalize, grid, block, 0, s, dws, sg);
         } else {
             const int dt = l.key.dtype;
-            if (l.key.mode == 0) {
+            if (l.key.fast == 2) {
+#define GX_MTA_TV(MODEV)                                                                                     \
+    switch (dt) {                                                                                            \
+        case F32: hipLaunchKernelGGL((k_mt_apply_tv<F32, MODEV>), grid, block, 0, s, dws, sg); break;      \
+        case F16: hipLaunchKernelGGL((k_mt_apply_tv<F16, MODEV>), grid, block, 0, s, dws, sg); break;      \
+        default: hipLaunchKernelGGL((k_mt_apply_tv<BF16, MODEV>), grid, block, 0, s, dws, sg); break;      \
+    }
+                if (l.key.mode == 0) { GX_MTA_TV(0) } else { GX_MTA_TV(1) }
+#undef GX_MTA_TV
+            } else if (l.key.mode == 0) {
                 if (l.key.fast) {
                     if (l.key.sr) launch_mt_apply<0, true, true>(dt, grid, s, dws, sg);
                     else launch_mt_apply<0, false, true>(dt, grid, s, dws, sg);
@@ -1772,10 +2246,10 @@ static int desc_to_work(const gefenx_tensor_desc& d, int i, const void* const* q
     in.p = d.p; in.grad = d.grad; in.dtype = d.dtype; in.mode = d.factored ? 0 : 1;
     if (d.factored) {
         in.R = d.rows; in.C = d.cols; in.ps0 = d.ps0; in.ps1 = d.ps1; in.gs0 = d.gs0; in.gs1 = d.gs1;
+    } else if (d.rows <= 1 || (d.ps1 == 1 && d.gs1 == 1 && d.ps0 == d.cols && d.gs0 == d.cols)) {
+        in.R = 1; in.C = N; in.ps0 = N; in.ps1 = 1; in.gs0 = N; in.gs1 = 1;  // contiguous: flat
     } else {
-        if (d.ps1 != 1 || d.gs1 != 1 || (d.rows > 1 && (d.ps0 != d.cols || d.gs0 != d.cols)))
-            return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: block-path descriptor %d must be contiguous", i);
-        in.R = 1; in.C = N; in.ps0 = N; in.ps1 = 1; in.gs0 = N; in.gs1 = 1;
+        in.R = d.rows; in.C = d.cols; in.ps0 = d.ps0; in.ps1 = d.ps1; in.gs0 = d.gs0; in.gs1 = d.gs1;
     }
     in.period = d.period;
     in.idx = d.m_codebook; in.mag = d.m_magnitude; in.v0 = d.v0; in.v1 = d.v1; in.qt = qt;

@@ -64,6 +64,23 @@ def _stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def _block_view_ok(p: torch.Tensor, grad: torch.Tensor, period: int) -> bool:
+    """The multi-tensor launcher steps a block-path parameter in place when
+    it and its grad are transposed views (strides (1, ld), ld >= rows, 16-byte
+    aligned storage rows) with rows, cols and period multiples of 8; other
+    non-contiguous block-path parameters take the contiguous-copy route."""
+    if p.ndim != 2 or grad.ndim != 2:
+        return False
+    rows, cols = p.shape
+    es = p.element_size()
+    if rows < 2 or rows % 8 or cols % 8 or period % 8:
+        return False
+    for t in (p, grad):
+        if t.stride(0) != 1 or t.stride(1) < rows or (t.stride(1) * es) % 16 or t.data_ptr() % 16:
+            return False
+    return True
+
+
 class Gefen(torch.optim.Optimizer):
     """Gefen optimizer (see module docstring).
 
@@ -468,10 +485,14 @@ class Gefen(torch.optim.Optimizer):
             v0, v1 = state["v_row"].data_ptr(), state["v_col"].data_ptr()
             ps0, ps1, gs0, gs1 = p.stride(0), p.stride(1), grad.stride(0), grad.stride(1)
         else:
-            rows, cols = 1, p.numel()
             ws = self._workspace(state, _native.WS_BLOCK, 0, 0, nb, p.device)
             v0, v1 = state["vmean"].data_ptr(), 0
-            ps0, ps1, gs0, gs1 = cols, 1, cols, 1
+            if p.is_contiguous() and grad.is_contiguous():
+                rows, cols = 1, p.numel()
+                ps0, ps1, gs0, gs1 = cols, 1, cols, 1
+            else:  # a transposed view (_block_view_ok): logical [rows, cols]
+                rows, cols = p.shape
+                ps0, ps1, gs0, gs1 = p.stride(0), p.stride(1), grad.stride(0), grad.stride(1)
         beta1, beta2 = group["beta1"], group["beta2"]
         return (p.data_ptr(), grad.data_ptr(), state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(),
                 v0, v1, ws.data_ptr(), rows, cols, ps0, ps1, gs0, gs1, period,
@@ -522,7 +543,9 @@ class Gefen(torch.optim.Optimizer):
                     prepared = self._prepare_factored(group, name, p, grad)
                 else:
                     prepared = self._prepare_block(group, name, p, grad)
-                batchable = self._multi_tensor and (factored or (p.is_contiguous() and grad.is_contiguous()))
+                batchable = self._multi_tensor and (
+                    factored or (p.is_contiguous() and grad.is_contiguous())
+                    or _block_view_ok(p, grad, prepared[0]["automatic_period"]))
                 if batchable:
                     rows, dtypes = batches.setdefault(p.device, ([], set()))
                     rows.append(self._desc_row(group, p, grad, factored, prepared))

@@ -193,7 +193,12 @@ typedef struct gefenx_tensor_desc {
     void* workspace;        /* zero-filled, gefenx_workspace_bytes(...) bytes */
     int64_t rows, cols;     /* logical 2D shape (1D: rows=1, cols=numel) */
     int64_t ps0, ps1;       /* param element strides */
-    int64_t gs0, gs1;       /* grad element strides */
+    int64_t gs0, gs1;       /* grad element strides.  Factored: any strides
+                             * (logical row-major order; transposed views,
+                             * strides (1, ld), take tiled kernels when rows,
+                             * cols and period are multiples of 8).  Block:
+                             * contiguous, or a grad that is contiguous or such
+                             * a transposed view (GEFENX_EINVAL otherwise). */
     int64_t period;
     int32_t dtype;          /* gefenx_dtype of p and grad */
     int32_t factored;       /* 1: factored second moment; 0: block vmean */

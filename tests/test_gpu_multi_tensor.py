@@ -99,8 +99,11 @@ def test_mixed_set_matches_per_parameter(dev):
 
 
 def test_block_path_for_2d_matches_per_parameter(dev):
-    shapes = [(64, 96), (40, 72), (4096,), (1000,)]
-    dtypes = [torch.bfloat16, torch.float32, torch.bfloat16, torch.float32]
+    # indices 1 and 4 get strided grads: transposed views stepped in place by
+    # the launcher; index 5 is a view with a contiguous grad (copy route)
+    shapes = [(64, 96), (200, 136, "T"), (4096,), (1000,), (328, 200, "T"), (96, 64, "T"), (40, 72)]
+    dtypes = [torch.bfloat16, torch.bfloat16, torch.bfloat16, torch.float32, torch.float32, torch.float16,
+              torch.float32]
     _run(dev, shapes, dtypes, factored_v_2d=False)
 
 

@@ -123,6 +123,141 @@ def test_factored_transposed_view_matches_oracle(dev, dtype):
     _say("case", _run_factored(dev, dtype, 96, 64, 768, 0.01, 2, seed=5, transposed=True))
 
 
+def _strided(t2d, layout, dev, pad=16):
+    """Device copy of a logical [R, C] tensor in the given storage layout:
+    'contig' row-major; 'view' the .t() of a contiguous [C, R] tensor (strides
+    (1, R)); 'view_ld' the same with storage rows of R + pad (strides
+    (1, R + pad))."""
+    if layout == "contig":
+        return t2d.contiguous().to(dev)
+    if layout == "view":
+        return t2d.t().contiguous().to(dev).t()
+    R, C = t2d.shape
+    st = torch.zeros(C, R + pad, dtype=t2d.dtype)
+    st[:, :R] = t2d.t()
+    return st.to(dev)[:, :R].t()
+
+
+def _run_factored_strided(dev, dtype, rows, cols, period, p_layout, g_layout, steps=3, seed=0, wd=0.01):
+    """gefenx_factored_update through the C ABI with the parameter and the
+    grad in the given storage layouts (their strides go to the kernel as is)
+    against the oracle's logical row-major step."""
+    from gefen.kernels import _native
+    from gefen.kernels import automatic_gefen_fused as fused
+    lib = _native.load()
+    gen = torch.Generator().manual_seed(seed)
+    tdt = TDT[dtype]
+    cb = _codebook()
+    cb_dev = torch.from_numpy(cb).to(dev)
+    qt = fused.quant_table(cb_dev, tdt)
+    p0 = (torch.randn(rows, cols, generator=gen) * 0.02).to(tdt)
+    p_dev = _strided(p0, p_layout, dev)
+    nb = rows * cols // period
+    idx = torch.zeros(nb, period, dtype=torch.uint8, device=dev)
+    mag = torch.zeros(nb, 1, dtype=torch.float32, device=dev)
+    vr = torch.zeros(rows, dtype=torch.float32, device=dev)
+    vc = torch.zeros(cols, dtype=torch.float32, device=dev)
+    ws = torch.zeros(int(lib.gefenx_workspace_bytes(_native.WS_FACTORED, rows, cols, nb)), dtype=torch.uint8,
+                     device=dev)
+    st = {"p": p0.float().numpy(), "idx": np.zeros(rows * cols, np.uint8), "mag": np.zeros(nb, np.float32),
+          "v_row": np.zeros(rows, np.float32), "v_col": np.zeros(cols, np.float32)}
+    tag = ""
+    for s in range(1, steps + 1):
+        g = (torch.randn(rows, cols, generator=gen) * 10 ** gen_uniform(gen, -4, -2)).to(tdt)
+        g_dev = _strided(g, g_layout, dev)
+        bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+        tag = "factored %s [%d,%d] P=%d p:%s g:%s step %d" % (tdt, rows, cols, period, p_layout, g_layout, s)
+        _say("case", tag)
+        _native.check(lib.gefenx_factored_update(
+            p_dev.data_ptr(), g_dev.data_ptr(), fused._dtype_code(tdt), rows, cols,
+            p_dev.stride(0), p_dev.stride(1), g_dev.stride(0), g_dev.stride(1),
+            idx.data_ptr(), mag.data_ptr(), vr.data_ptr(), vc.data_ptr(), period, qt.data_ptr(),
+            B1, B2, LR, EPS, 1.0 / bc2, 1.0 / bc1, 1.0 - LR * wd, 0, 0, None, None,
+            ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream), tag)
+        p_np, i_np, m_np, r_np, c_np = orc.factored_step(
+            st["p"], g.float().numpy(), st["idx"], st["mag"], st["v_row"], st["v_col"], period,
+            cb, dtype, beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), i_np, err_msg=tag + " idx")
+        np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), m_np, err_msg=tag + " mag")
+        np.testing.assert_allclose(vr.cpu().numpy(), r_np, rtol=1e-6, err_msg=tag + " v_row")
+        np.testing.assert_allclose(vc.cpu().numpy(), c_np, rtol=1e-6, err_msg=tag + " v_col")
+        _assert_p(p_dev.float().cpu().numpy(), p_np, dtype, tag + " p")
+        st = {"p": p_dev.float().cpu().numpy(), "idx": i_np, "mag": m_np,
+              "v_row": vr.cpu().numpy(), "v_col": vc.cpu().numpy()}
+    return tag
+
+
+# Transposed-view kernels (strides (1, ld)): ragged 64-tiles, blocks that
+# straddle rows, several 1024-column tiles and 64-row bands per workgroup,
+# one-chunk blocks (P = 8) and a single block.
+STRIDED_CASES = [
+    (orc.BF16, 200, 136, 400, "view", "view"),
+    (orc.BF16, 200, 136, 400, "view_ld", "view_ld"),
+    (orc.BF16, 4104, 4120, 1080, "view", "view"),
+    (orc.F32, 328, 200, 1640, "view", "view"),
+    (orc.F16, 136, 264, 88, "view_ld", "view"),
+    (orc.BF16, 64, 64, 8, "view", "view"),
+    (orc.BF16, 128, 192, 24576, "view", "view"),
+    (orc.BF16, 200, 136, 400, "contig", "view"),    # view stats, general apply
+    (orc.F32, 200, 136, 400, "view", "contig"),      # contiguous stats, general apply
+]
+
+
+@pytest.mark.parametrize("case", STRIDED_CASES, ids=lambda c: "%s-%dx%d-P%d-p_%s-g_%s" % c)
+def test_factored_strided_matches_oracle(dev, case):
+    dtype, rows, cols, period, pl, gl = case
+    _run_factored_strided(dev, dtype, rows, cols, period, pl, gl, seed=rows + cols)
+
+
+BLOCK_VIEW_CASES = [
+    (orc.BF16, 200, 136, 400, "view"),
+    (orc.BF16, 200, 136, 400, "view_ld"),
+    (orc.F32, 328, 200, 1640, "view"),
+    (orc.F16, 136, 264, 88, "view"),
+    (orc.BF16, 1096, 2056, 2056, "view"),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_VIEW_CASES, ids=lambda c: "%s-%dx%d-P%d-%s" % c)
+def test_block_view_matches_oracle(dev, case):
+    """factored_v_2d=False with a transposed-view parameter and grad: the
+    multi-tensor launcher steps it in place (tiled view kernels, block
+    vmean) -- indices and magnitudes bit-exact against the oracle's block
+    step, vmean within 1e-6, params within 1 ulp."""
+    from gefen import Gefen
+    dtype, rows, cols, period, layout = case
+    gen = torch.Generator().manual_seed(rows * 3 + cols)
+    tdt = TDT[dtype]
+    cb = _codebook()
+    p0 = (torch.randn(rows, cols, generator=gen) * 0.02).to(tdt)
+    p = torch.nn.Parameter(_strided(p0, layout, dev))
+    assert p.stride(0) == 1
+    wd = 0.01
+    opt = Gefen([("w", p)], lr=LR, betas=(B1, B2), eps=EPS, weight_decay=wd, factored_v_2d=False)
+    opt._gefen_codebook = torch.from_numpy(cb).float().to(dev)
+    opt.state[p]["automatic_period"] = period
+    nb = rows * cols // period
+    ref = {"p": p0.float().numpy(), "idx": np.zeros(rows * cols, np.uint8), "mag": np.zeros(nb, np.float32),
+           "vm": np.zeros(nb, np.float32)}
+    for s in range(1, 4):
+        g = (torch.randn(rows, cols, generator=gen) * 10 ** gen_uniform(gen, -4, -2)).to(tdt)
+        p.grad = _strided(g, layout, dev)
+        tag = "block view %s [%d,%d] P=%d %s step %d" % (tdt, rows, cols, period, layout, s)
+        _say("case", tag)
+        opt.step()
+        torch.cuda.synchronize()
+        bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+        p1, i1, m1, v1 = orc.block_step(ref["p"], g.float().numpy(), ref["idx"], ref["mag"], ref["vm"], period,
+                                        cb, dtype, beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd)
+        st = opt.state[p]
+        np.testing.assert_array_equal(st["m_codebook"].cpu().numpy().reshape(-1), i1, err_msg=tag + " idx")
+        np.testing.assert_array_equal(st["m_magnitude"].cpu().numpy().reshape(-1), m1, err_msg=tag + " mag")
+        np.testing.assert_allclose(st["vmean"].cpu().numpy().reshape(-1), v1, rtol=1e-6, err_msg=tag + " vmean")
+        _assert_p(p.detach().float().cpu().numpy(), p1, dtype, tag + " p")
+        ref = {"p": p.detach().float().cpu().numpy(), "idx": i1, "mag": m1, "vm": st["vmean"].cpu().numpy().reshape(-1)}
+
+
 def _run_block(dev, dtype, n, period, wd, steps, seed):
     from gefen.kernels import automatic_gefen_fused as fused
     gen = torch.Generator().manual_seed(seed)
