@@ -76,9 +76,10 @@ struct FactTiles {
     }
 };
 
-// Block-max accumulators are sharded when there are few blocks: workgroup w
-// folds into shard (w % shards), so one huge block is not a single atomic
-// hot spot; the finalize kernels take the max over the shards.
+// Block-max (and block-path sum-of-squares) accumulators are sharded when
+// there are few blocks: workgroup w folds into shard (w % shards), so one huge
+// block is not a single atomic hot spot; the finalize kernels reduce the
+// shards in a fixed order.
 constexpr int64_t kMagShardMaxBlocks = 4096;
 constexpr int64_t kMagShards = 32;
 inline int64_t mag_shards(int64_t nb) { return nb <= kMagShardMaxBlocks ? kMagShards : 1; }
@@ -113,13 +114,14 @@ struct FactoredWs {
 };
 
 struct BlockWs {
-    // double blk_sq[nb] (zero between steps), uint32 magbits[nb] (zero between
-    // steps), float mag_old[nb], float step[nb], float minv[nb]
+    // double blk_sq[shards][nb] (zero between steps), uint32
+    // magbits[shards][nb] (zero between steps), float mag_old[nb], float
+    // step[nb], float minv[nb]
     size_t off_sq, off_magbits, off_magold, off_step, off_minv, total;
     static BlockWs make(int64_t nb) {
         BlockWs w;
         size_t o = 0;
-        w.off_sq = o;      o += align256(sizeof(double) * (size_t)nb);
+        w.off_sq = o;      o += align256(sizeof(double) * (size_t)(nb * mag_shards(nb)));
         w.off_magbits = o; o += align256(sizeof(uint32_t) * (size_t)(nb * mag_shards(nb)));
         w.off_magold = o;  o += align256(sizeof(float) * (size_t)nb);
         w.off_step = o;    o += align256(sizeof(float) * (size_t)nb);

@@ -370,7 +370,8 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
 // Requires R, C, P multiples of 8 and 16-byte aligned storage rows.
 // ====================================================================
 constexpr int kTv = 64;
-constexpr int kTvTilesPerWg = 4;  // apply: consecutive tiles per workgroup
+constexpr int kTvTilesPerWg = 4;   // apply: consecutive tiles per workgroup
+constexpr int kTvLdsBlocks = 512;  // stats: LDS block accumulators per workgroup
 
 template <int DT>
 struct TvTile {
@@ -451,6 +452,8 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
     __shared__ TT s_t[2];
     __shared__ double s_row[kTvStatsMaxRows];
     __shared__ double s_col[kWaves][kTv];
+    __shared__ uint32_t s_bmax[kTvLdsBlocks];
+    __shared__ double s_bsum[MODE == 1 ? kTvLdsBlocks : 1];
     const QTable* qt = wr.qt;
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
     for (int k = threadIdx.x; k < kTvStatsMaxRows; k += kThreads) s_row[k] = 0.0;
@@ -464,11 +467,23 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
     const double invP = wr.invP;
     const MomentumCoef mc = wr.mc;
     uint32_t* mb = wr.magbits + (wg % wr.shards) * wr.nb;
+    double* bsq = MODE == 1 ? wr.blk_sq + (wg % wr.shards) * wr.nb : nullptr;
     const int64_t ctile = wg % wr.ct, rtile = wg / wr.ct;
     const int64_t c_begin = ctile * kFactTileCols;
     const int64_t c_end = std::min<int64_t>(c_begin + kFactTileCols, C);
     const int64_t r_begin = rtile * wr.tile_rows;
     const int64_t r_end = std::min<int64_t>(r_begin + wr.tile_rows, R);
+    // blocks of the region: few of them (large periods) reduce in LDS and
+    // leave with one atomic per block and workgroup
+    const int64_t b_lo = div_floor(r_begin * C + c_begin, P, invP);
+    const int64_t b_span = div_floor((r_end - 1) * C + (c_end - 1), P, invP) - b_lo + 1;
+    const bool lds_blk = b_span <= kTvLdsBlocks;
+    if (lds_blk) {
+        for (int k = threadIdx.x; k < b_span; k += kThreads) {
+            s_bmax[k] = 0u;
+            if constexpr (MODE == 1) s_bsum[k] = 0.0;
+        }
+    }
     const int n_rb = (int)((r_end - r_begin + kTv - 1) / kTv);
     const int n_sub = (int)((c_end - c_begin + kTv - 1) / kTv) * n_rb;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -565,9 +580,16 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
             }
             const int64_t pb = __shfl_up(b, 1, kChunk);
             if (b >= 0 && (jc == 0 || pb != b)) {
-                if (m != 0u) atomicMax(mb + b, m);
-                if constexpr (MODE == 1) {
-                    if (rsd != 0.0) atomicAdd(wr.blk_sq + b, rsd);
+                if (lds_blk) {
+                    if (m != 0u) atomicMax(&s_bmax[b - b_lo], m);
+                    if constexpr (MODE == 1) {
+                        if (rsd != 0.0) atomicAdd(&s_bsum[b - b_lo], rsd);
+                    }
+                } else {
+                    if (m != 0u) atomicMax(mb + b, m);
+                    if constexpr (MODE == 1) {
+                        if (rsd != 0.0) atomicAdd(bsq + b, rsd);
+                    }
                 }
             }
         }
@@ -597,9 +619,19 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
         }
         cur = nxt;
     }
+    __syncthreads();
     if constexpr (MODE == 0) {
-        __syncthreads();
         for (int64_t r = r_begin + tid; r < r_end; r += kThreads) *gbl(row_part + ctile * R + r) = s_row[r - r_begin];
+    }
+    if (lds_blk) {
+        for (int k = tid; k < b_span; k += kThreads) {
+            const uint32_t m = s_bmax[k];
+            if (m != 0u) atomicMax(mb + b_lo + k, m);
+            if constexpr (MODE == 1) {
+                const double v = s_bsum[k];
+                if (v != 0.0) atomicAdd(bsq + b_lo + k, v);
+            }
+        }
     }
 }
 
@@ -619,6 +651,7 @@ __device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int
     const double invP = w.invP;
     const MomentumCoef mc = w.mc;
     uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
+    double* bsq = w.blk_sq + (wg % w.shards) * w.nb;
     const int64_t nchunks = (N + kChunk - 1) / kChunk;
     const int64_t stride = nwg * kThreads;
     int64_t cur = -1;
@@ -650,7 +683,7 @@ __device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int
                     if (cur >= 0) {
                         bsum += (double)csum;
                         csum = 0.0f;
-                        if (bsum != 0.0) atomicAdd(w.blk_sq + cur, bsum);
+                        if (bsum != 0.0) atomicAdd(bsq + cur, bsum);
                         if (cbits) atomicMax(mb + cur, cbits);
                     }
                     bsum = 0.0;
@@ -675,11 +708,11 @@ __device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int
         const double s = wave_sum_d(bsum);
         const uint32_t m = wave_max_u(cbits);
         if (lane == 0 && c0 >= 0) {
-            if (s != 0.0) atomicAdd(w.blk_sq + c0, s);
+            if (s != 0.0) atomicAdd(bsq + c0, s);
             if (m) atomicMax(mb + c0, m);
         }
     } else if (cur >= 0) {
-        if (bsum != 0.0) atomicAdd(w.blk_sq + cur, bsum);
+        if (bsum != 0.0) atomicAdd(bsq + cur, bsum);
         if (cbits) atomicMax(mb + cur, cbits);
     }
 }
@@ -705,12 +738,15 @@ template <int DT>
 __device__ __forceinline__ void stats_block_fast(const TensorWork& w, int64_t wg) {
     using T = typename Elem<DT>::T;
     __shared__ float s_cbr[kCodebookMax];
+    __shared__ int64_t s_wblk[kWaves];
+    __shared__ uint32_t s_wbits[kWaves];
+    __shared__ double s_wsum[kWaves];
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(w.qt->cbr + threadIdx.x);
     __syncthreads();
     const T* g = static_cast<const T*>(w.grad);
     const uint8_t* idxp = w.idx;
     const float* mag = w.mag;
-    double* bsq = w.blk_sq;
+    double* bsq = w.blk_sq + (wg % w.shards) * w.nb;
     const int64_t P = w.P;
     const MomentumCoef mc = w.mc;
     uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
@@ -773,7 +809,35 @@ __device__ __forceinline__ void stats_block_fast(const TensorWork& w, int64_t wg
         blk += dB;
         if (pin >= P) { pin -= P; ++blk; }
     }
-    bstats_flush(mb, bsq, wblk, wbits, wsum);
+    // last run of each wave: one atomic pair per workgroup when the waves agree
+    const uint32_t rb = wblk >= 0 ? wave_max_u63(wbits) : 0u;
+    const double rs = wblk >= 0 ? wave_sum_d63(wsum) : 0.0;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 63) {
+        s_wblk[wave] = wblk;
+        s_wbits[wave] = rb;
+        s_wsum[wave] = rs;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        bool same = true;
+        for (int ww = 1; ww < kWaves; ++ww) same = same && (s_wblk[ww] == s_wblk[0]);
+        for (int ww = 0; ww < kWaves; ++ww) {
+            const int64_t b = s_wblk[ww];
+            if (b < 0) continue;
+            uint32_t m = s_wbits[ww];
+            double t = s_wsum[ww];
+            if (same) {
+                if (ww > 0) break;
+                for (int v = 1; v < kWaves; ++v) {
+                    m = s_wbits[v] > m ? s_wbits[v] : m;
+                    t += s_wsum[v];
+                }
+            }
+            if (m) atomicMax(mb + b, m);
+            if (t != 0.0) atomicAdd(bsq + b, t);
+        }
+    }
 }
 
 __device__ __forceinline__ bool block_stats_fast_ok(const TensorWork& w) {
@@ -856,8 +920,12 @@ __device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) 
     const StepScalars sc = read_scalars(w);
     const float fP = (float)w.P;
     for (int64_t b = wg * kThreads + threadIdx.x; b < w.nb; b += w.nbw * kThreads) {
-        float mean = (float)w.blk_sq[b] / fP;
-        w.blk_sq[b] = 0.0;
+        double sq = 0.0;
+        for (int64_t sh = 0; sh < w.shards; ++sh) {
+            sq += w.blk_sq[sh * w.nb + b];
+            w.blk_sq[sh * w.nb + b] = 0.0;
+        }
+        float mean = (float)sq / fP;
         if (w.bf16_mean) mean = round_dt<BF16>(mean);
         const float v = __builtin_fmaf(mean, w.alpha2, w.v0[b] * w.beta2);
         w.v0[b] = v;
