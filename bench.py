@@ -80,17 +80,82 @@ def fill_grads(torch, params, step_seed, device):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gefen_step_llama3_8b_traffic.json")
+APPLY_KERNEL = "k_mt_apply<2, 0, false, true>"  # bf16, factored, nearest rounding, contiguous fast path
+KERNEL_SOURCES = ("gefenx_update.hip", "gefenx_device.h", "gefenx_common.h")
+
+
+def _kernel_source_sha():
+    """sha256 over the sources of the step kernels: a committed traffic
+    measurement counts only for the kernels it was taken on."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, "gefen-x_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
 
 
 def _measured_traffic():
     """HBM bytes per launch of the factored apply from the committed rocprofv3
     PMC passes (FETCH_SIZE x its copy-calibrated scale + WRITE_SIZE x its
-    scale), or None when no measurement is committed."""
+    scale); None when no measurement is committed or it was taken on other
+    kernel sources."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return float(json.load(f)["apply_traffic_bytes_per_launch"])
-    except (OSError, KeyError, ValueError):
+            t = json.load(f)
+    except (OSError, ValueError):
         return None
+    if t.get("kernel_source_sha256") != _kernel_source_sha():
+        _log("bench: %s was measured on other kernel sources; traffic reported as null" %
+             os.path.relpath(TRAFFIC_FILE, ROOT))
+        return None
+    try:
+        return float(t["apply_traffic_bytes_per_launch"])
+    except (KeyError, ValueError, TypeError):
+        return None
+
+
+def _pmc_avg(path, counter, pattern):
+    """Average per dispatch of `counter` over the kernels whose name contains
+    `pattern`, from a rocprofv3 --pmc csv (a file, or a directory searched for
+    *counter_collection.csv)."""
+    import csv
+    import glob
+    files = [path] if os.path.isfile(path) else sorted(glob.glob(os.path.join(path, "**", "*counter_collection.csv"),
+                                                                 recursive=True))
+    vals = []
+    for fn in files:
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter and pattern in r["Kernel_Name"]:
+                    vals.append(float(r["Counter_Value"]))
+    if not vals:
+        raise SystemExit("no %s rows for kernels matching %r under %s" % (counter, pattern, path))
+    return sum(vals) / len(vals), len(vals)
+
+
+def write_traffic(fetch, write, copy_fetch, copy_write):
+    """Combine the four PMC passes (the bench's apply kernel: FETCH_SIZE,
+    WRITE_SIZE; the --calibrate-copy run: FETCH_SIZE, WRITE_SIZE) into the
+    committed traffic figure.  Counters are KiB per dispatch; each is scaled
+    so that the plain 1 GiB copy reads and writes exactly 1 GiB."""
+    copy_bytes = float(1 << 30)
+    cf, _ = _pmc_avg(copy_fetch, "FETCH_SIZE", "copyBuffer")
+    cw, _ = _pmc_avg(copy_write, "WRITE_SIZE", "copyBuffer")
+    sf, sw = copy_bytes / (cf * 1024.0), copy_bytes / (cw * 1024.0)
+    af, nf = _pmc_avg(fetch, "FETCH_SIZE", APPLY_KERNEL)
+    aw, nw = _pmc_avg(write, "WRITE_SIZE", APPLY_KERNEL)
+    out = {"kernel": APPLY_KERNEL, "dispatches": [nf, nw],
+           "fetch_kib_per_dispatch": af, "write_kib_per_dispatch": aw,
+           "copy_fetch_kib": cf, "copy_write_kib": cw, "fetch_scale": sf, "write_scale": sw,
+           "apply_read_bytes_per_launch": af * 1024.0 * sf, "apply_write_bytes_per_launch": aw * 1024.0 * sw,
+           "apply_traffic_bytes_per_launch": af * 1024.0 * sf + aw * 1024.0 * sw,
+           "kernel_source_sha256": _kernel_source_sha()}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(json.dumps(out))
+    return 0
 
 
 def cpu_baseline(seconds: float = 12.0):
@@ -293,7 +358,12 @@ def main(argv=None):
                     help="gefen: configs[1], the headline Llama-3-8B Gefen step (default); "
                          "muon: configs[3], GefenMuonHybrid with MFMA utilisation; "
                          "qwen: configs[2], the many-tensor Qwen3-4B set, factored on and off")
+    ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="write the committed traffic figure from four rocprofv3 --pmc csv outputs (the bench's "
+                         "FETCH_SIZE and WRITE_SIZE passes, then --calibrate-copy's) and exit")
     args = ap.parse_args(argv)
+    if args.traffic_from:
+        return write_traffic(*args.traffic_from)
     if args.calibrate_copy:
         import torch
         src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")  # 1 GiB
