@@ -292,6 +292,21 @@ __device__ __forceinline__ double wave_sum_d63(double v) {
     v += dpp64<0x143, 0xc>(v);
     return v;
 }
+// sum over each aligned group of 8 lanes, in all 8 (every lane adds the same
+// two operands at each step, so the 8 results are bitwise equal)
+__device__ __forceinline__ double group8_sum_d(double v) {
+    v += dpp64<0xB1, 0xf>(v);
+    v += dpp64<0x4E, 0xf>(v);
+    v += dpp64<0x141, 0xf>(v);
+    return v;
+}
+// sum over the wave, in every lane (lane 63's DPP total, read as a scalar)
+__device__ __forceinline__ double wave_allsum_d(double v) {
+    const uint64_t b = (uint64_t)__double_as_longlong(wave_sum_d63(v));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
 // max over the wave, valid in lane 63
 __device__ __forceinline__ uint32_t wave_max_u63(uint32_t v) {
     uint32_t o;

@@ -22,56 +22,234 @@ __device__ __forceinline__ float load_elem(const void* base, int64_t i) {
 // err(p) = sqrt(mean_b var_b(x)), x = fp32(g)^2 widened to float64
 // (partitioning.py:62-84 via gefen.py:2639-2655).
 
-// Small periods (P <= kWavePeriod): one wave per block, numpy's two-pass
-// variance (mean, then mean squared deviation) in float64.
+// Small periods: numpy's two-pass variance (mean, then mean squared
+// deviation) per block in float64 (k_var_tile).  Every workgroup reduces its blocks'
+// variances in LDS and writes one partial (no shared-address atomics); the
+// partials of a period are summed in a fixed order by k_var_sum.
 constexpr int64_t kWavePeriod = 4096;
+constexpr int64_t kThreadPeriod = 64;   // below: a thread per block
+constexpr int64_t kGroupPeriod = 512;   // below: 8 lanes per block; from here a wave per block
 constexpr int64_t kSeg = 65536;  // elements per workgroup segment of a large block
+constexpr int kVarGrid = 2048;   // workgroups (and partials) per small-period pass
+
+__device__ __forceinline__ void var_partial(double acc, double* part) {
+    __shared__ double sh[kT / 64];
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < kT / 64; ++w) t += sh[w];
+        part[blockIdx.x] = t;
+    }
+}
+
+// One kernel for every P <= kWavePeriod: a workgroup takes tiles of whole
+// blocks (about kVarTile elements) and stages their raw elements in LDS --
+// 16-byte loads from the 16-byte boundary below the tile, lanes outside it
+// dropped, the next tile's loads in flight during this tile's math -- then
+// runs the two passes from LDS on x = fp32(g)^2: a thread per block when
+// P < 64 (rows padded to an odd pitch, so the threads' strided reads fall in
+// distinct banks), 8 lanes per block when P < 512, a wave per block otherwise.
+constexpr int kVarTile = 8192;
 
 template <int DT>
-__global__ void __launch_bounds__(kT) k_var_wave(const void* g, int64_t nb, int64_t P, double* total) {
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = ((int64_t)blockIdx.x * kT + threadIdx.x) >> 6;
-    const int64_t nwaves = ((int64_t)gridDim.x * kT) >> 6;
+struct VarTile {
+    using T = typename Elem<DT>::T;
+    static constexpr int kPerVec = 16 / (int)sizeof(T);                      // elements per 16-byte load
+    static constexpr int kVecs = (kVarTile + 2 * kPerVec) / kPerVec;          // covers any alignment
+    static constexpr int kVecPerThread = (kVecs + kT - 1) / kT;
+};
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_var_tile(const void* g, int64_t nb, int64_t P, double* part) {
+    using T = typename Elem<DT>::T;
+    using VT = VarTile<DT>;
+    __shared__ T sx[kVarTile + kVarTile / 2];
+    const T* gt = static_cast<const T*>(g);
+    const int Pi = (int)P;
+    const bool thread_blocks = P < kThreadPeriod;
+    const int pitch = thread_blocks ? (Pi | 1) : Pi;
+    const int nbt = kVarTile / Pi;                                            // blocks per tile
+    const uint32_t magic = ((1u << 19) + (uint32_t)Pi - 1u) / (uint32_t)Pi;  // e / P for e < 2^13, P < 64
+    const int64_t ntiles = (nb + nbt - 1) / nbt;
+    const int64_t total = nb * P;
+    const double fP = (double)P;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t misalign = (int64_t)((((uintptr_t)gt) & 15) / sizeof(T));  // base pointer offset in elements
     double acc = 0.0;
-    for (int64_t b = wave; b < nb; b += nwaves) {
-        const int64_t base = b * P;
-        double s = 0.0;
-        for (int64_t j = lane; j < P; j += 64) {
-            const float v = load_elem<DT>(g, base + j);
-            s += (double)(v * v);
+
+    u32x4 cur[VT::kVecPerThread], nxt[VT::kVecPerThread];
+    int64_t a_cur = 0, a_nxt = 0;  // element index (relative to gt) of vector 0
+    auto fetch = [&](int64_t tile, u32x4* v, int64_t& a0) {
+        const int64_t base = tile * nbt * P;
+        const int64_t hi = std::min<int64_t>(base + (int64_t)nbt * P, total);
+        a0 = ((base + misalign) & ~(int64_t)(VT::kPerVec - 1)) - misalign;  // 16-byte aligned address
+#pragma unroll
+        for (int q = 0; q < VT::kVecPerThread; ++q) {
+            const int64_t e0 = a0 + (int64_t)(tid + q * kT) * VT::kPerVec;
+            v[q] = u32x4{0u, 0u, 0u, 0u};
+            if (e0 + VT::kPerVec > base && e0 < hi) {
+                if (e0 >= 0 && e0 + VT::kPerVec <= total) {
+                    v[q] = *gbl(reinterpret_cast<const u32x4*>(gt + e0));
+                } else {  // a vector straddling the tensor's ends: element loads
+                    T tmp[VT::kPerVec];
+#pragma unroll
+                    for (int k = 0; k < VT::kPerVec; ++k) {
+                        const int64_t e = e0 + k;
+                        tmp[k] = (e >= 0 && e < total) ? gt[e] : T(0);
+                    }
+                    __builtin_memcpy(&v[q], tmp, sizeof(tmp));
+                }
+            }
         }
-        const double mean = wave_sum_d(s) / (double)P;
-        double d2 = 0.0;
-        for (int64_t j = lane; j < P; j += 64) {
-            const float v = load_elem<DT>(g, base + j);
-            const double d = (double)(v * v) - mean;
-            d2 += d * d;
+    };
+
+    int64_t tile = blockIdx.x;
+    if (tile < ntiles) fetch(tile, cur, a_cur);
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t b0 = tile * nbt;
+        const int nbl = (int)std::min<int64_t>(nbt, nb - b0);
+        const int elems = nbl * Pi;
+        const int64_t base = b0 * P;
+        // stage this tile's elements
+#pragma unroll
+        for (int q = 0; q < VT::kVecPerThread; ++q) {
+            const T* el = reinterpret_cast<const T*>(&cur[q]);
+            const int64_t e0 = a_cur + (int64_t)(tid + q * kT) * VT::kPerVec - base;
+#pragma unroll
+            for (int k = 0; k < VT::kPerVec; ++k) {
+                const int64_t e = e0 + k;
+                if (e >= 0 && e < elems) {
+                    const int ei = (int)e;
+                    const int at = thread_blocks ? ei + (pitch - Pi) * (int)(((uint32_t)ei * magic) >> 19) : ei;
+                    sx[at] = el[k];
+                }
+            }
         }
-        d2 = wave_sum_d(d2);
-        if (lane == 0) acc += d2 / (double)P;
+        __syncthreads();
+        if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x, nxt, a_nxt);
+        if (thread_blocks) {
+            for (int bl = tid; bl < nbl; bl += kT) {
+                const T* x = sx + bl * pitch;
+                double s = 0.0;
+                for (int j = 0; j < Pi; ++j) {
+                    const float v = to_f32<DT>(x[j]);
+                    s += (double)(v * v);
+                }
+                const double mean = s / fP;
+                double d2 = 0.0;
+                for (int j = 0; j < Pi; ++j) {
+                    const float v = to_f32<DT>(x[j]);
+                    const double d = (double)(v * v) - mean;
+                    d2 += d * d;
+                }
+                acc += d2 / fP;
+            }
+        } else if (P < kGroupPeriod) {
+            const int gl = lane & 7;
+            for (int bl = wave * 8 + (lane >> 3); bl < nbl; bl += kT / 8) {
+                const T* x = sx + bl * pitch;
+                double s = 0.0;
+                for (int j = gl; j < Pi; j += 8) {
+                    const float v = to_f32<DT>(x[j]);
+                    s += (double)(v * v);
+                }
+                const double mean = group8_sum_d(s) / fP;
+                double d2 = 0.0;
+                for (int j = gl; j < Pi; j += 8) {
+                    const float v = to_f32<DT>(x[j]);
+                    const double d = (double)(v * v) - mean;
+                    d2 += d * d;
+                }
+                d2 = group8_sum_d(d2);
+                if (gl == 0) acc += d2 / fP;
+            }
+        } else {
+            for (int bl = wave; bl < nbl; bl += kT / 64) {
+                const T* x = sx + bl * pitch;
+                double s = 0.0;
+                for (int j = lane; j < Pi; j += 64) {
+                    const float v = to_f32<DT>(x[j]);
+                    s += (double)(v * v);
+                }
+                const double mean = wave_allsum_d(s) / fP;
+                double d2 = 0.0;
+                for (int j = lane; j < Pi; j += 64) {
+                    const float v = to_f32<DT>(x[j]);
+                    const double d = (double)(v * v) - mean;
+                    d2 += d * d;
+                }
+                d2 = wave_sum_d63(d2);
+                if (lane == 63) acc += d2 / fP;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < VT::kVecPerThread; ++q) cur[q] = nxt[q];
+        a_cur = a_nxt;
     }
-    if (lane == 0 && acc != 0.0) atomicAdd(total, acc);
+    var_partial(acc, part);
+}
+
+// totals[i] = sum of the n partials of period i, in index order (one wave per period).
+__global__ void __launch_bounds__(64) k_var_sum(const double* part, int n, double* totals) {
+    const double* q = part + (int64_t)blockIdx.x * kVarGrid;
+    double t = 0.0;
+    for (int k = threadIdx.x; k < n; k += 64) t += q[k];
+    t = wave_sum_d(t);
+    if (threadIdx.x == 0) totals[blockIdx.x] += t;
 }
 
 // Large periods: one workgroup per kSeg-element segment of a block; float64
 // (sum, sum of squares) per segment, combined per block with two atomics.
+// Segments whose start is 16-byte aligned and whose length is a multiple of
+// 8 read 8 elements per load (two loads in flight per thread).
 template <int DT>
 __global__ void __launch_bounds__(kT) k_var_seg(const void* g, int64_t P, int64_t segs_per_block,
                                                double* s1, double* s2) {
+    using T = typename Elem<DT>::T;
     __shared__ double sh[2][kT / 64];
     const int64_t b = (int64_t)blockIdx.x / segs_per_block;
     const int64_t sg = (int64_t)blockIdx.x - b * segs_per_block;
     const int64_t lo = b * P + sg * kSeg;
     const int64_t hi = std::min<int64_t>(lo + kSeg, (b + 1) * P);
-    double a1 = 0.0, a2 = 0.0;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += kT) {
-        const float v = load_elem<DT>(g, i);
-        const double x = (double)(v * v);
-        a1 += x;
-        a2 += x * x;
+    double a1 = 0.0, a2 = 0.0, c1 = 0.0, c2 = 0.0;
+    const T* gt = static_cast<const T*>(g);
+    if ((((uintptr_t)(gt + lo)) & 15) == 0 && ((hi - lo) & 7) == 0) {
+        const int64_t nch = (hi - lo) >> 3;
+        int64_t c = threadIdx.x;
+        for (; c + kT < nch; c += 2 * kT) {
+            float x[8], y[8];
+            load8<DT>(gt + lo + c * 8, x);
+            load8<DT>(gt + lo + (c + kT) * 8, y);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const double p = (double)(x[k] * x[k]);
+                const double q = (double)(y[k] * y[k]);
+                a1 += p; a2 += p * p;
+                c1 += q; c2 += q * q;
+            }
+        }
+        if (c < nch) {
+            float x[8];
+            load8<DT>(gt + lo + c * 8, x);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const double p = (double)(x[k] * x[k]);
+                a1 += p; a2 += p * p;
+            }
+        }
+    } else {
+        for (int64_t i = lo + threadIdx.x; i < hi; i += kT) {
+            const float v = load_elem<DT>(g, i);
+            const double x = (double)(v * v);
+            a1 += x;
+            a2 += x * x;
+        }
     }
-    a1 = wave_sum_d(a1);
-    a2 = wave_sum_d(a2);
+    a1 = wave_sum_d(a1 + c1);
+    a2 = wave_sum_d(a2 + c2);
     if ((threadIdx.x & 63) == 0) { sh[0][threadIdx.x >> 6] = a1; sh[1][threadIdx.x >> 6] = a2; }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -268,27 +446,39 @@ int gefenx_block_variance_errors(const void* grad, int dtype, int64_t numel, con
             return set_error(GEFENX_EINVAL, "period %lld does not divide numel %lld", (long long)P, (long long)numel);
         if (P > kWavePeriod) max_nb = std::max<int64_t>(max_nb, numel / P);
     }
-    double* dev = nullptr;  // [n_periods] totals, then 2 * max_nb block sums
-    const size_t bytes = sizeof(double) * ((size_t)n_periods + 2 * (size_t)max_nb + 1);
+    // [n_periods] totals, [n_periods][kVarGrid] small-period partials (zero
+    // where a pass uses fewer workgroups), then 2 * max_nb block sums
+    double* dev = nullptr;
+    const int64_t n_part = (int64_t)n_periods * kVarGrid;
+    const size_t bytes = sizeof(double) * ((size_t)n_periods + (size_t)n_part + 2 * (size_t)max_nb + 1);
     if (hipMalloc(&dev, bytes) != hipSuccess)
         return set_error(GEFENX_ENOMEM, "gefenx_block_variance_errors: hipMalloc(%zu) failed", bytes);
     double* totals = dev;
-    double* s1 = dev + n_periods;
+    double* part = dev + n_periods;
+    double* s1 = part + n_part;
     double* s2 = s1 + max_nb;
-    const int64_t fill = (int64_t)n_periods + 2 * max_nb;
+    const int64_t fill = (int64_t)n_periods + n_part + 2 * max_nb;
     hipLaunchKernelGGL(k_zero_f64, dim3(grid_cap(fill, kT, 4096)), dim3(kT), 0, s, dev, fill);
+    bool any_small = false;
     for (int i = 0; i < n_periods && rc == GEFENX_OK; ++i) {
         const int64_t P = periods[i];
         const int64_t nb = numel / P;
         if (P == 1) continue;  // single-element blocks have zero variance
+        double* pi = part + (int64_t)i * kVarGrid;
         if (P <= kWavePeriod) {
-            GX_DISPATCH(dtype, k_var_wave, dim3(grid_cap(nb * 64, kT, 16384)), dim3(kT), s, grad, nb, P, totals + i);
+            const int64_t tiles = (nb + kVarTile / P - 1) / (kVarTile / P);
+            GX_DISPATCH(dtype, k_var_tile, dim3(grid_cap(tiles, 1, kVarGrid)), dim3(kT), s, grad, nb, P, pi);
+            any_small = true;
         } else {
             const int64_t spb = (P + kSeg - 1) / kSeg;
             GX_DISPATCH(dtype, k_var_seg, dim3((unsigned)(nb * spb)), dim3(kT), s, grad, P, spb, s1, s2);
             hipLaunchKernelGGL(k_var_finish, dim3(grid_cap(nb, kT, 4096)), dim3(kT), 0, s, s1, s2, nb, P, totals + i);
         }
         rc = check("block variance");
+    }
+    if (rc == GEFENX_OK && any_small && n_periods > 0) {
+        hipLaunchKernelGGL(k_var_sum, dim3((unsigned)n_periods), dim3(64), 0, s, part, kVarGrid, totals);
+        rc = check("block variance sum");
     }
     std::vector<double> host((size_t)std::max(n_periods, 1));
     if (rc == GEFENX_OK && n_periods > 0) {
