@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "gefenx_common.h"
+#include "gefenx_dp.h"
 #include "gefenx_internal.h"
 #include "../../include/gefenx.h"
 
@@ -210,26 +211,11 @@ int gefenx_exact_dp(const float* active_centers, const float* active_counts,
         if (!(active_counts[i] > 0.0f))
             return set_error(GEFENX_EINVAL, "exact DP expects strictly positive counts for all active histogram bins.");
     if (k > n_points) {
-        // _build_padded_codebook: quantization.py:59-72
-        std::vector<float> cb((size_t)k);
-        for (int i = 0; i < k; ++i) cb[(size_t)i] = active_centers[std::min(i, n_points - 1)];
-        if (force_endpoints) { cb[0] = -1.0f; cb[(size_t)k - 1] = 1.0f; }
-        std::sort(cb.begin(), cb.end());
-        std::copy(cb.begin(), cb.end(), codebook_out);
+        dp_padded(active_centers, n_points, k, force_endpoints, codebook_out);
         return GEFENX_OK;
     }
     const int n = n_points;
-    std::vector<double> pw((size_t)n + 1, 0.0), pwx((size_t)n + 1, 0.0), pwx2((size_t)n + 1, 0.0);
-    double aw = 0.0, awx = 0.0, awx2 = 0.0;  // torch.cumsum: sequential float64 scan
-    for (int i = 0; i < n; ++i) {
-        const double w = (double)active_counts[i];
-        const double c = (double)active_centers[i];
-        const double wx = w * c;
-        const double cc = c * c;
-        const double wx2 = w * cc;
-        aw += w; awx += wx; awx2 += wx2;
-        pw[(size_t)i + 1] = aw; pwx[(size_t)i + 1] = awx; pwx2[(size_t)i + 1] = awx2;
-    }
+    const DpPrefix pre = dp_prefix(active_centers, active_counts, n);
     const size_t W = (size_t)n + 1;
     std::vector<double> prev(W, std::numeric_limits<double>::infinity()), cur(W);
     std::vector<int32_t> bt((size_t)(k + 1) * W, -1);
@@ -238,27 +224,15 @@ int gefenx_exact_dp(const float* active_centers, const float* active_counts,
     const int nthreads = (int)std::max(1u, std::min(hw ? hw : 1u, 16u));
     for (int c = 1; c <= k; ++c) {
         std::fill(cur.begin(), cur.end(), std::numeric_limits<double>::infinity());
+        const bool endpoint = force_endpoints && (c == 1 || c == k);
+        const double fc = (c == 1) ? -1.0 : 1.0;
         auto work = [&](int tid) {
             for (int end = c + tid; end <= n; end += nthreads) {
                 double best = std::numeric_limits<double>::infinity();
                 int32_t best_start = -1;
                 for (int s = c; s <= end; ++s) {
-                    const double sw = pw[(size_t)end] - pw[(size_t)s - 1];
-                    const double swx = pwx[(size_t)end] - pwx[(size_t)s - 1];
-                    const double swx2 = pwx2[(size_t)end] - pwx2[(size_t)s - 1];
-                    double cost;
-                    if (force_endpoints && (c == 1 || c == k)) {
-                        const double fc = (c == 1) ? -1.0 : 1.0;
-                        const double t1 = 2.0 * fc;
-                        const double t2 = t1 * swx;
-                        const double t3 = fc * fc;
-                        const double t4 = t3 * sw;
-                        cost = (swx2 - t2) + t4;
-                    } else {
-                        const double sq = swx * swx;
-                        cost = swx2 - sq / sw;
-                    }
-                    const double cand = prev[(size_t)s - 1] + cost;
+                    const double cand = prev[(size_t)s - 1] +
+                                        dp_cost(pre.pw.data(), pre.pwx.data(), pre.pwx2.data(), s, end, endpoint, fc);
                     if (cand < best) { best = cand; best_start = s; }
                 }
                 cur[(size_t)end] = best;
@@ -274,22 +248,8 @@ int gefenx_exact_dp(const float* active_centers, const float* active_counts,
         }
         std::swap(prev, cur);
     }
-    std::vector<float> cb((size_t)k);
-    int64_t end = n;
-    for (int c = k; c >= 1; --c) {
-        const int64_t s = bt[(size_t)c * W + (size_t)end];
-        if (force_endpoints && c == 1) cb[(size_t)c - 1] = -1.0f;
-        else if (force_endpoints && c == k) cb[(size_t)c - 1] = 1.0f;
-        else {
-            if (s < 1) return set_error(GEFENX_EINVAL, "gefenx_exact_dp: infeasible segmentation");
-            const double sw = pw[(size_t)end] - pw[(size_t)s - 1];
-            const double swx = pwx[(size_t)end] - pwx[(size_t)s - 1];
-            cb[(size_t)c - 1] = (float)(swx / sw);
-        }
-        end = s - 1;
-    }
-    std::sort(cb.begin(), cb.end());
-    std::copy(cb.begin(), cb.end(), codebook_out);
+    if (!dp_backtrack(pre, bt.data(), W, n, k, force_endpoints, codebook_out))
+        return set_error(GEFENX_EINVAL, "gefenx_exact_dp: infeasible segmentation");
     return GEFENX_OK;
 }
 

@@ -2,11 +2,13 @@
 // the block-absmax-normalised histogram the exact-DP codebook is learned from,
 // plus the standalone second-moment EMAs.
 #include "gefenx_device.h"
+#include "gefenx_dp.h"
 #include "gefenx_internal.h"
 #include "../../include/gefenx.h"
 
 #include <algorithm>
 #include <cmath>
+#include <limits>
 #include <vector>
 
 namespace gx {
@@ -401,6 +403,42 @@ __global__ void __launch_bounds__(kT) k_vmean(float* vmean, const void* g, int64
     }
 }
 
+// ---------------------------------------------------------- exact DP
+// Level c of the exact-DP codebook solver (quantization.py:75-139) for every
+// segment end at once: one wave per end, lanes over the segment starts s,
+// each lane keeping its first strict minimum of prev[s-1] + cost(s, end); the
+// wave then takes the (value, start) lexicographic minimum, which is the
+// sequential scan's first minimum.  Costs are the host solver's operations
+// in the same order (dp_cost), so values and choices are bit-identical.
+__global__ void __launch_bounds__(kT) k_dp_level(const double* __restrict__ pw, const double* __restrict__ pwx,
+                                                const double* __restrict__ pwx2, const double* __restrict__ prev,
+                                                double* __restrict__ cur, int32_t* __restrict__ bt_row, int c, int n,
+                                                int endpoint, double fc) {
+    const int lane = threadIdx.x & 63;
+    const int64_t w = ((int64_t)blockIdx.x * kT + threadIdx.x) >> 6;
+    const int end = c + (int)w;
+    if (end > n) return;  // whole waves
+    double best = __builtin_huge_val();
+    int best_s = -1;
+    for (int s = c + lane; s <= end; s += 64) {
+        const double cand = prev[s - 1] + dp_cost(pw, pwx, pwx2, s, end, endpoint != 0, fc);
+        if (cand < best) { best = cand; best_s = s; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const double ob = __shfl_xor(best, off, 64);
+        const int os = __shfl_xor(best_s, off, 64);
+        if (ob < best || (ob == best && os >= 0 && (best_s < 0 || os < best_s))) {
+            best = ob;
+            best_s = os;
+        }
+    }
+    if (lane == 0) {
+        cur[end] = best;
+        bt_row[end] = best_s;
+    }
+}
+
 static int grid_cap(int64_t items, int per, int cap) {
     int64_t g = (items + per - 1) / per;
     return (int)std::max<int64_t>(1, std::min<int64_t>(g, cap));
@@ -551,6 +589,65 @@ int gefenx_vmean_update(float* vmean, const void* grad, int dtype, int64_t numel
     GX_DISPATCH(dtype, k_vmean, dim3(grid_cap(nb * 64, kT, 8192)), dim3(kT), s, vmean, grad, nb, period,
                 (float)beta2, (float)(1.0 - beta2));
     return check("gefenx_vmean_update");
+}
+
+int gefenx_exact_dp_device(const float* active_centers, const float* active_counts, int n_points, int k,
+                           int force_endpoints, float* codebook_out, void* stream) {
+    if (!active_centers || !active_counts || !codebook_out || n_points < 1 || k < 1)
+        return set_error(GEFENX_EINVAL, "gefenx_exact_dp_device: bad arguments (n=%d k=%d)", n_points, k);
+    for (int i = 0; i < n_points; ++i)
+        if (!(active_counts[i] > 0.0f))
+            return set_error(GEFENX_EINVAL, "exact DP expects strictly positive counts for all active histogram bins.");
+    if (k > n_points) {
+        dp_padded(active_centers, n_points, k, force_endpoints, codebook_out);
+        return GEFENX_OK;
+    }
+    const int n = n_points;
+    const DpPrefix pre = dp_prefix(active_centers, active_counts, n);
+    const size_t W = (size_t)n + 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // device: pw, pwx, pwx2, prev, cur (double [W] each), bt (int32 [k+1][W])
+    const size_t dbytes = sizeof(double) * 5 * W;
+    const size_t btbytes = sizeof(int32_t) * (size_t)(k + 1) * W;
+    char* dev = nullptr;
+    if (hipMalloc((void**)&dev, dbytes + btbytes) != hipSuccess)
+        return set_error(GEFENX_ENOMEM, "gefenx_exact_dp_device: hipMalloc(%zu) failed", dbytes + btbytes);
+    double* d_pw = reinterpret_cast<double*>(dev);
+    double* d_pwx = d_pw + W;
+    double* d_pwx2 = d_pwx + W;
+    double* d_prev = d_pwx2 + W;
+    double* d_cur = d_prev + W;
+    int32_t* d_bt = reinterpret_cast<int32_t*>(dev + dbytes);
+    std::vector<double> prev0(W, std::numeric_limits<double>::infinity());
+    prev0[0] = 0.0;
+    std::vector<int32_t> bt((size_t)(k + 1) * W, -1);
+    int rc = GEFENX_OK;
+    if (hipMemcpyAsync(d_pw, pre.pw.data(), sizeof(double) * W, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(d_pwx, pre.pwx.data(), sizeof(double) * W, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(d_pwx2, pre.pwx2.data(), sizeof(double) * W, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(d_prev, prev0.data(), sizeof(double) * W, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(d_bt, bt.data(), btbytes, hipMemcpyHostToDevice, s) != hipSuccess)
+        rc = set_error(GEFENX_ELAUNCH, "gefenx_exact_dp_device: upload failed");
+    for (int c = 1; c <= k && rc == GEFENX_OK; ++c) {
+        const int ends = n - c + 1;
+        if (ends > 0) {
+            const bool endpoint = force_endpoints && (c == 1 || c == k);
+            const double fc = (c == 1) ? -1.0 : 1.0;
+            hipLaunchKernelGGL(k_dp_level, dim3((unsigned)(((int64_t)ends * 64 + kT - 1) / kT)), dim3(kT), 0, s,
+                               d_pw, d_pwx, d_pwx2, d_prev, d_cur, d_bt + (size_t)c * W, c, n, endpoint ? 1 : 0, fc);
+            rc = check("exact DP level");
+        }
+        std::swap(d_prev, d_cur);
+    }
+    if (rc == GEFENX_OK && (hipMemcpyAsync(bt.data(), d_bt, btbytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                            hipStreamSynchronize(s) != hipSuccess))
+        rc = set_error(GEFENX_ELAUNCH, "gefenx_exact_dp_device: download failed");
+    hipStreamSynchronize(s);
+    hipFree(dev);
+    if (rc) return rc;
+    if (!dp_backtrack(pre, bt.data(), W, n, k, force_endpoints, codebook_out))
+        return set_error(GEFENX_EINVAL, "gefenx_exact_dp_device: infeasible segmentation");
+    return GEFENX_OK;
 }
 
 }  // extern "C"

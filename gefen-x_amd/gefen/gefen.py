@@ -298,7 +298,7 @@ class Gefen(torch.optim.Optimizer):
                  "active_centers": centers[active], "active_counts": counts[active],
                  "active_sums": centers[active] * counts[active]}
         cb = quantization_module.exact_dp(histogram_stats=stats, num_codebooks=NUM_CODEBOOKS,
-                                          force_endpoints=True)
+                                          force_endpoints=True, device=counts_dev.device)
         return cb.to(counts_dev.device)
 
     def _maybe_refresh_gefen_codebook(self):

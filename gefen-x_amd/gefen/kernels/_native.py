@@ -85,6 +85,7 @@ SIGNATURES = {
     "gefenx_exact_histogram": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
     "gefenx_block_variance_errors": (_I, [_P, _I, _I64, _P, _I, _P, _P]),
     "gefenx_exact_dp": (_I, [_P, _P, _I, _I, _I, _P]),
+    "gefenx_exact_dp_device": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "gefenx_multi_tensor_step": (_I, [_P, _I, _P, _I, _I64, _P, _SZ, _P]),
     "gefenx_multi_tensor_scratch_bytes": (_SZ, [_I]),
     "gefenx_ns_workspace_bytes": (_SZ, [_I64, _I64, _I64]),

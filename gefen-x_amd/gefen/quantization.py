@@ -4,7 +4,9 @@ exact_dp keeps the reference's signature and result: the optimal 256-centre
 1-D weighted k-means over the active histogram bins with forced +-1 endpoints
 (quantization.py:197-253), padded when there are fewer active bins than
 centres (quantization.py:59-72).  The O(k n^2) float64 DP runs in the C ABI
-(gefenx_exact_dp, host threads) instead of numba or pure Python.
+instead of numba or pure Python: on the HIP device when one is given
+(gefenx_exact_dp_device), else on host threads (gefenx_exact_dp); both make
+the same float64 operations and the same first-minimum choices.
 """
 from __future__ import annotations
 
@@ -43,7 +45,10 @@ def save_distribution_histogram_pt_from_counts(hist, prefix, suffix, num_samples
     logger.info("Saved distribution histogram data to %s", path)
 
 
-def exact_dp(histogram_stats: dict, num_codebooks: int, force_endpoints: bool = True) -> torch.Tensor:
+def exact_dp(histogram_stats: dict, num_codebooks: int, force_endpoints: bool = True,
+             device: torch.device = None) -> torch.Tensor:
+    """quantization.py:197-253.  With a HIP `device` the DP levels run there
+    (gefenx_exact_dp_device, bit-identical); otherwise on host threads."""
     from gefen.kernels import _native
     centers = histogram_stats["active_centers"].detach().cpu().to(torch.float32).contiguous()
     counts = histogram_stats["active_counts"].detach().cpu().to(torch.float32).contiguous()
@@ -52,7 +57,16 @@ def exact_dp(histogram_stats: dict, num_codebooks: int, force_endpoints: bool = 
     if not torch.all(counts > 0):
         raise ValueError("exact DP expects strictly positive counts for all active histogram bins.")
     out = torch.empty(num_codebooks, dtype=torch.float32)
-    _native.check(_native.load().gefenx_exact_dp(
+    lib = _native.load()
+    if device is not None and torch.device(device).type == "cuda":
+        dev = torch.device(device)
+        with torch.cuda.device(dev):
+            _native.check(lib.gefenx_exact_dp_device(
+                centers.data_ptr(), counts.data_ptr(), centers.numel(), int(num_codebooks),
+                1 if force_endpoints else 0, out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream),
+                "exact_dp")
+        return out
+    _native.check(lib.gefenx_exact_dp(
         centers.data_ptr(), counts.data_ptr(), centers.numel(), int(num_codebooks),
         1 if force_endpoints else 0, out.data_ptr()), "exact_dp")
     return out

@@ -177,6 +177,14 @@ int gefenx_block_variance_errors(const void* grad, int dtype, int64_t numel,
 int gefenx_exact_dp(const float* active_centers, const float* active_counts,
                     int n_points, int k, int force_endpoints, float* codebook_out);
 
+/* The same solver with each DP level on the device (one launch per centre,
+ * every segment end in parallel), bit-identical to gefenx_exact_dp; host
+ * inputs and output, synchronous on `stream`.  Replaces the same
+ * quantization.exact_dp (quantization.py:197-253). */
+int gefenx_exact_dp_device(const float* active_centers, const float* active_counts,
+                           int n_points, int k, int force_endpoints, float* codebook_out,
+                           void* stream);
+
 /* ------------------------------------------------------------------------
  * Multi-tensor step: one launch sequence for many parameters.  No
  * counterpart in the reference (its fused path is one call per parameter,

@@ -62,6 +62,36 @@ def test_learned_codebook_matches_reference_golden(dev):
     _native.load()
 
 
+def test_device_exact_dp_matches_host_and_golden(dev):
+    """gefenx_exact_dp_device (DP levels on the GPU) against the reference's
+    learned codebook and, bit for bit, against the host solver on random
+    histograms: all active bins, sparse bins, fewer bins than centres, k
+    below 256, and ties (equal counts on a symmetric grid)."""
+    from gefen import quantization
+    z = np.load(os.path.join(GOLD, "learn.npz"))
+    counts = np.zeros(4096, np.int64)
+    for tag in ("w", "b"):
+        counts += _hist_gpu(torch.from_numpy(z["g_" + tag]).to(dev), int(z["period_" + tag]))
+    centers, cnts = orc.histogram_stats(counts)
+    stats = {"active_centers": torch.from_numpy(centers), "active_counts": torch.from_numpy(cnts)}
+    np.testing.assert_array_equal(quantization.exact_dp(stats, 256, True, device=dev).numpy(), z["cb"])
+    rng = np.random.default_rng(7)
+    grid = (np.arange(4096, dtype=np.float32) + 0.5) / 2048 - 1
+    cases = [(4096, 256, True), (700, 256, True), (100, 256, True), (300, 16, True), (513, 64, False)]
+    for n, k, force in cases:
+        sel = np.sort(rng.choice(4096, size=n, replace=False))
+        c = grid[sel].astype(np.float32)
+        w = np.floor(rng.pareto(1.2, size=n) * 50 + 1).astype(np.float32)
+        st = {"active_centers": torch.from_numpy(c), "active_counts": torch.from_numpy(w)}
+        host = quantization.exact_dp(st, k, force).numpy()
+        devr = quantization.exact_dp(st, k, force, device=dev).numpy()
+        np.testing.assert_array_equal(devr, host, err_msg="n=%d k=%d force=%s" % (n, k, force))
+    st = {"active_centers": torch.from_numpy(grid[::8].copy()),
+          "active_counts": torch.ones(512, dtype=torch.float32)}
+    np.testing.assert_array_equal(quantization.exact_dp(st, 256, True, device=dev).numpy(),
+                                  quantization.exact_dp(st, 256, True).numpy(), err_msg="ties")
+
+
 def test_period_search_matches_reference_golden(dev):
     from gefen import partitioning
     z = np.load(os.path.join(GOLD, "period.npz"))
