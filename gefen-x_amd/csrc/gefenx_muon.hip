@@ -12,8 +12,10 @@
 //                product is an "NT" GEMM C = A B^T with K contiguous in both
 //                operands: G = X X^T; GG = G G^T (G is symmetric); BX =
 //                B (X^T)^T -- so the kernel keeps X and X^T side by side and
-//                the X update writes both.  bf16 MFMA 32x32x16, fp32
-//                accumulation, LDS double buffering.
+//                the X update writes both.  G and B = bG + cGG are symmetric:
+//                only their lower-triangle tiles are computed, each mirrored
+//                as it is stored (about 30% fewer MFMAs per iteration).  bf16
+//                MFMA 32x32x16, fp32 accumulation, LDS double buffering.
 //   normuon      per-row EMA of the mean square of the update, rescaled to
 //                keep the Frobenius norm (gefen_muon.py:1192-1230).
 //   apply        p = D(p * (1 - lr*wd)); p = D(fma(update, alpha, p)),
@@ -327,8 +329,6 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a) {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 32;
-constexpr int kLds = kBK + 8;  // bf16 per LDS row: 80 B, spreads the 16-B MFMA operand reads over banks
 
 struct GemmArgs {
     const uint16_t* A; int64_t lda, sA;   // sA: elements between batch items
@@ -339,25 +339,32 @@ struct GemmArgs {
     int64_t M, N, K;
     float alpha, beta;
     int vec;                              // 16-byte loads allowed (K, lda, ldb % 8 == 0, aligned)
+    int tri;                              // D symmetric (A = B, C symmetric): lower-triangle tiles only,
+                                          // each off-diagonal tile also stores its mirror through Dt = D
 };
 
 __device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ uint16_t f2bf(float x) { return (uint16_t)f32_to_bf16(x); }
 
-// Load a 128 x 32 tile (rows r0.., k k0..) of a row-major bf16 matrix into
-// two 16-byte registers per thread; rows >= R or k >= K read as zero.
+// Load a ROWS x BK tile (rows r0.., k k0..) of a row-major bf16 matrix into
+// ROWS*BK/2048 16-byte registers per thread; rows >= R or k >= K read as zero.
+template <int ROWS, int BK, bool VEC>
 __device__ __forceinline__ void gemm_load_tile(const uint16_t* __restrict__ base, int64_t ld, int64_t R,
-                                               int64_t K, int64_t r0, int64_t k0, bool vec, u32x4 v[2]) {
+                                               int64_t K, int64_t r0, int64_t k0, u32x4* v) {
+    constexpr int kCpr = BK / 8;  // 16-byte chunks per row
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = threadIdx.x + i * kT;  // 512 chunks of 8 bf16
-        const int row = c >> 2;
-        const int kc = (c & 3) * 8;
+    for (int i = 0; i < ROWS * kCpr / kT; ++i) {
+        const int c = threadIdx.x + i * kT;
+        const int row = c / kCpr;
+        const int kc = (c % kCpr) * 8;
         const int64_t gr = r0 + row;
         const int64_t gk = k0 + kc;
-        if (vec) {
-            if (gr < R && gk < K) v[i] = *gbl(reinterpret_cast<const u32x4*>(base + gr * ld + gk));
-            else v[i] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (VEC) {
+            // no branch around the load (out-of-range lanes read element 0 and
+            // are zeroed after), so the wait counters stay exact
+            const bool ok = gr < R && gk < K;
+            const u32x4 t = *gbl(reinterpret_cast<const u32x4*>(base + (ok ? gr * ld + gk : 0)));
+            v[i] = ok ? t : u32x4{0u, 0u, 0u, 0u};
         } else {
             uint32_t w[4];
 #pragma unroll
@@ -371,30 +378,264 @@ __device__ __forceinline__ void gemm_load_tile(const uint16_t* __restrict__ base
     }
 }
 
-__device__ __forceinline__ void gemm_store_tile(uint16_t* __restrict__ s, const u32x4 v[2]) {
+template <int ROWS, int BK>
+__device__ __forceinline__ void gemm_store_tile(uint16_t* __restrict__ s, const u32x4* v) {
+    constexpr int kCpr = BK / 8;
+    constexpr int kPitch = BK + 8;  // bf16 per LDS row: the pad spreads 16-byte operand reads over banks
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < ROWS * kCpr / kT; ++i) {
         const int c = threadIdx.x + i * kT;
-        const int row = c >> 2;
-        const int kc = (c & 3) * 8;
-        *reinterpret_cast<u32x4*>(s + row * kLds + kc) = v[i];
+        const int row = c / kCpr;
+        const int kc = (c % kCpr) * 8;
+        *reinterpret_cast<u32x4*>(s + row * kPitch + kc) = v[i];
     }
 }
 
+// Epilogue of a 128 x 128 tile through LDS, one 64-row half at a time (the
+// waves with wm == h own rows h*64 .. h*64+63): accumulators -> fp32 tile;
+// every thread then forms bf16(alpha*acc + beta*C) for 8 consecutive columns
+// (16-byte C loads and D stores) and writes the rounded value back; the
+// transposed copy reads the tile by columns and stores rows of Dt as 16-byte
+// vectors -- the same bf16 values as D.
+__device__ __forceinline__ void gemm_epilogue_128(const GemmArgs& g, const f32x16 (&acc)[2][2], float* sOut,
+                                                  int64_t m0, int64_t n0, int wm, int wn, int l32, int lhi) {
+    constexpr int WM = 2, WN = 2, kT_ = kT;
+    constexpr int kOutPitch = 129;
+    const int64_t bz = blockIdx.z;
+    const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
+    uint16_t* D = g.D + bz * g.sD;
+    uint16_t* Dt = (g.Dt && !(g.tri && blockIdx.x == blockIdx.y)) ? g.Dt + bz * g.sDt : nullptr;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (wm == h) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        const int col = wn * (32 * WN) + j * 32 + l32;
+                        sOut[row * kOutPitch + col] = acc[i][j][r];
+                    }
+        }
+        __syncthreads();
+        const int64_t R0 = m0 + h * 64;
+        // D: 64 rows x 16 vectors of 8 columns
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int v = tid + k * kT;
+            const int row = v >> 4, c8 = (v & 15) * 8;
+            const int64_t gr = R0 + row, gc = n0 + c8;
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = g.alpha * sOut[row * kOutPitch + c8 + e];
+            const bool full = gr < g.M && gc + 8 <= g.N;
+            if (C != nullptr) {
+                const uint16_t* cp = C + gr * g.ldc + gc;
+                if (full && (reinterpret_cast<uintptr_t>(cp) & 15) == 0) {
+                    const u32x4 cv = *gbl(reinterpret_cast<const u32x4*>(cp));
+                    const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        x[e] = __builtin_fmaf(g.beta, bf16f((uint16_t)(cw[e >> 1] >> (16 * (e & 1)))), x[e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (gr < g.M && gc + e < g.N) x[e] = __builtin_fmaf(g.beta, bf16f(*gbl(cp + e)), x[e]);
+                }
+            }
+            uint16_t hv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hv[e] = f2bf(x[e]);
+                sOut[row * kOutPitch + c8 + e] = bf16f(hv[e]);
+            }
+            uint16_t* dp = D + gr * g.ldd + gc;
+            if (full && (reinterpret_cast<uintptr_t>(dp) & 15) == 0) {
+                const u32x4 dv = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16),
+                                  (uint32_t)hv[4] | ((uint32_t)hv[5] << 16), (uint32_t)hv[6] | ((uint32_t)hv[7] << 16)};
+                *gbl(reinterpret_cast<u32x4*>(dp)) = dv;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (gr < g.M && gc + e < g.N) *gbl(dp + e) = hv[e];
+            }
+        }
+        if (Dt != nullptr) {
+            __syncthreads();
+            // Dt: 128 columns x 8 vectors of 8 rows
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int v = tid + k * kT;
+                const int cc = v >> 3, r8 = (v & 7) * 8;
+                const int64_t gc = n0 + cc, gr = R0 + r8;
+                if (gc >= g.N) continue;
+                uint16_t hv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = f2bf(sOut[(r8 + e) * kOutPitch + cc]);
+                uint16_t* tp = Dt + gc * g.lddt + gr;
+                if (gr + 8 <= g.M && (reinterpret_cast<uintptr_t>(tp) & 15) == 0) {
+                    const u32x4 tv = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16),
+                                      (uint32_t)hv[4] | ((uint32_t)hv[5] << 16), (uint32_t)hv[6] | ((uint32_t)hv[7] << 16)};
+                    *gbl(reinterpret_cast<u32x4*>(tp)) = tv;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (gr + e < g.M) *gbl(tp + e) = hv[e];
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// D = alpha * A B^T + beta * C (A [M x K], B [N x K], C and D [M x N], all
+// row-major bf16, fp32 accumulation; optional transposed copy Dt = D^T).
+// Workgroup tile (64*WM) x (64*WN): 2 x 2 waves, each (32*WM) x (32*WN) as
+// WM x WN blocks of mfma_f32_32x32x16_bf16, so each wave reads WM + WN
+// operand fragments from LDS per WM*WN MFMAs.  K in steps of BK, LDS double
+// buffered, the next step's global loads in flight during this step's MFMAs.
+template <int WM, int WN, int BK, bool VEC>
 __global__ void __launch_bounds__(kT) k_gemm_nt(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) uint16_t sA[2][kBM * kLds];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[2][kBN * kLds];
+    constexpr int BM = 64 * WM, BN = 64 * WN;
+    constexpr int kPitch = BK + 8;
+    constexpr int kOutPitch = BN + 1;  // fp32 epilogue tile: odd pitch, conflict-free column reads
+    constexpr size_t kLoopBytes = sizeof(uint16_t) * 2 * (size_t)(BM + BN) * kPitch;
+    constexpr size_t kOutBytes = sizeof(float) * 64 * (size_t)kOutPitch;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kLoopBytes > kOutBytes ? kLoopBytes : kOutBytes];
+    uint16_t (*sA)[BM * kPitch] = reinterpret_cast<uint16_t (*)[BM * kPitch]>(smem);
+    uint16_t (*sB)[BN * kPitch] = reinterpret_cast<uint16_t (*)[BN * kPitch]>(smem + sizeof(uint16_t) * 2 * BM * kPitch);
+    float* sOut = reinterpret_cast<float*>(smem);
+    if (g.tri && blockIdx.x > blockIdx.y) return;  // upper triangle: the mirror of a lower tile
     const int64_t bz = blockIdx.z;
     const uint16_t* A = g.A + bz * g.sA;
     const uint16_t* B = g.B + bz * g.sB;
-    const int64_t m0 = (int64_t)blockIdx.y * kBM;
-    const int64_t n0 = (int64_t)blockIdx.x * kBN;
+    const int64_t m0 = (int64_t)blockIdx.y * BM;
+    const int64_t n0 = (int64_t)blockIdx.x * BN;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;   // 2 x 2 waves, 64 x 64 each
+    const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, lhi = lane >> 5;
-    const bool vec = g.vec != 0;
 
+    f32x16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int64_t nk = cdiv(g.K, BK);
+    constexpr int kRa = BM * BK / 8 / kT, kRb = BN * BK / 8 / kT;
+    auto mma_step = [&](const uint16_t* a_s, const uint16_t* b_s) {
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            bf16x8 av[WM], bv[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const int row = wm * (32 * WM) + i * 32 + l32;
+                av[i] = *reinterpret_cast<const bf16x8*>(a_s + row * kPitch + ks * 16 + lhi * 8);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const int col = wn * (32 * WN) + j * 32 + l32;
+                bv[j] = *reinterpret_cast<const bf16x8*>(b_s + col * kPitch + ks * 16 + lhi * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    // one register stage: step kt+1's loads fly during step kt's MFMAs
+    u32x4 ra[kRa], rb[kRb];
+    gemm_load_tile<BM, BK, VEC>(A, g.lda, g.M, g.K, m0, 0, ra);
+    gemm_load_tile<BN, BK, VEC>(B, g.ldb, g.N, g.K, n0, 0, rb);
+    gemm_store_tile<BM, BK>(sA[0], ra);
+    gemm_store_tile<BN, BK>(sB[0], rb);
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int cur = (int)(kt & 1);
+        if (kt + 1 < nk) {
+            gemm_load_tile<BM, BK, VEC>(A, g.lda, g.M, g.K, m0, (kt + 1) * BK, ra);
+            gemm_load_tile<BN, BK, VEC>(B, g.ldb, g.N, g.K, n0, (kt + 1) * BK, rb);
+        }
+        mma_step(sA[cur], sB[cur]);
+        if (kt + 1 < nk) {
+            gemm_store_tile<BM, BK>(sA[cur ^ 1], ra);
+            gemm_store_tile<BN, BK>(sB[cur ^ 1], rb);
+        }
+        __syncthreads();
+    }
+
+    static_assert(WM == 2 && WN == 2, "the LDS epilogue covers 128 x 128 tiles");
+    gemm_epilogue_128(g, acc, sOut, m0, n0, wm, wn, l32, lhi);
+}
+
+// Direct-to-LDS variant (K a multiple of BK, 16-byte aligned rows): the
+// operand tiles go from HBM straight into LDS (global_load_lds_dwordx4, no
+// staging registers, no LDS store instructions).  Tile 128 x 128, K steps of
+// BK, an S-stage LDS ring: step kt+S-1's loads are issued as step kt's MFMAs
+// start, and a step waits only for its own loads.  A tile row (BK bf16 =
+// BK/8 chunks of 16 bytes) keeps chunk c in slot c ^ f(row), f(row) =
+// (row >> 1) & 7 (BK 64) or (row >> 2) & 3 (BK 32): the 32 rows one MFMA
+// operand read touches then spread over all 64 banks.  Each load instruction
+// fills 1 KB of LDS; its lanes fetch the global chunks their slots hold.
+// Rows past M / N read a clamped valid row (their outputs are not stored).
+template <int BK>
+__device__ __forceinline__ int dl_slot(int row, int c) {
+    if constexpr (BK == 64) return c ^ ((row >> 1) & 7);
+    else return c ^ ((row >> 2) & 3);
+}
+
+template <int BK>
+__device__ __forceinline__ void dl_load_stage(const uint16_t* __restrict__ A, int64_t lda, int64_t M,
+                                              const uint16_t* __restrict__ B, int64_t ldb, int64_t N,
+                                              int64_t m0, int64_t n0, int64_t k0, uint16_t* stage) {
+    constexpr int kCpr = BK / 8;             // chunks per row
+    constexpr int kRpi = 64 / kCpr;          // rows per 1 KB instruction
+    constexpr int kIpt = 128 / kRpi;         // instructions per operand tile
+    constexpr int kIpw = 2 * kIpt / (kT / 64);  // instructions per wave
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < kIpw; ++q) {
+        const int inst = wave * kIpw + q;
+        const bool is_b = inst >= kIpt;
+        const int ti = is_b ? inst - kIpt : inst;
+        const int row = ti * kRpi + lane / kCpr;  // tile row 0..127
+        const int slot = lane % kCpr;
+        const int chunk = dl_slot<BK>(row, slot);  // the swizzle is an involution
+        const uint16_t* base = is_b ? B : A;
+        const int64_t ld = is_b ? ldb : lda;
+        const int64_t lim = is_b ? N : M;
+        int64_t gr = (is_b ? n0 : m0) + row;
+        gr = gr < lim ? gr : lim - 1;
+        const uint16_t* src = base + gr * ld + k0 + chunk * 8;
+        uint16_t* dst = stage + (is_b ? 128 * BK : 0) + ti * kRpi * BK;  // wave-uniform
+        __builtin_amdgcn_global_load_lds((const GX_GLOBAL void*)src, (__attribute__((address_space(3))) void*)dst, 16,
+                                         0, 0);
+    }
+}
+
+template <int BK, int S>
+__global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
+    if (g.tri && blockIdx.x > blockIdx.y) return;  // upper triangle: the mirror of a lower tile
+    constexpr int kStage = 2 * 128 * BK;                        // bf16 per stage: A then B
+    constexpr int kIpw = 2 * (128 * BK * 2 / 1024) / (kT / 64);  // load instructions per wave and stage
+    constexpr int kSmem = S * kStage > 64 * 129 * 2 ? S * kStage : 64 * 129 * 2;  // epilogue tile fits
+    __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
+    const int64_t bz = blockIdx.z;
+    const uint16_t* A = g.A + bz * g.sA;
+    const uint16_t* B = g.B + bz * g.sB;
+    const int64_t m0 = (int64_t)blockIdx.y * 128;
+    const int64_t n0 = (int64_t)blockIdx.x * 128;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -402,34 +643,35 @@ __global__ void __launch_bounds__(kT) k_gemm_nt(GemmArgs g) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    const int64_t nk = cdiv(g.K, kBK);
-    u32x4 ra[2], rb[2];
-    gemm_load_tile(A, g.lda, g.M, g.K, m0, 0, vec, ra);
-    gemm_load_tile(B, g.ldb, g.N, g.K, n0, 0, vec, rb);
-    gemm_store_tile(sA[0], ra);
-    gemm_store_tile(sB[0], rb);
-    __syncthreads();
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        const int cur = (int)(kt & 1);
-        if (kt + 1 < nk) {
-            gemm_load_tile(A, g.lda, g.M, g.K, m0, (kt + 1) * kBK, vec, ra);
-            gemm_load_tile(B, g.ldb, g.N, g.K, n0, (kt + 1) * kBK, vec, rb);
-        }
-        const uint16_t* a_s = sA[cur];
-        const uint16_t* b_s = sB[cur];
+    const int64_t nk = g.K / BK;
 #pragma unroll
-        for (int ks = 0; ks < kBK / 16; ++ks) {
+    for (int st = 0; st < S - 1; ++st)
+        if (st < nk) dl_load_stage<BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, st * BK, smem + st * kStage);
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        // step kt's loads were issued S-1 steps ago; later ones may still fly
+        const int64_t later = std::min<int64_t>(S - 2, nk - 1 - kt);
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kIpw));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | kIpw);
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();  // every wave's loads of step kt landed; step kt-1's buffer is free
+        if (kt + S - 1 < nk)
+            dl_load_stage<BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, (kt + S - 1) * BK,
+                              smem + ((kt + S - 1) % S) * kStage);
+        const uint16_t* a_s = smem + (kt % S) * kStage;
+        const uint16_t* b_s = a_s + 128 * BK;
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int c = ks * 2 + lhi;
             bf16x8 av[2], bv[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int row = wm * 64 + i * 32 + l32;
-                av[i] = *reinterpret_cast<const bf16x8*>(a_s + row * kLds + ks * 16 + lhi * 8);
+                av[i] = *reinterpret_cast<const bf16x8*>(a_s + row * BK + dl_slot<BK>(row, c) * 8);
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int col = wn * 64 + j * 32 + l32;
-                bv[j] = *reinterpret_cast<const bf16x8*>(b_s + col * kLds + ks * 16 + lhi * 8);
+                const int row = wn * 64 + j * 32 + l32;
+                bv[j] = *reinterpret_cast<const bf16x8*>(b_s + row * BK + dl_slot<BK>(row, c) * 8);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -437,48 +679,9 @@ __global__ void __launch_bounds__(kT) k_gemm_nt(GemmArgs g) {
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
-        if (kt + 1 < nk) {
-            gemm_store_tile(sA[cur ^ 1], ra);
-            gemm_store_tile(sB[cur ^ 1], rb);
-        }
-        __syncthreads();
     }
-
-    // epilogue: lane holds D[row][col], col = l32, row = (r/4)*8 + lhi*4 + r%4
-    const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
-    uint16_t* D = g.D + bz * g.sD;
-    uint16_t* Dt = g.Dt ? g.Dt + bz * g.sDt : nullptr;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t col = n0 + wn * 64 + j * 32 + l32;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                uint16_t hv[4];
-                const int64_t rbase = m0 + wm * 64 + i * 32 + q * 8 + lhi * 4;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int64_t row = rbase + e;
-                    float v = g.alpha * acc[i][j][q * 4 + e];
-                    if (C != nullptr && row < g.M && col < g.N) v = __builtin_fmaf(g.beta, bf16f(*gbl(C + row * g.ldc + col)), v);
-                    hv[e] = f2bf(v);
-                    if (row < g.M && col < g.N) *gbl(D + row * g.ldd + col) = hv[e];
-                }
-                if (Dt != nullptr && col < g.N) {
-                    uint16_t* dst = Dt + col * g.lddt + rbase;
-                    if (rbase + 3 < g.M && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
-                        const u32x2 pk = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
-                        *gbl(reinterpret_cast<u32x2*>(dst)) = pk;
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (rbase + e < g.M) *gbl(Dt + col * g.lddt + rbase + e) = hv[e];
-                    }
-                }
-            }
-        }
-    }
+    __syncthreads();
+    gemm_epilogue_128(g, acc, reinterpret_cast<float*>(smem), m0, n0, wm, wn, l32, lhi);
 }
 
 static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
@@ -487,11 +690,23 @@ static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
     const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     a.vec = (g.K % 8 == 0) && (g.lda % 8 == 0) && (g.ldb % 8 == 0) && (g.sA % 8 == 0) && (g.sB % 8 == 0) &&
             al(g.A) && al(g.B);
-    if (cdiv(g.M, kBM) > 65535 || batch > 65535 || cdiv(g.N, kBN) > 2147483647LL)
+    constexpr int bm = 128, bn = 128;
+    if (g.tri && (g.M != g.N || g.Dt != g.D || g.lddt != g.ldd || g.sDt != g.sD))
+        return set_error(GEFENX_EINVAL, "newton-schulz gemm: symmetric mode needs a square D mirrored into itself");
+    if (cdiv(g.M, bm) > 65535 || batch > 65535 || cdiv(g.N, bn) > 2147483647LL)
         return set_error(GEFENX_EINVAL, "newton-schulz gemm: %lld x %lld x batch %lld exceeds the launch grid",
                          (long long)g.M, (long long)g.N, (long long)batch);
-    const dim3 grid((unsigned)cdiv(g.N, kBN), (unsigned)cdiv(g.M, kBM), (unsigned)batch);
-    hipLaunchKernelGGL(k_gemm_nt, grid, dim3(kT), 0, s, a);
+    const dim3 grid((unsigned)cdiv(g.N, bn), (unsigned)cdiv(g.M, bm), (unsigned)batch);
+    // direct-to-LDS when K is a multiple of 64 and the operands are 16-byte
+    // aligned (every Newton-Schulz product of 64-multiple shapes); the
+    // register-staged kernel otherwise
+    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (a.vec && g.K % 64 == 0 && al16(g.A) && al16(g.B))
+        hipLaunchKernelGGL((k_gemm_dl<64, 2>), grid, dim3(kT), 0, s, a);
+    else if (a.vec)
+        hipLaunchKernelGGL((k_gemm_nt<2, 2, 64, true>), grid, dim3(kT), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm_nt<2, 2, 64, false>), grid, dim3(kT), 0, s, a);
     return launch_check("newton-schulz gemm");
 }
 
@@ -798,15 +1013,17 @@ int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch,
     rc = launch_check("newton-schulz prologue");
     if (rc) return rc;
     int cur = 0;
+    // algorithmic FLOPs of the iteration (three full products), as quoted for
+    // the reference; the symmetric products execute about half of theirs
     const double flops_iter = 2.0 * (double)batch * ((double)m * m * n * 2.0 + (double)m * m * m);
     for (int it = 0; it < steps; ++it) {
         const float a = (float)abc[3 * it], b = (float)abc[3 * it + 1], c = (float)abc[3 * it + 2];
         int ph = prof_begin(GEFENX_K_NS_GEMM, 0.0, flops_iter, s);
-        // G = X X^T
-        GemmArgs g1{X, n, N, X, n, N, nullptr, 0, 0, G, m, m * m, nullptr, 0, 0, m, m, n, 1.0f, 0.0f, 0};
+        // G = X X^T (symmetric: lower tiles, mirrored)
+        GemmArgs g1{X, n, N, X, n, N, nullptr, 0, 0, G, m, m * m, G, m, m * m, m, m, n, 1.0f, 0.0f, 0, 1};
         rc = gemm_nt(g1, batch, s);
-        // B = b G + c G G^T
-        GemmArgs gg{G, m, m * m, G, m, m * m, G, m, m * m, Bm, m, m * m, nullptr, 0, 0, m, m, m, c, b, 0};
+        // B = b G + c G G^T (symmetric: lower tiles, mirrored)
+        GemmArgs gg{G, m, m * m, G, m, m * m, G, m, m * m, Bm, m, m * m, Bm, m, m * m, m, m, m, c, b, 0, 1};
         if (!rc) rc = gemm_nt(gg, batch, s);
         // X = a X + B X  (B operand X^T), X^T of the result into the other buffer
         GemmArgs gx{Bm, m, m * m, Xt[cur], m, N, X, n, N, X, n, N, Xt[cur ^ 1], m, N, m, n, m, 1.0f, a, 0};

@@ -49,7 +49,11 @@ def _bf16_np(t):
     return t.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("mnk", [(128, 128, 32), (256, 192, 160), (200, 136, 72), (100, 60, 30), (33, 257, 48)])
+# K % 64 == 0 with 16-byte aligned operands takes the direct-to-LDS kernel
+# (the last three: full tiles, partial tiles, a single K step); the rest the
+# register-staged one (K = 30 also without 16-byte loads)
+@pytest.mark.parametrize("mnk", [(128, 128, 32), (256, 192, 160), (200, 136, 72), (100, 60, 30), (33, 257, 48),
+                                 (256, 192, 128), (200, 136, 192), (130, 300, 64)])
 def test_gemm_nt_matches_float64(dev, lib, mnk):
     M, N, K = mnk
     gen = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
@@ -144,7 +148,7 @@ def test_newton_schulz_matches_reference_golden(dev, lib, name):
     assert np.linalg.norm(got - o) <= NS_REL * max(np.linalg.norm(o), 1e-30), name
 
 
-@pytest.mark.parametrize("shape", [(3, 256, 384), (2, 320, 136), (1, 130, 70)])
+@pytest.mark.parametrize("shape", [(3, 256, 384), (2, 320, 136), (1, 130, 70), (2, 512, 1280)])
 def test_newton_schulz_batched_matches_oracle(dev, lib, shape):
     rng = np.random.default_rng(sum(shape))
     m = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
