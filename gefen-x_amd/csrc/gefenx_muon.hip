@@ -391,42 +391,46 @@ __device__ __forceinline__ void gemm_store_tile(uint16_t* __restrict__ s, const 
     }
 }
 
-// Epilogue of a 128 x 128 tile through LDS, one 64-row half at a time (the
-// waves with wm == h own rows h*64 .. h*64+63): accumulators -> fp32 tile;
-// every thread then forms bf16(alpha*acc + beta*C) for 8 consecutive columns
-// (16-byte C loads and D stores) and writes the rounded value back; the
-// transposed copy reads the tile by columns and stores rows of Dt as 16-byte
-// vectors -- the same bf16 values as D.
-__device__ __forceinline__ void gemm_epilogue_128(const GemmArgs& g, const f32x16 (&acc)[2][2], float* sOut,
-                                                  int64_t m0, int64_t n0, int wm, int wn, int l32, int lhi) {
-    constexpr int WM = 2, WN = 2, kT_ = kT;
-    constexpr int kOutPitch = 129;
+// Epilogue of a (64*WM) x (64*WN) tile through LDS, one 64-row slab at a
+// time (wave (wm, wn) holds rows wm*32*WM + 32i .. +32, block i of slab
+// wm*WM/2 + i/2): accumulators -> fp32 slab; every thread then forms
+// bf16(alpha*acc + beta*C) for 8 consecutive columns (16-byte C loads and D
+// stores) and writes the rounded value back; the transposed copy reads the
+// slab by columns and stores rows of Dt as 16-byte vectors -- the same bf16
+// values as D.
+template <int WM, int WN>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16 (&acc)[WM][WN], float* sOut,
+                                              int64_t m0, int64_t n0, int wm, int wn, int l32, int lhi) {
+    constexpr int BN = 64 * WN;
+    constexpr int kOutPitch = BN + 1;  // odd: conflict-free column reads
+    constexpr int kVecD = 64 * BN / 8 / kT;  // D vectors per thread and slab
     const int64_t bz = blockIdx.z;
     const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
     uint16_t* D = g.D + bz * g.sD;
     uint16_t* Dt = (g.Dt && !(g.tri && blockIdx.x == blockIdx.y)) ? g.Dt + bz * g.sDt : nullptr;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        if (wm == h) {
+    for (int h = 0; h < WM; ++h) {
+        if (wm == h / (WM / 2)) {
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
+            for (int ii = 0; ii < 2; ++ii) {
+                const int i = 2 * (h % (WM / 2)) + ii;
 #pragma unroll
                 for (int j = 0; j < WN; ++j)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int row = i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        const int row = ii * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
                         const int col = wn * (32 * WN) + j * 32 + l32;
                         sOut[row * kOutPitch + col] = acc[i][j][r];
                     }
+            }
         }
         __syncthreads();
         const int64_t R0 = m0 + h * 64;
-        // D: 64 rows x 16 vectors of 8 columns
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < kVecD; ++k) {
             const int v = tid + k * kT;
-            const int row = v >> 4, c8 = (v & 15) * 8;
+            const int row = v / (BN / 8), c8 = (v % (BN / 8)) * 8;
             const int64_t gr = R0 + row, gc = n0 + c8;
             float x[8];
 #pragma unroll
@@ -465,9 +469,8 @@ __device__ __forceinline__ void gemm_epilogue_128(const GemmArgs& g, const f32x1
         }
         if (Dt != nullptr) {
             __syncthreads();
-            // Dt: 128 columns x 8 vectors of 8 rows
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < kVecD; ++k) {
                 const int v = tid + k * kT;
                 const int cc = v >> 3, r8 = (v & 7) * 8;
                 const int64_t gc = n0 + cc, gr = R0 + r8;
@@ -571,8 +574,7 @@ __global__ void __launch_bounds__(kT) k_gemm_nt(GemmArgs g) {
         __syncthreads();
     }
 
-    static_assert(WM == 2 && WN == 2, "the LDS epilogue covers 128 x 128 tiles");
-    gemm_epilogue_128(g, acc, sOut, m0, n0, wm, wn, l32, lhi);
+    gemm_epilogue<WM, WN>(g, acc, sOut, m0, n0, wm, wn, l32, lhi);
 }
 
 // Direct-to-LDS variant (K a multiple of BK, 16-byte aligned rows): the
@@ -591,13 +593,13 @@ __device__ __forceinline__ int dl_slot(int row, int c) {
     else return c ^ ((row >> 2) & 3);
 }
 
-template <int BK>
+template <int TILE, int BK>
 __device__ __forceinline__ void dl_load_stage(const uint16_t* __restrict__ A, int64_t lda, int64_t M,
                                               const uint16_t* __restrict__ B, int64_t ldb, int64_t N,
                                               int64_t m0, int64_t n0, int64_t k0, uint16_t* stage) {
     constexpr int kCpr = BK / 8;             // chunks per row
     constexpr int kRpi = 64 / kCpr;          // rows per 1 KB instruction
-    constexpr int kIpt = 128 / kRpi;         // instructions per operand tile
+    constexpr int kIpt = TILE / kRpi;        // instructions per operand tile
     constexpr int kIpw = 2 * kIpt / (kT / 64);  // instructions per wave
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -605,7 +607,7 @@ __device__ __forceinline__ void dl_load_stage(const uint16_t* __restrict__ A, in
         const int inst = wave * kIpw + q;
         const bool is_b = inst >= kIpt;
         const int ti = is_b ? inst - kIpt : inst;
-        const int row = ti * kRpi + lane / kCpr;  // tile row 0..127
+        const int row = ti * kRpi + lane / kCpr;  // tile row
         const int slot = lane % kCpr;
         const int chunk = dl_slot<BK>(row, slot);  // the swizzle is an involution
         const uint16_t* base = is_b ? B : A;
@@ -614,39 +616,42 @@ __device__ __forceinline__ void dl_load_stage(const uint16_t* __restrict__ A, in
         int64_t gr = (is_b ? n0 : m0) + row;
         gr = gr < lim ? gr : lim - 1;
         const uint16_t* src = base + gr * ld + k0 + chunk * 8;
-        uint16_t* dst = stage + (is_b ? 128 * BK : 0) + ti * kRpi * BK;  // wave-uniform
+        uint16_t* dst = stage + (is_b ? TILE * BK : 0) + ti * kRpi * BK;  // wave-uniform
         __builtin_amdgcn_global_load_lds((const GX_GLOBAL void*)src, (__attribute__((address_space(3))) void*)dst, 16,
                                          0, 0);
     }
 }
 
-template <int BK, int S>
+// WM x WM blocks of 32 x 32 per wave, 2 x 2 waves: tile (64*WM)^2.
+template <int WM, int BK, int S>
 __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
     if (g.tri && blockIdx.x > blockIdx.y) return;  // upper triangle: the mirror of a lower tile
-    constexpr int kStage = 2 * 128 * BK;                        // bf16 per stage: A then B
-    constexpr int kIpw = 2 * (128 * BK * 2 / 1024) / (kT / 64);  // load instructions per wave and stage
-    constexpr int kSmem = S * kStage > 64 * 129 * 2 ? S * kStage : 64 * 129 * 2;  // epilogue tile fits
+    constexpr int TILE = 64 * WM;
+    constexpr int kStage = 2 * TILE * BK;                        // bf16 per stage: A then B
+    constexpr int kIpw = 2 * (TILE * BK * 2 / 1024) / (kT / 64);  // load instructions per wave and stage
+    constexpr int kEpi = 2 * 64 * (TILE + 1);                    // the epilogue's fp32 slab, in bf16 units
+    constexpr int kSmem = S * kStage > kEpi ? S * kStage : kEpi;
     __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
     const int64_t bz = blockIdx.z;
     const uint16_t* A = g.A + bz * g.sA;
     const uint16_t* B = g.B + bz * g.sB;
-    const int64_t m0 = (int64_t)blockIdx.y * 128;
-    const int64_t n0 = (int64_t)blockIdx.x * 128;
+    const int64_t m0 = (int64_t)blockIdx.y * TILE;
+    const int64_t n0 = (int64_t)blockIdx.x * TILE;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, lhi = lane >> 5;
-    f32x16 acc[2][2];
+    f32x16 acc[WM][WM];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WM; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     const int64_t nk = g.K / BK;
 #pragma unroll
     for (int st = 0; st < S - 1; ++st)
-        if (st < nk) dl_load_stage<BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, st * BK, smem + st * kStage);
+        if (st < nk) dl_load_stage<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, st * BK, smem + st * kStage);
     for (int64_t kt = 0; kt < nk; ++kt) {
         // step kt's loads were issued S-1 steps ago; later ones may still fly
         const int64_t later = std::min<int64_t>(S - 2, nk - 1 - kt);
@@ -655,33 +660,33 @@ __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
         else __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();  // every wave's loads of step kt landed; step kt-1's buffer is free
         if (kt + S - 1 < nk)
-            dl_load_stage<BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, (kt + S - 1) * BK,
-                              smem + ((kt + S - 1) % S) * kStage);
+            dl_load_stage<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, (kt + S - 1) * BK,
+                                    smem + ((kt + S - 1) % S) * kStage);
         const uint16_t* a_s = smem + (kt % S) * kStage;
-        const uint16_t* b_s = a_s + 128 * BK;
+        const uint16_t* b_s = a_s + TILE * BK;
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             const int c = ks * 2 + lhi;
-            bf16x8 av[2], bv[2];
+            bf16x8 av[WM], bv[WM];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + l32;
+            for (int i = 0; i < WM; ++i) {
+                const int row = wm * (32 * WM) + i * 32 + l32;
                 av[i] = *reinterpret_cast<const bf16x8*>(a_s + row * BK + dl_slot<BK>(row, c) * 8);
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = wn * 64 + j * 32 + l32;
+            for (int j = 0; j < WM; ++j) {
+                const int row = wn * (32 * WM) + j * 32 + l32;
                 bv[j] = *reinterpret_cast<const bf16x8*>(b_s + row * BK + dl_slot<BK>(row, c) * 8);
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < WM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < WM; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
     }
     __syncthreads();
-    gemm_epilogue_128(g, acc, reinterpret_cast<float*>(smem), m0, n0, wm, wn, l32, lhi);
+    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), m0, n0, wm, wn, l32, lhi);
 }
 
 static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
@@ -690,19 +695,22 @@ static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
     const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     a.vec = (g.K % 8 == 0) && (g.lda % 8 == 0) && (g.ldb % 8 == 0) && (g.sA % 8 == 0) && (g.sB % 8 == 0) &&
             al(g.A) && al(g.B);
-    constexpr int bm = 128, bn = 128;
     if (g.tri && (g.M != g.N || g.Dt != g.D || g.lddt != g.ldd || g.sDt != g.sD))
         return set_error(GEFENX_EINVAL, "newton-schulz gemm: symmetric mode needs a square D mirrored into itself");
+    // direct-to-LDS when K is a multiple of 64 and the operands are 16-byte
+    // aligned (every Newton-Schulz product of 64-multiple shapes), the
+    // register-staged kernel otherwise; both 128 x 128 tiles (measured on the
+    // Newton-Schulz batches: 256 x 256 tiles, K steps of 32 and 3-stage rings
+    // were no faster)
+    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool dl = a.vec && g.K % 64 == 0 && al16(g.A) && al16(g.B);
+    constexpr int bm = 128, bn = 128;
     if (cdiv(g.M, bm) > 65535 || batch > 65535 || cdiv(g.N, bn) > 2147483647LL)
         return set_error(GEFENX_EINVAL, "newton-schulz gemm: %lld x %lld x batch %lld exceeds the launch grid",
                          (long long)g.M, (long long)g.N, (long long)batch);
     const dim3 grid((unsigned)cdiv(g.N, bn), (unsigned)cdiv(g.M, bm), (unsigned)batch);
-    // direct-to-LDS when K is a multiple of 64 and the operands are 16-byte
-    // aligned (every Newton-Schulz product of 64-multiple shapes); the
-    // register-staged kernel otherwise
-    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    if (a.vec && g.K % 64 == 0 && al16(g.A) && al16(g.B))
-        hipLaunchKernelGGL((k_gemm_dl<64, 2>), grid, dim3(kT), 0, s, a);
+    if (dl)
+        hipLaunchKernelGGL((k_gemm_dl<2, 64, 2>), grid, dim3(kT), 0, s, a);
     else if (a.vec)
         hipLaunchKernelGGL((k_gemm_nt<2, 2, 64, true>), grid, dim3(kT), 0, s, a);
     else
