@@ -125,12 +125,20 @@ __device__ __forceinline__ void store_idx8(uint8_t* __restrict__ base, const uin
 template <int DT> struct Raw8 { uint32_t w[4]; };
 template <> struct Raw8<F32> { float f[8]; };
 
+// Streamed data (grads, parameters, indices) is read once per pass: the loads
+// are non-temporal, so they do not displace the per-row / per-block values
+// the kernels reuse (measured on MI355X: +7% on an apply-shaped stream, +10%
+// on a stats-shaped one).
 template <int DT>
 __device__ __forceinline__ void load_raw8(const typename Elem<DT>::T* __restrict__ base, Raw8<DT>& r) {
     if constexpr (DT == F32) {
-        load8<F32>(base, r.f);
+        const GX_GLOBAL f32x4* q = gbl(reinterpret_cast<const f32x4*>(base));
+        const f32x4 a = __builtin_nontemporal_load(q);
+        const f32x4 b = __builtin_nontemporal_load(q + 1);
+        r.f[0] = a.x; r.f[1] = a.y; r.f[2] = a.z; r.f[3] = a.w;
+        r.f[4] = b.x; r.f[5] = b.y; r.f[6] = b.z; r.f[7] = b.w;
     } else {
-        const u32x4 v = *gbl(reinterpret_cast<const u32x4*>(base));
+        const u32x4 v = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(base)));
         r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
     }
 }
@@ -144,7 +152,7 @@ __device__ __forceinline__ float raw_elem(const Raw8<DT>& r, int k) {
 struct RawIdx8 { uint32_t lo, hi; };
 
 __device__ __forceinline__ RawIdx8 load_raw_idx8(const uint8_t* __restrict__ base) {
-    const u32x2 v = *gbl(reinterpret_cast<const u32x2*>(base));
+    const u32x2 v = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x2*>(base)));
     return RawIdx8{v.x, v.y};
 }
 

@@ -429,7 +429,7 @@ template <int DT>
 __device__ __forceinline__ u32x4 tv_load(const typename Elem<DT>::T* base, int64_t ld, int64_t r, int64_t c,
                                          bool ok) {
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (ok) v = *gbl(reinterpret_cast<const u32x4*>(base + c * ld + r));
+    if (ok) v = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(base + c * ld + r)));
     return v;
 }
 
