@@ -28,6 +28,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -2096,41 +2097,66 @@ static void launch_mt_apply(int dtype, dim3 grid, hipStream_t s, const TensorWor
     }
 }
 
+// Byte offsets of the descriptor image [works | segments | coarse index] that
+// the multi-tensor launches read from device memory.
+struct MtImage {
+    size_t works, segs, coarse, end;
+};
+
+static MtImage image_layout(const MtLayout& L, size_t base) {
+    MtImage im;
+    im.works = base;
+    im.segs = im.works + align256(sizeof(TensorWork) * L.works.size());
+    im.coarse = im.segs + align256(sizeof(Seg) * L.segs.size());
+    im.end = im.coarse + align256(sizeof(int32_t) * L.coarse.size());
+    return im;
+}
+
+static void write_image(const MtLayout& L, const MtImage& im, char* h) {
+    std::memcpy(h + im.works, L.works.data(), sizeof(TensorWork) * L.works.size());
+    std::memcpy(h + im.segs, L.segs.data(), sizeof(Seg) * L.segs.size());
+    std::memcpy(h + im.coarse, L.coarse.data(), sizeof(int32_t) * L.coarse.size());
+}
+
+static int launch_layout(const MtLayout& L, char* dev, const MtImage& im, hipStream_t s, bool prof);
+
 static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hipStream_t s) {
-    const size_t works_bytes = align256(sizeof(TensorWork) * L.works.size());
-    const size_t segs_bytes = sizeof(Seg) * L.segs.size();
-    const size_t coarse_bytes = sizeof(int32_t) * L.coarse.size();
-    const size_t need = works_bytes + align256(segs_bytes) + align256(coarse_bytes);
+    const MtImage im = image_layout(L, 0);
+    const size_t need = im.end;
     if (scratch_bytes < need)
         return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: scratch %zu bytes < required %zu", scratch_bytes, need);
     int dev = 0;
     hipGetDevice(&dev);
-    std::lock_guard<std::mutex> lk(g_stage_mu);
-    Staging& st = g_stage[dev];
-    const int b = st.next;
-    st.next ^= 1;
-    if (st.done[b] == nullptr && hipEventCreateWithFlags(&st.done[b], hipEventDisableTiming) != hipSuccess)
-        return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: event creation failed");
-    if (st.host[b] != nullptr) hipEventSynchronize(st.done[b]);  // previous upload from this buffer finished
-    if (st.cap[b] < need) {
-        if (st.host[b]) hipHostFree(st.host[b]);
-        st.host[b] = nullptr;
-        st.cap[b] = 0;
-        if (hipHostMalloc(&st.host[b], need, hipHostMallocDefault) != hipSuccess)
-            return set_error(GEFENX_ENOMEM, "gefenx_multi_tensor_step: pinned staging of %zu bytes failed", need);
-        st.cap[b] = need;
+    {
+        std::lock_guard<std::mutex> lk(g_stage_mu);
+        Staging& st = g_stage[dev];
+        const int b = st.next;
+        st.next ^= 1;
+        if (st.done[b] == nullptr && hipEventCreateWithFlags(&st.done[b], hipEventDisableTiming) != hipSuccess)
+            return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: event creation failed");
+        if (st.host[b] != nullptr) hipEventSynchronize(st.done[b]);  // previous upload from this buffer finished
+        if (st.cap[b] < need) {
+            if (st.host[b]) hipHostFree(st.host[b]);
+            st.host[b] = nullptr;
+            st.cap[b] = 0;
+            if (hipHostMalloc(&st.host[b], need, hipHostMallocDefault) != hipSuccess)
+                return set_error(GEFENX_ENOMEM, "gefenx_multi_tensor_step: pinned staging of %zu bytes failed", need);
+            st.cap[b] = need;
+        }
+        char* h = static_cast<char*>(st.host[b]);
+        write_image(L, im, h);
+        if (hipMemcpyAsync(scratch, h, need, hipMemcpyHostToDevice, s) != hipSuccess)
+            return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: descriptor upload failed");
+        hipEventRecord(st.done[b], s);
     }
-    char* h = static_cast<char*>(st.host[b]);
-    std::memcpy(h, L.works.data(), sizeof(TensorWork) * L.works.size());
-    std::memcpy(h + works_bytes, L.segs.data(), segs_bytes);
-    std::memcpy(h + works_bytes + align256(segs_bytes), L.coarse.data(), coarse_bytes);
-    if (hipMemcpyAsync(scratch, h, need, hipMemcpyHostToDevice, s) != hipSuccess)
-        return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: descriptor upload failed");
-    hipEventRecord(st.done[b], s);
-    const TensorWork* dws = reinterpret_cast<const TensorWork*>(scratch);
-    const Seg* dsegs = reinterpret_cast<const Seg*>(static_cast<char*>(scratch) + works_bytes);
-    const int32_t* dcoarse = reinterpret_cast<const int32_t*>(static_cast<char*>(scratch) + works_bytes +
-                                                             align256(segs_bytes));
+    return launch_layout(L, static_cast<char*>(scratch), im, s, true);
+}
+
+// Enqueue the phase launches of L reading the descriptor image at dev.
+static int launch_layout(const MtLayout& L, char* dev, const MtImage& im, hipStream_t s, bool prof) {
+    const TensorWork* dws = reinterpret_cast<const TensorWork*>(dev + im.works);
+    const Seg* dsegs = reinterpret_cast<const Seg*>(dev + im.segs);
+    const int32_t* dcoarse = reinterpret_cast<const int32_t*>(dev + im.coarse);
     for (const Launch& l : L.launches) {
         if (l.wgs <= 0) continue;
         if (l.wgs > 2147483647LL) return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: launch too large");
@@ -2140,7 +2166,7 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
         int kind = kinds[l.phase];
         if (l.key.mode == 1 && l.phase == 0) kind = GEFENX_K_BLOCK_STATS;
         if (l.key.mode == 1 && l.phase == 2) kind = GEFENX_K_BLOCK_APPLY;
-        int ph = prof_begin(kind, l.bytes, 0.0, s);
+        int ph = prof ? prof_begin(kind, l.bytes, 0.0, s) : -1;
         if (l.phase == 0) {
             if (l.key.mode == 0) {
 #define GX_MTS(DTV)                                                                                          \
@@ -2213,7 +2239,75 @@ static size_t multi_scratch_bytes(int n_works, size_t n_segs) {
            align256(sizeof(int32_t) * 6 * n_segs);
 }
 
+// ------------------------------------------------------------ capturable plan
+
+// Descriptor image upload as a kernel node: src is the plan's pinned host
+// image (device-visible), dst the plan's device buffer; n16 16-byte words.
+__global__ __launch_bounds__(kThreads) void k_image_copy(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                         int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n16; i += (int64_t)gridDim.x * kThreads)
+        dst[i] = src[i];
+}
+
+__device__ __forceinline__ double capt_lr(const gefenx_capt_desc& c) {
+    if (c.lr_dev == nullptr) return c.lr;
+    switch (c.lr_dtype) {
+        case F64: return *static_cast<const double*>(c.lr_dev);
+        case F16: return (double)f16_to_f32(*static_cast<const uint16_t*>(c.lr_dev));
+        case BF16: return (double)bf16_to_f32(*static_cast<const uint16_t*>(c.lr_dev));
+        default: return (double)*static_cast<const float*>(c.lr_dev);
+    }
+}
+
+// One thread per parameter: step counters += 1 (fp32, as torch's add_ on a
+// 0-dim fp32 tensor), then the scalar row in float64 cast to fp32 --
+// bc = 1 - beta^step, sqrt for the block path, reciprocal (the op chain of
+// gefen.py:1984-1995).  lr: the device value when given (the weight-decay
+// factor from its float64 value, gefen.py:1996-2001), else the host value
+// (gefen.py:2003-2004).  Thread 0 also advances {global step, next seed,
+// seed of this step}.
+__global__ __launch_bounds__(kThreads) void k_capt_prologue(const gefenx_capt_desc* __restrict__ d, int n,
+                                                            int64_t* __restrict__ counter) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i == 0 && counter != nullptr) {
+        const int64_t seed = counter[1];
+        counter[2] = seed;
+        counter[1] = seed + 1;
+        counter[0] = counter[0] + 1;
+    }
+    if (i >= n) return;
+    const gefenx_capt_desc c = d[i];
+    const float st = *c.step + 1.0f;
+    const float st2 = *c.bc2_step + 1.0f;
+    *c.step = st;
+    *c.bc2_step = st2;
+    double bc2 = 1.0 - pow(c.beta2, (double)st2);
+    if (c.sqrt_bc2) bc2 = sqrt(bc2);
+    const double bc1 = 1.0 - pow(c.beta1, (double)st);
+    const double lr = capt_lr(c);
+    c.scalars[0] = (float)lr;
+    c.scalars[1] = (float)(1.0 / bc2);
+    c.scalars[2] = (float)(1.0 / bc1);
+    c.scalars[3] = c.weight_decay != 0.0 ? (float)(1.0 - lr * c.weight_decay) : 1.0f;
+}
+
 }  // namespace gx
+
+// A fixed tensor set's descriptor image and launch list (include/gefenx.h).
+struct gefenx_mt_plan {
+    gx::MtLayout L;
+    gx::MtImage im;
+    size_t capt_off = 0;
+    int n_capt = 0;
+    int64_t* counter = nullptr;
+    size_t bytes = 0;
+    int device = 0;
+    void* host = nullptr;      // pinned image
+    void* host_dev = nullptr;  // its device-visible address
+    bool uploaded = false;     // an eager launch copied the image into uploaded_to on uploaded_on
+    void* uploaded_to = nullptr;
+    hipStream_t uploaded_on = nullptr;
+};
 
 using namespace gx;
 
@@ -2299,7 +2393,7 @@ int gefenx_block_update(
 }
 
 static int desc_to_work(const gefenx_tensor_desc& d, int i, const void* const* qtables, int sr,
-                        int64_t seed, TensorWork& w) {
+                        int64_t seed, const float* step_scalars, const int64_t* seed_dev, TensorWork& w) {
     int rc = check_dtype(d.dtype, "gefenx_multi_tensor_step");
     if (rc) return rc;
     const int64_t N = d.rows * d.cols;
@@ -2324,6 +2418,7 @@ static int desc_to_work(const gefenx_tensor_desc& d, int i, const void* const* q
     in.lerp_w = d.lerp_w; in.beta2 = d.beta2; in.alpha2 = d.alpha2; in.eps = d.eps;
     in.sc = StepScalars{d.lr, d.inv_bc2, d.inv_bc1, d.wd_factor};
     in.sr = sr ? 1 : 0; in.seed = (uint64_t)seed;
+    in.step_scalars = step_scalars; in.seed_dev = seed_dev;
     in.workspace = d.workspace;
     in.ws_bytes = d.factored ? gefenx_workspace_bytes(GEFENX_WS_FACTORED, d.rows, d.cols, N / d.period)
                              : gefenx_workspace_bytes(GEFENX_WS_BLOCK, 0, 0, N / d.period);
@@ -2331,7 +2426,7 @@ static int desc_to_work(const gefenx_tensor_desc& d, int i, const void* const* q
 }
 
 static int build_layout(const gefenx_tensor_desc* descs, int n, const void* const* qtables, int sr,
-                        int64_t seed, MtLayout& L) {
+                        int64_t seed, const float* const* step_scalars, const int64_t* seed_dev, MtLayout& L) {
     if (n < 0 || (n > 0 && (!descs || !qtables)))
         return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: bad descriptor array");
     std::vector<TensorWork> works;
@@ -2339,7 +2434,8 @@ static int build_layout(const gefenx_tensor_desc* descs, int n, const void* cons
     for (int i = 0; i < n; ++i) {
         if (descs[i].rows * descs[i].cols == 0) continue;  // empty tensors are a no-op
         TensorWork w;
-        int rc = desc_to_work(descs[i], i, qtables, sr, seed, w);
+        int rc = desc_to_work(descs[i], i, qtables, sr, seed, step_scalars ? step_scalars[i] : nullptr,
+                              seed_dev, w);
         if (rc) return rc;
         works.push_back(w);
     }
@@ -2357,11 +2453,115 @@ int gefenx_multi_tensor_step(const gefenx_tensor_desc* descs, int n, const void*
                              int stochastic_round, int64_t rng_seed, void* desc_scratch_dev,
                              size_t desc_scratch_bytes, void* stream) {
     MtLayout L;
-    int rc = build_layout(descs, n, qtables_dev, stochastic_round, rng_seed, L);
+    int rc = build_layout(descs, n, qtables_dev, stochastic_round, rng_seed, nullptr, nullptr, L);
     if (rc) return rc;
     if (L.works.empty()) return GEFENX_OK;
     if (!desc_scratch_dev) return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: null scratch");
     return run_multi(L, desc_scratch_dev, desc_scratch_bytes, static_cast<hipStream_t>(stream));
+}
+
+int gefenx_mt_plan_create(const gefenx_tensor_desc* descs, int n, const float* const* step_scalars,
+                          const void* const* qtables_dev, int stochastic_round, int64_t rng_seed,
+                          const gefenx_capt_desc* capt, int n_capt, int64_t* counter_dev,
+                          gefenx_mt_plan** plan_out) {
+    if (!plan_out) return set_error(GEFENX_EINVAL, "gefenx_mt_plan_create: null plan_out");
+    *plan_out = nullptr;
+    if (n_capt < 0 || (n_capt > 0 && !capt))
+        return set_error(GEFENX_EINVAL, "gefenx_mt_plan_create: bad capturable descriptor array");
+    for (int i = 0; i < n_capt; ++i) {
+        const gefenx_capt_desc& c = capt[i];
+        if (!c.step || !c.bc2_step || !c.scalars)
+            return set_error(GEFENX_EINVAL, "gefenx_mt_plan_create: capturable descriptor %d has a null pointer", i);
+        if (c.lr_dev && (c.lr_dtype < GEFENX_F32 || c.lr_dtype > GEFENX_F64))
+            return set_error(GEFENX_EINVAL, "gefenx_mt_plan_create: capturable descriptor %d: lr dtype code %d", i,
+                             c.lr_dtype);
+    }
+    const int64_t* seed_dev = counter_dev ? counter_dev + 2 : nullptr;
+    auto plan = std::make_unique<gefenx_mt_plan>();
+    int rc = build_layout(descs, n, qtables_dev, stochastic_round, rng_seed, step_scalars, seed_dev, plan->L);
+    if (rc) return rc;
+    plan->im = image_layout(plan->L, 0);
+    plan->capt_off = plan->im.end;
+    plan->n_capt = n_capt;
+    plan->counter = counter_dev;
+    (void)hipGetDevice(&plan->device);
+    plan->bytes = std::max<size_t>(plan->capt_off + align256(sizeof(gefenx_capt_desc) * (size_t)n_capt), 256);
+    // Pinned allocation is host work; let it through while this thread's
+    // stream is being captured.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    const hipError_t e = hipHostMalloc(&plan->host, plan->bytes, hipHostMallocDefault);
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    if (e != hipSuccess) {
+        plan->host = nullptr;
+        return set_error(GEFENX_ENOMEM, "gefenx_mt_plan_create: pinned image of %zu bytes failed", plan->bytes);
+    }
+    if (hipHostGetDevicePointer(&plan->host_dev, plan->host, 0) != hipSuccess) {
+        (void)hipHostFree(plan->host);
+        plan->host = nullptr;
+        return set_error(GEFENX_ELAUNCH, "gefenx_mt_plan_create: pinned image has no device address");
+    }
+    char* h = static_cast<char*>(plan->host);
+    std::memset(h, 0, plan->bytes);
+    write_image(plan->L, plan->im, h);
+    if (n_capt > 0) std::memcpy(h + plan->capt_off, capt, sizeof(gefenx_capt_desc) * (size_t)n_capt);
+    *plan_out = plan.release();
+    return GEFENX_OK;
+}
+
+size_t gefenx_mt_plan_device_bytes(const gefenx_mt_plan* plan) { return plan ? plan->bytes : 0; }
+
+int gefenx_mt_plan_launch(gefenx_mt_plan* plan, void* dev_buf, size_t dev_bytes, void* stream) {
+    if (!plan || !dev_buf) return set_error(GEFENX_EINVAL, "gefenx_mt_plan_launch: null plan or buffer");
+    if (dev_bytes < plan->bytes)
+        return set_error(GEFENX_EINVAL, "gefenx_mt_plan_launch: buffer %zu bytes < required %zu", dev_bytes,
+                         plan->bytes);
+    if (reinterpret_cast<uintptr_t>(dev_buf) % 256 != 0)
+        return set_error(GEFENX_EINVAL, "gefenx_mt_plan_launch: buffer not 256-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess)
+        return set_error(GEFENX_ELAUNCH, "gefenx_mt_plan_launch: stream capture query failed");
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    const dim3 block(kThreads);
+    if (capturing || !plan->uploaded || plan->uploaded_to != dev_buf || plan->uploaded_on != s) {
+        const int64_t n16 = (int64_t)(plan->bytes / 16);
+        const unsigned grid = (unsigned)std::min<int64_t>((n16 + kThreads - 1) / kThreads, 1024);
+        hipLaunchKernelGGL(k_image_copy, dim3(grid), block, 0, s, static_cast<const uint4*>(plan->host_dev),
+                           static_cast<uint4*>(dev_buf), n16);
+        int rc = launch_check("plan image copy");
+        if (rc) return rc;
+        if (!capturing) {
+            plan->uploaded = true;
+            plan->uploaded_to = dev_buf;
+            plan->uploaded_on = s;
+        }
+    }
+    char* dev = static_cast<char*>(dev_buf);
+    if (plan->n_capt > 0 || plan->counter != nullptr) {
+        const unsigned grid = (unsigned)std::max(1, (plan->n_capt + kThreads - 1) / kThreads);
+        hipLaunchKernelGGL(k_capt_prologue, dim3(grid), block, 0, s,
+                           reinterpret_cast<const gefenx_capt_desc*>(dev + plan->capt_off), plan->n_capt,
+                           plan->counter);
+        int rc = launch_check("capturable prologue");
+        if (rc) return rc;
+    }
+    if (plan->L.works.empty()) return GEFENX_OK;
+    return launch_layout(plan->L, dev, plan->im, s, !capturing);
+}
+
+void gefenx_mt_plan_destroy(gefenx_mt_plan* plan) {
+    if (!plan) return;
+    if (plan->host) {
+        // the last launch's image copy may still be reading the pinned image
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(plan->device);
+        (void)hipDeviceSynchronize();
+        (void)hipHostFree(plan->host);
+        (void)hipSetDevice(cur);
+    }
+    delete plan;
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@ import logging
 import math
 import os
 import warnings
+from collections import OrderedDict
 from typing import Iterable, Optional, Tuple, Union
 
 import numpy as np
@@ -41,8 +42,19 @@ HISTOGRAM_BINS = NUM_CODEBOOKS * 16
 GEFEN_EXACT_HISTOGRAM_CHUNK = 1 << 28
 _CHECKPOINT_FORMAT_VERSION = 1
 
-# Keys of per-parameter state that exist only at run time (workspaces).
-_RUNTIME_STATE_KEYS = ("_gefenx_ws",)
+# Keys of per-parameter state that exist only at run time (workspaces and the
+# capturable per-step scalar row).
+_RUNTIME_STATE_KEYS = ("_gefenx_ws", "_capt_scalars")
+
+# Step-like per-parameter counters: python ints, or 0-dim fp32 device tensors
+# under capturable=True (gefen.py:1887-1895, 5680-5705).
+_COUNTER_KEYS = ("step", "vmean_step", "factored_step")
+
+# Eager-only capturable plans kept per optimizer (plans a capture recorded are
+# kept for the optimizer's lifetime).
+_CAPT_PLAN_CACHE = 4
+
+_LR_DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
 # numpy image of gefenx_tensor_desc (field order and offsets of the C struct)
 _DESC_DTYPE = np.dtype(_native.TensorDesc)
@@ -134,6 +146,9 @@ class Gefen(torch.optim.Optimizer):
         self._deterministic = deterministic
         self._codebook_refresh_every = codebook_refresh_every
         self.capturable = capturable
+        # device step counters / scalar rows / launch plans (subclasses with
+        # their own step may turn this off)
+        self._capt_on = capturable
         self._stochastic_round = stochastic_round
         self.verbose = verbose
         self._gefen_codebook = None
@@ -144,6 +159,13 @@ class Gefen(torch.optim.Optimizer):
         # call; GEFENX_MULTI_TENSOR=0 selects one call per parameter.
         self._multi_tensor = os.environ.get("GEFENX_MULTI_TENSOR", "1") != "0"
         self._mt_scratch = {}
+        # capturable=True: per device an int64[3] {global step, next rounding
+        # seed, seed of the running step} advanced on the device each step,
+        # and the launch plans of the tensor sets stepped so far.
+        self._capt_counters = {}
+        self._gefen_global_step_by_device = {}
+        self._sr_seed_by_device = {}
+        self._capt_plans = OrderedDict()
         defaults = dict(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps, weight_decay=weight_decay)
         super().__init__(self._normalize_param_groups(params), defaults)
 
@@ -381,16 +403,23 @@ class Gefen(torch.optim.Optimizer):
                 period, name, numel))
         nb = numel // period
         state["automatic_period"] = period
-        state["step"] = 0
+        state["step"] = self._new_step_counter(p.device)
         state["m_codebook"] = torch.zeros(nb, period, dtype=torch.uint8, device=p.device)
         state["m_magnitude"] = torch.zeros(nb, 1, dtype=torch.float32, device=p.device)
         if factored:
             state["v_row"] = torch.zeros(p.shape[0], dtype=torch.float32, device=p.device)
             state["v_col"] = torch.zeros(p.shape[1], dtype=torch.float32, device=p.device)
-            state["factored_step"] = 0
+            state["factored_step"] = self._new_step_counter(p.device)
         else:
             state["vmean"] = torch.zeros(nb, 1, dtype=torch.float32, device=p.device)
-            state["vmean_step"] = 0
+            state["vmean_step"] = self._new_step_counter(p.device)
+
+    def _new_step_counter(self, device, value=0):
+        """gefen.py:1887-1895: a python int, or under capturable a 0-dim fp32
+        device tensor so the bias corrections are computed on the device."""
+        if self._capt_on:
+            return torch.full((), float(value), dtype=torch.float32, device=device)
+        return int(value)
 
     def _workspace(self, state, kind, rows, cols, nb, device):
         ws = state.get("_gefenx_ws")
@@ -409,7 +438,9 @@ class Gefen(torch.optim.Optimizer):
         if "v_row" not in state:  # resume from a block-vmean checkpoint (gefen.py:2840-2852)
             state["v_row"] = torch.zeros(p.shape[0], dtype=torch.float32, device=p.device)
             state["v_col"] = torch.zeros(p.shape[1], dtype=torch.float32, device=p.device)
-            state["factored_step"] = 0
+            state["factored_step"] = self._new_step_counter(p.device)
+        if self._capt_on:  # counters and scalars advance on the device
+            return state, None, None, None, None
         state["step"] += 1
         state["factored_step"] += 1
         lr = self._lr_value(group)
@@ -425,9 +456,12 @@ class Gefen(torch.optim.Optimizer):
             self._init_state(state, p, grad, name, factored=False)
         if "vmean" not in state:  # resume from a factored checkpoint (gefen.py:3567-3586)
             state["vmean"] = torch.zeros_like(state["m_magnitude"])
-            state["vmean_step"] = 0
+            state["vmean_step"] = self._new_step_counter(p.device)
         elif "vmean_step" not in state:
-            state["vmean_step"] = state["step"]
+            step = state["step"]
+            state["vmean_step"] = step.clone() if torch.is_tensor(step) else step
+        if self._capt_on:
+            return state, None, None, None, None
         state["step"] += 1
         state["vmean_step"] += 1
         lr = self._lr_value(group)
@@ -440,6 +474,9 @@ class Gefen(torch.optim.Optimizer):
         if grad.numel() == 0:
             return
         state, lr, inv_bc2, inv_bc1, wdf = prepared or self._prepare_factored(group, name, p, grad)
+        scalars_ptr, seed_ptr = self._capt_pointers(state, p.device)
+        if scalars_ptr is not None:
+            lr, inv_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
         rows, cols = p.shape
         period = state["automatic_period"]
         nb = p.numel() // period
@@ -451,7 +488,7 @@ class Gefen(torch.optim.Optimizer):
             state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(),
             state["v_row"].data_ptr(), state["v_col"].data_ptr(), period, qt.data_ptr(),
             group["beta1"], group["beta2"], lr, group["eps"], inv_bc2, inv_bc1, wdf,
-            1 if self._stochastic_round else 0, self._gefen_global_step, None, None,
+            1 if self._stochastic_round else 0, self._kernel_rng_seed(), scalars_ptr, seed_ptr,
             ws.data_ptr(), ws.numel(), _stream_of(p)), "factored update of " + name)
 
     def _step_automatic(self, group, name, p, grad, prepared=None):
@@ -459,6 +496,9 @@ class Gefen(torch.optim.Optimizer):
         if grad.numel() == 0:
             return
         state, lr, inv_sqrt_bc2, inv_bc1, wdf = prepared or self._prepare_block(group, name, p, grad)
+        scalars_ptr, seed_ptr = self._capt_pointers(state, p.device)
+        if scalars_ptr is not None:
+            lr, inv_sqrt_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
         period = state["automatic_period"]
         nb = p.numel() // period
         p_k = p if p.is_contiguous() else p.contiguous()
@@ -469,7 +509,7 @@ class Gefen(torch.optim.Optimizer):
             p_k.data_ptr(), g_k.data_ptr(), _fused._dtype_code(p.dtype), p.numel(), period,
             state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(), state["vmean"].data_ptr(),
             qt.data_ptr(), group["beta1"], group["beta2"], lr, group["eps"], inv_sqrt_bc2, inv_bc1, wdf,
-            1 if self._stochastic_round else 0, self._gefen_global_step, None, None,
+            1 if self._stochastic_round else 0, self._kernel_rng_seed(), scalars_ptr, seed_ptr,
             ws.data_ptr(), ws.numel(), _stream_of(p)), "block update of " + name)
         if p_k is not p:
             p.copy_(p_k)
@@ -477,6 +517,8 @@ class Gefen(torch.optim.Optimizer):
     def _desc_row(self, group, p, grad, factored, prepared):
         """One gefenx_tensor_desc (include/gefenx.h) as a tuple in field order."""
         state, lr, inv_bc2, inv_bc1, wdf = prepared
+        if lr is None:  # capturable: the tensor reads its scalar row on the device
+            lr, inv_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
         period = state["automatic_period"]
         nb = p.numel() // period
         if factored:
@@ -521,41 +563,234 @@ class Gefen(torch.optim.Optimizer):
                 self._gefen_global_step, scratch.data_ptr(), scratch.numel(),
                 torch.cuda.current_stream(device).cuda_stream), "multi-tensor step")
 
+    # -------------------------------------------------------- capturable
+
+    def _kernel_rng_seed(self) -> int:
+        """gefen.py:1755-1768: the host rounding seed; under capturable the
+        kernels read it from the device counter instead."""
+        return 0 if self._capt_on else self._gefen_global_step
+
+    def _assert_capturable_if_capturing(self) -> bool:
+        """gefen.py:1614-1641; returns whether the current stream is capturing."""
+        capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+        if capturing and not self.capturable:
+            raise RuntimeError(
+                "Attempting CUDA graph capture of {}.step() but capturable=False. Construct the optimizer "
+                "with capturable=True to make step() graph-safe.".format(type(self).__name__))
+        if capturing:
+            devices = {p.device for g in self.param_groups for p in g["params"]}
+            capture_device = torch.device("cuda", torch.cuda.current_device())
+            if devices != {capture_device}:
+                raise RuntimeError("CUDA graph capture requires every Gefen parameter on the current capture "
+                                   "device {}; found {}".format(capture_device, sorted(map(str, devices))))
+        return capturing
+
+    def _cuda_param_devices(self):
+        return sorted({p.device for g in self.param_groups for p in g["params"] if p.device.type == "cuda"},
+                      key=lambda d: -1 if d.index is None else d.index)
+
+    def _ensure_gefen_global_step_devices(self):
+        """gefen.py:1826-1853: one device counter per parameter device, created
+        eagerly (a counter created inside a capture would be reset by every
+        replay)."""
+        if not self._capt_on:
+            return
+        for device in self._cuda_param_devices():
+            if device in self._capt_counters:
+                continue
+            buf = torch.full((3,), int(self._gefen_global_step), dtype=torch.int64, device=device)
+            self._capt_counters[device] = buf
+            self._gefen_global_step_by_device[device] = buf[0]
+            if self._stochastic_round:
+                self._sr_seed_by_device[device] = buf[1]
+
+    def _reset_gefen_global_step_devices(self):
+        self._capt_counters.clear()
+        self._gefen_global_step_by_device.clear()
+        self._sr_seed_by_device.clear()
+        self._capt_plans_clear()
+        self._ensure_gefen_global_step_devices()
+
+    def _device_gefen_global_step(self):
+        steps = [int(buf[0].item()) for buf in self._capt_counters.values()]
+        if any(s != steps[0] for s in steps[1:]):
+            raise RuntimeError("Gefen capturable global-step counters disagree across devices: {}".format(steps))
+        return steps[0] if steps else None
+
+    def _synchronize_gefen_global_step_for_checkpoint(self):
+        """gefen.py:1855-1870: the host mirror from the device counter after
+        graph replays."""
+        if not self._capt_on:
+            return
+        self._ensure_gefen_global_step_devices()
+        device_step = self._device_gefen_global_step()
+        if device_step is not None:
+            self._gefen_global_step = device_step
+
+    def _capt_pointers(self, state, device):
+        """(scalar row pointer, seed pointer) of one tensor under capturable,
+        (None, None) otherwise."""
+        if not self._capt_on:
+            return None, None
+        counter = self._capt_counters[device]
+        return state["_capt_scalars"].data_ptr(), counter.data_ptr() + 2 * counter.element_size()
+
+    def _capt_ready_state(self, state, p, capturing):
+        """Counters as 0-dim fp32 device tensors and the scalar row; inside a
+        capture they must already exist (step 1 and state creation run eagerly)."""
+        ok = all(torch.is_tensor(state.get(k)) and state[k].device == p.device and state[k].dtype == torch.float32
+                 for k in _COUNTER_KEYS if k in state)
+        if capturing:
+            if not ok or "_capt_scalars" not in state:
+                raise RuntimeError("Gefen capturable: a parameter's state was created or converted inside a "
+                                   "graph capture; run one eager step() after construction, load_state_dict or "
+                                   "a new parameter getting gradients, then capture")
+            return
+        for k in _COUNTER_KEYS:
+            if k in state and not (torch.is_tensor(state[k]) and state[k].device == p.device
+                                   and state[k].dtype == torch.float32):
+                v = state[k].item() if torch.is_tensor(state[k]) else state[k]
+                state[k] = self._new_step_counter(p.device, v)
+        if "_capt_scalars" not in state or state["_capt_scalars"].device != p.device:
+            state["_capt_scalars"] = torch.ones(4, dtype=torch.float32, device=p.device)
+
+    def _capt_row(self, group, p, state, factored):
+        """One gefenx_capt_desc (include/gefenx.h) in field order."""
+        lr = group["lr"]
+        lr_dev, lr_val, lr_code = 0, 0.0, 0
+        if torch.is_tensor(lr) and lr.device.type == "cuda":
+            if lr.device != p.device:
+                raise RuntimeError("capturable tensor lr on {} but parameter on {}".format(lr.device, p.device))
+            if lr.dtype not in _LR_DTYPE_CODES:
+                raise TypeError("capturable tensor lr of dtype {} (fp32/fp16/bf16/fp64 only)".format(lr.dtype))
+            lr_dev, lr_code = lr.data_ptr(), _LR_DTYPE_CODES[lr.dtype]
+        else:
+            lr_val = float(lr)  # a host value: baked into a captured graph, as for torch.optim
+        bc2_key = "factored_step" if factored else "vmean_step"
+        return (state["step"].data_ptr(), state[bc2_key].data_ptr(), state["_capt_scalars"].data_ptr(), lr_dev,
+                lr_val, float(group["weight_decay"]), float(group["beta1"]), float(group["beta2"]), lr_code,
+                0 if factored else 1)
+
+    def _capt_plans_clear(self):
+        plans, self._capt_plans = self._capt_plans, OrderedDict()
+        lib = _native.load() if plans else None
+        for ent in plans.values():
+            if not ent[2]:  # a plan some graph recorded stays alive (its graph may replay)
+                lib.gefenx_mt_plan_destroy(ent[0])
+
+    def _capt_launch(self, device, rows, scalar_ptrs, capt_rows, dtypes, capturing):
+        """Prologue + multi-tensor phases for one device through a cached plan
+        (gefenx_mt_plan_*): kernels only, so the launch can be captured."""
+        lib = _native.load()
+        counter = self._capt_counters[device]
+        cb = self._gefen_codebook_on(device)
+        qt = [0, 0, 0]
+        for dt in dtypes:
+            qt[_fused._dtype_code(dt)] = _fused.quant_table(cb, dt).data_ptr()
+        sr = 1 if self._stochastic_round else 0
+        key = (device, tuple(rows), tuple(scalar_ptrs), tuple(capt_rows), tuple(qt), sr, counter.data_ptr())
+        ent = self._capt_plans.get(key)
+        if ent is None:
+            n, m = len(rows), len(capt_rows)
+            descs = np.array(rows, dtype=_DESC_DTYPE) if n else None
+            ss = (ctypes.c_void_p * max(n, 1))(*scalar_ptrs)
+            capt = (_native.CaptDesc * max(m, 1))(*[_native.CaptDesc(*r) for r in capt_rows])
+            qt_arr = (ctypes.c_void_p * 3)(*qt)
+            handle = ctypes.c_void_p()
+            with torch.cuda.device(device):
+                _native.check(lib.gefenx_mt_plan_create(
+                    descs.ctypes.data if n else None, n, ss, qt_arr, sr, 0, capt, m, counter.data_ptr(),
+                    ctypes.byref(handle)), "capturable plan")
+            nbytes = int(lib.gefenx_mt_plan_device_bytes(handle))
+            ent = [handle, torch.empty(nbytes, dtype=torch.uint8, device=device), False]
+            self._capt_plans[key] = ent
+            if not capturing:
+                eager = [k for k, e in self._capt_plans.items() if not e[2] and k != key]
+                for k in eager[:max(0, len(eager) - _CAPT_PLAN_CACHE + 1)]:
+                    lib.gefenx_mt_plan_destroy(self._capt_plans.pop(k)[0])
+        else:
+            self._capt_plans.move_to_end(key)
+        if capturing:
+            ent[2] = True
+        with torch.cuda.device(device):
+            _native.check(lib.gefenx_mt_plan_launch(ent[0], ent[1].data_ptr(), ent[1].numel(),
+                                                    torch.cuda.current_stream(device).cuda_stream),
+                          "capturable step")
+
+    # -------------------------------------------------------------- step
+
     @torch.no_grad()
     def step(self, closure=None):
+        capturing = self._assert_capturable_if_capturing()
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
         self._validate_grads()
-        self._maybe_refresh_gefen_codebook()
-        if (self._codebook_refresh_every and self._gefen_global_step > 0
-                and self._gefen_global_step % self._codebook_refresh_every == 0):
-            self._refresh_codebook_with_requant()
-        batches = {}  # device -> (desc rows, dtypes)
+        if capturing:
+            if self._gefen_codebook is None and any(p.grad is not None and p.numel()
+                                                    for g in self.param_groups for p in g["params"]):
+                raise RuntimeError("Gefen capturable: step 1 (period search and codebook learning) runs on the "
+                                   "host; run at least one eager step() before capturing")
+            if set(self._cuda_param_devices()) - set(self._capt_counters):
+                raise RuntimeError("Gefen capturable: run one eager step() before capturing (the device "
+                                   "step counters are created eagerly)")
+        else:
+            self._maybe_refresh_gefen_codebook()
+            if (self._codebook_refresh_every and self._gefen_global_step > 0
+                    and self._gefen_global_step % self._codebook_refresh_every == 0):
+                self._refresh_codebook_with_requant()
+            self._ensure_gefen_global_step_devices()
+        batches = {}  # device -> (desc rows, dtypes, scalar-row pointers, capturable rows)
+        deferred = []  # single-tensor launches that read the prologue's scalar rows
         for group in self.param_groups:
             for name, p in self._iter_group_params_with_names(group):
                 grad = p.grad
                 if grad is None or grad.numel() == 0:
                     continue
                 factored = self._factored_v_2d and p.ndim == 2 and not hasattr(p, "placements")
+                if capturing and "step" not in self.state[p]:
+                    raise RuntimeError("Gefen capturable: parameter {} has no state yet; its first step runs "
+                                       "eagerly".format(name))
                 if factored:
                     prepared = self._prepare_factored(group, name, p, grad)
                 else:
                     prepared = self._prepare_block(group, name, p, grad)
+                state = prepared[0]
                 batchable = self._multi_tensor and (
                     factored or (p.is_contiguous() and grad.is_contiguous())
-                    or _block_view_ok(p, grad, prepared[0]["automatic_period"]))
+                    or _block_view_ok(p, grad, state["automatic_period"]))
+                if self._capt_on:
+                    self._capt_ready_state(state, p, capturing)
+                    rows, dtypes, sptrs, crows = batches.setdefault(p.device, ([], set(), [], []))
+                    crows.append(self._capt_row(group, p, state, factored))
+                    if batchable:
+                        rows.append(self._desc_row(group, p, grad, factored, prepared))
+                        sptrs.append(state["_capt_scalars"].data_ptr())
+                        dtypes.add(p.dtype)
+                    else:
+                        deferred.append((group, name, p, grad, factored, prepared))
+                    continue
                 if batchable:
-                    rows, dtypes = batches.setdefault(p.device, ([], set()))
+                    rows, dtypes, _, _ = batches.setdefault(p.device, ([], set(), [], []))
                     rows.append(self._desc_row(group, p, grad, factored, prepared))
                     dtypes.add(p.dtype)
                 elif factored:
                     self._step_automatic_factored(group, name, p, grad, prepared)
                 else:
                     self._step_automatic(group, name, p, grad, prepared)
-        for device, (rows, dtypes) in batches.items():
-            self._multi_tensor_step(device, rows, dtypes)
+        if self._capt_on:
+            for device in self._capt_counters:
+                rows, dtypes, sptrs, crows = batches.get(device, ([], set(), [], []))
+                self._capt_launch(device, rows, sptrs, crows, dtypes, capturing)
+            for group, name, p, grad, factored, prepared in deferred:
+                if factored:
+                    self._step_automatic_factored(group, name, p, grad, prepared)
+                else:
+                    self._step_automatic(group, name, p, grad, prepared)
+        else:
+            for device, (rows, dtypes, _, _) in batches.items():
+                self._multi_tensor_step(device, rows, dtypes)
         self._gefen_global_step += 1
         return loss
 
@@ -564,6 +799,7 @@ class Gefen(torch.optim.Optimizer):
     def state_dict(self):
         """gefen.py:4558-4707: runtime workspaces stripped; codebook, global
         step and deterministic flag recorded; metadata mirrored per group."""
+        self._synchronize_gefen_global_step_for_checkpoint()
         sd = super().state_dict()
         for st in sd["state"].values():
             for k in _RUNTIME_STATE_KEYS:
@@ -607,15 +843,18 @@ class Gefen(torch.optim.Optimizer):
             for k, dt in dtypes.items():
                 if dt is not None and torch.is_tensor(st.get(k)) and st[k].dtype != dt:
                     st[k] = st[k].to(dt)
-            for k in ("step", "vmean_step", "factored_step"):
-                if torch.is_tensor(st.get(k)):
-                    st[k] = int(st[k].item())
+            for k in _COUNTER_KEYS:  # counters follow this optimizer's capturable mode (gefen.py:5680-5705)
+                if k in st:
+                    v = st[k].item() if torch.is_tensor(st[k]) else st[k]
+                    st[k] = self._new_step_counter(p.device, v)
         if global_step is None and meta is not None:
             global_step = meta.get("global_step")
         if codebook is None and meta is not None:
             codebook = meta.get("codebook")
         if global_step is not None:
             self._gefen_global_step = int(global_step)
+        if self._capt_on:
+            self._reset_gefen_global_step_devices()
         if codebook is not None:
             dev = next((p.device for g in self.param_groups for p in g["params"]), torch.device("cpu"))
             self._gefen_codebook = codebook.to(device=dev, dtype=torch.float32)

@@ -254,6 +254,7 @@ class GefenMuon(Gefen):
         super().__init__(params, lr=lr, betas=(momentum, 0.0), eps=eps, weight_decay=weight_decay, fused=fused,
                          factored_v_2d=False, stochastic_round=stochastic_round, deterministic=deterministic,
                          capturable=capturable, verbose=verbose)
+        self._capt_on = False  # the Muon step keeps host counters; capture is refused in step()
 
     def add_param_group(self, param_group):
         """2D parameters only; Muon defaults filled into the group
@@ -321,6 +322,9 @@ class GefenMuon(Gefen):
 
     @torch.no_grad()
     def step(self, closure=None):
+        if self._assert_capturable_if_capturing():
+            raise RuntimeError("GefenMuon: graph capture of step() is not supported by this build (its "
+                               "Newton-Schulz lr and NorMuon step scalars are host values)")
         loss = None
         if closure is not None:
             with torch.enable_grad():

@@ -53,6 +53,17 @@ class TensorDesc(ctypes.Structure):
     ]
 
 
+class CaptDesc(ctypes.Structure):
+    """Mirror of ``gefenx_capt_desc`` (include/gefenx.h)."""
+
+    _fields_ = [
+        ("step", ctypes.c_void_p), ("bc2_step", ctypes.c_void_p), ("scalars", ctypes.c_void_p),
+        ("lr_dev", ctypes.c_void_p), ("lr", ctypes.c_double), ("weight_decay", ctypes.c_double),
+        ("beta1", ctypes.c_double), ("beta2", ctypes.c_double),
+        ("lr_dtype", ctypes.c_int32), ("sqrt_bc2", ctypes.c_int32),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -88,6 +99,10 @@ SIGNATURES = {
     "gefenx_exact_dp_device": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "gefenx_multi_tensor_step": (_I, [_P, _I, _P, _I, _I64, _P, _SZ, _P]),
     "gefenx_multi_tensor_scratch_bytes": (_SZ, [_I]),
+    "gefenx_mt_plan_create": (_I, [_P, _I, _P, _P, _I, _I64, _P, _I, _P, _P]),
+    "gefenx_mt_plan_device_bytes": (_SZ, [_P]),
+    "gefenx_mt_plan_launch": (_I, [_P, _P, _SZ, _P]),
+    "gefenx_mt_plan_destroy": (None, [_P]),
     "gefenx_ns_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "gefenx_newton_schulz": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I, _D, _P, _SZ, _P]),
     "gefenx_normuon_workspace_bytes": (_SZ, [_I64]),

@@ -231,6 +231,75 @@ int gefenx_multi_tensor_step(const gefenx_tensor_desc* descs, int n,
 size_t gefenx_multi_tensor_scratch_bytes(int n);
 
 /* ------------------------------------------------------------------------
+ * Capturable step (graph capture / replay).  Replaces the reference's
+ * capturable machinery: the per-parameter device scalar buffer refresh
+ * (_refresh_capturable_step_scalars, gefen.py:1929-2005, and its batched
+ * cohort form _capt_batched_refresh, gefen.py:2006-2465), the device global
+ * step and stochastic-rounding seed (_advance_gefen_global_step /
+ * _advance_sr_seeds, gefen.py:1842-1853, 1872-1885) and the kernels' device
+ * scalar / seed pointers (resolve_step_scalars_ptr / resolve_seed_dev_ptr,
+ * kernels/automatic_gefen_fused_kernel.cu:2044-2098).
+ *
+ * A plan is built once on the host for a fixed set of tensors (pointers,
+ * shapes, periods, hyperparameters) and launched every step.  A launch
+ * enqueues kernels only -- no host synchronisation, copy node or memset -- so
+ * it can be recorded into a graph and replayed:
+ *   1. the plan's descriptor image is copied into its device buffer by a
+ *      kernel that reads the plan's pinned host image (only on the first
+ *      launch into a buffer, and on every launch recorded by a capture);
+ *   2. the prologue kernel advances every parameter's device step counters
+ *      and writes its fp32[4] scalar row, and advances the global step /
+ *      seed counter;
+ *   3. the multi-tensor stats / finalize / apply launches, each tensor
+ *      reading its scalars and the stochastic-rounding seed from the device.
+ * ---------------------------------------------------------------------- */
+typedef struct gefenx_capt_desc {
+    float* step;            /* device fp32 0-dim: state["step"] (+= 1) */
+    float* bc2_step;        /* device fp32 0-dim: factored_step or vmean_step (+= 1) */
+    float* scalars;         /* device fp32[4] written: lr, 1/bc2 (factored) or
+                             * 1/sqrt(bc2) (block), 1/bc1, weight-decay factor */
+    const void* lr_dev;     /* NULL: the host `lr` below; else a device 0-dim lr */
+    double lr;              /* host lr (used when lr_dev is NULL) */
+    double weight_decay;
+    double beta1, beta2;
+    int32_t lr_dtype;       /* dtype of *lr_dev: GEFENX_F32 or GEFENX_F64 */
+    int32_t sqrt_bc2;       /* 1: block path (1/sqrt(bc2)); 0: factored (1/bc2) */
+} gefenx_capt_desc;
+
+typedef struct gefenx_mt_plan gefenx_mt_plan;
+
+/* Build a plan.  descs[n]: as gefenx_multi_tensor_step (their lr / inv_bc2 /
+ * inv_bc1 / wd_factor fields are ignored when step_scalars[i] is set).
+ * step_scalars: NULL, or n device fp32[4] rows (NULL entries allowed) that
+ * the tensors read their per-step scalars from.  capt[n_capt]: counters and
+ * scalar rows the prologue refreshes (any tensors, also ones stepped by the
+ * single-tensor entry points with the same scalar rows).  counter_dev: NULL,
+ * or a device int64[3] = {global step, next seed, seed of the running step}:
+ * each launch sets [2] = [1], then increments [0] and [1]; with
+ * stochastic_round the tensors take their rounding seed from [2] instead of
+ * rng_seed.  Host work only (validation, layout, pinned image); allowed
+ * while a stream is being captured.  The arrays are copied. */
+int gefenx_mt_plan_create(const gefenx_tensor_desc* descs, int n, const float* const* step_scalars,
+                          const void* const* qtables_dev, int stochastic_round, int64_t rng_seed,
+                          const gefenx_capt_desc* capt, int n_capt, int64_t* counter_dev,
+                          gefenx_mt_plan** plan_out);
+
+/* Bytes of the device buffer a launch of `plan` needs. */
+size_t gefenx_mt_plan_device_bytes(const gefenx_mt_plan* plan);
+
+/* Enqueue one step of `plan` on `stream` (see above).  dev_buf: a device
+ * buffer of gefenx_mt_plan_device_bytes(plan) bytes owned by the caller for
+ * the plan's lifetime; once a launch has uploaded into it outside a capture,
+ * later launches on the same stream skip the copy.  Launches of one plan on
+ * several streams at once race. */
+int gefenx_mt_plan_launch(gefenx_mt_plan* plan, void* dev_buf, size_t dev_bytes, void* stream);
+
+/* Free a plan (synchronises the device before its pinned image is freed).
+ * Never call it while a graph that recorded a launch of the plan may still
+ * be replayed. */
+void gefenx_mt_plan_destroy(gefenx_mt_plan* plan);
+
+/* ------------------------------------------------------------------------
  * Newton-Schulz orthogonalisation of a batch of matrices on bf16 MFMA.
  * Replaces _zeropower_via_newtonschulz / _zeropower_via_newtonschulz_batched
  * (gefen_muon.py:236-291, 353-393).  in: [batch, rows, cols] contiguous of

@@ -204,3 +204,33 @@ def test_exact_dp_is_optimal_on_tiny_inputs(lib):
             best = (cost, centers)
     got = _dp(lib, pts, w, k)
     np.testing.assert_allclose(got, np.sort(np.array(best[1], np.float32)), rtol=0, atol=1e-6)
+
+
+def _c_layout(struct, fields):
+    """sizeof and offsetof of a header struct, from a program gcc builds."""
+    import shutil
+    import subprocess
+    import tempfile
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    body = 'printf("%zu", sizeof({s}));\n'.format(s=struct)
+    body += "".join('printf(" %zu", offsetof({s}, {f}));\n'.format(s=struct, f=f) for f in fields)
+    src = "#include <stddef.h>\n#include <stdio.h>\n#include \"gefenx.h\"\nint main(void) {\n" + body + "return 0;\n}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "layout.c"), os.path.join(d, "layout")
+        with open(c, "w") as f:
+            f.write(src)
+        subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), "-o", exe, c], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()
+    return int(out[0]), [int(x) for x in out[1:]]
+
+
+@pytest.mark.parametrize("struct, mirror", [("gefenx_tensor_desc", "TensorDesc"), ("gefenx_capt_desc", "CaptDesc")])
+def test_ctypes_mirrors_match_header_layout(struct, mirror):
+    """The Python descriptor mirrors have the C structs' size and offsets."""
+    from gefen.kernels import _native
+    cls = getattr(_native, mirror)
+    names = [f for f, _ in cls._fields_]
+    size, offsets = _c_layout(struct, names)
+    assert ctypes.sizeof(cls) == size
+    assert [getattr(cls, f).offset for f in names] == offsets
