@@ -358,6 +358,46 @@ def bench_qwen(args):
     return 0
 
 
+def bench_capturable(torch, params, dev, steps, lr=6e-5):
+    """capturable=True on the same tensor set: eager stepping, then one
+    captured step replayed (device step counters, tensor lr, no host work per
+    replay).  Returns ms per step of each and the host time of an eager call."""
+    from gefen import Gefen
+    lr_t = torch.tensor(lr, device=dev)
+    opt = Gefen(params, lr=lr_t, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, factored_v_2d=True,
+                capturable=True)
+    for _ in range(3):
+        opt.step()
+    torch.cuda.synchronize()
+    host = 0.0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        h0 = time.perf_counter()
+        opt.step()
+        host += time.perf_counter() - h0
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        opt.step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        opt.step()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3 / steps
+    del graph, opt
+    torch.cuda.synchronize()
+    return {"eager_ms_per_step": eager_ms, "graph_replay_ms_per_step": graph_ms,
+            "eager_host_ms_per_call": host * 1e3 / steps, "steps": steps}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -365,6 +405,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-capturable", action="store_true",
+                    help="skip the capturable=True eager / graph-replay timing on the headline set")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy 4 times (scale for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -434,6 +476,13 @@ def main(argv=None):
     lib.gefenx_profile_enable(0)
     ms_step = elapsed * 1e3 / args.steps
     value = n_params / (elapsed / args.steps)
+    host = 0.0
+    for _ in range(5):  # host cost of one eager call (enqueue only)
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        opt.step()
+        host += time.perf_counter() - h0
+    torch.cuda.synchronize()
 
     kinds = {}
     for name, kind in (("stats", _native.K_STATS), ("finalize", _native.K_FINALIZE), ("apply", _native.K_APPLY),
@@ -475,6 +524,12 @@ def main(argv=None):
                      "algo_bytes_per_launch": apply_bytes / max(1, apply_n),
                      "avg_launch_ms": apply_ms / max(1, apply_n)},
     }
+    out["eager_host_ms_per_call"] = host * 1e3 / 5
+    if not args.no_capturable:
+        del opt
+        _log("bench: capturable eager and graph replay ...")
+        out["capturable"] = bench_capturable(torch, params, dev, min(args.steps, 20))
+        _log("bench: capturable %s" % json.dumps(out["capturable"]))
     if not args.no_cpu_baseline:
         _log("bench: cpu baseline (oracle) ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -851,8 +851,10 @@ __global__ void __launch_bounds__(kT) k_row_norm(const uint16_t* U, int64_t R, i
 // scale[r] = bf16(frob_scale / denom[r]).  One workgroup.
 __global__ void __launch_bounds__(kT) k_normuon_scale(const float* row_norm, float* v, int64_t R, float beta2,
                                                       float alpha, float bc, float eps, float* denom,
-                                                      uint16_t* scale) {
+                                                      uint16_t* scale, const float* step_dev, double beta2_d) {
     __shared__ double s_a[kT / 64], s_b[kT / 64];
+    // device step counter (capturable): the same float64 bias correction
+    if (step_dev != nullptr) bc = (float)(1.0 - pow(beta2_d, (double)*gbl(step_dev)));
     double sa = 0.0, sb = 0.0;
     for (int64_t r = threadIdx.x; r < R; r += kT) {
         const float rn = row_norm[r];
@@ -882,9 +884,14 @@ __global__ void __launch_bounds__(kT) k_normuon_scale(const float* row_norm, flo
 // when a NorMuon scale is given, else u.
 template <int DT>
 __global__ void __launch_bounds__(kT) k_muon_apply(void* p, const uint16_t* U, const uint16_t* scale, int64_t R,
-                                                   int64_t C, float wdf, int wd, float alpha) {
+                                                   int64_t C, float wdf, int wd, float alpha, const float* scalars,
+                                                   double lr_ratio) {
     using T = typename Elem<DT>::T;
     T* pp = static_cast<T*>(p);
+    if (scalars != nullptr) {  // capturable: lr and 1 - lr*wd from the device scalar row
+        wdf = *gbl(scalars + 3);
+        alpha = round_dt<DT>((float)(-((double)*gbl(scalars) * lr_ratio)));
+    }
     const int64_t N = R * C;
     for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
         float u = bf16f(*gbl(U + e));
@@ -1047,9 +1054,9 @@ int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch,
 
 int gefenx_normuon_scale(const void* update, int64_t rows, int64_t cols, float* normuon_v, double beta2,
                          int64_t step, double eps, void* scale_out, void* workspace, size_t workspace_bytes,
-                         void* stream) {
+                         const float* step_dev, void* stream) {
     if (rows <= 0 || cols <= 0) return GEFENX_OK;
-    if (!update || !normuon_v || !scale_out || !workspace || step < 1)
+    if (!update || !normuon_v || !scale_out || !workspace || (step < 1 && !step_dev))
         return set_error(GEFENX_EINVAL, "gefenx_normuon_scale: bad argument");
     const size_t need = 2 * align256(sizeof(float) * (size_t)rows);
     if (workspace_bytes < need)
@@ -1060,9 +1067,9 @@ int gefenx_normuon_scale(const void* update, int64_t rows, int64_t cols, float* 
     hipLaunchKernelGGL(k_row_norm, dim3((unsigned)cdiv(rows, kT / 64)), dim3(kT), 0, s,
                        static_cast<const uint16_t*>(update), rows, cols, row_norm);
     const float alpha = (float)((1.0 - beta2) / (double)cols);
-    const float bc = (float)(1.0 - std::pow(beta2, (double)step));
+    const float bc = step_dev ? 1.0f : (float)(1.0 - std::pow(beta2, (double)step));
     hipLaunchKernelGGL(k_normuon_scale, dim3(1), dim3(kT), 0, s, row_norm, normuon_v, rows, (float)beta2, alpha, bc,
-                       (float)eps, denom, static_cast<uint16_t*>(scale_out));
+                       (float)eps, denom, static_cast<uint16_t*>(scale_out), step_dev, beta2);
     return launch_check("normuon scale");
 }
 
@@ -1071,7 +1078,8 @@ size_t gefenx_normuon_workspace_bytes(int64_t rows) {
 }
 
 int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_scale, int64_t rows, int64_t cols,
-                      double lr, double weight_decay, double adjusted_lr, void* stream) {
+                      double lr, double weight_decay, double adjusted_lr, const float* step_scalars,
+                      double lr_ratio, void* stream) {
     int rc = check_dt(dtype, "gefenx_muon_apply");
     if (rc) return rc;
     if (rows <= 0 || cols <= 0) return GEFENX_OK;
@@ -1085,9 +1093,12 @@ int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_sc
     const uint16_t* u = static_cast<const uint16_t*>(update);
     const uint16_t* sc = static_cast<const uint16_t*>(row_scale);
     switch (dtype) {
-        case F32: hipLaunchKernelGGL(k_muon_apply<F32>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha); break;
-        case F16: hipLaunchKernelGGL(k_muon_apply<F16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha); break;
-        default: hipLaunchKernelGGL(k_muon_apply<BF16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha); break;
+        case F32: hipLaunchKernelGGL(k_muon_apply<F32>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha,
+                                   step_scalars, lr_ratio); break;
+        case F16: hipLaunchKernelGGL(k_muon_apply<F16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha,
+                                   step_scalars, lr_ratio); break;
+        default: hipLaunchKernelGGL(k_muon_apply<BF16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha,
+                                   step_scalars, lr_ratio); break;
     }
     return launch_check("muon apply");
 }

@@ -2278,9 +2278,12 @@ __global__ __launch_bounds__(kThreads) void k_capt_prologue(const gefenx_capt_de
     if (i >= n) return;
     const gefenx_capt_desc c = d[i];
     const float st = *c.step + 1.0f;
-    const float st2 = *c.bc2_step + 1.0f;
     *c.step = st;
-    *c.bc2_step = st2;
+    float st2 = st;
+    if (c.bc2_step != nullptr) {
+        st2 = *c.bc2_step + 1.0f;
+        *c.bc2_step = st2;
+    }
     double bc2 = 1.0 - pow(c.beta2, (double)st2);
     if (c.sqrt_bc2) bc2 = sqrt(bc2);
     const double bc1 = 1.0 - pow(c.beta1, (double)st);
@@ -2470,7 +2473,7 @@ int gefenx_mt_plan_create(const gefenx_tensor_desc* descs, int n, const float* c
         return set_error(GEFENX_EINVAL, "gefenx_mt_plan_create: bad capturable descriptor array");
     for (int i = 0; i < n_capt; ++i) {
         const gefenx_capt_desc& c = capt[i];
-        if (!c.step || !c.bc2_step || !c.scalars)
+        if (!c.step || !c.scalars)
             return set_error(GEFENX_EINVAL, "gefenx_mt_plan_create: capturable descriptor %d has a null pointer", i);
         if (c.lr_dev && (c.lr_dtype < GEFENX_F32 || c.lr_dtype > GEFENX_F64))
             return set_error(GEFENX_EINVAL, "gefenx_mt_plan_create: capturable descriptor %d: lr dtype code %d", i,

@@ -48,7 +48,7 @@ _RUNTIME_STATE_KEYS = ("_gefenx_ws", "_capt_scalars")
 
 # Step-like per-parameter counters: python ints, or 0-dim fp32 device tensors
 # under capturable=True (gefen.py:1887-1895, 5680-5705).
-_COUNTER_KEYS = ("step", "vmean_step", "factored_step")
+_COUNTER_KEYS = ("step", "vmean_step", "factored_step", "normuon_step")
 
 # Eager-only capturable plans kept per optimizer (plans a capture recorded are
 # kept for the optimizer's lifetime).
@@ -627,6 +627,15 @@ class Gefen(torch.optim.Optimizer):
         if device_step is not None:
             self._gefen_global_step = device_step
 
+    def _assert_capture_ready(self):
+        if self._gefen_codebook is None and any(p.grad is not None and p.numel()
+                                                for g in self.param_groups for p in g["params"]):
+            raise RuntimeError("{} capturable: step 1 (period search and codebook learning) runs on the host; "
+                               "run at least one eager step() before capturing".format(type(self).__name__))
+        if set(self._cuda_param_devices()) - set(self._capt_counters):
+            raise RuntimeError("{} capturable: run one eager step() before capturing (the device step counters "
+                               "are created eagerly)".format(type(self).__name__))
+
     def _capt_pointers(self, state, device):
         """(scalar row pointer, seed pointer) of one tensor under capturable,
         (None, None) otherwise."""
@@ -654,8 +663,9 @@ class Gefen(torch.optim.Optimizer):
         if "_capt_scalars" not in state or state["_capt_scalars"].device != p.device:
             state["_capt_scalars"] = torch.ones(4, dtype=torch.float32, device=p.device)
 
-    def _capt_row(self, group, p, state, factored):
-        """One gefenx_capt_desc (include/gefenx.h) in field order."""
+    def _capt_row(self, group, p, state, bc2_key, sqrt_bc2):
+        """One gefenx_capt_desc (include/gefenx.h) in field order; bc2_key
+        names the counter of the second-moment bias correction (or None)."""
         lr = group["lr"]
         lr_dev, lr_val, lr_code = 0, 0.0, 0
         if torch.is_tensor(lr) and lr.device.type == "cuda":
@@ -666,10 +676,9 @@ class Gefen(torch.optim.Optimizer):
             lr_dev, lr_code = lr.data_ptr(), _LR_DTYPE_CODES[lr.dtype]
         else:
             lr_val = float(lr)  # a host value: baked into a captured graph, as for torch.optim
-        bc2_key = "factored_step" if factored else "vmean_step"
-        return (state["step"].data_ptr(), state[bc2_key].data_ptr(), state["_capt_scalars"].data_ptr(), lr_dev,
-                lr_val, float(group["weight_decay"]), float(group["beta1"]), float(group["beta2"]), lr_code,
-                0 if factored else 1)
+        return (state["step"].data_ptr(), state[bc2_key].data_ptr() if bc2_key else 0,
+                state["_capt_scalars"].data_ptr(), lr_dev, lr_val, float(group["weight_decay"]),
+                float(group["beta1"]), float(group["beta2"]), lr_code, 1 if sqrt_bc2 else 0)
 
     def _capt_plans_clear(self):
         plans, self._capt_plans = self._capt_plans, OrderedDict()
@@ -728,13 +737,7 @@ class Gefen(torch.optim.Optimizer):
                 loss = closure()
         self._validate_grads()
         if capturing:
-            if self._gefen_codebook is None and any(p.grad is not None and p.numel()
-                                                    for g in self.param_groups for p in g["params"]):
-                raise RuntimeError("Gefen capturable: step 1 (period search and codebook learning) runs on the "
-                                   "host; run at least one eager step() before capturing")
-            if set(self._cuda_param_devices()) - set(self._capt_counters):
-                raise RuntimeError("Gefen capturable: run one eager step() before capturing (the device "
-                                   "step counters are created eagerly)")
+            self._assert_capture_ready()
         else:
             self._maybe_refresh_gefen_codebook()
             if (self._codebook_refresh_every and self._gefen_global_step > 0
@@ -763,7 +766,8 @@ class Gefen(torch.optim.Optimizer):
                 if self._capt_on:
                     self._capt_ready_state(state, p, capturing)
                     rows, dtypes, sptrs, crows = batches.setdefault(p.device, ([], set(), [], []))
-                    crows.append(self._capt_row(group, p, state, factored))
+                    crows.append(self._capt_row(group, p, state, "factored_step" if factored else "vmean_step",
+                                                not factored))
                     if batchable:
                         rows.append(self._desc_row(group, p, grad, factored, prepared))
                         sptrs.append(state["_capt_scalars"].data_ptr())

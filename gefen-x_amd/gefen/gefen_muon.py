@@ -254,7 +254,6 @@ class GefenMuon(Gefen):
         super().__init__(params, lr=lr, betas=(momentum, 0.0), eps=eps, weight_decay=weight_decay, fused=fused,
                          factored_v_2d=False, stochastic_round=stochastic_round, deterministic=deterministic,
                          capturable=capturable, verbose=verbose)
-        self._capt_on = False  # the Muon step keeps host counters; capture is refused in step()
 
     def add_param_group(self, param_group):
         """2D parameters only; Muon defaults filled into the group
@@ -284,7 +283,7 @@ class GefenMuon(Gefen):
                 raise ValueError("Automatic partition period {} does not divide parameter {} with numel {}".format(
                     period, name, numel))
             state["automatic_period"] = period
-            state["step"] = 0
+            state["step"] = self._new_step_counter(p.device)
             nb = numel // period
             state["m_codebook"] = torch.zeros(nb, period, dtype=torch.uint8, device=p.device)
             state["m_magnitude"] = torch.zeros(nb, 1, dtype=torch.float32, device=p.device)
@@ -322,24 +321,46 @@ class GefenMuon(Gefen):
 
     @torch.no_grad()
     def step(self, closure=None):
-        if self._assert_capturable_if_capturing():
-            raise RuntimeError("GefenMuon: graph capture of step() is not supported by this build (its "
-                               "Newton-Schulz lr and NorMuon step scalars are host values)")
+        capturing = self._assert_capturable_if_capturing()
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
         self._validate_grads()
-        self._maybe_refresh_gefen_codebook()
+        if capturing:
+            self._assert_capture_ready()
+        else:
+            self._maybe_refresh_gefen_codebook()
+            self._ensure_gefen_global_step_devices()
         lib = _native.load()
         # shape buckets: one Newton-Schulz launch sequence per bucket chunk
         buckets = OrderedDict()
+        capt_rows = {}
         for gi, group in enumerate(self.param_groups):
             for name, p in self._iter_group_params_with_names(group):
                 if p.grad is None or p.numel() == 0:
                     continue
+                if capturing and "step" not in self.state[p]:
+                    raise RuntimeError("GefenMuon capturable: parameter {} has no state yet; its first step runs "
+                                       "eagerly".format(name))
+                state = self._prepare_muon_state(name, p, p.grad)
+                if group.get("normuon", False):
+                    v = state.get("normuon_v")
+                    if v is None or v.shape[0] != p.shape[0]:
+                        if capturing:
+                            raise RuntimeError("GefenMuon capturable: NorMuon state of {} is created eagerly".format(
+                                name))
+                        state["normuon_v"] = torch.zeros(p.shape[0], 1, dtype=torch.float32, device=p.device)
+                        state["normuon_step"] = self._new_step_counter(p.device)
+                if self._capt_on:
+                    self._capt_ready_state(state, p, capturing)
+                    capt_rows.setdefault(p.device, []).append(
+                        self._capt_row(group, p, state, "normuon_step" if "normuon_step" in state else None, 0))
                 key = (p.device, tuple(p.shape), p.grad.dtype, gi)
                 buckets.setdefault(key, []).append((group, name, p, p.grad))
+        if self._capt_on:  # step counters, scalar rows, global step and seed on the device
+            for device in self._capt_counters:
+                self._capt_launch(device, [], [], capt_rows.get(device, []), set(), capturing)
         for (device, shape, gdtype, gi), items in buckets.items():
             group = self.param_groups[gi]
             rows, cols = shape
@@ -360,40 +381,44 @@ class GefenMuon(Gefen):
         dcode = _fused._dtype_code(gdtype)
         with torch.cuda.device(device):
             for i, (grp, name, p, grad) in enumerate(chunk):
-                state = self._prepare_muon_state(name, p, grad)
+                state = self.state[p]
                 g = grad if grad.is_contiguous() else grad.contiguous()
                 ws = self._momentum_workspace(state, device)
+                scalars_ptr, seed_ptr = self._capt_pointers(state, device)
                 _native.check(lib.gefenx_quantized_momentum_update(
                     g.data_ptr(), dcode, numel, int(state["automatic_period"]), state["m_codebook"].data_ptr(),
                     state["m_magnitude"].data_ptr(), qt.data_ptr(), mom[i].data_ptr(), float(grp["momentum"]),
-                    1 if self._stochastic_round else 0, self._gefen_global_step, None,
+                    1 if self._stochastic_round else 0, self._kernel_rng_seed(), seed_ptr,
                     1 if grp["nesterov"] else 0, ws.data_ptr(), ws.numel(), stream), "muon momentum of " + name)
-                state["step"] += 1
+                if not self._capt_on:
+                    state["step"] += 1
             ortho = _zeropower_via_newtonschulz_batched(mom, schedule, len(schedule), group["eps"])
-            lr = self._lr_value(group)
+            lr = 0.0 if self._capt_on else self._lr_value(group)  # capturable: read on the device
             wd = group["weight_decay"]
             for i, (grp, name, p, grad) in enumerate(chunk):
                 state = self.state[p]
+                scalars_ptr, _ = self._capt_pointers(state, device)
                 scale_ptr = None
                 if grp.get("normuon", False):
-                    v = state.get("normuon_v")
-                    if v is None or v.shape[0] != rows:
-                        v = torch.zeros(rows, 1, dtype=torch.float32, device=device)
-                        state["normuon_v"] = v
-                        state["normuon_step"] = 0
-                    state["normuon_step"] += 1
+                    v = state["normuon_v"]
+                    step_ptr = None
+                    if self._capt_on:
+                        step_ptr = state["normuon_step"].data_ptr()
+                    else:
+                        state["normuon_step"] += 1
                     scale = self._buffer(("scale", device), rows, torch.bfloat16, device)
                     nws = self._buffer(("nws", device), int(lib.gefenx_normuon_workspace_bytes(rows)), torch.uint8,
                                        device)
                     _native.check(lib.gefenx_normuon_scale(
                         ortho[i].data_ptr(), rows, cols, v.data_ptr(), float(grp["normuon_beta2"]),
-                        int(state["normuon_step"]), float(grp["normuon_eps"]), scale.data_ptr(), nws.data_ptr(),
-                        nws.numel(), stream), "normuon of " + name)
+                        0 if self._capt_on else int(state["normuon_step"]), float(grp["normuon_eps"]),
+                        scale.data_ptr(), nws.data_ptr(), nws.numel(), step_ptr, stream), "normuon of " + name)
                     scale_ptr = scale.data_ptr()
-                adjusted = _adjust_lr(lr, grp["adjust_lr_fn"], p.shape)
+                ratio = _adjust_lr_ratio(grp["adjust_lr_fn"], p.shape)
+                adjusted = 0.0 if self._capt_on else _adjust_lr(lr, grp["adjust_lr_fn"], p.shape)
                 pk = p if p.is_contiguous() else p.contiguous()
                 _native.check(lib.gefenx_muon_apply(
                     pk.data_ptr(), _fused._dtype_code(p.dtype), ortho[i].data_ptr(), scale_ptr, rows, cols, lr,
-                    float(wd) if wd > 0.0 else 0.0, adjusted, stream), "muon apply of " + name)
+                    float(wd) if wd > 0.0 else 0.0, adjusted, scalars_ptr, ratio, stream), "muon apply of " + name)
                 if pk is not p:
                     p.copy_(pk)

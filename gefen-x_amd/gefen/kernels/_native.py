@@ -106,8 +106,8 @@ SIGNATURES = {
     "gefenx_ns_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "gefenx_newton_schulz": (_I, [_P, _I, _P, _I64, _I64, _I64, _P, _I, _D, _P, _SZ, _P]),
     "gefenx_normuon_workspace_bytes": (_SZ, [_I64]),
-    "gefenx_normuon_scale": (_I, [_P, _I64, _I64, _P, _D, _I64, _D, _P, _P, _SZ, _P]),
-    "gefenx_muon_apply": (_I, [_P, _I, _P, _P, _I64, _I64, _D, _D, _D, _P]),
+    "gefenx_normuon_scale": (_I, [_P, _I64, _I64, _P, _D, _I64, _D, _P, _P, _SZ, _P, _P]),
+    "gefenx_muon_apply": (_I, [_P, _I, _P, _P, _I64, _I64, _D, _D, _D, _P, _D, _P]),
     "gefenx_gemm_nt_bf16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _P]),
     "gefenx_profile_enable": (_I, [_I]),
     "gefenx_profile_read": (_I, [_I, _P, _P, _P, _P]),

@@ -255,7 +255,8 @@ size_t gefenx_multi_tensor_scratch_bytes(int n);
  * ---------------------------------------------------------------------- */
 typedef struct gefenx_capt_desc {
     float* step;            /* device fp32 0-dim: state["step"] (+= 1) */
-    float* bc2_step;        /* device fp32 0-dim: factored_step or vmean_step (+= 1) */
+    float* bc2_step;        /* device fp32 0-dim: factored_step or vmean_step (+= 1);
+                             * NULL: none (bc2 then uses `step`) */
     float* scalars;         /* device fp32[4] written: lr, 1/bc2 (factored) or
                              * 1/sqrt(bc2) (block), 1/bc1, weight-decay factor */
     const void* lr_dev;     /* NULL: the host `lr` below; else a device 0-dim lr */
@@ -318,19 +319,26 @@ int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch,
 /* NorMuon row scale of a bf16 update [rows, cols] (gefen_muon.py:1192-1230):
  * normuon_v (fp32 [rows], mutated) <- v*beta2 + row_sq*((1-beta2)/cols);
  * scale_out (bf16 [rows]) = bf16(frob_scale / (sqrt(v/(1-beta2^step)) + eps)).
+ * step_dev: NULL, or a device fp32 0-dim step counter read instead of `step`
+ * (capturable mode; the counter is advanced by the capturable prologue).
  * workspace: gefenx_normuon_workspace_bytes(rows) bytes. */
 size_t gefenx_normuon_workspace_bytes(int64_t rows);
 int gefenx_normuon_scale(const void* update, int64_t rows, int64_t cols, float* normuon_v,
                          double beta2, int64_t step, double eps, void* scale_out,
-                         void* workspace, size_t workspace_bytes, void* stream);
+                         void* workspace, size_t workspace_bytes, const float* step_dev,
+                         void* stream);
 
 /* Muon parameter update (gefen_muon.py:1286-1300): p = D(p*(1-lr*wd)) when
  * weight_decay > 0, then p = D(fma(u, D(-adjusted_lr), p)) with u the bf16
  * update [rows, cols], multiplied first by row_scale (bf16 [rows], NorMuon)
- * and rounded to bf16 when row_scale is not NULL. */
+ * and rounded to bf16 when row_scale is not NULL.  step_scalars: NULL, or a
+ * device fp32[4] scalar row of the capturable prologue (gefenx_capt_desc):
+ * then 1-lr*wd is its [3] and adjusted_lr = (double)[0] * lr_ratio
+ * (capturable mode, gefen_muon.py:1243-1270). */
 int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_scale,
                       int64_t rows, int64_t cols, double lr, double weight_decay,
-                      double adjusted_lr, void* stream);
+                      double adjusted_lr, const float* step_scalars, double lr_ratio,
+                      void* stream);
 
 /* The Newton-Schulz GEMM alone: D = bf16(alpha * A B^T + beta * C) for bf16
  * row-major A [M, K], B [N, K], C / D [M, N] (C may be NULL).  No counterpart

@@ -85,8 +85,9 @@ def _compare(opt_a, params_a, opt_b, params_b, tag):
     for (name, pa), (_, pb) in zip(params_a, params_b):
         sa, sb = opt_a.state[pa], opt_b.state[pb]
         for k in ("m_codebook", "m_magnitude"):
-            assert torch.equal(sa[k], sb[k]), "%s %s %s" % (tag, name, k)
-        for k in ("v_row", "v_col", "vmean"):
+            if k in sa or k in sb:
+                assert torch.equal(sa[k], sb[k]), "%s %s %s" % (tag, name, k)
+        for k in ("v_row", "v_col", "vmean", "normuon_v", "exp_avg", "exp_avg_sq"):
             if k in sa:
                 torch.testing.assert_close(sa[k], sb[k], rtol=1e-6, atol=0, msg="%s %s %s" % (tag, name, k))
         torch.testing.assert_close(pa.detach().float(), pb.detach().float(), rtol=2.0 ** -7, atol=1e-9,
@@ -96,7 +97,7 @@ def _compare(opt_a, params_a, opt_b, params_b, tag):
 def _counter_values(opt):
     out = set()
     for st in opt.state.values():
-        for k in ("step", "vmean_step", "factored_step"):
+        for k in ("step", "vmean_step", "factored_step", "normuon_step"):
             if k in st:
                 v = st[k]
                 assert torch.is_tensor(v) and v.is_cuda and v.dim() == 0 and v.dtype == torch.float32, (k, v)
@@ -127,17 +128,19 @@ def test_eager_capturable_matches_host_scalars(dev, factored, sr):
     assert runs[1][0].state_dict()["gefen_global_step"] == steps
 
 
-def _lockstep(dev, specs, dtype, factored, sr, warmup=3, replays=4, lr_start=1e-3, lr_decay=0.9, seed=0):
+def _lockstep(dev, specs, dtype, factored, sr, warmup=3, replays=4, lr_start=1e-3, lr_decay=0.9, seed=0,
+              make=None):
     """Captured optimizer vs eager twin, compared after every step."""
     steps = warmup + replays
     lr_sched = [lr_start * lr_decay ** i for i in range(steps)]
     grads = _grads(seed + 1, specs, steps, dtype, dev)
+    make = make or (lambda ps, lr_: _make_opt(ps, lr_, factored, sr))
     ref_params = _make_params(seed, specs, dtype, dev)
     ref_lr = torch.tensor(lr_start, device=dev)
-    ref_opt = _make_opt(ref_params, ref_lr, factored, sr)
+    ref_opt = make(ref_params, ref_lr)
     params = _make_params(seed, specs, dtype, dev)
     lr = torch.tensor(lr_start, device=dev)
-    opt = _make_opt(params, lr, factored, sr)
+    opt = make(params, lr)
     static = [torch.zeros_like(p) for _, p in params]
     for (_, p), sg in zip(params, static):
         p.grad = sg
@@ -363,3 +366,66 @@ def test_capture_with_grads_produced_in_graph(dev):
         torch.cuda.synchronize()
         _compare(opt, params, ref_opt, ref_params, "in-graph grads step %d" % i)
     assert opt.state_dict()["gefen_global_step"] == steps
+
+
+MUON_SPECS = [("h1", (64, 48)), ("h2", (32, 64)), ("h3", (64, 48))]
+HYBRID_MUON_SPECS = [("h1.weight", (64, 48)), ("h2.weight", (32, 64))]
+HYBRID_BACKUP_SPECS = [("embed.weight", (96, 32)), ("norm.weight", (64,))]
+
+
+def _muon(params, lr, sr=False, capturable=True):
+    from gefen import GefenMuon
+    return GefenMuon(params, lr=lr, weight_decay=WD, normuon=True, stochastic_round=sr, capturable=capturable)
+
+
+def _hybrid(params, lr, backup="gefen", sr=False, capturable=True):
+    from gefen import GefenMuonHybrid
+    n = len(HYBRID_MUON_SPECS)
+    return GefenMuonHybrid(params[:n], params[n:], lr=lr, backup_optimizer=backup, weight_decay=WD,
+                           stochastic_round=sr, capturable=capturable)
+
+
+@pytest.mark.parametrize("sr", [False, True])
+def test_muon_eager_capturable_matches_host_scalars(dev, sr):
+    """GefenMuon (NorMuon on): capturable eager stepping equals the host path;
+    step and normuon_step are device counters."""
+    _say("muon eager parity sr=%s" % sr)
+    steps, dtype = 5, torch.bfloat16
+    grads = _grads(3, MUON_SPECS, steps, dtype, dev)
+    runs = []
+    for capturable in (False, True):
+        params = _make_params(2, MUON_SPECS, dtype, dev)
+        opt = _muon(params, 1e-3, sr, capturable)
+        for i in range(steps):
+            for (_, p), g in zip(params, grads[i]):
+                p.grad = g.clone()
+            opt.step()
+        runs.append((opt, params))
+    torch.cuda.synchronize()
+    _compare(runs[1][0], runs[1][1], runs[0][0], runs[0][1], "muon capturable vs host")
+    assert _counter_values(runs[1][0]) == {float(steps)}
+    assert any("normuon_step" in st for st in runs[1][0].state.values())
+
+
+@pytest.mark.parametrize("sr", [False, True])
+def test_muon_graph_replay_matches_eager_every_step(dev, sr):
+    _say("muon lockstep replay sr=%s" % sr)
+    opt, params, _, steps, lr_sched, _ = _lockstep(dev, MUON_SPECS, torch.bfloat16, False, sr, seed=11,
+                                                   make=lambda ps, lr: _muon(ps, lr, sr))
+    assert _counter_values(opt) == {float(steps)}
+    for _, p in params:
+        got = [float(x) for x in opt.state[p]["_capt_scalars"].cpu().tolist()]
+        lr32 = float(np.float32(lr_sched[-1]))
+        assert got[0] == lr32 and got[3] == float(np.float32(1.0 - lr32 * WD)), got
+    assert opt.state_dict()["gefen_global_step"] == steps
+
+
+@pytest.mark.parametrize("backup", ["gefen", "adamw"])
+def test_hybrid_graph_replay_matches_eager_every_step(dev, backup):
+    _say("hybrid lockstep replay backup=%s" % backup)
+    specs = HYBRID_MUON_SPECS + HYBRID_BACKUP_SPECS
+    opt, params, _, steps, _, _ = _lockstep(dev, specs, torch.float32, False, False, seed=21,
+                                            make=lambda ps, lr: _hybrid(ps, lr, backup))
+    assert _counter_values(opt.muon) == {float(steps)}
+    if backup == "gefen":
+        assert _counter_values(opt.backup) == {float(steps)}

@@ -170,7 +170,10 @@ def test_newton_schulz_fp32_input(dev, lib):
 
 
 @pytest.mark.parametrize("dtype", [orc.BF16, orc.F32])
-def test_normuon_and_apply_match_oracle(dev, lib, dtype):
+@pytest.mark.parametrize("device_scalars", [False, True])
+def test_normuon_and_apply_match_oracle(dev, lib, dtype, device_scalars):
+    """device_scalars: the capturable form (step counter and the scalar row
+    [lr, -, -, 1 - lr*wd] read on the device) gives the same result."""
     from gefen.kernels import automatic_gefen_fused as fused
     td = TORCH_DT[dtype]
     rng = np.random.default_rng(9)
@@ -182,13 +185,19 @@ def test_normuon_and_apply_match_oracle(dev, lib, dtype):
     vd = torch.from_numpy(v0.copy()).to(dev)
     scale = torch.empty(R, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(int(lib.gefenx_normuon_workspace_bytes(R)), dtype=torch.uint8, device=dev)
-    _check(lib.gefenx_normuon_scale(ud.data_ptr(), R, C, vd.data_ptr(), 0.95, 3, 1e-8, scale.data_ptr(),
-                                    ws.data_ptr(), ws.numel(), _stream(dev)), lib)
-    pd = torch.from_numpy(p0.copy()).to(td).to(dev)
     lr, wd = 1e-3, 0.01
-    adj = lr * orc.adjust_lr_ratio("match_rms_adamw", (R, C))
-    _check(lib.gefenx_muon_apply(pd.data_ptr(), fused._dtype_code(td), ud.data_ptr(), scale.data_ptr(), R, C, lr, wd,
-                                 adj, _stream(dev)), lib)
+    ratio = orc.adjust_lr_ratio("match_rms_adamw", (R, C))
+    adj = lr * ratio
+    step_dev = torch.full((), 3.0, dtype=torch.float32, device=dev) if device_scalars else None
+    row = (torch.tensor([np.float32(lr), 1.0, 1.0, np.float32(1.0 - lr * wd)], dtype=torch.float32, device=dev)
+           if device_scalars else None)
+    _check(lib.gefenx_normuon_scale(ud.data_ptr(), R, C, vd.data_ptr(), 0.95, 0 if device_scalars else 3, 1e-8,
+                                    scale.data_ptr(), ws.data_ptr(), ws.numel(),
+                                    step_dev.data_ptr() if device_scalars else None, _stream(dev)), lib)
+    pd = torch.from_numpy(p0.copy()).to(td).to(dev)
+    _check(lib.gefenx_muon_apply(pd.data_ptr(), fused._dtype_code(td), ud.data_ptr(), scale.data_ptr(), R, C,
+                                 0.0 if device_scalars else lr, wd, 0.0 if device_scalars else adj,
+                                 row.data_ptr() if device_scalars else None, ratio, _stream(dev)), lib)
     torch.cuda.synchronize()
     o2, v = orc.normuon(upd, v0, 3)
     np.testing.assert_allclose(vd.cpu().numpy(), v, rtol=1e-6)
