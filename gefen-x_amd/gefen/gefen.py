@@ -200,9 +200,10 @@ class Gefen(torch.optim.Optimizer):
             groups = []
             for gi, g in enumerate(params):
                 g = dict(g)
-                names, ps = self._split_names(g["params"], prefix="group_{}_param_".format(gi))
+                names, ps, synth = self._split_names(g["params"], prefix="group_{}_param_".format(gi))
                 g["params"] = ps
                 g["param_names"] = names
+                g["param_names_synthesized"] = synth
                 if "betas" in g:
                     b = g.pop("betas")
                     g["beta1"], g["beta2"] = b
@@ -210,19 +211,21 @@ class Gefen(torch.optim.Optimizer):
                                              g.get("eps", 0.0), g.get("weight_decay", 0.0))
                 groups.append(g)
             return groups
-        names, ps = self._split_names(params, prefix="param_")
-        return [{"params": ps, "param_names": names}]
+        names, ps, synth = self._split_names(params, prefix="param_")
+        return [{"params": ps, "param_names": names, "param_names_synthesized": synth}]
 
     def _split_names(self, items, prefix):
         if isinstance(items, torch.Tensor):
             items = [items]
-        names, ps = [], []
+        names, ps, synth = [], [], []
         seen = set(self._param_names.values())
         for i, it in enumerate(list(items)):
             if isinstance(it, (tuple, list)) and len(it) == 2 and isinstance(it[0], str):
                 name, p = str(it[0]).lower(), it[1]
+                synth.append(False)
             else:
                 name, p = "{}{}".format(prefix, i), it
+                synth.append(True)
             if not isinstance(p, torch.Tensor):
                 raise TypeError("optimizer can only optimize Tensors, got {}".format(type(p)))
             base, k = name, 1
@@ -233,7 +236,7 @@ class Gefen(torch.optim.Optimizer):
             self._param_names[p] = name
             names.append(name)
             ps.append(p)
-        return names, ps
+        return names, ps, synth
 
     def _iter_group_params_with_names(self, group):
         names = group.get("param_names") or [self._param_names.get(p, "param") for p in group["params"]]
@@ -805,56 +808,128 @@ class Gefen(torch.optim.Optimizer):
         step and deterministic flag recorded; metadata mirrored per group."""
         self._synchronize_gefen_global_step_for_checkpoint()
         sd = super().state_dict()
-        for st in sd["state"].values():
-            for k in _RUNTIME_STATE_KEYS:
-                st.pop(k, None)
+        state = {}
+        for pid, st in sd["state"].items():
+            state[pid] = {k: v for k, v in st.items() if k not in _RUNTIME_STATE_KEYS}
+        # every parameter carries its stable name (gefen.py:4562-4565), also
+        # before its first step
+        for g_saved, g_live in zip(sd["param_groups"], self.param_groups):
+            for pid, (name, _) in zip(g_saved["params"], self._iter_group_params_with_names(g_live)):
+                entry = state.setdefault(pid, {})
+                entry["name"] = entry.get("name", name)
+        sd["state"] = {pid: state[pid] for pid in sorted(state)}
         codebook = None if self._gefen_codebook is None else self._gefen_codebook.detach().cpu().clone()
         sd["gefen_global_step"] = self._gefen_global_step
         sd["gefen_deterministic"] = self._deterministic
         sd["gefen_codebook"] = codebook
+        anchor = next((p.device for g in self.param_groups for p in g["params"]), torch.device("cpu"))
         meta = {"format_version": _CHECKPOINT_FORMAT_VERSION, "global_step": self._gefen_global_step,
-                "codebook": codebook, "deterministic": self._deterministic}
+                "codebook": codebook, "deterministic": self._deterministic,
+                "device_anchor": torch.zeros(1, dtype=torch.uint8, device=anchor)}
         for g in sd["param_groups"]:
             g["_gefen_checkpoint_metadata"] = meta
         return sd
+
+    def _checkpoint_metadata(self, metas, n_groups, global_step, codebook, deterministic, has_det):
+        """Checks of gefen.py:5478-5603: per-group metadata present on all
+        groups or none, consistent, agreeing with the top-level keys; the
+        replica-determinism policy must match this optimizer's."""
+        def same_cb(a, b):
+            return a is b or (torch.is_tensor(a) and torch.is_tensor(b) and torch.equal(a.cpu(), b.cpu()))
+
+        if has_det and type(deterministic) is not bool:
+            raise ValueError("Gefen checkpoint top-level deterministic policy must be a bool, got {!r}".format(
+                deterministic))
+        if metas:
+            if len(metas) != n_groups:
+                raise ValueError("Gefen checkpoint metadata is present on only some parameter groups")
+            first = metas[0]
+            if first.get("format_version") not in (1, 2):
+                raise ValueError("Unsupported Gefen checkpoint metadata format_version: {}".format(
+                    first.get("format_version")))
+            for m in metas:
+                if "deterministic" in m and type(m["deterministic"]) is not bool:
+                    raise ValueError("Gefen checkpoint parameter-group deterministic policy must be a bool, "
+                                     "got {!r}".format(m["deterministic"]))
+            for m in metas[1:]:
+                if (m.get("global_step") != first.get("global_step")
+                        or not same_cb(m.get("codebook"), first.get("codebook"))
+                        or m.get("deterministic") != first.get("deterministic")):
+                    raise ValueError("Gefen checkpoint parameter groups carry inconsistent optimizer metadata")
+            if global_step is None:
+                global_step = first.get("global_step", 0)
+            elif global_step != first.get("global_step", 0):
+                raise ValueError("Gefen checkpoint top-level and parameter-group global steps disagree")
+            if codebook is None:
+                codebook = first.get("codebook")
+            elif first.get("codebook") is not None and not same_cb(codebook, first.get("codebook")):
+                raise ValueError("Gefen checkpoint top-level and parameter-group codebooks disagree")
+            if deterministic is None:
+                deterministic = first.get("deterministic")
+            elif first.get("deterministic") is not None and deterministic != first.get("deterministic"):
+                raise ValueError("Gefen checkpoint top-level and parameter-group deterministic policies disagree")
+        if deterministic is not None and deterministic != self._deterministic:
+            raise ValueError("Gefen checkpoint deterministic={!r}, but this optimizer was constructed with "
+                             "deterministic={!r}; refusing to change the replica-determinism policy "
+                             "silently".format(deterministic, self._deterministic))
+        return (0 if global_step is None else global_step), codebook, deterministic
 
     def load_state_dict(self, state_dict):
         """gefen.py:5456-5707: restore saved state dtypes (torch casts floating
         state to the param dtype) and the optimizer-level codebook/step."""
         sd = dict(state_dict)
         global_step = sd.pop("gefen_global_step", None)
-        sd.pop("gefen_deterministic", None)
+        has_det = "gefen_deterministic" in sd
+        deterministic = sd.pop("gefen_deterministic", None)
         codebook = sd.pop("gefen_codebook", None)
-        meta = None
+        metas = []
         groups = []
         for g in sd["param_groups"]:
             g = dict(g)
-            meta = g.pop("_gefen_checkpoint_metadata", meta)
+            m = g.pop("_gefen_checkpoint_metadata", None)
+            if m is not None:
+                metas.append(m)
             groups.append(g)
         sd["param_groups"] = groups
-        saved = {k: {kk: (vv.dtype if torch.is_tensor(vv) else None) for kk, vv in v.items()}
-                 for k, v in sd["state"].items()}
+        global_step, codebook, deterministic = self._checkpoint_metadata(
+            metas, len(groups), global_step, codebook, deterministic, has_det)
+        if any(isinstance(st, dict) and "m_codebook" in st for st in (sd.get("state") or {}).values()) \
+                and codebook is None:
+            raise ValueError("Gefen checkpoint contains quantized momentum indices but no frozen codebook; loading "
+                             "it would reinterpret the restored indices with a different codebook")
+        # torch's loader rebuilds every iterable it meets (a str becomes the
+        # text of a generator), so names bypass it
+        names = {}
+        state = {}
+        for pid, st in (sd.get("state") or {}).items():
+            st = dict(st)
+            if isinstance(st.get("name"), str):
+                names[pid] = st.pop("name")
+            state[pid] = st
+        sd["state"] = state
+        saved = {k: {kk: vv for kk, vv in v.items() if torch.is_tensor(vv)} for k, v in sd["state"].items()}
         super().load_state_dict(sd)
         id_map = {}
         for gi, g in enumerate(self.param_groups):
             for p in g["params"]:
                 id_map[len(id_map)] = p
-        for pid, dtypes in saved.items():
+        for pid, name in names.items():
+            if pid in id_map:
+                self.state[id_map[pid]]["name"] = name
+        for pid, tensors in saved.items():
             p = id_map.get(pid)
             if p is None:
                 continue
             st = self.state[p]
-            for k, dt in dtypes.items():
-                if dt is not None and torch.is_tensor(st.get(k)) and st[k].dtype != dt:
-                    st[k] = st[k].to(dt)
+            # torch casts floating state to the parameter's dtype; restore the
+            # saved tensor instead (a cast back would keep the bf16 rounding)
+            for k, v in tensors.items():
+                if torch.is_tensor(st.get(k)) and st[k].dtype != v.dtype:
+                    st[k] = v.to(device=st[k].device, dtype=v.dtype)
             for k in _COUNTER_KEYS:  # counters follow this optimizer's capturable mode (gefen.py:5680-5705)
                 if k in st:
                     v = st[k].item() if torch.is_tensor(st[k]) else st[k]
                     st[k] = self._new_step_counter(p.device, v)
-        if global_step is None and meta is not None:
-            global_step = meta.get("global_step")
-        if codebook is None and meta is not None:
-            codebook = meta.get("codebook")
         if global_step is not None:
             self._gefen_global_step = int(global_step)
         if self._capt_on:

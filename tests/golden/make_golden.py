@@ -18,6 +18,8 @@ Cases (each a separate file so they can be regenerated independently):
   muon_ns.npz      _zeropower_via_newtonschulz on bf16 inputs gefen_muon.py:236-291
   muon_<dt>.npz    GefenMuon(fused=False) trajectories         gefen_muon.py:2945-3030
   hybrid_bf16.npz  GefenMuonHybrid(fused=False) trajectory      hybrid.py:693-776
+  ckpt_<name>.pt   a reference-written Gefen checkpoint            gefen.py:4558-4707
+  ckpt_<name>.npz  the reference's trajectory after loading it     gefen.py:5456-5707
 
 Usage:  python tests/golden/make_golden.py [case ...]   (default: all but config1)
 """
@@ -484,6 +486,64 @@ def case_hybrid():
     _save("hybrid_bf16.npz", **out)
 
 
+# --------------------------------------------------------------- checkpoints
+
+CKPT_CASES = {
+    # name: (trajectory case whose params/grads are used, steps before the checkpoint)
+    "fact_bf16": ("fact_bf16", 3),
+    "block_bf16": ("block_bf16", 3),
+}
+
+
+def case_checkpoint(name):
+    """A reference-written checkpoint (ckpt_<name>.pt: Gefen.state_dict() after
+    `pre` steps, period search and codebook learned by the reference itself,
+    gefen.py:4558-4707) and the trajectory a fresh reference optimizer takes
+    after loading it (gefen.py:5456-5707) and stepping the remaining grads
+    (ckpt_<name>.npz).  The .pt holds only tensors, numbers, strings and
+    containers, so tests load it with torch.load(weights_only=True)."""
+    import copy
+    _ref()
+    from gefen import Gefen
+    traj_name, pre = CKPT_CASES[name]
+    dtype, factored, params, grads, wd, steps = step_case_inputs(traj_name)
+    ps = [(n, torch.nn.Parameter(t.clone())) for n, t, _ in params]
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        opt = Gefen(ps, lr=LR, betas=BETAS, eps=EPS, weight_decay=wd, fused=False, factored_v_2d=factored)
+    for step_grads in grads[:pre]:
+        for (_, p), gv in zip(ps, step_grads):
+            p.grad = gv.clone()
+        opt.step()
+    sd = copy.deepcopy(opt.state_dict())
+    torch.save(sd, os.path.join(HERE, "ckpt_%s.pt" % name))
+    torch.load(os.path.join(HERE, "ckpt_%s.pt" % name), weights_only=True)  # loadable without unpickling code
+    out = {"pre": np.int64(pre), "steps": np.int64(steps), "factored": np.int64(factored), "wd": np.float64(wd)}
+    for n, p in ps:
+        out["p%d_%s" % (pre, n)] = _f32(p)
+    # resume: fresh params holding the trained values, fresh optimizer, load, step on
+    ps2 = [(n, torch.nn.Parameter(p.detach().clone())) for n, p in ps]
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        opt2 = Gefen(ps2, lr=LR, betas=BETAS, eps=EPS, weight_decay=wd, fused=False, factored_v_2d=factored)
+        opt2.load_state_dict(copy.deepcopy(sd))
+    for s in range(pre + 1, steps + 1):
+        for (n, p), gv in zip(ps2, grads[s - 1]):
+            p.grad = gv.clone()
+            out["g%d_%s" % (s, n)] = _f32(gv)
+        opt2.step()
+        for n, p in ps2:
+            st = opt2.state[p]
+            out["p%d_%s" % (s, n)] = _f32(p)
+            out["idx%d_%s" % (s, n)] = st["m_codebook"].numpy().reshape(-1).copy()
+            out["mag%d_%s" % (s, n)] = _f32(st["m_magnitude"]).reshape(-1)
+            for key in ("v_row", "v_col", "vmean"):
+                if key in st:
+                    out["%s%d_%s" % (key, s, n)] = _f32(st[key]).reshape(-1)
+    out["global_step"] = np.int64(opt2.state_dict()["gefen_global_step"])
+    _save("ckpt_%s.npz" % name, **out)
+
+
 CASES = {"nearest": case_nearest, "lut": case_lut, "dp": case_dp,
          "learn": case_learn, "period": case_period, "config1": case_config1}
 for _n in STEP_CASES:
@@ -492,6 +552,8 @@ CASES["muon_ns"] = case_muon_ns
 for _n in MUON_CASES:
     CASES[_n] = (lambda n=_n: case_muon(n))
 CASES["hybrid"] = case_hybrid
+for _n in CKPT_CASES:
+    CASES["ckpt_" + _n] = (lambda n=_n: case_checkpoint(n))
 
 
 def main(argv):
