@@ -27,6 +27,17 @@ template <class T> __device__ __forceinline__ const GX_GLOBAL T* gbl(const T* p)
     return (const GX_GLOBAL T*)p;
 }
 
+// Atomics on device memory through the global address space: they become
+// global_atomic_* instructions, which the compiler's wait-counter tracking
+// orders with the other vector memory operations (a flat atomic makes every
+// later wait drain all outstanding loads).
+__device__ __forceinline__ void gatomic_max(uint32_t* p, uint32_t v) {
+    (void)__hip_atomic_fetch_max(gbl(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void gatomic_add(double* p, double v) {
+    (void)__hip_atomic_fetch_add(gbl(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int DT> struct Elem { using T = uint16_t; };
 template <> struct Elem<F32> { using T = float; };
 
@@ -169,11 +180,22 @@ struct MomentumCoef {
 };
 
 // u = lerp(cr * mag_old, g, w): gefen.py:3465-3470 / ATen lerp kernel.
+// LF picks lerp's form at compile time: 1 small weight (fma(w, g - cm, cm)),
+// 2 large weight (fma(w - 1, g - cm, g)), 0 decided per call from mc.small.
+// Hot loops take 1 or 2 (the choice is uniform over a launch), so the
+// compiler does not evaluate both forms and select.
+constexpr int kLerpRuntime = 0;
+constexpr int kLerpSmall = 1;
+constexpr int kLerpLarge = 2;
+
+template <int LF = kLerpRuntime>
 __device__ __forceinline__ float momentum_value(float cr, float mag_old, float g,
                                                 const MomentumCoef& mc) {
     const float cm = cr * mag_old;
     const float d = g - cm;
-    return mc.small ? __builtin_fmaf(mc.w, d, cm) : __builtin_fmaf(mc.wm1, d, g);
+    if constexpr (LF == kLerpSmall) return __builtin_fmaf(mc.w, d, cm);
+    else if constexpr (LF == kLerpLarge) return __builtin_fmaf(mc.wm1, d, g);
+    else return mc.small ? __builtin_fmaf(mc.w, d, cm) : __builtin_fmaf(mc.wm1, d, g);
 }
 
 // Nearest-codeword index through the exact threshold table (see gefenx_host.cpp).

@@ -41,6 +41,7 @@ constexpr int64_t kWaves = kThreads / 64;
 constexpr int64_t kApplyChunksPerThread = 8;   // apply: 4 iterations of 2 chunks
 constexpr int64_t kBlockStatsChunksPerThread = 8;
 constexpr int64_t kFinBlocksPerWg = 1024;
+constexpr int64_t kDefaultCohortElems = 0;  // one cohort per step (see cohort_limit)
 
 struct StepScalars {
     float lr, inv_bc2, inv_bc1, wdf;
@@ -106,7 +107,7 @@ struct WaveMax {
 __device__ __forceinline__ void wavemax_flush(uint32_t* __restrict__ mb, WaveMax& wm) {
     if (wm.blk >= 0) {
         const uint32_t m = wave_max_u(wm.bits);
-        if ((threadIdx.x & 63) == 0 && m != 0u) atomicMax(mb + wm.blk, m);
+        if ((threadIdx.x & 63) == 0 && m != 0u) gatomic_max(mb + wm.blk, m);
     }
     wm.bits = 0u;
 }
@@ -115,7 +116,7 @@ __device__ __forceinline__ void wavemax_flush(uint32_t* __restrict__ mb, WaveMax
 __device__ __forceinline__ void wavemax_flush63(uint32_t* __restrict__ mb, WaveMax& wm) {
     if (wm.blk >= 0) {
         const uint32_t m = wave_max_u63(wm.bits);
-        if ((threadIdx.x & 63) == 63 && m != 0u) atomicMax(mb + wm.blk, m);
+        if ((threadIdx.x & 63) == 63 && m != 0u) gatomic_max(mb + wm.blk, m);
     }
     wm.bits = 0u;
 }
@@ -130,14 +131,21 @@ __device__ __forceinline__ void wavemax_flush63(uint32_t* __restrict__ mb, WaveM
 // Both go out as float64 partials (no float atomics, deterministic).
 // FAST: contiguous, 16-byte aligned grad, C % 8 == 0, P % 8 == 0.
 // ====================================================================
-template <int DT, bool FAST>
-__device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg) {
+struct FactStatsLds {
+    float cbr[kCodebookMax];
+    double col[kWaves][kChunk][2][64];  // float64 column sums: [wave][k][h][lane]
+    int64_t wblk[kWaves];
+    uint32_t wbits[kWaves];
+};
+
+template <int DT, bool FAST, int LF>
+__device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg, FactStatsLds& lds) {
     using T = typename Elem<DT>::T;
     constexpr int H = 2;  // chunks per lane per row
-    __shared__ float s_cbr[kCodebookMax];
-    __shared__ double s_col[kWaves - 1][kFactTileCols];
-    __shared__ int64_t s_wblk[kWaves];
-    __shared__ uint32_t s_wbits[kWaves];
+    float* s_cbr = lds.cbr;
+    auto& s_col = lds.col;
+    int64_t* s_wblk = lds.wblk;
+    uint32_t* s_wbits = lds.wbits;
     const QTable* qt = wr.qt;
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
 
@@ -154,17 +162,20 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: row state in SGPRs
     const int64_t ctile = wg % ct;
     const int64_t rtile = wg / ct;
     const int64_t tc0 = ctile * kFactTileCols;
     const int64_t span = std::min<int64_t>(kFactTileCols, C - tc0);
-    int64_t cc[H];
+    int64_t cc[H], ccl[H];
     int nv[H];
 #pragma unroll
     for (int h = 0; h < H; ++h) {
         cc[h] = tc0 + h * (kFactTileCols / 2) + (int64_t)lane * kChunk;
         nv[h] = (int)std::max<int64_t>(0, std::min<int64_t>(kChunk, C - cc[h]));
+        // FAST loads every chunk unconditionally: a chunk past C (nv == 0,
+        // skipped by the math) reads the row's last chunk instead
+        ccl[h] = nv[h] > 0 ? cc[h] : C - kChunk;
     }
     const int64_t r_begin = rtile * tile_rows;
     const int64_t r_end = std::min<int64_t>(r_begin + tile_rows, R);
@@ -181,49 +192,82 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
     const int64_t dB4 = div_floor(d4, P, invP);
     const int64_t dP4 = d4 - dB4 * P;
 
+    // column sums: fp32 in registers over 8 rows, then added into the wave's
+    // float64 slots in LDS (each lane owns its 16 columns' slots)
     float colf[H][kChunk];
-    double cold[H][kChunk];
 #pragma unroll
     for (int h = 0; h < H; ++h)
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) { colf[h][k] = 0.0f; cold[h][k] = 0.0; }
+        for (int k = 0; k < kChunk; ++k) { colf[h][k] = 0.0f; s_col[wave][k][h][lane] = 0.0; }
+    auto flush_cols = [&]() {
+#pragma unroll
+        for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                s_col[wave][k][h][lane] += (double)colf[h][k];
+                colf[h][k] = 0.0f;
+            }
+    };
     int nrows_f = 0;
     WaveMax wm{-1, 0u};
     float mag_cur = 0.0f;
+    bool mag_ok = false;
+    // chunk h of every lane inside C (hall) / of some lane (hany): wave-uniform
+    bool hall[H], hany[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        hall[h] = tc0 + (h + 1) * (kFactTileCols / 2) <= C;
+        hany[h] = tc0 + h * (kFactTileCols / 2) < C;
+    }
 
-    for (int64_t r0 = r_begin + wave; r0 < r_end; r0 += 2 * kWaves) {
-        // loads of two rows (r0, r0 + 4) before any math
+    // One batch = the wave's next two rows (r0, r0 + 4): raw grads and
+    // indices, plus (FAST) the old magnitude of each row segment's first
+    // block.  FAST keeps the next batch in flight while the current one is
+    // reduced, so a wave never waits for a load it issued in the same step.
+    struct Batch {
         Raw8<DT> graw[2][H];
         RawIdx8 iraw[2][H];
         float gsc[2][H][kChunk];
         uint32_t isc[2][H][kChunk];
+        float mo[2];
+    };
+    int64_t pblk = blk, ppin = pin;  // block position of the next batch to load
+    auto load_batch = [&](int64_t rr0, Batch& b) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int64_t r = r0 + (int64_t)u * kWaves;
+            const int64_t r = rr0 + (int64_t)u * kWaves;
+            if constexpr (FAST) {
+                // rows past the tile re-read the tile's last row; the math
+                // stops before them (C % 8 == 0, so nv is 0 or 8)
+                const int64_t rl = r < r_end ? r : r_end - 1;
 #pragma unroll
-            for (int h = 0; h < H; ++h) {
-                const int64_t e0 = r * C + cc[h];
-                if constexpr (FAST) {
-                    if (r < r_end && nv[h] == kChunk) {
-                        load_raw8<DT>(g + e0, graw[u][h]);
-                        iraw[u][h] = load_raw_idx8(idxp + e0);
-                    } else {
-                        graw[u][h] = Raw8<DT>{};
-                        iraw[u][h] = RawIdx8{0u, 0u};
-                    }
-                } else {
+                for (int h = 0; h < H; ++h) {
+                    const int64_t el = rl * C + ccl[h];
+                    load_raw8<DT>(g + el, b.graw[u][h]);
+                    b.iraw[u][h] = load_raw_idx8(idxp + el);
+                }
+                b.mo[u] = *gbl(mag_old + (pblk < nb ? pblk : nb - 1));
+                ppin += dP4;
+                pblk += dB4;
+                if (ppin >= P) { ppin -= P; ++pblk; }
+            } else {
+#pragma unroll
+                for (int h = 0; h < H; ++h) {
+                    const int64_t e0 = r * C + cc[h];
 #pragma unroll
                     for (int k = 0; k < kChunk; ++k) {
                         const bool ok = r < r_end && k < nv[h];
-                        gsc[u][h][k] = ok ? to_f32<DT>(*gbl(g + r * gs0 + (cc[h] + k) * gs1)) : 0.0f;
-                        isc[u][h][k] = ok ? (uint32_t)*gbl(idxp + e0 + k) : 0u;
+                        b.gsc[u][h][k] = ok ? to_f32<DT>(*gbl(g + r * gs0 + (cc[h] + k) * gs1)) : 0.0f;
+                        b.isc[u][h][k] = ok ? (uint32_t)*gbl(idxp + e0 + k) : 0u;
                     }
                 }
             }
         }
+    };
+    auto reduce_batch = [&](int64_t rr0, const Batch& b) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int64_t r = r0 + (int64_t)u * kWaves;
+            const int64_t r = rr0 + (int64_t)u * kWaves;
             if (r >= r_end) break;
             float rs[H];
             const bool uniform = (pin + span - 1) < P;
@@ -231,29 +275,79 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
                 if (blk != wm.blk) {
                     wavemax_flush63(mb, wm);
                     wm.blk = blk;
-                    mag_cur = *gbl(mag_old + blk);
-                }
-                uint32_t m = wm.bits;
-#pragma unroll
-                for (int h = 0; h < H; ++h) {
-                    rs[h] = 0.0f;
-                    if (nv[h] == 0) continue;  // columns past C (last tile)
-#pragma unroll
-                    for (int k = 0; k < kChunk; ++k) {
-                        if (!FAST && k >= nv[h]) continue;
-                        float gv;
-                        uint32_t ix;
-                        if constexpr (FAST) { gv = raw_elem<DT>(graw[u][h], k); ix = raw_idx(iraw[u][h], k); }
-                        else { gv = gsc[u][h][k]; ix = isc[u][h][k]; }
-                        const float uu = momentum_value(s_cbr[ix], mag_cur, gv, mc);
-                        const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
-                        m = ub > m ? ub : m;
-                        const float sq = gv * gv;
-                        rs[h] += sq;
-                        colf[h][k] += sq;
+                    if constexpr (FAST) {
+                        mag_cur = b.mo[u];
+                        mag_ok = (__float_as_uint(mag_cur) & 0x7fffffffu) < 0x7e967699u;  // |m| < 1e38, not NaN
+                    } else {
+                        mag_cur = *gbl(mag_old + blk);
                     }
                 }
-                wm.bits = m;
+                if constexpr (FAST) {
+                    // |u| max as floats (v_max3 with |.| modifiers).  Exact when
+                    // every u is finite, which holds when the old magnitude is
+                    // below 1e38 and every g^2 is finite (then |g - cm| cannot
+                    // overflow); otherwise the row is redone with the ordered
+                    // integer max, which ranks NaN above inf like torch's amax.
+                    float mf = 0.0f;
+                    auto chunk = [&](int h, auto masked) {
+                        rs[h] = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < kChunk; ++k) {
+                            float gv = raw_elem<DT>(b.graw[u][h], k);
+                            if constexpr (decltype(masked)::value) gv = nv[h] > 0 ? gv : 0.0f;
+                            const float uu = momentum_value<LF>(s_cbr[raw_idx(b.iraw[u][h], k)], mag_cur, gv, mc);
+                            if constexpr (decltype(masked)::value) mf = nv[h] > 0 ? __builtin_fmaxf(mf, fabsf(uu)) : mf;
+                            else mf = __builtin_fmaxf(mf, fabsf(uu));
+                            rs[h] = __builtin_fmaf(gv, gv, rs[h]);
+                            colf[h][k] = __builtin_fmaf(gv, gv, colf[h][k]);
+                        }
+                    };
+#pragma unroll
+                    for (int h = 0; h < H; ++h) {
+                        if (hall[h]) chunk(h, std::false_type{});
+                        else if (hany[h]) chunk(h, std::true_type{});
+                        else rs[h] = 0.0f;
+                    }
+                    // integer test: NaN and inf both fail it, whatever the
+                    // compiler assumes about float compares
+                    const bool fin = (__float_as_uint(rs[0] + rs[1]) & 0x7fffffffu) < 0x7f800000u;
+                    if (__builtin_expect(mag_ok && __all(fin), 1)) {
+                        const uint32_t mb_ = __float_as_uint(mf);
+                        wm.bits = mb_ > wm.bits ? mb_ : wm.bits;
+                    } else {
+                        uint32_t m = wm.bits;
+#pragma unroll
+                        for (int h = 0; h < H; ++h) {
+                            if (nv[h] == 0) continue;
+#pragma unroll
+                            for (int k = 0; k < kChunk; ++k) {
+                                const float uu = momentum_value<LF>(s_cbr[raw_idx(b.iraw[u][h], k)], mag_cur,
+                                                                    raw_elem<DT>(b.graw[u][h], k), mc);
+                                const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
+                                m = ub > m ? ub : m;
+                            }
+                        }
+                        wm.bits = m;
+                    }
+                } else {
+                    uint32_t m = wm.bits;
+#pragma unroll
+                    for (int h = 0; h < H; ++h) {
+                        rs[h] = 0.0f;
+                        if (nv[h] == 0) continue;  // columns past C (last tile)
+#pragma unroll
+                        for (int k = 0; k < kChunk; ++k) {
+                            if (k >= nv[h]) continue;
+                            const float gv = b.gsc[u][h][k];
+                            const float uu = momentum_value<LF>(s_cbr[b.isc[u][h][k]], mag_cur, gv, mc);
+                            const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
+                            m = ub > m ? ub : m;
+                            rs[h] = __builtin_fmaf(gv, gv, rs[h]);
+                            colf[h][k] = __builtin_fmaf(gv, gv, colf[h][k]);
+                        }
+                    }
+                    wm.bits = m;
+                }
             } else {
                 // blocks end inside this row segment: per-lane runs, one atomic per run
                 wavemax_flush63(mb, wm);
@@ -273,16 +367,15 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
                         if (k < nv[h]) {
                             float gv;
                             uint32_t ix;
-                            if constexpr (FAST) { gv = raw_elem<DT>(graw[u][h], k); ix = raw_idx(iraw[u][h], k); }
-                            else { gv = gsc[u][h][k]; ix = isc[u][h][k]; }
-                            const float uu = momentum_value(s_cbr[ix], mo, gv, mc);
+                            if constexpr (FAST) { gv = raw_elem<DT>(b.graw[u][h], k); ix = raw_idx(b.iraw[u][h], k); }
+                            else { gv = b.gsc[u][h][k]; ix = b.isc[u][h][k]; }
+                            const float uu = momentum_value<LF>(s_cbr[ix], mo, gv, mc);
                             const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
                             m = ub > m ? ub : m;
-                            const float sq = gv * gv;
-                            rs[h] += sq;
-                            colf[h][k] += sq;
+                            rs[h] = __builtin_fmaf(gv, gv, rs[h]);
+                            colf[h][k] = __builtin_fmaf(gv, gv, colf[h][k]);
                             if (++pp == P) {
-                                if (m) atomicMax(mb + bb, m);
+                                if (m) gatomic_max(mb + bb, m);
                                 m = 0u;
                                 pp = 0;
                                 ++bb;
@@ -290,7 +383,7 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
                             }
                         }
                     }
-                    if (m) atomicMax(mb + bb, m);
+                    if (m) gatomic_max(mb + bb, m);
                 }
             }
             double rsum = 0.0;
@@ -299,35 +392,51 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
             rsum = wave_sum_d63(rsum);
             if (lane == 63) *gbl(row_part + ctile * R + r) = rsum;
             if (++nrows_f == 8) {
-#pragma unroll
-                for (int h = 0; h < H; ++h)
-#pragma unroll
-                    for (int k = 0; k < kChunk; ++k) { cold[h][k] += (double)colf[h][k]; colf[h][k] = 0.0f; }
+                flush_cols();
                 nrows_f = 0;
             }
             pin += dP4;
             blk += dB4;
             if (pin >= P) { pin -= P; ++blk; }
         }
+    };
+
+    constexpr int64_t kStep = 2 * kWaves;
+    int64_t r0 = r_begin + wave;
+    if (r0 < r_end) {
+        Batch ba, bb;
+        load_batch(r0, ba);
+        if constexpr (FAST) {
+            // The prefetch is unconditional (past the tile it re-reads the
+            // tile's last row, which is still in cache), so every step has
+            // the same loads in flight and the compiler can wait for the
+            // current batch alone instead of draining the queue.
+            for (;;) {
+                load_batch(r0 + kStep, bb);
+                reduce_batch(r0, ba);
+                r0 += kStep;
+                if (r0 >= r_end) break;
+                load_batch(r0 + kStep, ba);
+                reduce_batch(r0, bb);
+                r0 += kStep;
+                if (r0 >= r_end) break;
+            }
+        } else {
+            for (;;) {
+                reduce_batch(r0, ba);
+                r0 += kStep;
+                if (r0 >= r_end) break;
+                load_batch(r0, ba);
+            }
+        }
     }
-#pragma unroll
-    for (int h = 0; h < H; ++h)
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) cold[h][k] += (double)colf[h][k];
+    flush_cols();
 
     // final block-max flush: one atomic per workgroup when the waves agree
     const uint32_t wbits = wm.blk >= 0 ? wave_max_u63(wm.bits) : 0u;
     if (lane == 63) {
         s_wblk[wave] = wm.blk;
         s_wbits[wave] = wbits;
-    }
-    // column partials: waves 1..3 park theirs in LDS, wave 0 adds and stores
-    if (wave > 0) {
-#pragma unroll
-        for (int h = 0; h < H; ++h)
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k)
-                s_col[wave - 1][h * (kFactTileCols / 2) + lane * kChunk + k] = cold[h][k];
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -338,23 +447,23 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg)
             m = s_wbits[ww] > m ? s_wbits[ww] : m;
         }
         if (same) {
-            if (s_wblk[0] >= 0 && m) atomicMax(mb + s_wblk[0], m);
+            if (s_wblk[0] >= 0 && m) gatomic_max(mb + s_wblk[0], m);
         } else {
             for (int ww = 0; ww < kWaves; ++ww)
-                if (s_wblk[ww] >= 0 && s_wbits[ww]) atomicMax(mb + s_wblk[ww], s_wbits[ww]);
+                if (s_wblk[ww] >= 0 && s_wbits[ww]) gatomic_max(mb + s_wblk[ww], s_wbits[ww]);
         }
     }
-    if (wave == 0) {
+    // column partials of the tile: waves summed in order 0..3; thread t
+    // stores columns t, t + 256, ... (coalesced)
 #pragma unroll
-        for (int h = 0; h < H; ++h) {
+    for (int j = 0; j < kFactTileCols / kThreads; ++j) {
+        const int c = threadIdx.x + j * kThreads;
+        const int h = c / (kFactTileCols / 2), cl = c % (kFactTileCols / 2);
+        const int ln = cl / kChunk, k = cl % kChunk;
+        double sum = s_col[0][k][h][ln];
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                double sum = cold[h][k];
-#pragma unroll
-                for (int ww = 0; ww < kWaves - 1; ++ww) sum += s_col[ww][h * (kFactTileCols / 2) + lane * kChunk + k];
-                if (k < nv[h]) *gbl(col_part + rtile * C + cc[h] + k) = sum;
-            }
-        }
+        for (int ww = 1; ww < kWaves; ++ww) sum += s_col[ww][k][h][ln];
+        if (c < span) *gbl(col_part + rtile * C + tc0 + c) = sum;
     }
 }
 
@@ -587,9 +696,9 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
                         if (rsd != 0.0) atomicAdd(&s_bsum[b - b_lo], rsd);
                     }
                 } else {
-                    if (m != 0u) atomicMax(mb + b, m);
+                    if (m != 0u) gatomic_max(mb + b, m);
                     if constexpr (MODE == 1) {
-                        if (rsd != 0.0) atomicAdd(bsq + b, rsd);
+                        if (rsd != 0.0) gatomic_add(bsq + b, rsd);
                     }
                 }
             }
@@ -627,10 +736,10 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
     if (lds_blk) {
         for (int k = tid; k < b_span; k += kThreads) {
             const uint32_t m = s_bmax[k];
-            if (m != 0u) atomicMax(mb + b_lo + k, m);
+            if (m != 0u) gatomic_max(mb + b_lo + k, m);
             if constexpr (MODE == 1) {
                 const double v = s_bsum[k];
-                if (v != 0.0) atomicAdd(bsq + b_lo + k, v);
+                if (v != 0.0) gatomic_add(bsq + b_lo + k, v);
             }
         }
     }
@@ -684,8 +793,8 @@ __device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int
                     if (cur >= 0) {
                         bsum += (double)csum;
                         csum = 0.0f;
-                        if (bsum != 0.0) atomicAdd(bsq + cur, bsum);
-                        if (cbits) atomicMax(mb + cur, cbits);
+                        if (bsum != 0.0) gatomic_add(bsq + cur, bsum);
+                        if (cbits) gatomic_max(mb + cur, cbits);
                     }
                     bsum = 0.0;
                     cbits = 0u;
@@ -709,12 +818,12 @@ __device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int
         const double s = wave_sum_d(bsum);
         const uint32_t m = wave_max_u(cbits);
         if (lane == 0 && c0 >= 0) {
-            if (s != 0.0) atomicAdd(bsq + c0, s);
-            if (m) atomicMax(mb + c0, m);
+            if (s != 0.0) gatomic_add(bsq + c0, s);
+            if (m) gatomic_max(mb + c0, m);
         }
     } else if (cur >= 0) {
-        if (bsum != 0.0) atomicAdd(bsq + cur, bsum);
-        if (cbits) atomicMax(mb + cur, cbits);
+        if (bsum != 0.0) gatomic_add(bsq + cur, bsum);
+        if (cbits) gatomic_max(mb + cur, cbits);
     }
 }
 
@@ -730,8 +839,8 @@ __device__ __forceinline__ void bstats_flush(uint32_t* __restrict__ mb, double* 
     const uint32_t r = wave_max_u63(bits);
     const double t = wave_sum_d63(sum);
     if ((threadIdx.x & 63) == 63) {
-        if (r) atomicMax(mb + blk, r);
-        if (t != 0.0) atomicAdd(bsq + blk, t);
+        if (r) gatomic_max(mb + blk, r);
+        if (t != 0.0) gatomic_add(bsq + blk, t);
     }
 }
 
@@ -802,8 +911,8 @@ __device__ __forceinline__ void stats_block_fast(const TensorWork& w, int64_t wg
             wbits = 0u;
             wsum = 0.0;
             if (valid) {
-                if (m) atomicMax(mb + blk, m);
-                if (cs != 0.0f) atomicAdd(bsq + blk, (double)cs);
+                if (m) gatomic_max(mb + blk, m);
+                if (cs != 0.0f) gatomic_add(bsq + blk, (double)cs);
             }
         }
         pin += dP;
@@ -835,8 +944,8 @@ __device__ __forceinline__ void stats_block_fast(const TensorWork& w, int64_t wg
                     t += s_wsum[v];
                 }
             }
-            if (m) atomicMax(mb + b, m);
-            if (t != 0.0) atomicAdd(bsq + b, t);
+            if (m) gatomic_max(mb + b, m);
+            if (t != 0.0) gatomic_add(bsq + b, t);
         }
     }
 }
@@ -1330,7 +1439,7 @@ __device__ __forceinline__ void fast_load(const FastArgs<DT>& a, const Pos& ps, 
 // Requantise and apply one chunk: new indices in ix, new parameter values
 // in pv.  GENERAL_Q: the table may hold several thresholds per bucket (the
 // fq entries do not describe it), so every element takes the exact search.
-template <int DT, int MODE>
+template <int DT, int MODE, int LF>
 __device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTables& ft, const ChunkIn<DT>& in,
                                           bool general_q, uint32_t ix[kChunk], float pv[kChunk]) {
     const float m_old = in.m_old, m_new = in.m_new, y = in.y;
@@ -1339,7 +1448,7 @@ __device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTable
     bool bad = (y == 0.0f) || general_q;
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        const float u = momentum_value(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
+        const float u = momentum_value<LF>(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
         const float q0 = u * y;
         const float r = __builtin_fmaf(-q0, m_new, u);
         xs[k] = __builtin_fmaf(r, y, q0);
@@ -1349,7 +1458,7 @@ __device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTable
         const bool nz = m_new > 0.0f;
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
-            const float u = momentum_value(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
+            const float u = momentum_value<LF>(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
             const float x = nz ? div_by_block(u, m_new, y) : 0.0f;
             ix[k] = quant_global(x, a.qt);
         }
@@ -1378,12 +1487,12 @@ __device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTable
 }
 
 // Requantise and apply one chunk, then store its indices and parameters.
-template <int DT, int MODE>
+template <int DT, int MODE, int LF>
 __device__ __forceinline__ void fast_compute(const FastArgs<DT>& a, const FastTables& ft, int64_t e0,
                                              const ChunkIn<DT>& in) {
     uint32_t ix[kChunk];
     float pv[kChunk];
-    fast_math<DT, MODE>(a, ft, in, false, ix, pv);
+    fast_math<DT, MODE, LF>(a, ft, in, false, ix, pv);
     store_idx8(a.idx + e0, ix);
     store8<DT>(a.p + e0, pv);
 }
@@ -1415,7 +1524,7 @@ __device__ __forceinline__ FastArgs<DT> make_fast_args(const TensorWork& w, floa
     return a;
 }
 
-template <int DT, int MODE>
+template <int DT, int MODE, int LF>
 __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, const FastTables& ft,
                                            float row_scale) {
     const FastArgs<DT> a = make_fast_args<DT>(w, row_scale);
@@ -1446,9 +1555,9 @@ __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, cons
         const int64_t eb = ea + kThreads * kChunk;
         const Pos p2 = advance_fast<DT, MODE>(a, p1);
         const Pos p3 = advance_fast<DT, MODE>(a, p2);
-        fast_compute<DT, MODE>(a, ft, ea, A);
+        fast_compute<DT, MODE, LF>(a, ft, ea, A);
         if (i + 2 < n) fast_load<DT, MODE>(a, p2, ea + 2 * kThreads * kChunk, A);
-        if (i + 1 < n) fast_compute<DT, MODE>(a, ft, eb, B);
+        if (i + 1 < n) fast_compute<DT, MODE, LF>(a, ft, eb, B);
         if (i + 3 < n) fast_load<DT, MODE>(a, p3, eb + 2 * kThreads * kChunk, B);
         p0 = p2;
         p1 = p3;
@@ -1463,7 +1572,7 @@ __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, cons
 // p go to LDS, the chunks requantise and apply (indices straight to HBM, new
 // p back into the LDS tile), then p leaves along storage rows.  The next
 // tile's loads are in flight during the current tile's math.
-template <int DT, int MODE>
+template <int DT, int MODE, int LF>
 __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const FastTables& ft,
                                          TvTile<DT>& tg, TvTile<DT>& tp, float row_scale) {
     using TT = TvTile<DT>;
@@ -1547,7 +1656,7 @@ __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const 
             in.rv = cur.rv[h];
             uint32_t ix[kChunk];
             float pv[kChunk];
-            fast_math<DT, MODE>(a, ft, in, general_q, ix, pv);
+            fast_math<DT, MODE, LF>(a, ft, in, general_q, ix, pv);
             store_idx8(a.idx + (r0 + i) * C + c0 + kChunk * jc, ix);
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) tv_put<DT>(tp, i, kChunk * jc + k, pv[k]);
@@ -1580,7 +1689,8 @@ __device__ __forceinline__ void apply_tv_wg(const TensorWork& w, int64_t wg, TvA
         row_scale = (1.0f / stored_mean(w)) * sc.inv_bc2;
     }
     __syncthreads();
-    apply_tv<DT, MODE>(w, wg, lds.f, lds.g, lds.p, row_scale);
+    if (w.mc.small) apply_tv<DT, MODE, kLerpSmall>(w, wg, lds.f, lds.g, lds.p, row_scale);
+    else apply_tv<DT, MODE, kLerpLarge>(w, wg, lds.f, lds.g, lds.p, row_scale);
 }
 
 // LDS of the apply kernels: the fast tables or the general ones, never both.
@@ -1607,7 +1717,8 @@ __device__ __forceinline__ void apply_wg(const TensorWork& w, int64_t wg, int64_
                 row_scale = (1.0f / stored_mean(w)) * sc.inv_bc2;
             }
             __syncthreads();
-            apply_fast<DT, MODE>(w, wg, lds.f, row_scale);
+            if (w.mc.small) apply_fast<DT, MODE, kLerpSmall>(w, wg, lds.f, row_scale);
+            else apply_fast<DT, MODE, kLerpLarge>(w, wg, lds.f, row_scale);
             return;
         }
     }
@@ -1654,9 +1765,18 @@ __device__ __forceinline__ Seg find_seg(const SegTable& tb, int64_t wg) {
     return r;
 }
 
+// One LDS image for both lerp forms (each instantiation would otherwise
+// declare its own).
+template <int DT, bool FAST>
+__device__ __forceinline__ void stats_factored_wg(const TensorWork& w, int64_t wg) {
+    __shared__ FactStatsLds lds;
+    if (w.mc.small) stats_factored<DT, FAST, kLerpSmall>(w, wg, lds);
+    else stats_factored<DT, FAST, kLerpLarge>(w, wg, lds);
+}
+
 template <int DT, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_factored_stats(TensorWork w) {
-    stats_factored<DT, FAST>(w, blockIdx.x);
+    stats_factored_wg<DT, FAST>(w, blockIdx.x);
 }
 
 template <int DT>
@@ -1693,7 +1813,7 @@ template <int DT, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_mt_factored_stats(const TensorWork* __restrict__ ws,
                                                                 SegTable tb) {
     const Seg sg = find_seg(tb, blockIdx.x);
-    stats_factored<DT, FAST>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
+    stats_factored_wg<DT, FAST>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
 }
 
 template <int DT, int MODE>
@@ -1989,7 +2109,8 @@ struct GroupKey {
 };
 
 struct Launch {
-    int phase;       // 0 stats, 1 finalize, 2 apply
+    int phase;       // 0 stats, 1 finalize, 2 apply, 3 mean(v_row)
+    int cohort;      // index of the cohort the launch belongs to
     GroupKey key;
     size_t seg_off;  // index of the first Seg in the segment array
     int nseg;
@@ -2009,14 +2130,30 @@ struct Staging {
 static std::mutex g_stage_mu;
 static std::map<int, Staging> g_stage;  // per device; never freed (process lifetime)
 
+// Cohorts: consecutive parameters whose summed element count stays within
+// the limit.  Each cohort runs stats -> finalize -> mean -> apply; with more
+// than one cohort, the stats of cohort k+1 run on a side stream while cohort
+// k applies.  Default: one cohort per step (on the Llama-3-8B set, 256M-element
+// cohorts overlapped this way measured no faster: both passes already share
+// the same HBM ceiling).  GEFENX_COHORT_ELEMS sets the limit (<= 0: one
+// cohort); GEFENX_PIPELINE=0 keeps every launch on the caller's stream.
 static int64_t cohort_limit() {
     static int64_t v = -1;
     if (v < 0) {
         const char* e = std::getenv("GEFENX_COHORT_ELEMS");
-        v = e ? std::atoll(e) : (int64_t)1 << 62;  // default: one cohort per step
+        v = e ? std::atoll(e) : kDefaultCohortElems;
         if (v <= 0) v = (int64_t)1 << 62;
     }
     return v;
+}
+
+static bool pipeline_enabled() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = std::getenv("GEFENX_PIPELINE");
+        v = (e && std::atoi(e) == 0) ? 0 : 1;
+    }
+    return v == 1;
 }
 
 struct MtLayout {
@@ -2033,7 +2170,7 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
     L.launches.clear();
     const int n = (int)works.size();
     const int64_t limit = cohort_limit();
-    int c0 = 0;
+    int c0 = 0, cohort = 0;
     while (c0 < n) {
         int c1 = c0;
         int64_t acc = 0;
@@ -2053,6 +2190,7 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
             for (auto& kv : groups) {
                 Launch l;
                 l.phase = phase;
+                l.cohort = cohort;
                 l.key = kv.first;
                 l.seg_off = L.segs.size();
                 l.nseg = (int)kv.second.size();
@@ -2085,6 +2223,7 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
             }
         }
         c0 = c1;
+        ++cohort;
     }
 }
 
@@ -2152,13 +2291,13 @@ static int run_multi(const MtLayout& L, void* scratch, size_t scratch_bytes, hip
     return launch_layout(L, static_cast<char*>(scratch), im, s, true);
 }
 
-// Enqueue the phase launches of L reading the descriptor image at dev.
-static int launch_layout(const MtLayout& L, char* dev, const MtImage& im, hipStream_t s, bool prof) {
+// Enqueue one phase launch of a layout whose descriptor image is at dev.
+static int enqueue_launch(const Launch& l, char* dev, const MtImage& im, hipStream_t s, bool prof) {
     const TensorWork* dws = reinterpret_cast<const TensorWork*>(dev + im.works);
     const Seg* dsegs = reinterpret_cast<const Seg*>(dev + im.segs);
     const int32_t* dcoarse = reinterpret_cast<const int32_t*>(dev + im.coarse);
-    for (const Launch& l : L.launches) {
-        if (l.wgs <= 0) continue;
+    {
+        if (l.wgs <= 0) return GEFENX_OK;
         if (l.wgs > 2147483647LL) return set_error(GEFENX_EINVAL, "gefenx_multi_tensor_step: launch too large");
         const dim3 grid((unsigned)l.wgs), block(kThreads);
         const SegTable sg{dsegs + l.seg_off, dcoarse + l.coarse_off, l.nseg, l.gshift};
@@ -2228,6 +2367,80 @@ static int launch_layout(const MtLayout& L, char* dev, const MtImage& im, hipStr
         prof_end(ph, s);
         int rc = launch_check("multi-tensor launch");
         if (rc) return rc;
+    }
+    return GEFENX_OK;
+}
+
+// Side stream and event pool of one device for the cohort pipeline (default
+// priority; created on first use, kept for the process lifetime).
+struct Pipe {
+    hipStream_t side = nullptr;
+    std::vector<hipEvent_t> ev;
+};
+static std::mutex g_pipe_mu;
+static std::map<int, Pipe> g_pipe;
+
+static int pipe_get(size_t n_events, Pipe*& out) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(g_pipe_mu);
+    Pipe& p = g_pipe[dev];
+    if (p.side == nullptr && hipStreamCreateWithFlags(&p.side, hipStreamNonBlocking) != hipSuccess) {
+        p.side = nullptr;
+        return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: side stream creation failed");
+    }
+    while (p.ev.size() < n_events) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+            return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: event creation failed");
+        p.ev.push_back(e);
+    }
+    out = &p;
+    return GEFENX_OK;
+}
+
+// Enqueue the phase launches of L reading the descriptor image at dev.
+// One cohort: everything on s in plan order.  Several: the stats, finalize
+// and mean launches of every cohort go to the device's side stream, which
+// first waits for all work enqueued on s so far; cohort k's applies wait on
+// the event recorded after its mean launch, so the side stream runs the
+// stats of later cohorts while s applies earlier ones.  s ends after the
+// last apply, which follows every side-stream launch, so work enqueued on s
+// afterwards sees the whole step.  Calls that overlap on one device must
+// come from one host thread at a time (the side stream is shared).
+static int launch_layout(const MtLayout& L, char* dev, const MtImage& im, hipStream_t s, bool prof) {
+    const int n_cohorts = L.launches.empty() ? 0 : L.launches.back().cohort + 1;
+    if (n_cohorts <= 1 || !pipeline_enabled()) {
+        for (const Launch& l : L.launches) {
+            int rc = enqueue_launch(l, dev, im, s, prof);
+            if (rc) return rc;
+        }
+        return GEFENX_OK;
+    }
+    Pipe* pp = nullptr;
+    int rc = pipe_get((size_t)n_cohorts + 1, pp);
+    if (rc) return rc;
+    hipStream_t side = pp->side;
+    if (hipEventRecord(pp->ev[0], s) != hipSuccess || hipStreamWaitEvent(side, pp->ev[0], 0) != hipSuccess)
+        return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: stream fork failed");
+    size_t i = 0;
+    const size_t nl = L.launches.size();
+    for (int c = 0; c < n_cohorts; ++c) {
+        size_t j = i;
+        for (; j < nl && L.launches[j].cohort == c; ++j)
+            if (L.launches[j].phase != 2) {
+                rc = enqueue_launch(L.launches[j], dev, im, side, prof);
+                if (rc) return rc;
+            }
+        hipEvent_t ready = pp->ev[(size_t)c + 1];
+        if (hipEventRecord(ready, side) != hipSuccess || hipStreamWaitEvent(s, ready, 0) != hipSuccess)
+            return set_error(GEFENX_ELAUNCH, "gefenx_multi_tensor_step: cohort hand-off failed");
+        for (size_t k = i; k < j; ++k)
+            if (L.launches[k].phase == 2) {
+                rc = enqueue_launch(L.launches[k], dev, im, s, prof);
+                if (rc) return rc;
+            }
+        i = j;
     }
     return GEFENX_OK;
 }

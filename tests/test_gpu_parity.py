@@ -118,6 +118,66 @@ def test_factored_matches_oracle(dev, case):
     _say("case", _run_factored(dev, dtype, rows, cols, period, wd, 3, seed=rows * 7 + cols))
 
 
+NONFINITE_CASES = ["nan", "inf", "huge", "tiny_mag"]
+
+
+@pytest.mark.parametrize("kind", NONFINITE_CASES)
+def test_factored_nonfinite_grads_block_max(dev, kind):
+    """Block magnitudes and indices when grads hold NaN, inf, values whose
+    square overflows fp32 (1e20), or when the old magnitude is huge.  The
+    stats pass takes the |u| max as floats only while every u is provably
+    finite and falls back to the ordered-integer max (NaN above inf, torch's
+    amax) otherwise; both must give the oracle's magnitudes bit for bit."""
+    from gefen.kernels import automatic_gefen_fused as fused
+    rows, cols, period = 64, 1024, 8192  # full column tiles, 8 rows per block
+    gen = torch.Generator().manual_seed(17)
+    cb = _codebook()
+    cb_dev = torch.from_numpy(cb).to(dev)
+    p0 = (torch.randn(rows, cols, generator=gen) * 0.02).to(torch.bfloat16)
+    p_dev = p0.to(dev)
+    nb = rows * cols // period
+    idx = torch.zeros(nb, period, dtype=torch.uint8, device=dev)
+    mag = torch.zeros(nb, 1, dtype=torch.float32, device=dev)
+    vr = torch.zeros(rows, dtype=torch.float32, device=dev)
+    vc = torch.zeros(cols, dtype=torch.float32, device=dev)
+    st = {"p": p0.float().numpy(), "idx": np.zeros(rows * cols, np.uint8), "mag": np.zeros(nb, np.float32),
+          "v_row": np.zeros(rows, np.float32), "v_col": np.zeros(cols, np.float32)}
+    for s in range(1, 4):
+        g = torch.randn(rows, cols, generator=gen) * 1e-3
+        if s >= 2:  # step 1 builds finite state; later steps plant the values
+            if kind == "nan":
+                g[3, 100] = float("nan")      # block 0
+                g[40, 1000] = float("nan")    # block 5
+            elif kind == "inf":
+                g[9, 7] = float("inf")        # block 1
+                g[20, 512] = float("-inf")    # block 2
+            elif kind == "huge":
+                g[12, 300] = 1e20             # g^2 overflows fp32: exact fallback
+                g[50, 900] = -3e19
+        g = g.to(torch.bfloat16)
+        if kind == "tiny_mag" and s == 2:
+            # huge old magnitudes (>= 1e38) must take the exact path
+            m_host = torch.from_numpy(st["mag"]).clone()
+            m_host[3] = 2e38
+            m_host[6] = 3.0e38
+            mag.copy_(m_host.view(nb, 1))
+            st["mag"] = m_host.numpy()
+        bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+        fused.gefen_factored_update_cuda(
+            p_dev, g.to(dev).reshape(-1).view(nb, period), idx, mag, vr, vc, cb_dev, cols,
+            B1, B2, LR, EPS, 1.0 / bc2, 1.0 / bc1, 1.0 - LR * 0.01)
+        p_np, i_np, m_np, r_np, c_np = orc.factored_step(
+            st["p"], g.float().numpy(), st["idx"], st["mag"], st["v_row"], st["v_col"], period,
+            cb, orc.BF16, beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=0.01)
+        torch.cuda.synchronize()
+        tag = "nonfinite %s step %d" % (kind, s)
+        _say(tag)
+        np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), m_np, err_msg=tag + " mag")
+        np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), i_np, err_msg=tag + " idx")
+        st = {"p": p_dev.float().cpu().numpy(), "idx": i_np, "mag": m_np,
+              "v_row": vr.cpu().numpy(), "v_col": vc.cpu().numpy()}
+
+
 @pytest.mark.parametrize("dtype", [orc.BF16, orc.F32])
 def test_factored_transposed_view_matches_oracle(dev, dtype):
     _say("case", _run_factored(dev, dtype, 96, 64, 768, 0.01, 2, seed=5, transposed=True))
