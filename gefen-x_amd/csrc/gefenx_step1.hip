@@ -28,6 +28,11 @@ __device__ __forceinline__ float load_elem(const void* base, int64_t i) {
 // deviation) per block in float64 (k_var_tile).  Every workgroup reduces its blocks'
 // variances in LDS and writes one partial (no shared-address atomics); the
 // partials of a period are summed in a fixed order by k_var_sum.
+// x of one element: fp32(g)^2 widened to float64, or fp32(g) itself when the
+// input already holds squares (the reference's input_is_squared).
+template <bool SQ>
+__device__ __forceinline__ double var_x(float v) { return SQ ? (double)(v * v) : (double)v; }
+
 constexpr int64_t kWavePeriod = 4096;
 constexpr int64_t kThreadPeriod = 64;   // below: a thread per block
 constexpr int64_t kGroupPeriod = 512;   // below: 8 lanes per block; from here a wave per block
@@ -63,7 +68,7 @@ struct VarTile {
     static constexpr int kVecPerThread = (kVecs + kT - 1) / kT;
 };
 
-template <int DT>
+template <int DT, bool SQ = true>
 __global__ void __launch_bounds__(kT) k_var_tile(const void* g, int64_t nb, int64_t P, double* part) {
     using T = typename Elem<DT>::T;
     using VT = VarTile<DT>;
@@ -137,13 +142,13 @@ __global__ void __launch_bounds__(kT) k_var_tile(const void* g, int64_t nb, int6
                 double s = 0.0;
                 for (int j = 0; j < Pi; ++j) {
                     const float v = to_f32<DT>(x[j]);
-                    s += (double)(v * v);
+                    s += var_x<SQ>(v);
                 }
                 const double mean = s / fP;
                 double d2 = 0.0;
                 for (int j = 0; j < Pi; ++j) {
                     const float v = to_f32<DT>(x[j]);
-                    const double d = (double)(v * v) - mean;
+                    const double d = var_x<SQ>(v) - mean;
                     d2 += d * d;
                 }
                 acc += d2 / fP;
@@ -155,13 +160,13 @@ __global__ void __launch_bounds__(kT) k_var_tile(const void* g, int64_t nb, int6
                 double s = 0.0;
                 for (int j = gl; j < Pi; j += 8) {
                     const float v = to_f32<DT>(x[j]);
-                    s += (double)(v * v);
+                    s += var_x<SQ>(v);
                 }
                 const double mean = group8_sum_d(s) / fP;
                 double d2 = 0.0;
                 for (int j = gl; j < Pi; j += 8) {
                     const float v = to_f32<DT>(x[j]);
-                    const double d = (double)(v * v) - mean;
+                    const double d = var_x<SQ>(v) - mean;
                     d2 += d * d;
                 }
                 d2 = group8_sum_d(d2);
@@ -173,13 +178,13 @@ __global__ void __launch_bounds__(kT) k_var_tile(const void* g, int64_t nb, int6
                 double s = 0.0;
                 for (int j = lane; j < Pi; j += 64) {
                     const float v = to_f32<DT>(x[j]);
-                    s += (double)(v * v);
+                    s += var_x<SQ>(v);
                 }
                 const double mean = wave_allsum_d(s) / fP;
                 double d2 = 0.0;
                 for (int j = lane; j < Pi; j += 64) {
                     const float v = to_f32<DT>(x[j]);
-                    const double d = (double)(v * v) - mean;
+                    const double d = var_x<SQ>(v) - mean;
                     d2 += d * d;
                 }
                 d2 = wave_sum_d63(d2);
@@ -207,7 +212,7 @@ __global__ void __launch_bounds__(64) k_var_sum(const double* part, int n, doubl
 // (sum, sum of squares) per segment, combined per block with two atomics.
 // Segments whose start is 16-byte aligned and whose length is a multiple of
 // 8 read 8 elements per load (two loads in flight per thread).
-template <int DT>
+template <int DT, bool SQ = true>
 __global__ void __launch_bounds__(kT) k_var_seg(const void* g, int64_t P, int64_t segs_per_block,
                                                double* s1, double* s2) {
     using T = typename Elem<DT>::T;
@@ -227,8 +232,8 @@ __global__ void __launch_bounds__(kT) k_var_seg(const void* g, int64_t P, int64_
             load8<DT>(gt + lo + (c + kT) * 8, y);
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const double p = (double)(x[k] * x[k]);
-                const double q = (double)(y[k] * y[k]);
+                const double p = var_x<SQ>(x[k]);
+                const double q = var_x<SQ>(y[k]);
                 a1 += p; a2 += p * p;
                 c1 += q; c2 += q * q;
             }
@@ -238,14 +243,14 @@ __global__ void __launch_bounds__(kT) k_var_seg(const void* g, int64_t P, int64_
             load8<DT>(gt + lo + c * 8, x);
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const double p = (double)(x[k] * x[k]);
+                const double p = var_x<SQ>(x[k]);
                 a1 += p; a2 += p * p;
             }
         }
     } else {
         for (int64_t i = lo + threadIdx.x; i < hi; i += kT) {
             const float v = load_elem<DT>(g, i);
-            const double x = (double)(v * v);
+            const double x = var_x<SQ>(v);
             a1 += x;
             a2 += x * x;
         }
@@ -457,6 +462,14 @@ static int check(const char* what) {
         else hipLaunchKernelGGL(KERNEL<BF16>, grid, block, 0, stream, __VA_ARGS__);                 \
     } while (0)
 
+// The same for inputs that already hold squares.
+#define GX_DISPATCH_SQ(dtype, KERNEL, grid, block, stream, ...)                                          \
+    do {                                                                                                  \
+        if ((dtype) == F32) hipLaunchKernelGGL((KERNEL<F32, false>), grid, block, 0, stream, __VA_ARGS__);   \
+        else if ((dtype) == F16) hipLaunchKernelGGL((KERNEL<F16, false>), grid, block, 0, stream, __VA_ARGS__); \
+        else hipLaunchKernelGGL((KERNEL<BF16, false>), grid, block, 0, stream, __VA_ARGS__);                 \
+    } while (0)
+
 static int dtype_ok(int dtype, const char* fn) {
     if (dtype == F64) return set_error(GEFENX_EDTYPE, "%s: not implemented for 'Double'", fn);
     if (dtype != F32 && dtype != F16 && dtype != BF16) return set_error(GEFENX_EINVAL, "%s: bad dtype %d", fn, dtype);
@@ -472,6 +485,11 @@ extern "C" {
 
 int gefenx_block_variance_errors(const void* grad, int dtype, int64_t numel, const int64_t* periods,
                                  int n_periods, double* err_host, void* stream) {
+    return gefenx_block_variance_errors_ex(grad, dtype, numel, periods, n_periods, 0, err_host, stream);
+}
+
+int gefenx_block_variance_errors_ex(const void* grad, int dtype, int64_t numel, const int64_t* periods,
+                                    int n_periods, int input_is_squared, double* err_host, void* stream) {
     int rc = dtype_ok(dtype, "gefenx_block_variance_errors");
     if (rc) return rc;
     if (!grad || !periods || !err_host || numel <= 0 || n_periods < 0)
@@ -505,11 +523,17 @@ int gefenx_block_variance_errors(const void* grad, int dtype, int64_t numel, con
         double* pi = part + (int64_t)i * kVarGrid;
         if (P <= kWavePeriod) {
             const int64_t tiles = (nb + kVarTile / P - 1) / (kVarTile / P);
-            GX_DISPATCH(dtype, k_var_tile, dim3(grid_cap(tiles, 1, kVarGrid)), dim3(kT), s, grad, nb, P, pi);
+            if (input_is_squared)
+                GX_DISPATCH_SQ(dtype, k_var_tile, dim3(grid_cap(tiles, 1, kVarGrid)), dim3(kT), s, grad, nb, P, pi);
+            else
+                GX_DISPATCH(dtype, k_var_tile, dim3(grid_cap(tiles, 1, kVarGrid)), dim3(kT), s, grad, nb, P, pi);
             any_small = true;
         } else {
             const int64_t spb = (P + kSeg - 1) / kSeg;
-            GX_DISPATCH(dtype, k_var_seg, dim3((unsigned)(nb * spb)), dim3(kT), s, grad, P, spb, s1, s2);
+            if (input_is_squared)
+                GX_DISPATCH_SQ(dtype, k_var_seg, dim3((unsigned)(nb * spb)), dim3(kT), s, grad, P, spb, s1, s2);
+            else
+                GX_DISPATCH(dtype, k_var_seg, dim3((unsigned)(nb * spb)), dim3(kT), s, grad, P, spb, s1, s2);
             hipLaunchKernelGGL(k_var_finish, dim3(grid_cap(nb, kT, 4096)), dim3(kT), 0, s, s1, s2, nb, P, totals + i);
         }
         rc = check("block variance");

@@ -6,6 +6,7 @@ state_dict format; the step runs hand-written gfx950 HIP kernels through the C
 ABI in include/gefenx.h.
 """
 from gefen.gefen import Gefen
+from gefen.kernels import period_variance as _period_variance  # noqa: F401 (registers its custom op)
 from gefen.gefen_muon import GefenMuon
 from gefen.hybrid import GefenMuonHybrid
 from gefen.params import DEFAULT_BACKUP_SUBSTRINGS, is_muon_param, split_params_for_muon, validate_split

@@ -95,6 +95,7 @@ SIGNATURES = {
     "gefenx_vmean_update": (_I, [_P, _P, _I, _I64, _I64, _D, _P]),
     "gefenx_exact_histogram": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
     "gefenx_block_variance_errors": (_I, [_P, _I, _I64, _P, _I, _P, _P]),
+    "gefenx_block_variance_errors_ex": (_I, [_P, _I, _I64, _P, _I, _I, _P, _P]),
     "gefenx_exact_dp": (_I, [_P, _P, _I, _I, _I, _P]),
     "gefenx_exact_dp_device": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "gefenx_multi_tensor_step": (_I, [_P, _I, _P, _I, _I64, _P, _SZ, _P]),

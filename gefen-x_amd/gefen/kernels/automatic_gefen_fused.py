@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import warnings
 from typing import Optional
 
 import torch
@@ -222,14 +223,14 @@ def _strides_2d(t: torch.Tensor, rows: int, cols: int):
     raise ValueError("expected a 2D tensor or a contiguous tensor")
 
 
-def gefen_factored_update_cuda(p, grad_view, m_sign, m_magnitude, v_row, v_col, codebook, cols,
-                               beta1, beta2, lr, eps, inv_bias_correction_2,
-                               inv_bias_correction_1, weight_decay_factor,
-                               stochastic_round=False, rng_seed=0, step_scalars=None,
-                               codebook_lut=None, seed_dev=None) -> None:
-    """Factored second-moment fused update of one 2D param (reference :581-650).
-    p may be a strided (e.g. transposed) view: the kernel walks it in logical
-    row-major order, so no contiguous copy is made."""
+def _factored_update_impl(p: torch.Tensor, grad_view: torch.Tensor, m_sign: torch.Tensor,
+                          m_magnitude: torch.Tensor, v_row: torch.Tensor, v_col: torch.Tensor,
+                          codebook: torch.Tensor, cols: int, beta1: float, beta2: float, lr: float,
+                          eps: float, inv_bias_correction_2: float, inv_bias_correction_1: float,
+                          weight_decay_factor: float, stochastic_round: bool = False, rng_seed: int = 0,
+                          step_scalars: Optional[torch.Tensor] = None,
+                          codebook_lut: Optional[torch.Tensor] = None,
+                          seed_dev: Optional[torch.Tensor] = None) -> None:
     _check_common(p, grad_view, m_sign, m_magnitude, codebook)
     cols = int(cols)
     numel = p.numel()
@@ -283,38 +284,41 @@ def _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_ind
         ws.numel(), _stream(p.device)), what)
 
 
-def automatic_gefen_fused_full_update_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook,
-                                           packed_indices, beta1, beta2, lr, eps,
-                                           inv_sqrt_bias_correction_2, inv_bias_correction_1,
-                                           weight_decay_factor, stochastic_round=False,
-                                           rng_seed=0, step_scalars=None, codebook_lut=None,
-                                           seed_dev=None) -> None:
-    """Block-vmean fused update (reference :511-579, v1-full)."""
+def _fused_full_update_impl(p: torch.Tensor, grad_view: torch.Tensor, m_sign: torch.Tensor,
+                            m_magnitude: torch.Tensor, vmean: torch.Tensor, codebook: torch.Tensor,
+                            packed_indices: bool, beta1: float, beta2: float, lr: float, eps: float,
+                            inv_sqrt_bias_correction_2: float, inv_bias_correction_1: float,
+                            weight_decay_factor: float, stochastic_round: bool = False, rng_seed: int = 0,
+                            step_scalars: Optional[torch.Tensor] = None,
+                            codebook_lut: Optional[torch.Tensor] = None,
+                            seed_dev: Optional[torch.Tensor] = None) -> None:
     _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1,
                   beta2, lr, eps, inv_sqrt_bias_correction_2, inv_bias_correction_1,
                   weight_decay_factor, stochastic_round, rng_seed, step_scalars, seed_dev,
                   "automatic_gefen_fused_full_update_cuda")
 
 
-def automatic_gefen_fused_update_v2_full_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook,
-                                              packed_indices, beta1, beta2, lr, eps,
-                                              inv_sqrt_bias_correction_2, inv_bias_correction_1,
-                                              weight_decay_factor, stochastic_round=False,
-                                              rng_seed=0, step_scalars=None, codebook_lut=None,
-                                              seed_dev=None) -> None:
-    """Block-vmean fused update (reference :712-771, v2-full): same kernels."""
+def _fused_update_v2_full_impl(p: torch.Tensor, grad_view: torch.Tensor, m_sign: torch.Tensor,
+                               m_magnitude: torch.Tensor, vmean: torch.Tensor, codebook: torch.Tensor,
+                               packed_indices: bool, beta1: float, beta2: float, lr: float, eps: float,
+                               inv_sqrt_bias_correction_2: float, inv_bias_correction_1: float,
+                               weight_decay_factor: float, stochastic_round: bool = False, rng_seed: int = 0,
+                               step_scalars: Optional[torch.Tensor] = None,
+                               codebook_lut: Optional[torch.Tensor] = None,
+                               seed_dev: Optional[torch.Tensor] = None) -> None:
     _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1,
                   beta2, lr, eps, inv_sqrt_bias_correction_2, inv_bias_correction_1,
                   weight_decay_factor, stochastic_round, rng_seed, step_scalars, seed_dev,
                   "automatic_gefen_fused_update_v2_full_cuda")
 
 
-def gefen_quantized_momentum_update_cuda(grad_view, m_sign, m_magnitude, codebook, momentum_out,
-                                         beta1, stochastic_round=False, rng_seed=0,
-                                         seed_dev=None, codebook_lut=None,
-                                         nesterov=False) -> None:
-    """Muon momentum: advance the quantised EMA and emit the dense momentum
-    (reference :652-710)."""
+def _quantized_momentum_update_impl(grad_view: torch.Tensor, m_sign: torch.Tensor,
+                                    m_magnitude: torch.Tensor, codebook: torch.Tensor,
+                                    momentum_out: torch.Tensor, beta1: float,
+                                    stochastic_round: bool = False, rng_seed: int = 0,
+                                    seed_dev: Optional[torch.Tensor] = None,
+                                    codebook_lut: Optional[torch.Tensor] = None,
+                                    nesterov: bool = False) -> None:
     for name, t in (("m_sign", m_sign), ("m_magnitude", m_magnitude),
                     ("codebook", codebook), ("momentum_out", momentum_out)):
         if t.device != grad_view.device:
@@ -340,3 +344,117 @@ def gefen_quantized_momentum_update_cuda(grad_view, m_sign, m_magnitude, codeboo
         float(beta1), 1 if stochastic_round else 0, int(rng_seed), sd, 1 if nesterov else 0,
         ws.data_ptr(), ws.numel(), _stream(grad_view.device)),
         "gefen_quantized_momentum_update_cuda")
+
+
+# ---------------------------------------------------------------- compile surface
+
+def _compile_op_fake(*args, **kwargs) -> None:
+    """The ops return nothing and only mutate their declared arguments."""
+    return None
+
+
+def _register_compile_ops() -> bool:
+    """torch.library custom ops ``gefen::fused_full_update``,
+    ``gefen::factored_update``, ``gefen::quantized_momentum_update`` and
+    ``gefen::fused_update_v2_full`` (reference kernels/automatic_gefen_fused.py:
+    440-509), each running the C-ABI implementation below, so a traced
+    optimizer step keeps the kernel calls in its graph as opaque mutating ops
+    instead of breaking the graph at every call.  The public wrappers route
+    through them only while tracing and only on the capturable entry (device
+    step scalars and a codebook LUT given); eager calls run the same
+    implementation directly.  These kernels never rebind a state tensor's
+    storage (magnitudes are written in place), so the in-place mutation
+    contract holds on every path.  A registration failure leaves the eager
+    path intact and warns once."""
+    custom_op = getattr(torch.library, "custom_op", None)
+    if custom_op is None:
+        return False
+    try:
+        for name, fn, mutates in (
+                ("fused_full_update", _fused_full_update_impl, ("p", "m_sign", "m_magnitude", "vmean")),
+                ("factored_update", _factored_update_impl, ("p", "m_sign", "m_magnitude", "v_row", "v_col")),
+                ("quantized_momentum_update", _quantized_momentum_update_impl,
+                 ("m_sign", "m_magnitude", "momentum_out")),
+                ("fused_update_v2_full", _fused_update_v2_full_impl, ("p", "m_sign", "m_magnitude", "vmean"))):
+            opdef = custom_op("gefen::" + name, fn, mutates_args=mutates)
+            opdef.register_fake(_compile_op_fake)
+    except Exception as exc:  # noqa: BLE001 -- degrade to the eager path, loudly
+        warnings.warn("gefen: torch.library custom-op registration failed ({}: {}); torch.compile(step) "
+                      "will graph-break at each fused kernel call".format(type(exc).__name__, exc),
+                      RuntimeWarning, stacklevel=2)
+        return False
+    return True
+
+
+_COMPILE_OPS_REGISTERED = _register_compile_ops()
+
+
+def _tracing() -> bool:
+    return _COMPILE_OPS_REGISTERED and torch.compiler.is_compiling()
+
+
+def automatic_gefen_fused_full_update_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook,
+                                           packed_indices, beta1, beta2, lr, eps,
+                                           inv_sqrt_bias_correction_2, inv_bias_correction_1,
+                                           weight_decay_factor, stochastic_round=False,
+                                           rng_seed=0, step_scalars=None, codebook_lut=None,
+                                           seed_dev=None) -> None:
+    """Block-vmean fused update (reference :511-579, v1-full).  step_scalars:
+    fp32 device [lr, 1/sqrt(bc2), 1/bc1, wd factor] read by the kernel
+    (capturable); seed_dev: int64 device seed for stochastic rounding."""
+    args = (p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1, beta2, lr, eps,
+            inv_sqrt_bias_correction_2, inv_bias_correction_1, weight_decay_factor, stochastic_round,
+            rng_seed, step_scalars, codebook_lut, seed_dev)
+    if step_scalars is not None and codebook_lut is not None and _tracing():
+        torch.ops.gefen.fused_full_update(*args)
+        return
+    _fused_full_update_impl(*args)
+
+
+def automatic_gefen_fused_update_v2_full_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook,
+                                              packed_indices, beta1, beta2, lr, eps,
+                                              inv_sqrt_bias_correction_2, inv_bias_correction_1,
+                                              weight_decay_factor, stochastic_round=False,
+                                              rng_seed=0, step_scalars=None, codebook_lut=None,
+                                              seed_dev=None) -> None:
+    """Block-vmean fused update (reference :712-771, v2-full): same kernels."""
+    args = (p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1, beta2, lr, eps,
+            inv_sqrt_bias_correction_2, inv_bias_correction_1, weight_decay_factor, stochastic_round,
+            rng_seed, step_scalars, codebook_lut, seed_dev)
+    if step_scalars is not None and codebook_lut is not None and _tracing():
+        torch.ops.gefen.fused_update_v2_full(*args)
+        return
+    _fused_update_v2_full_impl(*args)
+
+
+def gefen_factored_update_cuda(p, grad_view, m_sign, m_magnitude, v_row, v_col, codebook, cols,
+                               beta1, beta2, lr, eps, inv_bias_correction_2,
+                               inv_bias_correction_1, weight_decay_factor,
+                               stochastic_round=False, rng_seed=0, step_scalars=None,
+                               codebook_lut=None, seed_dev=None) -> None:
+    """Factored second-moment fused update of one 2D param (reference :581-650).
+    p may be a strided (e.g. transposed) view: the kernel walks it in logical
+    row-major order, so no contiguous copy is made.  step_scalars (capturable):
+    fp32 device [lr, 1/bc2, 1/bc1, wd factor]."""
+    args = (p, grad_view, m_sign, m_magnitude, v_row, v_col, codebook, cols, beta1, beta2, lr, eps,
+            inv_bias_correction_2, inv_bias_correction_1, weight_decay_factor, stochastic_round, rng_seed,
+            step_scalars, codebook_lut, seed_dev)
+    if step_scalars is not None and codebook_lut is not None and _tracing():
+        torch.ops.gefen.factored_update(*args)
+        return
+    _factored_update_impl(*args)
+
+
+def gefen_quantized_momentum_update_cuda(grad_view, m_sign, m_magnitude, codebook, momentum_out,
+                                         beta1, stochastic_round=False, rng_seed=0,
+                                         seed_dev=None, codebook_lut=None,
+                                         nesterov=False) -> None:
+    """Muon momentum: advance the quantised EMA and emit the dense momentum
+    (reference :652-710).  Magnitudes are written in place, so the op is
+    traceable on both the capturable and the default path."""
+    args = (grad_view, m_sign, m_magnitude, codebook, momentum_out, beta1, stochastic_round, rng_seed,
+            seed_dev, codebook_lut, nesterov)
+    if codebook_lut is not None and _tracing():
+        torch.ops.gefen.quantized_momentum_update(*args)
+        return
+    _quantized_momentum_update_impl(*args)

@@ -171,6 +171,16 @@ int gefenx_block_variance_errors(const void* grad, int dtype, int64_t numel,
                                  const int64_t* periods, int n_periods,
                                  double* err_host, void* stream);
 
+/* The same with the reference kernel's input_is_squared switch
+ * (kernels/period_variance_kernel.cu:15-80, 82-164; binding
+ * kernels/period_variance_binding.cpp): nonzero takes x = fp32(value) (the
+ * caller already squared), zero squares as above.  Backs
+ * average_within_block_variance_cuda_kernel (kernels/period_variance.py:62-85)
+ * and the gefen::average_within_block_variance_cuda custom op. */
+int gefenx_block_variance_errors_ex(const void* grad, int dtype, int64_t numel,
+                                    const int64_t* periods, int n_periods,
+                                    int input_is_squared, double* err_host, void* stream);
+
 /* Exact optimal 1-D weighted k-means codebook (host, float64 DP with forced
  * +-1 endpoints), from active histogram bins.  Replaces quantization.exact_dp
  * (quantization.py:197-253).  codebook_out receives k sorted fp32 values. */
