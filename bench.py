@@ -95,11 +95,11 @@ def _kernel_source_sha():
     return h.hexdigest()
 
 
-def _measured_traffic():
-    """HBM bytes per launch of the factored apply from the committed rocprofv3
-    PMC passes (FETCH_SIZE x its copy-calibrated scale + WRITE_SIZE x its
-    scale); None when no measurement is committed or it was taken on other
-    kernel sources."""
+def _measured_traffic(key="apply_traffic_bytes_per_launch"):
+    """HBM bytes from the committed rocprofv3 PMC passes (FETCH_SIZE x its
+    copy-calibrated scale + WRITE_SIZE x its scale): per launch of the
+    factored apply by default, or `key` (e.g. the whole step's bytes); None
+    when no measurement is committed or it was taken on other kernel sources."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
@@ -110,7 +110,7 @@ def _measured_traffic():
              os.path.relpath(TRAFFIC_FILE, ROOT))
         return None
     try:
-        return float(t["apply_traffic_bytes_per_launch"])
+        return float(t[key])
     except (KeyError, ValueError, TypeError):
         return None
 
@@ -145,11 +145,20 @@ def write_traffic(fetch, write, copy_fetch, copy_write):
     sf, sw = copy_bytes / (cf * 1024.0), copy_bytes / (cw * 1024.0)
     af, nf = _pmc_avg(fetch, "FETCH_SIZE", APPLY_KERNEL)
     aw, nw = _pmc_avg(write, "WRITE_SIZE", APPLY_KERNEL)
+    # the other launches of the steady-state step (one of each per step)
+    step = af * 1024.0 * sf + aw * 1024.0 * sw
+    others = {}
+    for pat in ("k_mt_factored_stats", "k_mt_finalize", "k_mt_mean", "k_mt_apply<2, 1", "k_mt_block_stats"):
+        f, _ = _pmc_avg(fetch, "FETCH_SIZE", pat)
+        w, _ = _pmc_avg(write, "WRITE_SIZE", pat)
+        others[pat] = f * 1024.0 * sf + w * 1024.0 * sw
+        step += others[pat]
     out = {"kernel": APPLY_KERNEL, "dispatches": [nf, nw],
            "fetch_kib_per_dispatch": af, "write_kib_per_dispatch": aw,
            "copy_fetch_kib": cf, "copy_write_kib": cw, "fetch_scale": sf, "write_scale": sw,
            "apply_read_bytes_per_launch": af * 1024.0 * sf, "apply_write_bytes_per_launch": aw * 1024.0 * sw,
            "apply_traffic_bytes_per_launch": af * 1024.0 * sf + aw * 1024.0 * sw,
+           "other_launch_bytes": others, "step_traffic_bytes": step,
            "kernel_source_sha256": _kernel_source_sha()}
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(out, f, indent=1)
@@ -324,15 +333,19 @@ def bench_qwen(args):
         torch.cuda.synchronize()
         lib.gefenx_profile_reset()
         lib.gefenx_profile_enable(1)
-        host = 0.0
         t0 = time.perf_counter()
         for _ in range(args.steps):
+            opt.step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        lib.gefenx_profile_enable(0)
+        host = 0.0
+        for _ in range(5):  # host cost of one call (enqueue only, GPU idle at entry)
+            torch.cuda.synchronize()
             h0 = time.perf_counter()
             opt.step()
             host += time.perf_counter() - h0
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        lib.gefenx_profile_enable(0)
         launches = sum(_native.profile_read(k)[1] for k in (_native.K_STATS, _native.K_FINALIZE, _native.K_APPLY,
                                                              _native.K_BLOCK_STATS, _native.K_BLOCK_APPLY))
         apply_ms, apply_n, apply_b, _ = _native.profile_read(_native.K_APPLY)
@@ -342,7 +355,7 @@ def bench_qwen(args):
         results["factored" if factored else "block"] = {
             "ms_per_step": ms, "params_per_s": n_params / (elapsed / args.steps),
             "compulsory_GB_per_s": (apply_b + bapply_b) / args.steps / (ms / 1e3) / 1e9,
-            "launches_per_step": launches / args.steps, "host_us_per_step": host * 1e6 / args.steps}
+            "launches_per_step": launches / args.steps, "host_us_per_call": host * 1e6 / 5}
         _log("bench qwen factored=%s: %s" % (factored, results["factored" if factored else "block"]))
         del opt
         torch.cuda.empty_cache()
@@ -498,6 +511,7 @@ def main(argv=None):
     _log("bench: %.3f ms/step, %.1f GB/s compulsory over the whole step" % (
         ms_step, step_bytes / (ms_step / 1e3) / 1e9))
 
+    moved = _measured_traffic("step_traffic_bytes")
     out = {
         "metric": METRIC,
         "value": value,
@@ -516,6 +530,10 @@ def main(argv=None):
                    "weight_decay": 0.01, "parallelism": "single GPU"},
         "step_hbm_gbps": step_bytes / (ms_step / 1e3) / 1e9,
         "step_frac_of_peak": step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBPS,
+        # bytes the whole step moves (PMC: stats re-read of grads + indices,
+        # partials, finalize, applies) over the step time
+        "step_moved_gbps": (moved / (ms_step / 1e3) / 1e9) if moved else None,
+        "step_moved_frac_of_peak": (moved / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBPS) if moved else None,
         "kernel_ms_per_step": {k: v[0] / args.steps for k, v in kinds.items()},
         "first_step_s": t_first,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
