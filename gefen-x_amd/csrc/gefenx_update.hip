@@ -2137,23 +2137,17 @@ static std::map<int, Staging> g_stage;  // per device; never freed (process life
 // cohorts overlapped this way measured no faster: both passes already share
 // the same HBM ceiling).  GEFENX_COHORT_ELEMS sets the limit (<= 0: one
 // cohort); GEFENX_PIPELINE=0 keeps every launch on the caller's stream.
+// Both are read at every plan build (a getenv per step), so a process can
+// change them between steps.
 static int64_t cohort_limit() {
-    static int64_t v = -1;
-    if (v < 0) {
-        const char* e = std::getenv("GEFENX_COHORT_ELEMS");
-        v = e ? std::atoll(e) : kDefaultCohortElems;
-        if (v <= 0) v = (int64_t)1 << 62;
-    }
-    return v;
+    const char* e = std::getenv("GEFENX_COHORT_ELEMS");
+    int64_t v = e ? std::atoll(e) : kDefaultCohortElems;
+    return v > 0 ? v : (int64_t)1 << 62;
 }
 
 static bool pipeline_enabled() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = std::getenv("GEFENX_PIPELINE");
-        v = (e && std::atoi(e) == 0) ? 0 : 1;
-    }
-    return v == 1;
+    const char* e = std::getenv("GEFENX_PIPELINE");
+    return !(e && std::atoi(e) == 0);
 }
 
 struct MtLayout {

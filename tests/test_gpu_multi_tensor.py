@@ -128,3 +128,39 @@ def test_empty_and_gradless_params_are_skipped(dev):
     torch.cuda.synchronize()
     assert torch.equal(n.detach(), before)
     assert "m_codebook" in opt.state[a]
+
+
+@pytest.mark.parametrize("pipeline", ["1", "0"])
+def test_cohorts_match_one_launch_set(dev, monkeypatch, pipeline):
+    """Cohorts (GEFENX_COHORT_ELEMS): several launch sets per step, with the
+    stats of later cohorts on the side stream while earlier cohorts apply
+    (GEFENX_PIPELINE=1) or all on the caller's stream; results equal the
+    single-cohort step bit for bit, and work enqueued on the caller's stream
+    afterwards sees the whole step."""
+    from gefen import Gefen
+    shapes = [(64, 96), (1024, 2048), (4096,), (300, 24), (96, 64, "T"), (512, 512), (999,), (128, 640)]
+    dtypes = [torch.bfloat16, torch.bfloat16, torch.float32, torch.float32, torch.bfloat16, torch.float16,
+              torch.bfloat16, torch.bfloat16]
+    init = _make(shapes, dtypes, dev, 7)
+    pa, pb = _params(init, dev), _params(init, dev)
+    oa = Gefen(pa, lr=1e-3, weight_decay=0.01)
+    ob = Gefen(pb, lr=1e-3, weight_decay=0.01)
+    for s in range(3):
+        _grads(pa, s, 7)
+        _grads(pb, s, 7)
+        monkeypatch.setenv("GEFENX_COHORT_ELEMS", "300000")  # several cohorts
+        monkeypatch.setenv("GEFENX_PIPELINE", pipeline)
+        oa.step()
+        # read back right after the step on the caller's stream (no device sync)
+        snap = [a.detach().clone() for _, a in pa]
+        monkeypatch.delenv("GEFENX_COHORT_ELEMS")
+        monkeypatch.delenv("GEFENX_PIPELINE")
+        ob.step()
+        torch.cuda.synchronize()
+        for (name, a), (_, b), sa_p in zip(pa, pb, snap):
+            tag = "%s %s step %d pipeline %s" % (name, tuple(a.shape), s + 1, pipeline)
+            sa, sb = oa.state[a], ob.state[b]
+            assert torch.equal(sa["m_codebook"], sb["m_codebook"]), tag
+            assert torch.equal(sa["m_magnitude"], sb["m_magnitude"]), tag
+            assert torch.equal(a.detach(), b.detach()), tag
+            assert torch.equal(sa_p, b.detach()), tag
