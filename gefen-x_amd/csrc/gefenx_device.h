@@ -27,6 +27,15 @@ template <class T> __device__ __forceinline__ const GX_GLOBAL T* gbl(const T* p)
     return (const GX_GLOBAL T*)p;
 }
 
+// Wave-uniform read of device memory that no kernel writes while this one
+// runs, through the scalar cache (an s_load: it waits on lgkmcnt, not on the
+// vector-memory counter, and takes no vector-memory issue slot).  p must be
+// the same for every lane.
+template <class T>
+__device__ __forceinline__ T sload(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)p;
+}
+
 // Atomics on device memory through the global address space: they become
 // global_atomic_* instructions, which the compiler's wait-counter tracking
 // orders with the other vector memory operations (a flat atomic makes every

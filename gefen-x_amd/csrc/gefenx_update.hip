@@ -246,7 +246,7 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
                     load_raw8<DT>(g + el, b.graw[u][h]);
                     b.iraw[u][h] = load_raw_idx8(idxp + el);
                 }
-                b.mo[u] = *gbl(mag_old + (pblk < nb ? pblk : nb - 1));
+                b.mo[u] = sload(mag_old + (pblk < nb ? pblk : nb - 1));  // uniform: scalar load
                 ppin += dP4;
                 pblk += dB4;
                 if (ppin >= P) { ppin -= P; ++pblk; }
