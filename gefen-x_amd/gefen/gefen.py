@@ -93,6 +93,101 @@ def _block_view_ok(p: torch.Tensor, grad: torch.Tensor, period: int) -> bool:
     return True
 
 
+# ---------------------------------------------------------------- GradScaler
+
+def _amp_step_controls(optimizer):
+    """gefen.py:614-648: read GradScaler's temporary ``found_inf`` and
+    ``grad_scale`` attributes (scalar tensors or numbers) without touching any
+    gradient. Returns ``(overflow, grad_scale, scale_value)``; a grad_scale
+    that is non-finite or not positive is an error."""
+    found_inf = getattr(optimizer, "found_inf", None)
+    overflow = False
+    if found_inf is not None:
+        if torch.is_tensor(found_inf):
+            if found_inf.numel() != 1:
+                raise RuntimeError("GradScaler supplied a non-scalar found_inf tensor with shape {}".format(
+                    tuple(found_inf.shape)))
+            overflow = bool(found_inf.detach().item())
+        else:
+            overflow = bool(found_inf)
+    grad_scale = getattr(optimizer, "grad_scale", None)
+    scale_value = 0.0
+    if torch.is_tensor(grad_scale):
+        if grad_scale.numel() != 1:
+            raise RuntimeError("GradScaler supplied a non-scalar grad_scale tensor with shape {}".format(
+                tuple(grad_scale.shape)))
+        scale_value = float(grad_scale.detach().item())
+    elif grad_scale is not None:
+        scale_value = float(grad_scale)
+    if grad_scale is not None and (not math.isfinite(scale_value) or scale_value <= 0.0):
+        raise RuntimeError("GradScaler supplied a non-finite or non-positive grad_scale")
+    return overflow, grad_scale, scale_value
+
+
+@torch.no_grad()
+def _amp_prepare_step(optimizer) -> bool:
+    """gefen.py:651-707: the optimizer side of GradScaler's native protocol.
+
+    ``False`` on overflow: the caller returns before any codebook, state,
+    counter or parameter moves. ``grad_scale is None`` means the caller already
+    ran ``scaler.unscale_`` (or this is no AMP step), so gradients are left
+    alone. Otherwise every gradient is multiplied in place by the fp32
+    reciprocal of the scale, taken in fp64 as GradScaler.unscale_ takes it,
+    with one foreach multiply per device; each gradient rounds that product in
+    its own dtype."""
+    overflow, grad_scale, _ = _amp_step_controls(optimizer)
+    if overflow:
+        return False
+    if grad_scale is None:
+        return True
+    if torch.is_tensor(grad_scale):
+        inv_scale = grad_scale.detach().double().reciprocal().float()
+    else:
+        inv_scale = torch.tensor(float(grad_scale), dtype=torch.float64).reciprocal().float()
+    by_device = OrderedDict()
+    for group in optimizer.param_groups:
+        for p in group["params"]:
+            if p.grad is not None:
+                by_device.setdefault(p.grad.device, []).append(p.grad)
+    for device, grads in by_device.items():
+        torch._foreach_mul_(grads, inv_scale.to(device=device, non_blocking=True))
+    return True
+
+
+def _amp_native_scaling_required(optimizer) -> bool:
+    """gefen.py:853-894: take the native protocol only where GradScaler's own
+    unscale cannot run, which is a true fp16 gradient. fp32-master and bf16
+    training keep GradScaler's ordinary path (it skips ``step`` on overflow
+    itself, so schedulers see the skip). An FSDP1 FlatParameter with fp16
+    gradients needs the sharded scaler's cross-rank reduction: native handling
+    is declined for it with a one-time warning."""
+    has_fp16_grad = False
+    has_flat_param = False
+    for group in optimizer.param_groups:
+        for p in group["params"]:
+            if getattr(p, "_is_flat_param", False):
+                has_flat_param = True
+            if p.grad is not None and p.grad.dtype == torch.float16:
+                has_fp16_grad = True
+    if has_fp16_grad and has_flat_param:
+        if not getattr(optimizer, "_gefen_warned_sharded_fp16_amp", False):
+            warnings.warn(
+                "Gefen detected FP16 gradients on an FSDP1 FlatParameter and disabled optimizer-side AMP "
+                "unscaling. Use torch.distributed.fsdp.ShardedGradScaler (or call its unscale_ before step) so "
+                "non-finite detection is reduced across ranks.", RuntimeWarning, stacklevel=3)
+            optimizer._gefen_warned_sharded_fp16_amp = True
+        return False
+    return has_fp16_grad
+
+
+def _amp_gate(optimizer) -> bool:
+    """True when the step should go ahead: no GradScaler controls are attached,
+    or they were attached and the gradients are finite (now unscaled)."""
+    if not (hasattr(optimizer, "found_inf") or hasattr(optimizer, "grad_scale")):
+        return True
+    return _amp_prepare_step(optimizer)
+
+
 class Gefen(torch.optim.Optimizer):
     """Gefen optimizer (see module docstring).
 
@@ -573,6 +668,12 @@ class Gefen(torch.optim.Optimizer):
         kernels read it from the device counter instead."""
         return 0 if self._capt_on else self._gefen_global_step
 
+    @property
+    def _step_supports_amp_scaling(self) -> bool:
+        """gefen.py:1233-1239: GradScaler asks this before its overflow scan;
+        true fp16 gradients take the native protocol handled in ``step``."""
+        return _amp_native_scaling_required(self)
+
     def _assert_capturable_if_capturing(self) -> bool:
         """gefen.py:1614-1641; returns whether the current stream is capturing."""
         capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
@@ -739,6 +840,10 @@ class Gefen(torch.optim.Optimizer):
             with torch.enable_grad():
                 loss = closure()
         self._validate_grads()
+        # gefen.py:5730-5737: a GradScaler overflow returns before the codebook,
+        # the state, the counters or the parameters move.
+        if not _amp_gate(self):
+            return loss
         if capturing:
             self._assert_capture_ready()
         else:

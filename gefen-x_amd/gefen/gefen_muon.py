@@ -34,7 +34,7 @@ import numpy as np
 import torch
 import torch.nn as nn
 
-from gefen.gefen import Gefen, _stream_of
+from gefen.gefen import Gefen, _amp_gate, _stream_of
 from gefen.kernels import _native
 from gefen.kernels import automatic_gefen_fused as _fused
 
@@ -327,6 +327,9 @@ class GefenMuon(Gefen):
             with torch.enable_grad():
                 loss = closure()
         self._validate_grads()
+        # gefen_muon.py:1445-1512 (one process): overflow skips the whole step.
+        if not _amp_gate(self):
+            return loss
         if capturing:
             self._assert_capture_ready()
         else:

@@ -16,7 +16,7 @@ from typing import Iterable
 import torch
 import torch.nn as nn
 
-from gefen.gefen import Gefen
+from gefen.gefen import Gefen, _amp_gate, _amp_native_scaling_required
 from gefen.gefen_muon import GefenMuon
 from gefen.params import DEFAULT_BACKUP_SUBSTRINGS, split_params_for_muon, validate_split
 
@@ -210,6 +210,11 @@ class GefenMuonHybrid(torch.optim.Optimizer):
         raise AttributeError("GefenMuonHybrid.param_groups is the children's groups and cannot be replaced")
 
     @property
+    def _step_supports_amp_scaling(self) -> bool:
+        """hybrid.py:586-595: one protocol for the union of both halves."""
+        return _amp_native_scaling_required(self)
+
+    @property
     def state(self):
         return _StateView(self)
 
@@ -246,6 +251,13 @@ class GefenMuonHybrid(torch.optim.Optimizer):
         for o in self._subopts:
             if hasattr(o, "_validate_grads"):
                 o._validate_grads()
+        # hybrid.py:741-756: GradScaler attaches its controls to the composite;
+        # an overflow in either half skips both, and the automatic unscale
+        # covers every child gradient once (the children see no controls).
+        if not _amp_gate(self):
+            for post_hook in self._optimizer_step_post_hooks.values():
+                post_hook(self, args, kwargs)
+            return loss
         for o in self._subopts:
             if o is not self.muon:
                 o.step()
