@@ -689,6 +689,117 @@ __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
     gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), m0, n0, wm, wn, l32, lhi);
 }
 
+// One 1 KB direct-to-LDS load instruction (number q of this wave's share of
+// a stage) of the same layout as dl_load_stage.
+template <int TILE, int BK>
+__device__ __forceinline__ void dl_load_one(const uint16_t* __restrict__ A, int64_t lda, int64_t M,
+                                            const uint16_t* __restrict__ B, int64_t ldb, int64_t N,
+                                            int64_t m0, int64_t n0, int64_t k0, uint16_t* stage, int q) {
+    constexpr int kCpr = BK / 8;
+    constexpr int kRpi = 64 / kCpr;
+    constexpr int kIpt = TILE / kRpi;
+    constexpr int kIpw = 2 * kIpt / (kT / 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int inst = wave * kIpw + q;
+    const bool is_b = inst >= kIpt;
+    const int ti = is_b ? inst - kIpt : inst;
+    const int row = ti * kRpi + lane / kCpr;
+    const int chunk = dl_slot<BK>(row, lane % kCpr);
+    const uint16_t* base = is_b ? B : A;
+    const int64_t ld = is_b ? ldb : lda;
+    const int64_t lim = is_b ? N : M;
+    int64_t gr = (is_b ? n0 : m0) + row;
+    gr = gr < lim ? gr : lim - 1;
+    const uint16_t* src = base + gr * ld + k0 + chunk * 8;
+    uint16_t* dst = stage + (is_b ? TILE * BK : 0) + ti * kRpi * BK;  // wave-uniform
+    __builtin_amdgcn_global_load_lds((const GX_GLOBAL void*)src, (__attribute__((address_space(3))) void*)dst, 16,
+                                     0, 0);
+}
+
+// 256 x 256 tile for large grids (one workgroup per CU: 128 KB of LDS, 256
+// fp32 accumulators per lane), K steps of 64 in a two-stage LDS ring.  Each
+// wave owns 128 x 128 as 4 x 4 blocks of mfma_f32_32x32x16_bf16: per 16-wide
+// K sub-step, 16 MFMAs against 8 operand fragments, so the LDS reads per MFMA
+// are half those of the 128 x 128 tile.  The instruction order inside a step
+// is fixed with scheduling fences: after each row of 4 MFMAs come that row's
+// operand reads for the next sub-step (fragments double-buffered in
+// registers) and, in the first two sub-steps, two of the next stage's 16
+// direct-to-LDS tile loads, so reads and loads run under the MFMAs instead
+// of ahead of them.  The last step reloads its own K range into the idle
+// buffer (never read) so every step issues the same loads without a branch.
+__global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
+    constexpr int WM = 4, TILE = 256, BK = 64, KS = BK / 16;
+    if (g.tri && blockIdx.x > blockIdx.y) return;  // upper triangle: the mirror of a lower tile
+    constexpr int kStage = 2 * TILE * BK;
+    constexpr int kIpw = 2 * (TILE * BK * 2 / 1024) / (kT / 64);  // 16 load instructions per wave and stage
+    constexpr int kLoadKs = 2;
+    constexpr int kLpr = kIpw / (4 * kLoadKs);
+    static_assert(kLpr * 4 * kLoadKs == kIpw, "the loads spread evenly over the MFMA rows");
+    constexpr int kEpi = 2 * 64 * (TILE + 1);
+    constexpr int kSmem = 2 * kStage > kEpi ? 2 * kStage : kEpi;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
+    const int64_t bz = blockIdx.z;
+    const uint16_t* A = g.A + bz * g.sA;
+    const uint16_t* B = g.B + bz * g.sB;
+    const int64_t m0 = (int64_t)blockIdx.y * TILE;
+    const int64_t n0 = (int64_t)blockIdx.x * TILE;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
+    f32x16 acc[WM][WM];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WM; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const int64_t nk = g.K / BK;
+#pragma unroll
+    for (int q = 0; q < kIpw; ++q) dl_load_one<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, 0, smem, q);
+    auto rd = [&](const uint16_t* t, int half, int idx, int ks) {
+        const int row = half * (32 * WM) + idx * 32 + l32;
+        return *reinterpret_cast<const bf16x8*>(t + row * BK + dl_slot<BK>(row, ks * 2 + lhi) * 8);
+    };
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this step's loads, the only ones in flight
+        __syncthreads();                     // ... landed for every wave; the other buffer is idle
+        const uint16_t* a_s = smem + (kt & 1) * kStage;
+        const uint16_t* b_s = a_s + TILE * BK;
+        uint16_t* nxt = smem + ((kt + 1) & 1) * kStage;
+        const int64_t kn = (kt + 1 < nk ? kt + 1 : kt) * BK;
+        bf16x8 av[2][WM], bv[2][WM];
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            av[0][i] = rd(a_s, wm, i, 0);
+            bv[0][i] = rd(b_s, wn, i, 0);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < WM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks & 1][i], bv[ks & 1][j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (ks + 1 < KS) {
+                    av[(ks + 1) & 1][i] = rd(a_s, wm, i, ks + 1);
+                    bv[(ks + 1) & 1][i] = rd(b_s, wn, i, ks + 1);
+                }
+                if (ks < kLoadKs) {
+#pragma unroll
+                    for (int q = 0; q < kLpr; ++q)
+                        dl_load_one<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, kn, nxt, (ks * 4 + i) * kLpr + q);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the last (discarded) reload lands before the epilogue reuses LDS
+    __syncthreads();
+    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), m0, n0, wm, wn, l32, lhi);
+}
+
 static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
     if (g.M <= 0 || g.N <= 0 || batch <= 0) return GEFENX_OK;
     GemmArgs a = g;
@@ -699,15 +810,23 @@ static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
         return set_error(GEFENX_EINVAL, "newton-schulz gemm: symmetric mode needs a square D mirrored into itself");
     // direct-to-LDS when K is a multiple of 64 and the operands are 16-byte
     // aligned (every Newton-Schulz product of 64-multiple shapes), the
-    // register-staged kernel otherwise; both 128 x 128 tiles (measured on the
-    // Newton-Schulz batches: 256 x 256 tiles, K steps of 32 and 3-stage rings
-    // were no faster)
+    // register-staged kernel otherwise.  Direct-to-LDS products whose 256 x
+    // 256 tiles (lower triangle only when symmetric) fill the 256 CUs at least
+    // once take the 256 x 256 kernel; smaller grids keep 128 x 128 tiles
+    // (four times the workgroups).
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const bool dl = a.vec && g.K % 64 == 0 && al16(g.A) && al16(g.B);
     constexpr int bm = 128, bn = 128;
     if (cdiv(g.M, bm) > 65535 || batch > 65535 || cdiv(g.N, bn) > 2147483647LL)
         return set_error(GEFENX_EINVAL, "newton-schulz gemm: %lld x %lld x batch %lld exceeds the launch grid",
                          (long long)g.M, (long long)g.N, (long long)batch);
+    const int64_t t256m = cdiv(g.M, 256), t256n = cdiv(g.N, 256);
+    const int64_t big_tiles = (g.tri ? t256m * (t256m + 1) / 2 : t256m * t256n) * batch;
+    if (dl && big_tiles >= 256) {
+        const dim3 grid_big((unsigned)t256n, (unsigned)t256m, (unsigned)batch);
+        hipLaunchKernelGGL(k_gemm_big, grid_big, dim3(kT), 0, s, a);
+        return launch_check("newton-schulz gemm");
+    }
     const dim3 grid((unsigned)cdiv(g.N, bn), (unsigned)cdiv(g.M, bm), (unsigned)batch);
     if (dl)
         hipLaunchKernelGGL((k_gemm_dl<2, 64, 2>), grid, dim3(kT), 0, s, a);

@@ -49,11 +49,14 @@ def _bf16_np(t):
     return t.float().cpu().numpy()
 
 
-# K % 64 == 0 with 16-byte aligned operands takes the direct-to-LDS kernel
-# (the last three: full tiles, partial tiles, a single K step); the rest the
-# register-staged one (K = 30 also without 16-byte loads)
+# K % 64 == 0 with 16-byte aligned operands takes a direct-to-LDS kernel:
+# 128 x 128 tiles for (256, 192, 128), (200, 136, 192), (130, 300, 64) (full
+# tiles, partial tiles, a single K step), 256 x 256 tiles once those fill the
+# CUs (the last three: full tiles, partial edge tiles, a single K step); the
+# rest the register-staged one (K = 30 also without 16-byte loads)
 @pytest.mark.parametrize("mnk", [(128, 128, 32), (256, 192, 160), (200, 136, 72), (100, 60, 30), (33, 257, 48),
-                                 (256, 192, 128), (200, 136, 192), (130, 300, 64)])
+                                 (256, 192, 128), (200, 136, 192), (130, 300, 64),
+                                 (4096, 4096, 128), (4000, 4200, 192), (4096, 4096, 64)])
 def test_gemm_nt_matches_float64(dev, lib, mnk):
     M, N, K = mnk
     gen = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
@@ -154,6 +157,20 @@ def test_newton_schulz_batched_matches_oracle(dev, lib, shape):
     m = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
     got = _ns_gpu(dev, lib, m, orc.NS_STANDARD)
     for i in range(shape[0]):
+        o = orc.newton_schulz(m[i])
+        rel = np.linalg.norm(got[i] - o) / np.linalg.norm(o)
+        assert rel <= NS_REL, "batch item %d rel %.3e" % (i, rel)
+        s = np.linalg.svd(got[i].astype(np.float64), compute_uv=False)
+        assert s.max() < 1.3
+
+
+def test_newton_schulz_large_batch_matches_oracle(dev, lib):
+    """28 items of 1024 x 1024: the symmetric products (lower-triangle tiles,
+    mirrored) and the third product all run on the 256 x 256 tile kernel."""
+    rng = np.random.default_rng(1024)
+    m = (rng.standard_normal((28, 1024, 1024)) * 1e-3).astype(np.float32)
+    got = _ns_gpu(dev, lib, m, orc.NS_STANDARD)
+    for i in (0, 13, 27):
         o = orc.newton_schulz(m[i])
         rel = np.linalg.norm(got[i] - o) / np.linalg.norm(o)
         assert rel <= NS_REL, "batch item %d rel %.3e" % (i, rel)
