@@ -39,11 +39,13 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Factored stats tiling: a workgroup covers kFactTileCols columns (64 lanes x
 // two 8-column chunks) of `tile_rows` consecutive rows.  Tiles hold about
-// N/256 elements (so one parameter alone still fills the GPU), between 16K
-// and 256K (so a many-parameter launch writes few float64 partials).
+// N/256 elements (so one large parameter alone still fills the GPU), between
+// 64K (measured on 1024 x 4096 projections: 16K-element tiles spend a third
+// of the pass on per-workgroup set-up and flushes) and 1M (so a
+// many-parameter launch writes few float64 partials).
 constexpr int64_t kFactTileCols = 1024;
-constexpr int64_t kFactTileMinElems = 1 << 14;
-constexpr int64_t kFactTileMaxElems = 1 << 18;
+constexpr int64_t kFactTileMinElems = 1 << 16;
+constexpr int64_t kFactTileMaxElems = 1 << 20;
 
 // Transposed-view stats (strides (1, ld)) use the same column tiles but row
 // tiles of whole 64-row bands, at most kTvStatsMaxRows rows.
