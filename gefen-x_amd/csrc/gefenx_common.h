@@ -115,12 +115,25 @@ struct FactoredWs {
     }
 };
 
+// Block stats record of one workgroup: the sums of squares of its first and
+// last block (key -1: none), which may continue in neighbouring workgroups.
+struct DetRec {
+    int64_t kf;
+    double sf;
+    int64_t kl;
+    double sl;
+};
+
+// Elements per workgroup of the block stats with one element per item (the
+// smallest geometry, so it bounds the record count).
+constexpr int64_t kBlockStatsMinElems = 8 * 256;
+
 struct BlockWs {
     // double blk_sq[shards][nb] (zero between steps), uint32
     // magbits[shards][nb] (zero between steps), float mag_old[nb], float
-    // step[nb], float minv[nb]
-    size_t off_sq, off_magbits, off_magold, off_step, off_minv, total;
-    static BlockWs make(int64_t nb) {
+    // step[nb], float minv[nb], DetRec rec[ceil(numel / kBlockStatsMinElems)]
+    size_t off_sq, off_magbits, off_magold, off_step, off_minv, off_rec, total;
+    static BlockWs make(int64_t nb, int64_t numel) {
         BlockWs w;
         size_t o = 0;
         w.off_sq = o;      o += align256(sizeof(double) * (size_t)(nb * mag_shards(nb)));
@@ -128,6 +141,8 @@ struct BlockWs {
         w.off_magold = o;  o += align256(sizeof(float) * (size_t)nb);
         w.off_step = o;    o += align256(sizeof(float) * (size_t)nb);
         w.off_minv = o;    o += align256(sizeof(float) * (size_t)nb);
+        w.off_rec = o;     o += align256(sizeof(DetRec) * (size_t)((numel + kBlockStatsMinElems - 1) /
+                                                                   kBlockStatsMinElems));
         w.total = o;
         return w;
     }

@@ -193,7 +193,7 @@ size_t gefenx_workspace_bytes(int kind, int64_t rows, int64_t cols, int64_t num_
     if (rows < 0 || cols < 0 || num_blocks < 0) return 0;
     switch (kind) {
         case GEFENX_WS_FACTORED: return FactoredWs::make(rows, cols, num_blocks).total;
-        case GEFENX_WS_BLOCK: return BlockWs::make(num_blocks).total;
+        case GEFENX_WS_BLOCK: return BlockWs::make(num_blocks, rows * cols).total;
         case GEFENX_WS_MOMENTUM: return MomentumWs::make(num_blocks).total;
         default: return 0;
     }

@@ -251,16 +251,25 @@ __global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a) {
     }
 }
 
-template <int DT>
+template <int DT, bool SR>
 __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a) {
     using T = typename Elem<DT>::T;
-    __shared__ uint2 s_fq[kFqEntries];
+    __shared__ uint2 s_fq[SR ? 1 : kFqEntries];
     __shared__ float s_cbr[kCodebookMax];
+    __shared__ float s_cb[SR ? kCodebookMax : 1];
+    __shared__ int16_t s_lut[SR ? kLutEntries + 7 : 1];
     const QTable* qt = a.qt;
-    for (int i = threadIdx.x; i < kFqEntries; i += kT)
-        s_fq[i] = uint2{*gbl(qt->fq + 2 * i), *gbl(qt->fq + 2 * i + 1)};
+    if constexpr (SR) {
+        for (int i = threadIdx.x; i < kLutEntries + 7; i += kT) s_lut[i] = *gbl(qt->lut + i);
+        if (threadIdx.x < kCodebookMax) s_cb[threadIdx.x] = *gbl(qt->cb + threadIdx.x);
+    } else {
+        for (int i = threadIdx.x; i < kFqEntries; i += kT)
+            s_fq[i] = uint2{*gbl(qt->fq + 2 * i), *gbl(qt->fq + 2 * i + 1)};
+    }
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
     __syncthreads();
+    uint64_t seed = a.seed;
+    if (SR && a.seed_dev != nullptr) seed = (uint64_t)*gbl(a.seed_dev);
     const bool fastq = qt->max_cnt <= 1;
     const uint32_t kmax = (uint32_t)(qt->k - 1);
     const T* g = static_cast<const T*>(a.g);
@@ -302,7 +311,9 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a) {
             if (m_new > 0.0f) x = round_dt<DT>(div_by_block(u, den, y));
             else if (m_new != m_new) x = u / m_new;
             uint32_t ni;
-            if (fastq && x >= -1.0f && x <= 1.0f) {
+            if constexpr (SR) {
+                ni = quant_stochastic(x, s_cb, s_lut, qt->k, seed, e0 + k);
+            } else if (fastq && x >= -1.0f && x <= 1.0f) {
                 int b = (int)__builtin_fmaf(x, (float)(kBuckets / 2), (float)(kBuckets / 2));
                 b = b < 0 ? 0 : (b > kFqEntries - 1 ? kFqEntries - 1 : b);
                 const uint2 e = s_fq[b];
@@ -1095,8 +1106,26 @@ int gefenx_quantized_momentum_update(const void* grad, int dtype, int64_t numel,
     }
     GX_MOM(k_mom_max_fast, k_mom_max)
     hipLaunchKernelGGL(k_mom_finalize, dim3(grid_for(nb, 4096)), dim3(kT), 0, s, a);
-    GX_MOM(k_mom_emit_fast, k_mom_emit)
 #undef GX_MOM
+    if (!fast) {
+        switch (dtype) {
+            case F32: hipLaunchKernelGGL(k_mom_emit<F32>, dim3(grid), dim3(kT), 0, s, a); break;
+            case F16: hipLaunchKernelGGL(k_mom_emit<F16>, dim3(grid), dim3(kT), 0, s, a); break;
+            default: hipLaunchKernelGGL(k_mom_emit<BF16>, dim3(grid), dim3(kT), 0, s, a); break;
+        }
+    } else if (a.sr) {
+        switch (dtype) {
+            case F32: hipLaunchKernelGGL((k_mom_emit_fast<F32, true>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
+            case F16: hipLaunchKernelGGL((k_mom_emit_fast<F16, true>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
+            default: hipLaunchKernelGGL((k_mom_emit_fast<BF16, true>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
+        }
+    } else {
+        switch (dtype) {
+            case F32: hipLaunchKernelGGL((k_mom_emit_fast<F32, false>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
+            case F16: hipLaunchKernelGGL((k_mom_emit_fast<F16, false>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
+            default: hipLaunchKernelGGL((k_mom_emit_fast<BF16, false>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
+        }
+    }
     prof_end(ph, s);
     return launch_check("quantized momentum update");
 }

@@ -39,7 +39,6 @@ constexpr int kThreads = 256;
 constexpr int kChunk = 8;
 constexpr int64_t kWaves = kThreads / 64;
 constexpr int64_t kApplyChunksPerThread = 8;   // apply: 4 iterations of 2 chunks
-constexpr int64_t kBlockStatsChunksPerThread = 8;
 constexpr int64_t kFinBlocksPerWg = 1024;
 constexpr int64_t kDefaultCohortElems = 0;  // one cohort per step (see cohort_limit)
 
@@ -67,6 +66,7 @@ struct TensorWork {
     float* minv;
     float* vcs;          // factored: sqrt(v_col), written by finalize
     uint32_t* fin;       // factored: {finalize counter, bits of mean(v_row)}
+    struct DetRec* det_rec;  // block: per-workgroup first / last block partials
     const QTable* qt;
     const float* step_scalars;
     const int64_t* seed_dev;
@@ -75,12 +75,13 @@ struct TensorWork {
     int64_t ps0, ps1, gs0, gs1;
     int64_t ct, rt, tile_rows, shards;
     int64_t stats_wgs, nr, nc, nbw, fin_wgs, apply_wgs;
+    int64_t det_elems;   // block stats: elements per workgroup
     int64_t dR, dC, dB, dP;  // apply: chunk advance for a stride of apply_wgs*256*8 elements
     int64_t fR, fC, fB, fP;  // fast apply: advance for a stride of 256*8 elements
     uint64_t seed;
     int32_t dtype, mode;
     int32_t fast_stats, fast_apply;  // kernel variant: 0 general, 1 contiguous, 2 transposed view
-    int32_t write_p, sr, bf16_mean, pad_;
+    int32_t write_p, sr, bf16_mean, det_epl;  // det_epl: block stats elements per item (8 or 1)
     float eps, beta2, alpha2, pad2_;
     StepScalars sc;
     MomentumCoef mc;
@@ -746,212 +747,159 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
 }
 
 // ====================================================================
-// Block stats: grid-stride over logical chunks of the parameter with nwg
-// workgroups; per-block sum of squares (rounded through bf16 for bf16 grads,
-// gefen.py:180-190) and max |u|.
+// Block stats (block path): per-block sum of squared grads (rounded through
+// bf16 for bf16 grads, gefen.py:180-190) and max |u|, summed in an order that
+// does not depend on scheduling, so a run is bit-reproducible.
+// Workgroup wg owns elements [wg*E, (wg+1)*E), E = kDetIters * 256 * EPL.  In
+// iteration i, lane l of wave v takes the EPL elements of item
+// j = i*256 + v*64 + l, all in one block (EPL = 8 needs P % 8 == 0 and
+// N % 8 == 0; otherwise EPL = 1).  A wave's 64 items are combined per block
+// by a segmented suffix sum (Hillis-Steele steps masked at block starts: a
+// fixed schedule of float64 adds).  A block that starts and ends inside those
+// 64 items is complete and is stored; the first and last block partials of
+// each wave and iteration go to LDS, where wave 0 combines the workgroup's 64
+// of them the same way.  The workgroup's own first and last block partials
+// go to its record; finalize adds a block's stored sum and the records of
+// the workgroups it spans, in workgroup order.  Max |u| takes one atomic max
+// per block and wave (a max is exact in any order).
 // ====================================================================
-template <int DT>
-__device__ __forceinline__ void stats_block(const TensorWork& w, int64_t wg, int64_t nwg) {
-    using T = typename Elem<DT>::T;
-    __shared__ float s_cbr[kCodebookMax];
-    for (int i = threadIdx.x; i < kCodebookMax; i += kThreads) s_cbr[i] = w.qt->cbr[i];
-    __syncthreads();
-    const T* g = static_cast<const T*>(w.grad);
-    const int64_t N = w.N, P = w.P;
-    const double invP = w.invP;
-    const MomentumCoef mc = w.mc;
-    uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
-    double* bsq = w.blk_sq + (wg % w.shards) * w.nb;
-    const int64_t nchunks = (N + kChunk - 1) / kChunk;
-    const int64_t stride = nwg * kThreads;
-    int64_t cur = -1;
-    uint32_t cbits = 0u;
-    double bsum = 0.0;
-    float mo = 0.0f;
-    for (int64_t ch = wg * kThreads + threadIdx.x; ch < nchunks; ch += stride) {
-        const int64_t e0 = ch * kChunk;
-        const int nvalid = (int)std::min<int64_t>(kChunk, N - e0);
-        float gv[kChunk];
-        uint32_t ix[kChunk];
-        if (w.fast_stats && nvalid == kChunk) {
-            load8<DT>(g + e0, gv);
-            load_idx8(w.idx + e0, ix);
-        } else {
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                gv[k] = k < nvalid ? to_f32<DT>(g[e0 + k]) : 0.0f;
-                ix[k] = k < nvalid ? (uint32_t)w.idx[e0 + k] : 0u;
-            }
-        }
-        int64_t blk = div_floor(e0, P, invP);
-        int64_t pin = e0 - blk * P;
-        float csum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-            if (k < nvalid) {
-                if (blk != cur) {
-                    if (cur >= 0) {
-                        bsum += (double)csum;
-                        csum = 0.0f;
-                        if (bsum != 0.0) gatomic_add(bsq + cur, bsum);
-                        if (cbits) gatomic_max(mb + cur, cbits);
-                    }
-                    bsum = 0.0;
-                    cbits = 0u;
-                    cur = blk;
-                    mo = w.mag[blk];
-                }
-                const float u = momentum_value(s_cbr[ix[k]], mo, gv[k], mc);
-                const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                cbits = ub > cbits ? ub : cbits;
-                float sq = gv[k] * gv[k];
-                if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                csum += sq;
-                if (++pin == P) { pin = 0; ++blk; }
-            }
-        }
-        bsum += (double)csum;
-    }
+constexpr int kDetIters = 8;
+static_assert(2 * kDetIters * kWaves == 64, "the workgroup's run partials fill one wave");
+
+// Lane-order run starts (bit l: lane l begins a new key) and the segmented
+// suffix sum / max: each lane ends with the sum (max) of its run from itself
+// to the run's last lane, so a run's first lane holds the run's total.
+__device__ __forceinline__ uint64_t run_heads(int64_t key) {
     const int lane = threadIdx.x & 63;
-    const int64_t c0 = __shfl(cur, 0, 64);
-    if (__all(cur == c0)) {
-        const double s = wave_sum_d(bsum);
-        const uint32_t m = wave_max_u(cbits);
-        if (lane == 0 && c0 >= 0) {
-            if (s != 0.0) gatomic_add(bsq + c0, s);
-            if (m) gatomic_max(mb + c0, m);
-        }
-    } else if (cur >= 0) {
-        if (bsum != 0.0) gatomic_add(bsq + cur, bsum);
-        if (cbits) gatomic_max(mb + cur, cbits);
-    }
+    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)key, 1, 64);
+    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)((uint64_t)key >> 32), 1, 64);
+    const int64_t prev = (int64_t)(((uint64_t)hi << 32) | lo);
+    return (uint64_t)__ballot(lane == 0 || prev != key);
 }
 
-// Block stats, fast path (contiguous 16-byte aligned grad, 8-byte aligned
-// indices, P % 8 == 0 so a chunk never crosses a block): workgroup wg owns
-// chunks [wg * 256 * kBlockStatsChunksPerThread, ...), a wave covers 512
-// consecutive elements per iteration and keeps a running block max and sum
-// while the whole wave stays in one block, flushed with one atomic pair per
-// wave and block.
-__device__ __forceinline__ void bstats_flush(uint32_t* __restrict__ mb, double* __restrict__ bsq, int64_t blk,
-                                             uint32_t bits, double sum) {
-    if (blk < 0) return;
-    const uint32_t r = wave_max_u63(bits);
-    const double t = wave_sum_d63(sum);
-    if ((threadIdx.x & 63) == 63) {
-        if (r) gatomic_max(mb + blk, r);
-        if (t != 0.0) gatomic_add(bsq + blk, t);
+__device__ __forceinline__ double seg_suffix_sum(double v, uint64_t heads) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t after = lane < 63 ? heads >> (lane + 1) : 0ull;  // run starts past this lane
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const double o = __shfl_down(v, d, 64);
+        const bool ok = lane + d < 64 && (after & ((1ull << d) - 1ull)) == 0ull;
+        v = ok ? v + o : v;
     }
+    return v;
 }
 
-template <int DT>
-__device__ __forceinline__ void stats_block_fast(const TensorWork& w, int64_t wg) {
+__device__ __forceinline__ uint32_t seg_suffix_max(uint32_t m, uint64_t heads) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t after = lane < 63 ? heads >> (lane + 1) : 0ull;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_down((int)m, d, 64);
+        const bool ok = lane + d < 64 && (after & ((1ull << d) - 1ull)) == 0ull;
+        m = (ok && o > m) ? o : m;
+    }
+    return m;
+}
+
+template <int DT, int EPL>
+__device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg) {
     using T = typename Elem<DT>::T;
     __shared__ float s_cbr[kCodebookMax];
-    __shared__ int64_t s_wblk[kWaves];
-    __shared__ uint32_t s_wbits[kWaves];
-    __shared__ double s_wsum[kWaves];
+    __shared__ int64_t s_key[2 * kDetIters * kWaves];
+    __shared__ double s_sum[2 * kDetIters * kWaves];
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(w.qt->cbr + threadIdx.x);
     __syncthreads();
     const T* g = static_cast<const T*>(w.grad);
-    const uint8_t* idxp = w.idx;
-    const float* mag = w.mag;
-    double* bsq = w.blk_sq + (wg % w.shards) * w.nb;
-    const int64_t P = w.P;
+    const int64_t N = w.N, P = w.P, nb = w.nb;
     const MomentumCoef mc = w.mc;
-    uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
-    const int64_t nch = w.N / kChunk;
-    const int64_t first = wg * (kThreads * kBlockStatsChunksPerThread) + threadIdx.x;
-    const int64_t F = kThreads * kChunk;
-    const int64_t dB = F / P, dP = F - (F / P) * P;
-    int64_t blk, pin;
-    {
-        const int64_t e0 = first * kChunk;
-        blk = div_floor(e0, P, w.invP);
-        pin = e0 - blk * P;
-    }
-    int64_t wblk = -1;
-    uint32_t wbits = 0u;
-    double wsum = 0.0;
+    uint32_t* mb = w.magbits;
+    double* bsq = w.blk_sq;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t base = wg * (int64_t)(kDetIters * kThreads * EPL);
 #pragma unroll 1
-    for (int i = 0; i < kBlockStatsChunksPerThread; ++i) {
-        const int64_t ch = first + (int64_t)i * kThreads;
-        const bool valid = ch < nch;
-        uint32_t m = 0u;
-        float cs = 0.0f;
-        if (valid) {
-            Raw8<DT> gr;
-            load_raw8<DT>(g + ch * kChunk, gr);
-            const RawIdx8 ir = load_raw_idx8(idxp + ch * kChunk);
-            const float mo = *gbl(mag + blk);
+    for (int i = 0; i < kDetIters; ++i) {
+        const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
+        int64_t key = nb;  // past the end: a sentinel key, never stored
+        double val = 0.0;
+        uint32_t mx = 0u;
+        if (e0 < N) {
+            key = div_floor(e0, P, w.invP);
+            const float mo = *gbl(w.mag + key);
+            float cs = 0.0f;
+            if constexpr (EPL == kChunk) {
+                Raw8<DT> gr;
+                load_raw8<DT>(g + e0, gr);
+                const RawIdx8 ir = load_raw_idx8(w.idx + e0);
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                const float gv = raw_elem<DT>(gr, k);
-                const float u = momentum_value(s_cbr[raw_idx(ir, k)], mo, gv, mc);
-                const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                m = ub > m ? ub : m;
+                for (int k = 0; k < kChunk; ++k) {
+                    const float gv = raw_elem<DT>(gr, k);
+                    const float u = momentum_value(s_cbr[raw_idx(ir, k)], mo, gv, mc);
+                    const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                    mx = ub > mx ? ub : mx;
+                    float sq = gv * gv;
+                    if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                    cs += sq;
+                }
+            } else {
+                const float gv = to_f32<DT>(g[e0]);
+                const float u = momentum_value(s_cbr[w.idx[e0]], mo, gv, mc);
+                mx = __float_as_uint(u) & 0x7fffffffu;
                 float sq = gv * gv;
                 if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                cs += sq;
+                cs = sq;
             }
+            val = (double)cs;
         }
-        const int64_t b0 = __shfl(blk, 0, 64);  // lane 0 holds the wave's lowest chunk
-        if (__all(!valid || blk == b0)) {
-            if (b0 != wblk) {
-                bstats_flush(mb, bsq, wblk, wbits, wsum);
-                wblk = b0;
-                wbits = 0u;
-                wsum = 0.0;
-            }
-            wbits = m > wbits ? m : wbits;
-            wsum += (double)cs;
-        } else {
-            bstats_flush(mb, bsq, wblk, wbits, wsum);
-            wblk = -1;
-            wbits = 0u;
-            wsum = 0.0;
-            if (valid) {
-                if (m) gatomic_max(mb + blk, m);
-                if (cs != 0.0f) gatomic_add(bsq + blk, (double)cs);
-            }
+        const uint64_t heads = run_heads(key);
+        const double sv = seg_suffix_sum(val, heads);
+        const uint32_t sm = seg_suffix_max(mx, heads);
+        const bool start = (heads >> lane) & 1ull;
+        if (start && key < nb && sm != 0u) gatomic_max(mb + key, sm);
+        const int last = 63 - __clzll((long long)heads);
+        if (start && lane != 0 && lane != last && key < nb) bsq[key] = sv;  // complete inside these items
+        const int q = 2 * (i * kWaves + wave);
+        if (lane == 0) {
+            s_key[q] = key;
+            s_sum[q] = sv;
         }
-        pin += dP;
-        blk += dB;
-        if (pin >= P) { pin -= P; ++blk; }
-    }
-    // last run of each wave: one atomic pair per workgroup when the waves agree
-    const uint32_t rb = wblk >= 0 ? wave_max_u63(wbits) : 0u;
-    const double rs = wblk >= 0 ? wave_sum_d63(wsum) : 0.0;
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 63) {
-        s_wblk[wave] = wblk;
-        s_wbits[wave] = rb;
-        s_wsum[wave] = rs;
+        if (lane == last) {  // a single run: the second slot repeats the key with nothing to add
+            s_key[q + 1] = key;
+            s_sum[q + 1] = lane == 0 ? 0.0 : sv;
+        }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        bool same = true;
-        for (int ww = 1; ww < kWaves; ++ww) same = same && (s_wblk[ww] == s_wblk[0]);
-        for (int ww = 0; ww < kWaves; ++ww) {
-            const int64_t b = s_wblk[ww];
-            if (b < 0) continue;
-            uint32_t m = s_wbits[ww];
-            double t = s_wsum[ww];
-            if (same) {
-                if (ww > 0) break;
-                for (int v = 1; v < kWaves; ++v) {
-                    m = s_wbits[v] > m ? s_wbits[v] : m;
-                    t += s_wsum[v];
-                }
+    if (wave == 0) {
+        const int64_t key = s_key[lane];
+        const uint64_t heads = run_heads(key);
+        const double sv = seg_suffix_sum(s_sum[lane], heads);
+        const bool start = (heads >> lane) & 1ull;
+        const int last = 63 - __clzll((long long)heads);
+        if (start && lane != 0 && lane != last && key < nb) bsq[key] = sv;
+        DetRec* rec = w.det_rec + wg;
+        if (lane == 0) {
+            rec->kf = key < nb ? key : -1;
+            rec->sf = sv;
+            if (last == 0) {
+                rec->kl = -1;
+                rec->sl = 0.0;
             }
-            if (m) gatomic_max(mb + b, m);
-            if (t != 0.0) gatomic_add(bsq + b, t);
+        }
+        if (lane == last && last != 0) {
+            rec->kl = key < nb ? key : -1;
+            rec->sl = sv;
         }
     }
 }
 
 __device__ __forceinline__ bool block_stats_fast_ok(const TensorWork& w) {
-    return w.fast_stats && (w.P % kChunk) == 0 && (w.N % kChunk) == 0;
+    return w.det_epl == kChunk;
+}
+
+template <int DT>
+__device__ __forceinline__ void stats_block_wg(const TensorWork& w, int64_t wg) {
+    if (block_stats_fast_ok(w)) stats_block_det<DT, kChunk>(w, wg);
+    else stats_block_det<DT, 1>(w, wg);
 }
 
 // New magnitude (max over the shards), its reciprocal and the old magnitude.
@@ -1030,10 +978,23 @@ __device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) 
     const StepScalars sc = read_scalars(w);
     const float fP = (float)w.P;
     for (int64_t b = wg * kThreads + threadIdx.x; b < w.nb; b += w.nbw * kThreads) {
+        // the fixed-order stats store a block's sum (in shard 0) when the
+        // block is complete inside one workgroup, or leave it in the records
+        // of the workgroups it spans; the transposed-view stats accumulate
+        // into the shards
         double sq = 0.0;
         for (int64_t sh = 0; sh < w.shards; ++sh) {
             sq += w.blk_sq[sh * w.nb + b];
             w.blk_sq[sh * w.nb + b] = 0.0;
+        }
+        if (w.det_rec != nullptr) {
+            const int64_t wlo = (b * w.P) / w.det_elems;
+            const int64_t whi = ((b + 1) * w.P - 1) / w.det_elems;
+            for (int64_t r = wlo; r <= whi; ++r) {
+                const DetRec d = w.det_rec[r];
+                if (d.kf == b) sq += d.sf;
+                if (d.kl == b) sq += d.sl;
+            }
         }
         float mean = (float)sq / fP;
         if (w.bf16_mean) mean = round_dt<BF16>(mean);
@@ -1792,8 +1753,7 @@ __global__ void __launch_bounds__(kThreads) k_apply_tv(TensorWork w) {
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) k_block_stats(TensorWork w) {
-    if (block_stats_fast_ok(w)) stats_block_fast<DT>(w, blockIdx.x);
-    else stats_block<DT>(w, blockIdx.x, gridDim.x);
+    stats_block_wg<DT>(w, blockIdx.x);
 }
 
 __global__ void __launch_bounds__(kThreads) k_finalize(TensorWork w) {
@@ -1833,9 +1793,7 @@ template <int DT>
 __global__ void __launch_bounds__(kThreads) k_mt_block_stats(const TensorWork* __restrict__ ws,
                                                              SegTable tb) {
     const Seg sg = find_seg(tb, blockIdx.x);
-    const TensorWork& w = ws[sg.t];
-    if (block_stats_fast_ok(w)) stats_block_fast<DT>(w, (int64_t)blockIdx.x - sg.wg_begin);
-    else stats_block<DT>(w, (int64_t)blockIdx.x - sg.wg_begin, w.stats_wgs);
+    stats_block_wg<DT>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
 }
 
 __global__ void __launch_bounds__(kThreads) k_mt_finalize(const TensorWork* __restrict__ ws,
@@ -1968,7 +1926,7 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         }
         if (!w.fast_apply && tv_shape && tv_g && tv_p && !in.sr && w.write_p) w.fast_apply = 2;
     } else {
-        const BlockWs L = BlockWs::make(nb);
+        const BlockWs L = BlockWs::make(nb, N);
         if (in.ws_bytes < L.total)
             return set_error(GEFENX_EINVAL, "block update: workspace %zu bytes < required %zu", in.ws_bytes, L.total);
         w.blk_sq = reinterpret_cast<double*>(ws + L.off_sq);
@@ -1976,7 +1934,13 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         w.mag_old = reinterpret_cast<float*>(ws + L.off_magold);
         w.step = reinterpret_cast<float*>(ws + L.off_step);
         w.minv = reinterpret_cast<float*>(ws + L.off_minv);
-        w.stats_wgs = std::max<int64_t>(1, ceil_div(nchunks, kThreads * kBlockStatsChunksPerThread));
+        w.det_rec = reinterpret_cast<DetRec*>(ws + L.off_rec);
+        // fixed-order stats: 8 elements per item when chunks never cross a
+        // block (contiguous, aligned, P and N multiples of 8), else 1
+        w.det_epl = (aligned(in.grad, 16) && aligned(in.idx, 8) && in.period % kChunk == 0 && N % kChunk == 0)
+                        ? (int32_t)kChunk : 1;
+        w.det_elems = (int64_t)kDetIters * kThreads * w.det_epl;
+        w.stats_wgs = std::max<int64_t>(1, ceil_div(N, w.det_elems));
         w.nbw = std::max<int64_t>(1, std::min<int64_t>(4096, ceil_div(nb, kThreads)));
         w.fin_wgs = w.nbw;
         w.fast_stats = aligned(in.grad, 16) && aligned(in.idx, 8);
@@ -1993,6 +1957,7 @@ static int build_work(const WorkInput& in, TensorWork& w) {
                 w.ct = t.ct; w.rt = t.rt_tv; w.tile_rows = t.tv_rows;
                 w.stats_wgs = t.ct * t.rt_tv;
                 w.fast_stats = 2;
+                w.det_rec = nullptr;  // the view tiles accumulate into the shards
             } else if (!g_contig) {
                 return set_error(GEFENX_EINVAL,
                                  "block update: grad strides (%lld, %lld) of [%lld, %lld] are neither contiguous nor "
@@ -2631,7 +2596,7 @@ static int desc_to_work(const gefenx_tensor_desc& d, int i, const void* const* q
     in.step_scalars = step_scalars; in.seed_dev = seed_dev;
     in.workspace = d.workspace;
     in.ws_bytes = d.factored ? gefenx_workspace_bytes(GEFENX_WS_FACTORED, d.rows, d.cols, N / d.period)
-                             : gefenx_workspace_bytes(GEFENX_WS_BLOCK, 0, 0, N / d.period);
+                             : gefenx_workspace_bytes(GEFENX_WS_BLOCK, d.rows, d.cols, N / d.period);
     return build_work(in, w);
 }
 

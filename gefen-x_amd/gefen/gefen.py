@@ -601,7 +601,7 @@ class Gefen(torch.optim.Optimizer):
         nb = p.numel() // period
         p_k = p if p.is_contiguous() else p.contiguous()
         g_k = grad if grad.is_contiguous() else grad.contiguous()
-        ws = self._workspace(state, _native.WS_BLOCK, 0, 0, nb, p.device)
+        ws = self._workspace(state, _native.WS_BLOCK, 1, p.numel(), nb, p.device)
         qt = _fused.quant_table(self._gefen_codebook_on(p.device), p.dtype)
         _native.check(_native.load().gefenx_block_update(
             p_k.data_ptr(), g_k.data_ptr(), _fused._dtype_code(p.dtype), p.numel(), period,
@@ -625,7 +625,7 @@ class Gefen(torch.optim.Optimizer):
             v0, v1 = state["v_row"].data_ptr(), state["v_col"].data_ptr()
             ps0, ps1, gs0, gs1 = p.stride(0), p.stride(1), grad.stride(0), grad.stride(1)
         else:
-            ws = self._workspace(state, _native.WS_BLOCK, 0, 0, nb, p.device)
+            ws = self._workspace(state, _native.WS_BLOCK, 1, p.numel(), nb, p.device)
             v0, v1 = state["vmean"].data_ptr(), 0
             if p.is_contiguous() and grad.is_contiguous():
                 rows, cols = 1, p.numel()
@@ -868,9 +868,12 @@ class Gefen(torch.optim.Optimizer):
                 else:
                     prepared = self._prepare_block(group, name, p, grad)
                 state = prepared[0]
+                # deterministic=True (gefen.py:1048-1057): block-path views
+                # take the contiguous route, whose sums run in a fixed order
+                # (the view tiles accumulate with atomics)
                 batchable = self._multi_tensor and (
                     factored or (p.is_contiguous() and grad.is_contiguous())
-                    or _block_view_ok(p, grad, state["automatic_period"]))
+                    or (not self._deterministic and _block_view_ok(p, grad, state["automatic_period"])))
                 if self._capt_on:
                     self._capt_ready_state(state, p, capturing)
                     rows, dtypes, sptrs, crows = batches.setdefault(p.device, ([], set(), [], []))
@@ -1039,7 +1042,11 @@ class Gefen(torch.optim.Optimizer):
             self._gefen_global_step = int(global_step)
         if self._capt_on:
             self._reset_gefen_global_step_devices()
+        # The codebook is assigned unconditionally (gefen.py:5632-5641): a
+        # checkpoint without one (taken before step 1) clears any stale
+        # codebook, so the next step learns it again instead of skipping step 1.
         if codebook is not None:
             dev = next((p.device for g in self.param_groups for p in g["params"]), torch.device("cpu"))
-            self._gefen_codebook = codebook.to(device=dev, dtype=torch.float32)
-            self._gefen_codebook_by_device.clear()
+            codebook = codebook.to(device=dev, dtype=torch.float32)
+        self._gefen_codebook = codebook
+        self._gefen_codebook_by_device.clear()

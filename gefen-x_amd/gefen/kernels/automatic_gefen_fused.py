@@ -274,7 +274,7 @@ def _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_ind
     grad_c = grad_view if grad_view.is_contiguous() else grad_view.contiguous()
     ss, sd = _scalar_ptrs(step_scalars, seed_dev)
     qt = quant_table(codebook, p.dtype)
-    ws = workspace_for(m_magnitude, _native.WS_BLOCK, 0, 0, m_magnitude.numel())
+    ws = workspace_for(m_magnitude, _native.WS_BLOCK, 1, p.numel(), m_magnitude.numel())
     lib = _native.load()
     _native.check(lib.gefenx_block_update(
         p.data_ptr(), grad_c.data_ptr(), _dtype_code(p.dtype), p.numel(), period,

@@ -134,6 +134,23 @@ static float lerp_f(float self, float end, float w) {
  * idx and mag are updated in place; q (may be NULL) receives the reconstructed
  * momentum.  u_out (may be NULL) receives the pre-quantisation momentum.
  */
+/* Rounding of the requantisation: nearest (the default) or the fused
+ * kernels' stochastic rounding with a seed (kernels/automatic_gefen_fused_kernel.cu:
+ * 160-211, 273-328), keyed by the element's flat index in its tensor.  Set by
+ * orc_set_rounding before a step call; single-threaded use. */
+static int g_sr_on = 0;
+static uint64_t g_sr_seed = 0;
+uint8_t orc_sr_quantize(const float* cb, int k, float x, uint64_t seed, int64_t element_idx);
+
+void orc_set_rounding(int stochastic, uint64_t seed) {
+    g_sr_on = stochastic ? 1 : 0;
+    g_sr_seed = seed;
+}
+
+static uint8_t requantize(const float* cb, int k, float x, int64_t element_idx) {
+    return g_sr_on ? orc_sr_quantize(cb, k, x, g_sr_seed, element_idx) : orc_nearest(cb, k, x);
+}
+
 void orc_momentum_update(const float* g, uint8_t* idx, float* mag, int64_t nb,
                          int64_t period, const float* cb, int k, int dtype,
                          float w, float* q, float* u_out) {
@@ -158,7 +175,7 @@ void orc_momentum_update(const float* g, uint8_t* idx, float* mag, int64_t nb,
         const int nonzero = (m_new > 0.0f);
         for (int64_t j = 0; j < period; ++j) {
             float x = nonzero ? u[j] / m_new : 0.0f;
-            uint8_t ni = orc_nearest(cb, k, x);
+            uint8_t ni = requantize(cb, k, x, base + j);
             idx[base + j] = ni;
             if (q) q[base + j] = orc_round(cb[ni], dtype) * m_new;
         }
@@ -211,7 +228,7 @@ void orc_muon_momentum(const float* g, uint8_t* idx, float* mag, int64_t nb,
         for (int64_t j = 0; j < period; ++j) {
             float x = orc_round(u[j] / den, dtype);
             if (m_new <= 0.0f) x = 0.0f;
-            const uint8_t ni = orc_nearest(cb, k, x);
+            const uint8_t ni = requantize(cb, k, x, base + j);
             idx[base + j] = ni;
             float o = orc_round(orc_round(cb[ni], dtype) * m_new, dtype);
             if (nesterov) o = orc_round(fmaf(alpha_d, g[base + j], orc_round(o * beta_f, dtype)), dtype);

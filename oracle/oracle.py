@@ -72,6 +72,7 @@ def _lib():
     lib.orc_sr_uniform.argtypes = [ctypes.c_uint64, i64]
     lib.orc_sr_quantize.restype = ctypes.c_uint8
     lib.orc_sr_quantize.argtypes = [P, i, f, ctypes.c_uint64, i64]
+    lib.orc_set_rounding.argtypes = [i, ctypes.c_uint64]
     _LIB = lib
     return lib
 
@@ -112,6 +113,24 @@ def search_lut(codebook, buckets: int = 4096) -> np.ndarray:
     return lut
 
 
+class _Rounding:
+    """Requantisation of the step calls inside the block: nearest when
+    `seed` is None, else the fused kernels' stochastic rounding with that
+    seed (kernels/automatic_gefen_fused_kernel.cu:160-211, 273-328; element
+    index = flat index in the tensor)."""
+
+    def __init__(self, seed):
+        self.seed = seed
+
+    def __enter__(self):
+        if self.seed is not None:
+            _lib().orc_set_rounding(1, ctypes.c_uint64(int(self.seed) & (2**64 - 1)))
+
+    def __exit__(self, *exc):
+        if self.seed is not None:
+            _lib().orc_set_rounding(0, ctypes.c_uint64(0))
+
+
 def sr_uniform(seed: int, idx: int) -> float:
     """gefen_sr_uniform: kernels/automatic_gefen_fused_kernel.cu:141-151."""
     return float(_lib().orc_sr_uniform(ctypes.c_uint64(seed & (2**64 - 1)), idx))
@@ -127,10 +146,11 @@ def sr_quantize(codebook, x: float, seed: int, idx: int) -> int:
 # ---------------------------------------------------------------- momentum
 
 
-def momentum_update(g, idx, mag, period, codebook, dtype, beta1):
+def momentum_update(g, idx, mag, period, codebook, dtype, beta1, sr_seed=None):
     """Quantized-momentum recurrence: gefen.py:3438-3486.
 
-    Returns (new_idx, new_mag, q, u) without mutating the inputs.
+    Returns (new_idx, new_mag, q, u) without mutating the inputs.  sr_seed:
+    None (nearest rounding) or the stochastic-rounding seed.
     """
     g = _f32(g).reshape(-1)
     idx = np.ascontiguousarray(np.asarray(idx, dtype=np.uint8).reshape(-1)).copy()
@@ -139,12 +159,13 @@ def momentum_update(g, idx, mag, period, codebook, dtype, beta1):
     cb = _f32(codebook)
     q = np.empty_like(g)
     u = np.empty_like(g)
-    _lib().orc_momentum_update(_ptr(g), _ptr(idx), _ptr(mag), nb, period, _ptr(cb),
-                               cb.size, dtype, np.float32(1.0 - beta1), _ptr(q), _ptr(u))
+    with _Rounding(sr_seed):
+        _lib().orc_momentum_update(_ptr(g), _ptr(idx), _ptr(mag), nb, period, _ptr(cb),
+                                   cb.size, dtype, np.float32(1.0 - beta1), _ptr(q), _ptr(u))
     return idx, mag, q, u
 
 
-def muon_momentum(g, idx, mag, period, codebook, dtype, beta, nesterov=True):
+def muon_momentum(g, idx, mag, period, codebook, dtype, beta, nesterov=True, sr_seed=None):
     """GefenMuon decomposed quantised momentum: gefen_muon.py:1136-1144, 948-974.
 
     Returns (new_idx, new_mag, out) without mutating the inputs; out is the
@@ -156,8 +177,9 @@ def muon_momentum(g, idx, mag, period, codebook, dtype, beta, nesterov=True):
     nb = g.size // period
     cb = _f32(codebook)
     out = np.empty_like(g)
-    _lib().orc_muon_momentum(_ptr(g), _ptr(idx), _ptr(mag), nb, period, _ptr(cb), cb.size, dtype,
-                             float(beta), 1 if nesterov else 0, _ptr(out))
+    with _Rounding(sr_seed):
+        _lib().orc_muon_momentum(_ptr(g), _ptr(idx), _ptr(mag), nb, period, _ptr(cb), cb.size, dtype,
+                                 float(beta), 1 if nesterov else 0, _ptr(out))
     return idx, mag, out
 
 
@@ -243,7 +265,7 @@ def muon_apply(p, update, dtype, lr: float, wd: float, adjusted_lr: float) -> np
 
 
 def factored_step(p, g, idx, mag, v_row, v_col, period, codebook, dtype, *,
-                  beta1, beta2, lr, eps, bc1, bc2, wd):
+                  beta1, beta2, lr, eps, bc1, bc2, wd, sr_seed=None):
     """Decomposed factored step: gefen.py:2959-3018.  Returns new arrays."""
     p = _f32(p).copy()
     rows, cols = p.shape
@@ -253,14 +275,15 @@ def factored_step(p, g, idx, mag, v_row, v_col, period, codebook, dtype, *,
     v_row = _f32(v_row).reshape(-1).copy()
     v_col = _f32(v_col).reshape(-1).copy()
     cb = _f32(codebook)
-    _lib().orc_factored_step(_ptr(p), _ptr(g), _ptr(idx), _ptr(mag), _ptr(v_row),
-                             _ptr(v_col), rows, cols, period, _ptr(cb), cb.size, dtype,
-                             beta1, beta2, lr, eps, bc1, bc2, wd)
+    with _Rounding(sr_seed):
+        _lib().orc_factored_step(_ptr(p), _ptr(g), _ptr(idx), _ptr(mag), _ptr(v_row),
+                                 _ptr(v_col), rows, cols, period, _ptr(cb), cb.size, dtype,
+                                 beta1, beta2, lr, eps, bc1, bc2, wd)
     return p, idx, mag, v_row, v_col
 
 
 def block_step(p, g, idx, mag, vmean, period, codebook, dtype, *,
-               beta1, beta2, lr, eps, bc1, bc2, wd):
+               beta1, beta2, lr, eps, bc1, bc2, wd, sr_seed=None):
     """Non-fused block-vmean step: gefen.py:3776-3818 + 129-191 + 3329-3436."""
     shape = np.shape(p)
     p = _f32(p).reshape(-1).copy()
@@ -269,9 +292,10 @@ def block_step(p, g, idx, mag, vmean, period, codebook, dtype, *,
     mag = _f32(mag).reshape(-1).copy()
     vmean = _f32(vmean).reshape(-1).copy()
     cb = _f32(codebook)
-    _lib().orc_block_step(_ptr(p), _ptr(g), _ptr(idx), _ptr(mag), _ptr(vmean), p.size,
-                          period, _ptr(cb), cb.size, dtype, beta1, beta2, lr, eps,
-                          bc1, bc2, wd)
+    with _Rounding(sr_seed):
+        _lib().orc_block_step(_ptr(p), _ptr(g), _ptr(idx), _ptr(mag), _ptr(vmean), p.size,
+                              period, _ptr(cb), cb.size, dtype, beta1, beta2, lr, eps,
+                              bc1, bc2, wd)
     return p.reshape(shape), idx, mag, vmean
 
 

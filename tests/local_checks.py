@@ -1,0 +1,127 @@
+"""Local oracle checks of one optimizer step on tensors too large for the
+oracle to step whole (test helper, imported by the full-size GPU tests).
+
+What is local in the step (gefen.py:2959-3018, 3329-3486, 3776-3818):
+  - a block's new indices and magnitude depend only on that block's grads,
+    stored indices and old magnitude (oracle.momentum_update, bit-exact);
+  - a row's v_row only on that row's grads and old v_row, a column's v_col
+    only on that column (the EMA v <- fma(mean(g^2), 1-beta2, v*beta2));
+  - an element's new value only on its own p, its block's new index and
+    magnitude, v_row of its row, v_col of its column and mean(v_row).
+`FactoredProbe.capture` copies those inputs before the step and
+`FactoredProbe.verify` checks the GPU's results after it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import oracle as orc
+
+TDT_CODE = {torch.float32: orc.F32, torch.float16: orc.F16, torch.bfloat16: orc.BF16}
+ULP_RTOL = {orc.F32: 1e-6, orc.F16: 2.0 ** -10, orc.BF16: 2.0 ** -8}
+
+
+def _f(t):
+    return t.detach().float().cpu().numpy()
+
+
+def assert_within_ulp(got, ref, dtype, msg, atol=0.0):
+    """Half types: |got - ref| <= 1 ulp of ref in that dtype (exact spacing
+    of the stored value's binade, so 1 ulp means 1 ulp, also at the top of a
+    binade); fp32: 1e-6 relative.  `atol` adds an absolute allowance."""
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    err = np.abs(got - ref)
+    if dtype == orc.F32:
+        lim = 1e-6 * np.abs(ref)
+    else:
+        mant = 7 if dtype == orc.BF16 else 10
+        mag = np.abs(ref)
+        # spacing of the dtype at |ref| (normal numbers; subnormals use the
+        # smallest normal's spacing)
+        emin = -126 if dtype == orc.BF16 else -14
+        e = np.floor(np.log2(np.where(mag > 0, mag, 1.0)))
+        e = np.maximum(e, emin)
+        lim = np.where(mag > 0, 2.0 ** (e - mant), 2.0 ** (emin - mant))
+    bad = err > lim + atol
+    assert not bad.any(), "%s: %d of %d elements beyond 1 ulp (worst err %.3g at ref %.6g)" % (
+        msg, int(bad.sum()), err.size, float(err[bad].max()), float(ref[bad][np.argmax(err[bad])]))
+
+
+class FactoredProbe:
+    """Sampled blocks, rows and columns of one 2D factored parameter."""
+
+    def __init__(self, name, p, period, rows, cols, blocks):
+        self.name, self.p, self.P = name, p, int(period)
+        R, C = p.shape
+        self.R, self.C = R, C
+        self.rows = sorted({int(r) % R for r in rows})
+        self.cols = sorted({int(c) % C for c in cols})
+        nb = p.numel() // self.P
+        self.blocks = sorted({int(b) % nb for b in blocks})
+        self.dtype = TDT_CODE[p.dtype]
+
+    def capture(self, state):
+        p, g, P = self.p, self.p.grad, self.P
+        fresh = state is None or "step" not in state
+        self.p_rows = _f(p[self.rows])
+        self.g_cols = _f(g[:, self.cols]).T.copy()
+        self.g_rows = _f(g[self.rows])
+        self.vr_old = (np.zeros(len(self.rows), np.float32) if fresh
+                       else state["v_row"][self.rows].cpu().numpy())
+        self.vc_old = (np.zeros(len(self.cols), np.float32) if fresh
+                       else state["v_col"][self.cols].cpu().numpy())
+        gf = g.reshape(-1)
+        self.blk_in = []
+        for b in self.blocks:
+            gb = _f(gf[b * P:(b + 1) * P])
+            ib = np.zeros(P, np.uint8) if fresh else state["m_codebook"].reshape(-1)[b * P:(b + 1) * P].cpu().numpy()
+            mb = np.zeros(1, np.float32) if fresh else state["m_magnitude"].reshape(-1)[b:b + 1].cpu().numpy()
+            self.blk_in.append((gb, ib, mb))
+
+    @staticmethod
+    def _ema(sum_sq64, n, v_old, beta2):
+        ms = np.float32(np.float32(sum_sq64) / np.float32(n))
+        return np.float32(np.float64(ms) * np.float64(np.float32(1 - beta2)) +
+                          np.float64(np.float32(np.float32(v_old) * np.float32(beta2))))
+
+    def verify(self, state, codebook, *, step, beta1, beta2, lr, eps, wd, bc2_step=None):
+        P, dt, tag = self.P, self.dtype, "%s step %d" % (self.name, step)
+        idx_all = state["m_codebook"].reshape(-1)
+        mag_all = state["m_magnitude"].reshape(-1)
+        for b, (gb, ib, mb) in zip(self.blocks, self.blk_in):
+            i1, m1, _, _ = orc.momentum_update(gb, ib, mb, P, codebook, dt, beta1)
+            np.testing.assert_array_equal(idx_all[b * P:(b + 1) * P].cpu().numpy(), i1,
+                                          err_msg="%s block %d indices" % (tag, b))
+            np.testing.assert_array_equal(mag_all[b:b + 1].cpu().numpy(), m1,
+                                          err_msg="%s block %d magnitude" % (tag, b))
+        v_row = state["v_row"].cpu().numpy()
+        v_col = state["v_col"].cpu().numpy()
+        for j, r in enumerate(self.rows):
+            ref = self._ema(np.sum(self.g_rows[j].astype(np.float64) ** 2), self.C, self.vr_old[j], beta2)
+            np.testing.assert_allclose(v_row[r], ref, rtol=1e-6, err_msg="%s v_row[%d]" % (tag, r))
+        for j, c in enumerate(self.cols):
+            ref = self._ema(np.sum(self.g_cols[j].astype(np.float64) ** 2), self.R, self.vc_old[j], beta2)
+            np.testing.assert_allclose(v_col[c], ref, rtol=1e-6, err_msg="%s v_col[%d]" % (tag, c))
+        # elements of the sampled rows from the GPU's own v and new state
+        bc1 = 1 - beta1 ** step
+        bc2 = 1 - beta2 ** (step if bc2_step is None else bc2_step)
+        mean = np.float32(np.sum(v_row.astype(np.float64)) / self.R)
+        cbd = orc.round_dtype(np.asarray(codebook, np.float32), dt)
+        for j, r in enumerate(self.rows):
+            flat = np.arange(r * self.C, (r + 1) * self.C)
+            idx_r = idx_all[r * self.C:(r + 1) * self.C].cpu().numpy()
+            ub, inv = np.unique(flat // P, return_inverse=True)
+            mags = mag_all[torch.from_numpy(ub).to(mag_all.device)].cpu().numpy()[inv]
+            q = (cbd[idx_r] * mags.astype(np.float32)).astype(np.float32)
+            vh = (np.float32(v_row[r]) * v_col) / mean
+            h = np.sqrt(vh / np.float32(bc2)) + np.float32(eps)
+            stp = (np.float32(1.0) / h) * np.float32(1.0 / bc1)
+            pw = self.p_rows[j]
+            if wd > 0:
+                pw = orc.round_dtype((pw * np.float32(1 - lr * wd)).astype(np.float32), dt)
+            p_ref = orc.round_dtype((pw - (q * stp) * np.float32(lr)).astype(np.float32), dt)
+            # 1 ulp plus 1e-6 * lr: the stepsize carries the summation-order
+            # skew of v (1e-6 relative), visible where p cancels towards zero
+            assert_within_ulp(_f(self.p[r]), p_ref, dt, "%s row %d p" % (tag, r), atol=1e-6 * lr)

@@ -113,3 +113,20 @@ def test_load_refuses_mismatched_checkpoints():
     bad["gefen_global_step"] = 7
     with pytest.raises(ValueError, match="global steps disagree"):
         opt.load_state_dict(bad)
+
+
+def test_loading_a_codebookless_state_clears_the_codebook():
+    """gefen.py:5632-5641: the codebook is restored unconditionally, so a
+    checkpoint taken before step 1 (no codebook) clears a stale one and the
+    next step learns it again."""
+    sd, ref = _load("fact_bf16")
+    params, opt = _opt("fact_bf16", ref)
+    opt.load_state_dict(copy.deepcopy(sd))
+    assert opt._gefen_codebook is not None
+    _, fresh = _opt("fact_bf16", ref)
+    fresh_sd = fresh.state_dict()
+    assert fresh_sd["gefen_codebook"] is None
+    opt.load_state_dict(fresh_sd)
+    assert opt._gefen_codebook is None
+    assert opt._gefen_codebook_by_device == {}
+    assert opt._gefen_global_step == 0

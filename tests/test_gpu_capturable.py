@@ -429,3 +429,86 @@ def test_hybrid_graph_replay_matches_eager_every_step(dev, backup):
     assert _counter_values(opt.muon) == {float(steps)}
     if backup == "gefen":
         assert _counter_values(opt.backup) == {float(steps)}
+
+
+@pytest.mark.parametrize("factored", [True, False])
+@pytest.mark.parametrize("sr", [False, True])
+def test_graph_replay_matches_oracle(dev, factored, sr):
+    """Captured-and-replayed steps against the oracle directly (not only
+    against eager HIP): 3 eager steps (step 1 learns the period and the
+    codebook), then 4 replays of one captured step with fresh grads copied
+    into the static grad buffers and a device lr schedule.  After every step,
+    each parameter's indices and magnitudes are bit-exact with the oracle's
+    step (stochastic rounding seeded with the global step, as the reference's
+    device seed is), second moments within 1e-6 and parameters within one
+    bf16 ulp.  The oracle continues from the GPU's parameters and second
+    moments each step, so summation-order skew does not accumulate."""
+    from oracle import oracle as orc
+    from local_checks import assert_within_ulp
+    _say("replay vs oracle factored=%s sr=%s" % (factored, sr))
+    specs = [("w2d", (48, 64)), ("norm", (64,)), ("w2d_b", (32, 96))]
+    dtype = torch.bfloat16
+    warmup, replays = 3, 4
+    steps = warmup + replays
+    lr_sched = [1e-3 * 0.9 ** i for i in range(steps)]
+    grads = _grads(11, specs, steps, dtype, dev)
+    params = _make_params(5, specs, dtype, dev)
+    lr = torch.tensor(lr_sched[0], device=dev)
+    opt = _make_opt(params, lr, factored, sr)
+    static = [torch.zeros_like(p) for _, p in params]
+    for (_, p), sg in zip(params, static):
+        p.grad = sg
+    ref = {name: {"p": p.detach().float().cpu().numpy()} for name, p in params}
+    graph = None
+    side = torch.cuda.Stream()
+    for i in range(steps):
+        for sg, g in zip(static, grads[i]):
+            sg.copy_(g)
+        lr.fill_(lr_sched[i])
+        if i < warmup:
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                opt.step()
+            torch.cuda.current_stream().wait_stream(side)
+        else:
+            if graph is None:
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    opt.step()
+            graph.replay()
+        torch.cuda.synchronize()
+        s = i + 1
+        cb = opt._gefen_codebook.cpu().numpy()
+        lr32 = float(np.float32(lr_sched[i]))
+        kw = dict(beta1=BETAS[0], beta2=BETAS[1], lr=lr32, eps=1e-8, bc1=1 - BETAS[0] ** s,
+                  bc2=1 - BETAS[1] ** s, wd=WD, sr_seed=(i if sr else None))
+        for (name, p), g in zip(params, grads[i]):
+            st = opt.state[p]
+            r = ref[name]
+            per = int(st["automatic_period"])
+            gn = g.float().cpu().numpy()
+            if "idx" not in r:
+                r["idx"] = np.zeros(p.numel(), np.uint8)
+                r["mag"] = np.zeros(p.numel() // per, np.float32)
+                r["v_row"] = np.zeros(p.shape[0], np.float32)
+                r["v_col"] = np.zeros(p.shape[-1], np.float32)
+                r["vmean"] = np.zeros(p.numel() // per, np.float32)
+            if factored and p.ndim == 2:
+                pn, r["idx"], r["mag"], vr, vc = orc.factored_step(
+                    r["p"], gn, r["idx"], r["mag"], r["v_row"], r["v_col"], per, cb, orc.BF16, **kw)
+                np.testing.assert_allclose(st["v_row"].cpu().numpy(), vr, rtol=1e-6)
+                np.testing.assert_allclose(st["v_col"].cpu().numpy(), vc, rtol=1e-6)
+                r["v_row"], r["v_col"] = st["v_row"].cpu().numpy(), st["v_col"].cpu().numpy()
+            else:
+                pn, r["idx"], r["mag"], vm = orc.block_step(
+                    r["p"], gn, r["idx"], r["mag"], r["vmean"], per, cb, orc.BF16, **kw)
+                np.testing.assert_allclose(st["vmean"].cpu().numpy().reshape(-1), vm, rtol=1e-6)
+                r["vmean"] = st["vmean"].cpu().numpy().reshape(-1)
+            tag = "%s step %d (%s)" % (name, s, "eager" if i < warmup else "replay")
+            np.testing.assert_array_equal(st["m_codebook"].cpu().numpy().reshape(-1), r["idx"], err_msg=tag)
+            np.testing.assert_array_equal(st["m_magnitude"].cpu().numpy().reshape(-1), r["mag"], err_msg=tag)
+            got = p.detach().float().cpu().numpy()
+            assert_within_ulp(got, pn, orc.BF16, tag + " p", atol=1e-6 * lr32)
+            r["p"] = got
+    assert opt.state_dict()["gefen_global_step"] == steps

@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
+from local_checks import assert_within_ulp
 
 pytestmark = pytest.mark.gpu
 
@@ -88,7 +89,7 @@ def test_large_tensors_three_steps(dev):
             np.testing.assert_array_equal(sb["m_codebook"][bk].cpu().numpy(), i1, err_msg=tag)
             np.testing.assert_array_equal(sb["m_magnitude"][bk].cpu().numpy(), m1, err_msg=tag)
             np.testing.assert_allclose(sb["vmean"][bk].cpu().numpy(), v1, rtol=1e-6, err_msg=tag)
-            np.testing.assert_allclose(_f(b[bk * P1D:(bk + 1) * P1D]), p1, rtol=2.0 ** -7, atol=1e-9, err_msg=tag)
+            assert_within_ulp(_f(b[bk * P1D:(bk + 1) * P1D]), p1, orc.BF16, tag, atol=1e-6 * LR)
         # 2D: per-row momentum (one block per row), v_row / v_col, elements
         for j, r in enumerate(rows):
             i1, m1, q, _ = orc.momentum_update(g_rows[j], idx_rows[j], mag_rows[j:j + 1], P2D, cb_np, orc.BF16,
@@ -117,4 +118,4 @@ def test_large_tensors_three_steps(dev):
             stp = (np.float32(1.0) / h) * np.float32(1.0 / bc1)
             pw = orc.round_dtype((w_rows[j] * np.float32(1 - LR * WD)).astype(np.float32), orc.BF16)
             p_ref = orc.round_dtype((pw - (q * stp) * np.float32(LR)).astype(np.float32), orc.BF16)
-            np.testing.assert_allclose(_f(w[r]), p_ref, rtol=2.0 ** -7, atol=1e-9, err_msg="step %d row %d p" % (step, r))
+            assert_within_ulp(_f(w[r]), p_ref, orc.BF16, "step %d row %d p" % (step, r), atol=1e-6 * LR)

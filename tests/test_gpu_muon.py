@@ -327,3 +327,39 @@ def test_gefen_muon_hybrid_matches_reference_golden(dev):
             p.data.copy_(torch.from_numpy(ref).to(torch.bfloat16).to(dev))
     sd = opt.state_dict()
     assert set(sd) == {"muon", "backup", "backup_optimizer"} and sd["backup_optimizer"] == "gefen"
+
+
+@pytest.mark.parametrize("case", [(orc.BF16, 96 * 40, 96, True), (orc.F32, 3000, 24, False)],
+                         ids=lambda c: "dt%d-n%d-P%d-nest%d" % c)
+def test_muon_momentum_stochastic_rounding_matches_oracle(dev, lib, case):
+    """stochastic_round=1: indices, magnitudes and dense momentum bit-exact
+    against oracle.muon_momentum(sr_seed=...) (SplitMix64 keyed by the flat
+    element index, kernels/automatic_gefen_fused_kernel.cu:924)."""
+    dtype, numel, period, nesterov = case
+    from gefen.kernels import _native
+    from gefen.kernels import automatic_gefen_fused as fused
+    td = TORCH_DT[dtype]
+    rng = np.random.default_rng(numel + 7)
+    cb = np.load(os.path.join(GOLDEN, "learn.npz"))["cb"].astype(np.float32)
+    qt = fused.quant_table(torch.from_numpy(cb).to(dev), td)
+    idx_np, mag_np = _mom_state(numel, period, 2)
+    idx = torch.from_numpy(idx_np.copy()).to(dev)
+    mag = torch.from_numpy(mag_np.copy()).to(dev)
+    ws = torch.zeros(int(lib.gefenx_workspace_bytes(_native.WS_MOMENTUM, 0, 0, numel // period)) + 256,
+                     dtype=torch.uint8, device=dev)
+    for step in range(3):
+        seed = (1 << 33) + 17 * step
+        g = torch.from_numpy((rng.standard_normal(numel) * 1e-3).astype(np.float32)).to(td)
+        out = torch.empty(numel, dtype=td, device=dev)
+        gd = g.to(dev)
+        _check(lib.gefenx_quantized_momentum_update(gd.data_ptr(), fused._dtype_code(td), numel, period,
+                                                    idx.data_ptr(), mag.data_ptr(), qt.data_ptr(), out.data_ptr(),
+                                                    0.95, 1, seed, None, 1 if nesterov else 0, ws.data_ptr(),
+                                                    ws.numel(), _stream(dev)), lib)
+        torch.cuda.synchronize()
+        idx_np, mag_np, out_np = orc.muon_momentum(g.float().numpy(), idx_np, mag_np, period, cb, dtype, 0.95,
+                                                   nesterov, sr_seed=seed)
+        tag = "sr step %d %s" % (step, case)
+        np.testing.assert_array_equal(idx.cpu().numpy(), idx_np, err_msg=tag + " indices")
+        np.testing.assert_array_equal(mag.cpu().numpy(), mag_np, err_msg=tag + " magnitudes")
+        np.testing.assert_array_equal(out.float().cpu().numpy(), out_np, err_msg=tag + " momentum")

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
+from local_checks import assert_within_ulp
 
 pytestmark = pytest.mark.gpu
 
@@ -41,17 +42,15 @@ def _codebook():
 
 
 def _assert_p(got, ref, dtype, msg):
-    """fp32: 1e-6 relative; half types: 1 ulp; plus 1e-6 * lr absolute for
+    """fp32: 1e-6 relative; half types: 1 ulp of the reference value in its
+    dtype (the exact spacing of its binade); plus 1e-6 * lr absolute for
     every dtype -- the update term is ~lr in size and carries the stepsize's
     summation-order skew, which is what remains visible where p itself
     cancels towards zero."""
-    got = np.asarray(got, np.float64).reshape(-1)
-    ref = np.asarray(ref, np.float64).reshape(-1)
-    atol = 1e-6 * LR
-    np.testing.assert_allclose(got, ref, rtol=P_RTOL[dtype], atol=atol, err_msg=msg)
+    assert_within_ulp(got, ref, dtype, msg, atol=1e-6 * LR)
 
 
-def _run_factored(dev, dtype, rows, cols, period, wd, steps, seed, transposed=False):
+def _run_factored(dev, dtype, rows, cols, period, wd, steps, seed, transposed=False, sr_seed=None):
     from gefen.kernels import automatic_gefen_fused as fused
     gen = torch.Generator().manual_seed(seed)
     tdt = TDT[dtype]
@@ -74,15 +73,18 @@ def _run_factored(dev, dtype, rows, cols, period, wd, steps, seed, transposed=Fa
     for s in range(1, steps + 1):
         g = (torch.randn(rows, cols, generator=gen) * 10 ** gen_uniform(gen, -4, -2)).to(tdt)
         bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+        seed_s = None if sr_seed is None else sr_seed + s
         fused.gefen_factored_update_cuda(
             p_dev, g.to(dev).reshape(-1).view(nb, period), idx, mag, vr, vc, cb_dev, cols,
-            B1, B2, LR, EPS, 1.0 / bc2, 1.0 / bc1, 1.0 - LR * wd)
+            B1, B2, LR, EPS, 1.0 / bc2, 1.0 / bc1, 1.0 - LR * wd,
+            stochastic_round=seed_s is not None, rng_seed=seed_s or 0)
         p_np, i_np, m_np, r_np, c_np = orc.factored_step(
             st["p"], g.float().numpy(), st["idx"], st["mag"], st["v_row"], st["v_col"], period,
-            cb, dtype, beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd)
+            cb, dtype, beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd, sr_seed=seed_s)
         torch.cuda.synchronize()
-        tag = "factored %s [%d,%d] P=%d wd=%g step %d%s" % (tdt, rows, cols, period, wd, s,
-                                                            " transposed" if transposed else "")
+        tag = "factored %s [%d,%d] P=%d wd=%g step %d%s%s" % (tdt, rows, cols, period, wd, s,
+                                                              " transposed" if transposed else "",
+                                                              "" if seed_s is None else " sr seed %d" % seed_s)
         np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), i_np, err_msg=tag + " idx")
         np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), m_np, err_msg=tag + " mag")
         np.testing.assert_allclose(vr.cpu().numpy(), r_np, rtol=1e-6, err_msg=tag + " v_row")
@@ -318,7 +320,7 @@ def test_block_view_matches_oracle(dev, case):
         ref = {"p": p.detach().float().cpu().numpy(), "idx": i1, "mag": m1, "vm": st["vmean"].cpu().numpy().reshape(-1)}
 
 
-def _run_block(dev, dtype, n, period, wd, steps, seed):
+def _run_block(dev, dtype, n, period, wd, steps, seed, sr_seed=None):
     from gefen.kernels import automatic_gefen_fused as fused
     gen = torch.Generator().manual_seed(seed)
     tdt = TDT[dtype]
@@ -335,14 +337,17 @@ def _run_block(dev, dtype, n, period, wd, steps, seed):
     for s in range(1, steps + 1):
         g = (torch.randn(n, generator=gen) * 1e-3).to(tdt)
         bc1, bc2 = 1 - B1 ** s, 1 - B2 ** s
+        seed_s = None if sr_seed is None else sr_seed + s
         fused.automatic_gefen_fused_full_update_cuda(
             p_dev, g.to(dev).view(nb, period), idx, mag, vm, cb_dev, False, B1, B2, LR, EPS,
-            1.0 / np.sqrt(bc2), 1.0 / bc1, 1.0 - LR * wd)
+            1.0 / np.sqrt(bc2), 1.0 / bc1, 1.0 - LR * wd,
+            stochastic_round=seed_s is not None, rng_seed=seed_s or 0)
         p_np, i_np, m_np, v_np = orc.block_step(
             st["p"], g.float().numpy(), st["idx"], st["mag"], st["vmean"], period, cb, dtype,
-            beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd)
+            beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=wd, sr_seed=seed_s)
         torch.cuda.synchronize()
-        tag = "block %s n=%d P=%d wd=%g step %d" % (tdt, n, period, wd, s)
+        tag = "block %s n=%d P=%d wd=%g step %d%s" % (tdt, n, period, wd, s,
+                                                     "" if seed_s is None else " sr seed %d" % seed_s)
         np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), i_np, err_msg=tag + " idx")
         np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), m_np, err_msg=tag + " mag")
         np.testing.assert_allclose(vm.cpu().numpy().reshape(-1), v_np, rtol=1e-6, err_msg=tag + " vmean")
@@ -361,6 +366,9 @@ BLOCK_CASES = [
     (orc.F16, 3000, 24, 0.01),
     (orc.BF16, 1 << 20, 1 << 19, 0.01),
     (orc.BF16, 7, 7, 0.01),
+    (orc.BF16, 122880, 24576, 0.01),   # blocks straddle stats workgroups at odd offsets
+    (orc.F32, 122880, 40, 0.01),       # several blocks per wave
+    (orc.F16, 99999, 11111, 0.01),     # P % 8 != 0: one element per item, blocks over ~5 workgroups
 ]
 
 
@@ -368,6 +376,32 @@ BLOCK_CASES = [
 def test_block_matches_oracle(dev, case):
     dtype, n, period, wd = case
     _say("case", _run_block(dev, dtype, n, period, wd, 3, seed=n + period))
+
+
+SR_FACTORED_CASES = [
+    (orc.BF16, 64, 96, 768, False),
+    (orc.F32, 40, 72, 1440, False),
+    (orc.BF16, 30, 50, 3, False),       # generic path
+    (orc.BF16, 96, 64, 768, True),      # transposed view: logical element index
+    (orc.BF16, 1024, 2048, 1 << 20, False),
+]
+
+
+@pytest.mark.parametrize("case", SR_FACTORED_CASES, ids=lambda c: "%s-%dx%d-P%d-T%d" % c)
+def test_factored_stochastic_rounding_matches_oracle(dev, case):
+    """stochastic_round=True: the HIP kernels' SplitMix64 rounding against
+    oracle.factored_step(sr_seed=...) index for index (seed 2^40 + step, so
+    the seed's high bits are exercised)."""
+    dtype, rows, cols, period, transposed = case
+    _say("case", _run_factored(dev, dtype, rows, cols, period, 0.01, 3, seed=rows + cols, transposed=transposed,
+                               sr_seed=(1 << 40)))
+
+
+@pytest.mark.parametrize("case", [(orc.BF16, 4096, 64), (orc.F32, 999, 27), (orc.BF16, 1 << 20, 1 << 19)],
+                         ids=lambda c: "%s-n%d-P%d" % c)
+def test_block_stochastic_rounding_matches_oracle(dev, case):
+    dtype, n, period = case
+    _say("case", _run_block(dev, dtype, n, period, 0.01, 3, seed=n, sr_seed=12345))
 
 
 GOLDEN_CASES = ["fact_f32", "fact_bf16", "fact_f16", "block_bf16", "block_f32", "block_f16",

@@ -148,3 +148,83 @@ def test_free_running_indices_match_reference(name):
         for s in range(1, int(z["steps"]) + 1):
             st = _oracle_step(z, name, pn, s, st, dtype)
             np.testing.assert_array_equal(st["idx"], z["idx%d_%s" % (s, pn)])
+
+
+# ------------------------------------------------------------------ config 1
+
+def config1_inputs(step=None):
+    """BASELINE config 1 inputs, the seed protocol tests/golden/make_golden.py
+    used: W 4096x4096 and b 4096 fp32 ~ N(0, 0.02) from seed 0; the step-t
+    grads ~ N(0, 1e-3) from seed 1000 + t (W's first, then b's)."""
+    import torch
+    gen = torch.Generator().manual_seed(0)
+    w = torch.randn(4096, 4096, generator=gen) * 0.02
+    b = torch.randn(4096, generator=gen) * 0.02
+    if step is None:
+        return w.numpy(), b.numpy()
+    gt = torch.Generator().manual_seed(1000 + step)
+    return ((torch.randn(4096, 4096, generator=gt) * 1e-3).numpy(),
+            (torch.randn(4096, generator=gt) * 1e-3).numpy())
+
+
+C1_SUB = 4099  # subsample stride of the golden weight snapshots
+C1_WD = 0.01
+
+
+def _sha(a):
+    import hashlib
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def _assert_p_close(got, ref, p0, what):
+    scale = np.maximum(np.abs(p0), np.abs(ref)).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    bad = err > 1e-6 * scale
+    assert not bad.any(), "%s: %d elements beyond 1e-6 of max(|p0|,|p|), worst %.3g" % (
+        what, int(bad.sum()), float((err / np.maximum(scale, 1e-38)).max()))
+
+
+def test_config1_trajectory_matches_reference():
+    """the reference's CPU step (fused=False, factored)
+    on a 4096x4096 fp32 weight plus a 4096 bias for 10 steps.  Step 1 learns
+    the period of each tensor and the codebook from the step-1 grads; the
+    oracle free-runs the whole trajectory.  Per step: the sha256 of the full
+    4096x4096 index array and the magnitudes bit-exact, v_row / v_col / vmean
+    within 1e-6 relative (torch's CPU reductions sum in another order), the
+    weight subsample and the bias within 1e-6 of max(|p0|, |p|) per element:
+    a last-bit difference in a stepsize flips one rounding of p, and that
+    ulp (taken while |p| was near |p0|) is carried along even where p later
+    shrinks.  Measured: at most 2 ulps of that scale after 10 steps."""
+    z = _load("config1.npz")
+    w, b = config1_inputs()
+    w0_sub, b0 = w.reshape(-1)[::C1_SUB].copy(), b.copy()
+    gw, gb = config1_inputs(1)
+    pw = orc.resolve_period(gw, gw.shape)
+    pb = orc.resolve_period(gb, gb.shape)
+    assert (pw, pb) == (int(z["period_weight"]), int(z["period_bias"]))
+    cb = orc.learn_codebook([(gw, pw), (gb, pb)])
+    np.testing.assert_array_equal(cb, z["codebook"])
+    sw = {"idx": np.zeros(w.size, np.uint8), "mag": np.zeros(w.size // pw, np.float32),
+          "v_row": np.zeros(4096, np.float32), "v_col": np.zeros(4096, np.float32)}
+    sb = {"idx": np.zeros(b.size, np.uint8), "mag": np.zeros(b.size // pb, np.float32),
+          "vmean": np.zeros(b.size // pb, np.float32)}
+    for s in range(1, 11):
+        if s > 1:
+            gw, gb = config1_inputs(s)
+        bc1, bc2 = 1 - BETA1 ** s, 1 - BETA2 ** s
+        w, sw["idx"], sw["mag"], sw["v_row"], sw["v_col"] = orc.factored_step(
+            w, gw, sw["idx"], sw["mag"], sw["v_row"], sw["v_col"], pw, cb, orc.F32,
+            beta1=BETA1, beta2=BETA2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=C1_WD)
+        b, sb["idx"], sb["mag"], sb["vmean"] = orc.block_step(
+            b, gb, sb["idx"], sb["mag"], sb["vmean"], pb, cb, orc.F32,
+            beta1=BETA1, beta2=BETA2, lr=LR, eps=EPS, bc1=bc1, bc2=bc2, wd=C1_WD)
+        assert _sha(sw["idx"]) == str(z["sha_idx%d_weight" % s]), "weight indices, step %d" % s
+        np.testing.assert_array_equal(sw["idx"][::C1_SUB], z["idx_sub%d_weight" % s])
+        np.testing.assert_array_equal(sw["mag"], z["mag%d_weight" % s])
+        np.testing.assert_allclose(sw["v_row"], z["v_row%d_weight" % s], rtol=1e-6, atol=0)
+        np.testing.assert_allclose(sw["v_col"], z["v_col%d_weight" % s], rtol=1e-6, atol=0)
+        _assert_p_close(w.reshape(-1)[::C1_SUB], z["p_sub%d_weight" % s], w0_sub, "weight step %d" % s)
+        np.testing.assert_array_equal(sb["idx"], z["idx%d_bias" % s])
+        np.testing.assert_array_equal(sb["mag"], z["mag%d_bias" % s])
+        np.testing.assert_allclose(sb["vmean"], z["vmean%d_bias" % s], rtol=1e-6, atol=0)
+        _assert_p_close(b, z["p%d_bias" % s], b0, "bias step %d" % s)
