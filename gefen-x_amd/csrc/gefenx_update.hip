@@ -2494,7 +2494,79 @@ static int check_dtype(int dtype, const char* fn) {
     return GEFENX_OK;
 }
 
+// ------------------------------------------------------------ static scratch
+// Device scratch of gefenx_factored_update_noalloc: a file-scope array, one
+// copy per GPU the library runs on, held until the process ends.  In host
+// code the array's name is not a device address: scratch_on_device() resolves
+// it once per device (hipGetSymbolAddress with that device current) and every
+// host use -- kernel arguments, the clearing launch -- goes through the
+// resolved pointer.
+static __device__ __align__(256) unsigned char scratch[GEFENX_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kScratchDevices = 64;
+static void* g_scratch_addr[kScratchDevices];  // per device; nullptr until resolved
+static std::mutex g_scratch_mu;
+
+static int scratch_on_device(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+        return set_error(GEFENX_ELAUNCH, "gefenx_factored_update_noalloc: no usable current device");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_addr[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+            return set_error(GEFENX_ELAUNCH, "gefenx_factored_update_noalloc: hipGetSymbolAddress of the scratch "
+                             "array failed on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_addr[dev] = ptr;
+    }
+    *out = g_scratch_addr[dev];
+    return GEFENX_OK;
+}
+
+// Zero n 32-bit words (a kernel, not a memset node, so a captured graph
+// replays it like any other launch).
+__global__ __launch_bounds__(kThreads) void k_zero_words(uint32_t* __restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+        p[i] = 0u;
+}
+
 extern "C" {
+
+// Validation and work description shared by the factored entry points.
+static int factored_input(const char* fn, void* p, const void* grad, int dtype, int64_t rows, int64_t cols,
+                          int64_t ps0, int64_t ps1, int64_t gs0, int64_t gs1, uint8_t* m_codebook,
+                          float* m_magnitude, float* v_row, float* v_col, int64_t period, const void* qtable_dev,
+                          double beta1, double beta2, double lr, double eps, double inv_bias_correction_2,
+                          double inv_bias_correction_1, double weight_decay_factor, int stochastic_round,
+                          int64_t rng_seed, const float* step_scalars, const int64_t* seed_dev, WorkInput& in,
+                          bool& empty) {
+    empty = false;
+    int rc = check_dtype(dtype, fn);
+    if (rc) return rc;
+    if (rows < 0 || cols < 0) return set_error(GEFENX_EINVAL, "%s: negative shape", fn);
+    const int64_t N = rows * cols;
+    if (N == 0) {  // empty tensors are a no-op
+        empty = true;
+        return GEFENX_OK;
+    }
+    if (period <= 0 || N % period != 0)
+        return set_error(GEFENX_EINVAL, "%s: period %lld does not divide numel %lld", fn, (long long)period,
+                         (long long)N);
+    if (!p || !grad || !m_codebook || !m_magnitude || !v_row || !v_col || !qtable_dev)
+        return set_error(GEFENX_EINVAL, "%s: null pointer argument", fn);
+    in = WorkInput{};
+    in.p = p; in.grad = grad; in.dtype = dtype; in.mode = 0;
+    in.R = rows; in.C = cols; in.ps0 = ps0; in.ps1 = ps1; in.gs0 = gs0; in.gs1 = gs1; in.period = period;
+    in.idx = m_codebook; in.mag = m_magnitude; in.v0 = v_row; in.v1 = v_col; in.qt = qtable_dev;
+    in.lerp_w = (float)(1.0 - beta1); in.beta2 = (float)beta2; in.alpha2 = (float)(1.0 - beta2);
+    in.eps = (float)eps;
+    in.sc = StepScalars{(float)lr, (float)inv_bias_correction_2, (float)inv_bias_correction_1,
+                        (float)weight_decay_factor};
+    in.sr = stochastic_round ? 1 : 0; in.seed = (uint64_t)rng_seed;
+    in.step_scalars = step_scalars; in.seed_dev = seed_dev;
+    return GEFENX_OK;
+}
 
 int gefenx_factored_update(
     void* p, const void* grad, int dtype, int64_t rows, int64_t cols,
@@ -2506,31 +2578,65 @@ int gefenx_factored_update(
     double weight_decay_factor, int stochastic_round, int64_t rng_seed,
     const float* step_scalars, const int64_t* seed_dev,
     void* workspace, size_t workspace_bytes, void* stream) {
-    int rc = check_dtype(dtype, "gefenx_factored_update");
-    if (rc) return rc;
-    if (rows < 0 || cols < 0) return set_error(GEFENX_EINVAL, "gefenx_factored_update: negative shape");
-    const int64_t N = rows * cols;
-    if (N == 0) return GEFENX_OK;  // empty tensors are a no-op
-    if (period <= 0 || N % period != 0)
-        return set_error(GEFENX_EINVAL, "gefenx_factored_update: period %lld does not divide numel %lld",
-                         (long long)period, (long long)N);
-    if (!p || !grad || !m_codebook || !m_magnitude || !v_row || !v_col || !qtable_dev || !workspace)
-        return set_error(GEFENX_EINVAL, "gefenx_factored_update: null pointer argument");
-    WorkInput in{};
-    in.p = p; in.grad = grad; in.dtype = dtype; in.mode = 0;
-    in.R = rows; in.C = cols; in.ps0 = ps0; in.ps1 = ps1; in.gs0 = gs0; in.gs1 = gs1; in.period = period;
-    in.idx = m_codebook; in.mag = m_magnitude; in.v0 = v_row; in.v1 = v_col; in.qt = qtable_dev;
-    in.lerp_w = (float)(1.0 - beta1); in.beta2 = (float)beta2; in.alpha2 = (float)(1.0 - beta2);
-    in.eps = (float)eps;
-    in.sc = StepScalars{(float)lr, (float)inv_bias_correction_2, (float)inv_bias_correction_1,
-                        (float)weight_decay_factor};
-    in.sr = stochastic_round ? 1 : 0; in.seed = (uint64_t)rng_seed;
-    in.step_scalars = step_scalars; in.seed_dev = seed_dev;
+    WorkInput in;
+    bool empty = false;
+    int rc = factored_input("gefenx_factored_update", p, grad, dtype, rows, cols, ps0, ps1, gs0, gs1, m_codebook,
+                            m_magnitude, v_row, v_col, period, qtable_dev, beta1, beta2, lr, eps,
+                            inv_bias_correction_2, inv_bias_correction_1, weight_decay_factor, stochastic_round,
+                            rng_seed, step_scalars, seed_dev, in, empty);
+    if (rc || empty) return rc;
+    if (!workspace) return set_error(GEFENX_EINVAL, "gefenx_factored_update: null workspace");
     in.workspace = workspace; in.ws_bytes = workspace_bytes;
     TensorWork w;
     rc = build_work(in, w);
     if (rc) return rc;
     return run_single(w, static_cast<hipStream_t>(stream));
+}
+
+int gefenx_factored_update_noalloc(
+    void* p, const void* grad, int dtype, int64_t rows, int64_t cols,
+    int64_t ps0, int64_t ps1, int64_t gs0, int64_t gs1,
+    uint8_t* m_codebook, float* m_magnitude, float* v_row, float* v_col,
+    int64_t period, const void* qtable_dev,
+    double beta1, double beta2, double lr, double eps,
+    double inv_bias_correction_2, double inv_bias_correction_1,
+    double weight_decay_factor, int stochastic_round, int64_t rng_seed,
+    const float* step_scalars, const int64_t* seed_dev, void* stream) {
+    const char* fn = "gefenx_factored_update_noalloc";
+    WorkInput in;
+    bool empty = false;
+    int rc = factored_input(fn, p, grad, dtype, rows, cols, ps0, ps1, gs0, gs1, m_codebook, m_magnitude, v_row,
+                            v_col, period, qtable_dev, beta1, beta2, lr, eps, inv_bias_correction_2,
+                            inv_bias_correction_1, weight_decay_factor, stochastic_round, rng_seed, step_scalars,
+                            seed_dev, in, empty);
+    if (rc || empty) return rc;
+    const FactoredWs L = FactoredWs::make(rows, cols, rows * cols / period);
+    if (L.total > (size_t)GEFENX_NOALLOC_SCRATCH_BYTES)
+        return set_error(GEFENX_EINVAL, "%s: a [%lld, %lld] parameter with period %lld needs %zu bytes of scratch; "
+                         "the static scratch holds %zu (use gefenx_factored_update with a workspace)", fn,
+                         (long long)rows, (long long)cols, (long long)period, L.total,
+                         (size_t)GEFENX_NOALLOC_SCRATCH_BYTES);
+    void* ptr = nullptr;
+    rc = scratch_on_device(&ptr);
+    if (rc) return rc;
+    in.workspace = ptr;
+    in.ws_bytes = GEFENX_NOALLOC_SCRATCH_BYTES;
+    TensorWork w;
+    rc = build_work(in, w);
+    if (rc) return rc;
+    // the accumulators that must start at zero: block maxima and the
+    // finalize counter (the previous call on this GPU left them zero unless
+    // it failed part-way)
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* base = static_cast<char*>(ptr);
+    const int64_t nmag = (int64_t)((L.off_magold - L.off_magbits) / sizeof(uint32_t));
+    hipLaunchKernelGGL(k_zero_words, dim3((unsigned)std::min<int64_t>(1024, ceil_div(nmag, kThreads))),
+                       dim3(kThreads), 0, s, reinterpret_cast<uint32_t*>(base + L.off_magbits), nmag);
+    hipLaunchKernelGGL(k_zero_words, dim3(1), dim3(kThreads), 0, s, reinterpret_cast<uint32_t*>(base + L.off_fin),
+                       (int64_t)(256 / sizeof(uint32_t)));
+    rc = launch_check(fn);
+    if (rc) return rc;
+    return run_single(w, s);
 }
 
 int gefenx_block_update(

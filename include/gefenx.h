@@ -104,6 +104,32 @@ int gefenx_factored_update(
     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * The factored step without a workspace argument and without allocating:
+ * no counterpart in the reference.  For callers that cannot allocate device
+ * memory at step time (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * gefenx_factored_update minus (workspace, workspace_bytes): the kernels use
+ * a static device array of GEFENX_NOALLOC_SCRATCH_BYTES per GPU (held until
+ * the process ends), so shapes whose gefenx_workspace_bytes(GEFENX_WS_FACTORED,
+ * ...) exceeds it are rejected with GEFENX_EINVAL (every Llama-3-8B and
+ * Qwen3-4B tensor fits; the embedding needs 21 MiB).  The first call on a
+ * device resolves the array's address there (make it outside a capture).
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (two streams, two threads) race.  The call clears what must start at zero
+ * with a kernel, so it may be recorded into a graph.
+ * ---------------------------------------------------------------------- */
+#define GEFENX_NOALLOC_SCRATCH_BYTES (32u << 20)
+int gefenx_factored_update_noalloc(
+    void* p, const void* grad, int dtype, int64_t rows, int64_t cols,
+    int64_t ps0, int64_t ps1, int64_t gs0, int64_t gs1,
+    uint8_t* m_codebook, float* m_magnitude, float* v_row, float* v_col,
+    int64_t period, const void* qtable_dev,
+    double beta1, double beta2, double lr, double eps,
+    double inv_bias_correction_2, double inv_bias_correction_1,
+    double weight_decay_factor, int stochastic_round, int64_t rng_seed,
+    const float* step_scalars, const int64_t* seed_dev, void* stream);
+
+/* ------------------------------------------------------------------------
  * Block-vmean step (1D params, and 2D params with factored_v_2d=False).
  * Replaces automatic_gefen_fused_full_update_cuda
  * (kernels/automatic_gefen_fused_kernel.cu:2233-2409) and

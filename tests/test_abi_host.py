@@ -234,3 +234,19 @@ def test_ctypes_mirrors_match_header_layout(struct, mirror):
     size, offsets = _c_layout(struct, names)
     assert ctypes.sizeof(cls) == size
     assert [getattr(cls, f).offset for f in names] == offsets
+
+
+def test_noalloc_rejects_shapes_beyond_the_static_scratch(lib):
+    """gefenx_factored_update_noalloc checks the workspace its shape needs
+    against the static scratch before any HIP call: a 65536 x 40960 parameter
+    (~101 MiB of workspace) is refused with EINVAL, here on a machine without
+    a GPU (the pointers are never touched)."""
+    from gefen.kernels import _native
+    fake = 4096  # never dereferenced: the size check comes first
+    need = lib.gefenx_workspace_bytes(_native.WS_FACTORED, 65536, 40960, 65536)
+    assert need > (32 << 20)
+    rc = lib.gefenx_factored_update_noalloc(fake, fake, _native.DT_BF16, 65536, 40960, 40960, 1, 40960, 1,
+                                            fake, fake, fake, fake, 40960, fake, 0.9, 0.999, 1e-3, 1e-8, 1.0,
+                                            1.0, 1.0, 0, 0, None, None, None)
+    assert rc == _native.GEFENX_EINVAL
+    assert "static scratch" in _native.last_error()
