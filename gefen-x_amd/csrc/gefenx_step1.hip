@@ -295,13 +295,16 @@ __global__ void k_zero_u32(uint32_t* p, int64_t n) {
 
 // ---------------------------------------------------------------- histogram
 // gefen.py:455-469: absmax per block, x = g / absmax (0 when absmax is not
-// > 0), bin = clamp(floor((x + 1) / (2 / bins)), 0, bins - 1).  The absmax is
-// carried as ordered uint bits of |g| (NaN > inf > finite), so a NaN block
-// bins every element at x = 0 as the reference's torch.where does.
+// > 0), bin = clamp(floor((x + 1) * (bins / 2)), 0, bins - 1), the scaling of
+// the reference's histogram kernel (kernels/exact_histogram_fused_kernel.cu:
+// 66-76); for the optimizer's 4096 bins it equals the torch path's division
+// by 2 / bins exactly.  The absmax is carried as ordered uint bits of |g|
+// (NaN > inf > finite), so a NaN block bins every element at x = 0 as the
+// reference's torch.where does.
 
 __device__ __forceinline__ int bin_of(float v, float amax, bool nz, float scale, int bins) {
     const float x = nz ? v / amax : 0.0f;
-    const float t = floorf((x + 1.0f) * scale);  // dividing by 2/bins is exact scaling
+    const float t = floorf((x + 1.0f) * scale);
     if (!(t >= 0.0f)) return 0;
     if (t > (float)(bins - 1)) return bins - 1;
     return (int)t;
@@ -314,7 +317,7 @@ __global__ void __launch_bounds__(kT) k_hist_wave(const void* g, int64_t nb, int
     __shared__ uint32_t s_cnt[4096];
     for (int i = threadIdx.x; i < bins; i += kT) s_cnt[i] = 0u;
     __syncthreads();
-    const float scale = (float)(bins / 2);
+    const float scale = 0.5f * (float)bins;
     const int lane = threadIdx.x & 63;
     const int64_t wave = ((int64_t)blockIdx.x * kT + threadIdx.x) >> 6;
     const int64_t nwaves = ((int64_t)gridDim.x * kT) >> 6;
@@ -360,7 +363,7 @@ __global__ void __launch_bounds__(kT) k_hist_seg(const void* g, int64_t P, int64
     __shared__ uint32_t s_cnt[4096];
     for (int i = threadIdx.x; i < bins; i += kT) s_cnt[i] = 0u;
     __syncthreads();
-    const float scale = (float)(bins / 2);
+    const float scale = 0.5f * (float)bins;
     const int64_t b = (int64_t)blockIdx.x / segs_per_block;
     const int64_t sg = (int64_t)blockIdx.x - b * segs_per_block;
     const int64_t lo = b * P + sg * kSeg;
@@ -589,15 +592,20 @@ int gefenx_exact_histogram(const void* grad, int dtype, int64_t numel, int64_t p
 
 int gefenx_factored_v_ema(float* v_row, float* v_col, const float* row_sq, const float* col_sq,
                           int64_t rows, int64_t cols, double beta2, void* stream) {
-    if (!v_row || !v_col || !row_sq || !col_sq || rows < 0 || cols < 0)
-        return set_error(GEFENX_EINVAL, "gefenx_factored_v_ema: bad arguments");
+    if (rows == 0 && cols == 0) return GEFENX_OK;
+    if (rows <= 0 || cols <= 0)
+        return set_error(GEFENX_EINVAL, "gefenx_factored_v_ema: expected both v_row and v_col to be non-empty");
+    if (!v_row || !v_col || !row_sq || !col_sq)
+        return set_error(GEFENX_EINVAL, "gefenx_factored_v_ema: null pointer argument");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const float b2 = (float)beta2, a2 = (float)(1.0 - beta2);
-    // row_sq / cols and col_sq / rows as true divides (gefen.py:2994-2996)
+    // the aten chain v.mul_(beta2).add_(sq.div_(n), alpha=1-beta2) on the GPU
+    // (kernels/automatic_gefen_fused_kernel.cu:2010-2020): the scalar divide
+    // is a multiply by the fp32 reciprocal of n, then fma(1-beta2, t, v*beta2)
     if (rows) hipLaunchKernelGGL(k_v_ema, dim3(grid_cap(rows, kT, 1024)), dim3(kT), 0, s, v_row, row_sq, rows,
-                                 0.0f, b2, a2, 1, (float)cols);
+                                 1.0f / (float)cols, b2, a2, 0, (float)cols);
     if (cols) hipLaunchKernelGGL(k_v_ema, dim3(grid_cap(cols, kT, 1024)), dim3(kT), 0, s, v_col, col_sq, cols,
-                                 0.0f, b2, a2, 1, (float)rows);
+                                 1.0f / (float)rows, b2, a2, 0, (float)rows);
     return check("gefenx_factored_v_ema");
 }
 

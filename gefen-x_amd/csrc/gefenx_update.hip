@@ -82,6 +82,7 @@ struct TensorWork {
     int32_t dtype, mode;
     int32_t fast_stats, fast_apply;  // kernel variant: 0 general, 1 contiguous, 2 transposed view
     int32_t write_p, sr, bf16_mean, det_epl;  // det_epl: block stats elements per item (8 or 1)
+    int32_t partial, pad3_;  // partial: block path with the caller's per-block stepsize (no vmean)
     float eps, beta2, alpha2, pad2_;
     StepScalars sc;
     MomentumCoef mc;
@@ -986,6 +987,10 @@ __device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) 
         for (int64_t sh = 0; sh < w.shards; ++sh) {
             sq += w.blk_sq[sh * w.nb + b];
             w.blk_sq[sh * w.nb + b] = 0.0;
+        }
+        if (w.partial) {  // the stepsize comes from the caller: magnitudes only
+            finalize_magnitude(w, b);
+            continue;
         }
         if (w.det_rec != nullptr) {
             const int64_t wlo = (b * w.P) / w.det_elems;
@@ -2670,6 +2675,34 @@ int gefenx_block_update(
     TensorWork w;
     rc = build_work(in, w);
     if (rc) return rc;
+    return run_single(w, static_cast<hipStream_t>(stream));
+}
+
+int gefenx_momentum_apply(
+    void* p, const void* grad, int dtype, int64_t numel, int64_t period,
+    uint8_t* m_codebook, float* m_magnitude, const float* stepsize, const void* qtable_dev,
+    double beta1, double lr, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_dtype(dtype, "gefenx_momentum_apply");
+    if (rc) return rc;
+    if (numel < 0) return set_error(GEFENX_EINVAL, "gefenx_momentum_apply: negative numel");
+    if (numel == 0) return GEFENX_OK;
+    if (period <= 0 || numel % period != 0)
+        return set_error(GEFENX_EINVAL, "gefenx_momentum_apply: period %lld does not divide numel %lld",
+                         (long long)period, (long long)numel);
+    if (!p || !grad || !m_codebook || !m_magnitude || !stepsize || !qtable_dev || !workspace)
+        return set_error(GEFENX_EINVAL, "gefenx_momentum_apply: null pointer argument");
+    WorkInput in{};
+    in.p = p; in.grad = grad; in.dtype = dtype; in.mode = 1;
+    in.R = 1; in.C = numel; in.ps0 = numel; in.ps1 = 1; in.gs0 = numel; in.gs1 = 1; in.period = period;
+    in.idx = m_codebook; in.mag = m_magnitude; in.v0 = nullptr; in.v1 = nullptr; in.qt = qtable_dev;
+    in.lerp_w = (float)(1.0 - beta1); in.beta2 = 0.0f; in.alpha2 = 0.0f; in.eps = 0.0f;
+    in.sc = StepScalars{(float)lr, 1.0f, 1.0f, 1.0f};
+    in.workspace = workspace; in.ws_bytes = workspace_bytes;
+    TensorWork w;
+    rc = build_work(in, w);
+    if (rc) return rc;
+    w.partial = 1;
+    w.step = const_cast<float*>(stepsize);  // read by the apply, never written in this mode
     return run_single(w, static_cast<hipStream_t>(stream));
 }
 

@@ -390,14 +390,16 @@ class Gefen(torch.optim.Optimizer):
                                      "while learning Gefen codebook".format(period, name, flat.numel()))
                 yield name, flat, int(period), grad
 
-    def _learn_gefen_exact_codebook(self, reuse_existing_periods=False):
-        """learn_gefen_exact_codebook_from_grad_periods: gefen.py:417-517."""
+    def _grad_histogram_counts(self, bins, reuse_existing_periods):
+        """Block-absmax-normalised histogram of every gradient (gefen.py:
+        417-469) on the histogram kernel: (int64 counts on the device, number
+        of elements), or (None, 0) when no parameter has a gradient."""
         lib = _native.load()
         counts_dev = None
         total = 0
         for _, flat, period, _ in self._iter_gefen_grad_periods(reuse_existing_periods):
             if counts_dev is None:
-                counts_dev = torch.zeros(HISTOGRAM_BINS, dtype=torch.int64, device=flat.device)
+                counts_dev = torch.zeros(bins, dtype=torch.int64, device=flat.device)
             elif counts_dev.device != flat.device:
                 raise ValueError("all parameters must live on one device")
             f = flat if flat.is_contiguous() else flat.contiguous()
@@ -406,8 +408,13 @@ class Gefen(torch.optim.Optimizer):
                 part = f[start:start + chunk]
                 _native.check(lib.gefenx_exact_histogram(
                     part.data_ptr(), _fused._dtype_code(part.dtype), part.numel(), period,
-                    counts_dev.data_ptr(), HISTOGRAM_BINS, _stream_of(part)), "exact histogram")
+                    counts_dev.data_ptr(), bins, _stream_of(part)), "exact histogram")
             total += f.numel()
+        return counts_dev, total
+
+    def _learn_gefen_exact_codebook(self, reuse_existing_periods=False):
+        """learn_gefen_exact_codebook_from_grad_periods: gefen.py:417-517."""
+        counts_dev, total = self._grad_histogram_counts(HISTOGRAM_BINS, reuse_existing_periods)
         if total == 0:
             return None
         counts = counts_dev.cpu().to(torch.float32)
@@ -420,6 +427,34 @@ class Gefen(torch.optim.Optimizer):
         cb = quantization_module.exact_dp(histogram_stats=stats, num_codebooks=NUM_CODEBOOKS,
                                           force_endpoints=True, device=counts_dev.device)
         return cb.to(counts_dev.device)
+
+    def _maybe_save_gefen_grad_histogram(self):
+        """gefen.py:3095-3150: at the global steps listed in
+        quantization.LIST_STEPS_SAVE_HIST_GRAD, write the histogram of the
+        block-absmax-normalised gradients (codebook size x 16 bins) next to
+        quantization.SAVE_CODEBOOK_PREFIX; the counts come from the histogram
+        kernel (its binning equals the reference's for power-of-two bin
+        counts, e.g. 4096 for a 256-entry codebook)."""
+        steps = getattr(quantization_module, "LIST_STEPS_SAVE_HIST_GRAD", None)
+        if steps is None:
+            return
+        if self.capturable and steps:
+            raise ValueError("capturable=True is incompatible with LIST_STEPS_SAVE_HIST_GRAD: histogram collection "
+                             "and file output are host-driven")
+        if self._gefen_global_step not in steps:
+            return
+        prefix = getattr(quantization_module, "SAVE_CODEBOOK_PREFIX", None)
+        if prefix is None:
+            raise ValueError("LIST_STEPS_SAVE_HIST_GRAD requires SAVE_CODEBOOK_PREFIX to be set.")
+        if self._gefen_codebook is None:
+            raise ValueError("Expected Gefen codebook to be initialized before saving gradient histogram.")
+        bins = self._gefen_codebook.numel() * 16
+        counts_dev, total = self._grad_histogram_counts(bins, reuse_existing_periods=True)
+        if total == 0:
+            raise ValueError("Cannot save Gefen gradient histogram because no gradients were available.")
+        quantization_module.save_distribution_histogram_pt_from_counts(
+            hist=counts_dev.cpu().to(torch.float32), prefix=prefix,
+            suffix="grad_hist_step_{}".format(self._gefen_global_step), num_samples=total)
 
     def _maybe_refresh_gefen_codebook(self):
         if self._gefen_codebook is not None:
@@ -798,8 +833,11 @@ class Gefen(torch.optim.Optimizer):
         counter = self._capt_counters[device]
         cb = self._gefen_codebook_on(device)
         qt = [0, 0, 0]
+        tables = []  # the plan bakes these addresses in: it keeps the tensors alive
         for dt in dtypes:
-            qt[_fused._dtype_code(dt)] = _fused.quant_table(cb, dt).data_ptr()
+            t = _fused.quant_table(cb, dt)
+            tables.append(t)
+            qt[_fused._dtype_code(dt)] = t.data_ptr()
         sr = 1 if self._stochastic_round else 0
         key = (device, tuple(rows), tuple(scalar_ptrs), tuple(capt_rows), tuple(qt), sr, counter.data_ptr())
         ent = self._capt_plans.get(key)
@@ -815,7 +853,7 @@ class Gefen(torch.optim.Optimizer):
                     descs.ctypes.data if n else None, n, ss, qt_arr, sr, 0, capt, m, counter.data_ptr(),
                     ctypes.byref(handle)), "capturable plan")
             nbytes = int(lib.gefenx_mt_plan_device_bytes(handle))
-            ent = [handle, torch.empty(nbytes, dtype=torch.uint8, device=device), False]
+            ent = [handle, torch.empty(nbytes, dtype=torch.uint8, device=device), False, tables]
             self._capt_plans[key] = ent
             if not capturing:
                 eager = [k for k, e in self._capt_plans.items() if not e[2] and k != key]
@@ -848,6 +886,7 @@ class Gefen(torch.optim.Optimizer):
             self._assert_capture_ready()
         else:
             self._maybe_refresh_gefen_codebook()
+            self._maybe_save_gefen_grad_histogram()
             if (self._codebook_refresh_every and self._gefen_global_step > 0
                     and self._gefen_global_step % self._codebook_refresh_every == 0):
                 self._refresh_codebook_with_requant()

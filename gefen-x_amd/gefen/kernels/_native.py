@@ -89,6 +89,7 @@ SIGNATURES = {
     "gefenx_factored_update_noalloc": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64,
                                             _P, _P, _P, _P, _I64, _P,
                                             _D, _D, _D, _D, _D, _D, _D, _I, _I64, _P, _P, _P]),
+    "gefenx_momentum_apply": (_I, [_P, _P, _I, _I64, _I64, _P, _P, _P, _P, _D, _D, _P, _SZ, _P]),
     "gefenx_block_update": (_I, [_P, _P, _I, _I64, _I64, _P, _P, _P, _P,
                                  _D, _D, _D, _D, _D, _D, _D, _I, _I64, _P, _P,
                                  _P, _SZ, _P]),

@@ -22,7 +22,6 @@ from . import _native
 
 _LUT_BUCKETS = 4096
 _LUT_CACHE: dict = {}
-_QTABLE_CACHE: dict = {}
 
 # Routing constants of the reference (kernels/automatic_gefen_fused.py:23-50).
 # This build has ONE block-path kernel set; the predicates are kept because
@@ -99,11 +98,13 @@ def _codebook_search_lut(codebook: torch.Tensor) -> torch.Tensor:
 def quant_table(codebook: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     """Device byte image of the quantisation table for (codebook, grad dtype).
     One host build + one upload per codebook version (the exact-DP codebook is
-    frozen after step 1)."""
-    key = (codebook.data_ptr(), codebook._version, codebook.device, dtype)
-    cached = _QTABLE_CACHE.get(key)
-    if cached is not None:
-        return cached[1]
+    frozen after step 1).  The table is kept on the codebook tensor itself, so
+    it lives exactly as long as the codebook: a captured graph that baked its
+    address keeps working while the optimizer holds that codebook."""
+    key = (codebook._version, codebook.device, dtype)
+    cache = getattr(codebook, "_gefenx_qtables", None)
+    if cache is not None and key in cache:
+        return cache[key]
     lib = _native.load()
     cb = _host_codebook(codebook)
     if cb.numel() < 1 or cb.numel() > 256:
@@ -112,9 +113,10 @@ def quant_table(codebook: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     _native.check(lib.gefenx_qtable_build(cb.data_ptr(), cb.numel(), _dtype_code(dtype),
                                           host.data_ptr()), "qtable build")
     dev = host.to(codebook.device) if codebook.device.type != "cpu" else host
-    while len(_QTABLE_CACHE) >= 16:
-        _QTABLE_CACHE.pop(next(iter(_QTABLE_CACHE)))
-    _QTABLE_CACHE[key] = (codebook, dev)
+    if cache is None:
+        cache = {}
+        codebook._gefenx_qtables = cache
+    cache[key] = dev
     return dev
 
 
@@ -344,6 +346,154 @@ def _quantized_momentum_update_impl(grad_view: torch.Tensor, m_sign: torch.Tenso
         float(beta1), 1 if stochastic_round else 0, int(rng_seed), sd, 1 if nesterov else 0,
         ws.data_ptr(), ws.numel(), _stream(grad_view.device)),
         "gefen_quantized_momentum_update_cuda")
+
+
+def _momentum_apply_impl(p: torch.Tensor, grad_view: torch.Tensor, m_sign: torch.Tensor,
+                         m_magnitude: torch.Tensor, stepsize: torch.Tensor, codebook: torch.Tensor,
+                         packed_indices: bool, beta1: float, lr: float, what: str) -> None:
+    _check_common(p, grad_view, m_sign, m_magnitude, codebook, packed_indices)
+    if stepsize.device != p.device:
+        raise ValueError("stepsize device {} must match p device {}.".format(stepsize.device, p.device))
+    if stepsize.dtype != torch.float32:
+        raise ValueError("stepsize must be float32, got {}.".format(stepsize.dtype))
+    if p.numel() == 0:
+        return
+    if stepsize.numel() != m_magnitude.numel():
+        raise ValueError("stepsize must hold one entry per block ({}), got {}".format(
+            m_magnitude.numel(), stepsize.numel()))
+    if not p.is_contiguous():
+        raise ValueError("p must be contiguous")
+    period = _period_of(grad_view, m_magnitude)
+    grad_c = grad_view if grad_view.is_contiguous() else grad_view.contiguous()
+    step_c = stepsize if stepsize.is_contiguous() else stepsize.contiguous()
+    qt = quant_table(codebook, p.dtype)
+    ws = workspace_for(m_magnitude, _native.WS_BLOCK, 1, p.numel(), m_magnitude.numel())
+    _native.check(_native.load().gefenx_momentum_apply(
+        p.data_ptr(), grad_c.data_ptr(), _dtype_code(p.dtype), p.numel(), period, m_sign.data_ptr(),
+        m_magnitude.data_ptr(), step_c.data_ptr(), qt.data_ptr(), float(beta1), float(lr), ws.data_ptr(),
+        ws.numel(), _stream(p.device)), what)
+
+
+def automatic_gefen_fused_update_cuda(p: torch.Tensor, grad_view: torch.Tensor, m_sign: torch.Tensor,
+                                      m_magnitude: torch.Tensor, stepsize: torch.Tensor,
+                                      codebook: torch.Tensor, packed_indices: bool, beta1: float,
+                                      lr: float, *, use_v2: Optional[bool] = None) -> None:
+    """Legacy partial update (reference :202-265): requantise the momentum and
+    apply p -= c[idx'] * mag' * stepsize[b] * lr with the caller's per-block
+    stepsize (no second moment, no weight decay).  `use_v2` picks between the
+    reference's two kernels, which compute the same step; both routes reach
+    one C-ABI function here (gefenx_momentum_apply)."""
+    _momentum_apply_impl(p, grad_view, m_sign, m_magnitude, stepsize, codebook, packed_indices, beta1, lr,
+                         "automatic_gefen_fused_update_cuda")
+
+
+def _factored_v_ema_impl(v_row: torch.Tensor, v_col: torch.Tensor, row_sq: torch.Tensor,
+                         col_sq: torch.Tensor, beta2: float) -> None:
+    """Standalone factored EMA (reference binding :114-120, kernel
+    :2792-2850): v_row = v_row*beta2 + (row_sq/cols)*(1-beta2) and the same
+    for v_col with rows, as the GPU aten chain rounds it."""
+    tensors = (("v_row", v_row), ("v_col", v_col), ("row_sq", row_sq), ("col_sq", col_sq))
+    for name, t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError("Expected all tensors to be on CUDA ({} is on {}).".format(name, t.device))
+        if t.device != v_row.device:
+            raise ValueError("Expected all tensors on the same device.")
+        if not t.is_contiguous():
+            raise ValueError("Expected all tensors to be contiguous.")
+        if t.dtype != torch.float32:
+            raise ValueError("Expected all tensors to have dtype float32.")
+    rows, cols = v_row.numel(), v_col.numel()
+    if row_sq.numel() != rows or col_sq.numel() != cols:
+        raise ValueError("Expected row_sq/col_sq numel to match v_row/v_col.")
+    _native.check(_native.load().gefenx_factored_v_ema(
+        v_row.data_ptr(), v_col.data_ptr(), row_sq.data_ptr(), col_sq.data_ptr(), rows, cols, float(beta2),
+        _stream(v_row.device)), "gefen_factored_v_ema_cuda")
+
+
+def _check_lut(lut: Optional[torch.Tensor], codebook: torch.Tensor) -> None:
+    """The reference binding's `lut` argument: int16 with >= 2 entries on the
+    codebook's device, or empty (= full search).  The quantisation table is
+    derived from the codebook itself, so a valid LUT changes nothing."""
+    if lut is None or lut.numel() == 0:
+        return
+    if lut.dtype != torch.int16 or lut.numel() < 2:
+        raise ValueError("codebook LUT must be int16 with >= 2 entries (or empty)")
+    if lut.device != codebook.device:
+        raise ValueError("codebook LUT device {} must match codebook device {}.".format(lut.device, codebook.device))
+
+
+class _Extension:
+    """The object `_load_extension()` returns: the reference's pybind module
+    surface (kernels/automatic_gefen_fused_binding.cpp:122-256) -- the same
+    function names and positional argument order, `lut` included -- over the
+    C ABI.  The reference's tests call these names directly."""
+
+    @staticmethod
+    def automatic_gefen_fused_update_cuda(p, grad_view, m_sign, m_magnitude, stepsize, codebook, packed_indices,
+                                          beta1, lr):
+        _momentum_apply_impl(p, grad_view, m_sign, m_magnitude, stepsize, codebook, packed_indices, beta1, lr,
+                             "automatic_gefen_fused_update_cuda")
+
+    @staticmethod
+    def automatic_gefen_fused_update_v2_cuda(p, grad_view, m_sign, m_magnitude, stepsize, codebook,
+                                             packed_indices, beta1, lr):
+        _momentum_apply_impl(p, grad_view, m_sign, m_magnitude, stepsize, codebook, packed_indices, beta1, lr,
+                             "automatic_gefen_fused_update_v2_cuda")
+
+    @staticmethod
+    def automatic_gefen_fused_full_update_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook, lut,
+                                               packed_indices, beta1, beta2, lr, eps, inv_sqrt_bias_correction_2,
+                                               inv_bias_correction_1, weight_decay_factor, stochastic_round=False,
+                                               rng_seed=0, step_scalars=None, seed_dev=None):
+        _check_lut(lut, codebook)
+        _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1, beta2, lr, eps,
+                      inv_sqrt_bias_correction_2, inv_bias_correction_1, weight_decay_factor, stochastic_round,
+                      rng_seed, step_scalars, seed_dev, "automatic_gefen_fused_full_update_cuda")
+
+    @staticmethod
+    def automatic_gefen_fused_update_v2_full_cuda(p, grad_view, m_sign, m_magnitude, vmean, codebook, lut,
+                                                  packed_indices, beta1, beta2, lr, eps,
+                                                  inv_sqrt_bias_correction_2, inv_bias_correction_1,
+                                                  weight_decay_factor, stochastic_round=False, rng_seed=0,
+                                                  step_scalars=None, seed_dev=None):
+        _check_lut(lut, codebook)
+        _block_update(p, grad_view, m_sign, m_magnitude, vmean, codebook, packed_indices, beta1, beta2, lr, eps,
+                      inv_sqrt_bias_correction_2, inv_bias_correction_1, weight_decay_factor, stochastic_round,
+                      rng_seed, step_scalars, seed_dev, "automatic_gefen_fused_update_v2_full_cuda")
+
+    @staticmethod
+    def gefen_quantized_momentum_update_cuda(grad_view, m_sign, m_magnitude, codebook, lut, momentum_out, beta1,
+                                             stochastic_round, rng_seed, seed_dev, nesterov):
+        _check_lut(lut, codebook)
+        _quantized_momentum_update_impl(grad_view, m_sign, m_magnitude, codebook, momentum_out, beta1,
+                                        stochastic_round, rng_seed, seed_dev, None, nesterov)
+
+    @staticmethod
+    def gefen_factored_update_cuda(p, grad_view, m_sign, m_magnitude, v_row, v_col, codebook, lut, cols, beta1,
+                                   beta2, lr, eps, inv_bias_correction_2, inv_bias_correction_1,
+                                   weight_decay_factor, stochastic_round=False, rng_seed=0, step_scalars=None,
+                                   seed_dev=None):
+        _check_lut(lut, codebook)
+        _factored_update_impl(p, grad_view, m_sign, m_magnitude, v_row, v_col, codebook, cols, beta1, beta2, lr,
+                              eps, inv_bias_correction_2, inv_bias_correction_1, weight_decay_factor,
+                              stochastic_round, rng_seed, step_scalars, None, seed_dev)
+
+    @staticmethod
+    def gefen_factored_v_ema_cuda(v_row, v_col, row_sq, col_sq, beta2):
+        _factored_v_ema_impl(v_row, v_col, row_sq, col_sq, beta2)
+
+
+_EXTENSION_MODULE: Optional[_Extension] = None
+
+
+def _load_extension() -> _Extension:
+    """Reference :124-136: the extension module, loading the gfx950 library
+    on first use (raises if it is missing or does not load)."""
+    global _EXTENSION_MODULE
+    if _EXTENSION_MODULE is None:
+        _native.load()
+        _EXTENSION_MODULE = _Extension()
+    return _EXTENSION_MODULE
 
 
 # ---------------------------------------------------------------- compile surface

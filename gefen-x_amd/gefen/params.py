@@ -1,18 +1,27 @@
-"""Routing of parameters between Muon and the Gefen backup (reference
-params.py:30-187): 2D hidden weight matrices go to Muon; embeddings (by module
-type, which also catches tied heads), LM / classifier heads (by name) and every
-1D or other-shaped tensor go to the backup."""
+"""Routing of parameters between Muon and the Gefen backup, and checks of a
+hand-made split (reference params.py:30-187).
+
+Rule: a trainable parameter goes to Muon when it is 2D, is not the weight of
+an embedding module (identity test, so a head tied to an embedding follows
+it) and its lower-cased name contains none of the backup substrings;
+everything else -- embeddings, LM / classifier heads, norms, biases, other
+shapes -- goes to the backup optimizer.
+"""
 from __future__ import annotations
 
+import collections
 import logging
-from typing import Iterable, List, Tuple
+from typing import Iterable, List, Sequence, Tuple
 
 import torch
 import torch.nn as nn
 
 logger = logging.getLogger(__name__)
 
-# Name substrings routed to the backup (params.py:30-37).
+NamedParams = List[Tuple[str, nn.Parameter]]
+
+# Name substrings (case-insensitive) that keep a 2D weight off Muon
+# (params.py:30-37).  A routing table of the reference, kept identical.
 DEFAULT_BACKUP_SUBSTRINGS: Tuple[str, ...] = (
     "embed",
     "wte",
@@ -24,87 +33,84 @@ DEFAULT_BACKUP_SUBSTRINGS: Tuple[str, ...] = (
 
 
 def is_muon_param(name: str, param, backup_substrings=DEFAULT_BACKUP_SUBSTRINGS) -> bool:
-    """params.py:40-45: a 2D tensor whose name matches no backup substring."""
-    if param.ndim != 2:
-        return False
-    lname = name.lower()
-    return not any(sub.lower() in lname for sub in backup_substrings)
+    """params.py:40-45: 2D, and no backup substring in the lower-cased name."""
+    lowered = name.lower()
+    return param.ndim == 2 and all(s.lower() not in lowered for s in backup_substrings)
 
 
 def _embedding_param_ids(model: nn.Module) -> set:
-    """ids of every nn.Embedding / nn.EmbeddingBag weight (params.py:48-62)."""
-    ids = set()
-    for module in model.modules():
-        if isinstance(module, (nn.Embedding, nn.EmbeddingBag)):
-            weight = getattr(module, "weight", None)
-            if weight is not None:
-                ids.add(id(weight))
-    return ids
+    """Identities of the weights of every nn.Embedding / nn.EmbeddingBag
+    (params.py:48-62); a tied head shares one of these objects."""
+    kinds = (nn.Embedding, nn.EmbeddingBag)
+    return {id(m.weight) for m in model.modules() if isinstance(m, kinds) and getattr(m, "weight", None) is not None}
 
 
 def split_params_for_muon(
     model: nn.Module,
     backup_substrings: Iterable[str] = DEFAULT_BACKUP_SUBSTRINGS,
-) -> Tuple[List[Tuple[str, nn.Parameter]], List[Tuple[str, nn.Parameter]]]:
-    """(muon_named, backup_named) of the model's trainable parameters
-    (params.py:65-101); frozen parameters are skipped."""
-    backup_substrings = tuple(backup_substrings)
+) -> Tuple[NamedParams, NamedParams]:
+    """(muon, backup) lists of (name, param) pairs over the model's trainable
+    parameters, in model order (params.py:65-101); logs the split."""
+    subs = tuple(backup_substrings)
     embedding_ids = _embedding_param_ids(model)
-    muon: List[Tuple[str, nn.Parameter]] = []
-    backup: List[Tuple[str, nn.Parameter]] = []
-    for name, p in model.named_parameters():
-        if not p.requires_grad:
-            continue
-        if id(p) not in embedding_ids and is_muon_param(name, p, backup_substrings):
-            muon.append((name, p))
-        else:
-            backup.append((name, p))
-    logger.info("split_params_for_muon: %d muon / %d backup params; backup = %s", len(muon), len(backup),
+
+    def to_muon(name, p):
+        return id(p) not in embedding_ids and is_muon_param(name, p, subs)
+
+    trainable = [(n, p) for n, p in model.named_parameters() if p.requires_grad]
+    muon = [(n, p) for n, p in trainable if to_muon(n, p)]
+    backup = [(n, p) for n, p in trainable if not to_muon(n, p)]
+    logger.info("split_params_for_muon: Muon gets %d tensors, the backup %d: %s", len(muon), len(backup),
                 [n for n, _ in backup])
     return muon, backup
 
 
-def _check_named_pairs(named_params, which: str):
-    for item in named_params:
-        if (isinstance(item, (tuple, list)) and len(item) == 2 and isinstance(item[0], str)
-                and isinstance(item[1], torch.Tensor)):
-            continue
+def _is_named_pair(item) -> bool:
+    return (isinstance(item, (tuple, list)) and len(item) == 2 and isinstance(item[0], str)
+            and isinstance(item[1], torch.Tensor))
+
+
+def _require_named_pairs(items: Sequence, side: str) -> None:
+    """TypeError for anything but (str, tensor) pairs (params.py:104-124): a
+    bare 2-row tensor would otherwise unpack into two rows."""
+    bad = [item for item in items if not _is_named_pair(item)]
+    if bad:
         raise TypeError(
-            "validate_split expects the {} list to contain (name, param) pairs, got {!r}. Pass named parameters "
-            "(e.g. model.named_parameters() or the lists from split_params_for_muon), or build the optimizer via "
-            "GefenMuonHybrid.from_model(model, ...)".format(which, type(item)))
+            "validate_split: every entry of the {} list must be a (name, parameter) pair; found {!r}. Use "
+            "model.named_parameters(), the lists split_params_for_muon returns, or "
+            "GefenMuonHybrid.from_model(model, ...)".format(side, type(bad[0])))
 
 
 def validate_split(muon_named_params, backup_named_params, model: nn.Module = None):
-    """params.py:127-187: (name, param) pairs only; no parameter twice or in
-    both lists; unique names; with a model, every trainable parameter
-    covered.  Returns the two lists."""
-    muon_named_params = list(muon_named_params)
-    backup_named_params = list(backup_named_params)
-    _check_named_pairs(muon_named_params, "muon")
-    _check_named_pairs(backup_named_params, "backup")
-    muon_ids = {id(p) for _, p in muon_named_params}
-    backup_ids = {id(p) for _, p in backup_named_params}
-    if len(muon_ids) != len(muon_named_params):
-        raise ValueError("Duplicate parameter object in the muon list")
-    if len(backup_ids) != len(backup_named_params):
-        raise ValueError("Duplicate parameter object in the backup list")
-    overlap = muon_ids & backup_ids
-    if overlap:
-        dupes = [n for n, p in muon_named_params if id(p) in overlap]
-        raise ValueError("Parameter(s) {} appear in BOTH the muon and backup lists; they would be stepped twice per "
-                         "optimizer step".format(dupes))
-    names = [str(n).lower() for n, _ in muon_named_params] + [str(n).lower() for n, _ in backup_named_params]
-    if len(set(names)) != len(names):
-        seen, dupes = set(), set()
-        for n in names:
-            (dupes if n in seen else seen).add(n)
-        raise ValueError("Duplicate parameter name(s) {} across the muon/backup lists; the per-parameter codebook "
-                         "cache keys on the name, so duplicates collide".format(sorted(dupes)))
+    """params.py:127-187: raise on a split that would step a parameter twice
+    or never.  TypeError for entries that are not (name, param) pairs;
+    ValueError for a parameter object listed twice on one side, listed on
+    both sides, two entries whose names collide case-insensitively (the
+    codebook cache keys on names), and -- given `model` -- a trainable
+    parameter on neither side.  Returns the two lists."""
+    lists = {"muon": list(muon_named_params), "backup": list(backup_named_params)}
+    for side, items in lists.items():
+        _require_named_pairs(items, side)
+    owners = collections.defaultdict(list)  # id(param) -> [(side, name), ...]
+    for side, items in lists.items():
+        for name, p in items:
+            owners[id(p)].append((side, name))
+    for side in lists:
+        if any(sum(1 for s, _ in entries if s == side) > 1 for entries in owners.values()):
+            raise ValueError("Duplicate parameter object in the {} list".format(side))
+    in_both = [name for entries in owners.values() for s, name in entries
+               if s == "muon" and len({x for x, _ in entries}) == 2]
+    if in_both:
+        raise ValueError("Parameter(s) {} appear in BOTH the muon and backup lists, so every step would update "
+                         "them twice".format(in_both))
+    name_counts = collections.Counter(str(n).lower() for items in lists.values() for n, _ in items)
+    clashes = sorted(n for n, c in name_counts.items() if c > 1)
+    if clashes:
+        raise ValueError("Duplicate parameter name(s) {} across the two lists; names key the per-parameter "
+                         "codebook cache and must be unique".format(clashes))
     if model is not None:
-        covered = muon_ids | backup_ids
-        missing = [name for name, p in model.named_parameters() if p.requires_grad and id(p) not in covered]
-        if missing:
-            raise ValueError("Trainable parameter(s) {} are in neither the muon nor backup list; they would never "
-                             "be optimized".format(missing))
-    return muon_named_params, backup_named_params
+        uncovered = [n for n, p in model.named_parameters() if p.requires_grad and id(p) not in owners]
+        if uncovered:
+            raise ValueError("Trainable parameter(s) {} are in neither the muon nor the backup list and would "
+                             "never be updated".format(uncovered))
+    return lists["muon"], lists["backup"]

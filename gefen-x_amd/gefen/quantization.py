@@ -23,26 +23,34 @@ LIST_STEPS_SAVE_HIST_GRAD = None
 SAVE_CODEBOOK_PREFIX = None
 
 
+def _histogram_record(counts: torch.Tensor, num_samples: int, value_range) -> dict:
+    """The dumped dict (the reference's file layout: hist, bin_edges,
+    bin_centers, bin_width, range, num_bins, num_samples)."""
+    lo, hi = (float(v) for v in value_range)
+    hist = counts.detach().to(device="cpu", dtype=torch.float32)
+    nbins = hist.numel()
+    edges = torch.linspace(lo, hi, steps=nbins + 1, dtype=torch.float32)
+    return {"hist": hist, "bin_edges": edges, "bin_centers": (edges[1:] + edges[:-1]) * 0.5,
+            "bin_width": (hi - lo) / nbins, "range": (lo, hi), "num_bins": nbins,
+            "num_samples": int(num_samples)}
+
+
 def save_distribution_histogram_pt_from_counts(hist, prefix, suffix, num_samples, value_range=(-1.0, 1.0)):
-    if prefix is None:
-        raise ValueError("Cannot save gradient histogram because SAVE_CODEBOOK_PREFIX is None.")
-    if hist.dim() != 1:
-        raise ValueError("Expected 1D histogram counts, got dim={}.".format(hist.dim()))
-    if hist.numel() <= 0:
-        raise ValueError("Expected at least one histogram bin.")
-    if num_samples < 0:
-        raise ValueError("num_samples must be non-negative, got {}.".format(num_samples))
-    prefix_path = Path(prefix).expanduser().resolve()
-    prefix_path.parent.mkdir(parents=True, exist_ok=True)
-    path = prefix_path.parent / "{}_{}.pt".format(prefix_path.stem, suffix)
-    hist_cpu = hist.detach().cpu().to(torch.float32)
-    left, right = value_range
-    edges = torch.linspace(float(left), float(right), steps=hist_cpu.numel() + 1, dtype=torch.float32)
-    torch.save({"hist": hist_cpu, "bin_edges": edges, "bin_centers": 0.5 * (edges[:-1] + edges[1:]),
-                "bin_width": float(right - left) / float(hist_cpu.numel()),
-                "range": (float(left), float(right)), "num_bins": hist_cpu.numel(),
-                "num_samples": int(num_samples)}, path)
-    logger.info("Saved distribution histogram data to %s", path)
+    """Write a histogram of normalised gradients to `<dir of prefix>/<stem of
+    prefix>_<suffix>.pt` (reference quantization.py:12-56; ValueError for a
+    missing prefix, non-1D or empty counts, a negative sample count)."""
+    problems = [(prefix is None, "no SAVE_CODEBOOK_PREFIX is set"),
+                (prefix is not None and hist.dim() != 1, "the counts must be 1D, got dim={}".format(hist.dim())),
+                (prefix is not None and hist.numel() == 0, "the counts hold no bins"),
+                (num_samples < 0, "num_samples must be >= 0, got {}".format(num_samples))]
+    for failed, why in problems:
+        if failed:
+            raise ValueError("Cannot save the gradient histogram: " + why)
+    target = Path(prefix).expanduser().resolve()
+    out = target.with_name("{}_{}.pt".format(target.stem, suffix))
+    out.parent.mkdir(parents=True, exist_ok=True)
+    torch.save(_histogram_record(hist, num_samples, value_range), out)
+    logger.info("Saved distribution histogram data to %s", out)
 
 
 def exact_dp(histogram_stats: dict, num_codebooks: int, force_endpoints: bool = True,

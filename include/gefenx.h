@@ -76,6 +76,10 @@ int gefenx_search_lut(const float* codebook, int k, int buckets, int16_t* lut_ou
  * be reused across steps (and inside a captured graph) without clearing.
  * ---------------------------------------------------------------------- */
 enum gefenx_ws_kind { GEFENX_WS_FACTORED = 0, GEFENX_WS_BLOCK = 1, GEFENX_WS_MOMENTUM = 2 };
+/* FACTORED: the parameter's [rows, cols] and block count.  BLOCK: rows * cols
+ * = the parameter's numel (e.g. rows = 1, cols = numel) and its block count;
+ * the block sums need per-workgroup records sized from numel.  MOMENTUM:
+ * rows and cols unused. */
 size_t gefenx_workspace_bytes(int kind, int64_t rows, int64_t cols, int64_t num_blocks);
 
 /* ------------------------------------------------------------------------
@@ -164,12 +168,34 @@ int gefenx_quantized_momentum_update(
     const int64_t* seed_dev, int nesterov,
     void* workspace, size_t workspace_bytes, void* stream);
 
-/* Factored EMA alone: v <- fma(sq/n, 1-beta2, v*beta2) for row and column
- * sums.  Replaces gefen_factored_v_ema_cuda
- * (kernels/automatic_gefen_fused_kernel.cu:2792-2850). */
+/* Factored EMA alone, for row and column sums of squares:
+ * v <- fma(1-beta2, sq * RN(1/n), RN(v*beta2)) with n = cols for v_row and
+ * rows for v_col -- the GPU aten chain v.mul_(beta2).add_(sq.div_(n), 1-beta2)
+ * that the reference's standalone kernel reproduces bit for bit (the fused
+ * step's own EMA divides, as the reference's CPU step does).  rows == cols ==
+ * 0 is a no-op; exactly one of them zero is GEFENX_EINVAL.  Replaces
+ * gefen_factored_v_ema_cuda (kernels/automatic_gefen_fused_kernel.cu:1990-2042,
+ * 2792-2850; binding kernels/automatic_gefen_fused_binding.cpp:114-120). */
 int gefenx_factored_v_ema(float* v_row, float* v_col, const float* row_sq,
                           const float* col_sq, int64_t rows, int64_t cols,
                           double beta2, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Momentum requantisation and apply with a per-block stepsize the caller
+ * computed (the legacy partial update; no second moment, no weight decay):
+ * the quantised momentum advances as in gefenx_block_update, then
+ * p <- D(p - c[idx'] * mag' * stepsize[b] * lr) (lr == 0: p untouched).
+ * stepsize: device fp32 [numel/period].  workspace:
+ * gefenx_workspace_bytes(GEFENX_WS_BLOCK, 1, numel, numel/period).
+ * Replaces automatic_gefen_fused_update_cuda and
+ * automatic_gefen_fused_update_v2_cuda (kernels/automatic_gefen_fused_kernel.cu:
+ * 331-415, 2102-2231, 2411-2532; binding
+ * kernels/automatic_gefen_fused_binding.cpp:9-31); both compute this step.
+ * ---------------------------------------------------------------------- */
+int gefenx_momentum_apply(
+    void* p, const void* grad, int dtype, int64_t numel, int64_t period,
+    uint8_t* m_codebook, float* m_magnitude, const float* stepsize, const void* qtable_dev,
+    double beta1, double lr, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Block vmean EMA alone.  Replaces automatic_vmean_update_cuda
  * (kernels/automatic_vmean_kernel.cu:122-214); bf16 squares/means round

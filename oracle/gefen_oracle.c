@@ -371,10 +371,15 @@ void orc_block_step(float* p, const float* g, uint8_t* idx, float* mag,
 /*
  * learn_gefen_exact_codebook_from_grad_periods, torch histogram branch:
  * gefen.py:455-469.  counts has `bins` int64 entries and is accumulated.
+ * multiply = 0: floor((x + 1) / f32(2 / bins)) (the torch path); 1:
+ * floor((x + 1) * (0.5f * bins)) (the reference's histogram kernel,
+ * kernels/exact_histogram_fused_kernel.cu:66-76).  The two agree whenever
+ * bins is a power of two.
  */
-void orc_exact_histogram(const float* g, int64_t n, int64_t period, int bins,
-                         int64_t* counts) {
+void orc_exact_histogram_form(const float* g, int64_t n, int64_t period, int bins,
+                              int64_t* counts, int multiply) {
     const float bin_width = (float)(2.0 / (double)bins);
+    const float scale = 0.5f * (float)bins;
     const int64_t nb = n / period;
     for (int64_t b = 0; b < nb; ++b) {
         const float* blk = g + b * period;
@@ -388,7 +393,7 @@ void orc_exact_histogram(const float* g, int64_t n, int64_t period, int bins,
         const int nonzero = !saw_nan && amax > 0.0f;
         for (int64_t j = 0; j < period; ++j) {
             float x = nonzero ? blk[j] / amax : 0.0f;
-            float t = floorf((x + 1.0f) / bin_width);
+            float t = multiply ? floorf((x + 1.0f) * scale) : floorf((x + 1.0f) / bin_width);
             int64_t bi;
             if (isnan(t)) bi = 0; /* long() of NaN then clamp(0, bins-1) */
             else if (t < 0.0f) bi = 0;
@@ -397,6 +402,10 @@ void orc_exact_histogram(const float* g, int64_t n, int64_t period, int bins,
             counts[bi] += 1;
         }
     }
+}
+
+void orc_exact_histogram(const float* g, int64_t n, int64_t period, int bins, int64_t* counts) {
+    orc_exact_histogram_form(g, n, period, bins, counts, 0);
 }
 
 /* ------------------------------------------------------------ exact DP */
@@ -488,4 +497,49 @@ uint8_t orc_sr_quantize(const float* cb, int k, float x, uint64_t seed, int64_t 
     float p_up = (span > 0.0f) ? (v - lo) / span : 0.0f;
     float u = orc_sr_uniform(seed, element_idx);
     return (uint8_t)((u < p_up) ? r : l);
+}
+
+/* ------------------------------------------------ standalone factored EMA */
+
+/*
+ * gefen_factored_v_ema_cuda: kernels/automatic_gefen_fused_kernel.cu:1990-2042,
+ * 2792-2850 -- the GPU aten chain v.mul_(beta2).add_(sq.div_(n), alpha=1-beta2):
+ * t = sq * RN(1/n) (a scalar divide is a reciprocal multiply there),
+ * vb = RN(v * beta2), v' = fma(1 - beta2, t, vb).
+ */
+void orc_factored_v_ema(float* v, const float* sq, int64_t count, int64_t n, double beta2) {
+    const float inv = 1.0f / (float)(double)n;
+    const float b2 = (float)beta2;
+    const float a2 = (float)(1.0 - beta2);
+    for (int64_t i = 0; i < count; ++i) {
+        const float t = sq[i] * inv;
+        const float vb = v[i] * b2;
+        v[i] = fmaf(a2, t, vb);
+    }
+}
+
+/* ------------------------------------------- partial update (legacy pair) */
+
+/*
+ * automatic_gefen_fused_update_cuda / _v2_cuda: kernels/automatic_gefen_fused_kernel.cu:
+ * 331-415 -- the quantised-momentum recurrence of the CPU step (gefen.py:3438-3486)
+ * followed by p <- D(p - (q * stepsize[b]) * lr), no weight decay; lr == 0 leaves
+ * p untouched.  stepsize: fp32 [nb].
+ */
+void orc_partial_update(float* p, const float* g, uint8_t* idx, float* mag, const float* stepsize,
+                        int64_t n, int64_t period, const float* cb, int k, int dtype, double beta1,
+                        double lr) {
+    const int64_t nb = n / period;
+    float* q = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    orc_momentum_update(g, idx, mag, nb, period, cb, k, dtype, (float)(1.0 - beta1), q, NULL);
+    const float lr_f = (float)lr;
+    if (lr_f != 0.0f) {
+        for (int64_t b = 0; b < nb; ++b) {
+            for (int64_t j = 0; j < period; ++j) {
+                const int64_t e = b * period + j;
+                p[e] = orc_round(p[e] - (q[e] * stepsize[b]) * lr_f, dtype);
+            }
+        }
+    }
+    free(q);
 }

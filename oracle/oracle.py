@@ -17,7 +17,15 @@ Parity status of each function (how it is pinned):
   exact_histogram      reference golden vectors + integer order-freedom
   exact_dp             reference golden vectors (pure-Python DP) + brute force
   find_period          reference golden vectors + closed-form rule tests
-  sr_quantize          SplitMix64 known answer + unbiasedness invariant
+  sr_quantize          published SplitMix64 outputs, unbiasedness, bracket and
+                       endpoint cases (tests/test_oracle_sr.py)
+  vmean_update         reference golden block-step trajectories (through
+                       block_step) and the decomposition block_step = vmean_update
+                       + stepsize + partial_update (tests/test_oracle_boundary.py)
+  partial_update       the same decomposition against the pinned block_step
+  factored_v_ema       closed-form special cases (beta2 = 0, zero sums, power-of-two
+                       n) and agreement with factored_step's EMA where the
+                       reciprocal multiply is exact
 """
 from __future__ import annotations
 
@@ -66,6 +74,7 @@ def _lib():
     lib.orc_block_step.argtypes = [P, P, P, P, P, i64, i64, P, i, i,
                                    d, d, d, d, d, d, d]
     lib.orc_exact_histogram.argtypes = [P, i64, i64, i, P]
+    lib.orc_exact_histogram_form.argtypes = [P, i64, i64, i, P, i]
     lib.orc_exact_dp_kernel.restype = i
     lib.orc_exact_dp_kernel.argtypes = [P, P, P, i, i, i, P]
     lib.orc_sr_uniform.restype = f
@@ -73,6 +82,8 @@ def _lib():
     lib.orc_sr_quantize.restype = ctypes.c_uint8
     lib.orc_sr_quantize.argtypes = [P, i, f, ctypes.c_uint64, i64]
     lib.orc_set_rounding.argtypes = [i, ctypes.c_uint64]
+    lib.orc_factored_v_ema.argtypes = [P, P, i64, i64, d]
+    lib.orc_partial_update.argtypes = [P, P, P, P, P, i64, i64, P, i, i, d, d]
     _LIB = lib
     return lib
 
@@ -299,15 +310,55 @@ def block_step(p, g, idx, mag, vmean, period, codebook, dtype, *,
     return p.reshape(shape), idx, mag, vmean
 
 
+def vmean_update(vmean, g, period, dtype, beta2):
+    """automatic_vmean_update(use_fused=False): gefen.py:129-191.  Returns
+    the new vmean (bf16 grads square and average through bf16)."""
+    g = _f32(g).reshape(-1)
+    v = _f32(vmean).reshape(-1).copy()
+    _lib().orc_vmean_update(_ptr(v), _ptr(g), g.size // period, period, dtype, float(beta2))
+    return v
+
+
+def factored_v_ema(v, sq, n, beta2):
+    """gefen_factored_v_ema_cuda (kernels/automatic_gefen_fused_kernel.cu:
+    1990-2042, 2792-2850): v <- fma(1-beta2, sq * RN(1/n), RN(v*beta2)), the
+    rounding of the GPU aten chain v.mul_(beta2).add_(sq.div_(n), 1-beta2).
+    Returns the new v."""
+    v = _f32(v).reshape(-1).copy()
+    sq = _f32(sq).reshape(-1)
+    _lib().orc_factored_v_ema(_ptr(v), _ptr(sq), v.size, int(n), float(beta2))
+    return v
+
+
+def partial_update(p, g, idx, mag, stepsize, period, codebook, dtype, *, beta1, lr):
+    """automatic_gefen_fused_update_cuda (kernels/automatic_gefen_fused_kernel.cu:
+    331-415) on the CPU step's recurrence (gefen.py:3438-3486): momentum, then
+    p <- D(p - (q * stepsize[b]) * lr).  Returns (p, idx, mag)."""
+    shape = np.shape(p)
+    p = _f32(p).reshape(-1).copy()
+    g = _f32(g).reshape(-1)
+    idx = np.ascontiguousarray(np.asarray(idx, dtype=np.uint8).reshape(-1)).copy()
+    mag = _f32(mag).reshape(-1).copy()
+    st = _f32(stepsize).reshape(-1)
+    cb = _f32(codebook)
+    _lib().orc_partial_update(_ptr(p), _ptr(g), _ptr(idx), _ptr(mag), _ptr(st), p.size, period, _ptr(cb),
+                              cb.size, dtype, float(beta1), float(lr))
+    return p.reshape(shape), idx, mag
+
+
 # ------------------------------------------------------------ step-1 math
 
 
-def exact_histogram(g, period: int, bins: int = 4096, counts=None) -> np.ndarray:
-    """Block-absmax-normalised histogram: gefen.py:455-469."""
+def exact_histogram(g, period: int, bins: int = 4096, counts=None, kernel_scale: bool = False) -> np.ndarray:
+    """Block-absmax-normalised histogram: gefen.py:455-469 (bins from a
+    division by f32(2/bins)); kernel_scale=True bins with a multiply by
+    bins/2, as the reference's histogram kernel does
+    (kernels/exact_histogram_fused_kernel.cu:66-76).  Identical for
+    power-of-two bins."""
     g = _f32(g).reshape(-1)
     if counts is None:
         counts = np.zeros(bins, dtype=np.int64)
-    _lib().orc_exact_histogram(_ptr(g), g.size, period, bins, _ptr(counts))
+    _lib().orc_exact_histogram_form(_ptr(g), g.size, period, bins, _ptr(counts), 1 if kernel_scale else 0)
     return counts
 
 

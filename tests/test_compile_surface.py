@@ -73,3 +73,25 @@ def test_eager_default_path_skips_the_op():
     args["step_scalars"] = None
     with pytest.raises(ValueError, match="HIP device"):
         fused.gefen_factored_update_cuda(**args)
+
+
+def test_every_kernel_name_the_reference_optimizer_imports_resolves():
+    """The names gefen.py imports from the kernel modules (gefen.py:25-51,
+    the lazy histogram import at 444-446, partitioning.py:216) resolve here,
+    without a GPU (the library is loaded on first call)."""
+    import importlib
+    names = {
+        "gefen.partitioning": ["find_period_by_block_variance"],
+        "gefen.kernels.automatic_vmean": ["automatic_vmean_update_cuda", "_load_extension"],
+        "gefen.kernels.automatic_gefen_fused": [
+            "automatic_gefen_fused_update_cuda", "automatic_gefen_fused_full_update_cuda",
+            "automatic_gefen_fused_update_v2_full_cuda", "gefen_quantized_momentum_update_cuda",
+            "gefen_factored_update_cuda", "_should_use_v2_full", "_should_use_v2", "_CAPT_V1_FULL_TINY_NUMEL",
+            "_codebook_search_lut", "ensure_extension_loaded", "_load_extension"],
+        "gefen.kernels.exact_histogram_fused": ["gefen_exact_histogram_cuda", "_load_extension"],
+        "gefen.kernels.period_variance": ["average_within_block_variance_cuda_kernel"],
+    }
+    for mod, attrs in names.items():
+        m = importlib.import_module(mod)
+        for a in attrs:
+            assert hasattr(m, a), "%s.%s" % (mod, a)
