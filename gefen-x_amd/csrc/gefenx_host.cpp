@@ -12,7 +12,7 @@
 #include "gefenx_common.h"
 #include "gefenx_dp.h"
 #include "gefenx_internal.h"
-#include "../../include/gefenx.h"
+#include "gefenx.h"
 
 namespace gx {
 

@@ -6,7 +6,7 @@
 
 #include "gefenx_internal.h"
 #include "gefenx_profile.h"
-#include "../../include/gefenx.h"
+#include "gefenx.h"
 
 namespace gx {
 

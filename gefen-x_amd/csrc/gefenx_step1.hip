@@ -4,7 +4,7 @@
 #include "gefenx_device.h"
 #include "gefenx_dp.h"
 #include "gefenx_internal.h"
-#include "../../include/gefenx.h"
+#include "gefenx.h"
 
 #include <algorithm>
 #include <cmath>

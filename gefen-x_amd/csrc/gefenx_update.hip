@@ -21,7 +21,7 @@
 #include "gefenx_device.h"
 #include "gefenx_internal.h"
 #include "gefenx_profile.h"
-#include "../../include/gefenx.h"
+#include "gefenx.h"
 
 #include <algorithm>
 #include <cmath>

@@ -22,6 +22,7 @@
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math).
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -151,36 +152,62 @@ static uint8_t requantize(const float* cb, int k, float x, int64_t element_idx) 
     return g_sr_on ? orc_sr_quantize(cb, k, x, g_sr_seed, element_idx) : orc_nearest(cb, k, x);
 }
 
+/* Threads for the loops below (OpenMP).  Every parallel loop keeps each
+ * element's operation order -- per-row and per-column sums stay sequential in
+ * their own index order, the block max is an exact max -- so any thread count
+ * gives bit-identical results. */
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+
+/* Blocks at least this long are split across threads; shorter blocks are
+ * handed out whole. */
+#define ORC_PAR_BLOCK 16384
+
+static void momentum_block(const float* g, uint8_t* idx, float* mag, int64_t b, int64_t period,
+                           const float* cb, int k, int dtype, float w, float* q, float* u_out,
+                           float* u, int inner_parallel) {
+    const int64_t base = b * period;
+    const float m_old = mag[b];
+    float amax = 0.0f;
+    int saw_nan = 0;
+#pragma omp parallel for if (inner_parallel) reduction(max : amax) reduction(| : saw_nan) schedule(static)
+    for (int64_t j = 0; j < period; ++j) {
+        float c = orc_round(cb[idx[base + j]], dtype);
+        float cm = c * m_old;
+        float uu = lerp_f(cm, g[base + j], w);
+        u[j] = uu;
+        if (u_out) u_out[base + j] = uu;
+        float a = fabsf(uu);
+        if (isnan(a)) saw_nan = 1;
+        else if (a > amax) amax = a;
+    }
+    float m_new = saw_nan ? NAN : amax;
+    mag[b] = m_new;
+    const int nonzero = (m_new > 0.0f);
+#pragma omp parallel for if (inner_parallel) schedule(static)
+    for (int64_t j = 0; j < period; ++j) {
+        float x = nonzero ? u[j] / m_new : 0.0f;
+        uint8_t ni = requantize(cb, k, x, base + j);
+        idx[base + j] = ni;
+        if (q) q[base + j] = orc_round(cb[ni], dtype) * m_new;
+    }
+}
+
 void orc_momentum_update(const float* g, uint8_t* idx, float* mag, int64_t nb,
                          int64_t period, const float* cb, int k, int dtype,
                          float w, float* q, float* u_out) {
-    float* u = (float*)malloc(sizeof(float) * (size_t)(period > 0 ? period : 1));
-    for (int64_t b = 0; b < nb; ++b) {
-        const int64_t base = b * period;
-        const float m_old = mag[b];
-        float amax = 0.0f;
-        int saw_nan = 0;
-        for (int64_t j = 0; j < period; ++j) {
-            float c = orc_round(cb[idx[base + j]], dtype);
-            float cm = c * m_old;
-            float uu = lerp_f(cm, g[base + j], w);
-            u[j] = uu;
-            if (u_out) u_out[base + j] = uu;
-            float a = fabsf(uu);
-            if (isnan(a)) saw_nan = 1;
-            else if (j == 0 || a > amax) amax = a;
-        }
-        float m_new = saw_nan ? NAN : amax;
-        mag[b] = m_new;
-        const int nonzero = (m_new > 0.0f);
-        for (int64_t j = 0; j < period; ++j) {
-            float x = nonzero ? u[j] / m_new : 0.0f;
-            uint8_t ni = requantize(cb, k, x, base + j);
-            idx[base + j] = ni;
-            if (q) q[base + j] = orc_round(cb[ni], dtype) * m_new;
-        }
+    if (period >= ORC_PAR_BLOCK) {
+        float* u = (float*)malloc(sizeof(float) * (size_t)period);
+        for (int64_t b = 0; b < nb; ++b) momentum_block(g, idx, mag, b, period, cb, k, dtype, w, q, u_out, u, 1);
+        free(u);
+        return;
     }
-    free(u);
+#pragma omp parallel if (nb > 1)
+    {
+        float* u = (float*)malloc(sizeof(float) * (size_t)(period > 0 ? period : 1));
+#pragma omp for schedule(static)
+        for (int64_t b = 0; b < nb; ++b) momentum_block(g, idx, mag, b, period, cb, k, dtype, w, q, u_out, u, 0);
+        free(u);
+    }
 }
 
 /* ------------------------------------------------- Muon quantised momentum */
@@ -259,25 +286,41 @@ void orc_factored_step(float* p, const float* g, uint8_t* idx, float* mag,
                        double bc1, double bc2, double wd) {
     const int64_t n = rows * cols;
     const int64_t nb = n / period;
-    double* col_acc = (double*)calloc((size_t)cols, sizeof(double));
     const float beta2_f = (float)beta2;
     const float alpha_f = (float)(1.0 - beta2);
+    /* row sums, each over its columns in order */
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < rows; ++i) {
         double racc = 0.0;
         for (int64_t j = 0; j < cols; ++j) {
             float gv = g[i * cols + j];
             float sq = gv * gv;
             racc += (double)sq;
-            col_acc[j] += (double)sq;
         }
         float row_ms = (float)racc / (float)cols;
         v_row[i] = fmaf(row_ms, alpha_f, v_row[i] * beta2_f);
     }
-    for (int64_t j = 0; j < cols; ++j) {
-        float col_ms = (float)col_acc[j] / (float)rows;
-        v_col[j] = fmaf(col_ms, alpha_f, v_col[j] * beta2_f);
+    /* column sums, each over its rows in order; a thread owns a stripe of
+     * 64 columns and walks it row by row */
+    const int64_t stripes = (cols + 63) / 64;
+#pragma omp parallel for schedule(static)
+    for (int64_t st = 0; st < stripes; ++st) {
+        double cacc[64];
+        const int64_t j0 = st * 64;
+        const int64_t nj = cols - j0 < 64 ? cols - j0 : 64;
+        for (int64_t t = 0; t < nj; ++t) cacc[t] = 0.0;
+        for (int64_t i = 0; i < rows; ++i) {
+            const float* gr = g + i * cols + j0;
+            for (int64_t t = 0; t < nj; ++t) {
+                float sq = gr[t] * gr[t];
+                cacc[t] += (double)sq;
+            }
+        }
+        for (int64_t t = 0; t < nj; ++t) {
+            float col_ms = (float)cacc[t] / (float)rows;
+            v_col[j0 + t] = fmaf(col_ms, alpha_f, v_col[j0 + t] * beta2_f);
+        }
     }
-    free(col_acc);
     double vsum = 0.0;
     for (int64_t i = 0; i < rows; ++i) vsum += (double)v_row[i];
     float mean_r = (float)vsum / (float)rows;
@@ -291,6 +334,7 @@ void orc_factored_step(float* p, const float* g, uint8_t* idx, float* mag,
     const float inv_bc1_f = (float)(1.0 / bc1);
     const float lr_f = (float)lr;
     const float wdf_f = (float)(1.0 - lr * wd);
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < rows; ++i) {
         for (int64_t j = 0; j < cols; ++j) {
             const int64_t e = i * cols + j;
@@ -317,6 +361,7 @@ void orc_vmean_update(float* vmean, const float* g, int64_t nb, int64_t period,
                       int dtype, double beta2) {
     const float beta2_f = (float)beta2;
     const float alpha_f = (float)(1.0 - beta2);
+#pragma omp parallel for if (nb > 1) schedule(static)
     for (int64_t b = 0; b < nb; ++b) {
         double acc = 0.0;
         for (int64_t j = 0; j < period; ++j) {
@@ -346,6 +391,7 @@ void orc_block_step(float* p, const float* g, uint8_t* idx, float* mag,
     orc_vmean_update(vmean, g, nb, period, dtype, beta2);
     const float wdf_f = (float)(1.0 - lr * wd);
     if (wd > 0.0) {
+#pragma omp parallel for schedule(static)
         for (int64_t e = 0; e < n; ++e) p[e] = orc_round(p[e] * wdf_f, dtype);
     }
     const float sbc2_f = (float)sqrt(bc2);
@@ -354,6 +400,7 @@ void orc_block_step(float* p, const float* g, uint8_t* idx, float* mag,
     const float lr_f = (float)lr;
     float* q = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
     orc_momentum_update(g, idx, mag, nb, period, cb, k, dtype, (float)(1.0 - beta1), q, NULL);
+#pragma omp parallel for schedule(static)
     for (int64_t b = 0; b < nb; ++b) {
         float h = sqrtf(vmean[b]) / sbc2_f + eps_f;
         float step = (1.0f / h) * inv_bc1_f;

@@ -82,6 +82,8 @@ def _lib():
     lib.orc_sr_quantize.restype = ctypes.c_uint8
     lib.orc_sr_quantize.argtypes = [P, i, f, ctypes.c_uint64, i64]
     lib.orc_set_rounding.argtypes = [i, ctypes.c_uint64]
+    lib.orc_set_threads.argtypes = [i]
+    lib.orc_set_threads(1)
     lib.orc_factored_v_ema.argtypes = [P, P, i64, i64, d]
     lib.orc_partial_update.argtypes = [P, P, P, P, P, i64, i64, P, i, i, d, d]
     _LIB = lib
@@ -95,6 +97,12 @@ def _ptr(a: np.ndarray):
 
 def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def set_threads(n: int) -> None:
+    """Host threads of the step functions; results are bit-identical for
+    every thread count (the parallel loops keep each element's order)."""
+    _lib().orc_set_threads(int(n))
 
 
 def round_dtype(x: np.ndarray, dtype: int) -> np.ndarray:

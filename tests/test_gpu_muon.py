@@ -363,3 +363,64 @@ def test_muon_momentum_stochastic_rounding_matches_oracle(dev, lib, case):
         np.testing.assert_array_equal(idx.cpu().numpy(), idx_np, err_msg=tag + " indices")
         np.testing.assert_array_equal(mag.cpu().numpy(), mag_np, err_msg=tag + " magnitudes")
         np.testing.assert_array_equal(out.float().cpu().numpy(), out_np, err_msg=tag + " momentum")
+
+
+def _ns_torch_fp32(m, sched, eps=1e-7):
+    """The oracle's Newton-Schulz statement (gefen_muon.py:236-291: every
+    product and elementwise result rounded to bf16) with fp32 GEMMs on the
+    device (torch fp32 matmul on contiguous operands) instead of float64 on
+    the host -- for shapes the host cannot run in seconds."""
+    bf = lambda t: t.to(torch.bfloat16).float()
+    x = bf(m)
+    tall = x.shape[0] > x.shape[1]
+    if tall:
+        x = x.t().contiguous()
+    norm = bf(torch.linalg.vector_norm(x.double()).float().reshape(1))
+    norm = torch.clamp(norm, min=eps)
+    x = bf(x / bf(norm))
+    for a, b, c in sched:
+        gram = bf(x @ x.t().contiguous())
+        upd = bf(b * gram + c * (gram @ gram))
+        x = bf(a * x + upd @ x)
+    return x.t().contiguous() if tall else x
+
+
+@pytest.mark.parametrize("shape", [(4096, 14336), (14336, 4096)])
+def test_newton_schulz_workload_shape(dev, lib, shape):
+    """Llama-3-8B down / gate projection shapes (the Gram product has K =
+    14336, 224 K-steps of 64): within the reference's batched-vs-serial bound
+    (rel. Frobenius 2e-2) of an fp32-GEMM restatement, and every singular
+    value of the result in (0.5, 1.3)."""
+    rng = np.random.default_rng(shape[0])
+    m = torch.from_numpy((rng.standard_normal((2,) + shape) * 1e-3).astype(np.float32)).to(dev)
+    from gefen.kernels import automatic_gefen_fused as fused
+    b, r, c = m.shape
+    x = m.to(torch.bfloat16)
+    out = torch.empty(b, r, c, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(int(lib.gefenx_ns_workspace_bytes(b, r, c)), dtype=torch.uint8, device=dev)
+    abc = np.ascontiguousarray(np.asarray(orc.NS_STANDARD, np.float64).reshape(-1))
+    _check(lib.gefenx_newton_schulz(x.data_ptr(), fused._dtype_code(torch.bfloat16), out.data_ptr(), b, r, c,
+                                    abc.ctypes.data_as(ctypes.c_void_p), 5, 1e-7, ws.data_ptr(), ws.numel(),
+                                    _stream(dev)), lib)
+    torch.cuda.synchronize()
+    for i in range(b):
+        got = out[i].float()
+        ref = _ns_torch_fp32(m[i], orc.NS_STANDARD)
+        rel = (torch.linalg.vector_norm((got - ref).double()) / torch.linalg.vector_norm(ref.double())).item()
+        assert rel <= NS_REL, "item %d rel %.3e" % (i, rel)
+        small = got if got.shape[0] <= got.shape[1] else got.t().contiguous()
+        gram = (small @ small.t().contiguous()).double().cpu().numpy()
+        sv = np.sqrt(np.clip(np.linalg.eigvalsh(gram), 0.0, None))
+        assert 0.5 < sv.min() and sv.max() < 1.3, (i, sv.min(), sv.max())
+
+
+def test_newton_schulz_aspect_ratio_matches_oracle(dev, lib):
+    """1024 x 3584 (the down projection's aspect ratio at oracle size)
+    against the float64 oracle."""
+    rng = np.random.default_rng(3584)
+    m = (rng.standard_normal((1, 1024, 3584)) * 1e-3).astype(np.float32)
+    got = _ns_gpu(dev, lib, m, orc.NS_STANDARD)[0]
+    o = orc.newton_schulz(m[0])
+    assert np.linalg.norm(got - o) <= NS_REL * np.linalg.norm(o)
+    s = np.linalg.svd(got.astype(np.float64), compute_uv=False)
+    assert 0.5 < s.min() and s.max() < 1.3

@@ -122,3 +122,34 @@ def test_histogram_kernel_form_odd_bins():
     g = np.array([-1.0, 1.0, 0.0, 0.5], np.float32)  # one block, absmax 1
     c = orc.exact_histogram(g, 4, 37, kernel_scale=True)
     assert c[0] == 1 and c[36] == 1 and c[18] == 1 and c[int(np.floor(1.5 * 18.5))] == 1
+
+
+@pytest.mark.parametrize("period", [16, 4096, 1 << 16])
+def test_oracle_threads_are_bit_identical(period):
+    """The oracle's parallel loops keep each element's operation order:
+    factored, block and momentum steps give the same bits on 1 and 4
+    threads (many small blocks handed out whole, or few large blocks split)."""
+    rng = np.random.default_rng(period)
+    cb = np.load(os.path.join(GOLD, "learn.npz"))["cb"]
+    rows, cols = 256, 1024
+    p = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    g = (rng.standard_normal((rows, cols)) * 1e-3).astype(np.float32)
+    idx = rng.integers(0, 256, rows * cols).astype(np.uint8)
+    nb = rows * cols // period
+    mag = (rng.uniform(0.5, 1.5, nb) * 1e-3).astype(np.float32)
+    vr = np.abs(rng.standard_normal(rows) * 1e-6).astype(np.float32)
+    vc = np.abs(rng.standard_normal(cols) * 1e-6).astype(np.float32)
+    vm = np.abs(rng.standard_normal(nb) * 1e-6).astype(np.float32)
+    kw = dict(beta1=B1, beta2=B2, lr=LR, eps=EPS, bc1=0.5, bc2=0.01, wd=0.01)
+    outs = []
+    for threads in (1, 4):
+        orc.set_threads(threads)
+        try:
+            outs.append((orc.factored_step(p, g, idx, mag, vr, vc, period, cb, orc.BF16, **kw),
+                         orc.block_step(p, g, idx, mag, vm, period, cb, orc.F32, **kw),
+                         orc.momentum_update(g, idx, mag, period, cb, orc.F16, B1, sr_seed=77)))
+        finally:
+            orc.set_threads(1)
+    for a, b in zip(outs[0], outs[1]):
+        for x, y in zip(a, b):
+            assert np.asarray(x).tobytes() == np.asarray(y).tobytes()
