@@ -13,8 +13,14 @@ The step runs on MI355X through the C ABI in include/gefenx.h:
   1D / factored_v_2d=False
            block-shared second moment (gefen.py:3488-3818).
 
-This build is the fused GPU step only: parameters must live on a HIP device,
-and a missing gfx950 library raises instead of falling back to host math.
+This build steps on the GPU only: parameters must live on a HIP device, and a
+missing gfx950 library raises instead of falling back to host math.
+``fused=False`` (the reference's decomposed torch-op step and its merged
+small-tensor batching, gefen.py:3329-3486, 3832-4013) computes the same
+arithmetic, so it runs on the same kernels and the same multi-tensor launch.
+A parameter paged between devices between steps (CPU offload) takes its
+state along: the state follows the parameter's device at the next step
+(gefen.py:1897-1927).
 """
 from __future__ import annotations
 
@@ -45,6 +51,11 @@ _CHECKPOINT_FORMAT_VERSION = 1
 # Keys of per-parameter state that exist only at run time (workspaces and the
 # capturable per-step scalar row).
 _RUNTIME_STATE_KEYS = ("_gefenx_ws", "_capt_scalars")
+
+# Per-parameter state that follows a parameter paged to another device
+# between steps (gefen.py:66-77, 1897-1927).
+_COLOCATABLE_STATE_KEYS = ("m_codebook", "m_magnitude", "vmean", "vmean_step", "v_row", "v_col",
+                           "factored_step", "step", "stepsize", "_h_buf")
 
 # Step-like per-parameter counters: python ints, or 0-dim fp32 device tensors
 # under capturable=True (gefen.py:1887-1895, 5680-5705).
@@ -224,16 +235,15 @@ class Gefen(torch.optim.Optimizer):
                 "deterministic=True with factored_v_2d=True cannot honor stochastic_round=True: the "
                 "replica-exact factored path uses deterministic nearest-codeword quantization. Disable "
                 "stochastic rounding or factored_v_2d.")
-        if not fused:
-            raise ValueError("fused=False selects the reference's host-math step, which this MI355X "
-                             "build does not provide; use fused=True")
         self._validate_group_options(lr, betas, eps, weight_decay)
         if codebook_refresh_every < 0:
             raise ValueError("codebook_refresh_every must be >= 0 but is: {}".format(codebook_refresh_every))
         if capturable and codebook_refresh_every:
             raise ValueError("capturable=True is incompatible with codebook_refresh_every>0: the periodic "
                              "codebook re-learn is host-driven and cannot run inside a replayed CUDA graph.")
-        self.fused = True
+        # fused=False is the same step here (the decomposed step's arithmetic is
+        # what the kernels compute); the flag is kept for the reference's API.
+        self.fused = bool(fused)
         self._force_1d_period_one = force_1d_period_one
         self._force_2d_period_one = force_2d_period_one
         self._period_one_substrings = tuple(s.lower() for s in period_one_substrings)
@@ -508,7 +518,8 @@ class Gefen(torch.optim.Optimizer):
                     raise RuntimeError("gradient shape {} does not match parameter {} shape {}".format(
                         tuple(g.shape), name, tuple(p.shape)))
                 if g.device != p.device:
-                    raise RuntimeError("gradient of {} is on {}, parameter on {}".format(name, g.device, p.device))
+                    raise RuntimeError("gradient and parameter {} must be on the same device: gradient on {}, "
+                                       "parameter on {}".format(name, g.device, p.device))
                 if p.numel() and p.device.type != "cuda":
                     raise RuntimeError("Gefen (MI355X build) steps HIP device parameters only; {} is on {}".format(
                         name, p.device))
@@ -547,6 +558,23 @@ class Gefen(torch.optim.Optimizer):
             state["vmean"] = torch.zeros(nb, 1, dtype=torch.float32, device=p.device)
             state["vmean_step"] = self._new_step_counter(p.device)
 
+    def _colocate_param_state_(self, state, device: torch.device) -> None:
+        """gefen.py:1897-1927: a parameter relocated between steps (CPU offload
+        paging it CPU -> GPU, or a move to another GPU) finds its state on the
+        previous device; move the state tensors to the parameter's device.
+        Same-device steps return after one device compare (no copy, no
+        reassignment).  Under capturable the state addresses are part of the
+        recorded launches, so nothing moves."""
+        if self.capturable:
+            return
+        sentinel = state.get("m_codebook")
+        if sentinel is None or sentinel.device == device:
+            return
+        for key in _COLOCATABLE_STATE_KEYS:
+            value = state.get(key)
+            if torch.is_tensor(value) and value.device != device:
+                state[key] = value.to(device)  # a pure copy: indices and magnitudes move bit for bit
+
     def _new_step_counter(self, device, value=0):
         """gefen.py:1887-1895: a python int, or under capturable a 0-dim fp32
         device tensor so the bias corrections are computed on the device."""
@@ -568,6 +596,7 @@ class Gefen(torch.optim.Optimizer):
         state = self.state[p]
         if "step" not in state:
             self._init_state(state, p, grad, name, factored=True)
+        self._colocate_param_state_(state, grad.device)
         if "v_row" not in state:  # resume from a block-vmean checkpoint (gefen.py:2840-2852)
             state["v_row"] = torch.zeros(p.shape[0], dtype=torch.float32, device=p.device)
             state["v_col"] = torch.zeros(p.shape[1], dtype=torch.float32, device=p.device)
@@ -587,6 +616,7 @@ class Gefen(torch.optim.Optimizer):
         state = self.state[p]
         if "step" not in state:
             self._init_state(state, p, grad, name, factored=False)
+        self._colocate_param_state_(state, grad.device)
         if "vmean" not in state:  # resume from a factored checkpoint (gefen.py:3567-3586)
             state["vmean"] = torch.zeros_like(state["m_magnitude"])
             state["vmean_step"] = self._new_step_counter(p.device)
