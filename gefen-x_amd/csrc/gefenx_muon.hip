@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <vector>
 
 namespace gx {
 namespace muon {
@@ -46,23 +47,38 @@ static int launch_check(const char* what) {
 // ==================================================================
 // Quantised momentum
 // ==================================================================
-struct MomArgs {
+// A launch covers a batch of matrices of one shape [R, C] (blockIdx.y picks
+// the matrix): the grad, state and workspace pointers, the period and the
+// grad strides are per matrix, the scalars shared.  The dense momentum of
+// matrix i goes to out + i * N (row-major, the Newton-Schulz input stack).
+constexpr int kMaxBatch = 16;
+
+struct MomItem {
     const void* g;
+    int64_t gs0, gs1;   // grad strides in elements (logical row-major order)
     uint8_t* idx;
-    float* mag;       // m_magnitude (old on entry, new after finalize)
-    void* out;        // dense momentum, grad dtype
-    uint32_t* magbits;
+    float* mag;         // m_magnitude (old on entry, new after finalize)
+    uint32_t* magbits;  // workspace: sharded block max |u| (ordered bits)
     float* mag_old;
-    float* minv;      // RN(1 / max(mag_new, tiny)) or 0 when unusable
+    float* minv;        // RN(1 / max(mag_new, tiny)) or 0 when unusable
+    int64_t P, nb, shards;
+    double invP;
+};
+struct MomBatch {
+    MomItem it[kMaxBatch];
+};
+
+struct MomArgs {
+    void* out;        // dense momentum [n, N], grad dtype
     const QTable* qt;
     const int64_t* seed_dev;
-    int64_t N, P, nb, shards;
-    double invP;
+    int64_t N, C;
+    double invC;
     uint64_t seed;
     float w;          // (float)(1 - beta)
     float beta;       // (float)beta
     float alpha_d;    // D((float)(1 - beta)): torch's add_ alpha in the grad dtype
-    int nesterov, sr, dtype;
+    int nesterov;
 };
 
 // u = D(lerp(D(D(c) * m_old), g, w)); cr already rounded through D.
@@ -74,99 +90,124 @@ __device__ __forceinline__ float mom_u(float cr, float m_old, float g, float w) 
     return round_dt<DT>(l);
 }
 
+// Offset of logical element e of a [R, C] view with strides (gs0, gs1).
+__device__ __forceinline__ int64_t view_offset(int64_t e, int64_t C, double invC, int64_t s0, int64_t s1) {
+    const int64_t r = div_floor(e, C, invC);
+    return r * s0 + (e - r * C) * s1;
+}
+
+// Any layout: grid-stride over the matrix's elements.
 template <int DT>
-__global__ void __launch_bounds__(kT) k_mom_max(MomArgs a) {
+__global__ void __launch_bounds__(kT) k_mom_max(MomArgs a, MomBatch bt) {
     using T = typename Elem<DT>::T;
+    const MomItem& it = bt.it[blockIdx.y];
     __shared__ float s_cbr[kCodebookMax];
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(a.qt->cbr + threadIdx.x);
     __syncthreads();
-    const T* g = static_cast<const T*>(a.g);
-    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
+    const T* g = static_cast<const T*>(it.g);
+    const bool dense = it.gs1 == 1 && it.gs0 == a.C;
+    uint32_t* mb = it.magbits + ((int64_t)blockIdx.x % it.shards) * it.nb;
     const int64_t stride = (int64_t)gridDim.x * kT;
     int64_t cur = -1;
     uint32_t cbits = 0u;
     float mo = 0.0f;
     for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < a.N; e += stride) {
-        const int64_t b = div_floor(e, a.P, a.invP);
+        const int64_t b = div_floor(e, it.P, it.invP);
         if (b != cur) {
-            if (cur >= 0 && cbits) atomicMax(mb + cur, cbits);
+            if (cur >= 0 && cbits) gatomic_max(mb + cur, cbits);
             cur = b;
             cbits = 0u;
-            mo = *gbl(a.mag + b);
+            mo = *gbl(it.mag + b);
         }
-        const float gv = to_f32<DT>(*gbl(g + e));
-        const float u = mom_u<DT>(s_cbr[*gbl(a.idx + e)], mo, gv, a.w);
+        const int64_t ge = dense ? e : view_offset(e, a.C, a.invC, it.gs0, it.gs1);
+        const float gv = to_f32<DT>(*gbl(g + ge));
+        const float u = mom_u<DT>(s_cbr[*gbl(it.idx + e)], mo, gv, a.w);
         const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;  // ordered: NaN > inf > finite
         cbits = ub > cbits ? ub : cbits;
     }
-    if (cur >= 0 && cbits) atomicMax(mb + cur, cbits);
+    if (cur >= 0 && cbits) gatomic_max(mb + cur, cbits);
 }
 
-__global__ void __launch_bounds__(kT) k_mom_finalize(MomArgs a) {
-    for (int64_t b = (int64_t)blockIdx.x * kT + threadIdx.x; b < a.nb; b += (int64_t)gridDim.x * kT) {
-        a.mag_old[b] = a.mag[b];
+__global__ void __launch_bounds__(kT) k_mom_finalize(MomBatch bt) {
+    const MomItem& it = bt.it[blockIdx.y];
+    for (int64_t b = (int64_t)blockIdx.x * kT + threadIdx.x; b < it.nb; b += (int64_t)gridDim.x * kT) {
+        it.mag_old[b] = it.mag[b];
         uint32_t bits = 0u;
-        for (int64_t sh = 0; sh < a.shards; ++sh) {
-            const uint32_t v = a.magbits[sh * a.nb + b];
+        for (int64_t sh = 0; sh < it.shards; ++sh) {
+            const uint32_t v = it.magbits[sh * it.nb + b];
             bits = v > bits ? v : bits;
-            a.magbits[sh * a.nb + b] = 0u;
+            it.magbits[sh * it.nb + b] = 0u;
         }
         const float m = __uint_as_float(bits);
-        a.mag[b] = m;
-        a.minv[b] = block_recip(m < kTiny ? kTiny : m);
+        it.mag[b] = m;
+        it.minv[b] = block_recip(m < kTiny ? kTiny : m);
     }
 }
 
+// Requantise one element: x = D(u / m_new) (0 when the block is all zero,
+// NaN when its magnitude is), then the nearest or stochastic codeword.
 template <int DT>
-__global__ void __launch_bounds__(kT) k_mom_emit(MomArgs a) {
+__device__ __forceinline__ float mom_x(float u, float m_new, float y) {
+    float x = 0.0f;
+    if (m_new > 0.0f) x = round_dt<DT>(div_by_block(u, m_new < kTiny ? kTiny : m_new, y));
+    else if (m_new != m_new) x = u / m_new;  // NaN magnitude: NaN (masked_fill only zeroes mag <= 0)
+    return x;
+}
+
+// Dense momentum of codeword ni: D(D(c) * m_new), Nesterov D(fma(alpha, g, D(o * beta))).
+template <int DT>
+__device__ __forceinline__ float mom_out(float cr, float m_new, float gv, const MomArgs& a) {
+    float o = round_dt<DT>(cr * m_new);
+    if (a.nesterov) o = round_dt<DT>(__builtin_fmaf(a.alpha_d, gv, round_dt<DT>(o * a.beta)));
+    return o;
+}
+
+template <int DT, bool SR>
+__global__ void __launch_bounds__(kT) k_mom_emit(MomArgs a, MomBatch bt) {
     using T = typename Elem<DT>::T;
+    const MomItem& it = bt.it[blockIdx.y];
     __shared__ float s_cbr[kCodebookMax];
     __shared__ float s_cb[kCodebookMax];
-    __shared__ int16_t s_lut[kLutEntries + 7];
+    __shared__ int16_t s_lut[SR ? kLutEntries + 7 : 1];
     const QTable* qt = a.qt;
     for (int i = threadIdx.x; i < kCodebookMax; i += kT) {
         s_cbr[i] = *gbl(qt->cbr + i);
         s_cb[i] = *gbl(qt->cb + i);
     }
-    if (a.sr)
+    if constexpr (SR)
         for (int i = threadIdx.x; i < kLutEntries + 7; i += kT) s_lut[i] = *gbl(qt->lut + i);
     __syncthreads();
     uint64_t seed = a.seed;
-    if (a.sr && a.seed_dev != nullptr) seed = (uint64_t)*gbl(a.seed_dev);
+    if (SR && a.seed_dev != nullptr) seed = (uint64_t)*gbl(a.seed_dev);
     const int k = qt->k;
     const uint32_t kmax = (uint32_t)(k - 1);
-    const T* g = static_cast<const T*>(a.g);
-    T* out = static_cast<T*>(a.out);
+    const T* g = static_cast<const T*>(it.g);
+    const bool dense = it.gs1 == 1 && it.gs0 == a.C;
+    T* out = static_cast<T*>(a.out) + (int64_t)blockIdx.y * a.N;
     const int64_t stride = (int64_t)gridDim.x * kT;
     for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < a.N; e += stride) {
-        const int64_t b = div_floor(e, a.P, a.invP);
-        const float m_old = *gbl(a.mag_old + b);
-        const float m_new = *gbl(a.mag + b);
-        const float y = *gbl(a.minv + b);
-        const float gv = to_f32<DT>(*gbl(g + e));
-        const float u = mom_u<DT>(s_cbr[*gbl(a.idx + e)], m_old, gv, a.w);
-        float x = 0.0f;
-        if (m_new > 0.0f) {
-            const float den = m_new < kTiny ? kTiny : m_new;
-            x = round_dt<DT>(div_by_block(u, den, y));
-        } else if (m_new != m_new) {
-            x = u / m_new;  // NaN magnitude: NaN (masked_fill only zeroes mag <= 0)
-        }
+        const int64_t b = div_floor(e, it.P, it.invP);
+        const float m_old = *gbl(it.mag_old + b);
+        const float m_new = *gbl(it.mag + b);
+        const float y = *gbl(it.minv + b);
+        const int64_t ge = dense ? e : view_offset(e, a.C, a.invC, it.gs0, it.gs1);
+        const float gv = to_f32<DT>(*gbl(g + ge));
+        const float u = mom_u<DT>(s_cbr[*gbl(it.idx + e)], m_old, gv, a.w);
+        const float x = mom_x<DT>(u, m_new, y);
         uint32_t ni;
-        if (a.sr) ni = quant_stochastic(x, s_cb, s_lut, k, seed, e);
+        if constexpr (SR) ni = quant_stochastic(x, s_cb, s_lut, k, seed, e);
         else ni = quant_nearest(x, qt->bucket, qt->thr, kmax);
-        *gbl(a.idx + e) = (uint8_t)ni;
-        float o = round_dt<DT>(s_cbr[ni] * m_new);
-        if (a.nesterov) o = round_dt<DT>(__builtin_fmaf(a.alpha_d, gv, round_dt<DT>(o * a.beta)));
-        *gbl(out + e) = from_f32<DT>(o);
+        *gbl(it.idx + e) = (uint8_t)ni;
+        *gbl(out + e) = from_f32<DT>(mom_out<DT>(s_cbr[ni], m_new, gv, a));
     }
 }
 
 // ---------------------------------------------------- fast momentum path
-// P % 8 == 0, N % 8 == 0, 16-byte aligned grad / momentum, 8-byte aligned
-// indices: 8-element chunks never cross a block.  Workgroup w owns chunks
-// [w * 256 * kMomCpt, ...); thread t takes chunks t, t + 256, ... so a wave
-// covers 512 consecutive elements per iteration.
+// Contiguous grad, P % 8 == 0, N % 8 == 0, 16-byte aligned grad / momentum,
+// 8-byte aligned indices: 8-element chunks never cross a block.  Workgroup w
+// of a matrix owns chunks [w * 256 * kMomCpt, ...); thread t takes chunks t,
+// t + 256, ... so a wave covers 512 consecutive elements per step.  Every
+// chunk's loads are issued before the first chunk's math.
 constexpr int kChunk = 8;
 constexpr int kMomCpt = 8;
 
@@ -182,17 +223,16 @@ __device__ __forceinline__ BlkPos blk_advance(BlkPos q, int64_t dB, int64_t dP, 
 }
 
 template <int DT>
-__global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a) {
+__global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a, MomBatch bt) {
     using T = typename Elem<DT>::T;
+    const MomItem& it = bt.it[blockIdx.y];
     __shared__ float s_cbr[kCodebookMax];
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(a.qt->cbr + threadIdx.x);
-    __syncthreads();
-    const T* g = static_cast<const T*>(a.g);
-    const uint8_t* idxp = a.idx;
-    const float* mag = a.mag;
+    const T* g = static_cast<const T*>(it.g);
+    const uint8_t* idxp = it.idx;
     const float w = a.w;
-    const int64_t P = a.P;
-    uint32_t* mb = a.magbits + ((int64_t)blockIdx.x % a.shards) * a.nb;
+    const int64_t P = it.P;
+    uint32_t* mb = it.magbits + ((int64_t)blockIdx.x % it.shards) * it.nb;
     const int64_t nch = a.N / kChunk;
     const int64_t first = (int64_t)blockIdx.x * (kT * kMomCpt) + threadIdx.x;
     const int64_t F = (int64_t)kT * kChunk;
@@ -200,35 +240,46 @@ __global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a) {
     BlkPos pos;
     {
         const int64_t e0 = first * kChunk;
-        pos.blk = div_floor(e0, P, a.invP);
+        pos.blk = div_floor(e0, P, it.invP);
         pos.pin = e0 - pos.blk * P;
     }
-    int64_t wblk = -1;   // wave-uniform running block
-    uint32_t wbits = 0u;
-#pragma unroll 1
+    Raw8<DT> gr[kMomCpt];
+    RawIdx8 ir[kMomCpt];
+    float mo[kMomCpt];
+    int64_t blk[kMomCpt];
+#pragma unroll
     for (int i = 0; i < kMomCpt; ++i) {
         const int64_t ch = first + (int64_t)i * kT;
-        const bool valid = ch < nch;
+        blk[i] = pos.blk;
+        if (ch < nch) {
+            load_raw8<DT>(g + ch * kChunk, gr[i]);
+            ir[i] = load_raw_idx8(idxp + ch * kChunk);
+            mo[i] = *gbl(it.mag + pos.blk);
+        }
+        pos = blk_advance(pos, dB, dP, P);
+    }
+    __syncthreads();  // s_cbr
+    int64_t wblk = -1;   // wave-uniform running block
+    uint32_t wbits = 0u;
+#pragma unroll
+    for (int i = 0; i < kMomCpt; ++i) {
+        const bool valid = first + (int64_t)i * kT < nch;
         uint32_t m = 0u;
         if (valid) {
-            Raw8<DT> gr;
-            load_raw8<DT>(g + ch * kChunk, gr);
-            const RawIdx8 ir = load_raw_idx8(idxp + ch * kChunk);
-            const float mo = *gbl(mag + pos.blk);
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                const float u = mom_u<DT>(s_cbr[raw_idx(ir, k)], mo, raw_elem<DT>(gr, k), w);
+                const float u = mom_u<DT>(s_cbr[raw_idx(ir[i], k)], mo[i], raw_elem<DT>(gr[i], k), w);
                 const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
                 m = ub > m ? ub : m;
             }
         }
         // lane 0 holds the wave's lowest chunk, valid whenever any lane is
-        const int64_t b0 = __shfl(pos.blk, 0, 64);
-        if (__all(!valid || pos.blk == b0)) {
+        const int64_t b0 = __shfl(blk[i], 0, 64);
+        if (__all(!valid || blk[i] == b0)) {
             if (b0 != wblk) {
                 if (wblk >= 0) {
                     const uint32_t r = wave_max_u63(wbits);
-                    if ((threadIdx.x & 63) == 63 && r) atomicMax(mb + wblk, r);
+                    if ((threadIdx.x & 63) == 63 && r) gatomic_max(mb + wblk, r);
                 }
                 wblk = b0;
                 wbits = 0u;
@@ -237,28 +288,58 @@ __global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a) {
         } else {
             if (wblk >= 0) {
                 const uint32_t r = wave_max_u63(wbits);
-                if ((threadIdx.x & 63) == 63 && r) atomicMax(mb + wblk, r);
+                if ((threadIdx.x & 63) == 63 && r) gatomic_max(mb + wblk, r);
             }
             wblk = -1;
             wbits = 0u;
-            if (valid && m) atomicMax(mb + pos.blk, m);
+            if (valid && m) gatomic_max(mb + blk[i], m);
         }
-        pos = blk_advance(pos, dB, dP, P);
     }
     if (wblk >= 0) {
         const uint32_t r = wave_max_u63(wbits);
-        if ((threadIdx.x & 63) == 63 && r) atomicMax(mb + wblk, r);
+        if ((threadIdx.x & 63) == 63 && r) gatomic_max(mb + wblk, r);
     }
 }
 
 template <int DT, bool SR>
-__global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a) {
+__global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
     using T = typename Elem<DT>::T;
+    const MomItem& it = bt.it[blockIdx.y];
     __shared__ uint2 s_fq[SR ? 1 : kFqEntries];
     __shared__ float s_cbr[kCodebookMax];
     __shared__ float s_cb[SR ? kCodebookMax : 1];
     __shared__ int16_t s_lut[SR ? kLutEntries + 7 : 1];
     const QTable* qt = a.qt;
+    const T* g = static_cast<const T*>(it.g);
+    T* out = static_cast<T*>(a.out) + (int64_t)blockIdx.y * a.N;
+    uint8_t* idxp = it.idx;
+    const int64_t P = it.P;
+    const int64_t nch = a.N / kChunk;
+    const int64_t first = (int64_t)blockIdx.x * (kT * kMomCpt) + threadIdx.x;
+    const int64_t F = (int64_t)kT * kChunk;
+    const int64_t dB = F / P, dP = F - (F / P) * P;
+    BlkPos pos;
+    {
+        const int64_t e0 = first * kChunk;
+        pos.blk = div_floor(e0, P, it.invP);
+        pos.pin = e0 - pos.blk * P;
+    }
+    // this thread's chunks: loads first, then the tables into LDS
+    Raw8<DT> gr[kMomCpt];
+    RawIdx8 ir[kMomCpt];
+    float mold[kMomCpt], mnew[kMomCpt], yv[kMomCpt];
+#pragma unroll
+    for (int i = 0; i < kMomCpt; ++i) {
+        const int64_t ch = first + (int64_t)i * kT;
+        if (ch < nch) {
+            mold[i] = *gbl(it.mag_old + pos.blk);
+            mnew[i] = *gbl(it.mag + pos.blk);
+            yv[i] = *gbl(it.minv + pos.blk);
+            load_raw8<DT>(g + ch * kChunk, gr[i]);
+            ir[i] = load_raw_idx8(idxp + ch * kChunk);
+        }
+        pos = blk_advance(pos, dB, dP, P);
+    }
     if constexpr (SR) {
         for (int i = threadIdx.x; i < kLutEntries + 7; i += kT) s_lut[i] = *gbl(qt->lut + i);
         if (threadIdx.x < kCodebookMax) s_cb[threadIdx.x] = *gbl(qt->cb + threadIdx.x);
@@ -272,44 +353,19 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a) {
     if (SR && a.seed_dev != nullptr) seed = (uint64_t)*gbl(a.seed_dev);
     const bool fastq = qt->max_cnt <= 1;
     const uint32_t kmax = (uint32_t)(qt->k - 1);
-    const T* g = static_cast<const T*>(a.g);
-    T* out = static_cast<T*>(a.out);
-    uint8_t* idxp = a.idx;
-    const float w = a.w, beta = a.beta, alpha_d = a.alpha_d;
-    const bool nest = a.nesterov != 0;
-    const int64_t P = a.P;
-    const int64_t nch = a.N / kChunk;
-    const int64_t first = (int64_t)blockIdx.x * (kT * kMomCpt) + threadIdx.x;
-    const int64_t F = (int64_t)kT * kChunk;
-    const int64_t dB = F / P, dP = F - (F / P) * P;
-    if (first >= nch) return;
-    BlkPos pos;
-    {
-        const int64_t e0 = first * kChunk;
-        pos.blk = div_floor(e0, P, a.invP);
-        pos.pin = e0 - pos.blk * P;
-    }
-#pragma unroll 1
+    const float w = a.w;
+#pragma unroll
     for (int i = 0; i < kMomCpt; ++i) {
         const int64_t ch = first + (int64_t)i * kT;
         if (ch >= nch) break;
         const int64_t e0 = ch * kChunk;
-        const float m_old = *gbl(a.mag_old + pos.blk);
-        const float m_new = *gbl(a.mag + pos.blk);
-        const float y = *gbl(a.minv + pos.blk);
-        Raw8<DT> gr;
-        load_raw8<DT>(g + e0, gr);
-        const RawIdx8 ir = load_raw_idx8(idxp + e0);
-        const float den = m_new < kTiny ? kTiny : m_new;
         uint32_t ix[kChunk];
         float o[kChunk];
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
-            const float gv = raw_elem<DT>(gr, k);
-            const float u = mom_u<DT>(s_cbr[raw_idx(ir, k)], m_old, gv, w);
-            float x = 0.0f;
-            if (m_new > 0.0f) x = round_dt<DT>(div_by_block(u, den, y));
-            else if (m_new != m_new) x = u / m_new;
+            const float gv = raw_elem<DT>(gr[i], k);
+            const float u = mom_u<DT>(s_cbr[raw_idx(ir[i], k)], mold[i], gv, w);
+            const float x = mom_x<DT>(u, mnew[i], yv[i]);
             uint32_t ni;
             if constexpr (SR) {
                 ni = quant_stochastic(x, s_cb, s_lut, qt->k, seed, e0 + k);
@@ -322,13 +378,10 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a) {
                 ni = quant_nearest(x, qt->bucket, qt->thr, kmax);
             }
             ix[k] = ni;
-            float v = round_dt<DT>(s_cbr[ni] * m_new);
-            if (nest) v = round_dt<DT>(__builtin_fmaf(alpha_d, gv, round_dt<DT>(v * beta)));
-            o[k] = v;
+            o[k] = mom_out<DT>(s_cbr[ni], mnew[i], gv, a);
         }
         store_idx8(idxp + e0, ix);
         store8<DT>(out + e0, o);
-        pos = blk_advance(pos, dB, dP, P);
     }
 }
 
@@ -345,7 +398,7 @@ struct GemmArgs {
     const uint16_t* A; int64_t lda, sA;   // sA: elements between batch items
     const uint16_t* B; int64_t ldb, sB;
     const uint16_t* C; int64_t ldc, sC;   // epilogue input (nullptr: none)
-    uint16_t* D; int64_t ldd, sD;
+    uint16_t* D; int64_t ldd, sD;        // nullptr: only the transposed copy is stored
     uint16_t* Dt; int64_t lddt, sDt;      // transposed copy of D (nullptr: none)
     int64_t M, N, K;
     float alpha, beta;
@@ -417,7 +470,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16 (&
     constexpr int kVecD = 64 * BN / 8 / kT;  // D vectors per thread and slab
     const int64_t bz = blockIdx.z;
     const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
-    uint16_t* D = g.D + bz * g.sD;
+    uint16_t* D = g.D ? g.D + bz * g.sD : nullptr;
     uint16_t* Dt = (g.Dt && !(g.tri && blockIdx.x == blockIdx.y)) ? g.Dt + bz * g.sDt : nullptr;
     const int tid = threadIdx.x;
 #pragma unroll
@@ -467,6 +520,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16 (&
                 hv[e] = f2bf(x[e]);
                 sOut[row * kOutPitch + c8 + e] = bf16f(hv[e]);
             }
+            if (D == nullptr) continue;
             uint16_t* dp = D + gr * g.ldd + gc;
             if (full && (reinterpret_cast<uintptr_t>(dp) & 15) == 0) {
                 const u32x4 dv = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16),
@@ -851,52 +905,33 @@ static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
 // ==================================================================
 // Newton-Schulz driver kernels
 // ==================================================================
-// X (m x n) and Xt (n x m) from the input [R x C] of any grad dtype, values
-// rounded to bf16 (Tensor.bfloat16()); tall inputs (R > C) are transposed:
-// m = min(R, C), n = max(R, C).  The input's own layout goes to X (wide) or
-// Xt (tall) directly, the transposed layout through a 64 x 64 LDS tile, so
-// every global access is coalesced.  grid (ceil(C/64), ceil(R/64), batch).
-template <int DT>
-__global__ void __launch_bounds__(kT) k_ns_load(const void* in, int64_t R, int64_t Cc, int64_t s_in,
-                                                uint16_t* X, uint16_t* Xt, int64_t sX) {
+// Partial sums of squares (float64) of bf16(in), one per workgroup: the
+// Frobenius norm of X = in.bfloat16() read straight from the input.
+// grid (kParts, batch).  VEC: N % 8 == 0 and the input 16-byte aligned.
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kT) k_ns_sumsq(const void* in, int64_t N, double* part) {
     using T = typename Elem<DT>::T;
-    __shared__ uint16_t tile[64][65];
-    const int64_t bz = blockIdx.z;
-    const T* src = static_cast<const T*>(in) + bz * s_in;
-    const bool tall = R > Cc;
-    uint16_t* same = (tall ? Xt : X) + bz * sX;   // [R x C]
-    uint16_t* trans = (tall ? X : Xt) + bz * sX;  // [C x R]
-    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int id = threadIdx.x + i * kT;
-        const int row = id >> 6, col = id & 63;
-        const int64_t r = r0 + row, c = c0 + col;
-        if (r < R && c < Cc) {
-            const uint16_t h = f2bf(to_f32<DT>(*gbl(src + r * Cc + c)));
-            *gbl(same + r * Cc + c) = h;
-            tile[row][col] = h;
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int id = threadIdx.x + i * kT;
-        const int crow = id >> 6, rcol = id & 63;  // output row = input column
-        const int64_t c = c0 + crow, r = r0 + rcol;
-        if (r < R && c < Cc) *gbl(trans + c * R + r) = tile[rcol][crow];
-    }
-}
-
-// Partial sums of squares of X (float64), one per workgroup.
-__global__ void __launch_bounds__(kT) k_ns_sumsq(const uint16_t* X, int64_t N, int64_t sX, double* part) {
     __shared__ double s_w[kT / 64];
     const int64_t bz = blockIdx.y;
-    const uint16_t* x = X + bz * sX;
+    const T* x = static_cast<const T*>(in) + bz * N;
     double acc = 0.0;
-    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
-        const float v = bf16f(*gbl(x + e));
-        acc += (double)(v * v);
+    if constexpr (VEC) {
+        const int64_t n8 = N / 8;
+#pragma unroll 2
+        for (int64_t c = (int64_t)blockIdx.x * kT + threadIdx.x; c < n8; c += (int64_t)gridDim.x * kT) {
+            Raw8<DT> r;
+            load_raw8<DT>(x + c * 8, r);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float v = bf16f(f2bf(raw_elem<DT>(r, k)));
+                acc += (double)(v * v);
+            }
+        }
+    } else {
+        for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
+            const float v = bf16f(f2bf(to_f32<DT>(*gbl(x + e))));
+            acc += (double)(v * v);
+        }
     }
     acc = wave_sum_d(acc);
     if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = acc;
@@ -918,19 +953,80 @@ __global__ void k_ns_norm(const double* part, int nparts, int64_t batch, float e
     den[bz] = nb < eps ? bf16f(f2bf(eps)) : nb;
 }
 
-// X <- bf16(X / den) and Xt likewise.
-__global__ void __launch_bounds__(kT) k_ns_scale(uint16_t* X, uint16_t* Xt, int64_t N, int64_t sX, const float* den) {
-    const int64_t bz = blockIdx.y;
-    const float d = den[bz];
-    uint16_t* x = X + bz * sX;
-    uint16_t* xt = Xt + bz * sX;
-    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
-        *gbl(x + e) = f2bf(bf16f(*gbl(x + e)) / d);
-        *gbl(xt + e) = f2bf(bf16f(*gbl(xt + e)) / d);
+// X (m x n) and Xt (n x m) from the input [R x C] of any grad dtype:
+// bf16(bf16(in) / den), tall inputs (R > C) transposed (m = min(R, C),
+// n = max(R, C)).  A workgroup moves one 64 x 64 tile: rows of 8 elements
+// from the input to the same-layout output (16-byte stores), and through LDS
+// (pitch 66 bf16, so the column reads below spread over the banks) to the
+// transposed output, whose rows leave as 8-row 16-byte vectors, 8 lanes per
+// 128-byte row segment.  grid (ceil(C/64), ceil(R/64), batch).  VEC: C % 8
+// == 0 and the input, X and Xt 16-byte aligned (then every 8-element row
+// piece is in bounds or entirely out).
+constexpr int kTilePitch = 66;
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kT) k_ns_load(const void* in, int64_t R, int64_t Cc, uint16_t* X, uint16_t* Xt,
+                                                const float* den_p) {
+    using T = typename Elem<DT>::T;
+    __shared__ uint16_t tile[64 * kTilePitch];
+    const int64_t bz = blockIdx.z;
+    const int64_t N = R * Cc;
+    const T* src = static_cast<const T*>(in) + bz * N;
+    const bool tall = R > Cc;
+    uint16_t* same = (tall ? Xt : X) + bz * N;   // [R x C]
+    uint16_t* trans = (tall ? X : Xt) + bz * N;  // [C x R]
+    const float den = den_p[bz];
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int v = threadIdx.x + k * kT;
+        const int row = v >> 3, c8 = (v & 7) * 8;
+        const int64_t r = r0 + row, c = c0 + c8;
+        uint32_t h[8];
+        if (VEC && r < R && c < Cc) {
+            Raw8<DT> raw;
+            load_raw8<DT>(src + r * Cc + c, raw);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = f2bf(bf16f(f2bf(raw_elem<DT>(raw, e))) / den);
+            const u32x4 pk = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+            *gbl(reinterpret_cast<u32x4*>(same + r * Cc + c)) = pk;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                h[e] = 0u;
+                if (r < R && c + e < Cc) {
+                    h[e] = f2bf(bf16f(f2bf(to_f32<DT>(*gbl(src + r * Cc + c + e)))) / den);
+                    *gbl(same + r * Cc + c + e) = (uint16_t)h[e];
+                }
+            }
+        }
+        uint32_t* trow = reinterpret_cast<uint32_t*>(tile + row * kTilePitch + c8);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) trow[q] = h[2 * q] | (h[2 * q + 1] << 16);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int v = threadIdx.x + k * kT;
+        const int cc = v >> 3, r8 = (v & 7) * 8;  // output row (input column), first output column
+        const int64_t c = c0 + cc, r = r0 + r8;
+        if (c >= Cc) continue;
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = tile[(r8 + e) * kTilePitch + cc];
+        uint16_t* tp = trans + c * R + r;
+        if (VEC && r + 8 <= R && (R & 7) == 0) {
+            const u32x4 pk = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+            *gbl(reinterpret_cast<u32x4*>(tp)) = pk;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (r + e < R) *gbl(tp + e) = (uint16_t)h[e];
+        }
     }
 }
 
-// out [R x C] (bf16) from the final X / Xt.
+// out [R x C] (bf16) from the normalised X / Xt (a schedule of no steps).
 __global__ void __launch_bounds__(kT) k_ns_store(const uint16_t* src, int64_t N, int64_t sX, uint16_t* out, int64_t s_out) {
     const int64_t bz = blockIdx.y;
     for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT)
@@ -961,30 +1057,69 @@ struct NsWs {
 // ==================================================================
 // NorMuon and the Muon apply
 // ==================================================================
-// row_norm[r] = sqrt(sum_c u[r][c]^2) in fp32 from float64 partial sums
-// (torch.linalg.vector_norm(..., dtype=float32)); one wave per row.
+// The update stack U [n, R, C] (bf16, contiguous) from Newton-Schulz; matrix
+// i of a launch is blockIdx.y (row norms, apply) or blockIdx.x (NorMuon
+// scale).  Parameters may be strided views (logical row-major order).
+struct ApplyItem {
+    void* p;
+    int64_t ps0, ps1;       // parameter strides in elements
+    const float* scalars;   // capturable scalar row (fp32[4]) or nullptr
+    float* v;               // normuon_v [R]
+    const float* step_dev;  // capturable NorMuon step counter or nullptr
+    float bc;               // 1 - beta2^step (host step)
+};
+struct ApplyBatch {
+    ApplyItem it[kMaxBatch];
+};
+
+// row_norm[i][r] = sqrt(sum_c u[r][c]^2) in fp32 from float64 sums
+// (torch.linalg.vector_norm(..., dtype=float32)); one wave per row, 16-byte
+// loads when C % 8 == 0 and U is 16-byte aligned.
+template <bool VEC>
 __global__ void __launch_bounds__(kT) k_row_norm(const uint16_t* U, int64_t R, int64_t C, float* row_norm) {
     const int lane = threadIdx.x & 63;
     const int64_t r = (int64_t)blockIdx.x * (kT / 64) + (threadIdx.x >> 6);
+    const int64_t bz = blockIdx.y;
     if (r >= R) return;
+    const uint16_t* row = U + (bz * R + r) * C;
     double acc = 0.0;
-    for (int64_t c = lane; c < C; c += 64) {
-        const float v = bf16f(*gbl(U + r * C + c));
-        acc += (double)(v * v);
+    if constexpr (VEC) {
+#pragma unroll 4
+        for (int64_t c8 = lane; c8 < C / 8; c8 += 64) {
+            const u32x4 v = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(row + c8 * 8)));
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f = bf16f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+                acc += (double)(f * f);
+            }
+        }
+    } else {
+        for (int64_t c = lane; c < C; c += 64) {
+            const float v = bf16f(*gbl(row + c));
+            acc += (double)(v * v);
+        }
     }
     acc = wave_sum_d(acc);
-    if (lane == 0) row_norm[r] = (float)sqrt(acc);
+    if (lane == 0) row_norm[bz * R + r] = (float)sqrt(acc);
 }
 
 // v <- v*beta2 + row_sq * ((1-beta2)/C); denom = sqrt(v/bc) + eps;
 // frob_scale = sqrt(sum row_sq) / max(||row_norm / denom||, tiny);
-// scale[r] = bf16(frob_scale / denom[r]).  One workgroup.
-__global__ void __launch_bounds__(kT) k_normuon_scale(const float* row_norm, float* v, int64_t R, float beta2,
-                                                      float alpha, float bc, float eps, float* denom,
-                                                      uint16_t* scale, const float* step_dev, double beta2_d) {
+// scale[r] = bf16(frob_scale / denom[r]).  One workgroup per matrix.
+__global__ void __launch_bounds__(kT) k_normuon_scale(const float* row_norm, int64_t R, float beta2, float alpha,
+                                                      float eps, float* denom, uint16_t* scale, double beta2_d,
+                                                      ApplyBatch bt) {
+    const ApplyItem& it = bt.it[blockIdx.x];
     __shared__ double s_a[kT / 64], s_b[kT / 64];
+    const int64_t off = (int64_t)blockIdx.x * R;
+    row_norm += off;
+    denom += off;
+    scale += off;
+    float* v = it.v;
     // device step counter (capturable): the same float64 bias correction
-    if (step_dev != nullptr) bc = (float)(1.0 - pow(beta2_d, (double)*gbl(step_dev)));
+    float bc = it.bc;
+    if (it.step_dev != nullptr) bc = (float)(1.0 - pow(beta2_d, (double)*gbl(it.step_dev)));
     double sa = 0.0, sb = 0.0;
     for (int64_t r = threadIdx.x; r < R; r += kT) {
         const float rn = row_norm[r];
@@ -1010,25 +1145,79 @@ __global__ void __launch_bounds__(kT) k_normuon_scale(const float* row_norm, flo
     for (int64_t r = threadIdx.x; r < R; r += kT) scale[r] = f2bf(fs / denom[r]);
 }
 
-// p = D(p * wdf) (when wd); p = D(fma(u', alpha, p)), u' = bf16(u * scale[row])
-// when a NorMuon scale is given, else u.
+struct MuonApplyArgs {
+    const uint16_t* U;      // [n, R, C]
+    const uint16_t* scale;  // [n, R] NorMuon row scales, or nullptr
+    int64_t R, C;
+    double invC, lr_ratio;
+    float wdf, alpha;
+    int wd;
+};
+
+// One element: u' = bf16(u * scale[row]) with a NorMuon scale, else u;
+// p = D(p * wdf) (when wd), then p = D(fma(u', alpha, p)).
 template <int DT>
-__global__ void __launch_bounds__(kT) k_muon_apply(void* p, const uint16_t* U, const uint16_t* scale, int64_t R,
-                                                   int64_t C, float wdf, int wd, float alpha, const float* scalars,
-                                                   double lr_ratio) {
+__device__ __forceinline__ float muon_elem(float u, float sc, bool has_scale, float pv, float wdf, bool wd,
+                                           float alpha) {
+    if (has_scale) u = bf16f(f2bf(u * sc));
+    if (wd) pv = round_dt<DT>(pv * wdf);
+    return __builtin_fmaf(u, alpha, pv);
+}
+
+// FAST: contiguous 16-byte aligned parameter, C % 8 == 0: each thread takes
+// kApplyCpt chunks of 8 elements (one row each), all loads first.  Else any
+// strides, one element at a time.
+constexpr int kApplyCpt = 4;
+
+template <int DT, bool FAST>
+__global__ void __launch_bounds__(kT) k_muon_apply(MuonApplyArgs a, ApplyBatch bt) {
     using T = typename Elem<DT>::T;
-    T* pp = static_cast<T*>(p);
-    if (scalars != nullptr) {  // capturable: lr and 1 - lr*wd from the device scalar row
-        wdf = *gbl(scalars + 3);
-        alpha = round_dt<DT>((float)(-((double)*gbl(scalars) * lr_ratio)));
+    const ApplyItem& it = bt.it[blockIdx.y];
+    T* pp = static_cast<T*>(it.p);
+    float wdf = a.wdf, alpha = a.alpha;
+    if (it.scalars != nullptr) {  // capturable: lr and 1 - lr*wd from the device scalar row
+        wdf = *gbl(it.scalars + 3);
+        alpha = round_dt<DT>((float)(-((double)*gbl(it.scalars) * a.lr_ratio)));
     }
-    const int64_t N = R * C;
-    for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
-        float u = bf16f(*gbl(U + e));
-        if (scale != nullptr) u = bf16f(f2bf(u * bf16f(*gbl(scale + e / C))));
-        float pv = to_f32<DT>(*gbl(pp + e));
-        if (wd) pv = round_dt<DT>(pv * wdf);
-        *gbl(pp + e) = from_f32<DT>(__builtin_fmaf(u, alpha, pv));
+    const bool wd = a.wd != 0, has_scale = a.scale != nullptr;
+    const int64_t N = a.R * a.C;
+    const uint16_t* U = a.U + (int64_t)blockIdx.y * N;
+    const uint16_t* S = has_scale ? a.scale + (int64_t)blockIdx.y * a.R : nullptr;
+    if constexpr (FAST) {
+        const int64_t nch = N / 8;
+        const int64_t first = (int64_t)blockIdx.x * (kT * kApplyCpt) + threadIdx.x;
+        u32x4 uv[kApplyCpt];
+        Raw8<DT> pr[kApplyCpt];
+        float sc[kApplyCpt];
+#pragma unroll
+        for (int i = 0; i < kApplyCpt; ++i) {
+            const int64_t ch = first + (int64_t)i * kT;
+            if (ch < nch) {
+                uv[i] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(U + ch * 8)));
+                load_raw8<DT>(pp + ch * 8, pr[i]);
+                sc[i] = has_scale ? bf16f(*gbl(S + div_floor(ch * 8, a.C, a.invC))) : 1.0f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kApplyCpt; ++i) {
+            const int64_t ch = first + (int64_t)i * kT;
+            if (ch >= nch) break;
+            const uint32_t w[4] = {uv[i].x, uv[i].y, uv[i].z, uv[i].w};
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                o[e] = muon_elem<DT>(bf16f((uint16_t)(w[e >> 1] >> (16 * (e & 1)))), sc[i], has_scale,
+                                     raw_elem<DT>(pr[i], e), wdf, wd, alpha);
+            store8<DT>(pp + ch * 8, o);
+        }
+    } else {
+        for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
+            const int64_t r = div_floor(e, a.C, a.invC);
+            T* q = pp + r * it.ps0 + (e - r * a.C) * it.ps1;
+            const float o = muon_elem<DT>(bf16f(*gbl(U + e)), has_scale ? bf16f(*gbl(S + r)) : 1.0f, has_scale,
+                                          to_f32<DT>(*gbl(q)), wdf, wd, alpha);
+            *gbl(q) = from_f32<DT>(o);
+        }
     }
 }
 
@@ -1040,6 +1229,234 @@ static int check_dt(int dtype, const char* fn) {
     if (dtype == F64) return set_error(GEFENX_EDTYPE, "%s: not implemented for 'Double'", fn);
     if (dtype != F32 && dtype != F16 && dtype != BF16) return set_error(GEFENX_EINVAL, "%s: unknown dtype %d", fn, dtype);
     return GEFENX_OK;
+}
+
+// ------------------------------------------------------------ host side
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// One launch set (block max, finalize, requantise + emit) for n matrices of
+// one kind: FAST (the chunked kernels; every item qualifies) or general.
+static void mom_launch(const MomArgs& a, const MomBatch& bt, int n, int dtype, bool fast, bool sr, hipStream_t s) {
+    int64_t max_nb = 1;
+    for (int i = 0; i < n; ++i) max_nb = std::max(max_nb, bt.it[i].nb);
+    const dim3 gfin(grid_for(max_nb, 4096), (unsigned)n);
+    if (fast) {
+        const dim3 gf((unsigned)cdiv(a.N / kChunk, (int64_t)kT * kMomCpt), (unsigned)n);
+        switch (dtype) {
+            case F32: hipLaunchKernelGGL(k_mom_max_fast<F32>, gf, dim3(kT), 0, s, a, bt); break;
+            case F16: hipLaunchKernelGGL(k_mom_max_fast<F16>, gf, dim3(kT), 0, s, a, bt); break;
+            default: hipLaunchKernelGGL(k_mom_max_fast<BF16>, gf, dim3(kT), 0, s, a, bt); break;
+        }
+        hipLaunchKernelGGL(k_mom_finalize, gfin, dim3(kT), 0, s, bt);
+#define GX_EMIT_FAST(SRV)                                                                                  \
+    switch (dtype) {                                                                                       \
+        case F32: hipLaunchKernelGGL((k_mom_emit_fast<F32, SRV>), gf, dim3(kT), 0, s, a, bt); break;       \
+        case F16: hipLaunchKernelGGL((k_mom_emit_fast<F16, SRV>), gf, dim3(kT), 0, s, a, bt); break;       \
+        default: hipLaunchKernelGGL((k_mom_emit_fast<BF16, SRV>), gf, dim3(kT), 0, s, a, bt); break;       \
+    }
+        if (sr) { GX_EMIT_FAST(true) } else { GX_EMIT_FAST(false) }
+#undef GX_EMIT_FAST
+        return;
+    }
+    const dim3 g(grid_for(a.N, 16384), (unsigned)n);
+    switch (dtype) {
+        case F32: hipLaunchKernelGGL(k_mom_max<F32>, g, dim3(kT), 0, s, a, bt); break;
+        case F16: hipLaunchKernelGGL(k_mom_max<F16>, g, dim3(kT), 0, s, a, bt); break;
+        default: hipLaunchKernelGGL(k_mom_max<BF16>, g, dim3(kT), 0, s, a, bt); break;
+    }
+    hipLaunchKernelGGL(k_mom_finalize, gfin, dim3(kT), 0, s, bt);
+#define GX_EMIT(SRV)                                                                                       \
+    switch (dtype) {                                                                                       \
+        case F32: hipLaunchKernelGGL((k_mom_emit<F32, SRV>), g, dim3(kT), 0, s, a, bt); break;             \
+        case F16: hipLaunchKernelGGL((k_mom_emit<F16, SRV>), g, dim3(kT), 0, s, a, bt); break;             \
+        default: hipLaunchKernelGGL((k_mom_emit<BF16, SRV>), g, dim3(kT), 0, s, a, bt); break;             \
+    }
+    if (sr) { GX_EMIT(true) } else { GX_EMIT(false) }
+#undef GX_EMIT
+}
+
+// Validate one matrix of a momentum batch and describe it.
+static int mom_item(const char* fn, const gefenx_muon_item& in, int64_t rows, int64_t cols, MomItem& it) {
+    const int64_t numel = rows * cols;
+    if (in.period <= 0 || numel % in.period != 0)
+        return set_error(GEFENX_EINVAL, "%s: period %lld does not divide numel %lld", fn, (long long)in.period,
+                         (long long)numel);
+    if (!in.grad || !in.m_codebook || !in.m_magnitude || !in.workspace)
+        return set_error(GEFENX_EINVAL, "%s: null pointer argument", fn);
+    const int64_t nb = numel / in.period;
+    const MomentumWs L = MomentumWs::make(nb);
+    if (in.workspace_bytes < L.total)
+        return set_error(GEFENX_EINVAL, "%s: workspace %zu bytes < required %zu", fn, in.workspace_bytes, L.total);
+    char* ws = static_cast<char*>(in.workspace);
+    it.g = in.grad;
+    it.gs0 = in.grad_stride0;
+    it.gs1 = in.grad_stride1;
+    it.idx = in.m_codebook;
+    it.mag = in.m_magnitude;
+    it.magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
+    it.mag_old = reinterpret_cast<float*>(ws + L.off_magold);
+    it.minv = reinterpret_cast<float*>(ws + L.off_minv);
+    it.P = in.period;
+    it.nb = nb;
+    it.shards = mag_shards(nb);
+    it.invP = 1.0 / (double)in.period;
+    return GEFENX_OK;
+}
+
+// The momentum of n matrices [rows, cols]: runs of consecutive matrices of
+// one kind (chunked / general), at most kMaxBatch per launch set; matrix i
+// writes momentum_out + i * rows * cols.
+static int momentum_batch(const char* fn, const gefenx_muon_item* items, int n, int dtype, int64_t rows,
+                          int64_t cols, const void* qtable_dev, void* momentum_out, double beta1,
+                          int stochastic_round, int64_t rng_seed, const int64_t* seed_dev, int nesterov,
+                          hipStream_t s) {
+    int rc = check_dt(dtype, fn);
+    if (rc) return rc;
+    if (n < 0 || rows < 0 || cols < 0) return set_error(GEFENX_EINVAL, "%s: negative size", fn);
+    if (n == 0 || rows == 0 || cols == 0) return GEFENX_OK;
+    if (!items || !qtable_dev || !momentum_out) return set_error(GEFENX_EINVAL, "%s: null pointer argument", fn);
+    const int64_t numel = rows * cols;
+    if (cdiv(numel / kChunk, (int64_t)kT * kMomCpt) > 2147483647LL)
+        return set_error(GEFENX_EINVAL, "%s: %lld elements per matrix exceed the launch grid", fn, (long long)numel);
+    const size_t es = dtype == F32 ? 4 : 2;
+    std::vector<MomItem> its((size_t)n);
+    std::vector<char> fast((size_t)n);
+    for (int i = 0; i < n; ++i) {
+        rc = mom_item(fn, items[i], rows, cols, its[(size_t)i]);
+        if (rc) return rc;
+        const MomItem& it = its[(size_t)i];
+        fast[(size_t)i] = it.gs1 == 1 && it.gs0 == cols && it.P % kChunk == 0 && numel % kChunk == 0 &&
+                          al16(it.g) && (reinterpret_cast<uintptr_t>(it.idx) & 7) == 0 &&
+                          al16(static_cast<char*>(momentum_out) + (size_t)i * (size_t)numel * es);
+    }
+    MomArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.qt = static_cast<const QTable*>(qtable_dev);
+    a.seed_dev = seed_dev;
+    a.N = numel;
+    a.C = cols;
+    a.invC = 1.0 / (double)cols;
+    a.seed = (uint64_t)rng_seed;
+    a.w = (float)(1.0 - beta1);
+    a.beta = (float)beta1;
+    a.alpha_d = dtype == BF16 ? round_bf16(a.w) : dtype == F16 ? round_f16(a.w) : a.w;
+    a.nesterov = nesterov ? 1 : 0;
+    // algorithmic bytes: grad read, indices read + write, momentum written
+    int ph = prof_begin(GEFENX_K_MOMENTUM, (double)n * (double)numel * (2.0 * (double)es + 2.0), 0.0, s);
+    for (int i0 = 0; i0 < n;) {
+        int i1 = i0 + 1;
+        while (i1 < n && i1 - i0 < kMaxBatch && fast[(size_t)i1] == fast[(size_t)i0]) ++i1;
+        MomBatch bt;
+        std::memset(&bt, 0, sizeof(bt));
+        for (int i = i0; i < i1; ++i) bt.it[i - i0] = its[(size_t)i];
+        a.out = static_cast<char*>(momentum_out) + (size_t)i0 * (size_t)numel * es;
+        mom_launch(a, bt, i1 - i0, dtype, fast[(size_t)i0] != 0, stochastic_round != 0, s);
+        i0 = i1;
+    }
+    prof_end(ph, s);
+    return launch_check(fn);
+}
+
+static int normuon_batch(const char* fn, const gefenx_muon_item* items, int n, const void* update, int64_t rows,
+                         int64_t cols, double beta2, double eps, void* scale_out, void* workspace,
+                         size_t workspace_bytes, hipStream_t s) {
+    if (n < 0) return set_error(GEFENX_EINVAL, "%s: negative batch", fn);
+    if (n == 0 || rows <= 0 || cols <= 0) return GEFENX_OK;
+    if (!items || !update || !scale_out || !workspace) return set_error(GEFENX_EINVAL, "%s: bad argument", fn);
+    const size_t slab = align256(sizeof(float) * (size_t)n * (size_t)rows);
+    if (workspace_bytes < 2 * slab)
+        return set_error(GEFENX_EINVAL, "%s: workspace %zu bytes < required %zu", fn, workspace_bytes, 2 * slab);
+    if (cdiv(rows, kT / 64) > 2147483647LL) return set_error(GEFENX_EINVAL, "%s: too many rows", fn);
+    float* row_norm = static_cast<float*>(workspace);
+    float* denom = reinterpret_cast<float*>(static_cast<char*>(workspace) + slab);
+    const uint16_t* U = static_cast<const uint16_t*>(update);
+    const bool vec = cols % 8 == 0 && al16(U);
+    const float alpha = (float)((1.0 - beta2) / (double)cols);
+    for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
+        const int m = std::min(kMaxBatch, n - i0);
+        ApplyBatch bt;
+        std::memset(&bt, 0, sizeof(bt));
+        for (int i = 0; i < m; ++i) {
+            const gefenx_muon_item& in = items[i0 + i];
+            if (!in.normuon_v || (in.normuon_step < 1 && !in.normuon_step_dev))
+                return set_error(GEFENX_EINVAL, "%s: item %d has no NorMuon state or step", fn, i0 + i);
+            bt.it[i].v = in.normuon_v;
+            bt.it[i].step_dev = in.normuon_step_dev;
+            bt.it[i].bc = in.normuon_step_dev ? 1.0f : (float)(1.0 - std::pow(beta2, (double)in.normuon_step));
+        }
+        const uint16_t* Ui = U + (size_t)i0 * (size_t)rows * (size_t)cols;
+        float* rn = row_norm + (size_t)i0 * (size_t)rows;
+        const dim3 gr((unsigned)cdiv(rows, kT / 64), (unsigned)m);
+        if (vec) hipLaunchKernelGGL(k_row_norm<true>, gr, dim3(kT), 0, s, Ui, rows, cols, rn);
+        else hipLaunchKernelGGL(k_row_norm<false>, gr, dim3(kT), 0, s, Ui, rows, cols, rn);
+        hipLaunchKernelGGL(k_normuon_scale, dim3((unsigned)m), dim3(kT), 0, s, rn, rows, (float)beta2, alpha,
+                           (float)eps, denom + (size_t)i0 * (size_t)rows,
+                           static_cast<uint16_t*>(scale_out) + (size_t)i0 * (size_t)rows, beta2, bt);
+    }
+    return launch_check(fn);
+}
+
+static int apply_batch(const char* fn, const gefenx_muon_item* items, int n, int dtype, const void* update,
+                       const void* row_scale, int64_t rows, int64_t cols, double lr, double weight_decay,
+                       double adjusted_lr, double lr_ratio, hipStream_t s) {
+    int rc = check_dt(dtype, fn);
+    if (rc) return rc;
+    if (n < 0) return set_error(GEFENX_EINVAL, "%s: negative batch", fn);
+    if (n == 0 || rows <= 0 || cols <= 0) return GEFENX_OK;
+    if (!items || !update) return set_error(GEFENX_EINVAL, "%s: null pointer argument", fn);
+    const int64_t N = rows * cols;
+    MuonApplyArgs a;
+    a.R = rows;
+    a.C = cols;
+    a.invC = 1.0 / (double)cols;
+    a.lr_ratio = lr_ratio;
+    a.wdf = (float)(1.0 - lr * weight_decay);
+    a.wd = weight_decay > 0.0 ? 1 : 0;
+    float alpha = (float)(-adjusted_lr);
+    a.alpha = dtype == BF16 ? round_bf16(alpha) : dtype == F16 ? round_f16(alpha) : alpha;
+    const uint16_t* U = static_cast<const uint16_t*>(update);
+    const uint16_t* S = static_cast<const uint16_t*>(row_scale);
+    const int64_t fwgs = cdiv(N / 8, (int64_t)kT * kApplyCpt);
+    if (fwgs > 2147483647LL) return set_error(GEFENX_EINVAL, "%s: too large", fn);
+    std::vector<char> fast((size_t)n);
+    for (int i = 0; i < n; ++i) {
+        const gefenx_muon_item& in = items[i];
+        if (!in.param) return set_error(GEFENX_EINVAL, "%s: item %d has no parameter", fn, i);
+        fast[(size_t)i] = in.param_stride1 == 1 && in.param_stride0 == cols && cols % 8 == 0 && al16(in.param) &&
+                          al16(U + (size_t)i * (size_t)N);
+    }
+    for (int i0 = 0; i0 < n;) {
+        int i1 = i0 + 1;
+        while (i1 < n && i1 - i0 < kMaxBatch && fast[(size_t)i1] == fast[(size_t)i0]) ++i1;
+        ApplyBatch bt;
+        std::memset(&bt, 0, sizeof(bt));
+        for (int i = i0; i < i1; ++i) {
+            bt.it[i - i0].p = items[i].param;
+            bt.it[i - i0].ps0 = items[i].param_stride0;
+            bt.it[i - i0].ps1 = items[i].param_stride1;
+            bt.it[i - i0].scalars = items[i].step_scalars;
+        }
+        a.U = U + (size_t)i0 * (size_t)N;
+        a.scale = S ? S + (size_t)i0 * (size_t)rows : nullptr;
+        const unsigned m = (unsigned)(i1 - i0);
+        if (fast[(size_t)i0]) {
+            const dim3 g((unsigned)fwgs, m);
+            switch (dtype) {
+                case F32: hipLaunchKernelGGL((k_muon_apply<F32, true>), g, dim3(kT), 0, s, a, bt); break;
+                case F16: hipLaunchKernelGGL((k_muon_apply<F16, true>), g, dim3(kT), 0, s, a, bt); break;
+                default: hipLaunchKernelGGL((k_muon_apply<BF16, true>), g, dim3(kT), 0, s, a, bt); break;
+            }
+        } else {
+            const dim3 g(grid_for(N, 16384), m);
+            switch (dtype) {
+                case F32: hipLaunchKernelGGL((k_muon_apply<F32, false>), g, dim3(kT), 0, s, a, bt); break;
+                case F16: hipLaunchKernelGGL((k_muon_apply<F16, false>), g, dim3(kT), 0, s, a, bt); break;
+                default: hipLaunchKernelGGL((k_muon_apply<BF16, false>), g, dim3(kT), 0, s, a, bt); break;
+            }
+        }
+        i0 = i1;
+    }
+    return launch_check(fn);
 }
 
 }  // namespace muon
@@ -1055,79 +1472,30 @@ int gefenx_quantized_momentum_update(const void* grad, int dtype, int64_t numel,
                                      void* momentum_out, double beta1, int stochastic_round, int64_t rng_seed,
                                      const int64_t* seed_dev, int nesterov, void* workspace,
                                      size_t workspace_bytes, void* stream) {
-    int rc = check_dt(dtype, "gefenx_quantized_momentum_update");
+    const char* fn = "gefenx_quantized_momentum_update";
+    int rc = check_dt(dtype, fn);
     if (rc) return rc;
-    if (numel < 0) return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: negative numel");
+    if (numel < 0) return set_error(GEFENX_EINVAL, "%s: negative numel", fn);
     if (numel == 0) return GEFENX_OK;
-    if (period <= 0 || numel % period != 0)
-        return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: period %lld does not divide numel %lld",
-                         (long long)period, (long long)numel);
-    if (!grad || !m_codebook || !m_magnitude || !qtable_dev || !momentum_out || !workspace)
-        return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: null pointer argument");
-    const int64_t nb = numel / period;
-    const MomentumWs L = MomentumWs::make(nb);
-    if (workspace_bytes < L.total)
-        return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: workspace %zu bytes < required %zu",
-                         workspace_bytes, L.total);
-    char* ws = static_cast<char*>(workspace);
-    MomArgs a;
-    std::memset(&a, 0, sizeof(a));
-    a.g = grad; a.idx = m_codebook; a.mag = m_magnitude; a.out = momentum_out;
-    a.magbits = reinterpret_cast<uint32_t*>(ws + L.off_magbits);
-    a.mag_old = reinterpret_cast<float*>(ws + L.off_magold);
-    a.minv = reinterpret_cast<float*>(ws + L.off_minv);
-    a.qt = static_cast<const QTable*>(qtable_dev);
-    a.seed_dev = seed_dev;
-    a.N = numel; a.P = period; a.nb = nb; a.shards = mag_shards(nb); a.invP = 1.0 / (double)period;
-    a.seed = (uint64_t)rng_seed;
-    a.w = (float)(1.0 - beta1);
-    a.beta = (float)beta1;
-    a.alpha_d = dtype == BF16 ? round_bf16(a.w) : dtype == F16 ? round_f16(a.w) : a.w;
-    a.nesterov = nesterov ? 1 : 0;
-    a.sr = stochastic_round ? 1 : 0;
-    a.dtype = dtype;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const unsigned grid = grid_for(numel, 16384);
-    const auto al = [](const void* ptr, size_t n) { return (reinterpret_cast<uintptr_t>(ptr) % n) == 0; };
-    const bool fast = period % kChunk == 0 && al(grad, 16) && al(momentum_out, 16) && al(m_codebook, 8);
-    const int64_t fwgs = cdiv(numel / kChunk, (int64_t)kT * kMomCpt);
-    if (fast && fwgs > 2147483647LL) return set_error(GEFENX_EINVAL, "gefenx_quantized_momentum_update: too large");
-    // algorithmic bytes: grad read, indices read + write, momentum written
-    const double es = dtype == F32 ? 4.0 : 2.0;
-    int ph = prof_begin(GEFENX_K_MOMENTUM, (double)numel * (2.0 * es + 2.0), 0.0, s);
-#define GX_MOM(KFAST, KSLOW)                                                                             \
-    switch (dtype) {                                                                                     \
-        case F32: if (fast) hipLaunchKernelGGL(KFAST<F32>, dim3((unsigned)fwgs), dim3(kT), 0, s, a);     \
-                  else hipLaunchKernelGGL(KSLOW<F32>, dim3(grid), dim3(kT), 0, s, a); break;             \
-        case F16: if (fast) hipLaunchKernelGGL(KFAST<F16>, dim3((unsigned)fwgs), dim3(kT), 0, s, a);     \
-                  else hipLaunchKernelGGL(KSLOW<F16>, dim3(grid), dim3(kT), 0, s, a); break;             \
-        default: if (fast) hipLaunchKernelGGL(KFAST<BF16>, dim3((unsigned)fwgs), dim3(kT), 0, s, a);     \
-                 else hipLaunchKernelGGL(KSLOW<BF16>, dim3(grid), dim3(kT), 0, s, a); break;             \
-    }
-    GX_MOM(k_mom_max_fast, k_mom_max)
-    hipLaunchKernelGGL(k_mom_finalize, dim3(grid_for(nb, 4096)), dim3(kT), 0, s, a);
-#undef GX_MOM
-    if (!fast) {
-        switch (dtype) {
-            case F32: hipLaunchKernelGGL(k_mom_emit<F32>, dim3(grid), dim3(kT), 0, s, a); break;
-            case F16: hipLaunchKernelGGL(k_mom_emit<F16>, dim3(grid), dim3(kT), 0, s, a); break;
-            default: hipLaunchKernelGGL(k_mom_emit<BF16>, dim3(grid), dim3(kT), 0, s, a); break;
-        }
-    } else if (a.sr) {
-        switch (dtype) {
-            case F32: hipLaunchKernelGGL((k_mom_emit_fast<F32, true>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
-            case F16: hipLaunchKernelGGL((k_mom_emit_fast<F16, true>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
-            default: hipLaunchKernelGGL((k_mom_emit_fast<BF16, true>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
-        }
-    } else {
-        switch (dtype) {
-            case F32: hipLaunchKernelGGL((k_mom_emit_fast<F32, false>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
-            case F16: hipLaunchKernelGGL((k_mom_emit_fast<F16, false>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
-            default: hipLaunchKernelGGL((k_mom_emit_fast<BF16, false>), dim3((unsigned)fwgs), dim3(kT), 0, s, a); break;
-        }
-    }
-    prof_end(ph, s);
-    return launch_check("quantized momentum update");
+    gefenx_muon_item it;
+    std::memset(&it, 0, sizeof(it));
+    it.grad = grad;
+    it.grad_stride0 = numel;
+    it.grad_stride1 = 1;
+    it.m_codebook = m_codebook;
+    it.m_magnitude = m_magnitude;
+    it.period = period;
+    it.workspace = workspace;
+    it.workspace_bytes = workspace_bytes;
+    return momentum_batch(fn, &it, 1, dtype, 1, numel, qtable_dev, momentum_out, beta1, stochastic_round, rng_seed,
+                          seed_dev, nesterov, static_cast<hipStream_t>(stream));
+}
+
+int gefenx_muon_momentum_batch(const gefenx_muon_item* items, int n, int dtype, int64_t rows, int64_t cols,
+                               const void* qtable_dev, void* momentum_out, double beta1, int stochastic_round,
+                               int64_t rng_seed, const int64_t* seed_dev, int nesterov, void* stream) {
+    return momentum_batch("gefenx_muon_momentum_batch", items, n, dtype, rows, cols, qtable_dev, momentum_out,
+                          beta1, stochastic_round, rng_seed, seed_dev, nesterov, static_cast<hipStream_t>(stream));
 }
 
 size_t gefenx_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols) {
@@ -1156,31 +1524,53 @@ int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch,
     uint16_t* Bm = reinterpret_cast<uint16_t*>(ws + L.off_b);
     double* part = reinterpret_cast<double*>(ws + L.off_part);
     float* den = reinterpret_cast<float*>(ws + L.off_den);
+    uint16_t* o16 = static_cast<uint16_t*>(out);
     const int64_t m = std::min(rows, cols), n = std::max(rows, cols);
     const int64_t N = m * n;
     const bool tall = rows > cols;
-    const dim3 g2(grid_for(N, 4096), (unsigned)batch);
     const dim3 gt((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64), (unsigned)batch);
     if (cdiv(rows, 64) > 65535 || batch > 65535)
         return set_error(GEFENX_EINVAL, "gefenx_newton_schulz: %lld rows x batch %lld exceed the launch grid",
                          (long long)rows, (long long)batch);
+    // X = bf16(in) / max(bf16(||bf16(in)||), eps): the norm straight from the
+    // input, the division fused into the load that lays out X and X^T
+    const bool vin = N % 8 == 0 && al16(in);
+    const dim3 gp(NsWs::kParts, (unsigned)batch);
+#define GX_NS_SUMSQ(DTV)                                                                                   \
+    if (vin) hipLaunchKernelGGL((k_ns_sumsq<DTV, true>), gp, dim3(kT), 0, s, in, N, part);                \
+    else hipLaunchKernelGGL((k_ns_sumsq<DTV, false>), gp, dim3(kT), 0, s, in, N, part);
     switch (in_dtype) {
-        case F32: hipLaunchKernelGGL(k_ns_load<F32>, gt, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
-        case F16: hipLaunchKernelGGL(k_ns_load<F16>, gt, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
-        default: hipLaunchKernelGGL(k_ns_load<BF16>, gt, dim3(kT), 0, s, in, rows, cols, N, X, Xt[0], N); break;
+        case F32: GX_NS_SUMSQ(F32) break;
+        case F16: GX_NS_SUMSQ(F16) break;
+        default: GX_NS_SUMSQ(BF16) break;
     }
-    hipLaunchKernelGGL(k_ns_sumsq, dim3(NsWs::kParts, (unsigned)batch), dim3(kT), 0, s, X, N, N, part);
+#undef GX_NS_SUMSQ
     hipLaunchKernelGGL(k_ns_norm, dim3((unsigned)cdiv(batch, 64)), dim3(64), 0, s, part, NsWs::kParts, batch,
                        (float)eps, den);
-    hipLaunchKernelGGL(k_ns_scale, g2, dim3(kT), 0, s, X, Xt[0], N, N, den);
+    const bool vload = cols % 8 == 0 && al16(in);
+#define GX_NS_LOAD(DTV)                                                                                    \
+    if (vload) hipLaunchKernelGGL((k_ns_load<DTV, true>), gt, dim3(kT), 0, s, in, rows, cols, X, Xt[0], den); \
+    else hipLaunchKernelGGL((k_ns_load<DTV, false>), gt, dim3(kT), 0, s, in, rows, cols, X, Xt[0], den);
+    switch (in_dtype) {
+        case F32: GX_NS_LOAD(F32) break;
+        case F16: GX_NS_LOAD(F16) break;
+        default: GX_NS_LOAD(BF16) break;
+    }
+#undef GX_NS_LOAD
     rc = launch_check("newton-schulz prologue");
     if (rc) return rc;
+    if (steps == 0) {
+        const dim3 g2(grid_for(N, 4096), (unsigned)batch);
+        hipLaunchKernelGGL(k_ns_store, g2, dim3(kT), 0, s, tall ? Xt[0] : X, N, N, o16, N);
+        return launch_check("newton-schulz epilogue");
+    }
     int cur = 0;
     // algorithmic FLOPs of the iteration (three full products), as quoted for
     // the reference; the symmetric products execute about half of theirs
     const double flops_iter = 2.0 * (double)batch * ((double)m * m * n * 2.0 + (double)m * m * m);
     for (int it = 0; it < steps; ++it) {
         const float a = (float)abc[3 * it], b = (float)abc[3 * it + 1], c = (float)abc[3 * it + 2];
+        const bool last = it + 1 == steps;
         int ph = prof_begin(GEFENX_K_NS_GEMM, 0.0, flops_iter, s);
         // G = X X^T (symmetric: lower tiles, mirrored)
         GemmArgs g1{X, n, N, X, n, N, nullptr, 0, 0, G, m, m * m, G, m, m * m, m, m, n, 1.0f, 0.0f, 0, 1};
@@ -1188,16 +1578,18 @@ int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch,
         // B = b G + c G G^T (symmetric: lower tiles, mirrored)
         GemmArgs gg{G, m, m * m, G, m, m * m, G, m, m * m, Bm, m, m * m, Bm, m, m * m, m, m, m, c, b, 0, 1};
         if (!rc) rc = gemm_nt(gg, batch, s);
-        // X = a X + B X  (B operand X^T), X^T of the result into the other buffer
-        GemmArgs gx{Bm, m, m * m, Xt[cur], m, N, X, n, N, X, n, N, Xt[cur ^ 1], m, N, m, n, m, 1.0f, a, 0};
+        // X = a X + B X  (B operand X^T), X^T of the result into the other
+        // buffer; the last iteration writes the result straight to out in the
+        // input's orientation (X when wide, X^T when tall) and nothing else
+        uint16_t* D = last ? (tall ? nullptr : o16) : X;
+        uint16_t* Dt = last ? (tall ? o16 : nullptr) : Xt[cur ^ 1];
+        GemmArgs gx{Bm, m, m * m, Xt[cur], m, N, X, n, N, D, n, N, Dt, m, N, m, n, m, 1.0f, a, 0};
         if (!rc) rc = gemm_nt(gx, batch, s);
         prof_end(ph, s);
         if (rc) return rc;
         cur ^= 1;
     }
-    // result in the input's orientation: X (wide) or X^T (tall)
-    hipLaunchKernelGGL(k_ns_store, g2, dim3(kT), 0, s, tall ? Xt[cur] : X, N, N, static_cast<uint16_t*>(out), N);
-    return launch_check("newton-schulz epilogue");
+    return GEFENX_OK;
 }
 
 int gefenx_normuon_scale(const void* update, int64_t rows, int64_t cols, float* normuon_v, double beta2,
@@ -1206,49 +1598,48 @@ int gefenx_normuon_scale(const void* update, int64_t rows, int64_t cols, float* 
     if (rows <= 0 || cols <= 0) return GEFENX_OK;
     if (!update || !normuon_v || !scale_out || !workspace || (step < 1 && !step_dev))
         return set_error(GEFENX_EINVAL, "gefenx_normuon_scale: bad argument");
-    const size_t need = 2 * align256(sizeof(float) * (size_t)rows);
-    if (workspace_bytes < need)
-        return set_error(GEFENX_EINVAL, "gefenx_normuon_scale: workspace %zu bytes < required %zu", workspace_bytes, need);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    float* row_norm = static_cast<float*>(workspace);
-    float* denom = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(sizeof(float) * (size_t)rows));
-    hipLaunchKernelGGL(k_row_norm, dim3((unsigned)cdiv(rows, kT / 64)), dim3(kT), 0, s,
-                       static_cast<const uint16_t*>(update), rows, cols, row_norm);
-    const float alpha = (float)((1.0 - beta2) / (double)cols);
-    const float bc = step_dev ? 1.0f : (float)(1.0 - std::pow(beta2, (double)step));
-    hipLaunchKernelGGL(k_normuon_scale, dim3(1), dim3(kT), 0, s, row_norm, normuon_v, rows, (float)beta2, alpha, bc,
-                       (float)eps, denom, static_cast<uint16_t*>(scale_out), step_dev, beta2);
-    return launch_check("normuon scale");
+    gefenx_muon_item it;
+    std::memset(&it, 0, sizeof(it));
+    it.normuon_v = normuon_v;
+    it.normuon_step = step;
+    it.normuon_step_dev = step_dev;
+    return normuon_batch("gefenx_normuon_scale", &it, 1, update, rows, cols, beta2, eps, scale_out, workspace,
+                         workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 size_t gefenx_normuon_workspace_bytes(int64_t rows) {
     return 2 * align256(sizeof(float) * (size_t)(rows > 0 ? rows : 1));
 }
 
+size_t gefenx_normuon_batch_workspace_bytes(int n, int64_t rows) {
+    return 2 * align256(sizeof(float) * (size_t)(n > 0 ? n : 1) * (size_t)(rows > 0 ? rows : 1));
+}
+
+int gefenx_normuon_scale_batch(const gefenx_muon_item* items, int n, const void* update, int64_t rows, int64_t cols,
+                               double beta2, double eps, void* scale_out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+    return normuon_batch("gefenx_normuon_scale_batch", items, n, update, rows, cols, beta2, eps, scale_out, workspace,
+                         workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
 int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_scale, int64_t rows, int64_t cols,
                       double lr, double weight_decay, double adjusted_lr, const float* step_scalars,
                       double lr_ratio, void* stream) {
-    int rc = check_dt(dtype, "gefenx_muon_apply");
-    if (rc) return rc;
-    if (rows <= 0 || cols <= 0) return GEFENX_OK;
-    if (!p || !update) return set_error(GEFENX_EINVAL, "gefenx_muon_apply: null pointer argument");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const float wdf = (float)(1.0 - lr * weight_decay);
-    const int wd = weight_decay > 0.0 ? 1 : 0;
-    float alpha = (float)(-adjusted_lr);
-    alpha = dtype == BF16 ? round_bf16(alpha) : dtype == F16 ? round_f16(alpha) : alpha;
-    const unsigned grid = grid_for(rows * cols, 16384);
-    const uint16_t* u = static_cast<const uint16_t*>(update);
-    const uint16_t* sc = static_cast<const uint16_t*>(row_scale);
-    switch (dtype) {
-        case F32: hipLaunchKernelGGL(k_muon_apply<F32>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha,
-                                   step_scalars, lr_ratio); break;
-        case F16: hipLaunchKernelGGL(k_muon_apply<F16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha,
-                                   step_scalars, lr_ratio); break;
-        default: hipLaunchKernelGGL(k_muon_apply<BF16>, dim3(grid), dim3(kT), 0, s, p, u, sc, rows, cols, wdf, wd, alpha,
-                                   step_scalars, lr_ratio); break;
-    }
-    return launch_check("muon apply");
+    gefenx_muon_item it;
+    std::memset(&it, 0, sizeof(it));
+    it.param = p;
+    it.param_stride0 = cols;
+    it.param_stride1 = 1;
+    it.step_scalars = step_scalars;
+    return apply_batch("gefenx_muon_apply", &it, 1, dtype, update, row_scale, rows, cols, lr, weight_decay,
+                       adjusted_lr, lr_ratio, static_cast<hipStream_t>(stream));
+}
+
+int gefenx_muon_apply_batch(const gefenx_muon_item* items, int n, int dtype, const void* update,
+                            const void* row_scale, int64_t rows, int64_t cols, double lr, double weight_decay,
+                            double adjusted_lr, double lr_ratio, void* stream) {
+    return apply_batch("gefenx_muon_apply_batch", items, n, dtype, update, row_scale, rows, cols, lr, weight_decay,
+                       adjusted_lr, lr_ratio, static_cast<hipStream_t>(stream));
 }
 
 int gefenx_gemm_nt_bf16(const void* A, const void* B, const void* C, void* D, int64_t M, int64_t N, int64_t K,

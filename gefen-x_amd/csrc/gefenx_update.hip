@@ -82,7 +82,8 @@ struct TensorWork {
     int32_t dtype, mode;
     int32_t fast_stats, fast_apply;  // kernel variant: 0 general, 1 contiguous, 2 transposed view
     int32_t write_p, sr, bf16_mean, det_epl;  // det_epl: block stats elements per item (8 or 1)
-    int32_t partial, pad3_;  // partial: block path with the caller's per-block stepsize (no vmean)
+    int32_t partial;     // block path with the caller's per-block stepsize (no vmean)
+    int32_t fin_wide;    // block finalize: one workgroup per block (blocks span many stats records)
     float eps, beta2, alpha2, pad2_;
     StepScalars sc;
     MomentumCoef mc;
@@ -765,6 +766,8 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
 // per block and wave (a max is exact in any order).
 // ====================================================================
 constexpr int kDetIters = 8;
+// Stats records per block from which the block finalize takes a workgroup per block.
+constexpr int64_t kFinWideRecords = 32;
 static_assert(2 * kDetIters * kWaves == 64, "the workgroup's run partials fill one wave");
 
 // Lane-order run starts (bit l: lane l begins a new key) and the segmented
@@ -802,6 +805,12 @@ __device__ __forceinline__ uint32_t seg_suffix_max(uint32_t m, uint64_t heads) {
     return m;
 }
 
+// Flush a wave's running block max (wave-uniform key and value): one atomic
+// into the workgroup's shard.
+__device__ __forceinline__ void flush_det_max(uint32_t* mb, int64_t key, int64_t nb, uint32_t m) {
+    if ((threadIdx.x & 63) == 0 && key >= 0 && key < nb && m != 0u) gatomic_max(mb + key, m);
+}
+
 template <int DT, int EPL>
 __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg) {
     using T = typename Elem<DT>::T;
@@ -809,33 +818,57 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
     __shared__ int64_t s_key[2 * kDetIters * kWaves];
     __shared__ double s_sum[2 * kDetIters * kWaves];
     if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(w.qt->cbr + threadIdx.x);
-    __syncthreads();
     const T* g = static_cast<const T*>(w.grad);
     const int64_t N = w.N, P = w.P, nb = w.nb;
     const MomentumCoef mc = w.mc;
-    uint32_t* mb = w.magbits;
+    // max |u|: a wave carries the max of its current block across iterations
+    // and flushes it into its workgroup's shard when the block changes, so a
+    // block spanning many workgroups takes one atomic per wave, spread over
+    // the shards (finalize takes the max over them)
+    uint32_t* mb = w.magbits + (wg % w.shards) * nb;
     double* bsq = w.blk_sq;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t base = wg * (int64_t)(kDetIters * kThreads * EPL);
-#pragma unroll 1
+    // every iteration's loads first
+    Raw8<DT> gr[kDetIters];
+    RawIdx8 ir[kDetIters];
+    float graw[kDetIters];
+    uint32_t iraw[kDetIters];
+    float mo[kDetIters];
+    int64_t keys[kDetIters];
+#pragma unroll
     for (int i = 0; i < kDetIters; ++i) {
         const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
-        int64_t key = nb;  // past the end: a sentinel key, never stored
+        keys[i] = nb;  // past the end: a sentinel key, never stored
+        if (e0 < N) {
+            keys[i] = div_floor(e0, P, w.invP);
+            mo[i] = *gbl(w.mag + keys[i]);
+            if constexpr (EPL == kChunk) {
+                load_raw8<DT>(g + e0, gr[i]);
+                ir[i] = load_raw_idx8(w.idx + e0);
+            } else {
+                graw[i] = to_f32<DT>(*gbl(g + e0));
+                iraw[i] = *gbl(w.idx + e0);
+            }
+        }
+    }
+    __syncthreads();  // s_cbr
+    int64_t ck = -1;   // carried block and its running max (wave-uniform)
+    uint32_t cm = 0u;
+#pragma unroll
+    for (int i = 0; i < kDetIters; ++i) {
+        const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
+        const int64_t key = keys[i];
         double val = 0.0;
         uint32_t mx = 0u;
         if (e0 < N) {
-            key = div_floor(e0, P, w.invP);
-            const float mo = *gbl(w.mag + key);
             float cs = 0.0f;
             if constexpr (EPL == kChunk) {
-                Raw8<DT> gr;
-                load_raw8<DT>(g + e0, gr);
-                const RawIdx8 ir = load_raw_idx8(w.idx + e0);
 #pragma unroll
                 for (int k = 0; k < kChunk; ++k) {
-                    const float gv = raw_elem<DT>(gr, k);
-                    const float u = momentum_value(s_cbr[raw_idx(ir, k)], mo, gv, mc);
+                    const float gv = raw_elem<DT>(gr[i], k);
+                    const float u = momentum_value(s_cbr[raw_idx(ir[i], k)], mo[i], gv, mc);
                     const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
                     mx = ub > mx ? ub : mx;
                     float sq = gv * gv;
@@ -843,8 +876,8 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
                     cs += sq;
                 }
             } else {
-                const float gv = to_f32<DT>(g[e0]);
-                const float u = momentum_value(s_cbr[w.idx[e0]], mo, gv, mc);
+                const float gv = graw[i];
+                const float u = momentum_value(s_cbr[iraw[i]], mo[i], gv, mc);
                 mx = __float_as_uint(u) & 0x7fffffffu;
                 float sq = gv * gv;
                 if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
@@ -856,8 +889,24 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
         const double sv = seg_suffix_sum(val, heads);
         const uint32_t sm = seg_suffix_max(mx, heads);
         const bool start = (heads >> lane) & 1ull;
-        if (start && key < nb && sm != 0u) gatomic_max(mb + key, sm);
         const int last = 63 - __clzll((long long)heads);
+        // max: the first run continues the carried block or flushes it; runs
+        // strictly inside these 64 items are complete; the last run is carried
+        const int64_t k0 = __shfl(key, 0, 64);
+        const uint32_t m0 = (uint32_t)__shfl((int)sm, 0, 64);
+        if (k0 == ck) {
+            cm = m0 > cm ? m0 : cm;
+        } else {
+            flush_det_max(mb, ck, nb, cm);
+            ck = k0;
+            cm = m0;
+        }
+        if (last != 0) {
+            flush_det_max(mb, ck, nb, cm);
+            if (start && lane != last && lane != 0 && key < nb && sm != 0u) gatomic_max(mb + key, sm);
+            ck = __shfl(key, last, 64);
+            cm = (uint32_t)__shfl((int)sm, last, 64);
+        }
         if (start && lane != 0 && lane != last && key < nb) bsq[key] = sv;  // complete inside these items
         const int q = 2 * (i * kWaves + wave);
         if (lane == 0) {
@@ -869,6 +918,7 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
             s_sum[q + 1] = lane == 0 ? 0.0 : sv;
         }
     }
+    flush_det_max(mb, ck, nb, cm);
     __syncthreads();
     if (wave == 0) {
         const int64_t key = s_key[lane];
@@ -974,10 +1024,59 @@ __device__ __forceinline__ void finalize_factored(const TensorWork& w, int64_t w
     for (int64_t b = gtid; b < w.nb; b += gstride) finalize_magnitude(w, b);
 }
 
+// vmean EMA + per-block stepsize of block b from its sum of squares
+// (gefen.py:180-190, 3794-3805), then its magnitude.
+__device__ __forceinline__ void finalize_block_one(const TensorWork& w, const StepScalars& sc, int64_t b, double sq) {
+    float mean = (float)sq / (float)w.P;
+    if (w.bf16_mean) mean = round_dt<BF16>(mean);
+    const float v = __builtin_fmaf(mean, w.alpha2, w.v0[b] * w.beta2);
+    w.v0[b] = v;
+    const float h = sqrtf(v) * sc.inv_bc2 + w.eps;
+    w.step[b] = (1.0f / h) * sc.inv_bc1;
+    finalize_magnitude(w, b);
+}
+
+// Wide form: workgroup b sums block b's stored sum and the records of the
+// workgroups it spans (thread t takes records t, t+256, ... in order, then a
+// fixed-order reduction), so a block of tens of millions of elements is not
+// one thread's serial walk.
+__device__ __forceinline__ void finalize_block_wide(const TensorWork& w, int64_t b) {
+    __shared__ double s_part[kWaves];
+    const int tid = threadIdx.x;
+    double part = 0.0;
+    if (!w.partial) {
+        const int64_t wlo = (b * w.P) / w.det_elems;
+        const int64_t whi = ((b + 1) * w.P - 1) / w.det_elems;
+        for (int64_t r = wlo + tid; r <= whi; r += kThreads) {
+            const DetRec d = w.det_rec[r];
+            if (d.kf == b) part += d.sf;
+            if (d.kl == b) part += d.sl;
+        }
+    }
+    part = wave_sum_d(part);
+    if ((tid & 63) == 0) s_part[tid >> 6] = part;
+    __syncthreads();
+    if (tid != 0) return;
+    double sq = 0.0;
+    for (int64_t sh = 0; sh < w.shards; ++sh) {
+        sq += w.blk_sq[sh * w.nb + b];
+        w.blk_sq[sh * w.nb + b] = 0.0;
+    }
+    if (w.partial) {  // the stepsize comes from the caller: magnitudes only
+        finalize_magnitude(w, b);
+        return;
+    }
+    for (int ww = 0; ww < kWaves; ++ww) sq += s_part[ww];
+    finalize_block_one(w, read_scalars(w), b, sq);
+}
+
 // vmean EMA + per-block stepsize (gefen.py:180-190, 3794-3805) + magnitudes.
 __device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) {
+    if (w.fin_wide) {
+        if (wg < w.nb) finalize_block_wide(w, wg);
+        return;
+    }
     const StepScalars sc = read_scalars(w);
-    const float fP = (float)w.P;
     for (int64_t b = wg * kThreads + threadIdx.x; b < w.nb; b += w.nbw * kThreads) {
         // the fixed-order stats store a block's sum (in shard 0) when the
         // block is complete inside one workgroup, or leave it in the records
@@ -1001,13 +1100,7 @@ __device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) 
                 if (d.kl == b) sq += d.sl;
             }
         }
-        float mean = (float)sq / fP;
-        if (w.bf16_mean) mean = round_dt<BF16>(mean);
-        const float v = __builtin_fmaf(mean, w.alpha2, w.v0[b] * w.beta2);
-        w.v0[b] = v;
-        const float h = sqrtf(v) * sc.inv_bc2 + w.eps;
-        w.step[b] = (1.0f / h) * sc.inv_bc1;
-        finalize_magnitude(w, b);
+        finalize_block_one(w, sc, b, sq);
     }
 }
 
@@ -1971,6 +2064,13 @@ static int build_work(const WorkInput& in, TensorWork& w) {
             }
             w.fast_apply = (tv_shape && tv_g && tv_p && !in.sr && w.write_p) ? 2
                          : (g_contig && p_contig) ? w.fast_apply : 0;
+        }
+        // blocks that span many stats workgroups sum their records with a
+        // whole workgroup each (a thread would walk thousands of them)
+        if (w.det_rec != nullptr && w.P / w.det_elems + 2 >= kFinWideRecords) {
+            w.fin_wide = 1;
+            w.nbw = nb;
+            w.fin_wgs = nb;
         }
     }
     w.apply_wgs = std::max<int64_t>(1, ceil_div(nchunks, kThreads * kApplyChunksPerThread));

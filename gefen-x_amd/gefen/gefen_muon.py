@@ -376,52 +376,66 @@ class GefenMuon(Gefen):
         return loss
 
     def _step_chunk(self, lib, group, chunk, device, rows, cols, gdtype, schedule):
+        """One bucket chunk (matrices of one shape, dtype and group): batched
+        momentum, batched Newton-Schulz, batched NorMuon scale and apply.
+        Strided grads and parameters are read and written in place."""
         numel = rows * cols
+        n = len(chunk)
         stream = torch.cuda.current_stream(device).cuda_stream
         cb = self._gefen_codebook_on(device)
         qt = _fused.quant_table(cb, gdtype)
-        mom = self._buffer(("mom", device, gdtype), len(chunk) * numel, gdtype, device).view(len(chunk), rows, cols)
+        mom = self._buffer(("mom", device, gdtype), n * numel, gdtype, device).view(n, rows, cols)
         dcode = _fused._dtype_code(gdtype)
+        normuon = bool(group.get("normuon", False))
+        items = (_native.MuonItem * n)()
+        seed_ptr = None
+        for i, (_, name, p, grad) in enumerate(chunk):
+            state = self.state[p]
+            ws = self._momentum_workspace(state, device)
+            scalars_ptr, seed_ptr = self._capt_pointers(state, device)
+            it = items[i]
+            it.grad = grad.data_ptr()
+            it.grad_stride0, it.grad_stride1 = grad.stride()
+            it.m_codebook = state["m_codebook"].data_ptr()
+            it.m_magnitude = state["m_magnitude"].data_ptr()
+            it.period = int(state["automatic_period"])
+            it.workspace = ws.data_ptr()
+            it.workspace_bytes = ws.numel()
+            it.param = p.data_ptr()
+            it.param_stride0, it.param_stride1 = p.stride()
+            it.step_scalars = scalars_ptr
         with torch.cuda.device(device):
-            for i, (grp, name, p, grad) in enumerate(chunk):
-                state = self.state[p]
-                g = grad if grad.is_contiguous() else grad.contiguous()
-                ws = self._momentum_workspace(state, device)
-                scalars_ptr, seed_ptr = self._capt_pointers(state, device)
-                _native.check(lib.gefenx_quantized_momentum_update(
-                    g.data_ptr(), dcode, numel, int(state["automatic_period"]), state["m_codebook"].data_ptr(),
-                    state["m_magnitude"].data_ptr(), qt.data_ptr(), mom[i].data_ptr(), float(grp["momentum"]),
-                    1 if self._stochastic_round else 0, self._kernel_rng_seed(), seed_ptr,
-                    1 if grp["nesterov"] else 0, ws.data_ptr(), ws.numel(), stream), "muon momentum of " + name)
-                if not self._capt_on:
-                    state["step"] += 1
+            _native.check(lib.gefenx_muon_momentum_batch(
+                items, n, dcode, rows, cols, qt.data_ptr(), mom.data_ptr(), float(group["momentum"]),
+                1 if self._stochastic_round else 0, self._kernel_rng_seed(), seed_ptr,
+                1 if group["nesterov"] else 0, stream), "muon momentum of " + chunk[0][1])
+            if not self._capt_on:
+                for _, _, p, _ in chunk:
+                    self.state[p]["step"] += 1
             ortho = _zeropower_via_newtonschulz_batched(mom, schedule, len(schedule), group["eps"])
             lr = 0.0 if self._capt_on else self._lr_value(group)  # capturable: read on the device
             wd = group["weight_decay"]
-            for i, (grp, name, p, grad) in enumerate(chunk):
-                state = self.state[p]
-                scalars_ptr, _ = self._capt_pointers(state, device)
-                scale_ptr = None
-                if grp.get("normuon", False):
-                    v = state["normuon_v"]
-                    step_ptr = None
+            scale_ptr = None
+            if normuon:
+                for i, (_, _, p, _) in enumerate(chunk):
+                    state = self.state[p]
+                    items[i].normuon_v = state["normuon_v"].data_ptr()
                     if self._capt_on:
-                        step_ptr = state["normuon_step"].data_ptr()
+                        items[i].normuon_step_dev = state["normuon_step"].data_ptr()
                     else:
                         state["normuon_step"] += 1
-                    scale = self._buffer(("scale", device), rows, torch.bfloat16, device)
-                    nws = self._buffer(("nws", device), int(lib.gefenx_normuon_workspace_bytes(rows)), torch.uint8,
-                                       device)
-                    _native.check(lib.gefenx_normuon_scale(
-                        ortho[i].data_ptr(), rows, cols, v.data_ptr(), float(grp["normuon_beta2"]),
-                        0 if self._capt_on else int(state["normuon_step"]), float(grp["normuon_eps"]),
-                        scale.data_ptr(), nws.data_ptr(), nws.numel(), step_ptr, stream), "normuon of " + name)
-                    scale_ptr = scale.data_ptr()
-                ratio = _adjust_lr_ratio(grp["adjust_lr_fn"], p.shape)
-                adjusted = 0.0 if self._capt_on else _adjust_lr(lr, grp["adjust_lr_fn"], p.shape)
-                pk = p if p.is_contiguous() else p.contiguous()
-                _native.check(lib.gefenx_muon_apply(
-                    pk.data_ptr(), _fused._dtype_code(p.dtype), ortho[i].data_ptr(), scale_ptr, rows, cols, lr,
-                    float(wd) if wd > 0.0 else 0.0, adjusted, scalars_ptr, ratio, stream), "muon apply of " + name)
-                if pk is not p:
-                    p.copy_(pk)
+                        items[i].normuon_step = int(state["normuon_step"])
+                scale = self._buffer(("scale", device), n * rows, torch.bfloat16, device)
+                nws = self._buffer(("nws", device), int(lib.gefenx_normuon_batch_workspace_bytes(n, rows)),
+                                   torch.uint8, device)
+                _native.check(lib.gefenx_normuon_scale_batch(
+                    items, n, ortho.data_ptr(), rows, cols, float(group["normuon_beta2"]),
+                    float(group["normuon_eps"]), scale.data_ptr(), nws.data_ptr(), nws.numel(), stream),
+                    "normuon of " + chunk[0][1])
+                scale_ptr = scale.data_ptr()
+            shape = chunk[0][2].shape
+            ratio = _adjust_lr_ratio(group["adjust_lr_fn"], shape)
+            adjusted = 0.0 if self._capt_on else _adjust_lr(lr, group["adjust_lr_fn"], shape)
+            _native.check(lib.gefenx_muon_apply_batch(
+                items, n, _fused._dtype_code(chunk[0][2].dtype), ortho.data_ptr(), scale_ptr, rows, cols, lr,
+                float(wd) if wd > 0.0 else 0.0, adjusted, ratio, stream), "muon apply of " + chunk[0][1])

@@ -64,6 +64,19 @@ class CaptDesc(ctypes.Structure):
     ]
 
 
+class MuonItem(ctypes.Structure):
+    """Mirror of ``gefenx_muon_item`` (include/gefenx.h)."""
+
+    _fields_ = [
+        ("grad", ctypes.c_void_p), ("grad_stride0", ctypes.c_int64), ("grad_stride1", ctypes.c_int64),
+        ("m_codebook", ctypes.c_void_p), ("m_magnitude", ctypes.c_void_p), ("period", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("param", ctypes.c_void_p), ("param_stride0", ctypes.c_int64), ("param_stride1", ctypes.c_int64),
+        ("normuon_v", ctypes.c_void_p), ("normuon_step_dev", ctypes.c_void_p), ("normuon_step", ctypes.c_int64),
+        ("step_scalars", ctypes.c_void_p),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -113,6 +126,10 @@ SIGNATURES = {
     "gefenx_normuon_workspace_bytes": (_SZ, [_I64]),
     "gefenx_normuon_scale": (_I, [_P, _I64, _I64, _P, _D, _I64, _D, _P, _P, _SZ, _P, _P]),
     "gefenx_muon_apply": (_I, [_P, _I, _P, _P, _I64, _I64, _D, _D, _D, _P, _D, _P]),
+    "gefenx_muon_momentum_batch": (_I, [_P, _I, _I, _I64, _I64, _P, _P, _D, _I, _I64, _P, _I, _P]),
+    "gefenx_normuon_batch_workspace_bytes": (_SZ, [_I, _I64]),
+    "gefenx_normuon_scale_batch": (_I, [_P, _I, _P, _I64, _I64, _D, _D, _P, _P, _SZ, _P]),
+    "gefenx_muon_apply_batch": (_I, [_P, _I, _I, _P, _P, _I64, _I64, _D, _D, _D, _D, _P]),
     "gefenx_gemm_nt_bf16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _P]),
     "gefenx_profile_enable": (_I, [_I]),
     "gefenx_profile_read": (_I, [_I, _P, _P, _P, _P]),

@@ -378,6 +378,50 @@ int gefenx_newton_schulz(const void* in, int in_dtype, void* out, int64_t batch,
                          int64_t cols, const double* abc, int steps, double eps, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Batched Muon launches over matrices of one shape [rows, cols] (one launch
+ * set per up to 16 matrices instead of one per matrix; the reference steps
+ * them one at a time, gefen_muon.py:1064-1146, 1192-1300).  Each matrix is
+ * described by one gefenx_muon_item; the fields a call does not read may be
+ * left zero.  Grads and parameters may be strided views (logical row-major
+ * order), as in gefenx_tensor_desc.
+ * ---------------------------------------------------------------------- */
+typedef struct gefenx_muon_item {
+    const void* grad;            /* momentum: grad [rows, cols] of the batch dtype */
+    int64_t grad_stride0, grad_stride1;
+    uint8_t* m_codebook;         /* momentum: indices [numel] */
+    float* m_magnitude;          /* momentum: fp32 [numel/period] */
+    int64_t period;
+    void* workspace;             /* momentum: GEFENX_WS_MOMENTUM workspace of this matrix */
+    size_t workspace_bytes;
+    void* param;                 /* apply: parameter [rows, cols] */
+    int64_t param_stride0, param_stride1;
+    float* normuon_v;            /* NorMuon: fp32 [rows], mutated */
+    const float* normuon_step_dev; /* NorMuon: device fp32 step counter (capturable) or NULL */
+    int64_t normuon_step;        /* NorMuon: host step (>= 1) when normuon_step_dev is NULL */
+    const float* step_scalars;   /* apply: capturable scalar row fp32[4] or NULL */
+} gefenx_muon_item;
+
+/* gefenx_quantized_momentum_update for n matrices; matrix i emits its dense
+ * momentum to momentum_out + i * rows * cols (elements of the grad dtype). */
+int gefenx_muon_momentum_batch(const gefenx_muon_item* items, int n, int dtype, int64_t rows,
+                               int64_t cols, const void* qtable_dev, void* momentum_out, double beta1,
+                               int stochastic_round, int64_t rng_seed, const int64_t* seed_dev,
+                               int nesterov, void* stream);
+
+/* gefenx_normuon_scale for n matrices: update [n, rows, cols] bf16, scale_out
+ * [n, rows] bf16; workspace: gefenx_normuon_batch_workspace_bytes(n, rows). */
+size_t gefenx_normuon_batch_workspace_bytes(int n, int64_t rows);
+int gefenx_normuon_scale_batch(const gefenx_muon_item* items, int n, const void* update,
+                               int64_t rows, int64_t cols, double beta2, double eps, void* scale_out,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/* gefenx_muon_apply for n matrices: update [n, rows, cols] bf16, row_scale
+ * [n, rows] bf16 or NULL; each item's param, strides and step_scalars. */
+int gefenx_muon_apply_batch(const gefenx_muon_item* items, int n, int dtype, const void* update,
+                            const void* row_scale, int64_t rows, int64_t cols, double lr,
+                            double weight_decay, double adjusted_lr, double lr_ratio, void* stream);
+
 /* NorMuon row scale of a bf16 update [rows, cols] (gefen_muon.py:1192-1230):
  * normuon_v (fp32 [rows], mutated) <- v*beta2 + row_sq*((1-beta2)/cols);
  * scale_out (bf16 [rows]) = bf16(frob_scale / (sqrt(v/(1-beta2^step)) + eps)).

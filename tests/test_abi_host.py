@@ -225,7 +225,8 @@ def _c_layout(struct, fields):
     return int(out[0]), [int(x) for x in out[1:]]
 
 
-@pytest.mark.parametrize("struct, mirror", [("gefenx_tensor_desc", "TensorDesc"), ("gefenx_capt_desc", "CaptDesc")])
+@pytest.mark.parametrize("struct, mirror", [("gefenx_tensor_desc", "TensorDesc"), ("gefenx_capt_desc", "CaptDesc"),
+                                           ("gefenx_muon_item", "MuonItem")])
 def test_ctypes_mirrors_match_header_layout(struct, mirror):
     """The Python descriptor mirrors have the C structs' size and offsets."""
     from gefen.kernels import _native

@@ -369,6 +369,7 @@ BLOCK_CASES = [
     (orc.BF16, 122880, 24576, 0.01),   # blocks straddle stats workgroups at odd offsets
     (orc.F32, 122880, 40, 0.01),       # several blocks per wave
     (orc.F16, 99999, 11111, 0.01),     # P % 8 != 0: one element per item, blocks over ~5 workgroups
+    (orc.BF16, 3 << 22, 3 << 21, 0.01),  # two blocks of 768 stats workgroups each (workgroup-wide finalize)
 ]
 
 
