@@ -405,7 +405,37 @@ struct GemmArgs {
     int vec;                              // 16-byte loads allowed (K, lda, ldb % 8 == 0, aligned)
     int tri;                              // D symmetric (A = B, C symmetric): lower-triangle tiles only,
                                           // each off-diagonal tile also stores its mirror through Dt = D
+    int64_t nt_m, nt_n, batch;            // tile grid of the launch (set by gemm_nt)
 };
+
+// Workgroup -> (batch item, tile row, tile column), XCD-aware.  The hardware
+// deals consecutive workgroups round-robin to the 8 XCDs, each with its own
+// L2; renumber them so that every XCD runs one contiguous range of logical
+// tiles, and order the tiles of a matrix in bands of kGroupM tile rows,
+// column by column inside a band.  The ~32 tiles an XCD holds at once then
+// read kGroupM A panels and ~32/kGroupM B panels per K step, instead of
+// tiles scattered over the whole grid.  Returns false for the upper-triangle
+// tiles of a symmetric product (their values are the lower tiles' mirrors).
+constexpr int64_t kXcds = 8;
+constexpr int64_t kGroupM = 4;
+
+__device__ __forceinline__ bool gemm_tile(const GemmArgs& g, int64_t& bz, int64_t& tm, int64_t& tn) {
+    const int64_t T = g.nt_m * g.nt_n * g.batch;
+    const int64_t wid = blockIdx.x;
+    const int64_t q = T / kXcds, r = T % kXcds;
+    const int64_t x = wid % kXcds;
+    const int64_t L = x * q + (x < r ? x : r) + wid / kXcds;
+    const int64_t per = g.nt_m * g.nt_n;
+    bz = L / per;
+    const int64_t t = L - bz * per;
+    const int64_t band = g.nt_n * kGroupM;
+    const int64_t m0 = (t / band) * kGroupM;
+    const int64_t gm = g.nt_m - m0 < kGroupM ? g.nt_m - m0 : kGroupM;
+    const int64_t tin = t - (t / band) * band;
+    tm = m0 + tin % gm;
+    tn = tin / gm;
+    return !(g.tri && tn > tm);
+}
 
 __device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ uint16_t f2bf(float x) { return (uint16_t)f32_to_bf16(x); }
@@ -464,14 +494,14 @@ __device__ __forceinline__ void gemm_store_tile(uint16_t* __restrict__ s, const 
 // values as D.
 template <int WM, int WN>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16 (&acc)[WM][WN], float* sOut,
-                                              int64_t m0, int64_t n0, int wm, int wn, int l32, int lhi) {
+                                              int64_t bz, bool diag, int64_t m0, int64_t n0, int wm, int wn,
+                                              int l32, int lhi) {
     constexpr int BN = 64 * WN;
     constexpr int kOutPitch = BN + 1;  // odd: conflict-free column reads
     constexpr int kVecD = 64 * BN / 8 / kT;  // D vectors per thread and slab
-    const int64_t bz = blockIdx.z;
     const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
     uint16_t* D = g.D ? g.D + bz * g.sD : nullptr;
-    uint16_t* Dt = (g.Dt && !(g.tri && blockIdx.x == blockIdx.y)) ? g.Dt + bz * g.sDt : nullptr;
+    uint16_t* Dt = (g.Dt && !(g.tri && diag)) ? g.Dt + bz * g.sDt : nullptr;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int h = 0; h < WM; ++h) {
@@ -576,12 +606,12 @@ __global__ void __launch_bounds__(kT) k_gemm_nt(GemmArgs g) {
     uint16_t (*sA)[BM * kPitch] = reinterpret_cast<uint16_t (*)[BM * kPitch]>(smem);
     uint16_t (*sB)[BN * kPitch] = reinterpret_cast<uint16_t (*)[BN * kPitch]>(smem + sizeof(uint16_t) * 2 * BM * kPitch);
     float* sOut = reinterpret_cast<float*>(smem);
-    if (g.tri && blockIdx.x > blockIdx.y) return;  // upper triangle: the mirror of a lower tile
-    const int64_t bz = blockIdx.z;
+    int64_t bz, tm, tn;
+    if (!gemm_tile(g, bz, tm, tn)) return;  // upper triangle: the mirror of a lower tile
     const uint16_t* A = g.A + bz * g.sA;
     const uint16_t* B = g.B + bz * g.sB;
-    const int64_t m0 = (int64_t)blockIdx.y * BM;
-    const int64_t n0 = (int64_t)blockIdx.x * BN;
+    const int64_t m0 = tm * BM;
+    const int64_t n0 = tn * BN;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -639,7 +669,7 @@ __global__ void __launch_bounds__(kT) k_gemm_nt(GemmArgs g) {
         __syncthreads();
     }
 
-    gemm_epilogue<WM, WN>(g, acc, sOut, m0, n0, wm, wn, l32, lhi);
+    gemm_epilogue<WM, WN>(g, acc, sOut, bz, tm == tn, m0, n0, wm, wn, l32, lhi);
 }
 
 // Direct-to-LDS variant (K a multiple of BK, 16-byte aligned rows): the
@@ -690,18 +720,18 @@ __device__ __forceinline__ void dl_load_stage(const uint16_t* __restrict__ A, in
 // WM x WM blocks of 32 x 32 per wave, 2 x 2 waves: tile (64*WM)^2.
 template <int WM, int BK, int S>
 __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
-    if (g.tri && blockIdx.x > blockIdx.y) return;  // upper triangle: the mirror of a lower tile
+    int64_t bz, tm, tn;
+    if (!gemm_tile(g, bz, tm, tn)) return;  // upper triangle: the mirror of a lower tile
     constexpr int TILE = 64 * WM;
     constexpr int kStage = 2 * TILE * BK;                        // bf16 per stage: A then B
     constexpr int kIpw = 2 * (TILE * BK * 2 / 1024) / (kT / 64);  // load instructions per wave and stage
     constexpr int kEpi = 2 * 64 * (TILE + 1);                    // the epilogue's fp32 slab, in bf16 units
     constexpr int kSmem = S * kStage > kEpi ? S * kStage : kEpi;
     __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
-    const int64_t bz = blockIdx.z;
     const uint16_t* A = g.A + bz * g.sA;
     const uint16_t* B = g.B + bz * g.sB;
-    const int64_t m0 = (int64_t)blockIdx.y * TILE;
-    const int64_t n0 = (int64_t)blockIdx.x * TILE;
+    const int64_t m0 = tm * TILE;
+    const int64_t n0 = tn * TILE;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -751,7 +781,7 @@ __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
         }
     }
     __syncthreads();
-    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), m0, n0, wm, wn, l32, lhi);
+    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
 }
 
 // One 1 KB direct-to-LDS load instruction (number q of this wave's share of
@@ -794,7 +824,8 @@ __device__ __forceinline__ void dl_load_one(const uint16_t* __restrict__ A, int6
 // buffer (never read) so every step issues the same loads without a branch.
 __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
     constexpr int WM = 4, TILE = 256, BK = 64, KS = BK / 16;
-    if (g.tri && blockIdx.x > blockIdx.y) return;  // upper triangle: the mirror of a lower tile
+    int64_t bz, tm, tn;
+    if (!gemm_tile(g, bz, tm, tn)) return;  // upper triangle: the mirror of a lower tile
     constexpr int kStage = 2 * TILE * BK;
     constexpr int kIpw = 2 * (TILE * BK * 2 / 1024) / (kT / 64);  // 16 load instructions per wave and stage
     constexpr int kLoadKs = 2;
@@ -803,11 +834,10 @@ __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
     constexpr int kEpi = 2 * 64 * (TILE + 1);
     constexpr int kSmem = 2 * kStage > kEpi ? 2 * kStage : kEpi;
     __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
-    const int64_t bz = blockIdx.z;
     const uint16_t* A = g.A + bz * g.sA;
     const uint16_t* B = g.B + bz * g.sB;
-    const int64_t m0 = (int64_t)blockIdx.y * TILE;
-    const int64_t n0 = (int64_t)blockIdx.x * TILE;
+    const int64_t m0 = tm * TILE;
+    const int64_t n0 = tn * TILE;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -862,7 +892,7 @@ __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // the last (discarded) reload lands before the epilogue reuses LDS
     __syncthreads();
-    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), m0, n0, wm, wn, l32, lhi);
+    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
 }
 
 static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
@@ -882,17 +912,21 @@ static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const bool dl = a.vec && g.K % 64 == 0 && al16(g.A) && al16(g.B);
     constexpr int bm = 128, bn = 128;
-    if (cdiv(g.M, bm) > 65535 || batch > 65535 || cdiv(g.N, bn) > 2147483647LL)
+    if (cdiv(g.M, bm) * cdiv(g.N, bn) * batch > 2147483647LL)
         return set_error(GEFENX_EINVAL, "newton-schulz gemm: %lld x %lld x batch %lld exceeds the launch grid",
                          (long long)g.M, (long long)g.N, (long long)batch);
+    a.batch = batch;
     const int64_t t256m = cdiv(g.M, 256), t256n = cdiv(g.N, 256);
     const int64_t big_tiles = (g.tri ? t256m * (t256m + 1) / 2 : t256m * t256n) * batch;
     if (dl && big_tiles >= 256) {
-        const dim3 grid_big((unsigned)t256n, (unsigned)t256m, (unsigned)batch);
-        hipLaunchKernelGGL(k_gemm_big, grid_big, dim3(kT), 0, s, a);
+        a.nt_m = t256m;
+        a.nt_n = t256n;
+        hipLaunchKernelGGL(k_gemm_big, dim3((unsigned)(t256m * t256n * batch)), dim3(kT), 0, s, a);
         return launch_check("newton-schulz gemm");
     }
-    const dim3 grid((unsigned)cdiv(g.N, bn), (unsigned)cdiv(g.M, bm), (unsigned)batch);
+    a.nt_m = cdiv(g.M, bm);
+    a.nt_n = cdiv(g.N, bn);
+    const dim3 grid((unsigned)(a.nt_m * a.nt_n * batch));
     if (dl)
         hipLaunchKernelGGL((k_gemm_dl<2, 64, 2>), grid, dim3(kT), 0, s, a);
     else if (a.vec)
