@@ -301,7 +301,9 @@ __global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a, MomBatch bt) {
     }
 }
 
-template <int DT, bool SR>
+// NEST: Nesterov output, fixed per launch so the output loop has no branch
+// and its codebook reads issue together.
+template <int DT, bool SR, bool NEST>
 __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
     using T = typename Elem<DT>::T;
     const MomItem& it = bt.it[blockIdx.y];
@@ -359,26 +361,55 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
         const int64_t ch = first + (int64_t)i * kT;
         if (ch >= nch) break;
         const int64_t e0 = ch * kChunk;
-        uint32_t ix[kChunk];
-        float o[kChunk];
+        const float m_new = mnew[i], y = yv[i];
+        // x = D(u / m_new) through the block reciprocal (Markstein step) in
+        // every lane; a wave where any lane is outside that step's safe range
+        // (tiny |u|; zero, subnormal, huge or NaN magnitude: y == 0) redoes the
+        // chunk element by element with the guarded helpers
+        const float tb = 0x1.00001p-100f * fmaxf(m_new, 1.0f);
+        float us[kChunk], xs[kChunk];
+        bool bad = y == 0.0f;
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
-            const float gv = raw_elem<DT>(gr[i], k);
-            const float u = mom_u<DT>(s_cbr[raw_idx(ir[i], k)], mold[i], gv, w);
-            const float x = mom_x<DT>(u, mnew[i], yv[i]);
-            uint32_t ni;
-            if constexpr (SR) {
-                ni = quant_stochastic(x, s_cb, s_lut, qt->k, seed, e0 + k);
-            } else if (fastq && x >= -1.0f && x <= 1.0f) {
-                int b = (int)__builtin_fmaf(x, (float)(kBuckets / 2), (float)(kBuckets / 2));
+            const float u = mom_u<DT>(s_cbr[raw_idx(ir[i], k)], mold[i], raw_elem<DT>(gr[i], k), w);
+            const float q0 = u * y;
+            const float r = __builtin_fmaf(-q0, m_new, u);
+            us[k] = u;
+            xs[k] = round_dt<DT>(__builtin_fmaf(r, y, q0));
+            bad = bad || !(fabsf(u) >= tb);
+        }
+        uint32_t ix[kChunk];
+        if (__builtin_expect(__any(bad), 0)) {
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                const float x = mom_x<DT>(us[k], m_new, y);
+                if constexpr (SR) ix[k] = quant_stochastic(x, s_cb, s_lut, qt->k, seed, e0 + k);
+                else ix[k] = quant_nearest(x, qt->bucket, qt->thr, kmax);
+            }
+        } else if constexpr (SR) {
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) ix[k] = quant_stochastic(xs[k], s_cb, s_lut, qt->k, seed, e0 + k);
+        } else if (fastq) {
+            // |x| <= 1 here: one bucket entry {threshold, base index} per element
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                int b = (int)__builtin_fmaf(xs[k], (float)(kBuckets / 2), (float)(kBuckets / 2));
                 b = b < 0 ? 0 : (b > kFqEntries - 1 ? kFqEntries - 1 : b);
                 const uint2 e = s_fq[b];
-                ni = e.y + (__uint_as_float(e.x) < x ? 1u : 0u);
-            } else {
-                ni = quant_nearest(x, qt->bucket, qt->thr, kmax);
+                ix[k] = e.y + (__uint_as_float(e.x) < xs[k] ? 1u : 0u);
             }
-            ix[k] = ni;
-            o[k] = mom_out<DT>(s_cbr[ni], mnew[i], gv, a);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) ix[k] = quant_nearest(xs[k], qt->bucket, qt->thr, kmax);
+        }
+        float cr[kChunk], o[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) cr[k] = s_cbr[ix[k]];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            o[k] = round_dt<DT>(cr[k] * m_new);
+            if constexpr (NEST)
+                o[k] = round_dt<DT>(__builtin_fmaf(a.alpha_d, raw_elem<DT>(gr[i], k), round_dt<DT>(o[k] * a.beta)));
         }
         store_idx8(idxp + e0, ix);
         store8<DT>(out + e0, o);
@@ -1282,13 +1313,17 @@ static void mom_launch(const MomArgs& a, const MomBatch& bt, int n, int dtype, b
             default: hipLaunchKernelGGL(k_mom_max_fast<BF16>, gf, dim3(kT), 0, s, a, bt); break;
         }
         hipLaunchKernelGGL(k_mom_finalize, gfin, dim3(kT), 0, s, bt);
-#define GX_EMIT_FAST(SRV)                                                                                  \
+#define GX_EMIT_FAST(SRV, NV)                                                                              \
     switch (dtype) {                                                                                       \
-        case F32: hipLaunchKernelGGL((k_mom_emit_fast<F32, SRV>), gf, dim3(kT), 0, s, a, bt); break;       \
-        case F16: hipLaunchKernelGGL((k_mom_emit_fast<F16, SRV>), gf, dim3(kT), 0, s, a, bt); break;       \
-        default: hipLaunchKernelGGL((k_mom_emit_fast<BF16, SRV>), gf, dim3(kT), 0, s, a, bt); break;       \
+        case F32: hipLaunchKernelGGL((k_mom_emit_fast<F32, SRV, NV>), gf, dim3(kT), 0, s, a, bt); break;   \
+        case F16: hipLaunchKernelGGL((k_mom_emit_fast<F16, SRV, NV>), gf, dim3(kT), 0, s, a, bt); break;   \
+        default: hipLaunchKernelGGL((k_mom_emit_fast<BF16, SRV, NV>), gf, dim3(kT), 0, s, a, bt); break;   \
     }
-        if (sr) { GX_EMIT_FAST(true) } else { GX_EMIT_FAST(false) }
+        if (sr) {
+            if (a.nesterov) { GX_EMIT_FAST(true, true) } else { GX_EMIT_FAST(true, false) }
+        } else {
+            if (a.nesterov) { GX_EMIT_FAST(false, true) } else { GX_EMIT_FAST(false, false) }
+        }
 #undef GX_EMIT_FAST
         return;
     }
