@@ -424,3 +424,137 @@ def test_newton_schulz_aspect_ratio_matches_oracle(dev, lib):
     assert np.linalg.norm(got - o) <= NS_REL * np.linalg.norm(o)
     s = np.linalg.svd(got.astype(np.float64), compute_uv=False)
     assert 0.5 < s.min() and s.max() < 1.3
+
+
+@pytest.mark.parametrize("case", list(MUON_KW))
+def test_gefen_muon_strided_views_match_reference_golden(dev, case):
+    """The reference's GefenMuon trajectory with every parameter and grad
+    passed as a transposed view (storage [cols, rows], strides (1, rows)):
+    the batched momentum reads the grads and the batched apply writes the
+    parameters in place through their strides -- indices and magnitudes
+    bit-exact, parameters within the Newton-Schulz bound."""
+    from gefen import GefenMuon
+    dtype, kw, steps = MUON_KW[case]
+    td = TORCH_DT[dtype]
+    z = np.load(os.path.join(GOLDEN, case + ".npz"))
+    names = ["a", "b"]
+
+    def view(a):  # the values of `a` in a transposed-view tensor
+        return torch.from_numpy(np.ascontiguousarray(a.T)).to(td).to(dev).t()
+
+    ps = [(n, torch.nn.Parameter(view(z["p0_" + n]))) for n in names]
+    assert all(p.stride() == (1, p.shape[0]) for _, p in ps)
+    opt = GefenMuon(ps, **kw)
+    opt._gefen_codebook = torch.from_numpy(z["codebook"]).to(dev)
+    for n, p in ps:
+        opt.state[p]["automatic_period"] = int(z["period_" + n])
+    for s in range(1, steps + 1):
+        for n, p in ps:
+            p.grad = view(z["g%d_%s" % (s, n)])
+        opt.step()
+        torch.cuda.synchronize()
+        for n, p in ps:
+            st = opt.state[p]
+            tag = "%s strided step %d %s" % (case, s, n)
+            np.testing.assert_array_equal(st["m_codebook"].cpu().numpy().reshape(-1), z["idx%d_%s" % (s, n)],
+                                          err_msg=tag + " indices")
+            np.testing.assert_array_equal(st["m_magnitude"].cpu().numpy().reshape(-1), z["mag%d_%s" % (s, n)],
+                                          err_msg=tag + " magnitudes")
+            adj = kw["lr"] * orc.adjust_lr_ratio(kw.get("adjust_lr_fn"), p.shape)
+            ref = z["p%d_%s" % (s, n)]
+            _assert_update_close(p.detach().float().cpu().numpy(), ref, adj, dtype, tag + " params")
+            if "nv%d_%s" % (s, n) in z:
+                st["normuon_v"].copy_(torch.from_numpy(z["nv%d_%s" % (s, n)]).reshape(-1, 1).to(dev))
+            p.data.copy_(view(ref))
+            assert p.stride() == (1, p.shape[0])
+
+
+def test_momentum_batch_over_several_launches_matches_oracle(dev, lib):
+    """gefenx_muon_momentum_batch over 21 matrices of one shape (two launch
+    sets of 16 and 5, mixed periods, one strided grad making a third, general
+    run): every matrix's indices, magnitudes and momentum bit-exact against
+    oracle.muon_momentum."""
+    from gefen.kernels import _native
+    from gefen.kernels import automatic_gefen_fused as fused
+    rows, cols, n = 40, 96, 21
+    numel = rows * cols
+    rng = np.random.default_rng(7)
+    cb = np.load(os.path.join(GOLDEN, "learn.npz"))["cb"].astype(np.float32)
+    qt = fused.quant_table(torch.from_numpy(cb).to(dev), torch.bfloat16)
+    periods = [768 if i % 3 else 3840 for i in range(n)]
+    items = (_native.MuonItem * n)()
+    keep = []
+    state = []
+    for i in range(n):
+        idx_np, mag_np = _mom_state(numel, periods[i], i + 2)
+        idx = torch.from_numpy(idx_np.copy()).to(dev)
+        mag = torch.from_numpy(mag_np.copy()).to(dev)
+        ws = torch.zeros(int(lib.gefenx_workspace_bytes(_native.WS_MOMENTUM, 0, 0, numel // periods[i])),
+                         dtype=torch.uint8, device=dev)
+        g_np = (rng.standard_normal((rows, cols)) * 1e-3).astype(np.float32)
+        if i == 18:  # a transposed-view grad
+            g = torch.from_numpy(np.ascontiguousarray(g_np.T)).to(torch.bfloat16).to(dev).t()
+        else:
+            g = torch.from_numpy(g_np).to(torch.bfloat16).to(dev)
+        it = items[i]
+        it.grad = g.data_ptr()
+        it.grad_stride0, it.grad_stride1 = g.stride()
+        it.m_codebook, it.m_magnitude, it.period = idx.data_ptr(), mag.data_ptr(), periods[i]
+        it.workspace, it.workspace_bytes = ws.data_ptr(), ws.numel()
+        keep += [g, idx, mag, ws]
+        state.append((g, idx, mag, idx_np, mag_np))
+    out = torch.empty(n, rows, cols, dtype=torch.bfloat16, device=dev)
+    _check(lib.gefenx_muon_momentum_batch(items, n, fused._dtype_code(torch.bfloat16), rows, cols, qt.data_ptr(),
+                                          out.data_ptr(), 0.95, 0, 0, None, 1, _stream(dev)), lib)
+    torch.cuda.synchronize()
+    for i, (g, idx, mag, idx_np, mag_np) in enumerate(state):
+        ri, rm, ro = orc.muon_momentum(g.float().cpu().numpy(), idx_np, mag_np, periods[i], cb, orc.BF16, 0.95, True)
+        tag = "matrix %d" % i
+        np.testing.assert_array_equal(idx.cpu().numpy().reshape(-1), ri, err_msg=tag + " indices")
+        np.testing.assert_array_equal(mag.cpu().numpy().reshape(-1), rm, err_msg=tag + " magnitudes")
+        np.testing.assert_array_equal(out[i].float().cpu().numpy().reshape(-1), ro, err_msg=tag + " momentum")
+
+
+def test_normuon_and_apply_batch_match_single_matrix_calls(dev, lib):
+    """The batched NorMuon scale and apply over 18 matrices (two launch sets;
+    one transposed-view parameter) give the single-matrix entry points'
+    results bit for bit, and those are checked against the oracle above."""
+    from gefen.kernels import _native
+    rows, cols, n = 48, 64, 18
+    rng = np.random.default_rng(3)
+    upd = torch.from_numpy((rng.standard_normal((n, rows, cols)) * 0.05).astype(np.float32)).to(torch.bfloat16).to(dev)
+    p0 = (rng.standard_normal((n, rows, cols)) * 0.02).astype(np.float32)
+    v0 = (np.abs(rng.standard_normal((n, rows))) * 1e-3).astype(np.float32)
+    items = (_native.MuonItem * n)()
+    pb, vb = [], []
+    for i in range(n):
+        if i == 17:
+            p = torch.from_numpy(np.ascontiguousarray(p0[i].T)).to(torch.bfloat16).to(dev).t()
+        else:
+            p = torch.from_numpy(p0[i]).to(torch.bfloat16).to(dev)
+        v = torch.from_numpy(v0[i].copy()).to(dev)
+        items[i].param = p.data_ptr()
+        items[i].param_stride0, items[i].param_stride1 = p.stride()
+        items[i].normuon_v = v.data_ptr()
+        items[i].normuon_step = 3
+        pb.append(p)
+        vb.append(v)
+    scale = torch.empty(n, rows, dtype=torch.bfloat16, device=dev)
+    nws = torch.empty(int(lib.gefenx_normuon_batch_workspace_bytes(n, rows)), dtype=torch.uint8, device=dev)
+    _check(lib.gefenx_normuon_scale_batch(items, n, upd.data_ptr(), rows, cols, 0.95, 1e-8, scale.data_ptr(),
+                                          nws.data_ptr(), nws.numel(), _stream(dev)), lib)
+    _check(lib.gefenx_muon_apply_batch(items, n, 2, upd.data_ptr(), scale.data_ptr(), rows, cols, 0.02, 0.1,
+                                       0.02 * 0.2 * 8.0, 1.0, _stream(dev)), lib)
+    for i in range(n):
+        p = torch.from_numpy(p0[i]).to(torch.bfloat16).to(dev)
+        v = torch.from_numpy(v0[i].copy()).to(dev)
+        sc = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(int(lib.gefenx_normuon_workspace_bytes(rows)), dtype=torch.uint8, device=dev)
+        _check(lib.gefenx_normuon_scale(upd[i].data_ptr(), rows, cols, v.data_ptr(), 0.95, 3, 1e-8, sc.data_ptr(),
+                                        ws.data_ptr(), ws.numel(), None, _stream(dev)), lib)
+        _check(lib.gefenx_muon_apply(p.data_ptr(), 2, upd[i].data_ptr(), sc.data_ptr(), rows, cols, 0.02, 0.1,
+                                     0.02 * 0.2 * 8.0, None, 1.0, _stream(dev)), lib)
+        torch.cuda.synchronize()
+        assert torch.equal(sc, scale[i]), i
+        assert torch.equal(v, vb[i]), i
+        assert torch.equal(p, pb[i].contiguous()), i
