@@ -854,6 +854,60 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
         }
     }
     __syncthreads();  // s_cbr
+    // a workgroup whose elements all lie in one block (every block of at least
+    // this many elements, most of them) needs no segmented scans: each lane
+    // sums its items in iteration order, the waves combine by a fixed DPP
+    // pattern, then in wave order -- still the same order on every run
+    const int64_t wg_end = base + (int64_t)(kDetIters * kThreads * EPL) < N ? base + (int64_t)(kDetIters * kThreads * EPL)
+                                                                             : N;
+    const int64_t kfirst = div_floor(base, P, w.invP);
+    if (kfirst == div_floor(wg_end - 1, P, w.invP)) {
+        double lsum = 0.0;
+        uint32_t lmax = 0u;
+#pragma unroll
+        for (int i = 0; i < kDetIters; ++i) {
+            const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
+            if (e0 < N) {
+                float cs = 0.0f;
+                if constexpr (EPL == kChunk) {
+#pragma unroll
+                    for (int k = 0; k < kChunk; ++k) {
+                        const float gv = raw_elem<DT>(gr[i], k);
+                        const float u = momentum_value(s_cbr[raw_idx(ir[i], k)], mo[i], gv, mc);
+                        const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                        lmax = ub > lmax ? ub : lmax;
+                        float sq = gv * gv;
+                        if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                        cs += sq;
+                    }
+                } else {
+                    const float gv = graw[i];
+                    const float u = momentum_value(s_cbr[iraw[i]], mo[i], gv, mc);
+                    const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                    lmax = ub > lmax ? ub : lmax;
+                    float sq = gv * gv;
+                    if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                    cs = sq;
+                }
+                lsum += (double)cs;
+            }
+        }
+        lsum = wave_sum_d(lsum);
+        const uint32_t wmax = wave_max_u63(lmax);  // in lane 63
+        if (lane == 63 && wmax != 0u && kfirst < nb) gatomic_max(mb + kfirst, wmax);
+        if (lane == 0) s_sum[wave] = lsum;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double t = 0.0;
+            for (int v = 0; v < kWaves; ++v) t += s_sum[v];
+            DetRec* rec = w.det_rec + wg;
+            rec->kf = kfirst;
+            rec->sf = t;
+            rec->kl = -1;
+            rec->sl = 0.0;
+        }
+        return;
+    }
     int64_t ck = -1;   // carried block and its running max (wave-uniform)
     uint32_t cm = 0u;
 #pragma unroll
