@@ -258,6 +258,7 @@ class Gefen(torch.optim.Optimizer):
         self.verbose = verbose
         self._gefen_codebook = None
         self._gefen_codebook_by_device = {}
+        self._lr_slot = None  # (tensor lr, its _version, its value): see _lr_scalar
         self._gefen_global_step = 0
         self._param_names = {}
         # All parameters of a device go through one gefenx_multi_tensor_step
@@ -529,10 +530,23 @@ class Gefen(torch.optim.Optimizer):
                     raise RuntimeError("gradient dtype {} does not match parameter {} dtype {}".format(
                         g.dtype, name, p.dtype))
 
-    @staticmethod
-    def _lr_value(group) -> float:
+    def _lr_scalar(self, group) -> float:
+        """group["lr"] as a python float (gefen.py:1530-1555).  A tensor lr is
+        read from the device only when it is a different tensor or its
+        _version moved (an in-place scheduler update) since the last read:
+        one slot for all groups, so a constant or once-per-step-updated device
+        lr costs at most one host sync per step, not one per parameter, and a
+        fresh tensor per step cannot grow the cache.  Kept out of param_groups
+        and the state_dict."""
         lr = group["lr"]
-        return float(lr.item()) if torch.is_tensor(lr) else float(lr)
+        if not torch.is_tensor(lr):
+            return float(lr)
+        hit = getattr(self, "_lr_slot", None)
+        if hit is not None and hit[0] is lr and hit[1] == lr._version:
+            return hit[2]
+        value = float(lr.item())
+        self._lr_slot = (lr, lr._version, value)
+        return value
 
     def _init_state(self, state, p, grad, name, factored):
         numel = grad.numel()
@@ -605,7 +619,7 @@ class Gefen(torch.optim.Optimizer):
             return state, None, None, None, None
         state["step"] += 1
         state["factored_step"] += 1
-        lr = self._lr_value(group)
+        lr = self._lr_scalar(group)
         bc1 = 1 - group["beta1"] ** state["step"]
         bc2 = 1 - group["beta2"] ** state["factored_step"]
         return state, lr, 1.0 / bc2, 1.0 / bc1, 1.0 - lr * group["weight_decay"]
@@ -627,7 +641,7 @@ class Gefen(torch.optim.Optimizer):
             return state, None, None, None, None
         state["step"] += 1
         state["vmean_step"] += 1
-        lr = self._lr_value(group)
+        lr = self._lr_scalar(group)
         bc1 = 1 - group["beta1"] ** state["step"]
         bc2 = 1 - group["beta2"] ** state["vmean_step"]
         return state, lr, 1.0 / math.sqrt(bc2), 1.0 / bc1, 1.0 - lr * group["weight_decay"]

@@ -413,7 +413,7 @@ class GefenMuon(Gefen):
                 for _, _, p, _ in chunk:
                     self.state[p]["step"] += 1
             ortho = _zeropower_via_newtonschulz_batched(mom, schedule, len(schedule), group["eps"])
-            lr = 0.0 if self._capt_on else self._lr_value(group)  # capturable: read on the device
+            lr = 0.0 if self._capt_on else self._lr_scalar(group)  # capturable: read on the device
             wd = group["weight_decay"]
             scale_ptr = None
             if normuon:
