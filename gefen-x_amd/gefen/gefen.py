@@ -494,11 +494,16 @@ class Gefen(torch.optim.Optimizer):
         right = remap.clamp(0, k - 1)
         x = torch.from_numpy(old_h)
         choose = torch.where((x - new_h[left]).abs() <= (x - new_h[right]).abs(), left, right).to(torch.uint8)
+        # every remapped index tensor is built before any is written, so a
+        # failure part-way leaves the indices and the codebook as they were
+        staged = []
         for group in self.param_groups:
             for p in group["params"]:
                 st = self.state.get(p)
                 if st and "m_codebook" in st:
-                    st["m_codebook"].copy_(choose.to(st["m_codebook"].device)[st["m_codebook"].long()])
+                    staged.append((st["m_codebook"], choose.to(st["m_codebook"].device)[st["m_codebook"].long()]))
+        for dst, src in staged:
+            dst.copy_(src)
         self._gefen_codebook = new
         self._gefen_codebook_by_device.clear()
 
