@@ -279,13 +279,13 @@ class Gefen(torch.optim.Optimizer):
 
     @staticmethod
     def _validate_group_options(lr, betas, eps, weight_decay):
-        lr_val = float(lr.item()) if torch.is_tensor(lr) else lr
+        """gefen.py:1254-1275: the lr (a number or a 1-element tensor), betas
+        in [0, 1), weight_decay >= 0, eps finite and > 0."""
         if torch.is_tensor(lr) and lr.numel() != 1:
-            raise ValueError("Tensor lr must be 1-element")
+            raise ValueError("lr as a Tensor must be 1-element, got numel={}".format(lr.numel()))
+        lr_val = float(lr.item()) if torch.is_tensor(lr) else lr
         if not 0.0 <= lr_val:
             raise ValueError("Invalid learning rate: {}".format(lr_val))
-        if not 0.0 <= eps:
-            raise ValueError("Invalid epsilon value: {}".format(eps))
         if len(betas) != 2:
             raise ValueError("betas must be a pair")
         if not 0.0 <= betas[0] < 1.0:
@@ -294,33 +294,30 @@ class Gefen(torch.optim.Optimizer):
             raise ValueError("Invalid beta parameter at index 1: {}".format(betas[1]))
         if not 0.0 <= weight_decay:
             raise ValueError("Invalid weight_decay value: {}".format(weight_decay))
+        if not math.isfinite(eps) or eps <= 0.0:
+            raise ValueError("Invalid epsilon value: {}; eps must be finite and > 0".format(eps))
+
+    # A group's unnamed parameters are called <prefix><index>: "param_" in the
+    # implicit group of a plain parameter list, "group_<g>_param_" otherwise.
+    _PREFIX_KEY = "_gefenx_name_prefix"
 
     def _normalize_param_groups(self, params):
+        """gefen.py:1242-1251: a single tensor, an iterable of tensors or of
+        (name, tensor) pairs (one implicit group), or an iterable of group
+        dicts.  Each group then goes through add_param_group."""
         if isinstance(params, torch.Tensor):
-            raise TypeError("params argument given to the optimizer should be an iterable of Tensors "
-                            "or dicts, but got " + torch.typename(params))
+            params = [params]
         params = list(params)
         if len(params) == 0:
             raise ValueError("optimizer got an empty parameter list")
         if isinstance(params[0], dict):
-            groups = []
-            for gi, g in enumerate(params):
-                g = dict(g)
-                names, ps, synth = self._split_names(g["params"], prefix="group_{}_param_".format(gi))
-                g["params"] = ps
-                g["param_names"] = names
-                g["param_names_synthesized"] = synth
-                if "betas" in g:
-                    b = g.pop("betas")
-                    g["beta1"], g["beta2"] = b
-                self._validate_group_options(g.get("lr", 0.0), (g.get("beta1", 0.0), g.get("beta2", 0.0)),
-                                             g.get("eps", 0.0), g.get("weight_decay", 0.0))
-                groups.append(g)
-            return groups
-        names, ps, synth = self._split_names(params, prefix="param_")
-        return [{"params": ps, "param_names": names, "param_names_synthesized": synth}]
+            return [dict(g, **{self._PREFIX_KEY: "group_{}_param_".format(i)}) for i, g in enumerate(params)]
+        return [{"params": params, self._PREFIX_KEY: "param_"}]
 
     def _split_names(self, items, prefix):
+        """(names, tensors, synthesized flags) of a group's params, checked and
+        named without registering anything (add_param_group registers the
+        names once the whole group is valid)."""
         if isinstance(items, torch.Tensor):
             items = [items]
         names, ps, synth = [], [], []
@@ -333,16 +330,53 @@ class Gefen(torch.optim.Optimizer):
                 name, p = "{}{}".format(prefix, i), it
                 synth.append(True)
             if not isinstance(p, torch.Tensor):
-                raise TypeError("optimizer can only optimize Tensors, got {}".format(type(p)))
+                raise TypeError("Gefen can only optimize Tensors, but one of the params is {}".format(
+                    type(p).__name__))
+            if torch.is_complex(p):
+                raise ValueError("Gefen does not support complex parameters, but got a parameter with dtype "
+                                 "{}".format(p.dtype))
             base, k = name, 1
             while name in seen:
                 name = "{}_{}".format(base, k)
                 k += 1
             seen.add(name)
-            self._param_names[p] = name
             names.append(name)
             ps.append(p)
         return names, ps, synth
+
+    def _check_group_params(self, params):
+        """Subclass hook: reject parameters this optimizer cannot step."""
+
+    def add_param_group(self, param_group):
+        """gefen.py:1388-1525: all or nothing.  Hyperparameters (group value or
+        the constructor's), parameter types and duplicates (inside the group
+        and against the existing groups) are checked before anything is
+        registered; unnamed parameters get positional names."""
+        if not isinstance(param_group, dict):
+            raise TypeError("param_group must be a dict, got {}".format(type(param_group).__name__))
+        if "params" not in param_group:
+            raise ValueError("Gefen parameter group is missing the 'params' key.")
+        g = dict(param_group)
+        prefix = g.pop(self._PREFIX_KEY, "group_{}_param_".format(len(self.param_groups)))
+        if "betas" in g:
+            g["beta1"], g["beta2"] = g.pop("betas")
+        d = self.defaults
+        self._validate_group_options(g.get("lr", d["lr"]), (g.get("beta1", d["beta1"]), g.get("beta2", d["beta2"])),
+                                     g.get("eps", d["eps"]), g.get("weight_decay", d["weight_decay"]))
+        names, ps, synth = self._split_names(g["params"], prefix)
+        if len(ps) == 0:
+            raise ValueError("optimizer got an empty parameter list")
+        self._check_group_params(ps)
+        existing = {id(p) for grp in self.param_groups for p in grp["params"]}
+        batch = set()
+        for p in ps:
+            if id(p) in existing or id(p) in batch:
+                raise ValueError("some parameters appear in more than one parameter group")
+            batch.add(id(p))
+        g["params"], g["param_names"], g["param_names_synthesized"] = ps, names, synth
+        super().add_param_group(g)
+        for p, name in zip(ps, names):
+            self._param_names[p] = name
 
     def _iter_group_params_with_names(self, group):
         names = group.get("param_names") or [self._param_names.get(p, "param") for p in group["params"]]

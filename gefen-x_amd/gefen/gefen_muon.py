@@ -256,16 +256,26 @@ class GefenMuon(Gefen):
                          capturable=capturable, verbose=verbose)
 
     def add_param_group(self, param_group):
-        """2D parameters only; Muon defaults filled into the group
-        (gefen_muon.py:758-800)."""
-        for p in param_group["params"]:
+        """Muon defaults filled into the group, its NorMuon options checked,
+        2D parameters only (gefen_muon.py:758-800); all or nothing, as
+        Gefen.add_param_group."""
+        if isinstance(param_group, dict):
+            param_group = dict(param_group)
+            for k, v in self._muon_group_defaults.items():
+                param_group.setdefault(k, v)
+            if "momentum" in param_group:
+                param_group["beta1"] = param_group["momentum"]
+            nb2, neps = param_group["normuon_beta2"], param_group["normuon_eps"]
+            if not 0.0 <= nb2 < 1.0:
+                raise ValueError("normuon_beta2 must be in [0, 1) but is: {}".format(nb2))
+            if not math.isfinite(neps) or neps <= 0.0:
+                raise ValueError("normuon_eps must be finite and > 0 but is: {}".format(neps))
+        super().add_param_group(param_group)
+
+    def _check_group_params(self, params):
+        for p in params:
             if p.ndim != 2:
                 raise ValueError(_swapped_param_groups_error(p))
-        for k, v in self._muon_group_defaults.items():
-            param_group.setdefault(k, v)
-        if "momentum" in param_group:
-            param_group["beta1"] = param_group["momentum"]
-        super().add_param_group(param_group)
 
     # --------------------------------------------------------------- state
 
