@@ -210,6 +210,7 @@ __global__ void __launch_bounds__(kT) k_mom_emit(MomArgs a, MomBatch bt) {
 // chunk's loads are issued before the first chunk's math.
 constexpr int kChunk = 8;
 constexpr int kMomCpt = 8;
+static_assert(kT == kCodebookMax, "one codebook entry per thread");
 
 struct BlkPos {
     int64_t blk, pin;
@@ -222,12 +223,14 @@ __device__ __forceinline__ BlkPos blk_advance(BlkPos q, int64_t dB, int64_t dP, 
     return q;
 }
 
-template <int DT>
-__global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a, MomBatch bt) {
+// FULL: every chunk of the workgroup lies inside the matrix (all but its last
+// workgroup), so no load or store sits behind a branch and each wait names
+// exactly the chunk about to be used (a load behind a branch makes the
+// compiler assume, at the join, the path with fewer loads in flight, and
+// the first wait then drains every chunk's loads).
+template <int DT, bool FULL>
+__device__ __forceinline__ void mom_max_body(const MomArgs& a, const MomItem& it, float* s_cbr, float cbr_v) {
     using T = typename Elem<DT>::T;
-    const MomItem& it = bt.it[blockIdx.y];
-    __shared__ float s_cbr[kCodebookMax];
-    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(a.qt->cbr + threadIdx.x);
     const T* g = static_cast<const T*>(it.g);
     const uint8_t* idxp = it.idx;
     const float w = a.w;
@@ -251,19 +254,21 @@ __global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a, MomBatch bt) {
     for (int i = 0; i < kMomCpt; ++i) {
         const int64_t ch = first + (int64_t)i * kT;
         blk[i] = pos.blk;
-        if (ch < nch) {
+        if (FULL || ch < nch) {
             load_raw8<DT>(g + ch * kChunk, gr[i]);
             ir[i] = load_raw_idx8(idxp + ch * kChunk);
             mo[i] = *gbl(it.mag + pos.blk);
         }
         pos = blk_advance(pos, dB, dP, P);
+        if constexpr (FULL) __builtin_amdgcn_sched_barrier(0);  // chunk order kept: chunk i's data lands i-th
     }
+    s_cbr[threadIdx.x % kCodebookMax] = cbr_v;  // every thread: no branch, so the waits stay exact
     __syncthreads();  // s_cbr
     int64_t wblk = -1;   // wave-uniform running block
     uint32_t wbits = 0u;
 #pragma unroll
     for (int i = 0; i < kMomCpt; ++i) {
-        const bool valid = first + (int64_t)i * kT < nch;
+        const bool valid = FULL || first + (int64_t)i * kT < nch;
         uint32_t m = 0u;
         if (valid) {
 #pragma unroll
@@ -301,17 +306,46 @@ __global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a, MomBatch bt) {
     }
 }
 
-// NEST: Nesterov output, fixed per launch so the output loop has no branch
-// and its codebook reads issue together.
-template <int DT, bool SR, bool NEST>
-__global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
-    using T = typename Elem<DT>::T;
+template <int DT>
+__global__ void __launch_bounds__(kT) k_mom_max_fast(MomArgs a, MomBatch bt) {
     const MomItem& it = bt.it[blockIdx.y];
-    __shared__ uint2 s_fq[SR ? 1 : kFqEntries];
     __shared__ float s_cbr[kCodebookMax];
-    __shared__ float s_cb[SR ? kCodebookMax : 1];
-    __shared__ int16_t s_lut[SR ? kLutEntries + 7 : 1];
+    const float cbr_v = *gbl(a.qt->cbr + threadIdx.x % kCodebookMax);  // written to LDS after the chunk loads
+    if (((int64_t)blockIdx.x + 1) * (kT * kMomCpt) <= a.N / kChunk) mom_max_body<DT, true>(a, it, s_cbr, cbr_v);
+    else mom_max_body<DT, false>(a, it, s_cbr, cbr_v);
+}
+
+template <int DT, bool SR>
+struct EmitLds {
+    uint2 fq[SR ? 1 : kFqEntries];
+    float cbr[kCodebookMax];
+    float cb[SR ? kCodebookMax : 1];
+    int16_t lut[SR ? kLutEntries + 7 : 1];
+};
+
+// FULL: as in mom_max_body.  The nearest-rounding table is read into
+// registers before the chunks' loads are issued and written to LDS after, so
+// the LDS writes wait for the table alone, not for every chunk.
+template <int DT, bool SR, bool NEST, bool FULL>
+__device__ __forceinline__ void mom_emit_body(const MomArgs& a, const MomItem& it, EmitLds<DT, SR>& lds) {
+    using T = typename Elem<DT>::T;
+    uint2* s_fq = lds.fq;
+    float* s_cbr = lds.cbr;
+    float* s_cb = lds.cb;
+    int16_t* s_lut = lds.lut;
     const QTable* qt = a.qt;
+    constexpr int kFqVec = kFqEntries / 2;                // u32x4 per table
+    constexpr int kFqPer = (kFqVec + kT - 1) / kT;
+    u32x4 fqv[SR ? 1 : kFqPer];
+    if constexpr (!SR) {
+        const GX_GLOBAL u32x4* src = gbl(reinterpret_cast<const u32x4*>(qt->fq));
+#pragma unroll
+        for (int j = 0; j < kFqPer; ++j) {
+            const int i = threadIdx.x + j * kT;
+            fqv[j] = src[i < kFqVec ? i : kFqVec - 1];  // unconditional: no branch before the chunk loads
+        }
+    }
+    const float cbr_v = *gbl(qt->cbr + threadIdx.x % kCodebookMax);  // unconditional: no branch before the loads
     const T* g = static_cast<const T*>(it.g);
     T* out = static_cast<T*>(a.out) + (int64_t)blockIdx.y * a.N;
     uint8_t* idxp = it.idx;
@@ -333,7 +367,7 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
 #pragma unroll
     for (int i = 0; i < kMomCpt; ++i) {
         const int64_t ch = first + (int64_t)i * kT;
-        if (ch < nch) {
+        if (FULL || ch < nch) {
             mold[i] = *gbl(it.mag_old + pos.blk);
             mnew[i] = *gbl(it.mag + pos.blk);
             yv[i] = *gbl(it.minv + pos.blk);
@@ -341,15 +375,20 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
             ir[i] = load_raw_idx8(idxp + ch * kChunk);
         }
         pos = blk_advance(pos, dB, dP, P);
+        if constexpr (FULL) __builtin_amdgcn_sched_barrier(0);  // chunk order kept: chunk i's data lands i-th
     }
     if constexpr (SR) {
         for (int i = threadIdx.x; i < kLutEntries + 7; i += kT) s_lut[i] = *gbl(qt->lut + i);
         if (threadIdx.x < kCodebookMax) s_cb[threadIdx.x] = *gbl(qt->cb + threadIdx.x);
     } else {
-        for (int i = threadIdx.x; i < kFqEntries; i += kT)
-            s_fq[i] = uint2{*gbl(qt->fq + 2 * i), *gbl(qt->fq + 2 * i + 1)};
+        u32x4* dst = reinterpret_cast<u32x4*>(s_fq);
+#pragma unroll
+        for (int j = 0; j < kFqPer; ++j) {
+            const int i = threadIdx.x + j * kT;
+            if (j + 1 < kFqPer || i < kFqVec) dst[i] = fqv[j];
+        }
     }
-    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
+    s_cbr[threadIdx.x % kCodebookMax] = cbr_v;  // every thread: no branch, so the waits stay exact
     __syncthreads();
     uint64_t seed = a.seed;
     if (SR && a.seed_dev != nullptr) seed = (uint64_t)*gbl(a.seed_dev);
@@ -359,7 +398,7 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
 #pragma unroll
     for (int i = 0; i < kMomCpt; ++i) {
         const int64_t ch = first + (int64_t)i * kT;
-        if (ch >= nch) break;
+        if (!FULL && ch >= nch) break;
         const int64_t e0 = ch * kChunk;
         const float m_new = mnew[i], y = yv[i];
         // x = D(u / m_new) through the block reciprocal (Markstein step) in
@@ -414,6 +453,16 @@ __global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
         store_idx8(idxp + e0, ix);
         store8<DT>(out + e0, o);
     }
+}
+
+// NEST: Nesterov output, fixed per launch so the output loop has no branch
+// and its codebook reads issue together.
+template <int DT, bool SR, bool NEST>
+__global__ void __launch_bounds__(kT) k_mom_emit_fast(MomArgs a, MomBatch bt) {
+    __shared__ EmitLds<DT, SR> lds;
+    const MomItem& it = bt.it[blockIdx.y];
+    if (((int64_t)blockIdx.x + 1) * (kT * kMomCpt) <= a.N / kChunk) mom_emit_body<DT, SR, NEST, true>(a, it, lds);
+    else mom_emit_body<DT, SR, NEST, false>(a, it, lds);
 }
 
 // ==================================================================
@@ -1041,7 +1090,17 @@ __global__ void __launch_bounds__(kT) k_ns_load(const void* in, int64_t R, int64
     uint16_t* same = (tall ? Xt : X) + bz * N;   // [R x C]
     uint16_t* trans = (tall ? X : Xt) + bz * N;  // [C x R]
     const float den = den_p[bz];
+    const float yden = block_recip(den);  // RN(1/den), or 0 when den or 1/den is not normal
     const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    // both chunks' loads before any store (the output may alias the input as
+    // far as the compiler knows, so a load after a store could not move up)
+    Raw8<DT> raws[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int v = threadIdx.x + k * kT;
+        const int64_t r = r0 + (v >> 3), c = c0 + (v & 7) * 8;
+        if (VEC && r < R && c < Cc) load_raw8<DT>(src + r * Cc + c, raws[k]);
+    }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int v = threadIdx.x + k * kT;
@@ -1049,10 +1108,26 @@ __global__ void __launch_bounds__(kT) k_ns_load(const void* in, int64_t R, int64
         const int64_t r = r0 + row, c = c0 + c8;
         uint32_t h[8];
         if (VEC && r < R && c < Cc) {
-            Raw8<DT> raw;
-            load_raw8<DT>(src + r * Cc + c, raw);
+            const Raw8<DT>& raw = raws[k];
+            // x / den through the reciprocal with one Markstein correction
+            // (correctly rounded while x, the first quotient and 1/den stay
+            // clear of the subnormal range); a wave with any lane outside
+            // that (zero, tiny or NaN x) takes the guarded division instead
+            float xs[8], qs[8];
+            bool bad = yden == 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = f2bf(bf16f(f2bf(raw_elem<DT>(raw, e))) / den);
+            for (int e = 0; e < 8; ++e) {
+                xs[e] = bf16f(f2bf(raw_elem<DT>(raw, e)));
+                const float q0 = xs[e] * yden;
+                qs[e] = __builtin_fmaf(__builtin_fmaf(-q0, den, xs[e]), yden, q0);
+                bad = bad || !(fabsf(xs[e]) >= 0x1p-100f) || !(fabsf(q0) >= 0x1p-100f);
+            }
+            if (__builtin_expect(__any(bad), 0)) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qs[e] = div_by_block(xs[e], den, yden);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = f2bf(qs[e]);
             const u32x4 pk = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
             *gbl(reinterpret_cast<u32x4*>(same + r * Cc + c)) = pk;
         } else {

@@ -766,6 +766,7 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
 // per block and wave (a max is exact in any order).
 // ====================================================================
 constexpr int kDetIters = 8;
+static_assert(kThreads == kCodebookMax, "one codebook entry per thread");
 // Stats records per block from which the block finalize takes a workgroup per block.
 constexpr int64_t kFinWideRecords = 32;
 static_assert(2 * kDetIters * kWaves == 64, "the workgroup's run partials fill one wave");
@@ -811,15 +812,111 @@ __device__ __forceinline__ void flush_det_max(uint32_t* mb, int64_t key, int64_t
     if ((threadIdx.x & 63) == 0 && key >= 0 && key < nb && m != 0u) gatomic_max(mb + key, m);
 }
 
+// A workgroup whose elements all lie in one block (every block of at least
+// E elements, most of them): no per-element block index and no segmented
+// scans.  The old magnitude is one scalar load; each lane sums its items in
+// iteration order, the waves combine by a fixed DPP pattern, then in wave
+// order -- the same order on every run.  FULL: the workgroup's E elements
+// all lie inside the tensor, so no load sits behind a branch.
+template <int DT, int EPL, bool FULL>
+__device__ __forceinline__ void stats_block_one(const TensorWork& w, int64_t wg, int64_t kb, float* s_cbr,
+                                                double* s_sum) {
+    using T = typename Elem<DT>::T;
+    const T* g = static_cast<const T*>(w.grad);
+    const int64_t N = w.N;
+    const MomentumCoef mc = w.mc;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t base = wg * (int64_t)(kDetIters * kThreads * EPL);
+    const float mo = sload(w.mag + kb);
+    // the codebook goes into a register first and into LDS after the element
+    // loads are issued (loaded in this block, so the LDS write waits for it alone)
+    const float cbr_v = *gbl(w.qt->cbr + threadIdx.x % kCodebookMax);
+    Raw8<DT> gr[kDetIters];
+    RawIdx8 ir[kDetIters];
+    float graw[kDetIters];
+    uint32_t iraw[kDetIters];
+#pragma unroll
+    for (int i = 0; i < kDetIters; ++i) {
+        const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
+        if (FULL || e0 < N) {
+            if constexpr (EPL == kChunk) {
+                load_raw8<DT>(g + e0, gr[i]);
+                ir[i] = load_raw_idx8(w.idx + e0);
+            } else {
+                graw[i] = to_f32<DT>(*gbl(g + e0));
+                iraw[i] = *gbl(w.idx + e0);
+            }
+        }
+        if constexpr (FULL) __builtin_amdgcn_sched_barrier(0);  // iteration order kept: iteration i lands i-th
+    }
+    s_cbr[threadIdx.x % kCodebookMax] = cbr_v;  // every thread: no branch, so the waits stay exact
+    __syncthreads();
+    double lsum = 0.0;
+    uint32_t lmax = 0u;
+#pragma unroll
+    for (int i = 0; i < kDetIters; ++i) {
+        const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
+        if (FULL || e0 < N) {
+            float cs = 0.0f;
+            if constexpr (EPL == kChunk) {
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) {
+                    const float gv = raw_elem<DT>(gr[i], k);
+                    const float u = momentum_value(s_cbr[raw_idx(ir[i], k)], mo, gv, mc);
+                    const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                    lmax = ub > lmax ? ub : lmax;
+                    float sq = gv * gv;
+                    if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                    cs += sq;
+                }
+            } else {
+                const float gv = graw[i];
+                const float u = momentum_value(s_cbr[iraw[i]], mo, gv, mc);
+                const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
+                lmax = ub > lmax ? ub : lmax;
+                float sq = gv * gv;
+                if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                cs = sq;
+            }
+            lsum += (double)cs;
+        }
+    }
+    lsum = wave_sum_d(lsum);
+    const uint32_t wmax = wave_max_u63(lmax);  // in lane 63
+    uint32_t* mb = w.magbits + (wg % w.shards) * w.nb;
+    if (lane == 63 && wmax != 0u) gatomic_max(mb + kb, wmax);
+    if (lane == 0) s_sum[wave] = lsum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int v = 0; v < kWaves; ++v) t += s_sum[v];
+        DetRec* rec = w.det_rec + wg;
+        rec->kf = kb;
+        rec->sf = t;
+        rec->kl = -1;
+        rec->sl = 0.0;
+    }
+}
+
 template <int DT, int EPL>
 __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg) {
     using T = typename Elem<DT>::T;
     __shared__ float s_cbr[kCodebookMax];
     __shared__ int64_t s_key[2 * kDetIters * kWaves];
     __shared__ double s_sum[2 * kDetIters * kWaves];
-    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(w.qt->cbr + threadIdx.x);
-    const T* g = static_cast<const T*>(w.grad);
     const int64_t N = w.N, P = w.P, nb = w.nb;
+    constexpr int64_t E = (int64_t)kDetIters * kThreads * EPL;
+    const int64_t base = wg * E;
+    const int64_t wg_end = base + E < N ? base + E : N;
+    const int64_t kfirst = div_floor(base, P, w.invP);
+    if (kfirst == div_floor(wg_end - 1, P, w.invP)) {
+        if (base + E <= N) stats_block_one<DT, EPL, true>(w, wg, kfirst, s_cbr, s_sum);
+        else stats_block_one<DT, EPL, false>(w, wg, kfirst, s_cbr, s_sum);
+        return;
+    }
+    const float cbr_v = *gbl(w.qt->cbr + threadIdx.x % kCodebookMax);  // to LDS after the element loads
+    const T* g = static_cast<const T*>(w.grad);
     const MomentumCoef mc = w.mc;
     // max |u|: a wave carries the max of its current block across iterations
     // and flushes it into its workgroup's shard when the block changes, so a
@@ -829,7 +926,6 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
     double* bsq = w.blk_sq;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t base = wg * (int64_t)(kDetIters * kThreads * EPL);
     // every iteration's loads first
     Raw8<DT> gr[kDetIters];
     RawIdx8 ir[kDetIters];
@@ -853,61 +949,8 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
             }
         }
     }
+    s_cbr[threadIdx.x % kCodebookMax] = cbr_v;  // every thread: no branch, so the waits stay exact
     __syncthreads();  // s_cbr
-    // a workgroup whose elements all lie in one block (every block of at least
-    // this many elements, most of them) needs no segmented scans: each lane
-    // sums its items in iteration order, the waves combine by a fixed DPP
-    // pattern, then in wave order -- still the same order on every run
-    const int64_t wg_end = base + (int64_t)(kDetIters * kThreads * EPL) < N ? base + (int64_t)(kDetIters * kThreads * EPL)
-                                                                             : N;
-    const int64_t kfirst = div_floor(base, P, w.invP);
-    if (kfirst == div_floor(wg_end - 1, P, w.invP)) {
-        double lsum = 0.0;
-        uint32_t lmax = 0u;
-#pragma unroll
-        for (int i = 0; i < kDetIters; ++i) {
-            const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
-            if (e0 < N) {
-                float cs = 0.0f;
-                if constexpr (EPL == kChunk) {
-#pragma unroll
-                    for (int k = 0; k < kChunk; ++k) {
-                        const float gv = raw_elem<DT>(gr[i], k);
-                        const float u = momentum_value(s_cbr[raw_idx(ir[i], k)], mo[i], gv, mc);
-                        const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                        lmax = ub > lmax ? ub : lmax;
-                        float sq = gv * gv;
-                        if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                        cs += sq;
-                    }
-                } else {
-                    const float gv = graw[i];
-                    const float u = momentum_value(s_cbr[iraw[i]], mo[i], gv, mc);
-                    const uint32_t ub = __float_as_uint(u) & 0x7fffffffu;
-                    lmax = ub > lmax ? ub : lmax;
-                    float sq = gv * gv;
-                    if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                    cs = sq;
-                }
-                lsum += (double)cs;
-            }
-        }
-        lsum = wave_sum_d(lsum);
-        const uint32_t wmax = wave_max_u63(lmax);  // in lane 63
-        if (lane == 63 && wmax != 0u && kfirst < nb) gatomic_max(mb + kfirst, wmax);
-        if (lane == 0) s_sum[wave] = lsum;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double t = 0.0;
-            for (int v = 0; v < kWaves; ++v) t += s_sum[v];
-            DetRec* rec = w.det_rec + wg;
-            rec->kf = kfirst;
-            rec->sf = t;
-            rec->kl = -1;
-            rec->sl = 0.0;
-        }
-        return;
-    }
     int64_t ck = -1;   // carried block and its running max (wave-uniform)
     uint32_t cm = 0u;
 #pragma unroll
@@ -1660,6 +1703,29 @@ __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, cons
     }
     Pos p1 = advance_fast<DT, MODE>(a, p0);
     ChunkIn<DT> A, B;
+    if ((wg + 1) * (kThreads * kApplyChunksPerThread) <= nchunks) {
+        // A full workgroup (all but a tensor's last): straight-line code with
+        // every load and store unconditional, so each wait names exactly the
+        // chunk about to be computed and the next two chunks stay in flight.
+        // (A load or store behind a branch makes the compiler assume, at the
+        // join, the path with fewer operations in flight, and the waits then
+        // drain the prefetched chunks as well.)
+        fast_load<DT, MODE>(a, p0, first * kChunk, A);
+        fast_load<DT, MODE>(a, p1, (first + kThreads) * kChunk, B);
+#pragma unroll
+        for (int i = 0; i < (int)kApplyChunksPerThread; i += 2) {
+            const int64_t ea = (first + (int64_t)i * kThreads) * kChunk;
+            const int64_t eb = ea + kThreads * kChunk;
+            const Pos p2 = advance_fast<DT, MODE>(a, p1);
+            const Pos p3 = advance_fast<DT, MODE>(a, p2);
+            fast_compute<DT, MODE, LF>(a, ft, ea, A);
+            if (i + 2 < (int)kApplyChunksPerThread) fast_load<DT, MODE>(a, p2, ea + 2 * kThreads * kChunk, A);
+            fast_compute<DT, MODE, LF>(a, ft, eb, B);
+            if (i + 3 < (int)kApplyChunksPerThread) fast_load<DT, MODE>(a, p3, eb + 2 * kThreads * kChunk, B);
+            p1 = p3;
+        }
+        return;
+    }
     fast_load<DT, MODE>(a, p0, first * kChunk, A);
     if (n > 1) fast_load<DT, MODE>(a, p1, (first + kThreads) * kChunk, B);
 #pragma unroll 1

@@ -558,3 +558,21 @@ def test_normuon_and_apply_batch_match_single_matrix_calls(dev, lib):
         assert torch.equal(sc, scale[i]), i
         assert torch.equal(v, vb[i]), i
         assert torch.equal(p, pb[i].contiguous()), i
+
+
+@pytest.mark.parametrize("shape", [(96, 256), (256, 96), (64, 200)])
+def test_newton_schulz_normalisation_is_exact(dev, lib, shape):
+    """An empty schedule returns the normalised X = bf16(bf16(G) / bf16(||G||))
+    itself: bit-exact against the oracle's float32 division (the kernel divides
+    through the reciprocal with a correction step; zeros, tiny values and a
+    denominator of awkward mantissa must all round as the true quotient)."""
+    gen = np.random.default_rng(11)
+    m = gen.standard_normal(shape).astype(np.float32) * np.float32(3.0)
+    m[0, :5] = 0.0
+    m[1, :3] = -0.0
+    m[2, :4] = np.float32(1e-32)
+    m[3, :7] = gen.standard_normal(7).astype(np.float32) * np.float32(1e-29)
+    print("ns normalisation", shape, flush=True)
+    out = _ns_gpu(dev, lib, m[None], [])[0]
+    ref = orc.newton_schulz(m, [])
+    np.testing.assert_array_equal(out.view(np.uint32), ref.astype(np.float32).view(np.uint32))
