@@ -258,7 +258,7 @@ class Gefen(torch.optim.Optimizer):
         self.verbose = verbose
         self._gefen_codebook = None
         self._gefen_codebook_by_device = {}
-        self._lr_slot = None  # (tensor lr, its _version, its value): see _lr_scalar
+        self._lr_scalar_cache = None  # (tensor lr, its _version, its value): see _lr_scalar
         self._gefen_global_step = 0
         self._param_names = {}
         # All parameters of a device go through one gefenx_multi_tensor_step
@@ -314,34 +314,48 @@ class Gefen(torch.optim.Optimizer):
             return [dict(g, **{self._PREFIX_KEY: "group_{}_param_".format(i)}) for i, g in enumerate(params)]
         return [{"params": params, self._PREFIX_KEY: "param_"}]
 
-    def _split_names(self, items, prefix):
+    def _split_names(self, items, prefix, group_name=None):
         """(names, tensors, synthesized flags) of a group's params, checked and
         named without registering anything (add_param_group registers the
-        names once the whole group is valid)."""
+        names once the whole group is valid).  gefen.py:1451-1499: a given
+        name is lowercased and kept as is (two parameters may share one; their
+        states stay separate); an unnamed parameter alone in a group with a
+        "name" takes that name, otherwise its positional <prefix><index>; a
+        generated name that is already taken gets the first free _<n> suffix
+        and counts as synthesized."""
         if isinstance(items, torch.Tensor):
             items = [items]
+        items = list(items)
         names, ps, synth = [], [], []
         seen = set(self._param_names.values())
-        for i, it in enumerate(list(items)):
+
+        def free(base):
+            if base not in seen:
+                return base
+            k = 1
+            while "{}_{}".format(base, k) in seen:
+                k += 1
+            return "{}_{}".format(base, k)
+
+        for i, it in enumerate(items):
             if isinstance(it, (tuple, list)) and len(it) == 2 and isinstance(it[0], str):
-                name, p = str(it[0]).lower(), it[1]
-                synth.append(False)
+                name, p, generated = str(it[0]).lower(), it[1], False
+            elif group_name is not None and len(items) == 1:
+                base = str(group_name).lower()
+                name, p = free(base), it
+                generated = name != base
             else:
-                name, p = "{}{}".format(prefix, i), it
-                synth.append(True)
+                name, p, generated = free("{}{}".format(prefix, i)), it, True
             if not isinstance(p, torch.Tensor):
                 raise TypeError("Gefen can only optimize Tensors, but one of the params is {}".format(
                     type(p).__name__))
             if torch.is_complex(p):
                 raise ValueError("Gefen does not support complex parameters, but got a parameter with dtype "
                                  "{}".format(p.dtype))
-            base, k = name, 1
-            while name in seen:
-                name = "{}_{}".format(base, k)
-                k += 1
             seen.add(name)
             names.append(name)
             ps.append(p)
+            synth.append(generated)
         return names, ps, synth
 
     def _check_group_params(self, params):
@@ -363,9 +377,13 @@ class Gefen(torch.optim.Optimizer):
         d = self.defaults
         self._validate_group_options(g.get("lr", d["lr"]), (g.get("beta1", d["beta1"]), g.get("beta2", d["beta2"])),
                                      g.get("eps", d["eps"]), g.get("weight_decay", d["weight_decay"]))
-        names, ps, synth = self._split_names(g["params"], prefix)
+        names, ps, synth = self._split_names(g["params"], prefix, g.get("name"))
         if len(ps) == 0:
             raise ValueError("optimizer got an empty parameter list")
+        if g.get("name") is not None:
+            g["name"] = str(g["name"]).lower()
+        elif len(names) == 1:
+            g["name"] = names[0]
         self._check_group_params(ps)
         existing = {id(p) for grp in self.param_groups for p in grp["params"]}
         batch = set()
@@ -377,6 +395,7 @@ class Gefen(torch.optim.Optimizer):
         super().add_param_group(g)
         for p, name in zip(ps, names):
             self._param_names[p] = name
+            self.state[p]["name"] = name  # gefen.py:1520-1525: every state carries its parameter's name
 
     def _iter_group_params_with_names(self, group):
         names = group.get("param_names") or [self._param_names.get(p, "param") for p in group["params"]]
@@ -580,11 +599,11 @@ class Gefen(torch.optim.Optimizer):
         lr = group["lr"]
         if not torch.is_tensor(lr):
             return float(lr)
-        hit = getattr(self, "_lr_slot", None)
+        hit = getattr(self, "_lr_scalar_cache", None)
         if hit is not None and hit[0] is lr and hit[1] == lr._version:
             return hit[2]
         value = float(lr.item())
-        self._lr_slot = (lr, lr._version, value)
+        self._lr_scalar_cache = (lr, lr._version, value)
         return value
 
     def _init_state(self, state, p, grad, name, factored):
@@ -1146,6 +1165,9 @@ class Gefen(torch.optim.Optimizer):
         for pid, name in names.items():
             if pid in id_map:
                 self.state[id_map[pid]]["name"] = name
+        for p in id_map.values():  # a checkpoint without names keeps the registered ones
+            if "name" not in self.state[p]:
+                self.state[p]["name"] = self._param_names.get(p, "none")
         for pid, tensors in saved.items():
             p = id_map.get(pid)
             if p is None:

@@ -184,7 +184,9 @@ class GefenMuonHybrid(torch.optim.Optimizer):
         for item in items:
             if not (isinstance(item, (tuple, list)) and len(item) == 2 and isinstance(item[0], str)):
                 raise TypeError("GefenMuonHybrid's single-argument form needs an nn.Module or (name, param) pairs "
-                                "(e.g. model.named_parameters()); bare tensors cannot be routed")
+                                "(e.g. model.named_parameters()), got a bare {}.  Bare tensors can't be routed by "
+                                "name (an embedding or head would land in Muon): pass the model or use "
+                                "GefenMuonHybrid.from_model(model, ...).".format(type(item).__name__))
         from gefen.params import is_muon_param
         muon = [(n, p) for n, p in items if p.requires_grad and is_muon_param(n, p, subs)]
         backup = [(n, p) for n, p in items if p.requires_grad and not is_muon_param(n, p, subs)]
@@ -225,7 +227,7 @@ class GefenMuonHybrid(torch.optim.Optimizer):
     def __repr__(self):
         nm = sum(len(g["params"]) for g in self.muon.param_groups) if self.muon is not None else 0
         nb = sum(len(g["params"]) for g in self.backup.param_groups) if self.backup is not None else 0
-        return "GefenMuonHybrid(muon={} params, backup={} params, backup_optimizer={!r})".format(
+        return "GefenMuonHybrid(muon_params={}, backup_params={}, backup_optimizer={!r})".format(
             nm, nb, self.backup_optimizer)
 
     # --------------------------------------------------------------- step

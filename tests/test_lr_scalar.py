@@ -62,12 +62,12 @@ def test_fresh_tensor_is_read_and_cache_holds_one_slot():
     for k in range(5):
         opt.param_groups[0]["lr"] = torch.tensor(1e-3 * (k + 1))
         assert opt._lr_scalar(opt.param_groups[0]) == float(torch.tensor(1e-3 * (k + 1)))
-    assert isinstance(opt._lr_slot, tuple) and len(opt._lr_slot) == 3
+    assert isinstance(opt._lr_scalar_cache, tuple) and len(opt._lr_scalar_cache) == 3
 
 
 def test_cache_not_in_param_groups_or_state_dict():
     opt = _opt(torch.tensor(1e-3))
     opt._lr_scalar(opt.param_groups[0])
     sd = opt.state_dict()
-    assert all("_lr_slot" not in g for g in sd["param_groups"])
-    assert "_lr_slot" not in sd
+    assert all("_lr_scalar_cache" not in g for g in sd["param_groups"])
+    assert "_lr_scalar_cache" not in sd
