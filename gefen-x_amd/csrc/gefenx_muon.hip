@@ -1207,6 +1207,9 @@ struct ApplyItem {
     float* v;               // normuon_v [R]
     const float* step_dev;  // capturable NorMuon step counter or nullptr
     float bc;               // 1 - beta2^step (host step)
+    const void* g;          // cautious: the raw gradient view (parameter dtype)
+    int64_t gs0, gs1;
+    const unsigned long long* count;  // cautious: agreeing elements of the matrix
 };
 struct ApplyBatch {
     ApplyItem it[kMaxBatch];
@@ -1294,12 +1297,46 @@ struct MuonApplyArgs {
     int wd;
 };
 
-// One element: u' = bf16(u * scale[row]) with a NorMuon scale, else u;
-// p = D(p * wdf) (when wd), then p = D(fma(u', alpha, p)).
+// Cautious masking (gefen_muon.py:396-405): an element keeps its update when
+// update * grad, in torch's promoted dtype (bf16 for a bf16 grad, else fp32),
+// is > 0; the kept ones are scaled by bf16(fp32(numel) / fp32(max(agree, 1))),
+// the others become a zero of their own sign.
 template <int DT>
+__device__ __forceinline__ bool cautious_agree(float u, float g) {
+    float prod = u * g;
+    if constexpr (DT == BF16) prod = bf16f(f2bf(prod));
+    return prod > 0.0f;
+}
+
+__device__ __forceinline__ float cautious_scale(int64_t numel, unsigned long long agree) {
+    return bf16f(f2bf((float)numel / (float)(agree > 0ull ? agree : 1ull)));
+}
+
+// The 8 grad elements of row r, columns c .. c+7 of a strided view.
+template <int DT>
+__device__ __forceinline__ void load_grad8(const void* gp, int64_t gs0, int64_t gs1, int64_t r, int64_t c,
+                                           float out[8]) {
+    using T = typename Elem<DT>::T;
+    const T* g = static_cast<const T*>(gp) + r * gs0;
+    if (gs1 == 1 && (reinterpret_cast<uintptr_t>(g + c) & 15) == 0) {
+        Raw8<DT> raw;
+        load_raw8<DT>(g + c, raw);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) out[k] = raw_elem<DT>(raw, k);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) out[k] = to_f32<DT>(*gbl(g + (c + k) * gs1));
+    }
+}
+
+// One element: u' = bf16(u * scale[row]) with a NorMuon scale, else u; with
+// CAUT the cautious mask (gv the grad element, cs the matrix's scale); then
+// p = D(p * wdf) (when wd), then p = D(fma(u', alpha, p)).
+template <int DT, bool CAUT>
 __device__ __forceinline__ float muon_elem(float u, float sc, bool has_scale, float pv, float wdf, bool wd,
-                                           float alpha) {
+                                           float alpha, float gv = 0.0f, float cs = 1.0f) {
     if (has_scale) u = bf16f(f2bf(u * sc));
+    if constexpr (CAUT) u = cautious_agree<DT>(u, gv) ? bf16f(f2bf(u * cs)) : u * 0.0f;
     if (wd) pv = round_dt<DT>(pv * wdf);
     return __builtin_fmaf(u, alpha, pv);
 }
@@ -1309,7 +1346,7 @@ __device__ __forceinline__ float muon_elem(float u, float sc, bool has_scale, fl
 // strides, one element at a time.
 constexpr int kApplyCpt = 4;
 
-template <int DT, bool FAST>
+template <int DT, bool FAST, bool CAUT>
 __global__ void __launch_bounds__(kT) k_muon_apply(MuonApplyArgs a, ApplyBatch bt) {
     using T = typename Elem<DT>::T;
     const ApplyItem& it = bt.it[blockIdx.y];
@@ -1323,6 +1360,8 @@ __global__ void __launch_bounds__(kT) k_muon_apply(MuonApplyArgs a, ApplyBatch b
     const int64_t N = a.R * a.C;
     const uint16_t* U = a.U + (int64_t)blockIdx.y * N;
     const uint16_t* S = has_scale ? a.scale + (int64_t)blockIdx.y * a.R : nullptr;
+    float cs = 1.0f;
+    if constexpr (CAUT) cs = cautious_scale(N, *gbl(it.count));
     if constexpr (FAST) {
         const int64_t nch = N / 8;
         const int64_t first = (int64_t)blockIdx.x * (kT * kApplyCpt) + threadIdx.x;
@@ -1343,22 +1382,86 @@ __global__ void __launch_bounds__(kT) k_muon_apply(MuonApplyArgs a, ApplyBatch b
             const int64_t ch = first + (int64_t)i * kT;
             if (ch >= nch) break;
             const uint32_t w[4] = {uv[i].x, uv[i].y, uv[i].z, uv[i].w};
+            float gv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if constexpr (CAUT) {
+                const int64_t r = div_floor(ch * 8, a.C, a.invC);
+                load_grad8<DT>(it.g, it.gs0, it.gs1, r, ch * 8 - r * a.C, gv);
+            }
             float o[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                o[e] = muon_elem<DT>(bf16f((uint16_t)(w[e >> 1] >> (16 * (e & 1)))), sc[i], has_scale,
-                                     raw_elem<DT>(pr[i], e), wdf, wd, alpha);
+                o[e] = muon_elem<DT, CAUT>(bf16f((uint16_t)(w[e >> 1] >> (16 * (e & 1)))), sc[i], has_scale,
+                                           raw_elem<DT>(pr[i], e), wdf, wd, alpha, gv[e], cs);
             store8<DT>(pp + ch * 8, o);
         }
     } else {
         for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
             const int64_t r = div_floor(e, a.C, a.invC);
             T* q = pp + r * it.ps0 + (e - r * a.C) * it.ps1;
-            const float o = muon_elem<DT>(bf16f(*gbl(U + e)), has_scale ? bf16f(*gbl(S + r)) : 1.0f, has_scale,
-                                          to_f32<DT>(*gbl(q)), wdf, wd, alpha);
+            float gv = 0.0f;
+            if constexpr (CAUT) gv = to_f32<DT>(*gbl(static_cast<const T*>(it.g) + r * it.gs0 + (e - r * a.C) * it.gs1));
+            const float o = muon_elem<DT, CAUT>(bf16f(*gbl(U + e)), has_scale ? bf16f(*gbl(S + r)) : 1.0f, has_scale,
+                                                to_f32<DT>(*gbl(q)), wdf, wd, alpha, gv, cs);
             *gbl(q) = from_f32<DT>(o);
         }
     }
+}
+
+// Cautious agreement counts of n matrices (grid (parts, n)): the update u'
+// as the apply forms it (NorMuon row scale included) against the raw grad;
+// one atomic per wave into the matrix's 64-bit counter (a count is exact in
+// any order).  C % 8 == 0: chunks of 8 along a row, else element by element.
+struct CautItem {
+    const void* g;
+    int64_t gs0, gs1;
+    unsigned long long* count;
+};
+struct CautBatch {
+    CautItem it[kMaxBatch];
+};
+
+__global__ void k_cautious_zero(CautBatch bt, int n) {
+    if ((int)threadIdx.x < n) *gbl(bt.it[threadIdx.x].count) = 0ull;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kT) k_cautious_count(const uint16_t* U, const uint16_t* S, int64_t R, int64_t C,
+                                                        double invC, CautBatch bt) {
+    const CautItem& it = bt.it[blockIdx.y];
+    const int64_t N = R * C;
+    const uint16_t* u = U + (int64_t)blockIdx.y * N;
+    const uint16_t* s = S ? S + (int64_t)blockIdx.y * R : nullptr;
+    uint32_t cnt = 0u;
+    if (C % 8 == 0) {
+        for (int64_t ch = (int64_t)blockIdx.x * kT + threadIdx.x; ch < N / 8; ch += (int64_t)gridDim.x * kT) {
+            const int64_t r = div_floor(ch * 8, C, invC);
+            const u32x4 uv = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(u + ch * 8)));
+            float gv[8];
+            load_grad8<DT>(it.g, it.gs0, it.gs1, r, ch * 8 - r * C, gv);
+            const float sc = s ? bf16f(*gbl(s + r)) : 1.0f;
+            const uint32_t w[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float x = bf16f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+                if (s) x = bf16f(f2bf(x * sc));
+                cnt += cautious_agree<DT>(x, gv[e]) ? 1u : 0u;
+            }
+        }
+    } else {
+        using T = typename Elem<DT>::T;
+        for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < N; e += (int64_t)gridDim.x * kT) {
+            const int64_t r = div_floor(e, C, invC);
+            float x = bf16f(*gbl(u + e));
+            if (s) x = bf16f(f2bf(x * bf16f(*gbl(s + r))));
+            const float gv = to_f32<DT>(*gbl(static_cast<const T*>(it.g) + r * it.gs0 + (e - r * C) * it.gs1));
+            cnt += cautious_agree<DT>(x, gv) ? 1u : 0u;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cnt += (uint32_t)__shfl_xor((int)cnt, off, 64);
+    if ((threadIdx.x & 63) == 0 && cnt != 0u)
+        (void)__hip_atomic_fetch_add(gbl(it.count), (unsigned long long)cnt, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 static unsigned grid_for(int64_t n, int64_t cap = 8192) {
@@ -1542,7 +1645,7 @@ static int normuon_batch(const char* fn, const gefenx_muon_item* items, int n, c
 
 static int apply_batch(const char* fn, const gefenx_muon_item* items, int n, int dtype, const void* update,
                        const void* row_scale, int64_t rows, int64_t cols, double lr, double weight_decay,
-                       double adjusted_lr, double lr_ratio, hipStream_t s) {
+                       double adjusted_lr, double lr_ratio, const uint64_t* cautious_counts, hipStream_t s) {
     int rc = check_dt(dtype, fn);
     if (rc) return rc;
     if (n < 0) return set_error(GEFENX_EINVAL, "%s: negative batch", fn);
@@ -1566,6 +1669,7 @@ static int apply_batch(const char* fn, const gefenx_muon_item* items, int n, int
     for (int i = 0; i < n; ++i) {
         const gefenx_muon_item& in = items[i];
         if (!in.param) return set_error(GEFENX_EINVAL, "%s: item %d has no parameter", fn, i);
+        if (cautious_counts && !in.grad) return set_error(GEFENX_EINVAL, "%s: cautious item %d has no grad", fn, i);
         fast[(size_t)i] = in.param_stride1 == 1 && in.param_stride0 == cols && cols % 8 == 0 && al16(in.param) &&
                           al16(U + (size_t)i * (size_t)N);
     }
@@ -1579,26 +1683,72 @@ static int apply_batch(const char* fn, const gefenx_muon_item* items, int n, int
             bt.it[i - i0].ps0 = items[i].param_stride0;
             bt.it[i - i0].ps1 = items[i].param_stride1;
             bt.it[i - i0].scalars = items[i].step_scalars;
+            if (cautious_counts) {
+                bt.it[i - i0].g = items[i].grad;
+                bt.it[i - i0].gs0 = items[i].grad_stride0;
+                bt.it[i - i0].gs1 = items[i].grad_stride1;
+                bt.it[i - i0].count = reinterpret_cast<const unsigned long long*>(cautious_counts + i);
+            }
         }
         a.U = U + (size_t)i0 * (size_t)N;
         a.scale = S ? S + (size_t)i0 * (size_t)rows : nullptr;
         const unsigned m = (unsigned)(i1 - i0);
+#define GX_APPLY(FASTV, CAUTV)                                                                         \
+    switch (dtype) {                                                                                   \
+        case F32: hipLaunchKernelGGL((k_muon_apply<F32, FASTV, CAUTV>), g, dim3(kT), 0, s, a, bt); break; \
+        case F16: hipLaunchKernelGGL((k_muon_apply<F16, FASTV, CAUTV>), g, dim3(kT), 0, s, a, bt); break; \
+        default: hipLaunchKernelGGL((k_muon_apply<BF16, FASTV, CAUTV>), g, dim3(kT), 0, s, a, bt); break; \
+    }
         if (fast[(size_t)i0]) {
             const dim3 g((unsigned)fwgs, m);
-            switch (dtype) {
-                case F32: hipLaunchKernelGGL((k_muon_apply<F32, true>), g, dim3(kT), 0, s, a, bt); break;
-                case F16: hipLaunchKernelGGL((k_muon_apply<F16, true>), g, dim3(kT), 0, s, a, bt); break;
-                default: hipLaunchKernelGGL((k_muon_apply<BF16, true>), g, dim3(kT), 0, s, a, bt); break;
-            }
+            if (cautious_counts) { GX_APPLY(true, true) } else { GX_APPLY(true, false) }
         } else {
             const dim3 g(grid_for(N, 16384), m);
-            switch (dtype) {
-                case F32: hipLaunchKernelGGL((k_muon_apply<F32, false>), g, dim3(kT), 0, s, a, bt); break;
-                case F16: hipLaunchKernelGGL((k_muon_apply<F16, false>), g, dim3(kT), 0, s, a, bt); break;
-                default: hipLaunchKernelGGL((k_muon_apply<BF16, false>), g, dim3(kT), 0, s, a, bt); break;
-            }
+            if (cautious_counts) { GX_APPLY(false, true) } else { GX_APPLY(false, false) }
         }
+#undef GX_APPLY
         i0 = i1;
+    }
+    return launch_check(fn);
+}
+
+static int cautious_count_batch(const char* fn, const gefenx_muon_item* items, int n, int dtype, const void* update,
+                                const void* row_scale, int64_t rows, int64_t cols, uint64_t* counts,
+                                hipStream_t s) {
+    int rc = check_dt(dtype, fn);
+    if (rc) return rc;
+    if (n < 0) return set_error(GEFENX_EINVAL, "%s: negative batch", fn);
+    if (n == 0) return GEFENX_OK;
+    if (!items || !update || !counts) return set_error(GEFENX_EINVAL, "%s: null pointer argument", fn);
+    if (rows < 0 || cols < 0) return set_error(GEFENX_EINVAL, "%s: negative shape", fn);
+    for (int i = 0; i < n; ++i)
+        if (!items[i].grad) return set_error(GEFENX_EINVAL, "%s: item %d has no grad", fn, i);
+    const int64_t N = rows * cols;
+    if (N > 0 && cols % 8 == 0 && !al16(update)) return set_error(GEFENX_EINVAL, "%s: update not 16-byte aligned", fn);
+    const uint16_t* U = static_cast<const uint16_t*>(update);
+    const uint16_t* S = static_cast<const uint16_t*>(row_scale);
+    for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
+        const int m = std::min(n - i0, kMaxBatch);
+        CautBatch bt;
+        std::memset(&bt, 0, sizeof(bt));
+        for (int i = 0; i < m; ++i) {
+            bt.it[i].g = items[i0 + i].grad;
+            bt.it[i].gs0 = items[i0 + i].grad_stride0;
+            bt.it[i].gs1 = items[i0 + i].grad_stride1;
+            bt.it[i].count = reinterpret_cast<unsigned long long*>(counts + i0 + i);
+        }
+        // counters cleared by a kernel (no memset node under graph capture)
+        hipLaunchKernelGGL(k_cautious_zero, dim3(1), dim3(kMaxBatch), 0, s, bt, m);
+        if (N == 0) continue;
+        const dim3 g(grid_for(cols % 8 == 0 ? N / 8 : N, 2048), (unsigned)m);
+        const uint16_t* Ui = U + (size_t)i0 * (size_t)N;
+        const uint16_t* Si = S ? S + (size_t)i0 * (size_t)rows : nullptr;
+        const double invC = 1.0 / (double)cols;
+        switch (dtype) {
+            case F32: hipLaunchKernelGGL(k_cautious_count<F32>, g, dim3(kT), 0, s, Ui, Si, rows, cols, invC, bt); break;
+            case F16: hipLaunchKernelGGL(k_cautious_count<F16>, g, dim3(kT), 0, s, Ui, Si, rows, cols, invC, bt); break;
+            default: hipLaunchKernelGGL(k_cautious_count<BF16>, g, dim3(kT), 0, s, Ui, Si, rows, cols, invC, bt); break;
+        }
     }
     return launch_check(fn);
 }
@@ -1776,14 +1926,21 @@ int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_sc
     it.param_stride1 = 1;
     it.step_scalars = step_scalars;
     return apply_batch("gefenx_muon_apply", &it, 1, dtype, update, row_scale, rows, cols, lr, weight_decay,
-                       adjusted_lr, lr_ratio, static_cast<hipStream_t>(stream));
+                       adjusted_lr, lr_ratio, nullptr, static_cast<hipStream_t>(stream));
 }
 
 int gefenx_muon_apply_batch(const gefenx_muon_item* items, int n, int dtype, const void* update,
                             const void* row_scale, int64_t rows, int64_t cols, double lr, double weight_decay,
-                            double adjusted_lr, double lr_ratio, void* stream) {
+                            double adjusted_lr, double lr_ratio, const uint64_t* cautious_counts, void* stream) {
     return apply_batch("gefenx_muon_apply_batch", items, n, dtype, update, row_scale, rows, cols, lr, weight_decay,
-                       adjusted_lr, lr_ratio, static_cast<hipStream_t>(stream));
+                       adjusted_lr, lr_ratio, cautious_counts, static_cast<hipStream_t>(stream));
+}
+
+int gefenx_muon_cautious_count_batch(const gefenx_muon_item* items, int n, int dtype, const void* update,
+                                     const void* row_scale, int64_t rows, int64_t cols, uint64_t* counts,
+                                     void* stream) {
+    return cautious_count_batch("gefenx_muon_cautious_count_batch", items, n, dtype, update, row_scale, rows, cols,
+                                counts, static_cast<hipStream_t>(stream));
 }
 
 int gefenx_gemm_nt_bf16(const void* A, const void* B, const void* C, void* D, int64_t M, int64_t N, int64_t K,

@@ -234,8 +234,6 @@ class GefenMuon(Gefen):
             raise ValueError("normuon_beta2 must be in [0, 1) but is: {}".format(normuon_beta2))
         if not math.isfinite(normuon_eps) or normuon_eps <= 0.0:
             raise ValueError("normuon_eps must be finite and > 0 but is: {}".format(normuon_eps))
-        if cautious:
-            raise NotImplementedError("cautious masking is not part of this build's Muon step")
         self._sharded_mode = sharded_mode
         self._fp8_ns = fp8_ns
         self._fp8_ns_compile = fp8_ns_compile
@@ -446,6 +444,15 @@ class GefenMuon(Gefen):
             shape = chunk[0][2].shape
             ratio = _adjust_lr_ratio(group["adjust_lr_fn"], shape)
             adjusted = 0.0 if self._capt_on else _adjust_lr(lr, group["adjust_lr_fn"], shape)
+            pcode = _fused._dtype_code(chunk[0][2].dtype)
+            counts_ptr = None
+            if group.get("cautious", False):
+                # gefen_muon.py:1160-1161: the NorMuon-scaled update against the raw grad
+                counts = self._buffer(("caut", device), n, torch.int64, device)
+                _native.check(lib.gefenx_muon_cautious_count_batch(
+                    items, n, pcode, ortho.data_ptr(), scale_ptr, rows, cols, counts.data_ptr(), stream),
+                    "cautious mask of " + chunk[0][1])
+                counts_ptr = counts.data_ptr()
             _native.check(lib.gefenx_muon_apply_batch(
-                items, n, _fused._dtype_code(chunk[0][2].dtype), ortho.data_ptr(), scale_ptr, rows, cols, lr,
-                float(wd) if wd > 0.0 else 0.0, adjusted, ratio, stream), "muon apply of " + chunk[0][1])
+                items, n, pcode, ortho.data_ptr(), scale_ptr, rows, cols, lr,
+                float(wd) if wd > 0.0 else 0.0, adjusted, ratio, counts_ptr, stream), "muon apply of " + chunk[0][1])

@@ -129,7 +129,8 @@ SIGNATURES = {
     "gefenx_muon_momentum_batch": (_I, [_P, _I, _I, _I64, _I64, _P, _P, _D, _I, _I64, _P, _I, _P]),
     "gefenx_normuon_batch_workspace_bytes": (_SZ, [_I, _I64]),
     "gefenx_normuon_scale_batch": (_I, [_P, _I, _P, _I64, _I64, _D, _D, _P, _P, _SZ, _P]),
-    "gefenx_muon_apply_batch": (_I, [_P, _I, _I, _P, _P, _I64, _I64, _D, _D, _D, _D, _P]),
+    "gefenx_muon_apply_batch": (_I, [_P, _I, _I, _P, _P, _I64, _I64, _D, _D, _D, _D, _P, _P]),
+    "gefenx_muon_cautious_count_batch": (_I, [_P, _I, _I, _P, _P, _I64, _I64, _P, _P]),
     "gefenx_gemm_nt_bf16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _P]),
     "gefenx_profile_enable": (_I, [_I]),
     "gefenx_profile_read": (_I, [_I, _P, _P, _P, _P]),

@@ -417,10 +417,25 @@ int gefenx_normuon_scale_batch(const gefenx_muon_item* items, int n, const void*
                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* gefenx_muon_apply for n matrices: update [n, rows, cols] bf16, row_scale
- * [n, rows] bf16 or NULL; each item's param, strides and step_scalars. */
+ * [n, rows] bf16 or NULL; each item's param, strides and step_scalars.
+ * cautious_counts: NULL, or the agreement counts of
+ * gefenx_muon_cautious_count_batch for the same items and update: then each
+ * update element is cautiously masked (gefen_muon.py:396-405, 1148-1162)
+ * against the item's grad after the NorMuon row scale. */
 int gefenx_muon_apply_batch(const gefenx_muon_item* items, int n, int dtype, const void* update,
                             const void* row_scale, int64_t rows, int64_t cols, double lr,
-                            double weight_decay, double adjusted_lr, double lr_ratio, void* stream);
+                            double weight_decay, double adjusted_lr, double lr_ratio,
+                            const uint64_t* cautious_counts, void* stream);
+
+/* Cautious-mask agreement counts (gefen_muon.py:396-405): counts[i] (device
+ * uint64) = #elements of matrix i where u' * grad > 0, u' the bf16 update
+ * [n, rows, cols] (times row_scale [n, rows] bf16 when not NULL, rounded to
+ * bf16) and grad the item's gradient view of dtype `dtype`, the product
+ * taken in torch's promoted dtype (bf16 for bf16 grads, else fp32).  The
+ * counters are cleared by the call (a kernel, so it can be captured). */
+int gefenx_muon_cautious_count_batch(const gefenx_muon_item* items, int n, int dtype, const void* update,
+                                     const void* row_scale, int64_t rows, int64_t cols, uint64_t* counts,
+                                     void* stream);
 
 /* NorMuon row scale of a bf16 update [rows, cols] (gefen_muon.py:1192-1230):
  * normuon_v (fp32 [rows], mutated) <- v*beta2 + row_sq*((1-beta2)/cols);

@@ -256,6 +256,23 @@ def normuon(ortho, v, step: int, beta2: float = 0.95, eps: float = 1e-8):
     return bf16(o * scale[:, None]), v
 
 
+def cautious_mask(update, grad, grad_dtype: int) -> np.ndarray:
+    """_cautious_mask_: gefen_muon.py:396-405.  update: the bf16 update after
+    Newton-Schulz (and NorMuon); grad: the raw gradient, of grad_dtype.  The
+    sign test is on update * grad in torch's promoted dtype (bf16 for a bf16
+    grad, else fp32); scale = fp32(numel) / fp32(max(agree, 1)), applied as a
+    bf16 multiplier; a masked element keeps the sign of its zero."""
+    u = bf16(update)
+    g = round_dtype(np.asarray(grad, np.float32), grad_dtype)
+    prod = (u * g).astype(np.float32)
+    if grad_dtype == BF16:
+        prod = bf16(prod)
+    mask = prod > np.float32(0.0)
+    agree = max(int(mask.sum()), 1)
+    scale = bf16(np.array([np.float32(mask.size) / np.float32(agree)], np.float32))[0]
+    return bf16((u * mask.astype(np.float32)).astype(np.float32) * scale)
+
+
 def adjust_lr_ratio(fn, shape) -> float:
     """_adjust_lr_ratio: gefen_muon.py:409-419."""
     rows, cols = shape[:2]

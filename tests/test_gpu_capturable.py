@@ -373,9 +373,10 @@ HYBRID_MUON_SPECS = [("h1.weight", (64, 48)), ("h2.weight", (32, 64))]
 HYBRID_BACKUP_SPECS = [("embed.weight", (96, 32)), ("norm.weight", (64,))]
 
 
-def _muon(params, lr, sr=False, capturable=True):
+def _muon(params, lr, sr=False, capturable=True, cautious=False):
     from gefen import GefenMuon
-    return GefenMuon(params, lr=lr, weight_decay=WD, normuon=True, stochastic_round=sr, capturable=capturable)
+    return GefenMuon(params, lr=lr, weight_decay=WD, normuon=True, stochastic_round=sr, capturable=capturable,
+                     cautious=cautious)
 
 
 def _hybrid(params, lr, backup="gefen", sr=False, capturable=True):
@@ -418,6 +419,15 @@ def test_muon_graph_replay_matches_eager_every_step(dev, sr):
         lr32 = float(np.float32(lr_sched[-1]))
         assert got[0] == lr32 and got[3] == float(np.float32(1.0 - lr32 * WD)), got
     assert opt.state_dict()["gefen_global_step"] == steps
+
+
+def test_muon_cautious_graph_replay_matches_eager_every_step(dev):
+    """Cautious masking inside a captured step: its counters are cleared by a
+    kernel, so every replay recounts."""
+    _say("muon cautious lockstep replay")
+    opt, params, _, steps, _, _ = _lockstep(dev, MUON_SPECS, torch.bfloat16, False, False, seed=13,
+                                            make=lambda ps, lr: _muon(ps, lr, cautious=True))
+    assert _counter_values(opt) == {float(steps)}
 
 
 @pytest.mark.parametrize("backup", ["gefen", "adamw"])

@@ -544,7 +544,7 @@ def test_normuon_and_apply_batch_match_single_matrix_calls(dev, lib):
     _check(lib.gefenx_normuon_scale_batch(items, n, upd.data_ptr(), rows, cols, 0.95, 1e-8, scale.data_ptr(),
                                           nws.data_ptr(), nws.numel(), _stream(dev)), lib)
     _check(lib.gefenx_muon_apply_batch(items, n, 2, upd.data_ptr(), scale.data_ptr(), rows, cols, 0.02, 0.1,
-                                       0.02 * 0.2 * 8.0, 1.0, _stream(dev)), lib)
+                                       0.02 * 0.2 * 8.0, 1.0, None, _stream(dev)), lib)
     for i in range(n):
         p = torch.from_numpy(p0[i]).to(torch.bfloat16).to(dev)
         v = torch.from_numpy(v0[i].copy()).to(dev)
