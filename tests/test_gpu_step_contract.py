@@ -98,3 +98,59 @@ def test_bf16_vmean_is_the_model_dtype_square(dev):
     automatic_vmean_update_cuda(out, g.to(dev), 0.999)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), expected)
+
+
+def _clone_tree(v):
+    if torch.is_tensor(v):
+        return v.detach().clone()
+    if isinstance(v, dict):
+        return {k: _clone_tree(x) for k, x in v.items()}
+    if isinstance(v, (list, tuple)):
+        return type(v)(_clone_tree(x) for x in v)
+    return v
+
+
+def _same_tree(a, b):
+    if torch.is_tensor(b):
+        return torch.is_tensor(a) and a.dtype == b.dtype and torch.equal(a.to_dense() if a.is_sparse else a,
+                                                                          b.to_dense() if b.is_sparse else b)
+    if isinstance(b, dict):
+        return isinstance(a, dict) and set(a) == set(b) and all(_same_tree(a[k], b[k]) for k in b)
+    if isinstance(b, (list, tuple)):
+        return len(a) == len(b) and all(_same_tree(x, y) for x, y in zip(a, b))
+    return a == b
+
+
+@pytest.mark.parametrize("kind", ["gefen", "muon", "hybrid_gefen", "hybrid_adamw"])
+def test_later_sparse_gradient_is_refused_before_any_mutation(dev, kind):
+    """tests/test_step_preflight_atomicity.py (reference): once the first
+    parameter has state, a step whose second gradient is sparse raises before
+    anything moves: parameters, every state tensor, the global step and the
+    codebook are unchanged."""
+    from gefen import Gefen, GefenMuon, GefenMuonHybrid
+    gen = torch.Generator().manual_seed(991)
+    first = nn.Parameter((torch.randn(8, 8, generator=gen) * 0.02).to(dev))
+    invalid = nn.Parameter(torch.eye(8, device=dev).to_sparse())
+    if kind == "gefen":
+        opt = Gefen([("first", first), ("invalid", invalid)], lr=2e-3, factored_v_2d=False)
+    elif kind == "muon":
+        opt = GefenMuon([("first", first), ("invalid", invalid)], lr=2e-3, ns_steps=1)
+    else:
+        opt = GefenMuonHybrid([("first", first)], [("invalid", invalid)], lr=2e-3, ns_steps=1,
+                              ns_schedule="standard", normuon=False, backup_optimizer=kind.split("_")[1])
+    first.grad = torch.full_like(first, 0.002)
+    opt.step()
+    opt.zero_grad(set_to_none=True)
+    first.grad = torch.full_like(first, -0.003)
+    invalid.grad = torch.eye(8, device=dev).to_sparse()
+    torch.cuda.synchronize()
+    children = [c for c in ((opt.muon, opt.backup) if kind.startswith("hybrid") else (opt,)) if isinstance(c, Gefen)]
+    before = (first.detach().clone(), _clone_tree(opt.state_dict()),
+              [(c._gefen_global_step, _clone_tree(c._gefen_codebook)) for c in children])
+    with pytest.raises(RuntimeError, match="sparse|strided|layout"):
+        opt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(first, before[0])
+    assert _same_tree(opt.state_dict(), before[1])
+    for c, (gs, cb) in zip(children, before[2]):
+        assert c._gefen_global_step == gs and _same_tree(c._gefen_codebook, cb)
