@@ -154,6 +154,56 @@ def _zeropower_via_newtonschulz(grad: torch.Tensor, ns_coefficients, ns_steps: i
     return _zeropower_via_newtonschulz_batched(grad.unsqueeze(0), ns_coefficients, ns_steps, eps)[0]
 
 
+def _masked_copy_into_(update: torch.Tensor, grad, row_scale, counts) -> torch.Tensor:
+    """update <- u'' in place through the Muon apply kernel applied to a
+    buffer of -0: with lr 0, no weight decay and adjusted_lr -1 the apply
+    computes fma(u'', 1, -0) = u'' (signed zeros included), u'' the update
+    times the NorMuon row scale (row_scale) and/or cautiously masked (counts)."""
+    lib = _native.load()
+    rows, cols = update.shape
+    u = update.contiguous()
+    out_dtype = grad.dtype if grad is not None else torch.bfloat16
+    out = torch.full((rows, cols), -0.0, dtype=out_dtype, device=update.device)
+    item = (_native.MuonItem * 1)()
+    item[0].param = out.data_ptr()
+    item[0].param_stride0, item[0].param_stride1 = out.stride()
+    if grad is not None:
+        item[0].grad = grad.data_ptr()
+        item[0].grad_stride0, item[0].grad_stride1 = grad.stride()
+    with torch.cuda.device(update.device):
+        _native.check(lib.gefenx_muon_apply_batch(
+            item, 1, _fused._dtype_code(out_dtype), u.data_ptr(),
+            None if row_scale is None else row_scale.data_ptr(), rows, cols, 0.0, 0.0, -1.0, 1.0,
+            None if counts is None else counts.data_ptr(), _stream_of(update)), "muon update copy")
+    update.copy_(out)
+    return update
+
+
+def _cautious_mask_(update: torch.Tensor, grad: torch.Tensor) -> torch.Tensor:
+    """gefen_muon.py:396-405 on the GPU, in place: zero the elements of the bf16
+    update whose product with grad (in torch's promoted dtype) is not > 0 and
+    scale the rest by bf16(numel / max(agree, 1)).  The step itself masks
+    inside its apply pass; this is the standalone form of the same kernels.
+    (An fp16 grad stages the result through fp16, exact for bf16 values inside
+    fp16's range.)"""
+    if update.dim() != 2 or update.shape != grad.shape:
+        raise ValueError("_cautious_mask_ expects a 2D update and a grad of the same shape")
+    if update.dtype != torch.bfloat16 or update.device.type != "cuda" or grad.device != update.device:
+        raise ValueError("_cautious_mask_ expects a bf16 update and its grad on one HIP device")
+    lib = _native.load()
+    rows, cols = update.shape
+    u = update.contiguous()
+    item = (_native.MuonItem * 1)()
+    item[0].grad = grad.data_ptr()
+    item[0].grad_stride0, item[0].grad_stride1 = grad.stride()
+    counts = torch.empty(1, dtype=torch.int64, device=update.device)
+    with torch.cuda.device(update.device):
+        _native.check(lib.gefenx_muon_cautious_count_batch(
+            item, 1, _fused._dtype_code(grad.dtype), u.data_ptr(), None, rows, cols, counts.data_ptr(),
+            _stream_of(update)), "cautious mask")
+    return _masked_copy_into_(update, grad, None, counts)
+
+
 def _swapped_param_groups_error(param: torch.Tensor) -> str:
     return ("GefenMuon only optimizes 2D parameters, got a parameter of shape {}. Route 1D (norm/bias) and "
             "embedding/head parameters to a plain Gefen/AdamW backup (GefenMuonHybrid / split_params_for_muon "
@@ -252,6 +302,37 @@ class GefenMuon(Gefen):
         super().__init__(params, lr=lr, betas=(momentum, 0.0), eps=eps, weight_decay=weight_decay, fused=fused,
                          factored_v_2d=False, stochastic_round=stochastic_round, deterministic=deterministic,
                          capturable=capturable, verbose=verbose)
+
+    def _normuon_normalize(self, state, ortho: torch.Tensor, beta2: float, eps: float) -> torch.Tensor:
+        """gefen_muon.py:1192-1230 for one bf16 update, in place: the NorMuon
+        row scale of gefenx_normuon_scale (normuon_v and normuon_step created
+        in `state` when missing, then advanced) applied through the Muon apply
+        kernel.  The step itself scales inside its apply pass."""
+        if ortho.dim() != 2 or ortho.dtype != torch.bfloat16 or ortho.device.type != "cuda":
+            raise ValueError("_normuon_normalize expects a 2D bf16 update on a HIP device")
+        rows, cols = ortho.shape
+        v = state.get("normuon_v")
+        if v is None or v.shape[0] != rows:
+            v = torch.zeros(rows, 1, dtype=torch.float32, device=ortho.device)
+            state["normuon_v"] = v
+            state["normuon_step"] = self._new_step_counter(ortho.device)
+        lib = _native.load()
+        u = ortho.contiguous()
+        scale = torch.empty(rows, dtype=torch.bfloat16, device=ortho.device)
+        ws = torch.empty(int(lib.gefenx_normuon_workspace_bytes(rows)), dtype=torch.uint8, device=ortho.device)
+        step_dev = None
+        if torch.is_tensor(state["normuon_step"]):
+            state["normuon_step"] += 1
+            step_dev = state["normuon_step"].data_ptr()
+            step = 0
+        else:
+            state["normuon_step"] += 1
+            step = int(state["normuon_step"])
+        with torch.cuda.device(ortho.device):
+            _native.check(lib.gefenx_normuon_scale(
+                u.data_ptr(), rows, cols, v.data_ptr(), float(beta2), step, float(eps), scale.data_ptr(),
+                ws.data_ptr(), ws.numel(), step_dev, _stream_of(ortho)), "normuon")
+        return _masked_copy_into_(ortho, None, scale, None)
 
     def add_param_group(self, param_group):
         """Muon defaults filled into the group, its NorMuon options checked,

@@ -125,3 +125,33 @@ def test_lr_scalar_single_slot_contract():
     assert opt._lr_scalar(opt.param_groups[0]) == 1e-3
     assert getattr(opt, "_lr_scalar_cache", None) is None
     assert GefenMuon._lr_scalar is Gefen._lr_scalar
+
+
+class _FrozenLM(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(32, 16)
+        self.proj = nn.Linear(16, 16)
+        self.norm = nn.LayerNorm(16)
+        self.lm_head = nn.Linear(16, 32, bias=False)
+        self.frozen = nn.Linear(16, 16)
+        self.frozen.weight.requires_grad_(False)
+        self.frozen.bias.requires_grad_(False)
+
+
+def test_from_model_covers_every_trainable_parameter_and_only_those():
+    model = _FrozenLM()
+    opt = GefenMuonHybrid.from_model(model, lr=1e-3)
+    assert {id(p) for g in opt.param_groups for p in g["params"]} == {id(p) for p in model.parameters()
+                                                                       if p.requires_grad}
+
+
+def test_per_half_lr_and_the_hybrid_surface():
+    model = _FrozenLM()
+    opt = GefenMuonHybrid.from_model(model, lr=1e-3, backup_lr=5e-4)
+    lrs = {g["lr"] for g in opt.param_groups}
+    assert 5e-4 in lrs and any(abs(lr - 5e-4) > 1e-12 for lr in lrs)
+    with pytest.raises(NotImplementedError):
+        opt.add_param_group({"params": [nn.Parameter(torch.randn(4, 4))]})
+    with pytest.warns(UserWarning, match="adjust_lr_fn"):
+        GefenMuonHybrid.from_model(_FrozenLM(), lr=1e-3, adjust_lr_fn=None)
