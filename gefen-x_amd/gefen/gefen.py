@@ -1119,8 +1119,9 @@ class Gefen(torch.optim.Optimizer):
                 raise ValueError("Gefen checkpoint top-level and parameter-group deterministic policies disagree")
         if deterministic is not None and deterministic != self._deterministic:
             raise ValueError("Gefen checkpoint deterministic={!r}, but this optimizer was constructed with "
-                             "deterministic={!r}; refusing to change the replica-determinism policy "
-                             "silently".format(deterministic, self._deterministic))
+                             "deterministic={!r}.  Resuming under another replica-determinism policy requires "
+                             "an intentional state migration or a fresh optimizer; refusing to change the "
+                             "policy silently.".format(deterministic, self._deterministic))
         return (0 if global_step is None else global_step), codebook, deterministic
 
     def load_state_dict(self, state_dict):

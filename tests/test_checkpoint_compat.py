@@ -130,3 +130,54 @@ def test_loading_a_codebookless_state_clears_the_codebook():
     assert opt._gefen_codebook is None
     assert opt._gefen_codebook_by_device == {}
     assert opt._gefen_global_step == 0
+
+
+def _state_equal(a, b):
+    if torch.is_tensor(b):
+        return torch.is_tensor(a) and a.dtype == b.dtype and torch.equal(a, b)
+    if isinstance(b, dict):
+        return isinstance(a, dict) and set(a) == set(b) and all(_state_equal(a[k], b[k]) for k in b)
+    if isinstance(b, (list, tuple)):
+        return len(a) == len(b) and all(_state_equal(x, y) for x, y in zip(a, b))
+    return a == b
+
+
+def test_determinism_policy_tags():
+    """tests/test_deterministic_mode.py (reference): a checkpoint of the other
+    policy is refused before anything changes, also in the DCP shape (group
+    metadata only); tags must be real bools at both levels; an untagged
+    legacy checkpoint loads under the live policy; a matching tag loads."""
+    sd, ref = _load("fact_bf16")  # written with deterministic=False
+    assert sd["gefen_deterministic"] is False
+    _, opt = _opt("fact_bf16", ref, deterministic=True)
+    before = copy.deepcopy(opt.state_dict())
+    with pytest.raises(ValueError, match="intentional state migration"):
+        opt.load_state_dict(copy.deepcopy(sd))
+    assert _state_equal(opt.state_dict(), before)
+    dcp = {"state": copy.deepcopy(sd["state"]), "param_groups": copy.deepcopy(sd["param_groups"])}
+    with pytest.raises(ValueError, match="intentional state migration"):
+        opt.load_state_dict(dcp)
+    assert _state_equal(opt.state_dict(), before)
+    for tag in (None, 0, 1, "true"):
+        bad = copy.deepcopy(sd)
+        bad["gefen_deterministic"] = tag
+        _, o = _opt("fact_bf16", ref)
+        b0 = copy.deepcopy(o.state_dict())
+        with pytest.raises(ValueError, match="top-level deterministic policy must be a bool"):
+            o.load_state_dict(bad)
+        assert _state_equal(o.state_dict(), b0)
+    bad = copy.deepcopy(sd)
+    bad["param_groups"][0]["_gefen_checkpoint_metadata"]["deterministic"] = 1
+    _, o = _opt("fact_bf16", ref)
+    with pytest.raises(ValueError, match="parameter-group deterministic policy must be a bool"):
+        o.load_state_dict(bad)
+    legacy = copy.deepcopy(sd)
+    legacy.pop("gefen_deterministic")
+    for g in legacy["param_groups"]:
+        g["_gefen_checkpoint_metadata"].pop("deterministic")
+    _, o = _opt("fact_bf16", ref, deterministic=True)
+    o.load_state_dict(legacy)
+    assert o._deterministic is True
+    _, o = _opt("fact_bf16", ref, deterministic=False)
+    o.load_state_dict(copy.deepcopy(sd))
+    assert o._gefen_global_step == 3

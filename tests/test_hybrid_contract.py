@@ -155,3 +155,12 @@ def test_per_half_lr_and_the_hybrid_surface():
         opt.add_param_group({"params": [nn.Parameter(torch.randn(4, 4))]})
     with pytest.warns(UserWarning, match="adjust_lr_fn"):
         GefenMuonHybrid.from_model(_FrozenLM(), lr=1e-3, adjust_lr_fn=None)
+
+
+def test_one_determinism_policy_reaches_both_gefen_children():
+    opt = GefenMuonHybrid.from_model(nn.Sequential(nn.Linear(8, 8), nn.LayerNorm(8)), lr=1e-3,
+                                     backup_optimizer="gefen", deterministic=True)
+    assert opt._deterministic is True
+    assert opt.muon is not None and opt.muon._deterministic is True
+    assert opt.backup is not None and opt.backup._deterministic is True
+    assert set(opt.state_dict()) == {"muon", "backup", "backup_optimizer"}
