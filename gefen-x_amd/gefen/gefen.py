@@ -199,6 +199,17 @@ def _amp_gate(optimizer) -> bool:
     return _amp_prepare_step(optimizer)
 
 
+def _preflight_torch_groups(optimizer, saved_groups) -> None:
+    """torch.optim.Optimizer.load_state_dict's own refusals, made before any
+    load: the number of parameter groups and each group's size."""
+    groups = optimizer.param_groups
+    if len(groups) != len(saved_groups):
+        raise ValueError("loaded state dict has a different number of parameter groups")
+    if any(len(g["params"]) != len(sg["params"]) for g, sg in zip(groups, saved_groups)):
+        raise ValueError("loaded state dict contains a parameter group that doesn't match the size of "
+                         "optimizer's group")
+
+
 class Gefen(torch.optim.Optimizer):
     """Gefen optimizer (see module docstring).
 
@@ -1124,9 +1135,40 @@ class Gefen(torch.optim.Optimizer):
                              "policy silently.".format(deterministic, self._deterministic))
         return (0 if global_step is None else global_step), codebook, deterministic
 
+    def _preflight_state_dict(self, state_dict) -> None:
+        """Every refusal load_state_dict can make, made without changing
+        anything: the checkpoint metadata and codebook checks, then torch's
+        own group-count and group-size checks.  A composite owner (the hybrid)
+        runs this on both halves before loading either (hybrid.py:795-920)."""
+        sd = dict(state_dict)
+        global_step = sd.pop("gefen_global_step", None)
+        has_det = "gefen_deterministic" in sd
+        deterministic = sd.pop("gefen_deterministic", None)
+        codebook = sd.pop("gefen_codebook", None)
+        groups = list(sd.get("param_groups") or [])
+        metas = [g["_gefen_checkpoint_metadata"] for g in groups if "_gefen_checkpoint_metadata" in g]
+        _, codebook, _ = self._checkpoint_metadata(metas, len(groups), global_step, codebook, deterministic, has_det)
+        if any(isinstance(st, dict) and "m_codebook" in st for st in (sd.get("state") or {}).values()) \
+                and codebook is None:
+            raise ValueError("Gefen checkpoint contains quantized momentum indices but no frozen codebook; loading "
+                             "it would reinterpret the restored indices with a different codebook")
+        _preflight_torch_groups(self, groups)
+
     def load_state_dict(self, state_dict):
         """gefen.py:5456-5707: restore saved state dtypes (torch casts floating
-        state to the param dtype) and the optimizer-level codebook/step."""
+        state to the param dtype) and the optimizer-level codebook/step.  The
+        load post-hooks run once the whole state (dtypes, names, codebook,
+        global step) is in place, not inside torch's part of the load."""
+        hooks = self._optimizer_load_state_dict_post_hooks
+        self._optimizer_load_state_dict_post_hooks = OrderedDict()
+        try:
+            self._load_state_dict_raw(state_dict)
+        finally:
+            self._optimizer_load_state_dict_post_hooks = hooks
+        for hook in list(hooks.values()):
+            hook(self)
+
+    def _load_state_dict_raw(self, state_dict):
         sd = dict(state_dict)
         global_step = sd.pop("gefen_global_step", None)
         has_det = "gefen_deterministic" in sd

@@ -9,6 +9,8 @@ first, then Muon (hybrid.py:760-776).
 """
 from __future__ import annotations
 
+import collections
+import copy
 import warnings
 from collections.abc import Mapping
 from typing import Iterable
@@ -16,7 +18,7 @@ from typing import Iterable
 import torch
 import torch.nn as nn
 
-from gefen.gefen import Gefen, _amp_gate, _amp_native_scaling_required
+from gefen.gefen import Gefen, _amp_gate, _amp_native_scaling_required, _preflight_torch_groups
 from gefen.gefen_muon import GefenMuon
 from gefen.params import DEFAULT_BACKUP_SUBSTRINGS, split_params_for_muon, validate_split
 
@@ -295,12 +297,43 @@ class GefenMuonHybrid(torch.optim.Optimizer):
         if saved_backup != self.backup_optimizer:
             raise ValueError("checkpoint backup_optimizer {!r} does not match this hybrid's {!r}".format(
                 saved_backup, self.backup_optimizer))
-        for key, child in (("muon", self.muon), ("backup", self.backup)):
+        halves = (("muon", self.muon), ("backup", self.backup))
+        # both halves are checked before either loads, so a refusal of one
+        # leaves the other untouched (no load-then-roll-back)
+        for key, child in halves:
             part = state_dict.get(key)
             if (part is None) != (child is None):
                 raise ValueError("checkpoint {} half {} but this hybrid's is {}".format(
                     key, "absent" if part is None else "present", "absent" if child is None else "present"))
-            if child is not None:
-                child.load_state_dict(part)
+            if child is None:
+                continue
+            if isinstance(child, Gefen):
+                child._preflight_state_dict(part)
+            else:
+                _preflight_torch_groups(child, list(part.get("param_groups") or []))
+                # a torch optimizer may fail after it has replaced its state
+                # (AdamW without a saved "step"): load a shadow first
+                shadow = copy.copy(child)
+                shadow.state = collections.defaultdict(dict)
+                shadow.param_groups = [dict(g) for g in child.param_groups]
+                shadow._optimizer_load_state_dict_pre_hooks = collections.OrderedDict()
+                shadow._optimizer_load_state_dict_post_hooks = collections.OrderedDict()
+                shadow.load_state_dict(copy.deepcopy(part))
+        # commit both halves, then run the children's load post-hooks: a hook
+        # that raises cannot leave one half loaded and the other not
+        deferred = []
+        for key, child in halves:
+            if child is None:
+                continue
+            hooks = child._optimizer_load_state_dict_post_hooks
+            child._optimizer_load_state_dict_post_hooks = collections.OrderedDict()
+            try:
+                child.load_state_dict(state_dict[key])
+            finally:
+                child._optimizer_load_state_dict_post_hooks = hooks
+            deferred.append((child, hooks))
+        for child, hooks in deferred:
+            for hook in list(hooks.values()):
+                hook(child)
         for post_hook in self._optimizer_load_state_dict_post_hooks.values():
             post_hook(self)
