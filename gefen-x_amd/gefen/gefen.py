@@ -199,6 +199,74 @@ def _amp_gate(optimizer) -> bool:
     return _amp_prepare_step(optimizer)
 
 
+FUSE_HISTOGRAM_FOR_EXACT = True
+
+
+def _exact_histogram_counts(grad_periods, bins: int):
+    """gefen.py:429-468 on the histogram kernel: (int64 counts on the
+    grads' device, number of elements) over (name, flat grad, period, shape)
+    tuples; (None, 0) when there are none.  Chunks of
+    GEFEN_EXACT_HISTOGRAM_CHUNK elements, block-aligned, so chunking is exact."""
+    lib = _native.load()
+    counts_dev = None
+    total = 0
+    for _, flat, period, _ in grad_periods:
+        f = flat.reshape(-1)
+        if f.device.type != "cuda":
+            raise ValueError("the exact codebook histogram needs gradients on a HIP device (got {})".format(f.device))
+        if not f.is_contiguous():
+            f = f.contiguous()
+        if counts_dev is None:
+            counts_dev = torch.zeros(bins, dtype=torch.int64, device=f.device)
+        elif counts_dev.device != f.device:
+            raise ValueError("all parameters must live on one device")
+        chunk = max(1, GEFEN_EXACT_HISTOGRAM_CHUNK // period) * period
+        for start in range(0, f.numel(), chunk):
+            part = f[start:start + chunk]
+            _native.check(lib.gefenx_exact_histogram(
+                part.data_ptr(), _fused._dtype_code(part.dtype), part.numel(), int(period),
+                counts_dev.data_ptr(), bins, _stream_of(part)), "exact histogram")
+        total += f.numel()
+    return counts_dev, total
+
+
+def learn_gefen_exact_codebook_from_grad_periods(*, grad_periods, codebook_device, num_codebooks: int,
+                                                 force_endpoints: bool, verbose: bool, compute_mse_logging: bool,
+                                                 use_fused_histogram: bool = FUSE_HISTOGRAM_FOR_EXACT):
+    """gefen.py:417-517: the exact 1-D k-means codebook of the block-absmax
+    normalised grads.  grad_periods: (name, flat grad, period, shape) tuples.
+    Counts of num_codebooks * 16 bins come from the histogram kernel (int64,
+    block-aligned chunks of GEFEN_EXACT_HISTOGRAM_CHUNK elements, order-free,
+    so chunking is exact); the DP runs on the device of the grads.  The
+    product steps on HIP devices only, so use_fused_histogram is accepted for
+    the reference's signature and the grads must be device tensors.
+    Returns None when there are no elements."""
+    del use_fused_histogram
+    bins = int(num_codebooks) * 16
+    counts_dev, total = _exact_histogram_counts(grad_periods, bins)
+    if total == 0:
+        return None
+    counts = counts_dev.cpu().to(torch.float32)
+    edges = torch.linspace(-1.0, 1.0, steps=bins + 1, dtype=torch.float32)
+    centers = 0.5 * (edges[:-1] + edges[1:])
+    active = counts > 0
+    stats = {"bin_edges": edges, "bin_centers": centers, "bin_counts": counts, "active_bins": active,
+             "active_centers": centers[active], "active_counts": counts[active],
+             "active_sums": centers[active] * counts[active]}
+    codebook = quantization_module.exact_dp(histogram_stats=stats, num_codebooks=int(num_codebooks),
+                                            force_endpoints=force_endpoints, device=counts_dev.device)
+    codebook = codebook.to(codebook_device)
+    if verbose and compute_mse_logging:
+        cb = codebook.cpu()
+        ac = stats["active_centers"]
+        idx = torch.searchsorted(cb, ac)
+        lo, hi = (idx - 1).clamp(0, cb.numel() - 1), idx.clamp(0, cb.numel() - 1)
+        pick = torch.where((ac - cb[lo]).abs() <= (ac - cb[hi]).abs(), lo, hi)
+        mse = ((ac - cb[pick]).square() * stats["active_counts"]).sum().item() / total
+        print("  exact DP: MSE_normalized={:.6e}".format(mse))
+    return codebook
+
+
 def _preflight_torch_groups(optimizer, saved_groups) -> None:
     """torch.optim.Optimizer.load_state_dict's own refusals, made before any
     load: the number of parameter groups and each group's size."""
@@ -465,43 +533,22 @@ class Gefen(torch.optim.Optimizer):
                                      "while learning Gefen codebook".format(period, name, flat.numel()))
                 yield name, flat, int(period), grad
 
-    def _grad_histogram_counts(self, bins, reuse_existing_periods):
-        """Block-absmax-normalised histogram of every gradient (gefen.py:
-        417-469) on the histogram kernel: (int64 counts on the device, number
-        of elements), or (None, 0) when no parameter has a gradient."""
-        lib = _native.load()
-        counts_dev = None
-        total = 0
-        for _, flat, period, _ in self._iter_gefen_grad_periods(reuse_existing_periods):
-            if counts_dev is None:
-                counts_dev = torch.zeros(bins, dtype=torch.int64, device=flat.device)
-            elif counts_dev.device != flat.device:
-                raise ValueError("all parameters must live on one device")
-            f = flat if flat.is_contiguous() else flat.contiguous()
-            chunk = max(1, GEFEN_EXACT_HISTOGRAM_CHUNK // period) * period
-            for start in range(0, f.numel(), chunk):
-                part = f[start:start + chunk]
-                _native.check(lib.gefenx_exact_histogram(
-                    part.data_ptr(), _fused._dtype_code(part.dtype), part.numel(), period,
-                    counts_dev.data_ptr(), bins, _stream_of(part)), "exact histogram")
-            total += f.numel()
-        return counts_dev, total
+    def _grad_histogram_counts(self, bins, reuse_existing_periods=False):
+        """The step-1 histogram over this optimizer's gradients (gefen.py:
+        417-469): (int64 counts on the device, number of elements), or
+        (None, 0) when no parameter has a gradient."""
+        return _exact_histogram_counts(self._iter_gefen_grad_periods(reuse_existing_periods), bins)
 
     def _learn_gefen_exact_codebook(self, reuse_existing_periods=False):
-        """learn_gefen_exact_codebook_from_grad_periods: gefen.py:417-517."""
-        counts_dev, total = self._grad_histogram_counts(HISTOGRAM_BINS, reuse_existing_periods)
-        if total == 0:
+        """learn_gefen_exact_codebook_from_grad_periods (gefen.py:417-517)
+        over this optimizer's gradients: the 256-entry codebook, endpoints
+        forced, on the gradients' device; None without gradients."""
+        grad_periods = list(self._iter_gefen_grad_periods(reuse_existing_periods))
+        if not grad_periods:
             return None
-        counts = counts_dev.cpu().to(torch.float32)
-        edges = torch.linspace(-1.0, 1.0, steps=HISTOGRAM_BINS + 1, dtype=torch.float32)
-        centers = 0.5 * (edges[:-1] + edges[1:])
-        active = counts > 0
-        stats = {"bin_edges": edges, "bin_centers": centers, "bin_counts": counts, "active_bins": active,
-                 "active_centers": centers[active], "active_counts": counts[active],
-                 "active_sums": centers[active] * counts[active]}
-        cb = quantization_module.exact_dp(histogram_stats=stats, num_codebooks=NUM_CODEBOOKS,
-                                          force_endpoints=True, device=counts_dev.device)
-        return cb.to(counts_dev.device)
+        return learn_gefen_exact_codebook_from_grad_periods(
+            grad_periods=grad_periods, codebook_device=grad_periods[0][1].device, num_codebooks=NUM_CODEBOOKS,
+            force_endpoints=True, verbose=False, compute_mse_logging=False)
 
     def _maybe_save_gefen_grad_histogram(self):
         """gefen.py:3095-3150: at the global steps listed in

@@ -69,6 +69,22 @@ def average_within_block_variance_cpu(list_of_values, period_to_check, parameter
     return np.sqrt(values.reshape(-1, period_to_check).var(axis=1).mean())
 
 
+def average_within_block_variance_torch(values, period, parameter_name=None, parameter_shape=None):
+    """Reference partitioning.py:87-108: sqrt(mean over blocks of each
+    block's population variance) of a tensor's values.  A tensor on a HIP
+    device is reduced by the block-variance kernel (float64 sums), a host
+    tensor by the float64 restatement above."""
+    if not isinstance(values, torch.Tensor):
+        raise TypeError("Expected torch.Tensor, got {}".format(type(values).__name__))
+    flat = values.detach().reshape(-1)
+    n = flat.numel()
+    if n % period != 0:
+        raise ValueError("Expected length {} to be divisible by period {}.".format(n, period))
+    if flat.device.type == "cuda":
+        return block_variance_errors_device(flat.to(torch.float32), [int(period)], input_is_squared=True)[0]
+    return float(average_within_block_variance_cpu(flat.to(torch.float64).numpy(), period))
+
+
 def _finalize_period_results(list_periods_and_errors, print_results):
     if len(list_periods_and_errors) == 0:
         raise ValueError("Expected at least one valid period candidate.")
@@ -97,8 +113,9 @@ def _find_period_cpu(squared_values, print_results=True):
     return _finalize_period_results(results, print_results)
 
 
-def block_variance_errors_device(grad: torch.Tensor, periods):
-    """Errors of every candidate period for a device tensor (C ABI, one sync)."""
+def block_variance_errors_device(grad: torch.Tensor, periods, input_is_squared: bool = False):
+    """Errors of every candidate period for a device tensor (C ABI, one
+    sync); the values are squared first unless input_is_squared."""
     from gefen.kernels import _native
     from gefen.kernels.automatic_gefen_fused import _dtype_code, _stream
     flat = grad.detach().reshape(-1)
@@ -106,32 +123,37 @@ def block_variance_errors_device(grad: torch.Tensor, periods):
         flat = flat.contiguous()
     per = np.ascontiguousarray(np.asarray(periods, dtype=np.int64))
     out = np.zeros(max(1, per.size), dtype=np.float64)
-    _native.check(_native.load().gefenx_block_variance_errors(
+    _native.check(_native.load().gefenx_block_variance_errors_ex(
         flat.data_ptr(), _dtype_code(flat.dtype), flat.numel(), per.ctypes.data, int(per.size),
-        out.ctypes.data, _stream(flat.device)), "block variance errors")
+        1 if input_is_squared else 0, out.ctypes.data, _stream(flat.device)), "block variance errors")
     return [float(e) for e in out[: per.size]]
 
 
-def _find_period_device(grad: torch.Tensor, print_results=True):
+def _find_period_device(grad: torch.Tensor, print_results=True, input_is_squared=False):
+    if not isinstance(grad, torch.Tensor):
+        raise TypeError("Expected torch.Tensor for the device backends, got {}".format(type(grad).__name__))
+    if grad.device.type != "cuda":
+        raise ValueError("Expected a CUDA tensor for the device backends, got device {}".format(grad.device))
     divs = divisors(grad.numel())
     if not divs:
         raise ValueError("Could not find any valid period candidates.")
-    errs = block_variance_errors_device(grad, divs)
+    errs = block_variance_errors_device(grad, divs, input_is_squared)
     return _finalize_period_results(list(zip(divs, errs)), print_results)
 
 
 def find_period_by_block_variance(squared_grad_flattened_values, print_results=True,
                                   parameter_name=None, parameter_shape=None, backend="cpu",
                                   input_is_squared=True):
-    """Reference partitioning.py:274-313.  With backend="cuda_kernel" the
-    input is the raw (unsquared) device grad, as the reference passes it."""
+    """Reference partitioning.py:274-313.  "gpu" (the reference's torch
+    backend, always on squared values) and "cuda_kernel" (squared values,
+    or with input_is_squared=False the raw grad, squared by the kernel) both
+    run the block-variance kernel over all candidate periods at once."""
     if backend == "cpu":
         period = _find_period_cpu(squared_grad_flattened_values, print_results)
         n = len(np.asarray(squared_grad_flattened_values).reshape(-1))
     elif backend in ("cuda_kernel", "gpu"):
-        if input_is_squared:
-            raise ValueError("the device period search squares the grad itself (input_is_squared=False)")
-        period = _find_period_device(squared_grad_flattened_values, print_results)
+        squared = True if backend == "gpu" else bool(input_is_squared)
+        period = _find_period_device(squared_grad_flattened_values, print_results, input_is_squared=squared)
         n = int(squared_grad_flattened_values.numel())
     else:
         raise ValueError("Unexpected backend: {}".format(backend))
