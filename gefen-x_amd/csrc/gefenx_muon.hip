@@ -669,6 +669,99 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16 (&
     }
 }
 
+// Epilogue of a full (64*WM)^2 tile (every row and column in range, C, D and
+// Dt 16-byte aligned with leading dimensions and batch strides multiples of 8):
+// the same arithmetic as gemm_epilogue, with every global access unconditional
+// and the next slab's C rows loaded before this slab's barrier.
+template <int WM>
+__device__ __forceinline__ void gemm_epilogue_full(const GemmArgs& g, const f32x16 (&acc)[WM][WM], float* sOut,
+                                                   int64_t bz, bool diag, int64_t m0, int64_t n0, int wm, int wn,
+                                                   int l32, int lhi) {
+    constexpr int BN = 64 * WM;
+    constexpr int kOutPitch = BN + 1;
+    constexpr int kVecD = 64 * BN / 8 / kT;
+    const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
+    uint16_t* D = g.D ? g.D + bz * g.sD : nullptr;
+    uint16_t* Dt = (g.Dt && !(g.tri && diag)) ? g.Dt + bz * g.sDt : nullptr;
+    const int tid = threadIdx.x;
+    u32x4 cpf[2][kVecD];
+    auto fetch = [&](int h, u32x4 (&dst)[kVecD]) {
+#pragma unroll
+        for (int k = 0; k < kVecD; ++k) {
+            const int v = tid + k * kT;
+            const int row = v / (BN / 8), c8 = (v % (BN / 8)) * 8;
+            dst[k] = __builtin_nontemporal_load(
+                gbl(reinterpret_cast<const u32x4*>(C + (m0 + h * 64 + row) * g.ldc + n0 + c8)));
+        }
+    };
+    if (C != nullptr) fetch(0, cpf[0]);
+#pragma unroll
+    for (int h = 0; h < WM; ++h) {
+        if (wm == h / (WM / 2)) {
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                const int i = 2 * (h % (WM / 2)) + ii;
+#pragma unroll
+                for (int j = 0; j < WM; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = ii * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        const int col = wn * (32 * WM) + j * 32 + l32;
+                        sOut[row * kOutPitch + col] = acc[i][j][r];
+                    }
+            }
+        }
+        if (C != nullptr && h + 1 < WM) fetch(h + 1, cpf[(h + 1) & 1]);
+        __syncthreads();
+        const int64_t R0 = m0 + h * 64;
+#pragma unroll
+        for (int k = 0; k < kVecD; ++k) {
+            const int v = tid + k * kT;
+            const int row = v / (BN / 8), c8 = (v % (BN / 8)) * 8;
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = g.alpha * sOut[row * kOutPitch + c8 + e];
+            if (C != nullptr) {
+                const u32x4 cv = cpf[h & 1][k];
+                const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    x[e] = __builtin_fmaf(g.beta, bf16f((uint16_t)(cw[e >> 1] >> (16 * (e & 1)))), x[e]);
+            }
+            uint16_t hv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hv[e] = f2bf(x[e]);
+                sOut[row * kOutPitch + c8 + e] = bf16f(hv[e]);
+            }
+            if (D != nullptr) {
+                const u32x4 dv = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16),
+                                  (uint32_t)hv[4] | ((uint32_t)hv[5] << 16), (uint32_t)hv[6] | ((uint32_t)hv[7] << 16)};
+                *gbl(reinterpret_cast<u32x4*>(D + (R0 + row) * g.ldd + n0 + c8)) = dv;
+            }
+        }
+        if (Dt != nullptr) {
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kVecD; ++k) {
+                const int v = tid + k * kT;
+                const int cc = v >> 3, r8 = (v & 7) * 8;
+                uint16_t hv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = f2bf(sOut[(r8 + e) * kOutPitch + cc]);
+                const u32x4 tv = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16),
+                                  (uint32_t)hv[4] | ((uint32_t)hv[5] << 16), (uint32_t)hv[6] | ((uint32_t)hv[7] << 16)};
+                *gbl(reinterpret_cast<u32x4*>(Dt + (n0 + cc) * g.lddt + R0 + r8)) = tv;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ bool epi_aligned(const void* p, int64_t ld, int64_t s) {
+    return p == nullptr || ((reinterpret_cast<uintptr_t>(p) | (uintptr_t)(ld * 2) | (uintptr_t)(s * 2)) & 15) == 0;
+}
+
 // D = alpha * A B^T + beta * C (A [M x K], B [N x K], C and D [M x N], all
 // row-major bf16, fp32 accumulation; optional transposed copy Dt = D^T).
 // Workgroup tile (64*WM) x (64*WN): 2 x 2 waves, each (32*WM) x (32*WN) as
@@ -861,7 +954,11 @@ __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
         }
     }
     __syncthreads();
-    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
+    if (m0 + TILE <= g.M && n0 + TILE <= g.N && epi_aligned(g.C, g.ldc, g.sC) && epi_aligned(g.D, g.ldd, g.sD) &&
+        epi_aligned(g.Dt, g.lddt, g.sDt))
+        gemm_epilogue_full<WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
+    else
+        gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
 }
 
 // One 1 KB direct-to-LDS load instruction (number q of this wave's share of
@@ -902,6 +999,7 @@ __device__ __forceinline__ void dl_load_one(const uint16_t* __restrict__ A, int6
 // direct-to-LDS tile loads, so reads and loads run under the MFMAs instead
 // of ahead of them.  The last step reloads its own K range into the idle
 // buffer (never read) so every step issues the same loads without a branch.
+
 __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
     constexpr int WM = 4, TILE = 256, BK = 64, KS = BK / 16;
     int64_t bz, tm, tn;
@@ -972,7 +1070,12 @@ __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // the last (discarded) reload lands before the epilogue reuses LDS
     __syncthreads();
-    gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
+    const bool full = m0 + TILE <= g.M && n0 + TILE <= g.N && epi_aligned(g.C, g.ldc, g.sC) &&
+                      epi_aligned(g.D, g.ldd, g.sD) && epi_aligned(g.Dt, g.lddt, g.sDt);
+    if (full)
+        gemm_epilogue_full<WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
+    else
+        gemm_epilogue<WM, WM>(g, acc, reinterpret_cast<float*>(smem), bz, tm == tn, m0, n0, wm, wn, l32, lhi);
 }
 
 static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
