@@ -993,11 +993,13 @@ __device__ __forceinline__ void dl_load_one(const uint16_t* __restrict__ A, int6
 // wave owns 128 x 128 as 4 x 4 blocks of mfma_f32_32x32x16_bf16: per 16-wide
 // K sub-step, 16 MFMAs against 8 operand fragments, so the LDS reads per MFMA
 // are half those of the 128 x 128 tile.  The instruction order inside a step
-// is fixed with scheduling fences: after each row of 4 MFMAs come that row's
-// operand reads for the next sub-step (fragments double-buffered in
-// registers) and, in the first two sub-steps, two of the next stage's 16
-// direct-to-LDS tile loads, so reads and loads run under the MFMAs instead
-// of ahead of them.  The last step reloads its own K range into the idle
+// is fixed with scheduling fences, one MFMA at a time: between consecutive
+// MFMAs go the next sub-step's operand reads (fragments double-buffered in
+// registers; B fragments first, since the next sub-step's first row needs
+// all four, then A in row order) and, in the first two sub-steps, the next
+// stage's 16 direct-to-LDS tile loads (one after the first and one after
+// the last MFMA of each row), so reads and loads issue in the gaps between
+// MFMAs instead of in blocks ahead of them.  The last step reloads its own K range into the idle
 // buffer (never read) so every step issues the same loads without a branch.
 
 __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
@@ -1051,19 +1053,23 @@ __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
         for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
             for (int i = 0; i < WM; ++i) {
-                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int j = 0; j < WM; ++j)
+                for (int j = 0; j < WM; ++j) {
+                    __builtin_amdgcn_sched_barrier(0);
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks & 1][i], bv[ks & 1][j], acc[i][j], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                if (ks + 1 < KS) {
-                    av[(ks + 1) & 1][i] = rd(a_s, wm, i, ks + 1);
-                    bv[(ks + 1) & 1][i] = rd(b_s, wn, i, ks + 1);
-                }
-                if (ks < kLoadKs) {
-#pragma unroll
-                    for (int q = 0; q < kLpr; ++q)
-                        dl_load_one<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, kn, nxt, (ks * 4 + i) * kLpr + q);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (ks < kLoadKs) {
+                        if (j == 0 || j == 3)
+                            dl_load_one<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, kn, nxt,
+                                                  (ks * 4 + i) * kLpr + (j == 3));
+                    }
+                    // next sub-step's fragments: B first (row 0 needs all of them), then A in row order
+                    const int slot = ks < kLoadKs ? j - 1 : j;  // reads in slots 1, 2 (0, 1 without loads)
+                    if (ks + 1 < KS && slot >= 0 && slot < 2) {
+                        const int f = 2 * i + slot;  // 0..7
+                        if (f < 4) bv[(ks + 1) & 1][f] = rd(b_s, wn, f, ks + 1);
+                        else av[(ks + 1) & 1][f - 4] = rd(a_s, wm, f - 4, ks + 1);
+                    }
                 }
             }
         }
