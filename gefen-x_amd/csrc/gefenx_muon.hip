@@ -893,11 +893,11 @@ __device__ __forceinline__ void dl_load_stage(const uint16_t* __restrict__ A, in
 // WM x WM blocks of 32 x 32 per wave, 2 x 2 waves: tile (64*WM)^2.
 template <int WM, int BK, int S>
 __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
+    static_assert(S == 2, "two-stage ring: the loop waits for every load in flight at each step");
     int64_t bz, tm, tn;
     if (!gemm_tile(g, bz, tm, tn)) return;  // upper triangle: the mirror of a lower tile
     constexpr int TILE = 64 * WM;
     constexpr int kStage = 2 * TILE * BK;                        // bf16 per stage: A then B
-    constexpr int kIpw = 2 * (TILE * BK * 2 / 1024) / (kT / 64);  // load instructions per wave and stage
     constexpr int kEpi = 2 * 64 * (TILE + 1);                    // the epilogue's fp32 slab, in bf16 units
     constexpr int kSmem = S * kStage > kEpi ? S * kStage : kEpi;
     __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
@@ -921,11 +921,7 @@ __global__ void __launch_bounds__(kT) k_gemm_dl(GemmArgs g) {
     for (int st = 0; st < S - 1; ++st)
         if (st < nk) dl_load_stage<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, st * BK, smem + st * kStage);
     for (int64_t kt = 0; kt < nk; ++kt) {
-        // step kt's loads were issued S-1 steps ago; later ones may still fly
-        const int64_t later = std::min<int64_t>(S - 2, nk - 1 - kt);
-        if (later >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kIpw));
-        else if (later == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | kIpw);
-        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt's loads, the only ones in flight
         __syncthreads();  // every wave's loads of step kt landed; step kt-1's buffer is free
         if (kt + S - 1 < nk)
             dl_load_stage<TILE, BK>(A, g.lda, g.M, B, g.ldb, g.N, m0, n0, (kt + S - 1) * BK,
