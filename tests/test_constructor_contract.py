@@ -139,3 +139,16 @@ def test_hybrid_rejects_empty_params_and_add_param_group():
     opt = GefenMuonHybrid(_p2(), _p1(), lr=1e-3)
     with pytest.raises(NotImplementedError):
         opt.add_param_group({"params": [nn.Parameter(torch.randn(4, 4))]})
+
+
+def test_package_surface():
+    """The names the reference package exports (src/gefen/__init__.py:10-21)
+    that belong to the step: the optimizers, the split helpers, the kernels
+    module and the version string (the distributed-checkpoint classes are
+    not part of this build)."""
+    import gefen
+    for name in ("Gefen", "GefenMuon", "GefenMuonHybrid", "split_params_for_muon", "validate_split", "kernels",
+                 "__version__"):
+        assert name in gefen.__all__ and hasattr(gefen, name), name
+    assert isinstance(gefen.__version__, str) and gefen.__version__
+    assert hasattr(gefen.kernels, "automatic_gefen_fused")
