@@ -133,6 +133,13 @@ __device__ __forceinline__ void load_idx8(const uint8_t* __restrict__ base, uint
     }
 }
 
+// Workgroup barrier for data exchanged through LDS only: waits for this
+// wave's LDS operations, not for its global loads and stores in flight
+// (__syncthreads()'s workgroup fence makes the compiler drain those too, so a
+// prefetch issued before it would be waited for at once).  No global memory
+// written by one wave may be read by another across this barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ void store_idx8(uint8_t* __restrict__ base, const uint32_t ix[8]) {
     u32x2 a;
     a.x = ix[0] | (ix[1] << 8) | (ix[2] << 16) | (ix[3] << 24);

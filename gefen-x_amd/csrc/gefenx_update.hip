@@ -643,7 +643,7 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
         TT& t = s_t[s & 1];
 #pragma unroll
         for (int q = 0; q < TT::kVecPerThread; ++q) tv_put_vec<DT>(t, tid + q * kThreads, cur.v[q]);
-        __syncthreads();
+        lds_barrier();
         if (s + 1 < n_sub) fetch(s + 1, nxt);
         const int cs = s / n_rb, rb = s - cs * n_rb;
         float colf[kChunk];
@@ -723,7 +723,7 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
                 colacc[k] = 0.0;
                 if (lane < kChunk) s_col[wave][kChunk * lane + k] = v;
             }
-            __syncthreads();
+            lds_barrier();
             if (tid < kTv) {
                 const int64_t c = c_begin + (int64_t)cs * kTv + tid;
                 if (c < c_end)
@@ -1751,7 +1751,11 @@ __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, cons
 // p go to LDS, the chunks requantise and apply (indices straight to HBM, new
 // p back into the LDS tile), then p leaves along storage rows.  The next
 // tile's loads are in flight during the current tile's math.
-template <int DT, int MODE, int LF>
+// FULL: every tile of the workgroup is interior (R and C multiples of 64,
+// kTvTilesPerWg tiles), so each load and store is unconditional and the
+// tile loop has a fixed trip count: the wait before a tile's LDS writes then
+// covers only its own loads, not the previous tile's stores.
+template <int DT, int MODE, int LF, bool FULL>
 __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const FastTables& ft,
                                          TvTile<DT>& tg, TvTile<DT>& tp, float row_scale) {
     using TT = TvTile<DT>;
@@ -1762,7 +1766,7 @@ __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const 
     const int64_t ntiles = nrt * ((C + kTv - 1) / kTv);
     const int64_t t0 = wg * kTvTilesPerWg;
     if (t0 >= ntiles) return;
-    const int64_t t1 = std::min<int64_t>(t0 + kTvTilesPerWg, ntiles);
+    const int64_t t1 = FULL ? t0 + kTvTilesPerWg : std::min<int64_t>(t0 + kTvTilesPerWg, ntiles);
     const bool general_q = w.qt->max_cnt > 1;
     const int tid = threadIdx.x, jc = tid & 7, ib = tid >> 3;
 
@@ -1779,12 +1783,12 @@ __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const 
         for (int q = 0; q < TT::kVecPerThread; ++q) {
             const int V = tid + q * kThreads;
             const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
-            const bool ok = r < R && c < C;
+            const bool ok = FULL || (r < R && c < C);
             f.g[q] = tv_load<DT>(a.g, ldg, r, c, ok);
             f.p[q] = tv_load<DT>(a.p, ldp, r, c, ok);
         }
         const int64_t c = c0 + kChunk * jc;
-        if (MODE == 0 && c < C) {
+        if (MODE == 0 && (FULL || c < C)) {
             load_vcol(a.vcs + c, f.vc);
         } else {
 #pragma unroll
@@ -1793,7 +1797,7 @@ __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const 
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int64_t r = r0 + ib + 32 * h;
-            f.ok[h] = r < R && c < C;
+            f.ok[h] = FULL || (r < R && c < C);
             f.ix[h] = RawIdx8{0u, 0u};
             f.mo[h] = f.mn[h] = f.y[h] = f.rv[h] = 0.0f;
             if (f.ok[h]) {
@@ -1810,18 +1814,18 @@ __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const 
 
     Pre cur, nxt;
     fetch(t0, cur);
-    for (int64_t T = t0; T < t1; ++T) {
+    auto tile = [&](int64_t T, bool more) {
 #pragma unroll
         for (int q = 0; q < TT::kVecPerThread; ++q) {
             tv_put_vec<DT>(tg, tid + q * kThreads, cur.g[q]);
             tv_put_vec<DT>(tp, tid + q * kThreads, cur.p[q]);
         }
-        __syncthreads();
-        if (T + 1 < t1) fetch(T + 1, nxt);
+        lds_barrier();
+        if (more) fetch(T + 1, nxt);
         const int64_t r0 = (T % nrt) * kTv, c0 = (T / nrt) * kTv;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            if (!cur.ok[h]) continue;
+            if (!FULL && !cur.ok[h]) continue;
             const int i = ib + 32 * h;
             ChunkIn<DT> in;
             tv_raw8<DT>(tg, i, kChunk * jc, in.g);
@@ -1840,16 +1844,22 @@ __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const 
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) tv_put<DT>(tp, i, kChunk * jc + k, pv[k]);
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int q = 0; q < TT::kVecPerThread; ++q) {
             const int V = tid + q * kThreads;
             const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
-            if (r < R && c < C)
+            if (FULL || (r < R && c < C))
                 __builtin_nontemporal_store(tv_get_vec<DT>(tp, V), gbl(reinterpret_cast<u32x4*>(a.p + c * ldp + r)));
         }
-        __syncthreads();
+        lds_barrier();
         cur = nxt;
+    };
+    if constexpr (FULL) {
+#pragma unroll
+        for (int it = 0; it < kTvTilesPerWg; ++it) tile(t0 + it, it + 1 < kTvTilesPerWg);
+    } else {
+        for (int64_t T = t0; T < t1; ++T) tile(T, T + 1 < t1);
     }
 }
 
@@ -1868,8 +1878,15 @@ __device__ __forceinline__ void apply_tv_wg(const TensorWork& w, int64_t wg, TvA
         row_scale = (1.0f / stored_mean(w)) * sc.inv_bc2;
     }
     __syncthreads();
-    if (w.mc.small) apply_tv<DT, MODE, kLerpSmall>(w, wg, lds.f, lds.g, lds.p, row_scale);
-    else apply_tv<DT, MODE, kLerpLarge>(w, wg, lds.f, lds.g, lds.p, row_scale);
+    const int64_t ntiles = ((w.R + kTv - 1) / kTv) * ((w.C + kTv - 1) / kTv);
+    const bool full = w.R % kTv == 0 && w.C % kTv == 0 && (wg + 1) * kTvTilesPerWg <= ntiles;
+    if (full) {
+        if (w.mc.small) apply_tv<DT, MODE, kLerpSmall, true>(w, wg, lds.f, lds.g, lds.p, row_scale);
+        else apply_tv<DT, MODE, kLerpLarge, true>(w, wg, lds.f, lds.g, lds.p, row_scale);
+    } else {
+        if (w.mc.small) apply_tv<DT, MODE, kLerpSmall, false>(w, wg, lds.f, lds.g, lds.p, row_scale);
+        else apply_tv<DT, MODE, kLerpLarge, false>(w, wg, lds.f, lds.g, lds.p, row_scale);
+    }
 }
 
 // LDS of the apply kernels: the fast tables or the general ones, never both.
