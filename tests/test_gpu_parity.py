@@ -261,6 +261,10 @@ STRIDED_CASES = [
     (orc.F16, 136, 264, 88, "view_ld", "view"),
     (orc.BF16, 64, 64, 8, "view", "view"),
     (orc.BF16, 128, 192, 24576, "view", "view"),
+    # R and C multiples of 64: workgroups of four interior tiles take the
+    # full-tile apply (unconditional loads and stores), the last the general one
+    (orc.F32, 256, 192, 512, "view", "view"),
+    (orc.F16, 128, 384, 192, "view_ld", "view"),
     (orc.BF16, 200, 136, 400, "contig", "view"),    # view stats, general apply
     (orc.F32, 200, 136, 400, "view", "contig"),      # contiguous stats, general apply
 ]
@@ -278,6 +282,8 @@ BLOCK_VIEW_CASES = [
     (orc.F32, 328, 200, 1640, "view"),
     (orc.F16, 136, 264, 88, "view"),
     (orc.BF16, 1096, 2056, 2056, "view"),
+    (orc.BF16, 320, 256, 640, "view"),  # full-tile apply workgroups and a partial last one
+    (orc.F32, 256, 128, 64, "view_ld"),
 ]
 
 
