@@ -23,6 +23,64 @@ from gefen.gefen_muon import GefenMuon
 from gefen.params import DEFAULT_BACKUP_SUBSTRINGS, split_params_for_muon, validate_split
 
 
+_HOOK_REGISTRIES = (
+    "_optimizer_step_pre_hooks", "_optimizer_step_post_hooks",
+    "_optimizer_state_dict_pre_hooks", "_optimizer_state_dict_post_hooks",
+    "_optimizer_load_state_dict_pre_hooks", "_optimizer_load_state_dict_post_hooks",
+)
+
+_NATIVE_LR_WARNING = (
+    "GefenMuonHybrid: adjust_lr_fn={!r} uses Muon-native LR scaling, so an AdamW-scale lr will mis-scale "
+    "the 2D Muon matrices relative to the backup half. Use adjust_lr_fn='match_rms_adamw' (the default) to "
+    "share one AdamW-scale lr, or set muon_lr explicitly.")
+
+
+def _refuse_unusable_split(muon_named, backup_named, backup_optimizer):
+    """Argument checks that need the routed lists (hybrid.py:322-410).
+
+    Nothing to step is a ValueError.  So is a backup-only split whose every
+    parameter is a zero-numel placeholder: DeepSpeed ZeRO stage 3
+    (zero.Init) hands the optimizer 0-element 1-D stand-ins, the 2D routing
+    then finds no Muon matrix, and the hybrid would quietly run as its backup
+    alone.  A backup-only split with real storage (a 1D-only model), or with
+    a few empty slots among real tensors, is allowed.  Then the backup kind,
+    and a parameter routed twice or a name used twice (validate_split)."""
+    if not muon_named and not backup_named:
+        raise ValueError("GefenMuonHybrid received no parameters to optimize")
+    if not muon_named and all(t.numel() == 0 for _, t in backup_named):
+        raise ValueError(
+            "GefenMuonHybrid found no 2D Muon-eligible parameters and all {} supplied parameters are "
+            "zero-numel placeholders (first: {!r}), the signature of DeepSpeed ZeRO stage 3 partitioning "
+            "(zero.Init) before the optimizer is built.  The hybrid would silently run as a backup-only "
+            "optimizer at backup_lr with no Muon half.  Muon's 2D orthogonalisation cannot step ZeRO's "
+            "flattened 1-D partitions: use plain Gefen as the DeepSpeed client optimizer, or build the "
+            "hybrid without ZeRO partitioning (FSDP2 / DDP / single GPU).".format(
+                len(backup_named), backup_named[0][0]))
+    if backup_optimizer not in ("gefen", "adamw"):
+        raise ValueError("backup_optimizer must be 'gefen' or 'adamw' but is: {!r}".format(backup_optimizer))
+    validate_split(muon_named, backup_named)
+
+
+def _backup_cohorts(named, no_decay_substrings, *, lr, betas, eps, weight_decay):
+    """The backup half's parameter groups as [(named_params, group_overrides)].
+
+    Without no_decay_substrings: one cohort with no overrides (the child's
+    constructor defaults apply).  With them (hybrid.py:461-505): names that
+    contain any substring, case-insensitively, form a weight_decay=0 cohort
+    after the cohort of the other names; each carries the backup's
+    lr / betas / eps explicitly, and an empty cohort is left out."""
+    needles = [str(s).lower() for s in no_decay_substrings]
+    if not needles:
+        return [(list(named), {})]
+    exempt = [any(n in name.lower() for n in needles) for name, _ in named]
+    cohorts = []
+    for is_exempt, wd in ((False, weight_decay), (True, 0.0)):
+        members = [item for item, flag in zip(named, exempt) if flag == is_exempt]
+        if members:
+            cohorts.append((members, {"lr": lr, "betas": betas, "eps": eps, "weight_decay": wd}))
+    return cohorts
+
+
 class _StateView(Mapping):
     """Read view of the children's per-parameter state, keyed by parameter."""
 
@@ -91,86 +149,82 @@ class GefenMuonHybrid(torch.optim.Optimizer):
             raise TypeError("deterministic must be a bool")
         self._deterministic = deterministic
         self.capturable = capturable
+        muon_named, backup_named = self._resolve_lists(muon_named_params, backup_named_params,
+                                                       backup_substrings)
+        _refuse_unusable_split(muon_named, backup_named, backup_optimizer)
+        self.backup_optimizer = backup_optimizer
+        if adjust_lr_fn in (None, "original"):
+            warnings.warn(_NATIVE_LR_WARNING.format(adjust_lr_fn), stacklevel=2)
+
+        # Each half takes the shared lr / weight_decay unless it has its own.
+        half_lr = {"muon": lr, "backup": lr}
+        half_wd = {"muon": weight_decay, "backup": weight_decay}
+        for key, lr_override, wd_override in (("muon", muon_lr, muon_weight_decay),
+                                              ("backup", backup_lr, backup_weight_decay)):
+            if lr_override is not None:
+                half_lr[key] = lr_override
+            if wd_override is not None:
+                half_wd[key] = wd_override
+
+        self.muon = None
+        if muon_named:
+            self.muon = GefenMuon(
+                muon_named, lr=half_lr["muon"], weight_decay=half_wd["muon"], fused=fused,
+                stochastic_round=stochastic_round, deterministic=deterministic, capturable=capturable,
+                verbose=verbose, momentum=momentum, nesterov=nesterov, ns_steps=ns_steps,
+                ns_schedule=ns_schedule, adjust_lr_fn=adjust_lr_fn, sharded_mode=sharded_mode,
+                fp8_ns=fp8_ns, fp8_ns_compile=fp8_ns_compile, batched_ns=batched_ns,
+                batched_ns_workspace_bytes=batched_ns_workspace_bytes, normuon=normuon,
+                normuon_beta2=normuon_beta2, normuon_eps=normuon_eps, cautious=cautious)
+
+        self.backup = None
+        if backup_named:
+            cohorts = _backup_cohorts(backup_named, no_decay_substrings, lr=half_lr["backup"],
+                                      betas=betas, eps=eps, weight_decay=half_wd["backup"])
+            common = dict(lr=half_lr["backup"], betas=betas, eps=eps, weight_decay=half_wd["backup"],
+                          fused=fused, capturable=capturable)
+            if backup_optimizer == "gefen":
+                # block-shared second moment on the backup half: the hybrid
+                # recipe is the one measured with block vmean on the embedding
+                # and head (hybrid.py:524-545)
+                self.backup = Gefen(
+                    [dict(overrides, params=named) for named, overrides in cohorts],
+                    factored_v_2d=False, force_1d_period_one=backup_1d_period_one,
+                    force_2d_period_one=backup_2d_period_one, stochastic_round=stochastic_round,
+                    deterministic=deterministic, verbose=verbose, **common)
+            else:
+                # torch groups hold bare tensors; the names ride along as the
+                # group's parallel "param_names" list, so AdamW checkpoints
+                # carry the same routing names as Gefen ones
+                self.backup = torch.optim.AdamW(
+                    [dict(overrides, params=[t for _, t in named], param_names=[n for n, _ in named])
+                     for named, overrides in cohorts], **common)
+        self._adopt_children()
+
+    def _resolve_lists(self, first, backup_named_params, backup_substrings):
+        """The (muon, backup) named lists of the three call forms
+        (hybrid.py:300-330): two lists, or one model / named iterable that is
+        split here; backup_substrings belongs to the second form only."""
         if backup_named_params is None:
-            muon_named_params, backup_named_params = self._auto_split(muon_named_params, backup_substrings)
+            first, backup_named_params = self._auto_split(first, backup_substrings)
         elif backup_substrings is not None:
             raise TypeError("backup_substrings is only valid with the single-argument (model / named-params) "
                             "form; you also passed backup_named_params.")
-        muon_named_params = list(muon_named_params)
-        backup_named_params = list(backup_named_params)
-        if not muon_named_params and not backup_named_params:
-            raise ValueError("GefenMuonHybrid received no parameters to optimize")
-        if backup_optimizer not in ("gefen", "adamw"):
-            raise ValueError("backup_optimizer must be 'gefen' or 'adamw' but is: {!r}".format(backup_optimizer))
-        self.backup_optimizer = backup_optimizer
-        validate_split(muon_named_params, backup_named_params)
-        if adjust_lr_fn in (None, "original"):
-            warnings.warn(
-                "GefenMuonHybrid: adjust_lr_fn={!r} uses Muon-native LR scaling, so an AdamW-scale lr will "
-                "mis-scale the 2D Muon matrices relative to the backup half. Use adjust_lr_fn='match_rms_adamw' "
-                "(the default) to share one AdamW-scale lr, or set muon_lr explicitly.".format(adjust_lr_fn),
-                stacklevel=2)
-        muon_lr = lr if muon_lr is None else muon_lr
-        backup_lr = lr if backup_lr is None else backup_lr
-        muon_weight_decay = weight_decay if muon_weight_decay is None else muon_weight_decay
-        backup_weight_decay = weight_decay if backup_weight_decay is None else backup_weight_decay
-        self.muon = GefenMuon(
-            muon_named_params, lr=muon_lr, weight_decay=muon_weight_decay, momentum=momentum, nesterov=nesterov,
-            ns_steps=ns_steps, ns_schedule=ns_schedule, adjust_lr_fn=adjust_lr_fn, fused=fused,
-            sharded_mode=sharded_mode, fp8_ns=fp8_ns, fp8_ns_compile=fp8_ns_compile, batched_ns=batched_ns,
-            batched_ns_workspace_bytes=batched_ns_workspace_bytes, stochastic_round=stochastic_round,
-            deterministic=deterministic, normuon=normuon, normuon_beta2=normuon_beta2, normuon_eps=normuon_eps,
-            cautious=cautious, capturable=capturable, verbose=verbose) if muon_named_params else None
-        no_decay_substrings = tuple(s.lower() for s in no_decay_substrings)
+        return list(first), list(backup_named_params)
 
-        def _is_no_decay(name):
-            lname = name.lower()
-            return any(sub in lname for sub in no_decay_substrings)
-
-        if backup_named_params and no_decay_substrings:
-            decay = [(n, p) for n, p in backup_named_params if not _is_no_decay(n)]
-            no_decay = [(n, p) for n, p in backup_named_params if _is_no_decay(n)]
-            backup_groups = [g for g in (
-                {"params": decay, "lr": backup_lr, "betas": betas, "eps": eps, "weight_decay": backup_weight_decay}
-                if decay else None,
-                {"params": no_decay, "lr": backup_lr, "betas": betas, "eps": eps, "weight_decay": 0.0}
-                if no_decay else None) if g is not None]
-        else:
-            backup_groups = backup_named_params
-        if not backup_named_params:
-            self.backup = None
-        elif backup_optimizer == "gefen":
-            self.backup = Gefen(backup_groups, lr=backup_lr, betas=betas, eps=eps, weight_decay=backup_weight_decay,
-                                fused=fused, force_1d_period_one=backup_1d_period_one,
-                                force_2d_period_one=backup_2d_period_one, factored_v_2d=False,
-                                stochastic_round=stochastic_round, deterministic=deterministic,
-                                capturable=capturable, verbose=verbose)
-        else:
-            if no_decay_substrings:
-                adamw_groups = [{**{k: v for k, v in g.items() if k != "params"},
-                                 "params": [p for _, p in g["params"]], "param_names": [n for n, _ in g["params"]]}
-                                for g in backup_groups]
-            else:
-                adamw_groups = [{"params": [p for _, p in backup_groups], "param_names": [n for n, _ in backup_groups]}]
-            self.backup = torch.optim.AdamW(adamw_groups, lr=backup_lr, betas=betas, eps=eps,
-                                            weight_decay=backup_weight_decay, fused=fused, capturable=capturable)
-        self._subopts = [o for o in (self.muon, self.backup) if o is not None]
-        self._state_param_owner = {}
-        for o in self._subopts:
-            for group in o.param_groups:
-                for p in group["params"]:
-                    self._state_param_owner[id(p)] = (p, o)
-        # torch.optim.Optimizer.__init__ is not called: param_groups and state
-        # are the children's own (shared) objects, so an LR scheduler's in-place
-        # group["lr"] updates reach them.
+    def _adopt_children(self):
+        """Expose the children as this optimizer: their param_groups and state
+        are shared by reference (an LR scheduler's in-place group["lr"] writes
+        reach them), so torch.optim.Optimizer.__init__ is not run; only the
+        hook registries torch and its wrappers introspect are created."""
+        self._subopts = [child for child in (self.muon, self.backup) if child is not None]
+        # id(p) -> (p, child): the strong reference to p keeps its id unique
+        self._state_param_owner = {
+            id(p): (p, child)
+            for child in self._subopts for group in child.param_groups for p in group["params"]}
         self.defaults = self._subopts[0].defaults
-        from collections import OrderedDict
-        self._optimizer_step_pre_hooks = OrderedDict()
-        self._optimizer_step_post_hooks = OrderedDict()
-        self._optimizer_state_dict_pre_hooks = OrderedDict()
-        self._optimizer_state_dict_post_hooks = OrderedDict()
-        self._optimizer_load_state_dict_pre_hooks = OrderedDict()
-        self._optimizer_load_state_dict_post_hooks = OrderedDict()
+        for registry in _HOOK_REGISTRIES:
+            setattr(self, registry, collections.OrderedDict())
 
     # ------------------------------------------------------------ routing
 
@@ -312,13 +366,21 @@ class GefenMuonHybrid(torch.optim.Optimizer):
             else:
                 _preflight_torch_groups(child, list(part.get("param_groups") or []))
                 # a torch optimizer may fail after it has replaced its state
-                # (AdamW without a saved "step"): load a shadow first
+                # (AdamW without a saved "step"): load a shadow first.  The
+                # shadow runs the child's own load pre-hooks (a hook may
+                # migrate the checkpoint into a loadable one) but not its
+                # post-hooks.  torch's loader neither mutates its input nor
+                # copies tensors already on the parameter's device, so the
+                # shadow holds no second copy of the state; it is dropped
+                # before anything commits.
                 shadow = copy.copy(child)
                 shadow.state = collections.defaultdict(dict)
                 shadow.param_groups = [dict(g) for g in child.param_groups]
-                shadow._optimizer_load_state_dict_pre_hooks = collections.OrderedDict()
+                shadow._optimizer_load_state_dict_pre_hooks = collections.OrderedDict(
+                    child._optimizer_load_state_dict_pre_hooks)
                 shadow._optimizer_load_state_dict_post_hooks = collections.OrderedDict()
-                shadow.load_state_dict(copy.deepcopy(part))
+                shadow.load_state_dict(dict(part))
+                del shadow
         # commit both halves, then run the children's load post-hooks: a hook
         # that raises cannot leave one half loaded and the other not
         deferred = []

@@ -27,6 +27,10 @@ GEFENX_EDTYPE = -2
 GEFENX_ELAUNCH = -3
 GEFENX_ENOMEM = -4
 
+# GEFENX_ABI_VERSION this binding is written against (include/gefenx.h):
+# the struct layouts and workspace sizes below follow it.
+ABI_VERSION = 2
+
 DT_F32, DT_F16, DT_BF16, DT_F64 = 0, 1, 2, 3
 WS_FACTORED, WS_BLOCK, WS_MOMENTUM = 0, 1, 2
 
@@ -174,6 +178,11 @@ def load(path: str = LIB_PATH):
                 raise NativeLibraryError("{} does not export {}".format(path, name)) from exc
             fn.restype = res
             fn.argtypes = args
+        built = lib.gefenx_abi_version()
+        if built != ABI_VERSION:
+            raise NativeLibraryError(
+                "{} implements gefenx ABI version {}, this binding needs {} (rebuild with "
+                "__graft_entry__.build())".format(path, built, ABI_VERSION))
         _lib = lib
         return lib
 

@@ -26,7 +26,12 @@
 extern "C" {
 #endif
 
-#define GEFENX_ABI_VERSION 1
+/* 2: the block-path workspace (GEFENX_WS_BLOCK) grew by one fixed-order
+ * partial record per stats workgroup, sized from numel, so a block workspace
+ * sized by a version-1 header is too small for the multi-tensor launcher.
+ * Bindings compare gefenx_abi_version() with the version they were written
+ * against and refuse a mismatch. */
+#define GEFENX_ABI_VERSION 2
 
 enum gefenx_status {
     GEFENX_OK = 0,

@@ -39,7 +39,10 @@ def test_binding_signatures_cover_header():
 
 
 def test_abi_version(lib):
-    assert lib.gefenx_abi_version() == 1
+    from gefen.kernels import _native
+    assert lib.gefenx_abi_version() == _native.ABI_VERSION == 2
+    hdr = open(os.path.join(ROOT, "include", "gefenx.h")).read()
+    assert "#define GEFENX_ABI_VERSION 2" in hdr
 
 
 # ----------------------------------------------------------- quant table

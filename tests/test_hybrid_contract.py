@@ -164,3 +164,98 @@ def test_one_determinism_policy_reaches_both_gefen_children():
     assert opt.muon is not None and opt.muon._deterministic is True
     assert opt.backup is not None and opt.backup._deterministic is True
     assert set(opt.state_dict()) == {"muon", "backup", "backup_optimizer"}
+
+
+# ----------------------------------------------- ZeRO-3 placeholder guard
+# (the reference's tests/test_zero_incompat_guard_cpu.py:163-205, 313-325)
+
+
+def test_zero3_placeholders_refused_in_both_forms():
+    placeholders = [("model.embed.weight", nn.Parameter(torch.empty(0))),
+                    ("model.layers.0.mlp.w", nn.Parameter(torch.empty(0))),
+                    ("model.norm.weight", nn.Parameter(torch.empty(0)))]
+    with pytest.raises(ValueError, match="ZeRO stage 3") as info:
+        GefenMuonHybrid(placeholders, lr=1e-3, fused=False)
+    msg = str(info.value)
+    assert "zero-numel" in msg and "backup-only" in msg and "plain Gefen" in msg
+    with pytest.raises(ValueError, match="ZeRO stage 3"):
+        GefenMuonHybrid([], [("model.norm.weight", nn.Parameter(torch.empty(0)))], lr=1e-3, fused=False)
+
+
+def test_real_or_mixed_backup_only_sets_still_construct():
+    real = [("norm.weight", nn.Parameter(torch.randn(8))), ("norm.bias", nn.Parameter(torch.randn(8)))]
+    opt = GefenMuonHybrid([], real, lr=1e-3)
+    assert opt.muon is None and isinstance(opt.backup, Gefen)
+    mixed = [("real.weight", nn.Parameter(torch.zeros(8))), ("empty.slot", nn.Parameter(torch.zeros(0)))]
+    opt = GefenMuonHybrid([], mixed, lr=1e-3)
+    assert opt.muon is None and len(opt.param_groups) == 1
+    with pytest.raises(ValueError, match="no parameters"):
+        GefenMuonHybrid([], [], lr=1e-3)
+
+
+# ------------------------------------------------- backup group cohorts
+
+
+@pytest.mark.parametrize("backup", ["gefen", "adamw"])
+def test_no_decay_cohorts(backup):
+    model = TinyLM()
+    opt = GefenMuonHybrid.from_model(model, lr=1e-3, backup_lr=4e-4, backup_weight_decay=0.1,
+                                     weight_decay=0.05, betas=(0.8, 0.99), eps=1e-7,
+                                     no_decay_substrings=("NORM", "bias"), backup_optimizer=backup)
+    groups = opt.backup.param_groups
+    assert len(groups) == 2
+    decay, exempt = groups
+    assert set(decay["param_names"]) == {"embed.weight", "lm_head.weight"}
+    assert set(exempt["param_names"]) == {"hidden.bias", "norm.weight", "norm.bias"}
+    assert decay["weight_decay"] == 0.1 and exempt["weight_decay"] == 0.0
+    for g in groups:
+        assert g["lr"] == 4e-4 and g["eps"] == 1e-7
+        if backup == "adamw":
+            assert tuple(g["betas"]) == (0.8, 0.99)
+        else:
+            assert (g["beta1"], g["beta2"]) == (0.8, 0.99)
+    # the Muon half keeps the shared weight decay
+    assert all(g["weight_decay"] == 0.05 for g in opt.muon.param_groups)
+    # a substring no name contains leaves one decaying cohort (the empty one is dropped)
+    opt = GefenMuonHybrid.from_model(TinyLM(), lr=1e-3, weight_decay=0.05, no_decay_substrings=("zzz",),
+                                     backup_optimizer=backup)
+    assert len(opt.backup.param_groups) == 1 and opt.backup.param_groups[0]["weight_decay"] == 0.05
+
+
+@pytest.mark.parametrize("backup", ["gefen", "adamw"])
+def test_without_no_decay_one_default_group(backup):
+    opt = GefenMuonHybrid.from_model(TinyLM(), lr=2e-3, weight_decay=0.02, backup_optimizer=backup)
+    (g,) = opt.backup.param_groups
+    assert g["lr"] == 2e-3 and g["weight_decay"] == 0.02
+    assert opt.backup.defaults["lr"] == 2e-3 and opt.backup.defaults["weight_decay"] == 0.02
+    if backup == "gefen":
+        assert opt.backup._factored_v_2d is False
+
+
+# ------------------------------------ load: the shadow runs child pre-hooks
+
+
+def test_adamw_child_pre_hook_can_migrate_a_checkpoint():
+    """A checkpoint the AdamW child's own load pre-hook repairs (a missing
+    "step" added back) loads through the hybrid's preflight."""
+    p = nn.Parameter(torch.randn(6))
+    opt = GefenMuonHybrid([], [("bias", p)], lr=1e-3, backup_optimizer="adamw", fused=False)
+    p.grad = torch.full_like(p, 1e-3)
+    opt.backup.step()
+    ckpt = opt.state_dict()
+    del ckpt["backup"]["state"][0]["step"]
+
+    def add_step(child, sd):
+        for st in sd["state"].values():
+            st.setdefault("step", torch.tensor(1.0))
+        return sd
+
+    fresh_p = nn.Parameter(torch.randn(6))
+    fresh = GefenMuonHybrid([], [("bias", fresh_p)], lr=1e-3, backup_optimizer="adamw", fused=False)
+    with pytest.raises(KeyError, match="step"):
+        fresh.load_state_dict(ckpt)
+    assert not fresh.backup.state
+    fresh.backup.register_load_state_dict_pre_hook(add_step)
+    fresh.load_state_dict(ckpt)
+    assert float(fresh.backup.state[fresh_p]["step"]) == 1.0
+    assert torch.equal(fresh.backup.state[fresh_p]["exp_avg"], opt.backup.state[p]["exp_avg"])
