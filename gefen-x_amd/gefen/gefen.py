@@ -13,14 +13,16 @@ The step runs on MI355X through the C ABI in include/gefenx.h:
   1D / factored_v_2d=False
            block-shared second moment (gefen.py:3488-3818).
 
-This build steps on the GPU only: parameters must live on a HIP device, and a
-missing gfx950 library raises instead of falling back to host math.
-``fused=False`` (the reference's decomposed torch-op step and its merged
-small-tensor batching, gefen.py:3329-3486, 3832-4013) computes the same
-arithmetic, so it runs on the same kernels and the same multi-tensor launch.
-A parameter paged between devices between steps (CPU offload) takes its
-state along: the state follows the parameter's device at the next step
-(gefen.py:1897-1927).
+Every step runs on the GPU, and a missing gfx950 library raises instead of
+falling back to host math.  ``fused=False`` (the reference's decomposed
+torch-op step and its merged small-tensor batching, gefen.py:3329-3486,
+3832-4013) computes the same arithmetic, so it runs on the same kernels and
+the same multi-tensor launch.  A parameter paged between devices between
+steps (CPU offload) takes its state along: the state follows the parameter's
+device at the next step (gefen.py:1897-1927).  A parameter that is in host
+memory at step time keeps its state in host memory too, and is stepped on the
+current HIP device through pinned staging (gefen/host_staging.py) with the
+same kernels, bit for bit as if it lived on the device.
 """
 from __future__ import annotations
 
@@ -29,6 +31,7 @@ import logging
 import math
 import os
 import warnings
+import weakref
 from collections import OrderedDict
 from typing import Iterable, Optional, Tuple, Union
 
@@ -36,6 +39,7 @@ import numpy as np
 import torch
 import torch.nn as nn
 
+from gefen import host_staging
 from gefen import partitioning
 from gefen import quantization as quantization_module
 from gefen.kernels import _native
@@ -240,7 +244,8 @@ def learn_gefen_exact_codebook_from_grad_periods(*, grad_periods, codebook_devic
     so chunking is exact); the DP runs on the device of the grads.  The
     product steps on HIP devices only, so use_fused_histogram is accepted for
     the reference's signature and the grads must be device tensors.
-    Returns None when there are no elements."""
+    codebook_device None keeps the codebook on the grads' device.  Returns
+    None when there are no elements."""
     del use_fused_histogram
     bins = int(num_codebooks) * 16
     counts_dev, total = _exact_histogram_counts(grad_periods, bins)
@@ -255,7 +260,8 @@ def learn_gefen_exact_codebook_from_grad_periods(*, grad_periods, codebook_devic
              "active_sums": centers[active] * counts[active]}
     codebook = quantization_module.exact_dp(histogram_stats=stats, num_codebooks=int(num_codebooks),
                                             force_endpoints=force_endpoints, device=counts_dev.device)
-    codebook = codebook.to(codebook_device)
+    if codebook_device is not None:
+        codebook = codebook.to(codebook_device)
     if verbose and compute_mse_logging:
         cb = codebook.cpu()
         ac = stats["active_centers"]
@@ -351,6 +357,10 @@ class Gefen(torch.optim.Optimizer):
         self._gefen_global_step_by_device = {}
         self._sr_seed_by_device = {}
         self._capt_plans = OrderedDict()
+        # host-resident parameters (CPU offload): pinned / device staging
+        # arenas, and each such parameter's device workspace
+        self._host_stager = host_staging.HostStager()
+        self._offload_ws = {}  # id(p) -> (weak reference to p, workspace)
         defaults = dict(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps, weight_decay=weight_decay)
         super().__init__(self._normalize_param_groups(params), defaults)
 
@@ -505,6 +515,8 @@ class Gefen(torch.optim.Optimizer):
         flat = grad.detach().reshape(-1)
         if flat.numel() == 1:
             return 1
+        if flat.device.type == "cpu":  # a host-resident parameter: the search runs on the GPU
+            flat = flat.to(self._compute_device())
         return partitioning.find_period_by_block_variance(
             flat, print_results=False, parameter_name=param_name, parameter_shape=tuple(param.shape),
             backend="cuda_kernel", input_is_squared=False)
@@ -533,22 +545,44 @@ class Gefen(torch.optim.Optimizer):
                                      "while learning Gefen codebook".format(period, name, flat.numel()))
                 yield name, flat, int(period), grad
 
+    def _device_grad_periods(self, reuse_existing_periods=False, homes=None):
+        """_iter_gefen_grad_periods with every flat gradient on a HIP device:
+        a host-resident gradient is copied to the compute device one tensor
+        at a time, as the consumer reaches it (the histogram kernel reads it
+        there).  `homes`, when given, collects each gradient's own device."""
+        for name, flat, period, grad in self._iter_gefen_grad_periods(reuse_existing_periods):
+            if homes is not None:
+                homes.append(grad.device)
+            if flat.device.type == "cpu":
+                flat = flat.to(self._compute_device())
+            yield name, flat, period, grad
+
     def _grad_histogram_counts(self, bins, reuse_existing_periods=False):
         """The step-1 histogram over this optimizer's gradients (gefen.py:
         417-469): (int64 counts on the device, number of elements), or
         (None, 0) when no parameter has a gradient."""
-        return _exact_histogram_counts(self._iter_gefen_grad_periods(reuse_existing_periods), bins)
+        return _exact_histogram_counts(self._device_grad_periods(reuse_existing_periods), bins)
 
     def _learn_gefen_exact_codebook(self, reuse_existing_periods=False):
         """learn_gefen_exact_codebook_from_grad_periods (gefen.py:417-517)
         over this optimizer's gradients: the 256-entry codebook, endpoints
-        forced, on the gradients' device; None without gradients."""
-        grad_periods = list(self._iter_gefen_grad_periods(reuse_existing_periods))
-        if not grad_periods:
-            return None
-        return learn_gefen_exact_codebook_from_grad_periods(
-            grad_periods=grad_periods, codebook_device=grad_periods[0][1].device, num_codebooks=NUM_CODEBOOKS,
-            force_endpoints=True, verbose=False, compute_mse_logging=False)
+        forced; None without gradients.  Returns (codebook on the first
+        gradient's own device, as the reference keeps it, or None; the same
+        values on the device the histogram ran on)."""
+        homes = []
+        cb = learn_gefen_exact_codebook_from_grad_periods(
+            grad_periods=self._device_grad_periods(reuse_existing_periods, homes), codebook_device=None,
+            num_codebooks=NUM_CODEBOOKS, force_endpoints=True, verbose=False, compute_mse_logging=False)
+        if cb is None:
+            return None, None
+        return (cb if homes[0] == cb.device else cb.to(homes[0])), cb
+
+    def _adopt_codebook(self, home, computed):
+        """Make `home` the codebook; keep the copy on the compute device."""
+        self._gefen_codebook = home
+        self._gefen_codebook_by_device.clear()
+        if computed is not None and computed.device != home.device:
+            self._gefen_codebook_by_device[computed.device] = computed
 
     def _maybe_save_gefen_grad_histogram(self):
         """gefen.py:3095-3150: at the global steps listed in
@@ -581,12 +615,11 @@ class Gefen(torch.optim.Optimizer):
     def _maybe_refresh_gefen_codebook(self):
         if self._gefen_codebook is not None:
             return
-        cb = self._learn_gefen_exact_codebook(
+        cb, computed = self._learn_gefen_exact_codebook(
             reuse_existing_periods=any("automatic_period" in self.state.get(p, {})
                                        for g in self.param_groups for p in g["params"]))
         if cb is not None:
-            self._gefen_codebook = cb
-            self._gefen_codebook_by_device.clear()
+            self._adopt_codebook(cb, computed)
 
     def _refresh_codebook_with_requant(self):
         """gefen.py:3020-3070: re-learn, then map stored indices onto the new
@@ -594,7 +627,7 @@ class Gefen(torch.optim.Optimizer):
         old = self._gefen_codebook
         if old is None:
             return
-        new = self._learn_gefen_exact_codebook(reuse_existing_periods=True)
+        new, computed = self._learn_gefen_exact_codebook(reuse_existing_periods=True)
         if new is None:
             return
         old_h = old.detach().cpu().float().numpy()
@@ -615,8 +648,7 @@ class Gefen(torch.optim.Optimizer):
                     staged.append((st["m_codebook"], choose.to(st["m_codebook"].device)[st["m_codebook"].long()]))
         for dst, src in staged:
             dst.copy_(src)
-        self._gefen_codebook = new
-        self._gefen_codebook_by_device.clear()
+        self._adopt_codebook(new, computed)
 
     # -------------------------------------------------------------- step
 
@@ -638,13 +670,38 @@ class Gefen(torch.optim.Optimizer):
                     raise RuntimeError("gradient and parameter {} must be on the same device: gradient on {}, "
                                        "parameter on {}".format(name, g.device, p.device))
                 if p.numel() and p.device.type != "cuda":
-                    raise RuntimeError("Gefen (MI355X build) steps HIP device parameters only; {} is on {}".format(
-                        name, p.device))
+                    self._check_host_parameter(name, p)
                 if p.dtype == torch.float64:
                     raise NotImplementedError("Gefen fused kernels are not implemented for 'Double' ({})".format(name))
                 if g.dtype != p.dtype:
                     raise RuntimeError("gradient dtype {} does not match parameter {} dtype {}".format(
                         g.dtype, name, p.dtype))
+
+    # Whether parameters in host memory are stepped (through the pinned
+    # staging of gefen/host_staging.py); subclasses whose step has no staged
+    # path turn it off.
+    _steps_host_params = True
+
+    def _check_host_parameter(self, name, p):
+        """A parameter that is not on a HIP device: host memory is stepped on
+        the compute device through pinned staging (CPU offload, reference
+        gefen.py:1897-1927); anything else, or host memory without a HIP
+        device, or under capturable (a graph cannot record host memory), is
+        refused before anything mutates."""
+        if p.device.type != "cpu" or not self._steps_host_params:
+            raise RuntimeError("Gefen (MI355X build) steps HIP device parameters only; {} is on {}".format(
+                name, p.device))
+        if self.capturable:
+            raise RuntimeError("Gefen capturable=True steps HIP device parameters only; {} is in host memory "
+                               "(CUDA-graph capture cannot record host-resident tensors)".format(name))
+        if not torch.cuda.is_available():
+            raise RuntimeError("Gefen (MI355X build) steps host-resident parameters on a HIP device, and none is "
+                               "available ({} is on {})".format(name, p.device))
+
+    @staticmethod
+    def _compute_device():
+        """The HIP device that steps host-resident parameters: the current one."""
+        return torch.device("cuda", torch.cuda.current_device())
 
     def _lr_scalar(self, group) -> float:
         """group["lr"] as a python float (gefen.py:1530-1555).  A tensor lr is
@@ -809,30 +866,69 @@ class Gefen(torch.optim.Optimizer):
 
     def _desc_row(self, group, p, grad, factored, prepared):
         """One gefenx_tensor_desc (include/gefenx.h) as a tuple in field order."""
-        state, lr, inv_bc2, inv_bc1, wdf = prepared
-        if lr is None:  # capturable: the tensor reads its scalar row on the device
-            lr, inv_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
-        period = state["automatic_period"]
-        nb = p.numel() // period
+        state = prepared[0]
+        nb = p.numel() // state["automatic_period"]
         if factored:
             rows, cols = p.shape
             ws = self._workspace(state, _native.WS_FACTORED, rows, cols, nb, p.device)
             v0, v1 = state["v_row"].data_ptr(), state["v_col"].data_ptr()
-            ps0, ps1, gs0, gs1 = p.stride(0), p.stride(1), grad.stride(0), grad.stride(1)
+            strides = (p.stride(0), p.stride(1), grad.stride(0), grad.stride(1))
         else:
             ws = self._workspace(state, _native.WS_BLOCK, 1, p.numel(), nb, p.device)
             v0, v1 = state["vmean"].data_ptr(), 0
             if p.is_contiguous() and grad.is_contiguous():
                 rows, cols = 1, p.numel()
-                ps0, ps1, gs0, gs1 = cols, 1, cols, 1
+                strides = (cols, 1, cols, 1)
             else:  # a transposed view (_block_view_ok): logical [rows, cols]
                 rows, cols = p.shape
-                ps0, ps1, gs0, gs1 = p.stride(0), p.stride(1), grad.stride(0), grad.stride(1)
+                strides = (p.stride(0), p.stride(1), grad.stride(0), grad.stride(1))
+        return self._desc_fields(group, prepared, factored, p.dtype, rows, cols, strides, p.data_ptr(),
+                                 grad.data_ptr(), state["m_codebook"].data_ptr(),
+                                 state["m_magnitude"].data_ptr(), v0, v1, ws.data_ptr())
+
+    @staticmethod
+    def _desc_fields(group, prepared, factored, dtype, rows, cols, strides, p_ptr, g_ptr, idx_ptr, mag_ptr,
+                     v0, v1, ws_ptr):
+        state, lr, inv_bc2, inv_bc1, wdf = prepared
+        if lr is None:  # capturable: the tensor reads its scalar row on the device
+            lr, inv_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
         beta1, beta2 = group["beta1"], group["beta2"]
-        return (p.data_ptr(), grad.data_ptr(), state["m_codebook"].data_ptr(), state["m_magnitude"].data_ptr(),
-                v0, v1, ws.data_ptr(), rows, cols, ps0, ps1, gs0, gs1, period,
-                _fused._dtype_code(p.dtype), 1 if factored else 0,
-                lr, group["eps"], inv_bc2, inv_bc1, wdf, 1.0 - beta1, beta2, 1.0 - beta2)
+        return (p_ptr, g_ptr, idx_ptr, mag_ptr, v0, v1, ws_ptr, rows, cols) + tuple(strides) + (
+            state["automatic_period"], _fused._dtype_code(dtype), 1 if factored else 0,
+            lr, group["eps"], inv_bc2, inv_bc1, wdf, 1.0 - beta1, beta2, 1.0 - beta2)
+
+    def _launch_staged(self, device, items, arena):
+        """One multi-tensor launch over a chunk of host-resident parameters
+        whose parameter, gradient and state copies sit in `arena` (device
+        bytes laid out by host_staging); their workspaces stay on the device
+        between steps, outside the state dict (the state follows the
+        parameter to the host)."""
+        base = arena.data_ptr()
+        rows, dtypes = [], set()
+        for it in items:
+            state, p = it.prepared[0], it.p
+            at = {key: base + off for key, _, off in it.pieces}
+            nb = p.numel() // state["automatic_period"]
+            if it.factored:
+                r, c = p.shape
+                kind, wr, wc = _native.WS_FACTORED, r, c
+                v0, v1 = at["v_row"], at["v_col"]
+            else:
+                r, c = 1, p.numel()
+                kind, wr, wc = _native.WS_BLOCK, 1, c
+                v0, v1 = at["vmean"], 0
+            need = int(_native.load().gefenx_workspace_bytes(kind, wr, wc, nb))
+            ref, ws = self._offload_ws.get(id(p), (None, None))
+            if ref is None or ref() is not p or ws.numel() < need or ws.device != device:
+                for key in [k for k, (r, _) in self._offload_ws.items() if r() is None]:
+                    del self._offload_ws[key]  # parameters that no longer exist
+                ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
+                self._offload_ws[id(p)] = (weakref.ref(p), ws)
+            rows.append(self._desc_fields(it.group, it.prepared, it.factored, p.dtype, r, c, (c, 1, c, 1),
+                                          at["p"], base + it.grad_offset, at["m_codebook"], at["m_magnitude"],
+                                          v0, v1, ws.data_ptr()))
+            dtypes.add(p.dtype)
+        self._multi_tensor_step(device, rows, dtypes)
 
     def _multi_tensor_step(self, device, rows, dtypes):
         """All parameters of one device in one gefenx_multi_tensor_step call
@@ -1053,6 +1149,7 @@ class Gefen(torch.optim.Optimizer):
             self._ensure_gefen_global_step_devices()
         batches = {}  # device -> (desc rows, dtypes, scalar-row pointers, capturable rows)
         deferred = []  # single-tensor launches that read the prologue's scalar rows
+        host_items = []  # host-resident parameters (CPU offload)
         for group in self.param_groups:
             for name, p in self._iter_group_params_with_names(group):
                 grad = p.grad
@@ -1067,6 +1164,10 @@ class Gefen(torch.optim.Optimizer):
                 else:
                     prepared = self._prepare_block(group, name, p, grad)
                 state = prepared[0]
+                if p.device.type == "cpu":  # host-resident: stepped below through pinned staging
+                    state.pop("_gefenx_ws", None)  # a device workspace does not follow it to the host
+                    host_items.append(host_staging.StagedItem(group, name, p, grad, factored, prepared))
+                    continue
                 # deterministic=True (gefen.py:1048-1057): block-path views
                 # take the contiguous route, whose sums run in a fixed order
                 # (the view tiles accumulate with atomics)
@@ -1105,6 +1206,11 @@ class Gefen(torch.optim.Optimizer):
         else:
             for device, (rows, dtypes, _, _) in batches.items():
                 self._multi_tensor_step(device, rows, dtypes)
+        if host_items:
+            device = self._compute_device()
+            self._host_stager.run(host_items, device,
+                                  lambda items, arena: self._launch_staged(device, items, arena),
+                                  host_staging.chunk_bytes_from_env())
         self._gefen_global_step += 1
         return loss
 

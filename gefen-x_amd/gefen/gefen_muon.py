@@ -214,6 +214,9 @@ class GefenMuon(Gefen):
     """Muon with Gefen's quantised momentum; arguments mirror the reference
     (gefen_muon.py:546-573)."""
 
+    # Muon's momentum, Newton-Schulz and apply read device tensors only
+    _steps_host_params = False
+
     def __init__(
         self,
         params: Iterable[Union[nn.Parameter, Tuple[str, nn.Parameter]]],

@@ -58,12 +58,25 @@ def test_no_state_yet_is_a_no_op():
     assert st == {"name": "w"}
 
 
-def test_fused_false_is_accepted_and_host_parameters_are_refused():
+@pytest.mark.skipif(torch.cuda.is_available(), reason="host parameters are stepped when a HIP device exists")
+def test_host_parameters_without_a_hip_device_are_refused():
+    """Host-resident parameters are stepped on a HIP device through pinned
+    staging; with none available the step refuses before anything mutates
+    (there is no host arithmetic in the product)."""
     p = torch.nn.Parameter(torch.randn(16, 16))
     opt = Gefen([("w", p)], lr=1e-2, fused=False)
     assert opt.fused is False
     p.grad = torch.randn(16, 16) * 0.1
-    with pytest.raises(RuntimeError, match="HIP device"):
+    with pytest.raises(RuntimeError, match="on a HIP device, and none is available"):
         opt.step()
     assert opt._gefen_codebook is None
     assert "automatic_period" not in opt.state.get(p, {})
+
+
+def test_capturable_host_parameters_are_refused():
+    p = torch.nn.Parameter(torch.randn(16, 16))
+    opt = Gefen([("w", p)], lr=1e-2, capturable=True)
+    p.grad = torch.randn(16, 16) * 0.1
+    with pytest.raises(RuntimeError, match="capturable=True steps HIP device parameters only"):
+        opt.step()
+    assert opt._gefen_codebook is None

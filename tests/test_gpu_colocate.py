@@ -127,12 +127,15 @@ def test_fused_false_is_the_same_step(dev):
         assert torch.equal(pa, pb), n
 
 
-def test_host_parameter_is_refused_before_any_mutation(dev):
+def test_capturable_host_parameter_is_refused_before_any_mutation(dev):
+    """Host parameters are stepped through pinned staging (tests/
+    test_gpu_host_resident.py), but not under capturable=True: a graph
+    cannot record host memory."""
     from gefen import Gefen
     p = torch.nn.Parameter(torch.randn(16, 16))
-    opt = Gefen([("w", p)], lr=1e-2, fused=False)
+    opt = Gefen([("w", p)], lr=1e-2, capturable=True)
     p.grad = torch.randn(16, 16) * 0.1
-    with pytest.raises(RuntimeError, match="HIP device"):
+    with pytest.raises(RuntimeError, match="capturable=True steps HIP device parameters only"):
         opt.step()
     assert opt._gefen_codebook is None
     assert "automatic_period" not in opt.state.get(p, {})
