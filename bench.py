@@ -388,6 +388,41 @@ def qwen3_4b_shapes():
     return shapes
 
 
+def make_qwen_params(torch, dev, seed=0):
+    """The Qwen3-4B-shaped bf16 set, N(0, 0.02) from a seed; every 10th 2D
+    tensor is a transposed view (.t()) of [C, R] storage."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    params, n2d = [], 0
+    for name, shape in qwen3_4b_shapes():
+        if len(shape) == 2:
+            n2d += 1
+            if n2d % 10 == 0:
+                st = torch.empty(shape[1], shape[0], dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gen)
+                params.append((name, torch.nn.Parameter(st.t())))
+                continue
+        params.append((name, torch.nn.Parameter(
+            torch.empty(shape, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gen))))
+    return params
+
+
+def fill_qwen_grads(torch, params, step_seed, dev):
+    """Grads 1e-3 * StudentT(nu=3) from a seed, drawn as z * sqrt(3 / chi2_3)
+    (chi2_3 the sum of three squared normals); a transposed-view parameter
+    gets a grad of the same layout."""
+    gen = torch.Generator(device=dev).manual_seed(50_000 + step_seed)
+    for _, p in params:
+        shape = tuple(p.shape)
+        z = torch.empty(shape, dtype=torch.float32, device=dev).normal_(generator=gen)
+        chi2 = torch.zeros(shape, dtype=torch.float32, device=dev)
+        for _ in range(3):
+            chi2.add_(torch.empty(shape, dtype=torch.float32, device=dev).normal_(generator=gen).square_())
+        g = (z * torch.rsqrt(chi2.div_(3.0)) * 1e-3).to(torch.bfloat16)
+        del z, chi2
+        if not p.is_contiguous():
+            g = g.t().contiguous().t()
+        p.grad = g
+
+
 def bench_qwen(args):
     """the many-tensor launcher on a Qwen3-4B-shaped
     bf16 set (398 tensors, 4,022,468,096 params); 25 of the 253 2D tensors
@@ -399,25 +434,10 @@ def bench_qwen(args):
     from gefen.kernels import _native
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    shapes = qwen3_4b_shapes()
-    gen = torch.Generator(device=dev).manual_seed(0)
-    params, n2d = [], 0
-    for name, shape in shapes:
-        if len(shape) == 2:
-            n2d += 1
-            if n2d % 10 == 0:
-                st = torch.empty(shape[1], shape[0], dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gen)
-                params.append((name, torch.nn.Parameter(st.t())))
-                continue
-        params.append((name, torch.nn.Parameter(
-            torch.empty(shape, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gen))))
+    params = make_qwen_params(torch, dev)
     n_params = sum(p.numel() for _, p in params)
     n_views = sum(1 for _, p in params if not p.is_contiguous())
-    t3 = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
-    for _, p in params:
-        p.grad = (t3.sample(p.shape) * 1e-3).to(torch.bfloat16)
-        if not p.is_contiguous():
-            p.grad = p.grad.t().contiguous().t()
+    fill_qwen_grads(torch, params, 0, dev)
     lib = _native.load()
     results = {}
     for factored in (True, False):

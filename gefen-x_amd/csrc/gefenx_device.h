@@ -176,11 +176,44 @@ __device__ __forceinline__ float raw_elem(const Raw8<DT>& r, int k) {
     else return to_f32<DT>((uint16_t)((k & 1) ? (r.w[k >> 1] >> 16) : (r.w[k >> 1] & 0xffffu)));
 }
 
+// The same 8 elements through element loads, for a base that is not
+// 16-byte aligned (any element offset); packed as load_raw8 packs them.
+template <int DT>
+__device__ __forceinline__ void load_raw8_elems(const typename Elem<DT>::T* __restrict__ base, Raw8<DT>& r) {
+    if constexpr (DT == F32) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r.f[k] = *gbl(base + k);
+    } else {
+        const uint16_t* b = reinterpret_cast<const uint16_t*>(base);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.w[j] = (uint32_t)*gbl(b + 2 * j) | ((uint32_t)*gbl(b + 2 * j + 1) << 16);
+    }
+}
+
+// Squared-gradient accumulation.  The reference's decomposed step squares in
+// fp32 and sums in float64 (gefen.py:2959-2996, 129-191).  A double
+// accumulator does the same; a float one keeps 8-element fp32 partials, which
+// is exact per term for 16-bit grads (g*g fits in fp32) and within 1e-6
+// after the sum.
+__device__ __forceinline__ void sq_add(float& a, float g) { a = __builtin_fmaf(g, g, a); }
+__device__ __forceinline__ void sq_add(double& a, float g) { a += (double)(g * g); }
+
 struct RawIdx8 { uint32_t lo, hi; };
 
 __device__ __forceinline__ RawIdx8 load_raw_idx8(const uint8_t* __restrict__ base) {
     const u32x2 v = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x2*>(base)));
     return RawIdx8{v.x, v.y};
+}
+
+__device__ __forceinline__ RawIdx8 load_raw_idx8_elems(const uint8_t* __restrict__ base) {
+    RawIdx8 r{0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t v = (uint32_t)*gbl(base + k);
+        if (k < 4) r.lo |= v << (8 * k);
+        else r.hi |= v << (8 * (k - 4));
+    }
+    return r;
 }
 
 __device__ __forceinline__ uint32_t raw_idx(const RawIdx8& r, int k) {
@@ -277,6 +310,19 @@ __device__ __forceinline__ float div_by_block(float u, float b, float y) {
         }
     }
     return u / b;
+}
+
+// RN(u/d) for a divisor shared by many elements, with y = block_recip(d):
+// div_by_block's Markstein step wherever nothing under- or overflows (u zero
+// or 2^-100 <= |u|, |u*y| <= 2^100), the IEEE divide elsewhere.
+__device__ __forceinline__ float div_by_const(float u, float d, float y) {
+    const float q0 = u * y;
+    const float aq = fabsf(q0);
+    if (y != 0.0f && fabsf(u) >= 0x1p-100f && fabsf(u) <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f) {
+        const float r = __builtin_fmaf(-q0, d, u);
+        return __builtin_fmaf(r, y, q0);
+    }
+    return u == 0.0f && y != 0.0f ? q0 : u / d;
 }
 
 // Reciprocal for div_by_block: RN(1/b) when b and 1/b are normal and finite.

@@ -82,9 +82,11 @@ struct TensorWork {
     int32_t dtype, mode;
     int32_t fast_stats, fast_apply;  // kernel variant: 0 general, 1 contiguous, 2 transposed view
     int32_t write_p, sr, bf16_mean, det_epl;  // det_epl: block stats elements per item (8 or 1)
+    int32_t det_vec;     // block stats items: vector loads (grad 16-byte, indices 8-byte aligned)
     int32_t partial;     // block path with the caller's per-block stepsize (no vmean)
     int32_t fin_wide;    // block finalize: one workgroup per block (blocks span many stats records)
-    float eps, beta2, alpha2, pad2_;
+    float eps, beta2, alpha2;
+    float bc2_div;       // reference-order divisor (factored bc2, block sqrt(bc2)) or 0
     StepScalars sc;
     MomentumCoef mc;
 };
@@ -98,6 +100,36 @@ __device__ __forceinline__ StepScalars read_scalars(const TensorWork& w) {
         s.wdf = w.step_scalars[3];
     }
     return s;
+}
+
+// The factored stepsize of one element in the rounding order of the
+// reference's decomposed step (gefen.py:2996-3006): vh = (v_row*v_col)/mean,
+// h = sqrt(vh/bc2) + eps, (1/h) * (1/bc1), one fp32 rounding per operation.
+// The divisions by the tensor-wide mean and bc2 take div_by_const; sqrt and
+// 1/h are the correctly rounded operations.  Used for fp32 parameters when
+// the host gave bc2 (w.bc2_div); otherwise the kernels take the cheaper
+// sqrt(v_row*s) * sqrt(v_col) form, within 1e-6 of this.
+struct RefStep {
+    float mean, rmean, bc2, rbc2, eps, inv_bc1;
+    bool on;
+};
+
+__device__ __forceinline__ RefStep make_ref_step(const TensorWork& w, const StepScalars& sc, float mean) {
+    RefStep r;
+    r.on = w.bc2_div > 0.0f;
+    r.mean = mean;
+    r.rmean = block_recip(mean);
+    r.bc2 = w.bc2_div;
+    r.rbc2 = block_recip(w.bc2_div);
+    r.eps = w.eps;
+    r.inv_bc1 = sc.inv_bc1;
+    return r;
+}
+
+__device__ __forceinline__ float ref_step(const RefStep& r, float v_row, float v_col) {
+    const float vh = div_by_const(v_row * v_col, r.mean, r.rmean);
+    const float h = sqrtf(div_by_const(vh, r.bc2, r.rbc2)) + r.eps;
+    return (1.0f / h) * r.inv_bc1;
 }
 
 // Wave-uniform running block max of |u| as ordered uint bits (NaN > inf >
@@ -144,6 +176,9 @@ struct FactStatsLds {
 template <int DT, bool FAST, int LF>
 __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg, FactStatsLds& lds) {
     using T = typename Elem<DT>::T;
+    // fp32 grads: every square into a float64 accumulator, as the reference
+    // sums them; 16-bit grads: exact squares in 8-row / 16-column fp32 partials
+    using Acc = std::conditional_t<DT == F32, double, float>;
     constexpr int H = 2;  // chunks per lane per row
     float* s_cbr = lds.cbr;
     auto& s_col = lds.col;
@@ -195,20 +230,20 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
     const int64_t dB4 = div_floor(d4, P, invP);
     const int64_t dP4 = d4 - dB4 * P;
 
-    // column sums: fp32 in registers over 8 rows, then added into the wave's
+    // column sums: in registers over 8 rows, then added into the wave's
     // float64 slots in LDS (each lane owns its 16 columns' slots)
-    float colf[H][kChunk];
+    Acc colf[H][kChunk];
 #pragma unroll
     for (int h = 0; h < H; ++h)
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) { colf[h][k] = 0.0f; s_col[wave][k][h][lane] = 0.0; }
+        for (int k = 0; k < kChunk; ++k) { colf[h][k] = 0; s_col[wave][k][h][lane] = 0.0; }
     auto flush_cols = [&]() {
 #pragma unroll
         for (int h = 0; h < H; ++h)
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 s_col[wave][k][h][lane] += (double)colf[h][k];
-                colf[h][k] = 0.0f;
+                colf[h][k] = 0;
             }
     };
     int nrows_f = 0;
@@ -272,7 +307,7 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
         for (int u = 0; u < 2; ++u) {
             const int64_t r = rr0 + (int64_t)u * kWaves;
             if (r >= r_end) break;
-            float rs[H];
+            Acc rs[H];
             const bool uniform = (pin + span - 1) < P;
             if (uniform) {
                 if (blk != wm.blk) {
@@ -293,7 +328,7 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
                     // integer max, which ranks NaN above inf like torch's amax.
                     float mf = 0.0f;
                     auto chunk = [&](int h, auto masked) {
-                        rs[h] = 0.0f;
+                        rs[h] = 0;
 #pragma unroll
                         for (int k = 0; k < kChunk; ++k) {
                             float gv = raw_elem<DT>(b.graw[u][h], k);
@@ -301,19 +336,20 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
                             const float uu = momentum_value<LF>(s_cbr[raw_idx(b.iraw[u][h], k)], mag_cur, gv, mc);
                             if constexpr (decltype(masked)::value) mf = nv[h] > 0 ? __builtin_fmaxf(mf, fabsf(uu)) : mf;
                             else mf = __builtin_fmaxf(mf, fabsf(uu));
-                            rs[h] = __builtin_fmaf(gv, gv, rs[h]);
-                            colf[h][k] = __builtin_fmaf(gv, gv, colf[h][k]);
+                            sq_add(rs[h], gv);
+                            sq_add(colf[h][k], gv);
                         }
                     };
 #pragma unroll
                     for (int h = 0; h < H; ++h) {
                         if (hall[h]) chunk(h, std::false_type{});
                         else if (hany[h]) chunk(h, std::true_type{});
-                        else rs[h] = 0.0f;
+                        else rs[h] = 0;
                     }
                     // integer test: NaN and inf both fail it, whatever the
-                    // compiler assumes about float compares
-                    const bool fin = (__float_as_uint(rs[0] + rs[1]) & 0x7fffffffu) < 0x7f800000u;
+                    // compiler assumes about float compares (a square that
+                    // overflows fp32 is inf in either accumulator)
+                    const bool fin = (__float_as_uint((float)(rs[0] + rs[1])) & 0x7fffffffu) < 0x7f800000u;
                     if (__builtin_expect(mag_ok && __all(fin), 1)) {
                         const uint32_t mb_ = __float_as_uint(mf);
                         wm.bits = mb_ > wm.bits ? mb_ : wm.bits;
@@ -336,7 +372,7 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
                     uint32_t m = wm.bits;
 #pragma unroll
                     for (int h = 0; h < H; ++h) {
-                        rs[h] = 0.0f;
+                        rs[h] = 0;
                         if (nv[h] == 0) continue;  // columns past C (last tile)
 #pragma unroll
                         for (int k = 0; k < kChunk; ++k) {
@@ -345,8 +381,8 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
                             const float uu = momentum_value<LF>(s_cbr[b.isc[u][h][k]], mag_cur, gv, mc);
                             const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
                             m = ub > m ? ub : m;
-                            rs[h] = __builtin_fmaf(gv, gv, rs[h]);
-                            colf[h][k] = __builtin_fmaf(gv, gv, colf[h][k]);
+                            sq_add(rs[h], gv);
+                            sq_add(colf[h][k], gv);
                         }
                     }
                     wm.bits = m;
@@ -357,7 +393,7 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
                 wm.blk = -1;
 #pragma unroll
                 for (int h = 0; h < H; ++h) {
-                    rs[h] = 0.0f;
+                    rs[h] = 0;
                     if (nv[h] == 0) continue;
                     const int64_t off = pin + (cc[h] - tc0);
                     const int64_t db = div_floor(off, P, invP);
@@ -375,8 +411,8 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
                             const float uu = momentum_value<LF>(s_cbr[ix], mo, gv, mc);
                             const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
                             m = ub > m ? ub : m;
-                            rs[h] = __builtin_fmaf(gv, gv, rs[h]);
-                            colf[h][k] = __builtin_fmaf(gv, gv, colf[h][k]);
+                            sq_add(rs[h], gv);
+                            sq_add(colf[h][k], gv);
                             if (++pp == P) {
                                 if (m) gatomic_max(mb + bb, m);
                                 m = 0u;
@@ -646,14 +682,17 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
         lds_barrier();
         if (s + 1 < n_sub) fetch(s + 1, nxt);
         const int cs = s / n_rb, rb = s - cs * n_rb;
-        float colf[kChunk];
+        // squares into float64 per term for fp32 grads and on the block path
+        // (the reference's sums), else 8-element fp32 partials
+        using Acc = std::conditional_t<DT == F32 || MODE == 1, double, float>;
+        Acc colf[kChunk];
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) colf[k] = 0.0f;
+        for (int k = 0; k < kChunk; ++k) colf[k] = 0;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int i = ib + 32 * h;
             const int64_t b = cur.blk[h];
-            float rs = 0.0f;
+            Acc rs = 0;
             uint32_t m = 0u;
             if (b >= 0) {
                 Raw8<DT> gr;
@@ -666,8 +705,8 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
                     m = ub > m ? ub : m;
                     float sq = gv * gv;
                     if constexpr (MODE == 1 && DT == BF16) sq = round_dt<BF16>(sq);
-                    rs += sq;
-                    if constexpr (MODE == 0) colf[k] += sq;
+                    rs += (Acc)sq;
+                    if constexpr (MODE == 0) colf[k] += (Acc)sq;
                 }
             }
             double rsd = (double)rs;
@@ -841,8 +880,13 @@ __device__ __forceinline__ void stats_block_one(const TensorWork& w, int64_t wg,
         const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
         if (FULL || e0 < N) {
             if constexpr (EPL == kChunk) {
-                load_raw8<DT>(g + e0, gr[i]);
-                ir[i] = load_raw_idx8(w.idx + e0);
+                if (w.det_vec) {
+                    load_raw8<DT>(g + e0, gr[i]);
+                    ir[i] = load_raw_idx8(w.idx + e0);
+                } else {  // grad or indices not 16 / 8-byte aligned: the same items, element loads
+                    load_raw8_elems<DT>(g + e0, gr[i]);
+                    ir[i] = load_raw_idx8_elems(w.idx + e0);
+                }
             } else {
                 graw[i] = to_f32<DT>(*gbl(g + e0));
                 iraw[i] = *gbl(w.idx + e0);
@@ -858,7 +902,7 @@ __device__ __forceinline__ void stats_block_one(const TensorWork& w, int64_t wg,
     for (int i = 0; i < kDetIters; ++i) {
         const int64_t e0 = base + ((int64_t)i * kThreads + threadIdx.x) * EPL;
         if (FULL || e0 < N) {
-            float cs = 0.0f;
+            double cs = 0.0;  // every square into float64, as the reference sums them
             if constexpr (EPL == kChunk) {
 #pragma unroll
                 for (int k = 0; k < kChunk; ++k) {
@@ -868,7 +912,7 @@ __device__ __forceinline__ void stats_block_one(const TensorWork& w, int64_t wg,
                     lmax = ub > lmax ? ub : lmax;
                     float sq = gv * gv;
                     if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                    cs += sq;
+                    cs += (double)sq;
                 }
             } else {
                 const float gv = graw[i];
@@ -877,9 +921,9 @@ __device__ __forceinline__ void stats_block_one(const TensorWork& w, int64_t wg,
                 lmax = ub > lmax ? ub : lmax;
                 float sq = gv * gv;
                 if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                cs = sq;
+                cs = (double)sq;
             }
-            lsum += (double)cs;
+            lsum += cs;
         }
     }
     lsum = wave_sum_d(lsum);
@@ -941,8 +985,13 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
             keys[i] = div_floor(e0, P, w.invP);
             mo[i] = *gbl(w.mag + keys[i]);
             if constexpr (EPL == kChunk) {
-                load_raw8<DT>(g + e0, gr[i]);
-                ir[i] = load_raw_idx8(w.idx + e0);
+                if (w.det_vec) {
+                    load_raw8<DT>(g + e0, gr[i]);
+                    ir[i] = load_raw_idx8(w.idx + e0);
+                } else {  // grad or indices not 16 / 8-byte aligned: the same items, element loads
+                    load_raw8_elems<DT>(g + e0, gr[i]);
+                    ir[i] = load_raw_idx8_elems(w.idx + e0);
+                }
             } else {
                 graw[i] = to_f32<DT>(*gbl(g + e0));
                 iraw[i] = *gbl(w.idx + e0);
@@ -960,7 +1009,7 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
         double val = 0.0;
         uint32_t mx = 0u;
         if (e0 < N) {
-            float cs = 0.0f;
+            double cs = 0.0;  // every square into float64, as the reference sums them
             if constexpr (EPL == kChunk) {
 #pragma unroll
                 for (int k = 0; k < kChunk; ++k) {
@@ -970,7 +1019,7 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
                     mx = ub > mx ? ub : mx;
                     float sq = gv * gv;
                     if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                    cs += sq;
+                    cs += (double)sq;
                 }
             } else {
                 const float gv = graw[i];
@@ -978,9 +1027,9 @@ __device__ __forceinline__ void stats_block_det(const TensorWork& w, int64_t wg)
                 mx = __float_as_uint(u) & 0x7fffffffu;
                 float sq = gv * gv;
                 if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
-                cs = sq;
+                cs = (double)sq;
             }
-            val = (double)cs;
+            val = cs;
         }
         const uint64_t heads = run_heads(key);
         const double sv = seg_suffix_sum(val, heads);
@@ -1128,7 +1177,9 @@ __device__ __forceinline__ void finalize_block_one(const TensorWork& w, const St
     if (w.bf16_mean) mean = round_dt<BF16>(mean);
     const float v = __builtin_fmaf(mean, w.alpha2, w.v0[b] * w.beta2);
     w.v0[b] = v;
-    const float h = sqrtf(v) * sc.inv_bc2 + w.eps;
+    // the reference divides by sqrt(bc2) (gefen.py:3794-3805); without that
+    // divisor from the host, multiply by the scalar row's 1/sqrt(bc2)
+    const float h = (w.bc2_div > 0.0f ? sqrtf(v) / w.bc2_div : sqrtf(v) * sc.inv_bc2) + w.eps;
     w.step[b] = (1.0f / h) * sc.inv_bc1;
     finalize_magnitude(w, b);
 }
@@ -1258,6 +1309,7 @@ __device__ __forceinline__ void load_vcol(const float* __restrict__ vc, float v[
 struct ApplyCtx {
     float row_scale;  // (1 / mean(v_row)) * (1/bc2)
     float c1;         // (1/bc1) * lr
+    RefStep ref;      // fp32 factored: the reference-order stepsize
     bool wd;
     StepScalars sc;
     bool dense;
@@ -1308,22 +1360,28 @@ __device__ __forceinline__ void apply_chunk(const TensorWork& w, const SharedTab
         }
     }
     if (w.write_p) {
-        float rs = 0.0f, bstep = 0.0f;
-        if constexpr (MODE == 0) rs = w.v0[ps.row] * cx.row_scale;
-        else bstep = w.step[ps.blk] * cx.sc.lr;
+        float rs = 0.0f, bstep = 0.0f, vr = 0.0f;
+        if constexpr (MODE == 0) {
+            vr = w.v0[ps.row];
+            rs = vr * cx.row_scale;
+        } else {
+            bstep = w.step[ps.blk];
+        }
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
             const float q = st.cbr[ix[k]] * m_new;
-            float s;
-            if constexpr (MODE == 0) {
-                const float h = __builtin_amdgcn_sqrtf(rs * vcv[k]) + w.eps;
-                s = __builtin_amdgcn_rcpf(h) * cx.c1;
-            } else {
-                s = bstep;
-            }
             float pw = raw_elem<DT>(pr, k);
             if (cx.wd) pw = round_dt<DT>(pw * cx.sc.wdf);
-            pv[k] = pw - q * s;
+            if constexpr (MODE == 0) {
+                if (DT == F32 && cx.ref.on) {
+                    pv[k] = pw - (q * ref_step(cx.ref, vr, vcv[k])) * cx.sc.lr;
+                } else {
+                    const float h = __builtin_amdgcn_sqrtf(rs * vcv[k]) + w.eps;
+                    pv[k] = pw - q * (__builtin_amdgcn_rcpf(h) * cx.c1);
+                }
+            } else {
+                pv[k] = pw - (q * bstep) * cx.sc.lr;  // the reference's order (gefen.py:3806-3818)
+            }
         }
     }
 }
@@ -1342,7 +1400,12 @@ __device__ __forceinline__ void apply_phase(const TensorWork& w, int64_t wg, int
         if (w.seed_dev != nullptr) cx.seed = (uint64_t)w.seed_dev[0];
     }
     cx.row_scale = 0.0f;
-    if constexpr (MODE == 0) cx.row_scale = (1.0f / stored_mean(w)) * cx.sc.inv_bc2;
+    cx.ref.on = false;
+    if constexpr (MODE == 0) {
+        const float mean = stored_mean(w);
+        cx.row_scale = (1.0f / mean) * cx.sc.inv_bc2;
+        if constexpr (DT == F32) cx.ref = make_ref_step(w, cx.sc, mean);
+    }
     cx.c1 = cx.sc.inv_bc1 * cx.sc.lr;
     cx.wd = cx.sc.wdf != 1.0f;
 
@@ -1431,9 +1494,12 @@ __device__ __forceinline__ void apply_phase(const TensorWork& w, int64_t wg, int
             float m_new = w.mag[blk];
             float y = w.minv[blk];
             float bstep = 0.0f;
-            if constexpr (MODE == 1) bstep = w.step[blk] * cx.sc.lr;
-            float rs = 0.0f;
-            if constexpr (MODE == 0) rs = w.v0[row] * cx.row_scale;
+            if constexpr (MODE == 1) bstep = w.step[blk];
+            float rs = 0.0f, vr = 0.0f;
+            if constexpr (MODE == 0) {
+                vr = w.v0[row];
+                rs = vr * cx.row_scale;
+            }
             int64_t r = row, c = col;
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
@@ -1446,22 +1512,27 @@ __device__ __forceinline__ void apply_phase(const TensorWork& w, int64_t wg, int
                     ix[k] = ni;
                     if (w.write_p) {
                         const float q = st.cbr[ni] * m_new;
-                        float s;
-                        if constexpr (MODE == 0) {
-                            const float h = __builtin_amdgcn_sqrtf(rs * w.v1[c]) + w.eps;
-                            s = __builtin_amdgcn_rcpf(h) * cx.c1;
-                        } else {
-                            s = bstep;
-                        }
                         float pw = pv[k];
                         if (cx.wd) pw = round_dt<DT>(pw * cx.sc.wdf);
-                        pv[k] = pw - q * s;
+                        if constexpr (MODE == 0) {
+                            if (DT == F32 && cx.ref.on) {
+                                pv[k] = pw - (q * ref_step(cx.ref, vr, w.v1[c])) * cx.sc.lr;
+                            } else {
+                                const float h = __builtin_amdgcn_sqrtf(rs * w.v1[c]) + w.eps;
+                                pv[k] = pw - q * (__builtin_amdgcn_rcpf(h) * cx.c1);
+                            }
+                        } else {
+                            pv[k] = pw - (q * bstep) * cx.sc.lr;
+                        }
                     }
                     if (++c == w.C) {
                         c = 0;
                         ++r;
                         if constexpr (MODE == 0) {
-                            if (k + 1 < nvalid) rs = w.v0[r] * cx.row_scale;
+                            if (k + 1 < nvalid) {
+                                vr = w.v0[r];
+                                rs = vr * cx.row_scale;
+                            }
                         }
                     }
                     if (++pin == w.P) {
@@ -1471,7 +1542,7 @@ __device__ __forceinline__ void apply_phase(const TensorWork& w, int64_t wg, int
                             m_old = w.mag_old[blk];
                             m_new = w.mag[blk];
                             y = w.minv[blk];
-                            if constexpr (MODE == 1) bstep = w.step[blk] * cx.sc.lr;
+                            if constexpr (MODE == 1) bstep = w.step[blk];
                         }
                     }
                 }
@@ -1545,6 +1616,7 @@ struct FastArgs {
     float row_scale, c1, eps, wdf, lr;
     bool wd;
     MomentumCoef mc;
+    RefStep ref;         // fp32 factored: the reference-order stepsize (vcs then holds v_col itself)
 };
 
 // Inputs of one chunk, loaded one pipeline stage ahead of its math.
@@ -1627,18 +1699,30 @@ __device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTable
             ix[k] = e.y + (__uint_as_float(e.x) < xs[k] ? 1u : 0u);
         }
     }
-    float sr = 0.0f, bstep = 0.0f;
+    if constexpr (MODE == 0 && DT == F32) {
+        if (a.ref.on) {  // reference order; in.vc holds v_col
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                const float q = ft.cbr[ix[k]] * m_new;
+                float pw = raw_elem<DT>(in.p, k);
+                if (a.wd) pw = round_dt<DT>(pw * a.wdf);
+                pv[k] = pw - (q * ref_step(a.ref, in.rv, in.vc[k])) * a.lr;
+            }
+            return;
+        }
+    }
+    float sr = 0.0f;
     if constexpr (MODE == 0) sr = __builtin_amdgcn_sqrtf(in.rv * a.row_scale);
-    else bstep = in.rv * a.lr;
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
         const float q = ft.cbr[ix[k]] * m_new;
-        float st;
-        if constexpr (MODE == 0) st = __builtin_amdgcn_rcpf(__builtin_fmaf(sr, in.vc[k], a.eps)) * a.c1;
-        else st = bstep;
         float pw = raw_elem<DT>(in.p, k);
         if (a.wd) pw = round_dt<DT>(pw * a.wdf);
-        pv[k] = pw - q * st;
+        if constexpr (MODE == 0) {
+            pv[k] = pw - q * (__builtin_amdgcn_rcpf(__builtin_fmaf(sr, in.vc[k], a.eps)) * a.c1);
+        } else {
+            pv[k] = pw - (q * in.rv) * a.lr;  // the reference's order (gefen.py:3806-3818)
+        }
     }
 }
 
@@ -1677,6 +1761,13 @@ __device__ __forceinline__ FastArgs<DT> make_fast_args(const TensorWork& w, floa
     a.lr = sc.lr;
     a.wd = sc.wdf != 1.0f;
     a.mc = w.mc;
+    a.ref.on = false;
+    if constexpr (DT == F32) {
+        if (w.mode == 0 && w.bc2_div > 0.0f) {
+            a.ref = make_ref_step(w, sc, stored_mean(w));
+            a.vcs = w.v1;
+        }
+    }
     return a;
 }
 
@@ -2094,6 +2185,7 @@ struct WorkInput {
     float* v1;
     const void* qt;
     float lerp_w, beta2, alpha2, eps;
+    float bc2_div;  // reference-order divisor or 0 (gefenx_tensor_desc.bc2_div)
     StepScalars sc;
     int sr;
     uint64_t seed;
@@ -2102,6 +2194,16 @@ struct WorkInput {
     void* workspace;
     size_t ws_bytes;
 };
+
+// The divisor of the reference's decomposed step (bc2, or sqrt(bc2) on the
+// block path) from the reciprocal the C ABI passes, in double then rounded
+// once: (float)(1/(1/x)) equals (float)x unless x lies within ~2^-52 of an
+// fp32 rounding midpoint (none for beta2 in {0.5, 0.9, 0.95, ..., 0.9999}
+// over 200,000 steps).  Python descriptors carry the same value.
+static float reference_divisor(double inv) {
+    if (!(inv > 0.0) || !std::isfinite(inv)) return 0.0f;
+    return (float)(1.0 / inv);
+}
 
 static int build_work(const WorkInput& in, TensorWork& w) {
     std::memset(&w, 0, sizeof(w));
@@ -2118,6 +2220,8 @@ static int build_work(const WorkInput& in, TensorWork& w) {
     w.dtype = in.dtype; w.mode = in.mode; w.sr = in.sr;
     w.bf16_mean = in.dtype == BF16 ? 1 : 0;
     w.eps = in.eps; w.beta2 = in.beta2; w.alpha2 = in.alpha2;
+    // the divisor describes the host scalars; a device scalar row carries 1/bc2 only
+    w.bc2_div = in.step_scalars == nullptr && in.bc2_div > 0.0f ? in.bc2_div : 0.0f;
     w.sc = in.sc;
     w.mc = make_coef_w(in.lerp_w);
     w.write_p = (in.step_scalars != nullptr) || !(in.sc.lr == 0.0f && in.sc.wdf == 1.0f);
@@ -2171,9 +2275,12 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         w.minv = reinterpret_cast<float*>(ws + L.off_minv);
         w.det_rec = reinterpret_cast<DetRec*>(ws + L.off_rec);
         // fixed-order stats: 8 elements per item when chunks never cross a
-        // block (contiguous, aligned, P and N multiples of 8), else 1
-        w.det_epl = (aligned(in.grad, 16) && aligned(in.idx, 8) && in.period % kChunk == 0 && N % kChunk == 0)
-                        ? (int32_t)kChunk : 1;
+        // block (P and N multiples of 8), else 1.  The summation order then
+        // depends on the shape alone, not on where the grad starts in memory
+        // (a view into a flat bucket sums like a fresh tensor); a misaligned
+        // grad or index array loads its items element by element.
+        w.det_epl = (in.period % kChunk == 0 && N % kChunk == 0) ? (int32_t)kChunk : 1;
+        w.det_vec = aligned(in.grad, 16) && aligned(in.idx, 8) ? 1 : 0;
         w.det_elems = (int64_t)kDetIters * kThreads * w.det_epl;
         w.stats_wgs = std::max<int64_t>(1, ceil_div(N, w.det_elems));
         w.nbw = std::max<int64_t>(1, std::min<int64_t>(4096, ceil_div(nb, kThreads)));
@@ -2805,6 +2912,7 @@ static int factored_input(const char* fn, void* p, const void* grad, int dtype, 
     in.eps = (float)eps;
     in.sc = StepScalars{(float)lr, (float)inv_bias_correction_2, (float)inv_bias_correction_1,
                         (float)weight_decay_factor};
+    in.bc2_div = reference_divisor(inv_bias_correction_2);
     in.sr = stochastic_round ? 1 : 0; in.seed = (uint64_t)rng_seed;
     in.step_scalars = step_scalars; in.seed_dev = seed_dev;
     return GEFENX_OK;
@@ -2906,6 +3014,7 @@ int gefenx_block_update(
     in.eps = (float)eps;
     in.sc = StepScalars{(float)lr, (float)inv_sqrt_bias_correction_2, (float)inv_bias_correction_1,
                         (float)weight_decay_factor};
+    in.bc2_div = reference_divisor(inv_sqrt_bias_correction_2);
     in.sr = stochastic_round ? 1 : 0; in.seed = (uint64_t)rng_seed;
     in.step_scalars = step_scalars; in.seed_dev = seed_dev;
     in.workspace = workspace; in.ws_bytes = workspace_bytes;
@@ -2967,6 +3076,7 @@ static int desc_to_work(const gefenx_tensor_desc& d, int i, const void* const* q
     in.period = d.period;
     in.idx = d.m_codebook; in.mag = d.m_magnitude; in.v0 = d.v0; in.v1 = d.v1; in.qt = qt;
     in.lerp_w = d.lerp_w; in.beta2 = d.beta2; in.alpha2 = d.alpha2; in.eps = d.eps;
+    in.bc2_div = d.bc2_div;
     in.sc = StepScalars{d.lr, d.inv_bc2, d.inv_bc1, d.wd_factor};
     in.sr = sr ? 1 : 0; in.seed = (uint64_t)seed;
     in.step_scalars = step_scalars; in.seed_dev = seed_dev;

@@ -789,13 +789,16 @@ class Gefen(torch.optim.Optimizer):
             state["v_col"] = torch.zeros(p.shape[1], dtype=torch.float32, device=p.device)
             state["factored_step"] = self._new_step_counter(p.device)
         if self._capt_on:  # counters and scalars advance on the device
-            return state, None, None, None, None
+            return state, None, None, None, None, 0.0
         state["step"] += 1
         state["factored_step"] += 1
         lr = self._lr_scalar(group)
         bc1 = 1 - group["beta1"] ** state["step"]
         bc2 = 1 - group["beta2"] ** state["factored_step"]
-        return state, lr, 1.0 / bc2, 1.0 / bc1, 1.0 - lr * group["weight_decay"]
+        # and the divisor bc2, as the kernels' C entry points derive it from
+        # 1/bc2 (the kernels divide by it, as the reference's step does)
+        inv_bc2 = 1.0 / bc2
+        return state, lr, inv_bc2, 1.0 / bc1, 1.0 - lr * group["weight_decay"], 1.0 / inv_bc2
 
     def _prepare_block(self, group, name, p, grad):
         """State bookkeeping of gefen.py:3488-3586; returns the kernel scalars
@@ -811,19 +814,20 @@ class Gefen(torch.optim.Optimizer):
             step = state["step"]
             state["vmean_step"] = step.clone() if torch.is_tensor(step) else step
         if self._capt_on:
-            return state, None, None, None, None
+            return state, None, None, None, None, 0.0
         state["step"] += 1
         state["vmean_step"] += 1
         lr = self._lr_scalar(group)
         bc1 = 1 - group["beta1"] ** state["step"]
         bc2 = 1 - group["beta2"] ** state["vmean_step"]
-        return state, lr, 1.0 / math.sqrt(bc2), 1.0 / bc1, 1.0 - lr * group["weight_decay"]
+        inv_sqrt_bc2 = 1.0 / math.sqrt(bc2)
+        return state, lr, inv_sqrt_bc2, 1.0 / bc1, 1.0 - lr * group["weight_decay"], 1.0 / inv_sqrt_bc2
 
     def _step_automatic_factored(self, group, name, p, grad, prepared=None):
         """gefen.py:2784-3018 on the MI355X factored kernels (one parameter)."""
         if grad.numel() == 0:
             return
-        state, lr, inv_bc2, inv_bc1, wdf = prepared or self._prepare_factored(group, name, p, grad)
+        state, lr, inv_bc2, inv_bc1, wdf, _ = prepared or self._prepare_factored(group, name, p, grad)
         scalars_ptr, seed_ptr = self._capt_pointers(state, p.device)
         if scalars_ptr is not None:
             lr, inv_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
@@ -845,7 +849,7 @@ class Gefen(torch.optim.Optimizer):
         """gefen.py:3488-3818 on the MI355X block kernels (one parameter)."""
         if grad.numel() == 0:
             return
-        state, lr, inv_sqrt_bc2, inv_bc1, wdf = prepared or self._prepare_block(group, name, p, grad)
+        state, lr, inv_sqrt_bc2, inv_bc1, wdf, _ = prepared or self._prepare_block(group, name, p, grad)
         scalars_ptr, seed_ptr = self._capt_pointers(state, p.device)
         if scalars_ptr is not None:
             lr, inv_sqrt_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
@@ -889,13 +893,13 @@ class Gefen(torch.optim.Optimizer):
     @staticmethod
     def _desc_fields(group, prepared, factored, dtype, rows, cols, strides, p_ptr, g_ptr, idx_ptr, mag_ptr,
                      v0, v1, ws_ptr):
-        state, lr, inv_bc2, inv_bc1, wdf = prepared
+        state, lr, inv_bc2, inv_bc1, wdf, bc2_div = prepared
         if lr is None:  # capturable: the tensor reads its scalar row on the device
-            lr, inv_bc2, inv_bc1, wdf = 0.0, 1.0, 1.0, 1.0
+            lr, inv_bc2, inv_bc1, wdf, bc2_div = 0.0, 1.0, 1.0, 1.0, 0.0
         beta1, beta2 = group["beta1"], group["beta2"]
         return (p_ptr, g_ptr, idx_ptr, mag_ptr, v0, v1, ws_ptr, rows, cols) + tuple(strides) + (
             state["automatic_period"], _fused._dtype_code(dtype), 1 if factored else 0,
-            lr, group["eps"], inv_bc2, inv_bc1, wdf, 1.0 - beta1, beta2, 1.0 - beta2)
+            lr, group["eps"], inv_bc2, inv_bc1, wdf, 1.0 - beta1, beta2, 1.0 - beta2, bc2_div)
 
     def _launch_staged(self, device, items, arena):
         """One multi-tensor launch over a chunk of host-resident parameters

@@ -29,7 +29,7 @@ GEFENX_ENOMEM = -4
 
 # GEFENX_ABI_VERSION this binding is written against (include/gefenx.h):
 # the struct layouts and workspace sizes below follow it.
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DT_F32, DT_F16, DT_BF16, DT_F64 = 0, 1, 2, 3
 WS_FACTORED, WS_BLOCK, WS_MOMENTUM = 0, 1, 2
@@ -54,6 +54,7 @@ class TensorDesc(ctypes.Structure):
         ("lr", ctypes.c_float), ("eps", ctypes.c_float), ("inv_bc2", ctypes.c_float),
         ("inv_bc1", ctypes.c_float), ("wd_factor", ctypes.c_float),
         ("lerp_w", ctypes.c_float), ("beta2", ctypes.c_float), ("alpha2", ctypes.c_float),
+        ("bc2_div", ctypes.c_float),
     ]
 
 

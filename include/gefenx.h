@@ -29,9 +29,10 @@ extern "C" {
 /* 2: the block-path workspace (GEFENX_WS_BLOCK) grew by one fixed-order
  * partial record per stats workgroup, sized from numel, so a block workspace
  * sized by a version-1 header is too small for the multi-tensor launcher.
+ * 3: gefenx_tensor_desc gained the trailing field bc2_div.
  * Bindings compare gefenx_abi_version() with the version they were written
  * against and refuse a mismatch. */
-#define GEFENX_ABI_VERSION 2
+#define GEFENX_ABI_VERSION 3
 
 enum gefenx_status {
     GEFENX_OK = 0,
@@ -282,6 +283,16 @@ typedef struct gefenx_tensor_desc {
     float lerp_w;           /* (float)(1 - beta1): momentum lerp weight */
     float beta2;            /* (float)beta2 */
     float alpha2;           /* (float)(1 - beta2), rounded from double */
+    float bc2_div;          /* the divisor of the reference's CPU step, or 0:
+                             * factored (float)bc2, block (float)sqrt(bc2).
+                             * Given (and no step_scalars row), the step size
+                             * rounds as the reference's decomposed step does
+                             * (gefen.py:2996-3006, 3794-3805): the block path
+                             * h = sqrt(vmean) / bc2_div + eps for every dtype,
+                             * the factored path vh = (v_row * v_col) / mean,
+                             * h = sqrt(vh / bc2_div) + eps for fp32
+                             * parameters.  0: the kernels multiply by inv_bc2
+                             * (within 1e-6 of that). */
 } gefenx_tensor_desc;
 
 /* Step every tensor in descs[n] (host array; copied to the device inside the

@@ -23,6 +23,18 @@ static float div_by_block(float u, float b, float y) {
     return u / b;
 }
 
+/* gefenx_device.h div_by_const: the same step for any quotient size, with
+ * the range guards that keep it away from under- and overflow. */
+static float div_by_const(float u, float d, float y) {
+    float q0 = u * y;
+    float aq = fabsf(q0);
+    if (y != 0.0f && fabsf(u) >= 0x1p-100f && fabsf(u) <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f) {
+        float r = fmaf(-q0, d, u);
+        return fmaf(r, y, q0);
+    }
+    return u == 0.0f && y != 0.0f ? q0 : u / d;
+}
+
 static float block_recip(float b) {
     if (!(b >= 0x1p-125f) || !(b <= 0x1p125f)) return 0.0f;
     return 1.0f / b;
@@ -74,6 +86,24 @@ int main(int argc, char** argv) {
                 if (bad < 10) fprintf(stderr, "mismatch u=%a b=%a got=%a want=%a\n", u, b, got, want);
                 ++bad;
             }
+        }
+    }
+    /* div_by_const: random numerators and divisors over wide exponent ranges
+     * (quotients far above and below 1, zeros, the guard edges) */
+    for (long i = 0; i < n; ++i) {
+        uint64_t r = next(), r2 = next();
+        int ed = (int)(r % 241) - 120;
+        float d = ldexpf(1.0f + (float)((r >> 8) & 0x7fffff) / 8388608.0f, ed);
+        int eu = (int)(r2 % 253) - 126;
+        float u = ldexpf(1.0f + (float)((r2 >> 8) & 0x7fffff) / 8388608.0f, eu);
+        if ((r2 >> 40) % 97 == 0) u = 0.0f;
+        if (r2 & (1ULL << 61)) u = -u;
+        float y = block_recip(d);
+        float got = div_by_const(u, d, y), want = u / d;
+        ++checked;
+        if (memcmp(&got, &want, 4) != 0 && !(got != got && want != want)) {
+            if (bad < 10) fprintf(stderr, "div_by_const mismatch u=%a d=%a got=%a want=%a\n", u, d, got, want);
+            ++bad;
         }
     }
     printf("%ld %ld\n", bad, checked);

@@ -29,11 +29,14 @@ def _f(t):
 def assert_within_ulp(got, ref, dtype, msg, atol=0.0):
     """Half types: |got - ref| <= 1 ulp of ref in that dtype (exact spacing
     of the stored value's binade, so 1 ulp means 1 ulp, also at the top of a
-    binade); fp32: 1e-6 relative.  `atol` adds an absolute allowance."""
+    binade), plus `atol`; fp32: 1e-6 relative per element with no absolute
+    allowance (`atol` ignored: the fp32 step rounds in the reference's op
+    order, so even elements that cancel towards zero agree)."""
     got = np.asarray(got, np.float64).reshape(-1)
     ref = np.asarray(ref, np.float64).reshape(-1)
     err = np.abs(got - ref)
     if dtype == orc.F32:
+        atol = 0.0
         lim = 1e-6 * np.abs(ref)
     else:
         mant = 7 if dtype == orc.BF16 else 10
@@ -125,3 +128,66 @@ class FactoredProbe:
             # 1 ulp plus 1e-6 * lr: the stepsize carries the summation-order
             # skew of v (1e-6 relative), visible where p cancels towards zero
             assert_within_ulp(_f(self.p[r]), p_ref, dt, "%s row %d p" % (tag, r), atol=1e-6 * lr)
+
+
+class BlockProbe:
+    """Sampled momentum blocks of one block-vmean (factored_v_2d off or 1D)
+    parameter.  Blocks are independent on this path (gefen.py:3776-3818): a
+    block's new indices, magnitude, vmean and parameters depend only on its
+    own p, grad, indices, magnitude and vmean, so oracle.block_step over the
+    block alone gives its exact step."""
+
+    def __init__(self, name, p, period, blocks):
+        self.name, self.p, self.P = name, p, int(period)
+        nb = p.numel() // self.P
+        self.blocks = sorted({int(b) % nb for b in blocks})
+        self.dtype = TDT_CODE[p.dtype]
+
+    def capture(self, state):
+        P = self.P
+        pf = self.p.detach().reshape(-1)
+        gf = self.p.grad.reshape(-1)
+        idx = state["m_codebook"].reshape(-1)
+        mag = state["m_magnitude"].reshape(-1)
+        vm = state["vmean"].reshape(-1)
+        self.blk_in = [(_f(pf[b * P:(b + 1) * P]), _f(gf[b * P:(b + 1) * P]),
+                        idx[b * P:(b + 1) * P].cpu().numpy(), mag[b:b + 1].cpu().numpy(),
+                        vm[b:b + 1].cpu().numpy()) for b in self.blocks]
+
+    def verify(self, state, codebook, *, step, beta1, beta2, lr, eps, wd, bc2_step=None):
+        P, tag = self.P, "%s step %d" % (self.name, step)
+        bc1 = 1 - beta1 ** step
+        bc2 = 1 - beta2 ** (step if bc2_step is None else bc2_step)
+        pf = self.p.detach().reshape(-1)
+        idx = state["m_codebook"].reshape(-1)
+        mag = state["m_magnitude"].reshape(-1)
+        vm = state["vmean"].reshape(-1)
+        for b, (p0, g0, i0, m0, v0) in zip(self.blocks, self.blk_in):
+            p1, i1, m1, v1 = orc.block_step(p0, g0, i0, m0, v0, P, codebook, self.dtype, beta1=beta1, beta2=beta2,
+                                            lr=lr, eps=eps, bc1=bc1, bc2=bc2, wd=wd)
+            btag = "%s block %d" % (tag, b)
+            np.testing.assert_array_equal(idx[b * P:(b + 1) * P].cpu().numpy(), i1, err_msg=btag + " indices")
+            np.testing.assert_array_equal(mag[b:b + 1].cpu().numpy(), m1, err_msg=btag + " magnitude")
+            np.testing.assert_allclose(vm[b:b + 1].cpu().numpy(), v1, rtol=1e-6, err_msg=btag + " vmean")
+            assert_within_ulp(_f(pf[b * P:(b + 1) * P]), p1, self.dtype, btag + " p", atol=1e-6 * lr)
+
+
+def ns_torch_fp32(m, sched, eps=1e-7):
+    """The oracle's Newton-Schulz statement (oracle.newton_schulz,
+    gefen_muon.py:236-291: every product and elementwise result rounded to
+    bf16) with fp32 GEMMs on the device (torch fp32 matmul on contiguous
+    operands) instead of float64 on the host -- for shapes the host cannot
+    run in seconds."""
+    bf = lambda t: t.to(torch.bfloat16).float()
+    x = bf(m)
+    tall = x.shape[0] > x.shape[1]
+    if tall:
+        x = x.t().contiguous()
+    norm = bf(torch.linalg.vector_norm(x.double()).float().reshape(1))
+    norm = torch.clamp(norm, min=eps)
+    x = bf(x / bf(norm))
+    for a, b, c in sched:
+        gram = bf(x @ x.t().contiguous())
+        upd = bf(b * gram + c * (gram @ gram))
+        x = bf(a * x + upd @ x)
+    return x.t().contiguous() if tall else x

@@ -40,9 +40,9 @@ def test_binding_signatures_cover_header():
 
 def test_abi_version(lib):
     from gefen.kernels import _native
-    assert lib.gefenx_abi_version() == _native.ABI_VERSION == 2
+    assert lib.gefenx_abi_version() == _native.ABI_VERSION == 3
     hdr = open(os.path.join(ROOT, "include", "gefenx.h")).read()
-    assert "#define GEFENX_ABI_VERSION 2" in hdr
+    assert "#define GEFENX_ABI_VERSION 3" in hdr
 
 
 # ----------------------------------------------------------- quant table

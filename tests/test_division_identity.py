@@ -2,7 +2,9 @@
 fma correction (gefenx_device.h div_by_block).  The index bit-exactness depends
 on that being the correctly rounded quotient; this compiles the same sequence
 for the host (gcc, glibc fmaf) and compares it with IEEE division on ~20M
-pairs from the kernel's domain (|u| <= b)."""
+pairs from the kernel's domain (|u| <= b); then div_by_const (the same step
+for the factored stepsize's divisions by mean(v_row) and bc2, with under- and
+overflow guards) on ~20M pairs whose quotients range far above and below 1."""
 import os
 import subprocess
 import tempfile

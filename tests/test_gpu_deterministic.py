@@ -8,19 +8,26 @@ records (no float atomics; block maxima use integer atomic max, exact in any
 order).  With deterministic=True, block-path transposed views take the
 contiguous route (the view kernels accumulate with atomics).  This test runs
 a mixed set twice, in fresh optimizers, and compares every state tensor and
-parameter bit for bit after every step; the block sums cover blocks that span
-many stats workgroups, several blocks per wave, and the one-element-per-item
-kernel (P % 8 != 0).
+parameter bit for bit after every step (tests/det_workload.py); the block
+sums cover blocks that span many stats workgroups, several blocks per wave,
+and the one-element-per-item kernel (P % 8 != 0).  The same workload runs in
+two child processes as well, and a grad view at an element offset (not
+16-byte aligned) must step like an aligned one.
 """
+import os
+import subprocess
+import sys
+import tempfile
+
 import numpy as np
 import pytest
 import torch
 
+import det_workload
+
 pytestmark = pytest.mark.gpu
 
-SPECS = [("w2d", (96, 128)), ("big1d", (1 << 21,)), ("odd1d", (99999,)), ("fine1d", (122880,)),
-         ("wT", (64, 96))]
-PERIODS = {"big1d": 1 << 19, "odd1d": 11111, "fine1d": 40, "w2d": 768, "wT": 768}
+HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 @pytest.fixture(scope="module")
@@ -30,50 +37,76 @@ def dev():
     return torch.device("cuda", 0)
 
 
-def _bits(t):
-    """The tensor's bytes in logical order (a bitwise snapshot)."""
-    return t.detach().contiguous().clone().reshape(-1).view(torch.uint8)
-
-
-def _run(dev, factored):
-    from gefen import Gefen
-    gen = torch.Generator().manual_seed(4)
-    params = []
-    for name, shape in SPECS:
-        data = (torch.randn(*shape, generator=gen) * 0.02).to(torch.bfloat16)
-        if name == "wT":
-            p = torch.nn.Parameter(data.t().contiguous().to(dev).t())
-        else:
-            p = torch.nn.Parameter(data.to(dev))
-        params.append((name, p))
-    opt = Gefen(params, lr=1e-3, betas=(0.9, 0.999), weight_decay=0.01, factored_v_2d=factored,
-                deterministic=True)
-    for name, p in params:
-        opt.state[p]["automatic_period"] = PERIODS[name]
-    cb = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "learn.npz"))["cb"]
-    opt._gefen_codebook = torch.from_numpy(cb).float().to(dev)
-    snaps = []
-    for s in range(4):
-        for name, p in params:
-            g = (torch.randn(*p.shape, generator=gen) * 10 ** (-3 + s % 2)).to(torch.bfloat16)
-            p.grad = g.t().contiguous().to(dev).t() if name == "wT" else g.to(dev)
-        opt.step()
-        torch.cuda.synchronize()
-        snap = {}
-        for name, p in params:
-            st = opt.state[p]
-            snap[name] = {k: _bits(v) for k, v in st.items() if torch.is_tensor(v) and not k.startswith("_")}
-            snap[name]["p"] = _bits(p)
-        snaps.append(snap)
-    return snaps
-
-
 @pytest.mark.parametrize("factored", [True, False])
 def test_deterministic_runs_are_bit_identical(dev, factored):
     print("deterministic repeat factored=%s" % factored, flush=True)
-    a = _run(dev, factored)
-    b = _run(dev, factored)
+    a = det_workload.run(dev, factored)
+    b = det_workload.run(dev, factored)
     for s, (sa, sb) in enumerate(zip(a, b)):
         for name in sa:
             for k in sa[name]:
                 assert torch.equal(sa[name][k], sb[name][k]), (s, name, k)
+
+
+@pytest.mark.parametrize("factored", [True, False])
+def test_two_processes_are_bit_identical(dev, factored):
+    """Reference tests/test_deterministic_mode.py:433-441 (replicas end
+    bit-identical): the same workload in two fresh processes, one after the
+    other on the one GPU (so nothing process-dependent -- plan caches,
+    allocation addresses -- can feed an order), and in this process; every
+    state tensor and parameter after every step compared bit for bit."""
+    mode = "factored" if factored else "block"
+    here = det_workload.run(dev, factored)
+    outs = []
+    with tempfile.TemporaryDirectory() as d:
+        for i in range(2):
+            out = os.path.join(d, "run%d.npz" % i)
+            print("deterministic child %d (%s)" % (i, mode), flush=True)
+            res = subprocess.run([sys.executable, os.path.join(HERE, "det_workload.py"), out, mode],
+                                 capture_output=True, text=True, timeout=240)
+            assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-4000:]
+            with np.load(out) as z:
+                outs.append({k: z[k].copy() for k in z.files})
+    a, b = outs
+    assert set(a) == set(b) and a
+    for k in a:
+        assert np.array_equal(a[k], b[k]), ("child runs differ", k)
+    for s, snap in enumerate(here):
+        for name, kv in snap.items():
+            for k, v in kv.items():
+                assert np.array_equal(a["s%d/%s/%s" % (s, name, k)], v.cpu().numpy()), ("parent differs", s, name, k)
+
+
+@pytest.mark.parametrize("deterministic", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_block_sums_do_not_depend_on_grad_alignment(dev, deterministic, dtype):
+    """The block path's per-block sums run in an order fixed by the shape:
+    a grad that is a view at an element offset into a flat bucket (not
+    16-byte aligned) steps bit-identically to an aligned copy -- vmean,
+    indices, magnitudes and parameters."""
+    from gefen import Gefen
+    gen = torch.Generator().manual_seed(21)
+    n, period = 1 << 20, 1 << 16
+    init = (torch.randn(n, generator=gen) * 0.02).to(dtype)
+    runs = []
+    for offset in (0, 1):
+        p = torch.nn.Parameter(init.clone().to(dev))
+        opt = Gefen([("w", p)], lr=1e-3, weight_decay=0.01, deterministic=deterministic)
+        opt.state[p]["automatic_period"] = period
+        cb = np.load(os.path.join(HERE, "golden", "learn.npz"))["cb"]
+        opt._gefen_codebook = torch.from_numpy(cb).float().to(dev)
+        bucket = torch.empty(n + 8, dtype=dtype, device=dev)
+        ggen = torch.Generator().manual_seed(22)
+        for s in range(3):
+            g = (torch.randn(n, generator=ggen) * 1e-3).to(dtype)
+            view = bucket[offset:offset + n]
+            view.copy_(g.to(dev))
+            assert (view.data_ptr() % 16 == 0) == (offset == 0)
+            p.grad = view
+            opt.step()
+        torch.cuda.synchronize()
+        st = opt.state[p]
+        runs.append({k: det_workload._bits(st[k]) for k in ("m_codebook", "m_magnitude", "vmean")})
+        runs[-1]["p"] = det_workload._bits(p)
+    for k in runs[0]:
+        assert torch.equal(runs[0][k], runs[1][k]), (dtype, deterministic, k)

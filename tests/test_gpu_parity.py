@@ -42,10 +42,11 @@ def _codebook():
 
 
 def _assert_p(got, ref, dtype, msg):
-    """fp32: 1e-6 relative; half types: 1 ulp of the reference value in its
-    dtype (the exact spacing of its binade); plus 1e-6 * lr absolute for
-    every dtype -- the update term is ~lr in size and carries the stepsize's
-    summation-order skew, which is what remains visible where p itself
+    """fp32: 1e-6 relative per element (the fp32 step rounds in the
+    reference's op order); half types: 1 ulp of the reference value in its
+    dtype (the exact spacing of its binade) plus 1e-6 * lr absolute -- the
+    16-bit factored stepsize is sqrt(v_row*s) * sqrt(v_col), ulps off the
+    reference's rounding, which is what remains visible where p itself
     cancels towards zero."""
     assert_within_ulp(got, ref, dtype, msg, atol=1e-6 * LR)
 

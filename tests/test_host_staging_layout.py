@@ -17,7 +17,7 @@ def _item(name, shape, dtype, factored, period):
         state["v_row"], state["v_col"] = torch.zeros(shape[0]), torch.zeros(shape[1])
     else:
         state["vmean"] = torch.zeros(n // period, 1)
-    return hs.StagedItem(None, name, p, torch.zeros_like(p), factored, (state, 0.0, 1.0, 1.0, 1.0))
+    return hs.StagedItem(None, name, p, torch.zeros_like(p), factored, (state, 0.0, 1.0, 1.0, 1.0, 0.0))
 
 
 def test_chunk_layout_written_region_first_and_aligned():
