@@ -83,6 +83,7 @@ struct TensorWork {
     int32_t fast_stats, fast_apply;  // kernel variant: 0 general, 1 contiguous, 2 transposed view
     int32_t write_p, sr, bf16_mean, det_epl;  // det_epl: block stats elements per item (8 or 1)
     int32_t det_vec;     // block stats items: vector loads (grad 16-byte, indices 8-byte aligned)
+    int32_t row_apply;   // factored contiguous apply over row segments (apply_rows)
     int32_t partial;     // block path with the caller's per-block stepsize (no vmean)
     int32_t fin_wide;    // block finalize: one workgroup per block (blocks span many stats records)
     float eps, beta2, alpha2;
@@ -1834,6 +1835,102 @@ __device__ __forceinline__ void apply_fast(const TensorWork& w, int64_t wg, cons
     }
 }
 
+// Factored apply over row segments (contiguous p and grad, C >= 512).  The
+// tasks are 512-column segments of 8 rows, segment-fastest; wave v of
+// workgroup wg takes task 4*wg + v.  A lane keeps its 8 columns' sqrt(v_col)
+// in registers for the task's rows, v_row is a scalar load per row, and when
+// the segment lies inside one block in every row of the task, so are the
+// block's magnitudes and reciprocal: per 8 elements the lane loads only g, p
+// and the indices (the per-chunk v_col and block loads of apply_fast cost
+// ~6% of the apply time).  Two rows are in flight while one is computed.
+constexpr int64_t kRowSegCols = 64 * kChunk;
+constexpr int kRowsPerTask = 8;
+
+template <int DT, int LF>
+__device__ __forceinline__ void apply_rows(const TensorWork& w, int64_t wg, const FastTables& ft, float row_scale) {
+    const FastArgs<DT> a = make_fast_args<DT>(w, row_scale);
+    const int64_t C = w.C, R = w.R, P = w.P;
+    const int64_t nseg = (C + kRowSegCols - 1) / kRowSegCols;
+    const int64_t t = wg * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t rt = t / nseg;
+    const int64_t cs = (t - rt * nseg) * kRowSegCols;
+    const int64_t r0 = rt * kRowsPerTask;
+    if (r0 >= R) return;
+    const int64_t seglen = std::min<int64_t>(kRowSegCols, C - cs);
+    const int64_t c = cs + (int64_t)(threadIdx.x & 63) * kChunk;
+    const bool active = c < C;
+    const int64_t cl = active ? c : cs;  // idle lanes of a short segment re-read its first chunk
+    const int nrows = (int)std::min<int64_t>(kRowsPerTask, R - r0);
+    // block and offset of the segment's first element, row by row
+    // (wave-uniform): one block per row when pin + seglen <= P
+    const int64_t e_first = r0 * C + cs;
+    int64_t bk[kRowsPerTask];
+    bool uniform = true;
+    {
+        int64_t b = div_floor(e_first, P, w.invP);
+        int64_t pin = e_first - b * P;
+        const int64_t dB = div_floor(C, P, w.invP);
+        const int64_t dP = C - dB * P;
+#pragma unroll
+        for (int i = 0; i < kRowsPerTask; ++i) {
+            bk[i] = b;
+            uniform = uniform && (i >= nrows || pin + seglen <= P);
+            pin += dP;
+            b += dB;
+            if (pin >= P) { pin -= P; ++b; }
+        }
+    }
+    if (nrows == kRowsPerTask && seglen == kRowSegCols && uniform) {
+        float vc[kChunk];
+        load_vcol(a.vcs + c, vc);
+        auto load_row = [&](int i, ChunkIn<DT>& in) {
+            const int64_t r = r0 + i;
+            const int64_t e0 = r * C + c;
+            in.m_old = sload(a.mag_old + bk[i]);
+            in.m_new = sload(a.mag + bk[i]);
+            in.y = sload(a.minv + bk[i]);
+            in.rv = sload(a.vrow + r);
+            load_raw8<DT>(a.g + e0, in.g);
+            in.i = load_raw_idx8(a.idx + e0);
+            load_raw8<DT>(a.p + e0, in.p);
+        };
+        ChunkIn<DT> A, B;
+        load_row(0, A);
+        load_row(1, B);
+#pragma unroll
+        for (int i = 0; i < kRowsPerTask; i += 2) {
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) { A.vc[k] = vc[k]; B.vc[k] = vc[k]; }
+            fast_compute<DT, 0, LF>(a, ft, (r0 + i) * C + c, A);
+            if (i + 2 < kRowsPerTask) load_row(i + 2, A);
+            fast_compute<DT, 0, LF>(a, ft, (r0 + i + 1) * C + c, B);
+            if (i + 3 < kRowsPerTask) load_row(i + 3, B);
+        }
+        return;
+    }
+    // a short segment, fewer rows, or a block boundary inside the segment:
+    // one row at a time, per-lane block values
+#pragma unroll 1
+    for (int i = 0; i < nrows; ++i) {
+        const int64_t r = r0 + i;
+        const int64_t e0 = r * C + cl;
+        Pos ps;
+        ps.row = r;
+        ps.col = cl;
+        ps.blk = div_floor(e0, P, w.invP);
+        ps.pin = e0 - ps.blk * P;
+        ChunkIn<DT> in;
+        fast_load<DT, 0>(a, ps, e0, in);
+        uint32_t ix[kChunk];
+        float pv[kChunk];
+        fast_math<DT, 0, LF>(a, ft, in, false, ix, pv);
+        if (active) {
+            store_idx8(a.idx + e0, ix);
+            store8<DT>(a.p + e0, pv);
+        }
+    }
+}
+
 // Apply of a transposed view, MODE 0 factored / 1 block (nearest rounding; a
 // table with several thresholds per bucket takes the exact search for every
 // element).
@@ -2004,6 +2101,13 @@ __device__ __forceinline__ void apply_wg(const TensorWork& w, int64_t wg, int64_
                 row_scale = (1.0f / stored_mean(w)) * sc.inv_bc2;
             }
             __syncthreads();
+            if constexpr (MODE == 0) {
+                if (w.row_apply) {
+                    if (w.mc.small) apply_rows<DT, kLerpSmall>(w, wg, lds.f, row_scale);
+                    else apply_rows<DT, kLerpLarge>(w, wg, lds.f, row_scale);
+                    return;
+                }
+            }
             if (w.mc.small) apply_fast<DT, MODE, kLerpSmall>(w, wg, lds.f, row_scale);
             else apply_fast<DT, MODE, kLerpLarge>(w, wg, lds.f, row_scale);
             return;
@@ -2318,6 +2422,11 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         }
     }
     w.apply_wgs = std::max<int64_t>(1, ceil_div(nchunks, kThreads * kApplyChunksPerThread));
+    // contiguous factored tensors of at least one 512-column segment per row:
+    // row segments (apply_rows); any grid size works for the general apply
+    w.row_apply = (in.mode == 0 && w.fast_apply == 1 && in.R > 1 && in.C >= kRowSegCols) ? 1 : 0;
+    if (w.row_apply)
+        w.apply_wgs = ceil_div(ceil_div(in.C, kRowSegCols) * ceil_div(in.R, (int64_t)kRowsPerTask), (int64_t)kWaves);
     if (w.fast_apply == 2)
         w.apply_wgs = ceil_div(ceil_div(in.R, kTv) * ceil_div(in.C, kTv), kTvTilesPerWg);
     const int64_t S = w.apply_wgs * kThreads * kChunk;

@@ -112,6 +112,13 @@ FACTORED_CASES = [
     (orc.BF16, 7, 4100, 28700, 0.01),  # 2 column tiles, ragged tail
     (orc.F32, 300, 24, 1, 0.0),        # period 1: one block per element
     (orc.BF16, 1024, 2048, 1 << 20, 0.01),
+    # row-segment apply (512-column segments of 8 rows): a short last
+    # segment and a 4-row last tile; block boundaries inside segments (fp32);
+    # whole segments; one segment per row and a 1-row last tile
+    (orc.BF16, 100, 1000, 800, 0.01),
+    (orc.F32, 96, 1024, 768, 0.01),
+    (orc.BF16, 24, 2560, 20480, 0.0),
+    (orc.F16, 17, 512, 4352, 0.01),
 ]
 
 
