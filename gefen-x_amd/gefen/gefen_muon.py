@@ -184,12 +184,17 @@ def _cautious_mask_(update: torch.Tensor, grad: torch.Tensor) -> torch.Tensor:
     update whose product with grad (in torch's promoted dtype) is not > 0 and
     scale the rest by bf16(numel / max(agree, 1)).  The step itself masks
     inside its apply pass; this is the standalone form of the same kernels.
-    (An fp16 grad stages the result through fp16, exact for bf16 values inside
-    fp16's range.)"""
+    An fp16 grad is taken as its exact fp32 copy: torch's promoted dtype for
+    bf16 x fp16 is fp32, so the agreement decisions are the same, and the
+    masked, scaled update (a bf16 x bf16 product, exact in fp32) is staged in
+    fp32 and rounded to bf16 once, so no fp16 range or subnormal limit
+    applies to it."""
     if update.dim() != 2 or update.shape != grad.shape:
         raise ValueError("_cautious_mask_ expects a 2D update and a grad of the same shape")
     if update.dtype != torch.bfloat16 or update.device.type != "cuda" or grad.device != update.device:
         raise ValueError("_cautious_mask_ expects a bf16 update and its grad on one HIP device")
+    if grad.dtype == torch.float16:
+        grad = grad.float()
     lib = _native.load()
     rows, cols = update.shape
     u = update.contiguous()

@@ -191,3 +191,76 @@ def ns_torch_fp32(m, sched, eps=1e-7):
         upd = bf(b * gram + c * (gram @ gram))
         x = bf(a * x + upd @ x)
     return x.t().contiguous() if tall else x
+
+
+class StepTracker:
+    """The reference's decomposed step (oracle.factored_step / block_step)
+    for a set of parameters, started from the GPU optimizer's own step-1
+    periods and codebook (each checked against the oracle's when it is
+    learned), checked after every step: indices and magnitudes bit-exact,
+    v_row / v_col / vmean within 1e-6, parameters within 1 ulp (fp32:
+    1e-6 relative).  Parameters and grads are read in logical order, so
+    transposed views and strided grads need nothing special."""
+
+    def __init__(self, lr, wd, factored_2d, betas=(0.9, 0.999), eps=1e-8):
+        self.lr, self.wd, self.factored_2d = lr, wd, factored_2d
+        self.betas, self.eps = betas, eps
+        self.ref = {}
+        self.cb = None
+
+    def track(self, name, p):
+        self.ref[name] = {"p": _f(p).copy(), "dt": TDT_CODE[p.dtype], "shape": tuple(p.shape), "step": 0}
+
+    def learn(self, opt, named, grads):
+        """Step 1: the GPU's periods and codebook against the oracle's."""
+        for name, p in named:
+            r = self.ref[name]
+            if "per" in r or name not in grads:
+                continue
+            per = int(opt.state[p]["automatic_period"])
+            g = grads[name].reshape(-1)
+            want = 1 if g.size == 1 else orc.find_period(g, r["shape"])
+            assert per == want, "%s: period %d, oracle %d" % (name, per, want)
+            r["per"] = per
+        if self.cb is None:
+            self.cb = orc.learn_codebook([(grads[n].reshape(-1), self.ref[n]["per"]) for n, _ in named
+                                          if n in grads])
+            np.testing.assert_array_equal(opt._gefen_codebook.cpu().numpy(), self.cb, err_msg="codebook")
+
+    def step(self, name, g, lr=None):
+        r = self.ref[name]
+        lr = self.lr if lr is None else lr
+        r["step"] += 1
+        s = r["step"]
+        bc1, bc2 = 1 - self.betas[0] ** s, 1 - self.betas[1] ** s
+        per = r["per"]
+        fact = self.factored_2d and len(r["shape"]) == 2
+        if "idx" not in r:
+            n = int(np.prod(r["shape"]))
+            r["idx"], r["mag"] = np.zeros(n, np.uint8), np.zeros(n // per, np.float32)
+            if fact:
+                r["vr"], r["vc"] = np.zeros(r["shape"][0], np.float32), np.zeros(r["shape"][1], np.float32)
+            else:
+                r["vm"] = np.zeros(n // per, np.float32)
+        kw = dict(beta1=self.betas[0], beta2=self.betas[1], lr=lr, eps=self.eps, bc1=bc1, bc2=bc2, wd=self.wd)
+        if fact:
+            r["p"], r["idx"], r["mag"], r["vr"], r["vc"] = orc.factored_step(
+                r["p"], g, r["idx"], r["mag"], r["vr"], r["vc"], per, self.cb, r["dt"], **kw)
+        else:
+            r["p"], r["idx"], r["mag"], r["vm"] = orc.block_step(
+                r["p"], g, r["idx"], r["mag"], r["vm"], per, self.cb, r["dt"], **kw)
+
+    def check(self, opt, name, p, tag, lr=None):
+        r = self.ref[name]
+        st = opt.state[p]
+        tag = "%s %s step %d" % (tag, name, r["step"])
+        np.testing.assert_array_equal(st["m_codebook"].cpu().numpy().reshape(-1), r["idx"], err_msg=tag)
+        np.testing.assert_array_equal(st["m_magnitude"].cpu().numpy().reshape(-1), r["mag"], err_msg=tag)
+        if "vr" in r:
+            np.testing.assert_allclose(st["v_row"].cpu().numpy(), r["vr"], rtol=1e-6, err_msg=tag)
+            np.testing.assert_allclose(st["v_col"].cpu().numpy(), r["vc"], rtol=1e-6, err_msg=tag)
+        else:
+            np.testing.assert_allclose(st["vmean"].cpu().numpy().reshape(-1), r["vm"], rtol=1e-6, err_msg=tag)
+        got = _f(p).copy()
+        assert_within_ulp(got, r["p"], r["dt"], tag, atol=1e-6 * (self.lr if lr is None else lr))
+        r["p"] = got.reshape(r["shape"])  # continue from the GPU's parameters

@@ -127,3 +127,28 @@ def test_gefen_muon_cautious_follows_the_oracle_trajectory(dev):
             d_ref = ref - orc.muon_apply(before[n], np.zeros_like(ortho), orc.BF16, kw["lr"], kw["weight_decay"], 0.0)
             assert np.linalg.norm(got - ref) <= NS_REL * np.linalg.norm(d_ref) + 1e-6, (s, n)
             assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("dtype", [orc.F16, orc.BF16, orc.F32])
+def test_standalone_cautious_mask_keeps_bf16_range(dev, dtype):
+    """The standalone _cautious_mask_ (gefen_muon.py:396-405) on an update
+    where only a handful of elements agree with the grad, so the kept ones
+    are scaled by ~numel/8 (here 1024 x 4096 / 8 = 524288), and whose values
+    reach 100: u * scale reaches ~5e7, beyond fp16's range but inside bf16's.
+    Bit-exact against oracle.cautious_mask, finite, for every grad dtype."""
+    from gefen.gefen_muon import _cautious_mask_
+    gen = torch.Generator().manual_seed(3)
+    rows, cols = 1024, 4096
+    u = (torch.randn(rows, cols, generator=gen) * 30.0).clamp(-100, 100).to(torch.bfloat16)
+    g = -u.float() * 1e-3  # every product negative ...
+    flat = g.view(-1)
+    agree = torch.randperm(rows * cols, generator=gen)[:8]
+    flat[agree] = -flat[agree]  # ... except 8
+    g = g.to(TORCH_DT[dtype])
+    want = orc.cautious_mask(u.float().numpy(), g.float().numpy(), dtype)
+    got = _cautious_mask_(u.clone().to(dev), g.to(dev))
+    torch.cuda.synchronize()
+    got_np = got.float().cpu().numpy()
+    assert np.isfinite(got_np).all()
+    assert float(np.abs(got_np).max()) > 65504.0  # past fp16's largest finite value
+    np.testing.assert_array_equal(got_np, want)

@@ -22,12 +22,10 @@ import torch
 import torch.nn as nn
 
 from oracle import oracle as orc
-from local_checks import assert_within_ulp
+from local_checks import StepTracker, assert_within_ulp
 
 pytestmark = pytest.mark.gpu
 
-BETAS, EPS = (0.9, 0.999), 1e-8
-TDT = {torch.float32: orc.F32, torch.bfloat16: orc.BF16, torch.float16: orc.F16}
 
 
 @pytest.fixture(scope="module")
@@ -41,79 +39,6 @@ def _state_devices(opt, p):
     """Devices of every tensor-valued state entry of p (all keys, as the
     reference's test checks them)."""
     return {k: v.device for k, v in opt.state[p].items() if torch.is_tensor(v)}
-
-
-def _np(t):
-    # a copy: for an fp32 host tensor .float().cpu().numpy() would alias it
-    return t.detach().float().cpu().numpy().copy()
-
-
-class Oracle:
-    """The reference's decomposed step for a set of parameters, started from
-    the GPU optimizer's own step-1 periods and codebook (each checked
-    against the oracle's when it is learned)."""
-
-    def __init__(self, lr, wd, factored_2d):
-        self.lr, self.wd, self.factored_2d = lr, wd, factored_2d
-        self.ref = {}
-        self.cb = None
-
-    def track(self, name, p):
-        self.ref[name] = {"p": _np(p), "dt": TDT[p.dtype], "shape": tuple(p.shape), "step": 0}
-
-    def learn(self, opt, named, grads):
-        """Step 1: the GPU's periods and codebook against the oracle's."""
-        for name, p in named:
-            r = self.ref[name]
-            if "per" in r or name not in grads:
-                continue
-            per = int(opt.state[p]["automatic_period"])
-            g = grads[name].reshape(-1)
-            want = 1 if g.size == 1 else orc.find_period(g, r["shape"])
-            assert per == want, "%s: period %d, oracle %d" % (name, per, want)
-            r["per"] = per
-        if self.cb is None:
-            self.cb = orc.learn_codebook([(grads[n].reshape(-1), self.ref[n]["per"]) for n, _ in named
-                                          if n in grads])
-            np.testing.assert_array_equal(opt._gefen_codebook.cpu().numpy(), self.cb, err_msg="codebook")
-
-    def step(self, name, g, lr=None):
-        r = self.ref[name]
-        lr = self.lr if lr is None else lr
-        r["step"] += 1
-        s = r["step"]
-        bc1, bc2 = 1 - BETAS[0] ** s, 1 - BETAS[1] ** s
-        per = r["per"]
-        fact = self.factored_2d and len(r["shape"]) == 2
-        if "idx" not in r:
-            n = int(np.prod(r["shape"]))
-            r["idx"], r["mag"] = np.zeros(n, np.uint8), np.zeros(n // per, np.float32)
-            if fact:
-                r["vr"], r["vc"] = np.zeros(r["shape"][0], np.float32), np.zeros(r["shape"][1], np.float32)
-            else:
-                r["vm"] = np.zeros(n // per, np.float32)
-        kw = dict(beta1=BETAS[0], beta2=BETAS[1], lr=lr, eps=EPS, bc1=bc1, bc2=bc2, wd=self.wd)
-        if fact:
-            r["p"], r["idx"], r["mag"], r["vr"], r["vc"] = orc.factored_step(
-                r["p"], g, r["idx"], r["mag"], r["vr"], r["vc"], per, self.cb, r["dt"], **kw)
-        else:
-            r["p"], r["idx"], r["mag"], r["vm"] = orc.block_step(
-                r["p"], g, r["idx"], r["mag"], r["vm"], per, self.cb, r["dt"], **kw)
-
-    def check(self, opt, name, p, tag, lr=None):
-        r = self.ref[name]
-        st = opt.state[p]
-        tag = "%s %s step %d" % (tag, name, r["step"])
-        np.testing.assert_array_equal(st["m_codebook"].cpu().numpy().reshape(-1), r["idx"], err_msg=tag)
-        np.testing.assert_array_equal(st["m_magnitude"].cpu().numpy().reshape(-1), r["mag"], err_msg=tag)
-        if "vr" in r:
-            np.testing.assert_allclose(st["v_row"].cpu().numpy(), r["vr"], rtol=1e-6, err_msg=tag)
-            np.testing.assert_allclose(st["v_col"].cpu().numpy(), r["vc"], rtol=1e-6, err_msg=tag)
-        else:
-            np.testing.assert_allclose(st["vmean"].cpu().numpy().reshape(-1), r["vm"], rtol=1e-6, err_msg=tag)
-        got = _np(p)
-        assert_within_ulp(got, r["p"], r["dt"], tag, atol=1e-6 * (self.lr if lr is None else lr))
-        r["p"] = got.reshape(r["shape"])  # continue from the GPU's parameters
 
 
 def _run_schedule(named, opt, orc_, schedule, gen, scale, tag, lr_of=None):
@@ -150,7 +75,7 @@ def test_param_paged_cpu_gpu_cpu_across_steps(dev, factored, dtype):
     p = nn.Parameter(torch.randn(16, 16).to(dtype))
     named = [("w", p)]
     opt = Gefen(named, lr=1e-2, fused=False, factored_v_2d=factored)
-    track = Oracle(1e-2, 0.0, factored)
+    track = StepTracker(1e-2, 0.0, factored)
     track.track("w", p)
     before = p.detach().cpu().clone()
     cpu = torch.device("cpu")
@@ -167,7 +92,7 @@ def test_batched_group_paged_cpu_gpu_cpu(dev):
     torch.manual_seed(0)
     named = [("w%d" % i, nn.Parameter(torch.randn(8, 12))) for i in range(6)]
     opt = Gefen(named, lr=1e-2, fused=False, factored_v_2d=False)
-    track = Oracle(1e-2, 0.0, False)
+    track = StepTracker(1e-2, 0.0, False)
     for n, p in named:
         track.track(n, p)
     cpu = torch.device("cpu")
@@ -220,7 +145,7 @@ def test_checkpoint_saved_on_gpu_loads_and_steps_on_host(dev, factored):
         assert set(d.type for d in _state_devices(opt_cpu, p).values()) == {"cpu"}
 
     # the oracle continues from the checkpointed state
-    track = Oracle(1e-3, 0.0, factored)
+    track = StepTracker(1e-3, 0.0, factored)
     track.cb = cpu_state["gefen_codebook"].float().numpy()
     np.testing.assert_array_equal(opt_gpu._gefen_codebook.cpu().numpy(), track.cb)
     for name, p in zip(names, model_cpu.parameters()):
@@ -259,7 +184,7 @@ def test_grad_param_mismatch_fails_before_codebook_mutation(dev):
     assert opt._gefen_codebook is None
     assert "automatic_period" not in opt.state.get(p, {})
     # co-located on the host and retried: the codebook comes from this gradient
-    track = Oracle(1e-2, 0.0, True)
+    track = StepTracker(1e-2, 0.0, True)
     track.track("w", p)
     g = torch.randn(16, 16) * 0.1
     p.grad = g
@@ -280,7 +205,7 @@ def test_tensor_lr_survives_host_paging(dev, factored):
     p = nn.Parameter(torch.randn(16, 24).to(dev))
     named = [("w", p)]
     opt = Gefen(named, lr=lr, fused=False, factored_v_2d=factored)
-    track = Oracle(float(lr.item()), 0.0, factored)
+    track = StepTracker(float(lr.item()), 0.0, factored)
     track.track("w", p)
     before = p.detach().cpu().clone()
     cpu = torch.device("cpu")
@@ -321,7 +246,7 @@ def test_resume_after_paging_is_exact(dev, factored):
     reference, opt, p = run(-1)
     resumed, _, _ = run(2)
     assert torch.equal(reference, resumed)
-    track = Oracle(1e-2, 0.0, factored)
+    track = StepTracker(1e-2, 0.0, factored)
     track.track("w", nn.Parameter(init.clone()))
     r = track.ref["w"]
     r["per"] = int(opt.state[p]["automatic_period"])

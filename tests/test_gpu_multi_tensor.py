@@ -1,18 +1,24 @@
-"""gefenx_multi_tensor_step against one call per parameter.
+"""gefenx_multi_tensor_step against one call per parameter, and against
+the oracle.
 
 Both paths run the same phase code on the same per-parameter workgroup
 partition, so the multi-tensor launcher must reproduce the per-parameter
 entry points exactly: indices, magnitudes, second-moment state and params
 bit-identical (the block path's float64 per-block sums are reduced with
 atomics whose order may differ, hence the 1-ulp allowance on vmean and the
-params of block-path tensors).  The per-parameter path itself is pinned to
-the oracle by test_gpu_parity.py.
+params of block-path tensors).  Every tensor of the launcher's run is also
+checked against the oracle's decomposed step after every step
+(tests/local_checks.StepTracker: step-1 periods and codebook equal to the
+oracle's, indices and magnitudes bit-exact, v within 1e-6, params within
+1 ulp / 1e-6 relative).
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 import torch
+
+from local_checks import StepTracker
 
 pytestmark = pytest.mark.gpu
 
@@ -66,12 +72,22 @@ def _run(dev, shapes, dtypes, steps=4, seed=0, **kw):
     ob = Gefen(pb, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, **kw)
     oa._multi_tensor = True
     ob._multi_tensor = False
+    track = StepTracker(1e-3, 0.01, kw.get("factored_v_2d", True))
+    for name, a in pa:
+        if a.numel():
+            track.track(name, a)
     for s in range(steps):
         _grads(pa, s, seed)
         _grads(pb, s, seed)
+        grads = {name: a.grad.float().cpu().numpy().copy() for name, a in pa}
         oa.step()
         ob.step()
         torch.cuda.synchronize()
+        if s == 0:
+            track.learn(oa, pa, grads)
+        for name, a in pa:
+            track.step(name, grads[name])
+            track.check(oa, name, a, "launcher vs oracle")
         for (name, a), (_, b) in zip(pa, pb):
             sa, sb = oa.state[a], ob.state[b]
             tag = "%s %s %s step %d" % (name, tuple(a.shape), a.dtype, s + 1)

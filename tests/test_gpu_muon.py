@@ -518,7 +518,8 @@ def test_momentum_batch_over_several_launches_matches_oracle(dev, lib):
 def test_normuon_and_apply_batch_match_single_matrix_calls(dev, lib):
     """The batched NorMuon scale and apply over 18 matrices (two launch sets;
     one transposed-view parameter) give the single-matrix entry points'
-    results bit for bit, and those are checked against the oracle above."""
+    results bit for bit, and each matrix's normuon_v (1e-6) and parameters
+    (bit for bit) equal oracle.normuon / oracle.muon_apply."""
     from gefen.kernels import _native
     rows, cols, n = 48, 64, 18
     rng = np.random.default_rng(3)
@@ -558,6 +559,12 @@ def test_normuon_and_apply_batch_match_single_matrix_calls(dev, lib):
         assert torch.equal(sc, scale[i]), i
         assert torch.equal(v, vb[i]), i
         assert torch.equal(p, pb[i].contiguous()), i
+        # and the batched result against the oracle directly
+        u_ref, v_ref = orc.normuon(upd[i].float().cpu().numpy(), v0[i], 3, 0.95, 1e-8)
+        p_start = torch.from_numpy(p0[i]).to(torch.bfloat16).float().numpy()
+        p_ref = orc.muon_apply(p_start, u_ref, orc.BF16, 0.02, 0.1, 0.02 * 0.2 * 8.0)
+        np.testing.assert_allclose(vb[i].cpu().numpy(), v_ref, rtol=1e-6, err_msg="matrix %d normuon_v" % i)
+        np.testing.assert_array_equal(pb[i].float().cpu().numpy(), p_ref, err_msg="matrix %d params" % i)
 
 
 @pytest.mark.parametrize("shape", [(96, 256), (256, 96), (64, 200)])
