@@ -510,282 +510,355 @@ __device__ __forceinline__ void stats_factored(const TensorWork& wr, int64_t wg,
 // ====================================================================
 // Transposed views: g (and p) with strides (1, ld), ld >= R -- the layout of
 // x.t() for a contiguous [C, R] tensor x.  Logical row-major order still
-// fixes the blocks, the indices and v_row / v_col, but the data run along
-// logical columns.  Both view kernels move 64 x 64 logical tiles through
-// LDS: g and p travel between HBM and LDS along storage rows (16-byte
-// vectors, 128 B per storage row and tile for 16-bit types), while the math
-// and the index traffic run in logical 8-element chunks as in the contiguous
-// kernels.  Thread t owns the chunks at tile rows t/8 and t/8 + 32, tile
-// columns 8*(t%8) .. +7, so the 8 lanes of a tile row are adjacent.
+// fixes the blocks, the indices and v_row / v_col, but g and p run along
+// logical columns.  The view kernels walk 64 x 64 logical tiles, one per
+// wave at a time; lane l = 8b + a owns the 8 x 8 sub-block at tile rows
+// 8a .. 8a+7 and tile columns 8b .. 8b+7.  It loads g (and p) as 8 vectors
+// along storage rows (tile column 8b+k, rows 8a .. 8a+7: the 8 lanes of one
+// b read one 128-byte run for 16-bit types) and the indices as 8 logical
+// chunks (row 8a+j, columns 8b .. 8b+7: the 8 lanes of one a read one
+// 64-byte run).  Element (j, k) of the sub-block is element j of g vector k
+// and element k of index chunk j, so no data passes through LDS.  Chunk j
+// (8 elements of one logical row) lies in one block since P % 8 == 0.
 // Requires R, C, P multiples of 8 and 16-byte aligned storage rows.
 // ====================================================================
 constexpr int kTv = 64;
-constexpr int kTvTilesPerWg = 4;   // apply: consecutive tiles per workgroup
-constexpr int kTvLdsBlocks = 512;  // stats: LDS block accumulators per workgroup
+constexpr int kTvTilesPerWave = 2;  // apply: consecutive tiles per wave
+constexpr int kTvLdsBlocks = 512;   // stats: LDS block accumulators per workgroup
+constexpr int kTvFew = 4;           // blocks a tile may touch on the scalar-load path
 
-template <int DT>
-struct TvTile {
-    static constexpr int kEs = (int)sizeof(typename Elem<DT>::T);
-    static constexpr int kRowVec = 16 / kEs;                      // tile rows per 16-byte vector
-    static constexpr int kVecPerCol = kTv / kRowVec;              // vectors per storage-row segment
-    static constexpr int kVecPerThread = kTv * kVecPerCol / kThreads;
-    static constexpr int kPitch = kTv * kEs / 4 + 1;              // dwords per storage row (+1 skews banks)
-    uint32_t d[kTv * kPitch];
-};
-
-// Storage-row vector V of a tile: tile column j = V / kVecPerCol, first tile
-// row (V % kVecPerCol) * kRowVec.
-template <int DT>
-__device__ __forceinline__ void tv_put_vec(TvTile<DT>& t, int V, const u32x4& v) {
-    using TT = TvTile<DT>;
-    uint32_t* d = t.d + (V / TT::kVecPerCol) * TT::kPitch + (V % TT::kVecPerCol) * 4;
-    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint64_t u = (uint64_t)v;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-template <int DT>
-__device__ __forceinline__ u32x4 tv_get_vec(const TvTile<DT>& t, int V) {
-    using TT = TvTile<DT>;
-    const uint32_t* d = t.d + (V / TT::kVecPerCol) * TT::kPitch + (V % TT::kVecPerCol) * 4;
-    return u32x4{d[0], d[1], d[2], d[3]};
-}
-
-// Raw bits of tile element (row i, column j).
-template <int DT>
-__device__ __forceinline__ uint32_t tv_get(const TvTile<DT>& t, int i, int j) {
-    if constexpr (DT == F32) return t.d[j * TvTile<DT>::kPitch + i];
-    else return reinterpret_cast<const uint16_t*>(t.d)[j * 2 * TvTile<DT>::kPitch + i];
-}
-
-template <int DT>
-__device__ __forceinline__ void tv_put(TvTile<DT>& t, int i, int j, float v) {
-    if constexpr (DT == F32) t.d[j * TvTile<DT>::kPitch + i] = __float_as_uint(v);
-    else reinterpret_cast<uint16_t*>(t.d)[j * 2 * TvTile<DT>::kPitch + i] = (uint16_t)from_f32<DT>(v);
-}
-
-// The 8 elements of tile row i, columns j0 .. j0+7, packed as a chunk load.
-template <int DT>
-__device__ __forceinline__ void tv_raw8(const TvTile<DT>& t, int i, int j0, Raw8<DT>& r) {
-    if constexpr (DT == F32) {
+// Blocks of a lane's 8 chunks (rows r .. r+7 at column c) relative to b_lo;
+// (dB, dP) = divmod(C, P) advances one row.
+__device__ __forceinline__ void tv_chunk_blocks(int64_t r, int64_t c, int64_t C, int64_t P, double invP,
+                                                int64_t dB, int64_t dP, int64_t b_lo, int q[kChunk]) {
+    const int64_t e = r * C + c;
+    int64_t b = div_floor(e, P, invP);
+    int64_t pin = e - b * P;
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) r.f[k] = __uint_as_float(tv_get<DT>(t, i, j0 + k));
-    } else {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) r.w[m] = tv_get<DT>(t, i, j0 + 2 * m) | (tv_get<DT>(t, i, j0 + 2 * m + 1) << 16);
+    for (int j = 0; j < kChunk; ++j) {
+        q[j] = (int)(b - b_lo);
+        pin += dP;
+        b += dB;
+        if (pin >= P) { pin -= P; ++b; }
     }
 }
 
-// Logical element (r, c) of a view with strides (1, ld) lives at base[c*ld + r].
-template <int DT>
-__device__ __forceinline__ u32x4 tv_load(const typename Elem<DT>::T* base, int64_t ld, int64_t r, int64_t c,
-                                         bool ok) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (ok) v = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(base + c * ld + r)));
-    return v;
+__device__ __forceinline__ float tv_pick(int q, const float v[kTvFew]) {
+    return q == 0 ? v[0] : (q == 1 ? v[1] : (q == 2 ? v[2] : v[3]));
 }
+
+// The first kTvFew values of a per-block array from block b_lo on (indices
+// clamped to the array), as scalar loads.
+__device__ __forceinline__ void tv_sload_few(const float* arr, int64_t b_lo, int64_t nb, float v[kTvFew]) {
+#pragma unroll
+    for (int i = 0; i < kTvFew; ++i) v[i] = sload(arr + (b_lo + i < nb ? b_lo + i : nb - 1));
+}
+
+// Reduce-scatter of 8 float64 values over the 8 lanes of a group (lane bits
+// 0-2): lane i ends with the group's sum of v[i].  Partners at the three
+// steps: i ^ 7 (row_half_mirror), i ^ 2, i ^ 1 (quad_perm); a fixed order of
+// float64 adds.
+__device__ __forceinline__ double tv_scatter_lo(const double v[kChunk], int i) {
+    const bool hi = (i & 4) != 0, mid = (i & 2) != 0, lo = (i & 1) != 0;
+    double w[4], x[2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const double send = hi ? v[t] : v[t + 4];
+        w[t] = (hi ? v[t + 4] : v[t]) + dpp64<0x141, 0xf>(send);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const double send = mid ? w[t] : w[t + 2];
+        x[t] = (mid ? w[t + 2] : w[t]) + dpp64<0x4E, 0xf>(send);
+    }
+    const double send = lo ? x[0] : x[1];
+    return (lo ? x[1] : x[0]) + dpp64<0xB1, 0xf>(send);
+}
+
+// The same over lane bits 3-5 (partners lane ^ 32, lane ^ 16, lane ^ 8):
+// lane 8i + a ends with the sum of v[i] over its 8 lanes a + 8i'.
+__device__ __forceinline__ double tv_scatter_hi(const double v[kChunk], int i) {
+    const bool hi = (i & 4) != 0, mid = (i & 2) != 0, lo = (i & 1) != 0;
+    double w[4], x[2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const double send = hi ? v[t] : v[t + 4];
+        w[t] = (hi ? v[t + 4] : v[t]) + __shfl_xor(send, 32, 64);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const double send = mid ? w[t] : w[t + 2];
+        x[t] = (mid ? w[t + 2] : w[t]) + __shfl_xor(send, 16, 64);
+    }
+    const double send = lo ? x[0] : x[1];
+    return (lo ? x[1] : x[0]) + dpp64<0x128, 0xf>(send);  // row_ror:8 = lane ^ 8 within 16
+}
+
+template <int MODE>
+struct TvStatsLds {
+    float cbr[kCodebookMax];
+    double row[MODE == 0 ? kWaves : 1][MODE == 0 ? kTvStatsMaxRows : 1];
+    uint32_t bmax[kTvLdsBlocks];
+    double bsum[MODE == 1 ? kTvLdsBlocks : 1];
+};
 
 // Stats of a transposed view.  Workgroup (ctile, rtile) covers the same
 // kFactTileCols columns as the contiguous factored kernel (so row_part keeps
-// its layout) and tile_rows (<= 256) rows, as 64 x 64 sub-tiles with the row
-// bands innermost.  MODE 0 (factored): column sums stay in registers across
-// a column's bands (fp32 per sub-tile, then float64), row sums collect in
-// LDS (float64, one owner thread per row).  Block max |u| (and, MODE 1, the
-// block's sum of squares, each square rounded to bf16 for bf16 grads, fp32
-// per chunk, float64 across chunks): a segmented reduction over the 8 lanes
-// of a tile row (blocks are contiguous runs of chunks) and one atomic per
-// run.  Sub-tiles are double-buffered in LDS and the next one's loads are
-// issued before the current one's math.
-template <int DT, int MODE>
-__device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg) {
+// its layout) and tile_rows (<= 256) rows; wave w takes columns
+// [256w, 256w + 256) of them as 64 x 64 tiles, column steps innermost (the
+// two halves of each 128-byte index line in consecutive tiles of one wave).
+// MODE 0 (factored): squares in fp32 over a chunk's 8 columns and over a
+// vector's 8 rows (float64 for fp32 grads), then float64: a row's sum over the wave's
+// columns collects in its lanes across the column steps, a column's over the
+// tile rows in one lane (reduce-scatter over the 8 row groups of each tile),
+// and the 4 waves' row sums meet in LDS in wave order.  Block max |u| (and,
+// MODE 1, the block's sum of squares, each square rounded to bf16 for bf16
+// grads, in float64): when a tile touches at most kTvFew blocks (the common
+// case) its old magnitudes are scalar loads, the lanes keep one value per
+// block and the wave reduces each; otherwise per chunk.  Either way the
+// values go to the workgroup's LDS accumulators (<= 512 blocks) or the
+// shards.
+template <int DT, int MODE, int LF>
+__device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvStatsLds<MODE>& lds) {
     using T = typename Elem<DT>::T;
-    using TT = TvTile<DT>;
-    __shared__ float s_cbr[kCodebookMax];
-    __shared__ TT s_t[2];
-    __shared__ double s_row[kTvStatsMaxRows];
-    __shared__ double s_col[kWaves][kTv];
-    __shared__ uint32_t s_bmax[kTvLdsBlocks];
-    __shared__ double s_bsum[MODE == 1 ? kTvLdsBlocks : 1];
+    using Acc = std::conditional_t<DT == F32, double, float>;
+    constexpr int kSteps = (int)(kFactTileCols / kWaves / kTv);  // column steps per wave
     const QTable* qt = wr.qt;
-    if (threadIdx.x < kCodebookMax) s_cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
-    for (int k = threadIdx.x; k < kTvStatsMaxRows; k += kThreads) s_row[k] = 0.0;
+    if (threadIdx.x < kCodebookMax) lds.cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
+    if constexpr (MODE == 0) {
+        for (int k = threadIdx.x; k < kWaves * kTvStatsMaxRows; k += kThreads) (&lds.row[0][0])[k] = 0.0;
+    }
+    const float* s_cbr = lds.cbr;
 
     const T* g = static_cast<const T*>(wr.grad);
     const uint8_t* idxp = wr.idx;
     const float* mag_old = wr.mag;
     double* row_part = wr.row_part;
     double* col_part = wr.col_part;
-    const int64_t R = wr.R, C = wr.C, P = wr.P, ld = wr.gs1;
+    const int64_t R = wr.R, C = wr.C, P = wr.P, ld = wr.gs1, nb = wr.nb;
     const double invP = wr.invP;
     const MomentumCoef mc = wr.mc;
-    uint32_t* mb = wr.magbits + (wg % wr.shards) * wr.nb;
-    double* bsq = MODE == 1 ? wr.blk_sq + (wg % wr.shards) * wr.nb : nullptr;
+    uint32_t* mb = wr.magbits + (wg % wr.shards) * nb;
+    double* bsq = MODE == 1 ? wr.blk_sq + (wg % wr.shards) * nb : nullptr;
     const int64_t ctile = wg % wr.ct, rtile = wg / wr.ct;
     const int64_t c_begin = ctile * kFactTileCols;
     const int64_t c_end = std::min<int64_t>(c_begin + kFactTileCols, C);
     const int64_t r_begin = rtile * wr.tile_rows;
     const int64_t r_end = std::min<int64_t>(r_begin + wr.tile_rows, R);
-    // blocks of the region: few of them (large periods) reduce in LDS and
-    // leave with one atomic per block and workgroup
-    const int64_t b_lo = div_floor(r_begin * C + c_begin, P, invP);
-    const int64_t b_span = div_floor((r_end - 1) * C + (c_end - 1), P, invP) - b_lo + 1;
+    // blocks of the workgroup's region: few of them (large periods) reduce
+    // in LDS and leave with one atomic per block and workgroup
+    const int64_t b_wlo = div_floor(r_begin * C + c_begin, P, invP);
+    const int64_t b_span = div_floor((r_end - 1) * C + (c_end - 1), P, invP) - b_wlo + 1;
     const bool lds_blk = b_span <= kTvLdsBlocks;
     if (lds_blk) {
         for (int k = threadIdx.x; k < b_span; k += kThreads) {
-            s_bmax[k] = 0u;
-            if constexpr (MODE == 1) s_bsum[k] = 0.0;
+            lds.bmax[k] = 0u;
+            if constexpr (MODE == 1) lds.bsum[k] = 0.0;
         }
     }
-    const int n_rb = (int)((r_end - r_begin + kTv - 1) / kTv);
-    const int n_sub = (int)((c_end - c_begin + kTv - 1) / kTv) * n_rb;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int jc = tid & 7, ib = tid >> 3;
+    const int lane = threadIdx.x & 63, la = lane & 7, lb = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t cw0 = c_begin + (int64_t)wave * (kSteps * kTv);
+    const int64_t cw1 = std::min<int64_t>(cw0 + kSteps * kTv, c_end);
+    const int ncs = cw0 < c_end ? (int)((cw1 - cw0 + kTv - 1) / kTv) : 0;
+    const int nrb = (int)((r_end - r_begin + kTv - 1) / kTv);
+    const int ntile = ncs * nrb;
+    const int64_t dB = div_floor(C, P, invP);
+    const int64_t dP = C - dB * P;
+    __syncthreads();
 
-    struct Pre {
-        u32x4 v[TT::kVecPerThread];
-        RawIdx8 ix[2];
-        float mo[2];
-        int64_t blk[2];  // -1: chunk outside the tensor
+    auto put_max = [&](int64_t b, uint32_t m) {
+        if (m == 0u) return;
+        if (lds_blk) atomicMax(&lds.bmax[b - b_wlo], m);
+        else gatomic_max(mb + b, m);
     };
-    auto fetch = [&](int s, Pre& f) {
-        const int cs = s / n_rb, rb = s - cs * n_rb;
-        const int64_t r0 = r_begin + (int64_t)rb * kTv, c0 = c_begin + (int64_t)cs * kTv;
-#pragma unroll
-        for (int q = 0; q < TT::kVecPerThread; ++q) {
-            const int V = tid + q * kThreads;
-            const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
-            f.v[q] = tv_load<DT>(g, ld, r, c, r < r_end && c < c_end);
-        }
-        const int64_t c = c0 + kChunk * jc;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int64_t r = r0 + ib + 32 * h;
-            f.blk[h] = -1;
-            f.mo[h] = 0.0f;
-            f.ix[h] = RawIdx8{0u, 0u};
-            if (r < r_end && c < c_end) {
-                const int64_t e = r * C + c;
-                const int64_t b = div_floor(e, P, invP);
-                f.blk[h] = b;
-                f.mo[h] = *gbl(mag_old + b);
-                f.ix[h] = load_raw_idx8(idxp + e);
-            }
-        }
+    auto put_sum = [&](int64_t b, double v) {
+        if (v == 0.0) return;
+        if (lds_blk) atomicAdd(&lds.bsum[b - b_wlo], v);
+        else gatomic_add(bsq + b, v);
     };
 
-    Pre cur, nxt;
-    fetch(0, cur);
-    double colacc[kChunk];
+    struct Tile {
+        Raw8<DT> gv[kChunk];  // storage-row vectors: tile column 8b+k, rows 8a .. 8a+7
+        RawIdx8 iv[kChunk];   // index chunks: row 8a+j, columns 8b .. 8b+7
+    };
+    // lanes outside the region read its last sub-block instead (the math
+    // skips them)
+    auto load_tile = [&](int s, Tile& t) {
+        const int rb = s / ncs;
+        const int64_t r = r_begin + (int64_t)rb * kTv + 8 * la;
+        const int64_t c = cw0 + (int64_t)(s - rb * ncs) * kTv + 8 * lb;
+        const int64_t rl = r < r_end ? r : r_end - kChunk, cl = c < cw1 ? c : cw1 - kChunk;
 #pragma unroll
-    for (int k = 0; k < kChunk; ++k) colacc[k] = 0.0;
-    for (int s = 0; s < n_sub; ++s) {
-        TT& t = s_t[s & 1];
+        for (int k = 0; k < kChunk; ++k) load_raw8<DT>(g + (cl + k) * ld + rl, t.gv[k]);
 #pragma unroll
-        for (int q = 0; q < TT::kVecPerThread; ++q) tv_put_vec<DT>(t, tid + q * kThreads, cur.v[q]);
-        lds_barrier();
-        if (s + 1 < n_sub) fetch(s + 1, nxt);
-        const int cs = s / n_rb, rb = s - cs * n_rb;
-        // squares into float64 per term for fp32 grads and on the block path
-        // (the reference's sums), else 8-element fp32 partials
-        using Acc = std::conditional_t<DT == F32 || MODE == 1, double, float>;
+        for (int j = 0; j < kChunk; ++j) t.iv[j] = load_raw_idx8(idxp + (rl + j) * C + cl);
+    };
+
+    double racc[kChunk];  // MODE 0: the band's row sums of the lane's 8 rows over its columns so far
+    double cacc[kSteps];  // MODE 0: column 8b + a of each column step, over the bands so far
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) racc[j] = 0.0;
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) cacc[i] = 0.0;
+
+    auto reduce_tile = [&](int s, const Tile& t) {
+        const int rb = s / ncs, cs = s - rb * ncs;
+        const int64_t r0 = r_begin + (int64_t)rb * kTv, c0 = cw0 + (int64_t)cs * kTv;
+        const int64_t r = r0 + 8 * la, c = c0 + 8 * lb;
+        const bool ok = r < r_end && c < cw1;
+        const int64_t r_last = std::min<int64_t>(r0 + kTv, r_end) - 1;
+        const int64_t c_last = std::min<int64_t>(c0 + kTv, cw1) - 1;
+        const int64_t b_lo = uniform64(div_floor(r0 * C + c0, P, invP));
+        const int64_t b_hi = uniform64(div_floor(r_last * C + c_last, P, invP));
         Acc colf[kChunk];
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) colf[k] = 0;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int i = ib + 32 * h;
-            const int64_t b = cur.blk[h];
-            Acc rs = 0;
-            uint32_t m = 0u;
-            if (b >= 0) {
-                Raw8<DT> gr;
-                tv_raw8<DT>(t, i, kChunk * jc, gr);
-#pragma unroll
-                for (int k = 0; k < kChunk; ++k) {
-                    const float gv = raw_elem<DT>(gr, k);
-                    const float uu = momentum_value(s_cbr[raw_idx(cur.ix[h], k)], cur.mo[h], gv, mc);
-                    const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
-                    m = ub > m ? ub : m;
-                    float sq = gv * gv;
-                    if constexpr (MODE == 1 && DT == BF16) sq = round_dt<BF16>(sq);
-                    rs += (Acc)sq;
-                    if constexpr (MODE == 0) colf[k] += (Acc)sq;
-                }
-            }
-            double rsd = (double)rs;
-            if constexpr (MODE == 0) {
-                // row sum over the 8 lanes of tile row i; its jc == 0 lane owns s_row
-                rsd += __shfl_xor(rsd, 1, 64);
-                rsd += __shfl_xor(rsd, 2, 64);
-                rsd += __shfl_xor(rsd, 4, 64);
-                if (jc == 0 && b >= 0) s_row[rb * kTv + i] += rsd;
-            }
-            // segmented suffix reduction: after the scan, the first lane of
-            // each block run holds the run's max (and sum)
-#pragma unroll
-            for (int d = 1; d < kChunk; d <<= 1) {
-                const int64_t ob = __shfl_down(b, d, kChunk);
-                const uint32_t om = __shfl_down(m, d, kChunk);
-                const bool same = jc + d < kChunk && ob == b;
-                if (same) m = om > m ? om : m;
-                if constexpr (MODE == 1) {
-                    const double os = __shfl_down(rsd, d, kChunk);
-                    if (same) rsd += os;
-                }
-            }
-            const int64_t pb = __shfl_up(b, 1, kChunk);
-            if (b >= 0 && (jc == 0 || pb != b)) {
-                if (lds_blk) {
-                    if (m != 0u) atomicMax(&s_bmax[b - b_lo], m);
-                    if constexpr (MODE == 1) {
-                        if (rsd != 0.0) atomicAdd(&s_bsum[b - b_lo], rsd);
-                    }
-                } else {
-                    if (m != 0u) gatomic_max(mb + b, m);
-                    if constexpr (MODE == 1) {
-                        if (rsd != 0.0) gatomic_add(bsq + b, rsd);
-                    }
-                }
-            }
-        }
-        if constexpr (MODE == 1) {
-            cur = nxt;
-            continue;
-        }
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) colacc[k] += (double)colf[k];
-        if (rb == n_rb - 1) {
-            // column sums of this 64-column band: lanes of equal jc, then the waves
+        // one chunk: max |u| bits, fp32 (MODE 0) or float64 (MODE 1) square sums
+        auto chunk = [&](int j, float mo, uint32_t& m, Acc& rs, double& bs) {
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                double v = colacc[k];
-                v += __shfl_xor(v, 8, 64);
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
-                colacc[k] = 0.0;
-                if (lane < kChunk) s_col[wave][kChunk * lane + k] = v;
+                const float gv = raw_elem<DT>(t.gv[k], j);
+                const float uu = momentum_value<LF>(s_cbr[raw_idx(t.iv[j], k)], mo, gv, mc);
+                const uint32_t ub = __float_as_uint(uu) & 0x7fffffffu;
+                m = ub > m ? ub : m;
+                if constexpr (MODE == 0) {
+                    sq_add(rs, gv);
+                    sq_add(colf[k], gv);
+                } else {
+                    float sq = gv * gv;
+                    if constexpr (DT == BF16) sq = round_dt<BF16>(sq);
+                    bs += (double)sq;
+                }
             }
-            lds_barrier();
-            if (tid < kTv) {
-                const int64_t c = c_begin + (int64_t)cs * kTv + tid;
-                if (c < c_end)
-                    *gbl(col_part + rtile * C + c) = s_col[0][tid] + s_col[1][tid] + s_col[2][tid] + s_col[3][tid];
+        };
+        if (b_hi - b_lo < kTvFew) {
+            float mo[kTvFew];
+            tv_sload_few(mag_old, b_lo, nb, mo);
+            uint32_t mx[kTvFew] = {0u, 0u, 0u, 0u};
+            double bx[kTvFew] = {0.0, 0.0, 0.0, 0.0};
+            if (ok) {
+                int q[kChunk];
+                tv_chunk_blocks(r, c, C, P, invP, dB, dP, b_lo, q);
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) {
+                    uint32_t m = 0u;
+                    Acc rs = 0;
+                    double bs = 0.0;
+                    chunk(j, tv_pick(q[j], mo), m, rs, bs);
+                    if constexpr (MODE == 0) racc[j] += (double)rs;
+#pragma unroll
+                    for (int i = 0; i < kTvFew; ++i) {
+                        if (q[j] == i) {
+                            mx[i] = m > mx[i] ? m : mx[i];
+                            if constexpr (MODE == 1) bx[i] += bs;
+                        }
+                    }
+                }
+            }
+            const int nq = (int)(b_hi - b_lo) + 1;
+#pragma unroll
+            for (int i = 0; i < kTvFew; ++i) {
+                if (i < nq) {
+                    const uint32_t m = wave_max_u63(mx[i]);
+                    double v = 0.0;
+                    if constexpr (MODE == 1) v = wave_sum_d63(bx[i]);
+                    if (lane == 63) {
+                        put_max(b_lo + i, m);
+                        if constexpr (MODE == 1) put_sum(b_lo + i, v);
+                    }
+                }
+            }
+        } else if (ok) {
+            // many blocks in the tile (P small against C): per chunk
+            const int64_t e = r * C + c;
+            int64_t b = div_floor(e, P, invP);
+            int64_t pin = e - b * P;
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) {
+                uint32_t m = 0u;
+                Acc rs = 0;
+                double bs = 0.0;
+                chunk(j, *gbl(mag_old + b), m, rs, bs);
+                if constexpr (MODE == 0) racc[j] += (double)rs;
+                put_max(b, m);
+                if constexpr (MODE == 1) put_sum(b, bs);
+                pin += dP;
+                b += dB;
+                if (pin >= P) { pin -= P; ++b; }
             }
         }
-        cur = nxt;
+        if constexpr (MODE == 0) {
+            // column 8b + a of this tile, over its rows
+            double cv[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) cv[k] = (double)colf[k];
+            const double col = tv_scatter_lo(cv, la);
+#pragma unroll
+            for (int i = 0; i < kSteps; ++i) cacc[i] += (i == cs) ? col : 0.0;
+            if (cs == ncs - 1) {
+                // end of the band: row 8a + b over the wave's columns
+                const double row = tv_scatter_hi(racc, lb);
+                const int64_t rr = r0 + 8 * la + lb;
+                if (rr < r_end) lds.row[wave][rr - r_begin] = row;
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) racc[j] = 0.0;
+            }
+        }
+    };
+
+    if (ntile > 0) {
+        // one tile in flight per wave: a second register set (the next
+        // tile's loads issued before this one's math) measured no faster at
+        // two waves per SIMD than one set at three
+        Tile t;
+        for (int s = 0; s < ntile; ++s) {
+            load_tile(s, t);
+            reduce_tile(s, t);
+        }
+        if constexpr (MODE == 0) {
+            // column partials of the wave's columns over the tile rows
+#pragma unroll
+            for (int i = 0; i < kSteps; ++i) {
+                const int64_t cc = cw0 + (int64_t)i * kTv + 8 * lb + la;
+                if (i < ncs && cc < cw1) *gbl(col_part + rtile * C + cc) = cacc[i];
+            }
+        }
     }
     __syncthreads();
     if constexpr (MODE == 0) {
-        for (int64_t r = r_begin + tid; r < r_end; r += kThreads) *gbl(row_part + ctile * R + r) = s_row[r - r_begin];
+        for (int64_t r = r_begin + threadIdx.x; r < r_end; r += kThreads) {
+            const int64_t i = r - r_begin;
+            double v = lds.row[0][i];
+#pragma unroll
+            for (int ww = 1; ww < kWaves; ++ww) v += lds.row[ww][i];
+            *gbl(row_part + ctile * R + r) = v;
+        }
     }
     if (lds_blk) {
-        for (int k = tid; k < b_span; k += kThreads) {
-            const uint32_t m = s_bmax[k];
-            if (m != 0u) gatomic_max(mb + b_lo + k, m);
+        for (int k = threadIdx.x; k < b_span; k += kThreads) {
+            const uint32_t m = lds.bmax[k];
+            if (m != 0u) gatomic_max(mb + b_wlo + k, m);
             if constexpr (MODE == 1) {
-                const double v = s_bsum[k];
-                if (v != 0.0) gatomic_add(bsq + b_lo + k, v);
+                const double v = lds.bsum[k];
+                if (v != 0.0) gatomic_add(bsq + b_wlo + k, v);
             }
         }
     }
+}
+
+template <int DT, int MODE>
+__device__ __forceinline__ void stats_tv_wg(const TensorWork& w, int64_t wg) {
+    __shared__ TvStatsLds<MODE> lds;
+    if (w.mc.small) stats_tv<DT, MODE, kLerpSmall>(w, wg, lds);
+    else stats_tv<DT, MODE, kLerpLarge>(w, wg, lds);
 }
 
 // ====================================================================
@@ -1666,18 +1739,22 @@ __device__ __forceinline__ void fast_load(const FastArgs<DT>& a, const Pos& ps, 
 }
 
 // Requantise and apply one chunk: new indices in ix, new parameter values
-// in pv.  GENERAL_Q: the table may hold several thresholds per bucket (the
-// fq entries do not describe it), so every element takes the exact search.
+// in pv.  g and p are the chunk's grads and parameters as floats, iv its old
+// indices, vc its columns' sqrt(v_col) (v_col on the fp32 reference path),
+// rv its v_row (factored) or block stepsize (block).  GENERAL_Q: the table
+// may hold several thresholds per bucket (the fq entries do not describe
+// it), so every element takes the exact search.
 template <int DT, int MODE, int LF>
-__device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTables& ft, const ChunkIn<DT>& in,
-                                          bool general_q, uint32_t ix[kChunk], float pv[kChunk]) {
-    const float m_old = in.m_old, m_new = in.m_new, y = in.y;
+__device__ __forceinline__ void chunk_math(const FastArgs<DT>& a, const FastTables& ft, const float g[kChunk],
+                                           const float p[kChunk], const RawIdx8& iv, const float vc[kChunk],
+                                           float m_old, float m_new, float y, float rv, bool general_q,
+                                           uint32_t ix[kChunk], float pv[kChunk]) {
     const float tb = 0x1.00001p-100f * fmaxf(m_new, 1.0f);
     float xs[kChunk];
     bool bad = (y == 0.0f) || general_q;
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        const float u = momentum_value<LF>(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
+        const float u = momentum_value<LF>(ft.cbr[raw_idx(iv, k)], m_old, g[k], a.mc);
         const float q0 = u * y;
         const float r = __builtin_fmaf(-q0, m_new, u);
         xs[k] = __builtin_fmaf(r, y, q0);
@@ -1687,7 +1764,7 @@ __device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTable
         const bool nz = m_new > 0.0f;
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) {
-            const float u = momentum_value<LF>(ft.cbr[raw_idx(in.i, k)], m_old, raw_elem<DT>(in.g, k), a.mc);
+            const float u = momentum_value<LF>(ft.cbr[raw_idx(iv, k)], m_old, g[k], a.mc);
             const float x = nz ? div_by_block(u, m_new, y) : 0.0f;
             ix[k] = quant_global(x, a.qt);
         }
@@ -1701,30 +1778,42 @@ __device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTable
         }
     }
     if constexpr (MODE == 0 && DT == F32) {
-        if (a.ref.on) {  // reference order; in.vc holds v_col
+        if (a.ref.on) {  // reference order; vc holds v_col
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 const float q = ft.cbr[ix[k]] * m_new;
-                float pw = raw_elem<DT>(in.p, k);
+                float pw = p[k];
                 if (a.wd) pw = round_dt<DT>(pw * a.wdf);
-                pv[k] = pw - (q * ref_step(a.ref, in.rv, in.vc[k])) * a.lr;
+                pv[k] = pw - (q * ref_step(a.ref, rv, vc[k])) * a.lr;
             }
             return;
         }
     }
     float sr = 0.0f;
-    if constexpr (MODE == 0) sr = __builtin_amdgcn_sqrtf(in.rv * a.row_scale);
+    if constexpr (MODE == 0) sr = __builtin_amdgcn_sqrtf(rv * a.row_scale);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
         const float q = ft.cbr[ix[k]] * m_new;
-        float pw = raw_elem<DT>(in.p, k);
+        float pw = p[k];
         if (a.wd) pw = round_dt<DT>(pw * a.wdf);
         if constexpr (MODE == 0) {
-            pv[k] = pw - q * (__builtin_amdgcn_rcpf(__builtin_fmaf(sr, in.vc[k], a.eps)) * a.c1);
+            pv[k] = pw - q * (__builtin_amdgcn_rcpf(__builtin_fmaf(sr, vc[k], a.eps)) * a.c1);
         } else {
-            pv[k] = pw - (q * in.rv) * a.lr;  // the reference's order (gefen.py:3806-3818)
+            pv[k] = pw - (q * rv) * a.lr;  // the reference's order (gefen.py:3806-3818)
         }
     }
+}
+
+template <int DT, int MODE, int LF>
+__device__ __forceinline__ void fast_math(const FastArgs<DT>& a, const FastTables& ft, const ChunkIn<DT>& in,
+                                          bool general_q, uint32_t ix[kChunk], float pv[kChunk]) {
+    float g[kChunk], p[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        g[k] = raw_elem<DT>(in.g, k);
+        p[k] = raw_elem<DT>(in.p, k);
+    }
+    chunk_math<DT, MODE, LF>(a, ft, g, p, in.i, in.vc, in.m_old, in.m_new, in.y, in.rv, general_q, ix, pv);
 }
 
 // Requantise and apply one chunk, then store its indices and parameters.
@@ -1933,148 +2022,123 @@ __device__ __forceinline__ void apply_rows(const TensorWork& w, int64_t wg, cons
 
 // Apply of a transposed view, MODE 0 factored / 1 block (nearest rounding; a
 // table with several thresholds per bucket takes the exact search for every
-// element).
-// Workgroup wg owns tiles [wg*4, wg*4 + 4) in tile-row-fastest order, so its
-// storage-row segments of one tile column are consecutive.  Per tile: g and
-// p go to LDS, the chunks requantise and apply (indices straight to HBM, new
-// p back into the LDS tile), then p leaves along storage rows.  The next
-// tile's loads are in flight during the current tile's math.
-// FULL: every tile of the workgroup is interior (R and C multiples of 64,
-// kTvTilesPerWg tiles), so each load and store is unconditional and the
-// tile loop has a fixed trip count: the wait before a tile's LDS writes then
-// covers only its own loads, not the previous tile's stores.
-template <int DT, int MODE, int LF, bool FULL>
-__device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const FastTables& ft,
-                                         TvTile<DT>& tg, TvTile<DT>& tp, float row_scale) {
-    using TT = TvTile<DT>;
+// element).  Wave v of workgroup wg takes kTvTilesPerWave consecutive 64 x 64
+// tiles in tile-row-fastest order, so a wave's storage-row runs of one tile
+// column are consecutive.  Per tile a lane loads its sub-block's g and p
+// vectors and index chunks, sqrt(v_col) of its 8 columns and v_row of its 8
+// rows (factored) and the block values: scalar loads of the tile's first
+// kTvFew blocks when it touches no more, else per chunk.  Then chunk by
+// chunk it requantises and applies (indices stored per chunk) and collects
+// the new parameters into storage-row vectors, stored at the end.
+template <int DT, int MODE, int LF>
+__device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const FastTables& ft, float row_scale) {
     const FastArgs<DT> a = make_fast_args<DT>(w, row_scale);
-    const int64_t R = w.R, C = w.C, P = w.P, ldg = w.gs1, ldp = w.ps1;
+    const int64_t R = w.R, C = w.C, P = w.P, ldg = w.gs1, ldp = w.ps1, nb = w.nb;
     const double invP = w.invP;
     const int64_t nrt = (R + kTv - 1) / kTv;
     const int64_t ntiles = nrt * ((C + kTv - 1) / kTv);
-    const int64_t t0 = wg * kTvTilesPerWg;
-    if (t0 >= ntiles) return;
-    const int64_t t1 = FULL ? t0 + kTvTilesPerWg : std::min<int64_t>(t0 + kTvTilesPerWg, ntiles);
+    const int lane = threadIdx.x & 63, la = lane & 7, lb = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool general_q = w.qt->max_cnt > 1;
-    const int tid = threadIdx.x, jc = tid & 7, ib = tid >> 3;
-
-    struct Pre {
-        u32x4 g[TT::kVecPerThread], p[TT::kVecPerThread];
-        RawIdx8 ix[2];
-        float mo[2], mn[2], y[2], rv[2];
-        float vc[kChunk];
-        bool ok[2];
-    };
-    auto fetch = [&](int64_t T, Pre& f) {
+    const int64_t dB = div_floor(C, P, invP);
+    const int64_t dP = C - dB * P;
+    const int64_t t0 = (wg * kWaves + wave) * (int64_t)kTvTilesPerWave;
+#pragma unroll 1
+    for (int it = 0; it < kTvTilesPerWave; ++it) {
+        const int64_t T = t0 + it;
+        if (T >= ntiles) break;
         const int64_t r0 = (T % nrt) * kTv, c0 = (T / nrt) * kTv;
+        const int64_t r = r0 + 8 * la, c = c0 + 8 * lb;
+        const bool ok = r < R && c < C;
+        // lanes outside the tensor load the last sub-block and store nothing
+        const int64_t rl = r < R ? r : R - kChunk, cl = c < C ? c : C - kChunk;
+        Raw8<DT> gv[kChunk], pv[kChunk];
+        RawIdx8 iv[kChunk];
+        float vc[kChunk], vr[kChunk];
 #pragma unroll
-        for (int q = 0; q < TT::kVecPerThread; ++q) {
-            const int V = tid + q * kThreads;
-            const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
-            const bool ok = FULL || (r < R && c < C);
-            f.g[q] = tv_load<DT>(a.g, ldg, r, c, ok);
-            f.p[q] = tv_load<DT>(a.p, ldp, r, c, ok);
+        for (int k = 0; k < kChunk; ++k) {
+            load_raw8<DT>(a.g + (cl + k) * ldg + rl, gv[k]);
+            load_raw8<DT>(a.p + (cl + k) * ldp + rl, pv[k]);
         }
-        const int64_t c = c0 + kChunk * jc;
-        if (MODE == 0 && (FULL || c < C)) {
-            load_vcol(a.vcs + c, f.vc);
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) iv[j] = load_raw_idx8(a.idx + (rl + j) * C + cl);
+        if constexpr (MODE == 0) {
+            load_vcol(a.vcs + cl, vc);
+            load_vcol(a.vrow + rl, vr);
         } else {
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) f.vc[k] = 0.0f;
+            for (int k = 0; k < kChunk; ++k) vc[k] = vr[k] = 0.0f;
         }
+        // block values of the lane's chunks
+        float mo[kChunk], mn[kChunk], y[kChunk], bs[kChunk];
+        const int64_t r_last = std::min<int64_t>(r0 + kTv, R) - 1, c_last = std::min<int64_t>(c0 + kTv, C) - 1;
+        const int64_t b_lo = uniform64(div_floor(r0 * C + c0, P, invP));
+        const int64_t b_hi = uniform64(div_floor(r_last * C + c_last, P, invP));
+        if (b_hi - b_lo < kTvFew) {
+            float fo[kTvFew], fn[kTvFew], fy[kTvFew], fs[kTvFew];
+            tv_sload_few(a.mag_old, b_lo, nb, fo);
+            tv_sload_few(a.mag, b_lo, nb, fn);
+            tv_sload_few(a.minv, b_lo, nb, fy);
+            if constexpr (MODE == 1) tv_sload_few(a.bstep, b_lo, nb, fs);
+            int q[kChunk];
+            tv_chunk_blocks(rl, cl, C, P, invP, dB, dP, b_lo, q);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int64_t r = r0 + ib + 32 * h;
-            f.ok[h] = FULL || (r < R && c < C);
-            f.ix[h] = RawIdx8{0u, 0u};
-            f.mo[h] = f.mn[h] = f.y[h] = f.rv[h] = 0.0f;
-            if (f.ok[h]) {
-                const int64_t e = r * C + c;
-                const int64_t b = div_floor(e, P, invP);
-                f.mo[h] = *gbl(a.mag_old + b);
-                f.mn[h] = *gbl(a.mag + b);
-                f.y[h] = *gbl(a.minv + b);
-                f.rv[h] = MODE == 0 ? *gbl(a.vrow + r) : *gbl(a.bstep + b);
-                f.ix[h] = load_raw_idx8(a.idx + e);
+            for (int j = 0; j < kChunk; ++j) {
+                mo[j] = tv_pick(q[j], fo);
+                mn[j] = tv_pick(q[j], fn);
+                y[j] = tv_pick(q[j], fy);
+                bs[j] = MODE == 1 ? tv_pick(q[j], fs) : 0.0f;
+            }
+        } else {
+            const int64_t e = rl * C + cl;
+            int64_t b = div_floor(e, P, invP);
+            int64_t pin = e - b * P;
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) {
+                mo[j] = *gbl(a.mag_old + b);
+                mn[j] = *gbl(a.mag + b);
+                y[j] = *gbl(a.minv + b);
+                bs[j] = MODE == 1 ? *gbl(a.bstep + b) : 0.0f;
+                pin += dP;
+                b += dB;
+                if (pin >= P) { pin -= P; ++b; }
             }
         }
-    };
-
-    Pre cur, nxt;
-    fetch(t0, cur);
-    auto tile = [&](int64_t T, bool more) {
+        float po[kChunk][kChunk];  // new parameters: po[k][j] = element (j, k)
 #pragma unroll
-        for (int q = 0; q < TT::kVecPerThread; ++q) {
-            tv_put_vec<DT>(tg, tid + q * kThreads, cur.g[q]);
-            tv_put_vec<DT>(tp, tid + q * kThreads, cur.p[q]);
-        }
-        lds_barrier();
-        if (more) fetch(T + 1, nxt);
-        const int64_t r0 = (T % nrt) * kTv, c0 = (T / nrt) * kTv;
+        for (int j = 0; j < kChunk; ++j) {
+            float gj[kChunk], pj[kChunk];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (!FULL && !cur.ok[h]) continue;
-            const int i = ib + 32 * h;
-            ChunkIn<DT> in;
-            tv_raw8<DT>(tg, i, kChunk * jc, in.g);
-            tv_raw8<DT>(tp, i, kChunk * jc, in.p);
-            in.i = cur.ix[h];
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) in.vc[k] = cur.vc[k];
-            in.m_old = cur.mo[h];
-            in.m_new = cur.mn[h];
-            in.y = cur.y[h];
-            in.rv = cur.rv[h];
+            for (int k = 0; k < kChunk; ++k) {
+                gj[k] = raw_elem<DT>(gv[k], j);
+                pj[k] = raw_elem<DT>(pv[k], j);
+            }
             uint32_t ix[kChunk];
-            float pv[kChunk];
-            fast_math<DT, MODE, LF>(a, ft, in, general_q, ix, pv);
-            store_idx8(a.idx + (r0 + i) * C + c0 + kChunk * jc, ix);
+            float pn[kChunk];
+            chunk_math<DT, MODE, LF>(a, ft, gj, pj, iv[j], vc, mo[j], mn[j], y[j], MODE == 0 ? vr[j] : bs[j],
+                                     general_q, ix, pn);
+            if (ok) store_idx8(a.idx + (r + j) * C + c, ix);
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) tv_put<DT>(tp, i, kChunk * jc + k, pv[k]);
+            for (int k = 0; k < kChunk; ++k) po[k][j] = pn[k];
         }
-        lds_barrier();
+        if (ok) {
 #pragma unroll
-        for (int q = 0; q < TT::kVecPerThread; ++q) {
-            const int V = tid + q * kThreads;
-            const int64_t r = r0 + (V % TT::kVecPerCol) * TT::kRowVec, c = c0 + V / TT::kVecPerCol;
-            if (FULL || (r < R && c < C))
-                __builtin_nontemporal_store(tv_get_vec<DT>(tp, V), gbl(reinterpret_cast<u32x4*>(a.p + c * ldp + r)));
+            for (int k = 0; k < kChunk; ++k) store8<DT>(a.p + (c + k) * ldp + r, po[k]);
         }
-        lds_barrier();
-        cur = nxt;
-    };
-    if constexpr (FULL) {
-#pragma unroll
-        for (int it = 0; it < kTvTilesPerWg; ++it) tile(t0 + it, it + 1 < kTvTilesPerWg);
-    } else {
-        for (int64_t T = t0; T < t1; ++T) tile(T, T + 1 < t1);
     }
 }
 
-template <int DT>
-struct TvApplyLds {
-    FastTables f;
-    TvTile<DT> g, p;
-};
-
 template <int DT, int MODE>
-__device__ __forceinline__ void apply_tv_wg(const TensorWork& w, int64_t wg, TvApplyLds<DT>& lds) {
-    stage_fast(lds.f, w.qt);
+__device__ __forceinline__ void apply_tv_wg(const TensorWork& w, int64_t wg, FastTables& ft) {
+    stage_fast(ft, w.qt);
     float row_scale = 0.0f;
     if constexpr (MODE == 0) {
         const StepScalars sc = read_scalars(w);
         row_scale = (1.0f / stored_mean(w)) * sc.inv_bc2;
     }
     __syncthreads();
-    const int64_t ntiles = ((w.R + kTv - 1) / kTv) * ((w.C + kTv - 1) / kTv);
-    const bool full = w.R % kTv == 0 && w.C % kTv == 0 && (wg + 1) * kTvTilesPerWg <= ntiles;
-    if (full) {
-        if (w.mc.small) apply_tv<DT, MODE, kLerpSmall, true>(w, wg, lds.f, lds.g, lds.p, row_scale);
-        else apply_tv<DT, MODE, kLerpLarge, true>(w, wg, lds.f, lds.g, lds.p, row_scale);
-    } else {
-        if (w.mc.small) apply_tv<DT, MODE, kLerpSmall, false>(w, wg, lds.f, lds.g, lds.p, row_scale);
-        else apply_tv<DT, MODE, kLerpLarge, false>(w, wg, lds.f, lds.g, lds.p, row_scale);
-    }
+    if (w.mc.small) apply_tv<DT, MODE, kLerpSmall>(w, wg, ft, row_scale);
+    else apply_tv<DT, MODE, kLerpLarge>(w, wg, ft, row_scale);
 }
 
 // LDS of the apply kernels: the fast tables or the general ones, never both.
@@ -2172,13 +2236,13 @@ __global__ void __launch_bounds__(kThreads) k_factored_stats(TensorWork w) {
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) k_factored_stats_tv(TensorWork w) {
-    stats_tv<DT, 0>(w, blockIdx.x);
+    stats_tv_wg<DT, 0>(w, blockIdx.x);
 }
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) k_apply_tv(TensorWork w) {
-    __shared__ TvApplyLds<DT> lds;
-    apply_tv_wg<DT, 0>(w, blockIdx.x, lds);
+    __shared__ FastTables ft;
+    apply_tv_wg<DT, 0>(w, blockIdx.x, ft);
 }
 
 template <int DT>
@@ -2209,14 +2273,14 @@ __global__ void __launch_bounds__(kThreads) k_mt_factored_stats(const TensorWork
 template <int DT, int MODE>
 __global__ void __launch_bounds__(kThreads) k_mt_stats_tv(const TensorWork* __restrict__ ws, SegTable tb) {
     const Seg sg = find_seg(tb, blockIdx.x);
-    stats_tv<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
+    stats_tv_wg<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
 }
 
 template <int DT, int MODE>
 __global__ void __launch_bounds__(kThreads) k_mt_apply_tv(const TensorWork* __restrict__ ws, SegTable tb) {
-    __shared__ TvApplyLds<DT> lds;
+    __shared__ FastTables ft;
     const Seg sg = find_seg(tb, blockIdx.x);
-    apply_tv_wg<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin, lds);
+    apply_tv_wg<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin, ft);
 }
 
 template <int DT>
@@ -2367,7 +2431,11 @@ static int build_work(const WorkInput& in, TensorWork& w) {
             w.tile_rows = t.tv_rows;
             w.stats_wgs = t.ct * t.rt_tv;
         }
-        if (!w.fast_apply && tv_shape && tv_g && tv_p && !in.sr && w.write_p) w.fast_apply = 2;
+        // the view apply reads v_row and sqrt(v_col) (v_col on the fp32
+        // reference path) 8 floats at a time
+        if (!w.fast_apply && tv_shape && tv_g && tv_p && !in.sr && w.write_p && aligned(in.v0, 16) &&
+            aligned(in.v1, 16))
+            w.fast_apply = 2;
     } else {
         const BlockWs L = BlockWs::make(nb, N);
         if (in.ws_bytes < L.total)
@@ -2428,7 +2496,7 @@ static int build_work(const WorkInput& in, TensorWork& w) {
     if (w.row_apply)
         w.apply_wgs = ceil_div(ceil_div(in.C, kRowSegCols) * ceil_div(in.R, (int64_t)kRowsPerTask), (int64_t)kWaves);
     if (w.fast_apply == 2)
-        w.apply_wgs = ceil_div(ceil_div(in.R, kTv) * ceil_div(in.C, kTv), kTvTilesPerWg);
+        w.apply_wgs = ceil_div(ceil_div(in.R, kTv) * ceil_div(in.C, kTv), (int64_t)kWaves * kTvTilesPerWave);
     const int64_t S = w.apply_wgs * kThreads * kChunk;
     w.dR = S / w.C;
     w.dC = S - w.dR * w.C;

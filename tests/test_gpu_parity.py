@@ -275,6 +275,11 @@ STRIDED_CASES = [
     (orc.F16, 128, 384, 192, "view_ld", "view"),
     (orc.BF16, 200, 136, 400, "contig", "view"),    # view stats, general apply
     (orc.F32, 200, 136, 400, "view", "contig"),      # contiguous stats, general apply
+    # periods above 21 * (C + 1): every 64 x 64 tile touches at most 4
+    # blocks (scalar block loads), with block edges inside rows
+    (orc.BF16, 512, 320, 8192, "view", "view"),
+    (orc.F32, 256, 384, 12288, "view", "view"),
+    (orc.F16, 448, 200, 5600, "view_ld", "view_ld"),
 ]
 
 
@@ -292,6 +297,8 @@ BLOCK_VIEW_CASES = [
     (orc.BF16, 1096, 2056, 2056, "view"),
     (orc.BF16, 320, 256, 640, "view"),  # full-tile apply workgroups and a partial last one
     (orc.F32, 256, 128, 64, "view_ld"),
+    (orc.BF16, 512, 320, 8192, "view"),  # at most 4 blocks per 64 x 64 tile
+    (orc.F16, 448, 200, 5600, "view_ld"),
 ]
 
 
