@@ -205,6 +205,15 @@ __device__ __forceinline__ RawIdx8 load_raw_idx8(const uint8_t* __restrict__ bas
     return RawIdx8{v.x, v.y};
 }
 
+// The same through an ordinary load, for a wave that reads half of each
+// 128-byte line and the other half later: a non-temporal load does not keep
+// the line in L2, so the second half would be fetched from HBM again
+// (measured: one extra pass over the indices, 1 B per element).
+__device__ __forceinline__ RawIdx8 load_raw_idx8_cached(const uint8_t* __restrict__ base) {
+    const u32x2 v = *gbl(reinterpret_cast<const u32x2*>(base));
+    return RawIdx8{v.x, v.y};
+}
+
 __device__ __forceinline__ RawIdx8 load_raw_idx8_elems(const uint8_t* __restrict__ base) {
     RawIdx8 r{0u, 0u};
 #pragma unroll

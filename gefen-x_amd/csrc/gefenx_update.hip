@@ -699,7 +699,7 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvSta
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) load_raw8<DT>(g + (cl + k) * ld + rl, t.gv[k]);
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) t.iv[j] = load_raw_idx8(idxp + (rl + j) * C + cl);
+        for (int j = 0; j < kChunk; ++j) t.iv[j] = load_raw_idx8_cached(idxp + (rl + j) * C + cl);
     };
 
     double racc[kChunk];  // MODE 0: the band's row sums of the lane's 8 rows over its columns so far
@@ -2061,7 +2061,7 @@ __device__ __forceinline__ void apply_tv(const TensorWork& w, int64_t wg, const 
             load_raw8<DT>(a.p + (cl + k) * ldp + rl, pv[k]);
         }
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) iv[j] = load_raw_idx8(a.idx + (rl + j) * C + cl);
+        for (int j = 0; j < kChunk; ++j) iv[j] = load_raw_idx8_cached(a.idx + (rl + j) * C + cl);
         if constexpr (MODE == 0) {
             load_vcol(a.vcs + cl, vc);
             load_vcol(a.vrow + rl, vr);
