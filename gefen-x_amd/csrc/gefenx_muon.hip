@@ -672,26 +672,37 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16 (&
 // Epilogue of a full (64*WM)^2 tile (every row and column in range, C, D and
 // Dt 16-byte aligned with leading dimensions and batch strides multiples of 8):
 // the same arithmetic as gemm_epilogue, with every global access unconditional
-// and the next slab's C rows loaded before this slab's barrier.
+// and the next slab's C rows loaded before this slab's barrier.  The fp32 slab
+// has rows of 64*WM floats whose 16-byte groups are XOR-swizzled by
+// (row >> 3) & 7: the accumulator writes (32 consecutive columns per half
+// wave), the row pass (a thread takes 16-byte groups q and q + 8*WM of a row,
+// 4 + 4 columns, with 8-byte C loads and D stores) and the transposed copy's
+// column reads (8 rows per thread) each spread over the banks.
+template <int WM>
+__device__ __forceinline__ int epi_at(int row, int col) {
+    return row * (64 * WM) + 4 * ((col >> 2) ^ ((row >> 3) & 7)) + (col & 3);
+}
+
 template <int WM>
 __device__ __forceinline__ void gemm_epilogue_full(const GemmArgs& g, const f32x16 (&acc)[WM][WM], float* sOut,
                                                    int64_t bz, bool diag, int64_t m0, int64_t n0, int wm, int wn,
                                                    int l32, int lhi) {
     constexpr int BN = 64 * WM;
-    constexpr int kOutPitch = BN + 1;
-    constexpr int kVecD = 64 * BN / 8 / kT;
+    constexpr int kHalfG = BN / 8;            // 16-byte groups per half row
+    constexpr int kVecD = 64 * BN / 8 / kT;   // 8-element pieces per thread and slab
     const uint16_t* C = g.C ? g.C + bz * g.sC : nullptr;
     uint16_t* D = g.D ? g.D + bz * g.sD : nullptr;
     uint16_t* Dt = (g.Dt && !(g.tri && diag)) ? g.Dt + bz * g.sDt : nullptr;
     const int tid = threadIdx.x;
-    u32x4 cpf[2][kVecD];
-    auto fetch = [&](int h, u32x4 (&dst)[kVecD]) {
+    u32x2 cpf[2][kVecD][2];
+    auto fetch = [&](int h, u32x2 (&dst)[kVecD][2]) {
 #pragma unroll
         for (int k = 0; k < kVecD; ++k) {
             const int v = tid + k * kT;
-            const int row = v / (BN / 8), c8 = (v % (BN / 8)) * 8;
-            dst[k] = __builtin_nontemporal_load(
-                gbl(reinterpret_cast<const u32x4*>(C + (m0 + h * 64 + row) * g.ldc + n0 + c8)));
+            const int row = v / kHalfG, q = v % kHalfG;
+            const uint16_t* cp = C + (m0 + h * 64 + row) * g.ldc + n0 + 4 * q;
+            dst[k][0] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x2*>(cp)));
+            dst[k][1] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x2*>(cp + BN / 2)));
         }
     };
     if (C != nullptr) fetch(0, cpf[0]);
@@ -707,7 +718,7 @@ __device__ __forceinline__ void gemm_epilogue_full(const GemmArgs& g, const f32x
                     for (int r = 0; r < 16; ++r) {
                         const int row = ii * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
                         const int col = wn * (32 * WM) + j * 32 + l32;
-                        sOut[row * kOutPitch + col] = acc[i][j][r];
+                        sOut[epi_at<WM>(row, col)] = acc[i][j][r];
                     }
             }
         }
@@ -717,27 +728,31 @@ __device__ __forceinline__ void gemm_epilogue_full(const GemmArgs& g, const f32x
 #pragma unroll
         for (int k = 0; k < kVecD; ++k) {
             const int v = tid + k * kT;
-            const int row = v / (BN / 8), c8 = (v % (BN / 8)) * 8;
-            float x[8];
+            const int row = v / kHalfG, q = v % kHalfG;
+            f32x4* s0 = reinterpret_cast<f32x4*>(sOut + epi_at<WM>(row, 4 * q));
+            f32x4* s1 = reinterpret_cast<f32x4*>(sOut + epi_at<WM>(row, 4 * q + BN / 2));
+            const f32x4 a0 = *s0, a1 = *s1;
+            float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = g.alpha * sOut[row * kOutPitch + c8 + e];
+            for (int e = 0; e < 8; ++e) x[e] = g.alpha * x[e];
             if (C != nullptr) {
-                const u32x4 cv = cpf[h & 1][k];
-                const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
+                const uint32_t cw[4] = {cpf[h & 1][k][0].x, cpf[h & 1][k][0].y, cpf[h & 1][k][1].x,
+                                        cpf[h & 1][k][1].y};
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     x[e] = __builtin_fmaf(g.beta, bf16f((uint16_t)(cw[e >> 1] >> (16 * (e & 1)))), x[e]);
             }
             uint16_t hv[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                hv[e] = f2bf(x[e]);
-                sOut[row * kOutPitch + c8 + e] = bf16f(hv[e]);
-            }
+            for (int e = 0; e < 8; ++e) hv[e] = f2bf(x[e]);
+            *s0 = f32x4{bf16f(hv[0]), bf16f(hv[1]), bf16f(hv[2]), bf16f(hv[3])};
+            *s1 = f32x4{bf16f(hv[4]), bf16f(hv[5]), bf16f(hv[6]), bf16f(hv[7])};
             if (D != nullptr) {
-                const u32x4 dv = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16),
-                                  (uint32_t)hv[4] | ((uint32_t)hv[5] << 16), (uint32_t)hv[6] | ((uint32_t)hv[7] << 16)};
-                *gbl(reinterpret_cast<u32x4*>(D + (R0 + row) * g.ldd + n0 + c8)) = dv;
+                uint16_t* dp = D + (R0 + row) * g.ldd + n0 + 4 * q;
+                const u32x2 d0 = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
+                const u32x2 d1 = {(uint32_t)hv[4] | ((uint32_t)hv[5] << 16), (uint32_t)hv[6] | ((uint32_t)hv[7] << 16)};
+                *gbl(reinterpret_cast<u32x2*>(dp)) = d0;
+                *gbl(reinterpret_cast<u32x2*>(dp + BN / 2)) = d1;
             }
         }
         if (Dt != nullptr) {
@@ -748,7 +763,7 @@ __device__ __forceinline__ void gemm_epilogue_full(const GemmArgs& g, const f32x
                 const int cc = v >> 3, r8 = (v & 7) * 8;
                 uint16_t hv[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) hv[e] = f2bf(sOut[(r8 + e) * kOutPitch + cc]);
+                for (int e = 0; e < 8; ++e) hv[e] = f2bf(sOut[epi_at<WM>(r8 + e, cc)]);
                 const u32x4 tv = {(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16),
                                   (uint32_t)hv[4] | ((uint32_t)hv[5] << 16), (uint32_t)hv[6] | ((uint32_t)hv[7] << 16)};
                 *gbl(reinterpret_cast<u32x4*>(Dt + (n0 + cc) * g.lddt + R0 + r8)) = tv;
