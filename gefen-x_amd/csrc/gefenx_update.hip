@@ -2672,7 +2672,16 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
                 if (phase == 3 && w.mode != 0) continue;
                 groups[k].push_back(t);
             }
-            for (auto& kv : groups) {
+            // transposed-view stats before the contiguous ones: their index
+            // loads go through L2, so the contiguous stats' partials, which
+            // the finalize reads next, stay cached (measured on the Qwen3-4B
+            // set: stats 2.04 -> 1.98 ms, finalize 65 -> 58 us)
+            std::vector<std::pair<GroupKey, std::vector<int>>> ordered(groups.begin(), groups.end());
+            if (phase == 0)
+                std::stable_sort(ordered.begin(), ordered.end(), [](const auto& a, const auto& b) {
+                    return (a.first.fast == 2) > (b.first.fast == 2);
+                });
+            for (auto& kv : ordered) {
                 Launch l;
                 l.phase = phase;
                 l.cohort = cohort;
