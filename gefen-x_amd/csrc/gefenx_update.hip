@@ -1188,10 +1188,27 @@ __device__ __forceinline__ void finalize_magnitude(const TensorWork& w, int64_t 
     w.minv[b] = block_recip(m);
 }
 
+// Sum of p[0], p[stride], ..., p[(n-1)*stride] in index order (the sequential
+// sum, bit for bit), the loads issued four at a time.
+__device__ __forceinline__ double ordered_sum(const double* __restrict__ p, int64_t n, int64_t stride) {
+    double s = 0.0;
+    int64_t t = 0;
+    for (; t + 4 <= n; t += 4) {
+        double a[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a[k] = *gbl(p + (t + k) * stride);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s += a[k];
+    }
+    for (; t < n; ++t) s += *gbl(p + t * stride);
+    return s;
+}
+
 // ====================================================================
 // Factored finalize.  Workgroups [0, nr): v_row EMA from the ct row partials
 // plus one float64 partial of sum(v_row); [nr, nr+nc): v_col EMA from the rt
-// column partials (64 columns each); the rest: magnitudes.
+// column partials (one column per thread, partials in row-tile order); the
+// rest: magnitudes.
 // v <- fma(sum/n, 1-beta2, v*beta2)  (gefen.py:2994-2996)
 // ====================================================================
 __device__ __forceinline__ void finalize_factored(const TensorWork& w, int64_t wg) {
@@ -1201,8 +1218,7 @@ __device__ __forceinline__ void finalize_factored(const TensorWork& w, int64_t w
         const int64_t i = wg * kFinRowsPerWg + tid;
         double v64 = 0.0;
         if (i < w.R) {
-            double s = 0.0;
-            for (int64_t t = 0; t < w.ct; ++t) s += w.row_part[t * w.R + i];
+            const double s = ordered_sum(w.row_part + i, w.ct, w.R);
             const float ms = (float)s / (float)w.C;
             const float v = __builtin_fmaf(ms, w.alpha2, w.v0[i] * w.beta2);
             w.v0[i] = v;
@@ -1219,19 +1235,9 @@ __device__ __forceinline__ void finalize_factored(const TensorWork& w, int64_t w
         return;
     }
     if (wg < w.nr + w.nc) {
-        // wave k adds row tiles t = k, k+4, ...
-        __shared__ double s_cp[kWaves][64];
-        const int lane = tid & 63;
-        const int wave = tid >> 6;
-        const int64_t j = (wg - w.nr) * 64 + lane;
-        double s = 0.0;
-        if (j < w.C)
-            for (int64_t t = wave; t < w.rt; t += kWaves) s += w.col_part[t * w.C + j];
-        s_cp[wave][lane] = s;
-        __syncthreads();
-        if (wave == 0 && j < w.C) {
-            double tot = 0.0;
-            for (int ww = 0; ww < kWaves; ++ww) tot += s_cp[ww][lane];
+        const int64_t j = (wg - w.nr) * kThreads + tid;
+        if (j < w.C) {
+            const double tot = ordered_sum(w.col_part + j, w.rt, w.C);
             const float ms = (float)tot / (float)w.R;
             const float v = __builtin_fmaf(ms, w.alpha2, w.v1[j] * w.beta2);
             w.v1[j] = v;
@@ -2417,7 +2423,7 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         w.ct = t.ct; w.rt = t.rt; w.tile_rows = t.tile_rows;
         w.stats_wgs = t.ct * t.rt;
         w.nr = ceil_div(in.R, kFinRowsPerWg);
-        w.nc = ceil_div(in.C, 64);
+        w.nc = ceil_div(in.C, kThreads);
         w.nbw = std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(nb, kFinBlocksPerWg)));
         w.fin_wgs = w.nr + w.nc + w.nbw;
         const bool contig_g = (in.gs1 == 1 && in.gs0 == in.C);
