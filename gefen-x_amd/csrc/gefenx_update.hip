@@ -527,6 +527,7 @@ constexpr int kTvTilesPerWave = 2;  // apply: consecutive tiles per wave
 constexpr int kTvLdsBlocks = 512;   // stats: LDS block accumulators per workgroup
 constexpr int kTvFew = 4;           // blocks a tile may touch on the scalar-load path
 
+// A value every lane of the wave holds, moved to scalar registers.
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
     const uint64_t u = (uint64_t)v;
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
@@ -2029,8 +2030,11 @@ __device__ __forceinline__ void apply_rows(const TensorWork& w, int64_t wg, cons
 // Apply of a transposed view, MODE 0 factored / 1 block (nearest rounding; a
 // table with several thresholds per bucket takes the exact search for every
 // element).  Wave v of workgroup wg takes kTvTilesPerWave consecutive 64 x 64
-// tiles in tile-row-fastest order, so a wave's storage-row runs of one tile
-// column are consecutive.  Per tile a lane loads its sub-block's g and p
+// tiles in tile-row-fastest order, so a workgroup reads 1 KB runs of its 64
+// storage rows.  (The other half of each 128-byte index line belongs to the
+// next tile column and is fetched again; orders that read both halves in
+// the same step shorten those runs and measured ~20% slower.)  Per tile a
+// lane loads its sub-block's g and p
 // vectors and index chunks, sqrt(v_col) of its 8 columns and v_row of its 8
 // rows (factored) and the block values: scalar loads of the tile's first
 // kTvFew blocks when it touches no more, else per chunk.  Then chunk by
