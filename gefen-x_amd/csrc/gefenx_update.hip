@@ -2273,11 +2273,19 @@ __global__ void __launch_bounds__(kThreads) k_apply(TensorWork w) {
     apply_wg<DT, MODE, SR, FAST>(w, blockIdx.x, gridDim.x, lds);
 }
 
+// Factored stats of a launch group; the group's block-path tensors of the
+// same dtype (not transposed views) ride in the same launch.
 template <int DT, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_mt_factored_stats(const TensorWork* __restrict__ ws,
                                                                 SegTable tb) {
     const Seg sg = find_seg(tb, blockIdx.x);
-    stats_factored_wg<DT, FAST>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
+    const TensorWork& w = ws[sg.t];
+    const int64_t local = (int64_t)blockIdx.x - sg.wg_begin;
+    if (w.mode != 0) {
+        stats_block_wg<DT>(w, local);
+        return;
+    }
+    stats_factored_wg<DT, FAST>(w, local);
 }
 
 template <int DT, int MODE>
@@ -2291,13 +2299,6 @@ __global__ void __launch_bounds__(kThreads) k_mt_apply_tv(const TensorWork* __re
     __shared__ FastTables ft;
     const Seg sg = find_seg(tb, blockIdx.x);
     apply_tv_wg<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin, ft);
-}
-
-template <int DT>
-__global__ void __launch_bounds__(kThreads) k_mt_block_stats(const TensorWork* __restrict__ ws,
-                                                             SegTable tb) {
-    const Seg sg = find_seg(tb, blockIdx.x);
-    stats_block_wg<DT>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin);
 }
 
 __global__ void __launch_bounds__(kThreads) k_mt_finalize(const TensorWork* __restrict__ ws,
@@ -2314,13 +2315,20 @@ __global__ void __launch_bounds__(kThreads) k_mt_mean(const TensorWork* __restri
     mean_phase(ws[sg.t]);
 }
 
+// Apply of a launch group; with MODE 0 the group's block-path tensors of the
+// same dtype and variant (not transposed views) ride in the same launch.
 template <int DT, int MODE, bool SR, bool FAST>
 __global__ void __launch_bounds__(kThreads) k_mt_apply(const TensorWork* __restrict__ ws,
                                                        SegTable tb) {
     __shared__ ApplyLds lds;
     const Seg sg = find_seg(tb, blockIdx.x);
     const TensorWork& w = ws[sg.t];
-    apply_wg<DT, MODE, SR, FAST>(w, (int64_t)blockIdx.x - sg.wg_begin, w.apply_wgs, lds);
+    const int64_t local = (int64_t)blockIdx.x - sg.wg_begin;
+    if (MODE == 0 && w.mode != 0) {
+        apply_wg<DT, 1, SR, FAST>(w, local, w.apply_wgs, lds);
+        return;
+    }
+    apply_wg<DT, MODE, SR, FAST>(w, local, w.apply_wgs, lds);
 }
 
 // ====================================================================
@@ -2679,6 +2687,11 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
                 if (phase == 0) k.fast = w.fast_stats;
                 if (phase == 2) { k.fast = w.fast_apply; k.sr = w.sr; }
                 if (phase == 1 || phase == 3) k = GroupKey{0, 0, 0, 0};
+                // block-path tensors other than transposed views join the
+                // factored launches of their dtype (the kernels branch per
+                // tensor): two launches fewer per step when both paths occur
+                if (w.mode == 1 && phase == 0 && k.fast != 2) k = GroupKey{0, w.dtype, 1, 0};
+                if (w.mode == 1 && phase == 2 && k.fast != 2) k.mode = 0;
                 if (phase == 3 && w.mode != 0) continue;
                 groups[k].push_back(t);
             }
@@ -2822,17 +2835,12 @@ static int enqueue_launch(const Launch& l, char* dev, const MtImage& im, hipStre
                     default: GX_MTS(BF16); break;
                 }
 #undef GX_MTS
-            } else if (l.key.fast == 2) {
+            } else {
+                // block path: only transposed views form groups of their own
                 switch (l.key.dtype) {
                     case F32: hipLaunchKernelGGL((k_mt_stats_tv<F32, 1>), grid, block, 0, s, dws, sg); break;
                     case F16: hipLaunchKernelGGL((k_mt_stats_tv<F16, 1>), grid, block, 0, s, dws, sg); break;
                     default: hipLaunchKernelGGL((k_mt_stats_tv<BF16, 1>), grid, block, 0, s, dws, sg); break;
-                }
-            } else {
-                switch (l.key.dtype) {
-                    case F32: hipLaunchKernelGGL(k_mt_block_stats<F32>, grid, block, 0, s, dws, sg); break;
-                    case F16: hipLaunchKernelGGL(k_mt_block_stats<F16>, grid, block, 0, s, dws, sg); break;
-                    default: hipLaunchKernelGGL(k_mt_block_stats<BF16>, grid, block, 0, s, dws, sg); break;
                 }
             }
         } else if (l.phase == 3) {
@@ -2850,21 +2858,15 @@ static int enqueue_launch(const Launch& l, char* dev, const MtImage& im, hipStre
     }
                 if (l.key.mode == 0) { GX_MTA_TV(0) } else { GX_MTA_TV(1) }
 #undef GX_MTA_TV
-            } else if (l.key.mode == 0) {
+            } else {
+                // factored and block-path tensors together (k_mt_apply<.., 0, ..>
+                // branches per tensor)
                 if (l.key.fast) {
                     if (l.key.sr) launch_mt_apply<0, true, true>(dt, grid, s, dws, sg);
                     else launch_mt_apply<0, false, true>(dt, grid, s, dws, sg);
                 } else {
                     if (l.key.sr) launch_mt_apply<0, true, false>(dt, grid, s, dws, sg);
                     else launch_mt_apply<0, false, false>(dt, grid, s, dws, sg);
-                }
-            } else {
-                if (l.key.fast) {
-                    if (l.key.sr) launch_mt_apply<1, true, true>(dt, grid, s, dws, sg);
-                    else launch_mt_apply<1, false, true>(dt, grid, s, dws, sg);
-                } else {
-                    if (l.key.sr) launch_mt_apply<1, true, false>(dt, grid, s, dws, sg);
-                    else launch_mt_apply<1, false, false>(dt, grid, s, dws, sg);
                 }
             }
         }
