@@ -605,36 +605,37 @@ __device__ __forceinline__ double tv_scatter_hi(const double v[kChunk], int i) {
 template <int MODE>
 struct TvStatsLds {
     float cbr[kCodebookMax];
-    double row[MODE == 0 ? kWaves : 1][MODE == 0 ? kTvStatsMaxRows : 1];
+    double colp[MODE == 0 ? kWaves : 1][MODE == 0 ? kFactTileCols : 1];
     uint32_t bmax[kTvLdsBlocks];
     double bsum[MODE == 1 ? kTvLdsBlocks : 1];
 };
 
 // Stats of a transposed view.  Workgroup (ctile, rtile) covers the same
 // kFactTileCols columns as the contiguous factored kernel (so row_part keeps
-// its layout) and tile_rows (<= 256) rows; wave w takes columns
-// [256w, 256w + 256) of them as 64 x 64 tiles, column steps innermost (the
-// two halves of each 128-byte index line in consecutive tiles of one wave).
-// MODE 0 (factored): squares in fp32 over a chunk's 8 columns and over a
-// vector's 8 rows (float64 for fp32 grads), then float64: a row's sum over the wave's
-// columns collects in its lanes across the column steps, a column's over the
-// tile rows in one lane (reduce-scatter over the 8 row groups of each tile),
-// and the 4 waves' row sums meet in LDS in wave order.  Block max |u| (and,
-// MODE 1, the block's sum of squares, each square rounded to bf16 for bf16
-// grads, in float64): when a tile touches at most kTvFew blocks (the common
-// case) its old magnitudes are scalar loads, the lanes keep one value per
-// block and the wave reduces each; otherwise per chunk.  Either way the
-// values go to the workgroup's LDS accumulators (<= 512 blocks) or the
-// shards.
+// its layout) and tile_rows (<= 256) rows; wave w takes the 64-row band w and
+// walks the workgroup's columns in 64 x 64 tiles, so the 4 waves read 512-byte
+// runs of the same storage rows at about the same time (measured 6% faster
+// than 4 waves on 4 column ranges) and a wave reads the two halves of each
+// 128-byte index line in consecutive tiles.  MODE 0 (factored): squares in
+// fp32 over a chunk's 8 columns and over a vector's 8 rows (float64 for fp32
+// grads), then float64: a row's sum over the columns collects in its lanes
+// and leaves as the row partial (reduce-scatter over the 8 column groups),
+// a column's over the band in one lane (reduce-scatter over the 8 row
+// groups of each tile), and the 4 bands' column sums meet in LDS in band
+// order.  Block max |u| (and, MODE 1, the block's sum of squares, each square
+// rounded to bf16 for bf16 grads, in float64): when a tile touches at most
+// kTvFew blocks (the common case) its old magnitudes are scalar loads, the
+// lanes keep one value per block and the wave reduces each; otherwise per
+// chunk.  Either way the values go to the workgroup's LDS accumulators (<= 512
+// blocks) or the shards.
 template <int DT, int MODE, int LF>
 __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvStatsLds<MODE>& lds) {
     using T = typename Elem<DT>::T;
     using Acc = std::conditional_t<DT == F32, double, float>;
-    constexpr int kSteps = (int)(kFactTileCols / kWaves / kTv);  // column steps per wave
     const QTable* qt = wr.qt;
     if (threadIdx.x < kCodebookMax) lds.cbr[threadIdx.x] = *gbl(qt->cbr + threadIdx.x);
     if constexpr (MODE == 0) {
-        for (int k = threadIdx.x; k < kWaves * kTvStatsMaxRows; k += kThreads) (&lds.row[0][0])[k] = 0.0;
+        for (int k = threadIdx.x; k < kWaves * kFactTileCols; k += kThreads) (&lds.colp[0][0])[k] = 0.0;
     }
     const float* s_cbr = lds.cbr;
 
@@ -666,11 +667,10 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvSta
     }
     const int lane = threadIdx.x & 63, la = lane & 7, lb = lane >> 3;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t cw0 = c_begin + (int64_t)wave * (kSteps * kTv);
-    const int64_t cw1 = std::min<int64_t>(cw0 + kSteps * kTv, c_end);
-    const int ncs = cw0 < c_end ? (int)((cw1 - cw0 + kTv - 1) / kTv) : 0;
-    const int nrb = (int)((r_end - r_begin + kTv - 1) / kTv);
-    const int ntile = ncs * nrb;
+    const int64_t cw0 = c_begin, cw1 = c_end;
+    const int ncs = (int)((c_end - c_begin + kTv - 1) / kTv);
+    const int64_t rw0 = r_begin + (int64_t)wave * kTv;
+    const int ntile = rw0 < r_end ? ncs : 0;
     const int64_t dB = div_floor(C, P, invP);
     const int64_t dP = C - dB * P;
     __syncthreads();
@@ -693,9 +693,8 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvSta
     // lanes outside the region read its last sub-block instead (the math
     // skips them)
     auto load_tile = [&](int s, Tile& t) {
-        const int rb = s / ncs;
-        const int64_t r = r_begin + (int64_t)rb * kTv + 8 * la;
-        const int64_t c = cw0 + (int64_t)(s - rb * ncs) * kTv + 8 * lb;
+        const int64_t r = rw0 + 8 * la;
+        const int64_t c = cw0 + (int64_t)s * kTv + 8 * lb;
         const int64_t rl = r < r_end ? r : r_end - kChunk, cl = c < cw1 ? c : cw1 - kChunk;
 #pragma unroll
         for (int k = 0; k < kChunk; ++k) load_raw8<DT>(g + (cl + k) * ld + rl, t.gv[k]);
@@ -703,16 +702,13 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvSta
         for (int j = 0; j < kChunk; ++j) t.iv[j] = load_raw_idx8_cached(idxp + (rl + j) * C + cl);
     };
 
-    double racc[kChunk];  // MODE 0: the band's row sums of the lane's 8 rows over its columns so far
-    double cacc[kSteps];  // MODE 0: column 8b + a of each column step, over the bands so far
+    double racc[kChunk];  // MODE 0: row sums of the lane's 8 rows over the columns so far
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) racc[j] = 0.0;
-#pragma unroll
-    for (int i = 0; i < kSteps; ++i) cacc[i] = 0.0;
 
     auto reduce_tile = [&](int s, const Tile& t) {
-        const int rb = s / ncs, cs = s - rb * ncs;
-        const int64_t r0 = r_begin + (int64_t)rb * kTv, c0 = cw0 + (int64_t)cs * kTv;
+        const int cs = s;
+        const int64_t r0 = rw0, c0 = cw0 + (int64_t)cs * kTv;
         const int64_t r = r0 + 8 * la, c = c0 + 8 * lb;
         const bool ok = r < r_end && c < cw1;
         const int64_t r_last = std::min<int64_t>(r0 + kTv, r_end) - 1;
@@ -802,15 +798,11 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvSta
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) cv[k] = (double)colf[k];
             const double col = tv_scatter_lo(cv, la);
-#pragma unroll
-            for (int i = 0; i < kSteps; ++i) cacc[i] += (i == cs) ? col : 0.0;
+            lds.colp[wave][cs * kTv + 8 * lb + la] = col;
             if (cs == ncs - 1) {
-                // end of the band: row 8a + b over the wave's columns
                 const double row = tv_scatter_hi(racc, lb);
                 const int64_t rr = r0 + 8 * la + lb;
-                if (rr < r_end) lds.row[wave][rr - r_begin] = row;
-#pragma unroll
-                for (int j = 0; j < kChunk; ++j) racc[j] = 0.0;
+                if (rr < r_end) *gbl(row_part + ctile * R + rr) = row;
             }
         }
     };
@@ -824,23 +816,14 @@ __device__ __forceinline__ void stats_tv(const TensorWork& wr, int64_t wg, TvSta
             load_tile(s, t);
             reduce_tile(s, t);
         }
-        if constexpr (MODE == 0) {
-            // column partials of the wave's columns over the tile rows
-#pragma unroll
-            for (int i = 0; i < kSteps; ++i) {
-                const int64_t cc = cw0 + (int64_t)i * kTv + 8 * lb + la;
-                if (i < ncs && cc < cw1) *gbl(col_part + rtile * C + cc) = cacc[i];
-            }
-        }
     }
     __syncthreads();
     if constexpr (MODE == 0) {
-        for (int64_t r = r_begin + threadIdx.x; r < r_end; r += kThreads) {
-            const int64_t i = r - r_begin;
-            double v = lds.row[0][i];
+        for (int64_t k = threadIdx.x; k < c_end - c_begin; k += kThreads) {
+            double v = lds.colp[0][k];
 #pragma unroll
-            for (int ww = 1; ww < kWaves; ++ww) v += lds.row[ww][i];
-            *gbl(row_part + ctile * R + r) = v;
+            for (int ww = 1; ww < kWaves; ++ww) v += lds.colp[ww][k];
+            *gbl(col_part + rtile * C + c_begin + k) = v;
         }
     }
     if (lds_blk) {
