@@ -361,7 +361,7 @@ def bench_muon(args):
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": tflops / 2500.0, "traffic": None,
-                     "kernel": "k_gemm_big / k_gemm_dl (Newton-Schulz GEMMs, bf16 MFMA 32x32x16, direct-to-LDS; 256x256 tiles on large grids)",
+                     "kernel": "k_gemm_big16 / k_gemm_big / k_gemm_dl (Newton-Schulz GEMMs, bf16 MFMA, direct-to-LDS; 256x256 tiles on large grids, 16x16x32 when every tile is full)",
                      "flops_per_step": ns_flops / args.steps, "gemm_ms_per_step": ns_ms / args.steps,
                      "executed_flops_per_step": executed, "executed_tflops": exec_tflops,
                      "mfma_utilisation": exec_tflops / 2500.0},

@@ -52,8 +52,9 @@ def _bf16_np(t):
 # K % 64 == 0 with 16-byte aligned operands takes a direct-to-LDS kernel:
 # 128 x 128 tiles for (256, 192, 128), (200, 136, 192), (130, 300, 64) (full
 # tiles, partial tiles, a single K step), 256 x 256 tiles once those fill the
-# CUs (the last three: full tiles, partial edge tiles, a single K step); the
-# rest the register-staged one (K = 30 also without 16-byte loads)
+# CUs (the last three: full tiles on the 16x16x32 kernel, partial edge tiles
+# on the 32x32x16 one, a single K step on the 16x16x32 one); the rest the
+# register-staged one (K = 30 also without 16-byte loads)
 @pytest.mark.parametrize("mnk", [(128, 128, 32), (256, 192, 160), (200, 136, 72), (100, 60, 30), (33, 257, 48),
                                  (256, 192, 128), (200, 136, 192), (130, 300, 64),
                                  (4096, 4096, 128), (4000, 4200, 192), (4096, 4096, 64)])
