@@ -1159,14 +1159,18 @@ __device__ __forceinline__ void put_acc16(const f32x16 (&acc4)[8][2], float* sOu
 // 256 x 256 full tiles (M and N multiples of 256, epilogue operands aligned
 // as gemm_epilogue_full needs) on mfma_f32_16x16x32_bf16, which runs at a
 // higher clock than the 32x32x16 form for the same work (measured: ~2.05
-// against ~1.81 GHz with the MFMA pipes ~94% busy).  The schedule of
-// k_gemm_big: one workgroup per CU, K steps of 64 in a two-stage
-// direct-to-LDS ring, one barrier per step.  Each wave's 128 x 128 is 8 x 8
-// blocks of 16 x 16; a 32-wide K sub-step is 64 MFMAs against 16 operand
-// fragments.  Sub-step 0 reads sub-step 1's fragments (B first, three per
-// MFMA row in rows 0-5) and issues the next stage's 16 loads (two per row).
-// The accumulators live as four 16 x 16 blocks per 16-float vector: held as
-// 64 separate 4-float values the compiler's register allocation spilled.
+// against ~1.81 GHz with the MFMA pipes ~94% busy).  One workgroup per CU, K
+// steps of 64 in a two-stage direct-to-LDS ring.  Each wave's 128 x 128 is
+// 8 x 8 blocks of 16 x 16; a 32-wide K sub-step is 64 MFMAs against 16
+// operand fragments, two sub-steps per K step.  The step's barrier sits
+// between its sub-steps: sub-step 0 reads sub-step 1's fragments (the last
+// reads of this stage); after the barrier (every wave's reads of this stage
+// returned, the next stage landed) sub-step 1 issues the stage-after-next's
+// loads into this stage's buffer and reads the next stage's sub-step 0
+// fragments, so no step opens with an operand wait and the loads still lead
+// by one K step.  The accumulators live as four 16 x 16 blocks per 16-float
+// vector: held as 64 separate 4-float values the compiler's register
+// allocation spilled.
 __global__ void __launch_bounds__(kT) k_gemm_big16(GemmArgs g) {
     constexpr int TILE = 256, BK = 64;
     int64_t bz, tm, tn;
@@ -1199,49 +1203,72 @@ __global__ void __launch_bounds__(kT) k_gemm_big16(GemmArgs g) {
         const int row = half * 128 + idx * 16 + l16;
         return *reinterpret_cast<const bf16x8*>(t + row * BK + dl_slot<BK>(row, c) * 8);
     };
+    auto mma = [&](int i, int j, const bf16x8& a, const bf16x8& b) {
+        f32x4 c;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) c[r] = acc4[i][j >> 2][4 * (j & 3) + r];
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc4[i][j >> 2][4 * (j & 3) + r] = c[r];
+    };
+    // stage 0 landed for every wave; stage 1 (a reload of stage 0 when nk is
+    // 1, never read) in flight; sub-step 0 fragments of stage 0 read
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    {
+        const int64_t k1 = (nk > 1 ? 1 : 0) * BK;
+#pragma unroll
+        for (int q = 0; q < kIpw; ++q) dl_load_full<TILE, BK>(A, g.lda, B, g.ldb, m0, n0, k1, smem + kStage, wave, q);
+    }
+    bf16x8 f0a[8], f0b[8], f1a[8], f1b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        f0b[i] = rd(smem + TILE * BK, wn, i, lq);
+        f0a[i] = rd(smem, wm, i, lq);
+    }
+#pragma unroll 1
     for (int64_t kt = 0; kt < nk; ++kt) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this step's loads, the only ones in flight
-        __syncthreads();                     // ... landed for every wave; the other buffer is idle
         const uint16_t* a_s = smem + (kt & 1) * kStage;
         const uint16_t* b_s = a_s + TILE * BK;
-        uint16_t* nxt = smem + ((kt + 1) & 1) * kStage;
-        const int64_t kn = (kt + 1 < nk ? kt + 1 : kt) * BK;  // the last step reloads its own range (never read)
-        bf16x8 av[2][8], bv[2][8];
+        const uint16_t* a_n = smem + ((kt + 1) & 1) * kStage;
+        const uint16_t* b_n = a_n + TILE * BK;
+        uint16_t* nxt = smem + (kt & 1) * kStage;
+        const int64_t k2 = (kt + 2 < nk ? kt + 2 : nk - 1) * BK;  // past the end: a reload, never read
+        // sub-step 0: MFMAs on f0; sub-step 1's fragments (B first) read in rows 0-5
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            bv[0][i] = rd(b_s, wn, i, lq);
-            av[0][i] = rd(a_s, wm, i, lq);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                __builtin_amdgcn_sched_barrier(0);
+                mma(i, j, f0a[i], f0b[j]);
+                __builtin_amdgcn_sched_barrier(0);
+                const int f = 3 * i + (j == 1 ? 0 : j == 3 ? 1 : 2);
+                if ((j == 1 || j == 3 || j == 5) && f < 16) {
+                    if (f < 8) f1b[f] = rd(b_s, wn, f, 4 + lq);
+                    else f1a[f - 8] = rd(a_s, wm, f - 8, 4 + lq);
+                }
+            }
         }
+        __syncthreads();  // every wave's reads of stage kt returned; stage kt+1 landed (vmcnt(0))
+        // sub-step 1: MFMAs on f1; the stage-after-next's loads into stage kt's
+        // buffer (two per row) and the next stage's sub-step 0 fragments (rows 0-5)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int i = 0; i < 8; ++i) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    {
-                        f32x4 c;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) c[r] = acc4[i][j >> 2][4 * (j & 3) + r];
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[ks][i], bv[ks][j], c, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) acc4[i][j >> 2][4 * (j & 3) + r] = c[r];
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (ks == 0) {
-                        if (j == 0 || j == 4)
-                            dl_load_full<TILE, BK>(A, g.lda, B, g.ldb, m0, n0, kn, nxt, wave, 2 * i + (j == 4));
-                        const int f = 3 * i + (j == 1 ? 0 : j == 3 ? 1 : 2);
-                        if ((j == 1 || j == 3 || j == 5) && f < 16) {
-                            if (f < 8) bv[1][f] = rd(b_s, wn, f, 4 + lq);
-                            else av[1][f - 8] = rd(a_s, wm, f - 8, 4 + lq);
-                        }
-                    }
+            for (int j = 0; j < 8; ++j) {
+                __builtin_amdgcn_sched_barrier(0);
+                mma(i, j, f1a[i], f1b[j]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (j == 0 || j == 4) dl_load_full<TILE, BK>(A, g.lda, B, g.ldb, m0, n0, k2, nxt, wave, 2 * i + (j == 4));
+                const int f = 3 * i + (j == 1 ? 0 : j == 3 ? 1 : 2);
+                if ((j == 1 || j == 3 || j == 5) && f < 16) {
+                    if (f < 8) f0b[f] = rd(b_n, wn, f, lq);
+                    else f0a[f - 8] = rd(a_n, wm, f - 8, lq);
                 }
             }
         }
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // the last (discarded) reload lands before the epilogue reuses LDS
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the last (discarded) loads land before the epilogue reuses LDS
     __syncthreads();
     float* sOut = reinterpret_cast<float*>(smem);
     gemm_epilogue_full<4>(g, [&](int h) { put_acc16(acc4, sOut, h, wm, wn, lane); }, sOut, bz, tm == tn, m0, n0);
