@@ -1276,6 +1276,7 @@ __global__ void __launch_bounds__(kT) k_gemm_big16(GemmArgs g) {
 
 static int gemm_nt(const GemmArgs& g, int64_t batch, hipStream_t s) {
     if (g.M <= 0 || g.N <= 0 || batch <= 0) return GEFENX_OK;
+    if (g.K <= 0) return set_error(GEFENX_EINVAL, "newton-schulz gemm: K must be positive");
     GemmArgs a = g;
     const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     a.vec = (g.K % 8 == 0) && (g.lda % 8 == 0) && (g.ldb % 8 == 0) && (g.sA % 8 == 0) && (g.sB % 8 == 0) &&
@@ -2251,6 +2252,8 @@ int gefenx_gemm_nt_bf16(const void* A, const void* B, const void* C, void* D, in
                         float alpha, float beta, void* stream) {
     if (M < 0 || N < 0 || K < 0) return set_error(GEFENX_EINVAL, "gefenx_gemm_nt_bf16: negative shape");
     if (M == 0 || N == 0) return GEFENX_OK;
+    // every kernel reads the first K step of A and B before its loop
+    if (K == 0) return set_error(GEFENX_EINVAL, "gefenx_gemm_nt_bf16: K must be positive");
     if (!A || !B || !D) return set_error(GEFENX_EINVAL, "gefenx_gemm_nt_bf16: null pointer argument");
     GemmArgs g{static_cast<const uint16_t*>(A), K, 0, static_cast<const uint16_t*>(B), K, 0,
                static_cast<const uint16_t*>(C), N, 0, static_cast<uint16_t*>(D), N, 0, nullptr, 0, 0,

@@ -478,7 +478,8 @@ int gefenx_muon_apply(void* p, int dtype, const void* update, const void* row_sc
                       void* stream);
 
 /* The Newton-Schulz GEMM alone: D = bf16(alpha * A B^T + beta * C) for bf16
- * row-major A [M, K], B [N, K], C / D [M, N] (C may be NULL).  No counterpart
+ * row-major A [M, K], B [N, K], C / D [M, N] (C may be NULL; K >= 1, K == 0
+ * is GEFENX_EINVAL; M or N == 0 is a no-op).  No counterpart
  * in the reference (its Newton-Schulz calls torch.matmul / addmm); exposed
  * for testing and measuring the MFMA kernel. */
 int gefenx_gemm_nt_bf16(const void* A, const void* B, const void* C, void* D, int64_t M,

@@ -254,3 +254,14 @@ def test_noalloc_rejects_shapes_beyond_the_static_scratch(lib):
                                             1.0, 1.0, 0, 0, None, None, None)
     assert rc == _native.GEFENX_EINVAL
     assert "static scratch" in _native.last_error()
+
+
+def test_gemm_rejects_empty_contraction_before_any_launch(lib):
+    """K == 0 is refused on the host (the kernels read the first K step of A
+    and B before their loop); here on a machine without a GPU the call
+    returns before touching a device."""
+    from gefen.kernels import _native
+    rc = lib.gefenx_gemm_nt_bf16(ctypes.c_void_p(16), ctypes.c_void_p(16), None, ctypes.c_void_p(16),
+                                 8, 8, 0, 1.0, 0.0, None)
+    assert rc == _native.GEFENX_EINVAL
+    assert lib.gefenx_gemm_nt_bf16(None, None, None, None, 0, 8, 0, 1.0, 0.0, None) == _native.GEFENX_OK
