@@ -471,4 +471,22 @@ __device__ __forceinline__ void stage_sr(SharedSR& s, const QTable* __restrict__
     for (int i = threadIdx.x; i < kLutEntries + 7; i += blockDim.x) s.lut[i] = t->lut[i];
 }
 
+// Hands block b's shard values base[sh * nb + b] to f in shard order, then
+// zeroes them: every load is issued before any store (a store between them
+// would make each load wait for the previous one, as the compiler cannot
+// tell the addresses apart), eight at a time.
+template <typename T, typename F>
+__device__ __forceinline__ void drain_shards(T* base, int64_t shards, int64_t nb, int64_t b, F&& f) {
+    int64_t sh = 0;
+    for (; sh + 8 <= shards; sh += 8) {
+        T v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = base[(sh + k) * nb + b];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f(v[k]);
+    }
+    for (; sh < shards; ++sh) f(base[sh * nb + b]);
+    for (sh = 0; sh < shards; ++sh) base[sh * nb + b] = T(0);
+}
+
 }  // namespace gx

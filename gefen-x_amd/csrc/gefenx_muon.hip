@@ -133,11 +133,7 @@ __global__ void __launch_bounds__(kT) k_mom_finalize(MomBatch bt) {
     for (int64_t b = (int64_t)blockIdx.x * kT + threadIdx.x; b < it.nb; b += (int64_t)gridDim.x * kT) {
         it.mag_old[b] = it.mag[b];
         uint32_t bits = 0u;
-        for (int64_t sh = 0; sh < it.shards; ++sh) {
-            const uint32_t v = it.magbits[sh * it.nb + b];
-            bits = v > bits ? v : bits;
-            it.magbits[sh * it.nb + b] = 0u;
-        }
+        drain_shards(it.magbits, it.shards, it.nb, b, [&](uint32_t v) { bits = v > bits ? v : bits; });
         const float m = __uint_as_float(bits);
         it.mag[b] = m;
         it.minv[b] = block_recip(m < kTiny ? kTiny : m);

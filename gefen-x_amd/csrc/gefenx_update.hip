@@ -86,6 +86,7 @@ struct TensorWork {
     int32_t row_apply;   // factored contiguous apply over row segments (apply_rows)
     int32_t partial;     // block path with the caller's per-block stepsize (no vmean)
     int32_t fin_wide;    // block finalize: one workgroup per block (blocks span many stats records)
+    int32_t csplit;      // factored finalize: threads per column (1, 2, 4 or 8), each over a run of row tiles
     float eps, beta2, alpha2;
     float bc2_div;       // reference-order divisor (factored bc2, block sqrt(bc2)) or 0
     StepScalars sc;
@@ -1162,11 +1163,7 @@ __device__ __forceinline__ void finalize_magnitude(const TensorWork& w, int64_t 
     const float old = w.mag[b];
     w.mag_old[b] = old;
     uint32_t bits = 0u;
-    for (int64_t sh = 0; sh < w.shards; ++sh) {
-        const uint32_t v = w.magbits[sh * w.nb + b];
-        bits = v > bits ? v : bits;
-        w.magbits[sh * w.nb + b] = 0u;
-    }
+    drain_shards(w.magbits, w.shards, w.nb, b, [&](uint32_t v) { bits = v > bits ? v : bits; });
     const float m = __uint_as_float(bits);
     w.mag[b] = m;
     w.minv[b] = block_recip(m);
@@ -1191,7 +1188,9 @@ __device__ __forceinline__ double ordered_sum(const double* __restrict__ p, int6
 // ====================================================================
 // Factored finalize.  Workgroups [0, nr): v_row EMA from the ct row partials
 // plus one float64 partial of sum(v_row); [nr, nr+nc): v_col EMA from the rt
-// column partials (one column per thread, partials in row-tile order); the
+// column partials in row-tile order, csplit threads per column: thread p sums
+// the p-th run of ceil(rt / csplit) partials in order, then the runs are
+// added in order (one run, the plain sequential sum, when rt <= 32); the
 // rest: magnitudes.
 // v <- fma(sum/n, 1-beta2, v*beta2)  (gefen.py:2994-2996)
 // ====================================================================
@@ -1219,9 +1218,22 @@ __device__ __forceinline__ void finalize_factored(const TensorWork& w, int64_t w
         return;
     }
     if (wg < w.nr + w.nc) {
-        const int64_t j = (wg - w.nr) * kThreads + tid;
-        if (j < w.C) {
-            const double tot = ordered_sum(w.col_part + j, w.rt, w.C);
+        __shared__ double s_run[kThreads];
+        const int sp = w.csplit;
+        const int cpw = kThreads / sp;  // columns per workgroup
+        const int part = tid / cpw;
+        const int64_t j = (wg - w.nr) * cpw + tid % cpw;
+        const int64_t per = (w.rt + sp - 1) / sp;
+        const int64_t t0 = std::min<int64_t>((int64_t)part * per, w.rt);
+        const int64_t t1 = std::min<int64_t>(t0 + per, w.rt);
+        double tot = j < w.C ? ordered_sum(w.col_part + t0 * w.C + j, t1 - t0, w.C) : 0.0;
+        if (sp > 1) {
+            s_run[tid] = tot;
+            __syncthreads();
+            if (part == 0)
+                for (int q = 1; q < sp; ++q) tot += s_run[q * cpw + tid];
+        }
+        if (part == 0 && j < w.C) {
             const float ms = (float)tot / (float)w.R;
             const float v = __builtin_fmaf(ms, w.alpha2, w.v1[j] * w.beta2);
             w.v1[j] = v;
@@ -1270,10 +1282,7 @@ __device__ __forceinline__ void finalize_block_wide(const TensorWork& w, int64_t
     __syncthreads();
     if (tid != 0) return;
     double sq = 0.0;
-    for (int64_t sh = 0; sh < w.shards; ++sh) {
-        sq += w.blk_sq[sh * w.nb + b];
-        w.blk_sq[sh * w.nb + b] = 0.0;
-    }
+    drain_shards(w.blk_sq, w.shards, w.nb, b, [&](double v) { sq += v; });
     if (w.partial) {  // the stepsize comes from the caller: magnitudes only
         finalize_magnitude(w, b);
         return;
@@ -1295,10 +1304,7 @@ __device__ __forceinline__ void finalize_block(const TensorWork& w, int64_t wg) 
         // of the workgroups it spans; the transposed-view stats accumulate
         // into the shards
         double sq = 0.0;
-        for (int64_t sh = 0; sh < w.shards; ++sh) {
-            sq += w.blk_sq[sh * w.nb + b];
-            w.blk_sq[sh * w.nb + b] = 0.0;
-        }
+        drain_shards(w.blk_sq, w.shards, w.nb, b, [&](double v) { sq += v; });
         if (w.partial) {  // the stepsize comes from the caller: magnitudes only
             finalize_magnitude(w, b);
             continue;
@@ -2418,9 +2424,7 @@ static int build_work(const WorkInput& in, TensorWork& w) {
         w.ct = t.ct; w.rt = t.rt; w.tile_rows = t.tile_rows;
         w.stats_wgs = t.ct * t.rt;
         w.nr = ceil_div(in.R, kFinRowsPerWg);
-        w.nc = ceil_div(in.C, kThreads);
         w.nbw = std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(nb, kFinBlocksPerWg)));
-        w.fin_wgs = w.nr + w.nc + w.nbw;
         const bool contig_g = (in.gs1 == 1 && in.gs0 == in.C);
         const bool contig_p = (in.ps1 == 1 && in.ps0 == in.C);
         w.fast_stats = contig_g && (in.C % kChunk == 0) && aligned(in.grad, 16) && aligned(in.idx, 8);
@@ -2432,6 +2436,12 @@ static int build_work(const WorkInput& in, TensorWork& w) {
             w.tile_rows = t.tv_rows;
             w.stats_wgs = t.ct * t.rt_tv;
         }
+        // column sums over many row tiles (embeddings: ~250) split into up to
+        // 8 runs of <= 32 partials, so no thread waits on a long load chain
+        w.csplit = 1;
+        while (w.csplit < 8 && ceil_div(w.rt, (int64_t)w.csplit) > 32) w.csplit *= 2;
+        w.nc = ceil_div(in.C, kThreads / w.csplit);
+        w.fin_wgs = w.nr + w.nc + w.nbw;
         // the view apply reads v_row and sqrt(v_col) (v_col on the fp32
         // reference path) 8 floats at a time
         if (!w.fast_apply && tv_shape && tv_g && tv_p && !in.sr && w.write_p && aligned(in.v0, 16) &&
