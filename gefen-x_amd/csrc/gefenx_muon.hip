@@ -1107,7 +1107,7 @@ __global__ void __launch_bounds__(kT) k_gemm_big(GemmArgs g) {
 
 // One 1 KB direct-to-LDS load of a full tile (every row in range, no clamp),
 // the layout of dl_load_one: the instruction's first row at column k0 is a
-// wave-uniform address, each lane adds a 32-bit offset (its row within the
+// wave-uniform address, each lane adds its offset (its row within the
 // instruction and the chunk its slot holds).
 template <int TILE, int BK>
 __device__ __forceinline__ void dl_load_full(const uint16_t* __restrict__ A, int64_t lda,
@@ -1125,7 +1125,7 @@ __device__ __forceinline__ void dl_load_full(const uint16_t* __restrict__ A, int
     const unsigned char* ubase =
         reinterpret_cast<const unsigned char*>((is_b ? B : A) + ((is_b ? n0 : m0) + ti * kRpi) * ld + k0);
     const int rr = lane / kCpr;
-    const uint32_t voff = (uint32_t)(rr * ld * 2) + (uint32_t)dl_slot<BK>(ti * kRpi + rr, lane % kCpr) * 16u;
+    const int64_t voff = (int64_t)rr * ld * 2 + (int64_t)dl_slot<BK>(ti * kRpi + rr, lane % kCpr) * 16;
     uint16_t* dst = stage + (is_b ? TILE * BK : 0) + ti * kRpi * BK;  // wave-uniform
     __builtin_amdgcn_global_load_lds((const GX_GLOBAL void*)(ubase + voff),
                                      (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
