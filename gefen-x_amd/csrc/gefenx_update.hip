@@ -2436,8 +2436,9 @@ static int build_work(const WorkInput& in, TensorWork& w) {
             w.tile_rows = t.tv_rows;
             w.stats_wgs = t.ct * t.rt_tv;
         }
-        // column sums over many row tiles (embeddings: ~250) split into up to
-        // 8 runs of <= 32 partials, so no thread waits on a long load chain
+        // column sums over many row tiles (embeddings: ~250-300) split into
+        // up to 8 runs (of <= 32 partials up to 256 row tiles), so no thread
+        // waits on a long load chain
         w.csplit = 1;
         while (w.csplit < 8 && ceil_div(w.rt, (int64_t)w.csplit) > 32) w.csplit *= 2;
         w.nc = ceil_div(in.C, kThreads / w.csplit);
@@ -2693,10 +2694,20 @@ static void plan_multi(const std::vector<TensorWork>& works, MtLayout& L) {
             // the finalize reads next, stay cached (measured on the Qwen3-4B
             // set: stats 2.04 -> 1.98 ms, finalize 65 -> 58 us)
             std::vector<std::pair<GroupKey, std::vector<int>>> ordered(groups.begin(), groups.end());
-            if (phase == 0)
+            if (phase == 0) {
                 std::stable_sort(ordered.begin(), ordered.end(), [](const auto& a, const auto& b) {
                     return (a.first.fast == 2) > (b.first.fast == 2);
                 });
+                // inside a launch, tensors with the largest stats tiles first
+                // and the smallest last, so the launch's last round of
+                // workgroups, which leaves CUs idle, is one of short tiles
+                for (auto& kv : ordered)
+                    std::stable_sort(kv.second.begin(), kv.second.end(), [&](int a, int b) {
+                        const TensorWork& wa = works[(size_t)a];
+                        const TensorWork& wb = works[(size_t)b];
+                        return (double)wa.N * (double)wb.stats_wgs > (double)wb.N * (double)wa.stats_wgs;
+                    });
+            }
             for (auto& kv : ordered) {
                 Launch l;
                 l.phase = phase;
