@@ -40,16 +40,18 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // Factored stats tiling: a workgroup covers kFactTileCols columns (64 lanes x
 // two 8-column chunks) of `tile_rows` consecutive rows.  Tiles hold about
 // N/32 elements, between 64K (16K-element tiles spend a third of the pass on
-// per-workgroup set-up and flushes) and 512K.  The multi-tensor launch puts
-// every parameter's tiles in one grid, so fewer, larger tiles cost no
-// occupancy until the last wave of workgroups runs part-empty.  Measured
-// (step time): Llama-3-8B set 17.1-17.2 ms with N/256 capped at 1M, 16.5-16.65
-// with N/32 capped at 512K (caps of 256K or 2M slower); Qwen3-4B set 9.2-9.5
-// and 9.03-9.05 ms.  The tiling is per tensor, so a tensor's float64 partials
+// per-workgroup set-up and flushes) and 1M.  The multi-tensor launch puts
+// every parameter's tiles in one grid, largest tiles first, so fewer, larger
+// tiles cost no occupancy until the last round of workgroups, one of the
+// smallest tiles, runs part-empty.  Measured (stats kernel on the Llama-3-8B
+// set, tiles ordered by size): caps of 256K / 512K / 768K / 1M / 1.5M / 2M
+// 4.29-4.31 / 4.08 / 4.01-4.04 / 3.96-3.99 / 4.05-4.07 / 3.95-3.96 ms (1.5M
+// and 2M leave 4096-row tensors a short last row tile; 1M splits the common
+// shapes evenly).  The tiling is per tensor, so a tensor's float64 partials
 // do not depend on the other tensors of its launch.
 constexpr int64_t kFactTileCols = 1024;
 constexpr int64_t kFactTileMinElems = 1 << 16;
-constexpr int64_t kFactTileMaxElems = 1 << 19;
+constexpr int64_t kFactTileMaxElems = 1 << 20;
 
 // Transposed-view stats (strides (1, ld)) use the same column tiles but row
 // tiles of whole 64-row bands, at most kTvStatsMaxRows rows.
