@@ -2284,10 +2284,19 @@ __global__ void __launch_bounds__(kThreads) k_mt_stats_tv(const TensorWork* __re
 }
 
 template <int DT, int MODE>
+// The launch's workgroups are renumbered so that each XCD (the hardware deals
+// consecutive workgroups to the 8 XCDs in turn) runs one contiguous range of
+// them: a tile's index chunks are the first or second half of 128-byte lines
+// whose other half a workgroup a few places later reads, which then hits the
+// same L2 (measured on the Qwen3-4B views: 2.07 -> 1.76 GB read per launch,
+// the algorithmic bytes, at the same speed).
 __global__ void __launch_bounds__(kThreads) k_mt_apply_tv(const TensorWork* __restrict__ ws, SegTable tb) {
     __shared__ FastTables ft;
-    const Seg sg = find_seg(tb, blockIdx.x);
-    apply_tv_wg<DT, MODE>(ws[sg.t], (int64_t)blockIdx.x - sg.wg_begin, ft);
+    const int64_t G = gridDim.x, b = blockIdx.x;
+    const int64_t q = G / 8, r = G % 8, x = b % 8;
+    const int64_t L = x * q + (x < r ? x : r) + b / 8;
+    const Seg sg = find_seg(tb, L);
+    apply_tv_wg<DT, MODE>(ws[sg.t], L - sg.wg_begin, ft);
 }
 
 __global__ void __launch_bounds__(kThreads) k_mt_finalize(const TensorWork* __restrict__ ws,
